@@ -1,0 +1,208 @@
+/*
+ * vx27_hip.h -- C ABI of the MI355X (gfx950) token-mixer library.
+ *
+ * The reference (DavidPandleton/vx27) runs its mixers on the host, inline in
+ * vx27_qlayer (src/vx27_qfwd.c:92-215), through the void functions of
+ * vx27_deltanet.h / vx27_gqa.h / vx27_rope.h.  This header is the thin C ABI
+ * those callers use to run the same mixers on device-resident data:
+ *   - a context (device + HIP stream) and device memory helpers,
+ *   - DeltaNet recurrent decode (gate mapping, causal conv, delta rule,
+ *     gated output norm), one or many tokens per call,
+ *   - gated GQA decode over a bf16 KV cache (split-K flash decode),
+ *   - RoPE tables and KV-cache format helpers.
+ * The reference's own void API (include/vx27_deltanet.h etc.) is exported by
+ * the same library and routes through these entry points.
+ *
+ * Conventions: every entry point returns 0 on success and -1 on failure;
+ * the reason is in vx27_hip_last_error() (thread-local).  All pointers in
+ * descriptors are device pointers unless stated.  Calls on one context are
+ * serialised on its stream and are not thread-safe; distinct contexts are
+ * independent.  Kernels are enqueued asynchronously: call vx27_hip_sync()
+ * (or synchronise the stream) before reading results on the host.
+ */
+#ifndef VX27_HIP_H
+#define VX27_HIP_H
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef struct vx27_hip_ctx vx27_hip_ctx;
+
+/* ------------------------------------------------------------- context */
+/* Open a context on `device` with its own stream.  Mirrors the reference's
+ * init convention (int status + caller message buffer, vx27_gpu_reg.h:9). */
+int vx27_hip_open(vx27_hip_ctx **ctx, int device, char *err, size_t errlen);
+void vx27_hip_close(vx27_hip_ctx *ctx);
+int vx27_hip_sync(vx27_hip_ctx *ctx);
+/* Use a caller stream (hipStream_t) for subsequent calls; NULL restores the
+ * context's own stream. */
+int vx27_hip_set_stream(vx27_hip_ctx *ctx, void *hip_stream);
+void *vx27_hip_get_stream(vx27_hip_ctx *ctx);
+const char *vx27_hip_last_error(void);
+int vx27_hip_device_count(void);
+/* Library version string and the gfx target it was built for. */
+const char *vx27_hip_version(void);
+
+/* Kernel profiler: while enabled, the library records HIP events around
+ * each of its kernel launches on the context stream; prof_read synchronises
+ * and returns how many launches of `kernel` were recorded and their summed
+ * duration.  Enabling (or disabling) clears the records. */
+int vx27_hip_prof_enable(vx27_hip_ctx *ctx, int on);
+int vx27_hip_prof_read(vx27_hip_ctx *ctx, const char *kernel, int *count, double *total_ms);
+
+/* The context used by the reference-API drop-ins (opened on first use on
+ * device VX27_HIP_DEVICE from the environment, default 0). */
+vx27_hip_ctx *vx27_hip_default_ctx(void);
+
+/* Error behaviour of the void drop-ins, which cannot return a status:
+ * VX27_HIP_ERR_ABORT (default) prints the error and aborts the process;
+ * VX27_HIP_ERR_POISON fills the outputs with NaN, records the error and
+ * returns.  There is no host fallback in either mode. */
+#define VX27_HIP_ERR_ABORT 0
+#define VX27_HIP_ERR_POISON 1
+void vx27_hip_set_error_mode(int mode);
+
+/* -------------------------------------------------------------- memory */
+int vx27_hip_alloc(vx27_hip_ctx *ctx, void **dptr, size_t bytes);
+int vx27_hip_free(vx27_hip_ctx *ctx, void *dptr);
+int vx27_hip_h2d(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+int vx27_hip_d2h(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+int vx27_hip_d2d(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+int vx27_hip_memset(vx27_hip_ctx *ctx, void *dst, int byte, size_t bytes);
+
+/* dtype codes */
+#define VX27_F32 0
+#define VX27_BF16 1
+
+/* ------------------------------------------------------ DeltaNet decode */
+/* Stages of the reference DeltaNet branch (vx27_qfwd.c:92-155) applied
+ * around the exact gated delta rule (vx27_deltanet_step_exact,
+ * vx27_deltanet.c:71-102, which always l2-normalises q,k and scales q):
+ *   VX27_DN_CONV     causal conv width 4 + SiLU on the q|k|v channels, with
+ *                    the conv state carried in place (vx27_deltanet.c:106-122)
+ *   VX27_DN_PRE_RMS  rmsn(x)*(1+norm_w) on each q,k head (vx27_qfwd.c:123)
+ *   VX27_DN_PRE_L2   l2norm q,k and q *= 1/sqrt(hd) (vx27_qfwd.c:124-130)
+ *   VX27_DN_OUT_GATE out = rmsn_std(o)*norm_w * silu(z) (vx27_qfwd.c:147-151)
+ * No flags = step_exact on the given q,k,v (the recurrence alone). */
+#define VX27_DN_CONV 1u
+#define VX27_DN_PRE_RMS 2u
+#define VX27_DN_PRE_L2 4u
+#define VX27_DN_OUT_GATE 8u
+
+typedef struct {
+    int B;          /* independent sequences */
+    int nqk, nv;    /* QK heads and value heads; value head vh uses QK head vh*nqk/nv
+                       (vx27_qfwd.c:137); nv must be a multiple of nqk */
+    int hd;         /* head dim: 128 */
+    int steps;      /* tokens per sequence in this call (>= 1), run in order */
+    unsigned flags; /* VX27_DN_* */
+    float *S;       /* [B][nv][hd][hd] fp32 state, row = key dim, column = value dim; in/out */
+    float *conv_state;  /* [B][C][3] fp32, oldest first (VX27_DN_CONV); in/out */
+    const void *conv_w; /* [C][4] weights, tap 3 = newest (VX27_DN_CONV) */
+    int conv_w_dtype;   /* VX27_F32 or VX27_BF16 */
+    /* Per-token inputs, fp32, token t of sequence b at [t][b]:
+     *   VX27_DN_CONV:  x [steps][B][C], C = 2*nqk*hd + nv*hd, channels q|k|v
+     *   otherwise:     q,k [steps][B][nqk][hd], v [steps][B][nv][hd] */
+    const float *x, *q, *k, *v;
+    const float *a, *b;          /* [steps][B][nv] gate projections */
+    const float *A_log, *dt_bias;/* [nv] */
+    const float *norm_w;         /* [hd] (PRE_RMS uses 1+w, OUT_GATE uses w) */
+    const float *z;              /* [steps][B][nv][hd] (OUT_GATE) */
+    float *out;                  /* [steps][B][nv][hd] */
+} vx27_dn_desc;
+
+/* Run `steps` tokens of the DeltaNet mixer core for B sequences.  The state
+ * stays in registers across the steps of one call, so multi-step calls read
+ * and write S once per call. */
+int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d);
+
+/* ---------------------------------------------------------- GQA decode */
+/* KV cache format (bf16), for B sequences x n_kv heads x L positions, hd 256:
+ *   K: [B][n_kv][L][hd]            one row per position
+ *   V: [B][n_kv][L/32][hd][32]     32-position blocks stored dim-major
+ * L (the capacity) must be a multiple of 64.  Use vx27_hip_kv_write /
+ * vx27_hip_kv_read to move rows in or out of this layout. */
+#define VX27_GQA_NORM_W 1u  /* q/k norm as x*s*w (vx27_gqa.c:10-15) instead of x*s*(1+w) */
+
+typedef struct {
+    int B;
+    int n_q, n_kv, hd;       /* 24, 4, 256 (hd must be 256, n_q/n_kv <= 16) */
+    int rope_dim;            /* rotated leading dims per head (NeoX half split), 64 */
+    float rope_theta;        /* 1e7 */
+    float rope_yarn;         /* linear position scale, >= 1 */
+    int L;                   /* cache capacity (positions), multiple of 64 */
+    unsigned flags;          /* VX27_GQA_* */
+    const int *pos;          /* [B] device: position of the new token; keys 0..pos attended */
+    /* raw q (before norm/rope), element (b, h, i) at q[b*q_seq_stride + h*q_head_stride + i];
+     * the interleaved q_proj output of vx27_qfwd.c:160-167 is q_head_stride = 2*hd and
+     * gate = q + hd with the same strides. */
+    const float *q;
+    size_t q_seq_stride, q_head_stride;
+    const float *gate;       /* gate logits, same addressing with its own strides */
+    size_t gate_seq_stride, gate_head_stride;
+    const float *k_new, *v_new;  /* [B][n_kv][hd] raw k (before norm/rope) and v */
+    const float *q_norm_w, *k_norm_w;  /* [hd] */
+    uint16_t *k_cache, *v_cache;       /* bf16, format above; row pos is written */
+    float *out;              /* [B][n_q][hd]: attention * sigmoid(gate) */
+    int n_split;             /* key splits per (sequence, KV head); 0 = automatic */
+} vx27_gqa_desc;
+
+/* One decode step of the gated GQA mixer core (vx27_qfwd.c:172-211):
+ * rmsn q,k -> RoPE at pos -> append k,v (bf16) at pos -> softmax attention
+ * over positions 0..pos -> * sigmoid(gate). */
+int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d);
+
+/* Copy n rows of fp32 [n][n_kv][hd] K and V (positions p0..p0+n-1 of
+ * sequence b) into / out of the cache format, rounding to bf16 on write. */
+int vx27_hip_kv_write(vx27_hip_ctx *ctx, uint16_t *k_cache, uint16_t *v_cache, int B_total,
+                      int n_kv, int hd, int L, int b, int p0, int n,
+                      const float *k_rows, const float *v_rows);
+int vx27_hip_kv_read(vx27_hip_ctx *ctx, const uint16_t *k_cache, const uint16_t *v_cache,
+                     int B_total, int n_kv, int hd, int L, int b, int p0, int n,
+                     float *k_rows, float *v_rows);
+
+/* RoPE cos/sin tables on the device for n positions (device int array):
+ * cos/sin [n][rope_dim/2].  The frequency table powf(theta, -2i/rope_dim) is
+ * evaluated on the host exactly as vx27_rope.c:11; the angle is the same
+ * float product; cos/sin are the device's float functions. */
+int vx27_hip_rope_table(vx27_hip_ctx *ctx, const int *pos, int n, int rope_dim,
+                        float theta, float yarn, float *cosv, float *sinv);
+
+/* ------------------------------------ device forms of the reference API
+ * Same arguments, sizes and arithmetic as the reference function named, on
+ * device pointers.  The host-pointer drop-ins of vx27_deltanet.h, vx27_gqa.h
+ * and vx27_rope.h stage their buffers and call these. */
+/* vx27_deltanet_step_exact (vx27_deltanet.c:71-102) with decay = exp(g_log)
+ * given (the drop-in evaluates it with the host's exp); hd in [1, 256]. */
+int vx27_hip_step_exact(vx27_hip_ctx *ctx, float *S, const float *q, const float *k,
+                        const float *v, double beta, double decay, float *o, int hd);
+/* vx27_deltanet_update_{ref,tiled} (variant 0) / _avx2 (variant 1, fused
+ * multiply-add) -- vx27_deltanet.c:15-19, vx27_deltanet_avx2.c:6-24 */
+int vx27_hip_update_simple(vx27_hip_ctx *ctx, float *S, const float *k, const float *v,
+                           float decay, int hd, int variant);
+/* vx27_deltanet_retrieve_ref (0) / _avx2 (1) / _tiled (2) -- vx27_deltanet.c:20-49,
+ * vx27_deltanet_avx2.c:28-45 */
+int vx27_hip_retrieve_simple(vx27_hip_ctx *ctx, const float *S, const float *q, float *o,
+                             int hd, int variant);
+int vx27_hip_l2norm(vx27_hip_ctx *ctx, const float *x, float *y, int n);  /* vx27_deltanet.c:51-56 */
+int vx27_hip_rmsnorm(vx27_hip_ctx *ctx, const float *x, const float *w, float *y, int n,
+                     float eps);                                         /* vx27_gqa.c:10-15 */
+int vx27_hip_conv1d_step(vx27_hip_ctx *ctx, float *state, const float *x, const float *w,
+                         float *y, int C, int apply_silu);               /* vx27_deltanet.c:106-122 */
+int vx27_hip_rope_apply(vx27_hip_ctx *ctx, float *v, int n_heads, int head_dim, int rope_dim,
+                        const float *cosv, const float *sinv);           /* vx27_rope.c:18-29 */
+/* vx27_attn_1q (vx27_gqa.c:17-45) without its 1024-position cap, reentrant. */
+int vx27_hip_attn_1q(vx27_hip_ctx *ctx, const float *q, const float *kcache,
+                     const float *vcache, int n_pos, float *out);
+/* Context-owned device staging buffer of at least `bytes` for host-pointer
+ * callers (valid until the next vx27_hip_staging call on ctx). */
+int vx27_hip_staging(vx27_hip_ctx *ctx, size_t bytes, void **dptr);
+int vx27_hip_get_error_mode(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif

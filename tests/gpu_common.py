@@ -1,0 +1,80 @@
+"""Helpers shared by the GPU parity tests: oracle runs over the same inputs."""
+from __future__ import annotations
+
+import ctypes as C
+import sys
+
+import numpy as np
+
+from oracle import oracle as O
+
+
+def say(*a):
+    print(*a, flush=True)
+    sys.stdout.flush()
+
+
+def oracle_dn(d, flags, B, nqk, nv, steps, hd=128, threads=None):
+    """Run the oracle's DeltaNet decode (orc_dn_run) on dict d of a workload;
+    returns (out [steps][B][nv][hd], S, conv_state)."""
+    S = np.ascontiguousarray(d["S0"], np.float32).copy()
+    C_ = 2 * nqk * hd + nv * hd
+    conv = np.ascontiguousarray(d.get("conv0", np.zeros((B, C_, 3), np.float32)), np.float32).copy()
+    out = np.empty((steps, B, nv, hd), np.float32)
+    keep = {}
+
+    def p(name):
+        if name not in d or d[name] is None:
+            return None
+        keep[name] = np.ascontiguousarray(d[name], np.float32)
+        return keep[name].ctypes.data
+
+    r = O.DnRunArgs(B, nqk, nv, hd, steps, flags, threads or O.default_threads(),
+                    S.ctypes.data, conv.ctypes.data, p("conv_w"), p("x"), p("q"), p("k"), p("v"),
+                    p("a"), p("b"), p("A_log"), p("dt_bias"), p("norm_w"), p("z"), out.ctypes.data)
+    secs = O.lib().orc_dn_run(C.byref(r))
+    return out, S, conv, secs
+
+
+def maxabs(a, b):
+    return float(np.max(np.abs(np.asarray(a, np.float64) - np.asarray(b, np.float64))))
+
+
+def bitexact_frac(a, b):
+    return float(np.mean(np.asarray(a) == np.asarray(b)))
+
+
+def oracle_gqa_decode(d, Lcap, threads=None):
+    """Oracle for one gated-GQA decode step of every sequence of workload d
+    (gqa_decode): bf16 cache [B][Lcap][n_kv][hd] holding the prefix, append at
+    pos, attend 0..pos (double dot), gate.  Returns (out [B][n_q][hd],
+    appended k row, v row) per sequence."""
+    qg = np.ascontiguousarray(d["qg"], np.float32)
+    B, n_q, two_hd = qg.shape
+    hd = two_hd // 2
+    n_kv = d["k_new"].shape[1]
+    outs = np.empty((B, n_q, hd), np.float32)
+    kr = np.empty((B, n_kv, hd), np.uint16)
+    vr = np.empty((B, n_kv, hd), np.uint16)
+    qn = np.ascontiguousarray(d["q_norm_w"], np.float32)
+    kn = np.ascontiguousarray(d["k_norm_w"], np.float32)
+    for b in range(B):
+        pos = int(d["pos"][b])
+        kc = np.zeros((Lcap, n_kv, hd), np.uint16)
+        vc = np.zeros((Lcap, n_kv, hd), np.uint16)
+        nk = d["K"].shape[1]
+        kc[:nk] = d["K"][b]
+        vc[:nk] = d["V"][b]
+        cs, sn = O.rope_cos_sin(pos)
+        cfg = O.GqaCfg(n_q, n_kv, hd, 64, 1, qn.ctypes.data, kn.ctypes.data, kc.ctypes.data,
+                       vc.ctypes.data, n_kv * hd, hd, n_kv * hd, hd)
+        out = np.empty((n_q, hd), np.float32)
+        k1 = np.ascontiguousarray(d["k_new"][b], np.float32)
+        v1 = np.ascontiguousarray(d["v_new"][b], np.float32)
+        qb = np.ascontiguousarray(qg[b])
+        O.lib().orc_gqa_token(C.byref(cfg), qb.reshape(-1), 2 * hd, qb.ctypes.data + hd * 4, 2 * hd,
+                              k1.reshape(-1), v1.reshape(-1), pos, cs, sn, out.reshape(-1))
+        outs[b] = out
+        kr[b] = kc[pos]
+        vr[b] = vc[pos]
+    return outs, kr, vr

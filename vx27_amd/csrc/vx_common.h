@@ -1,0 +1,103 @@
+// Internal helpers shared by the HIP translation units of libvx27_hip.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+#include <stdio.h>
+
+#include "vx27_hip.h"
+
+// one profiled launch: events recorded around it on the context stream
+struct vx_prof_rec {
+    const char *name;
+    hipEvent_t e0, e1;
+};
+
+struct vx27_hip_ctx {
+    int device;
+    hipStream_t stream;      // stream used for every enqueue
+    hipStream_t own_stream;  // created by vx27_hip_open
+    // grow-only device scratch (split-K partials, staging), owned by the context
+    void *scratch;
+    size_t scratch_bytes;
+    // small staging for the drop-ins (host-pointer API)
+    void *stage;
+    size_t stage_bytes;
+    // kernel profiler (vx27_hip_prof_*): off unless enabled
+    int prof_on;
+    vx_prof_rec *prof;
+    int prof_n, prof_cap;
+};
+
+// thread-local error message
+void vx_set_error(const char *fmt, ...) __attribute__((format(printf, 1, 2)));
+
+#define VX_HIP(expr)                                                                   \
+    do {                                                                               \
+        hipError_t e_ = (expr);                                                        \
+        if (e_ != hipSuccess) {                                                        \
+            vx_set_error("%s:%d %s: %s", __FILE__, __LINE__, #expr, hipGetErrorString(e_)); \
+            return -1;                                                                 \
+        }                                                                              \
+    } while (0)
+
+#define VX_REQUIRE(cond, ...)          \
+    do {                               \
+        if (!(cond)) {                 \
+            vx_set_error(__VA_ARGS__); \
+            return -1;                 \
+        }                              \
+    } while (0)
+
+#define VX_LAUNCHED(name)                                                                    \
+    do {                                                                                     \
+        hipError_t e_ = hipGetLastError();                                                   \
+        if (e_ != hipSuccess) {                                                              \
+            vx_set_error("%s:%d launch of %s failed: %s", __FILE__, __LINE__, name,          \
+                         hipGetErrorString(e_));                                             \
+            return -1;                                                                       \
+        }                                                                                    \
+    } while (0)
+
+// Kernel profiler hooks (see vx27_hip_prof_enable).
+void vx_prof_begin(vx27_hip_ctx *ctx);
+void vx_prof_end(vx27_hip_ctx *ctx, const char *name);
+
+// Launch `kernel` on the context stream (profiled when enabled) and check it.
+#define VX_LAUNCH(ctx, kernel, grid, block, ...)                                  \
+    do {                                                                          \
+        vx_prof_begin(ctx);                                                       \
+        hipLaunchKernelGGL(kernel, grid, block, 0, (ctx)->stream, __VA_ARGS__);   \
+        vx_prof_end(ctx, #kernel);                                                \
+        VX_LAUNCHED(#kernel);                                                     \
+    } while (0)
+
+// Make the context's device current (contexts may live on different devices).
+int vx_ctx_enter(vx27_hip_ctx *ctx);
+// Device scratch of at least `bytes`, owned by ctx (synchronises before growing).
+int vx_ctx_scratch(vx27_hip_ctx *ctx, size_t bytes, void **out);
+// Host-pointer staging buffer of at least `bytes` (device memory).
+int vx_ctx_stage(vx27_hip_ctx *ctx, size_t bytes, void **out);
+
+// ------------------------------------------------------------ device math
+__device__ __forceinline__ float vx_bf16_to_f32(uint16_t h) {
+    return __uint_as_float((uint32_t)h << 16);
+}
+// round-to-nearest-even narrowing (NaN kept quiet)
+__device__ __forceinline__ uint16_t vx_f32_to_bf16(float x) {
+    uint32_t u = __float_as_uint(x);
+    if ((u & 0x7fffffffu) > 0x7f800000u) return (uint16_t)((u >> 16) | 0x40u);
+    u += 0x7fffu + ((u >> 16) & 1u);
+    return (uint16_t)(u >> 16);
+}
+
+// Full-wave (64 lanes) sums and maxima through cross-lane shuffles.
+__device__ __forceinline__ double vx_wave_sum_f64(double v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+__device__ __forceinline__ float vx_wave_sum_f32(float v) {
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}

@@ -1,0 +1,328 @@
+// Gated DeltaNet recurrent decode for gfx950.
+//
+// Work decomposition: one workgroup (128 lanes, 2 waves) per (sequence b,
+// value head vh).  Lane j owns column j of the head's 128x128 state S[i][j]
+// (i = key dim, j = value dim): the column lives in 128 VGPRs for all steps
+// of a call, so kv[j] = sum_i S[i][j] kn[i] and o[j] = sum_i S[i][j] qn[i] are
+// lane-local sums in the reference's row order (vx27_deltanet.c:84-101) with
+// no cross-lane reduction.  S is read and written once per call through a
+// buffer resource (one lane offset, scalar row offsets), coalesced 512 bytes
+// per row.
+//
+// The causal conv (vx27_deltanet.c:106-122) is fused when every workgroup
+// owns the conv channels it reads, i.e. nv == nqk (q_g, k_g, v_g all belong
+// to head g).  With nv > nqk several value heads read the same q/k channels,
+// so a channel-parallel conv kernel runs first and writes the activations.
+//
+// Arithmetic follows the reference op for op: this file is compiled with
+// -ffp-contract=off, double accumulations stay double, and each float
+// rounding of the reference happens at the same place.  Sums of squares over
+// a head's 128 elements are wave trees in double (the reference sums them
+// serially; the two can differ in the last bit of the double sum, far below
+// the float rounding that follows).
+#include "vx_common.h"
+
+namespace {
+
+constexpr int HD = 128;
+
+struct DnArgs {
+    int B, nqk, nv, steps;
+    unsigned flags;
+    int fused_conv;
+    float *S;
+    float *conv_state;
+    const void *conv_w;
+    int conv_bf16;
+    // activations: either x (fused conv) or q/k/v (already convolved or given)
+    const float *x;
+    const float *q, *k, *v;
+    size_t q_tok, k_tok, v_tok;   // per-(t,b) stride of q, k, v in floats
+    const double2 *gates;         // [steps][B][nv] (beta, decay)
+    const float *norm_w, *z;
+    float *out;
+};
+
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+
+__device__ __forceinline__ double softplus_d(double x) {
+    if (x > 20.0) return x;
+    if (x < -20.0) return exp(x);
+    return log(1.0 + exp(x));
+}
+
+// Gate mapping of vx27_deltanet.c:65-69 for every (token, sequence, value
+// head): beta = sigmoid(b), decay = exp(g_log) with g_log = -exp(A_log) *
+// softplus(a + dt_bias) (decay as vx27_deltanet.c:82).  A kernel of its own
+// so the recurrence kernel carries no transcendental code in its registers.
+__global__ __launch_bounds__(256) void dn_gate_kernel(int n, int nv, const float *a, const float *b,
+                                                      const float *A_log, const float *dt_bias,
+                                                      double2 *gates) {
+    const int e = blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= n) return;
+    const int vh = e % nv;
+    const double beta = 1.0 / (1.0 + exp(-(double)b[e]));
+    const double glog = -exp((double)A_log[vh]) * softplus_d((double)a[e] + (double)dt_bias[vh]);
+    gates[e] = make_double2(beta, exp(glog));
+}
+
+// one causal-conv step of a channel: window (c0 oldest, c1, c2, x)
+__device__ __forceinline__ float conv_step(float c[3], const float w[4], float x) {
+    float acc = w[0] * c[0];
+    acc = acc + w[1] * c[1];
+    acc = acc + w[2] * c[2];
+    acc = acc + w[3] * x;
+    c[0] = c[1];
+    c[1] = c[2];
+    c[2] = x;
+    return silu_f(acc);
+}
+
+__device__ __forceinline__ void load_conv_w(const void *w, int bf16, size_t ch, float out[4]) {
+    if (bf16) {
+        const uint16_t *p = (const uint16_t *)w + ch * 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++) out[t] = vx_bf16_to_f32(p[t]);
+    } else {
+        const float *p = (const float *)w + ch * 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++) out[t] = p[t];
+    }
+}
+
+// Sum of two per-lane doubles over the block's 128 lanes (2 waves); every
+// thread must call it (barrier inside).  slot is private to one call site.
+__device__ __forceinline__ void block_sum2(double &u, double &v, double (*slot)[2]) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const double su = vx_wave_sum_f64(u), sv = vx_wave_sum_f64(v);
+    if (lane == 0) {
+        slot[wave][0] = su;
+        slot[wave][1] = sv;
+    }
+    __syncthreads();
+    u = slot[0][0] + slot[1][0];
+    v = slot[0][1] + slot[1][1];
+}
+
+__global__ __launch_bounds__(HD) void dn_decode_kernel(DnArgs a) {
+    const int j = threadIdx.x;                 // owned column / channel
+    const int b = blockIdx.x / a.nv;
+    const int vh = blockIdx.x % a.nv;
+    const int g = vh * a.nqk / a.nv;           // QK head (vx27_qfwd.c:137)
+    const int qd = a.nqk * HD, vd = a.nv * HD, C = 2 * qd + vd;
+
+    __shared__ float s_qn[HD], s_kn[HD];
+    __shared__ double s_red[4][2][2];
+
+    // ---- state column into registers
+    const __amdgpu_buffer_rsrc_t Sr = __builtin_amdgcn_make_buffer_rsrc(
+        a.S + ((size_t)b * a.nv + vh) * HD * HD, 0, HD * HD * 4, 0x00020000);
+    float Sc[HD];
+#pragma unroll
+    for (int i = 0; i < HD; i++)
+        Sc[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(Sr, j * 4, i * HD * 4, 0));
+
+    // ---- owned conv channels (fused conv: nv == nqk, so g == vh)
+    const bool conv = a.fused_conv != 0;
+    float cq[3] = {0, 0, 0}, ck[3] = {0, 0, 0}, cv[3] = {0, 0, 0};
+    float wq[4] = {0, 0, 0, 0}, wk[4] = {0, 0, 0, 0}, wv[4] = {0, 0, 0, 0};
+    const size_t chq = (size_t)g * HD + j, chk = (size_t)qd + g * HD + j,
+                 chv = (size_t)2 * qd + (size_t)vh * HD + j;
+    float *cst = conv ? a.conv_state + (size_t)b * C * 3 : nullptr;
+    if (conv) {
+        load_conv_w(a.conv_w, a.conv_bf16, chq, wq);
+        load_conv_w(a.conv_w, a.conv_bf16, chk, wk);
+        load_conv_w(a.conv_w, a.conv_bf16, chv, wv);
+#pragma unroll
+        for (int t = 0; t < 3; t++) {
+            cq[t] = cst[chq * 3 + t];
+            ck[t] = cst[chk * 3 + t];
+            cv[t] = cst[chv * 3 + t];
+        }
+    }
+    const float nw = a.norm_w ? a.norm_w[j] : 1.0f;
+    const float qs = 1.0f / sqrtf((float)HD);
+
+    for (int t = 0; t < a.steps; t++) {
+        const size_t sb = (size_t)t * a.B + b;
+        const double2 gt = a.gates[sb * a.nv + vh];   // uniform address: scalar load
+        // ---- activations of this token
+        float qa, ka, va;
+        if (conv) {
+            const float *x = a.x + sb * C;
+            qa = conv_step(cq, wq, x[chq]);
+            ka = conv_step(ck, wk, x[chk]);
+            va = conv_step(cv, wv, x[chv]);
+        } else {
+            qa = a.q[sb * a.q_tok + (size_t)g * HD + j];
+            ka = a.k[sb * a.k_tok + (size_t)g * HD + j];
+            va = a.v[sb * a.v_tok + (size_t)vh * HD + j];
+        }
+        // ---- q/k normalisation chain
+        if (a.flags & VX27_DN_PRE_RMS) {       // rmsn(x)*(1+w), vx27_qfwd.c:32-39,123
+            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+            block_sum2(sq, sk, s_red[0]);
+            const float iq = 1.0f / sqrtf((float)(sq / HD) + 1e-6f);
+            const float ik = 1.0f / sqrtf((float)(sk / HD) + 1e-6f);
+            qa = (qa * iq) * (nw + 1.0f);
+            ka = (ka * ik) * (nw + 1.0f);
+        }
+        if (a.flags & VX27_DN_PRE_L2) {        // l2norm + q/sqrt(hd), vx27_qfwd.c:124-130
+            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+            block_sum2(sq, sk, s_red[1]);
+            qa = qa * (1.0f / sqrtf((float)sq + 1e-6f));
+            ka = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+            qa = qa * qs;
+        }
+        {                                       // inside step_exact, vx27_deltanet.c:77-80
+            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+            block_sum2(sq, sk, s_red[2]);
+            const float qn = qa * (1.0f / sqrtf((float)sq + 1e-6f));
+            s_qn[j] = qn * qs;
+            s_kn[j] = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+        }
+        __syncthreads();
+        const double beta = gt.x, decay = gt.y;
+        // ---- S *= decay ; kv = S^T kn   (double, rows in order)
+        double kv = 0.0;
+#pragma unroll
+        for (int i = 0; i < HD; i += 4) {
+            const float4 kn4 = *(const float4 *)&s_kn[i];
+            const float knv[4] = {kn4.x, kn4.y, kn4.z, kn4.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float sd = (float)((double)Sc[i + u] * decay);
+                Sc[i + u] = sd;
+                kv = kv + (double)sd * (double)knv[u];
+            }
+        }
+        // ---- S += kn (x) (v - kv)*beta ; o = S^T qn
+        // (compiler barrier: kn is re-read from LDS instead of held in registers)
+        __asm__ volatile("" ::: "memory");
+        const double dl = ((double)va - kv) * beta;
+        double o = 0.0;
+#pragma unroll
+        for (int i = 0; i < HD; i += 4) {
+            const float4 kn4 = *(const float4 *)&s_kn[i];
+            const float4 qn4 = *(const float4 *)&s_qn[i];
+            const float knv[4] = {kn4.x, kn4.y, kn4.z, kn4.w};
+            const float qnv[4] = {qn4.x, qn4.y, qn4.z, qn4.w};
+#pragma unroll
+            for (int u = 0; u < 4; u++) {
+                const float su = (float)((double)Sc[i + u] + (double)knv[u] * dl);
+                Sc[i + u] = su;
+                o = o + (double)su * (double)qnv[u];
+            }
+        }
+        float of = (float)o;
+        // ---- gated output norm (vx27_qfwd.c:147-151)
+        if (a.flags & VX27_DN_OUT_GATE) {
+            double so = (double)of * (double)of, unused = 0.0;
+            block_sum2(so, unused, s_red[3]);
+            const float is = 1.0f / sqrtf((float)(so / HD) + 1e-6f);
+            const float zz = a.z[sb * vd + (size_t)vh * HD + j];
+            of = ((of * is) * nw) * silu_f(zz);
+        } else {
+            __syncthreads();   // s_qn/s_kn are rewritten by the next step
+        }
+        a.out[sb * vd + (size_t)vh * HD + j] = of;
+    }
+
+    // ---- write back state and conv state
+#pragma unroll
+    for (int i = 0; i < HD; i++)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Sc[i]), Sr, j * 4, i * HD * 4, 0);
+    if (conv) {
+#pragma unroll
+        for (int t = 0; t < 3; t++) {
+            cst[chq * 3 + t] = cq[t];
+            cst[chk * 3 + t] = ck[t];
+            cst[chv * 3 + t] = cv[t];
+        }
+    }
+}
+
+// Channel-parallel causal conv over `steps` tokens: one thread per (b, c),
+// state carried in registers; act [steps][B][C] receives silu(conv).
+struct ConvArgs {
+    int B, C, steps, w_bf16;
+    float *state;
+    const void *w;
+    const float *x;
+    float *act;
+};
+__global__ __launch_bounds__(256) void dn_conv_kernel(ConvArgs a) {
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= (size_t)a.B * a.C) return;
+    const int b = (int)(id / a.C), c = (int)(id % a.C);
+    float w[4], st[3];
+    load_conv_w(a.w, a.w_bf16, (size_t)c, w);
+    float *sp = a.state + ((size_t)b * a.C + c) * 3;
+    st[0] = sp[0]; st[1] = sp[1]; st[2] = sp[2];
+    for (int t = 0; t < a.steps; t++) {
+        const size_t e = ((size_t)t * a.B + b) * a.C + c;
+        a.act[e] = conv_step(st, w, a.x[e]);
+    }
+    sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
+}
+
+}  // namespace
+
+extern "C" int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(d != nullptr, "vx27_hip_dn_decode: null descriptor");
+    VX_REQUIRE(d->hd == HD, "vx27_hip_dn_decode: hd must be 128 (got %d)", d->hd);
+    VX_REQUIRE(d->B >= 1 && d->nqk >= 1 && d->nv >= 1 && d->steps >= 1,
+               "vx27_hip_dn_decode: B, nqk, nv, steps must be >= 1");
+    VX_REQUIRE(d->nv % d->nqk == 0, "vx27_hip_dn_decode: nv must be a multiple of nqk (nqk=%d nv=%d)",
+               d->nqk, d->nv);
+    VX_REQUIRE((d->flags & ~15u) == 0, "vx27_hip_dn_decode: unknown flags %#x", d->flags);
+    VX_REQUIRE(d->S && d->out && d->a && d->b && d->A_log && d->dt_bias,
+               "vx27_hip_dn_decode: S, out, a, b, A_log, dt_bias are required");
+    const bool conv = (d->flags & VX27_DN_CONV) != 0;
+    if (conv) {
+        VX_REQUIRE(d->x && d->conv_state && d->conv_w, "vx27_hip_dn_decode: conv needs x, conv_state, conv_w");
+        VX_REQUIRE(d->conv_w_dtype == VX27_F32 || d->conv_w_dtype == VX27_BF16,
+                   "vx27_hip_dn_decode: conv_w_dtype must be VX27_F32 or VX27_BF16");
+    } else {
+        VX_REQUIRE(d->q && d->k && d->v, "vx27_hip_dn_decode: q, k, v are required without conv");
+    }
+    if (d->flags & (VX27_DN_PRE_RMS | VX27_DN_OUT_GATE))
+        VX_REQUIRE(d->norm_w != nullptr, "vx27_hip_dn_decode: norm_w required by PRE_RMS/OUT_GATE");
+    if (d->flags & VX27_DN_OUT_GATE) VX_REQUIRE(d->z != nullptr, "vx27_hip_dn_decode: z required by OUT_GATE");
+
+    const int qd = d->nqk * HD, vd = d->nv * HD, C = 2 * qd + vd;
+    DnArgs a = {};
+    a.B = d->B; a.nqk = d->nqk; a.nv = d->nv; a.steps = d->steps; a.flags = d->flags;
+    a.S = d->S; a.conv_state = d->conv_state; a.conv_w = d->conv_w;
+    a.conv_bf16 = d->conv_w_dtype == VX27_BF16;
+    a.norm_w = d->norm_w; a.z = d->z; a.out = d->out;
+    const bool sep_conv = conv && d->nv != d->nqk;
+    if (!conv) {
+        a.q = d->q; a.k = d->k; a.v = d->v;
+        a.q_tok = (size_t)qd; a.k_tok = (size_t)qd; a.v_tok = (size_t)vd;
+    } else if (!sep_conv) {
+        a.fused_conv = 1;
+        a.x = d->x;
+    }
+    // scratch: gates [steps][B][nv] double2, then (unfused conv) activations
+    const size_t n_gate = (size_t)d->steps * d->B * d->nv;
+    const size_t gate_bytes = (n_gate * sizeof(double2) + 255) & ~(size_t)255;
+    const size_t act_elems = sep_conv ? (size_t)d->steps * d->B * C : 0;
+    void *scr;
+    if (vx_ctx_scratch(ctx, gate_bytes + act_elems * sizeof(float), &scr)) return -1;
+    double2 *gates = (double2 *)scr;
+    VX_LAUNCH(ctx, dn_gate_kernel, dim3((unsigned)((n_gate + 255) / 256)), dim3(256), (int)n_gate, d->nv, d->a, d->b, d->A_log, d->dt_bias, gates);
+    a.gates = gates;
+    if (sep_conv) {
+        // shared q/k channels: convolve all channels first
+        float *act = (float *)((char *)scr + gate_bytes);
+        ConvArgs ca = {d->B, C, d->steps, a.conv_bf16, d->conv_state, d->conv_w, d->x, act};
+        const size_t nthr = (size_t)d->B * C;
+        VX_LAUNCH(ctx, dn_conv_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), ca);
+        a.q = act; a.k = act + qd; a.v = act + 2 * qd;
+        a.q_tok = a.k_tok = a.v_tok = (size_t)C;
+    }
+    VX_LAUNCH(ctx, dn_decode_kernel, dim3((unsigned)(d->B * d->nv)), dim3(HD), a);
+    return 0;
+}

@@ -1,0 +1,416 @@
+// Gated GQA decode over a bf16 KV cache for gfx950 (split-K flash decode).
+//
+// Reference semantics (vx27_qfwd.c:172-211): rmsn(q)*(1+w) and rmsn(k)*(1+w)
+// per head, NeoX RoPE on the first rope_dim dims, append k,v at position pos,
+// softmax(q.k / sqrt(hd)) over positions 0..pos, P.V, then * sigmoid(gate).
+//
+// Kernels per call:
+//   gqa_prep     one workgroup per (sequence, head): norm + RoPE of q (kept
+//                fp32 in scratch) and of the new k; k,v rounded to bf16 and
+//                appended to the cache.
+//   gqa_split    one wave per (split, KV head, sequence): streams its share of
+//                the cache once for all n_q/n_kv query heads of the group with
+//                v_mfma_f32_16x16x32_bf16, online softmax in fp32, writes a
+//                partial (m, l, O) per query head.
+//   gqa_combine  merges the partials, divides by l, applies sigmoid(gate).
+//
+// Tile algebra (32 keys per tile, query heads padded to 16):
+//   S^T[key][q] = K[key][:] . Q^T[:][q]    two 16-row MFMA blocks r=0,1 over
+//                                           8 k-steps of 32 dims.  Row m of
+//                                           block r loads key 8(m/4)+4r+m%4, so
+//                                           the C layout (lane (g,n) holds rows
+//                                           4g..4g+3) leaves lane (g,n) with keys
+//                                           8g..8g+7 of query head n.
+//   O^T[dim][q] += V^T[dim][key] . P^T[key][q]   16 MFMAs (16 dims each); the
+//                                           B operand of lane (g,n) is exactly
+//                                           its 8 probabilities, the A operand
+//                                           is 16 contiguous bytes of the
+//                                           dim-major V block.
+#include <math.h>
+
+#include "vx_common.h"
+
+namespace {
+
+constexpr int HDG = 256;      // head dim of the gated GQA layers
+constexpr int TILE = 32;      // keys per tile (V block size)
+constexpr int MAXR = 128;     // max rope_dim/2 carried in kernel arguments
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+struct RopeTab {
+    float freq[MAXR];
+};
+
+__device__ __forceinline__ size_t k_index(int B_unused, int n_kv, int L, int b, int h, int p, int i) {
+    (void)B_unused;
+    return (((size_t)b * n_kv + h) * L + p) * HDG + i;
+}
+__device__ __forceinline__ size_t v_index(int n_kv, int L, int b, int h, int p, int i) {
+    return ((((size_t)b * n_kv + h) * (L / TILE) + p / TILE) * HDG + i) * TILE + (p % TILE);
+}
+
+// Block-wide double sum over 256 threads (4 waves); contains barriers.
+__device__ __forceinline__ double block_sum256(double v, double *red) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    v = vx_wave_sum_f64(v);
+    __syncthreads();
+    if (lane == 0) red[wave] = v;
+    __syncthreads();
+    return ((red[0] + red[1]) + red[2]) + red[3];
+}
+
+struct PrepArgs {
+    int B, n_q, n_kv, rope_dim, L;
+    unsigned flags;
+    float yarn;
+    const int *pos;
+    const float *q;
+    size_t q_ss, q_hs;
+    const float *k_new, *v_new, *q_norm_w, *k_norm_w;
+    uint16_t *k_cache, *v_cache;
+    float *q_out;   // [B][n_q][256]
+    RopeTab rope;
+};
+
+// grid (n_q + n_kv, B), block 256
+__global__ __launch_bounds__(256) void gqa_prep(PrepArgs a) {
+    const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
+    __shared__ double red[4];
+    __shared__ float row[HDG];
+    __shared__ float cs[MAXR], sn[MAXR];
+    // positions outside the cache are clamped so no access leaves the buffers;
+    // the host contract is 0 <= pos < L
+    const int pos = min(max(a.pos[b], 0), a.L - 1);
+    const int half = a.rope_dim / 2;
+    if (i < half) {
+        const float ps = (float)pos / a.yarn;
+        const float ang = ps * a.rope.freq[i];
+        cs[i] = cosf(ang);
+        sn[i] = sinf(ang);
+    }
+    const bool is_q = h < a.n_q;
+    const int hk = h - a.n_q;
+    const float x = is_q ? a.q[(size_t)b * a.q_ss + (size_t)h * a.q_hs + i]
+                         : a.k_new[((size_t)b * a.n_kv + hk) * HDG + i];
+    const float w = is_q ? a.q_norm_w[i] : a.k_norm_w[i];
+    const double ss = block_sum256((double)x * (double)x, red);
+    const float s = 1.0f / sqrtf((float)(ss / HDG) + 1e-6f);
+    const float y = (a.flags & VX27_GQA_NORM_W) ? (x * s) * w : (x * s) * (w + 1.0f);
+    row[i] = y;
+    __syncthreads();
+    float r = y;
+    if (i < half) {
+        r = row[i] * cs[i] - row[i + half] * sn[i];
+    } else if (i < 2 * half) {
+        r = row[i - half] * sn[i - half] + row[i] * cs[i - half];
+    }
+    if (is_q) {
+        a.q_out[((size_t)b * a.n_q + h) * HDG + i] = r;
+    } else {
+        a.k_cache[k_index(a.B, a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(r);
+        const float vv = a.v_new[((size_t)b * a.n_kv + hk) * HDG + i];
+        a.v_cache[v_index(a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(vv);
+    }
+}
+
+struct SplitArgs {
+    int B, n_q, n_kv, L, n_split;
+    const int *pos;
+    const float *q_rot;          // [B][n_q][256]
+    const uint16_t *k_cache, *v_cache;
+    float *part_o;               // [B][n_kv][n_split][qg][256]
+    float *part_ml;              // [B][n_kv][n_split][qg][2]
+};
+
+__device__ __forceinline__ bf16x8_t load_bf16x8(const uint16_t *p) {
+    return *(const bf16x8_t *)p;
+}
+
+// grid (n_split, n_kv, B), block 64 (one wave)
+__global__ __launch_bounds__(64) void gqa_split(SplitArgs a) {
+    const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
+    const int lane = threadIdx.x, g = lane >> 4, n = lane & 15;
+    const int qg = a.n_q / a.n_kv;
+    const int n_keys = min(max(a.pos[b], 0), a.L - 1) + 1;
+    const int n_tiles = (n_keys + TILE - 1) / TILE;
+    const int per = (n_tiles + a.n_split - 1) / a.n_split;
+    const int t0 = split * per;
+    const int t1 = min(n_tiles, t0 + per);
+
+    // Q^T operand: lane (g,n) holds dims 32s + 8g + 0..7 of query head n
+    bf16x8_t qB[8];
+    {
+        const bool live = n < qg;
+        const float *qp = a.q_rot + ((size_t)b * a.n_q + (size_t)kvh * qg + (live ? n : 0)) * HDG;
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                const float v = live ? qp[32 * s + 8 * g + e] : 0.0f;
+                qB[s][e] = (__bf16)v;
+            }
+        }
+    }
+    floatx4_t acc[16];
+#pragma unroll
+    for (int t = 0; t < 16; t++) acc[t] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+    float m_run = -INFINITY, l_run = 0.0f;
+    const float scale_log2 = 0.0625f * 1.4426950408889634f;   // 1/sqrt(256) * log2(e)
+
+    const uint16_t *Kb = a.k_cache + ((size_t)b * a.n_kv + kvh) * (size_t)a.L * HDG;
+    const uint16_t *Vb = a.v_cache + ((size_t)b * a.n_kv + kvh) * (size_t)a.L * HDG;
+    // A-operand row m of block r holds key 8(m/4) + 4r + m%4
+    const int krow0 = 8 * (n >> 2) + (n & 3);
+
+    for (int tile = t0; tile < t1; tile++) {
+        const int key0 = tile * TILE;
+        // ---- scores S^T (two 16-key blocks)
+        floatx4_t sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
+        const uint16_t *kr0 = Kb + (size_t)(key0 + krow0) * HDG + 8 * g;
+        const uint16_t *kr1 = kr0 + 4 * HDG;
+        bf16x8_t ka[8], kb[8];
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            ka[s] = load_bf16x8(kr0 + 32 * s);
+            kb[s] = load_bf16x8(kr1 + 32 * s);
+        }
+        // V^T operand for this tile: 16 dims x 32 keys per MFMA
+        const uint16_t *vt = Vb + (size_t)tile * HDG * TILE + (size_t)n * TILE + 8 * g;
+        bf16x8_t va[16];
+#pragma unroll
+        for (int t = 0; t < 16; t++) va[t] = load_bf16x8(vt + (size_t)t * 16 * TILE);
+#pragma unroll
+        for (int s = 0; s < 8; s++) {
+            sc0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka[s], qB[s], sc0, 0, 0, 0);
+            sc1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kb[s], qB[s], sc1, 0, 0, 0);
+        }
+        // lane (g,n): keys key0 + 8g + 0..3 (sc0) and + 4..7 (sc1), query head n
+        float sv[8];
+        const int kbase = key0 + 8 * g;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            sv[e] = (kbase + e < n_keys) ? sc0[e] * scale_log2 : -INFINITY;
+            sv[4 + e] = (kbase + 4 + e < n_keys) ? sc1[e] * scale_log2 : -INFINITY;
+        }
+        float mt = sv[0];
+#pragma unroll
+        for (int e = 1; e < 8; e++) mt = fmaxf(mt, sv[e]);
+        mt = fmaxf(mt, __shfl_xor(mt, 16, 64));
+        mt = fmaxf(mt, __shfl_xor(mt, 32, 64));
+        const float m_new = fmaxf(m_run, mt);
+        const float alpha = (m_new == -INFINITY) ? 1.0f : exp2f(m_run - m_new);
+        bf16x8_t pB;
+        float lsum = 0.0f;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const float p = (m_new == -INFINITY) ? 0.0f : exp2f(sv[e] - m_new);
+            lsum += p;
+            pB[e] = (__bf16)p;
+        }
+        l_run = l_run * alpha + lsum;
+        m_run = m_new;
+        if (__any(alpha != 1.0f)) {
+#pragma unroll
+            for (int t = 0; t < 16; t++) acc[t] *= alpha;
+        }
+        // masked keys of the last tile: zero their V so cache garbage cannot leak
+        if (key0 + TILE > n_keys) {
+#pragma unroll
+            for (int t = 0; t < 16; t++)
+#pragma unroll
+                for (int e = 0; e < 8; e++)
+                    if (kbase + e >= n_keys) va[t][e] = (__bf16)0.0f;
+        }
+#pragma unroll
+        for (int t = 0; t < 16; t++)
+            acc[t] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(va[t], pB, acc[t], 0, 0, 0);
+    }
+    // ---- partials: lane (g,n) holds O^T[16t + 4g + i][n]
+    l_run += __shfl_xor(l_run, 16, 64);
+    l_run += __shfl_xor(l_run, 32, 64);
+    const size_t pidx = (((size_t)b * a.n_kv + kvh) * a.n_split + split) * qg;
+    if (n < qg) {
+        float *po = a.part_o + (pidx + n) * HDG;
+#pragma unroll
+        for (int t = 0; t < 16; t++) *(floatx4_t *)(po + 16 * t + 4 * g) = acc[t];
+        if (g == 0) {
+            a.part_ml[(pidx + n) * 2 + 0] = m_run;
+            a.part_ml[(pidx + n) * 2 + 1] = l_run;
+        }
+    }
+}
+
+struct CombArgs {
+    int B, n_q, n_kv, n_split;
+    const float *part_o, *part_ml;
+    const float *gate;
+    size_t g_ss, g_hs;
+    float *out;
+};
+
+// grid (n_q, B), block 256
+__global__ __launch_bounds__(256) void gqa_combine(CombArgs a) {
+    const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
+    const int qg = a.n_q / a.n_kv, kvh = h / qg, n = h % qg;
+    const size_t base = ((size_t)b * a.n_kv + kvh) * a.n_split;
+    float M = -INFINITY;
+    for (int s = 0; s < a.n_split; s++) M = fmaxf(M, a.part_ml[((base + s) * qg + n) * 2]);
+    float L = 0.0f, O = 0.0f;
+#pragma unroll 4
+    for (int s = 0; s < a.n_split; s++) {
+        const float m = a.part_ml[((base + s) * qg + n) * 2];
+        if (m == -INFINITY) continue;
+        const float w = exp2f(m - M);
+        L += a.part_ml[((base + s) * qg + n) * 2 + 1] * w;
+        O += a.part_o[((base + s) * qg + n) * HDG + i] * w;
+    }
+    const float gl = a.gate[(size_t)b * a.g_ss + (size_t)h * a.g_hs + i];
+    a.out[((size_t)b * a.n_q + h) * HDG + i] = (O / L) * (1.0f / (1.0f + expf(-gl)));
+}
+
+struct KvMoveArgs {
+    int n_kv, L, b, p0, n;
+    uint16_t *kc, *vc;
+    const uint16_t *kc_r, *vc_r;
+    const float *k_in, *v_in;
+    float *k_out, *v_out;
+};
+
+// grid (n, n_kv), block 256: write rows into the cache format
+__global__ __launch_bounds__(256) void kv_write_kernel(KvMoveArgs a) {
+    const int r = blockIdx.x, h = blockIdx.y, i = threadIdx.x, p = a.p0 + r;
+    const size_t src = ((size_t)r * a.n_kv + h) * HDG + i;
+    a.kc[k_index(0, a.n_kv, a.L, a.b, h, p, i)] = vx_f32_to_bf16(a.k_in[src]);
+    a.vc[v_index(a.n_kv, a.L, a.b, h, p, i)] = vx_f32_to_bf16(a.v_in[src]);
+}
+__global__ __launch_bounds__(256) void kv_read_kernel(KvMoveArgs a) {
+    const int r = blockIdx.x, h = blockIdx.y, i = threadIdx.x, p = a.p0 + r;
+    const size_t dst = ((size_t)r * a.n_kv + h) * HDG + i;
+    if (a.k_out) a.k_out[dst] = vx_bf16_to_f32(a.kc_r[k_index(0, a.n_kv, a.L, a.b, h, p, i)]);
+    if (a.v_out) a.v_out[dst] = vx_bf16_to_f32(a.vc_r[v_index(a.n_kv, a.L, a.b, h, p, i)]);
+}
+
+struct RopeTabArgs {
+    const int *pos;
+    int n, half;
+    float yarn;
+    float *cosv, *sinv;
+    RopeTab rope;
+};
+__global__ void rope_table_kernel(RopeTabArgs a) {
+    const int r = blockIdx.x, i = threadIdx.x;
+    if (i >= a.half) return;
+    const float ps = (float)a.pos[r] / a.yarn;
+    const float ang = ps * a.rope.freq[i];
+    a.cosv[(size_t)r * a.half + i] = cosf(ang);
+    a.sinv[(size_t)r * a.half + i] = sinf(ang);
+}
+
+// freq_i = powf(theta, -2i/rope_dim) on the host, as vx27_rope.c:11
+int fill_rope(RopeTab &t, int rope_dim, float theta) {
+    VX_REQUIRE(rope_dim >= 2 && rope_dim % 2 == 0 && rope_dim / 2 <= MAXR,
+               "rope_dim must be even and <= %d (got %d)", 2 * MAXR, rope_dim);
+    for (int i = 0; i < rope_dim / 2; i++) {
+        const float expo = (-2.0f * (float)i) / (float)rope_dim;
+        t.freq[i] = powf(theta, expo);
+    }
+    return 0;
+}
+
+}  // namespace
+
+extern "C" int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(d != nullptr, "vx27_hip_gqa_decode: null descriptor");
+    VX_REQUIRE(d->hd == HDG, "vx27_hip_gqa_decode: hd must be 256 (got %d)", d->hd);
+    VX_REQUIRE(d->B >= 1 && d->n_kv >= 1 && d->n_q >= d->n_kv && d->n_q % d->n_kv == 0 &&
+                   d->n_q / d->n_kv <= 16,
+               "vx27_hip_gqa_decode: need n_q = k*n_kv with k <= 16 (n_q=%d n_kv=%d)", d->n_q, d->n_kv);
+    VX_REQUIRE(d->L >= 64 && d->L % 64 == 0, "vx27_hip_gqa_decode: L must be a positive multiple of 64");
+    VX_REQUIRE(d->rope_dim >= 0 && d->rope_dim <= HDG, "vx27_hip_gqa_decode: bad rope_dim");
+    VX_REQUIRE(d->pos && d->q && d->gate && d->k_new && d->v_new && d->q_norm_w && d->k_norm_w &&
+                   d->k_cache && d->v_cache && d->out,
+               "vx27_hip_gqa_decode: null pointer in descriptor");
+    RopeTab rt = {};
+    if (d->rope_dim > 0 && fill_rope(rt, d->rope_dim, d->rope_theta)) return -1;
+    const float yarn = d->rope_yarn < 1.0f ? 1.0f : d->rope_yarn;
+    const int qg = d->n_q / d->n_kv;
+    int n_split = d->n_split;
+    if (n_split <= 0) {
+        // ~4096 waves over all (sequence, KV head) pairs, at least 4 tiles per wave
+        const int tiles = d->L / TILE;
+        n_split = (4096 + d->B * d->n_kv - 1) / (d->B * d->n_kv);
+        if (n_split > (tiles + 3) / 4) n_split = (tiles + 3) / 4;
+        if (n_split < 1) n_split = 1;
+    }
+    const size_t n_part = (size_t)d->B * d->n_kv * n_split * qg;
+    const size_t qbytes = (size_t)d->B * d->n_q * HDG * sizeof(float);
+    const size_t obytes = n_part * HDG * sizeof(float);
+    const size_t mlbytes = n_part * 2 * sizeof(float);
+    void *scr;
+    if (vx_ctx_scratch(ctx, qbytes + obytes + mlbytes, &scr)) return -1;
+    float *q_rot = (float *)scr;
+    float *part_o = q_rot + (size_t)d->B * d->n_q * HDG;
+    float *part_ml = part_o + n_part * HDG;
+
+    PrepArgs pa;
+    pa.B = d->B; pa.n_q = d->n_q; pa.n_kv = d->n_kv; pa.rope_dim = d->rope_dim; pa.L = d->L;
+    pa.flags = d->flags; pa.yarn = yarn; pa.pos = d->pos; pa.q = d->q;
+    pa.q_ss = d->q_seq_stride; pa.q_hs = d->q_head_stride;
+    pa.k_new = d->k_new; pa.v_new = d->v_new; pa.q_norm_w = d->q_norm_w; pa.k_norm_w = d->k_norm_w;
+    pa.k_cache = d->k_cache; pa.v_cache = d->v_cache; pa.q_out = q_rot; pa.rope = rt;
+    VX_LAUNCH(ctx, gqa_prep, dim3(d->n_q + d->n_kv, d->B), dim3(256), pa);
+
+    SplitArgs sa;
+    sa.B = d->B; sa.n_q = d->n_q; sa.n_kv = d->n_kv; sa.L = d->L; sa.n_split = n_split;
+    sa.pos = d->pos; sa.q_rot = q_rot; sa.k_cache = d->k_cache; sa.v_cache = d->v_cache;
+    sa.part_o = part_o; sa.part_ml = part_ml;
+    VX_LAUNCH(ctx, gqa_split, dim3(n_split, d->n_kv, d->B), dim3(64), sa);
+
+    CombArgs ca;
+    ca.B = d->B; ca.n_q = d->n_q; ca.n_kv = d->n_kv; ca.n_split = n_split;
+    ca.part_o = part_o; ca.part_ml = part_ml; ca.gate = d->gate;
+    ca.g_ss = d->gate_seq_stride; ca.g_hs = d->gate_head_stride; ca.out = d->out;
+    VX_LAUNCH(ctx, gqa_combine, dim3(d->n_q, d->B), dim3(256), ca);
+    return 0;
+}
+
+extern "C" int vx27_hip_kv_write(vx27_hip_ctx *ctx, uint16_t *k_cache, uint16_t *v_cache, int B_total,
+                                 int n_kv, int hd, int L, int b, int p0, int n,
+                                 const float *k_rows, const float *v_rows) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(hd == HDG, "vx27_hip_kv_write: hd must be 256");
+    VX_REQUIRE(L % 64 == 0 && b >= 0 && b < B_total && p0 >= 0 && n >= 0 && p0 + n <= L,
+               "vx27_hip_kv_write: rows [%d,%d) of sequence %d outside cache (L=%d, B=%d)", p0, p0 + n, b, L, B_total);
+    if (n == 0) return 0;
+    KvMoveArgs a = {n_kv, L, b, p0, n, k_cache, v_cache, nullptr, nullptr, k_rows, v_rows, nullptr, nullptr};
+    VX_LAUNCH(ctx, kv_write_kernel, dim3(n, n_kv), dim3(256), a);
+    return 0;
+}
+
+extern "C" int vx27_hip_kv_read(vx27_hip_ctx *ctx, const uint16_t *k_cache, const uint16_t *v_cache,
+                                int B_total, int n_kv, int hd, int L, int b, int p0, int n,
+                                float *k_rows, float *v_rows) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(hd == HDG, "vx27_hip_kv_read: hd must be 256");
+    VX_REQUIRE(L % 64 == 0 && b >= 0 && b < B_total && p0 >= 0 && n >= 0 && p0 + n <= L,
+               "vx27_hip_kv_read: rows [%d,%d) of sequence %d outside cache (L=%d, B=%d)", p0, p0 + n, b, L, B_total);
+    if (n == 0) return 0;
+    KvMoveArgs a = {n_kv, L, b, p0, n, nullptr, nullptr, k_cache, v_cache, nullptr, nullptr, k_rows, v_rows};
+    VX_LAUNCH(ctx, kv_read_kernel, dim3(n, n_kv), dim3(256), a);
+    return 0;
+}
+
+extern "C" int vx27_hip_rope_table(vx27_hip_ctx *ctx, const int *pos, int n, int rope_dim, float theta,
+                                   float yarn, float *cosv, float *sinv) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(pos && cosv && sinv && n >= 0, "vx27_hip_rope_table: bad arguments");
+    RopeTab rt = {};
+    if (fill_rope(rt, rope_dim, theta)) return -1;
+    if (n == 0) return 0;
+    RopeTabArgs a = {pos, n, rope_dim / 2, yarn < 1.0f ? 1.0f : yarn, cosv, sinv, rt};
+    VX_LAUNCH(ctx, rope_table_kernel, dim3(n), dim3(MAXR), a);
+    return 0;
+}

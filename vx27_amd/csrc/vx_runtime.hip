@@ -1,0 +1,248 @@
+// Context, stream, memory and error handling of libvx27_hip.
+#include <stdarg.h>
+#include <stdlib.h>
+#include <string.h>
+
+#include "vx_common.h"
+
+static thread_local char g_err[512] = "";
+
+void vx_set_error(const char *fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_err, sizeof g_err, fmt, ap);
+    va_end(ap);
+}
+
+extern "C" const char *vx27_hip_last_error(void) { return g_err; }
+
+extern "C" const char *vx27_hip_version(void) { return "vx27_hip 0.1 gfx950"; }
+
+extern "C" int vx27_hip_device_count(void) {
+    int n = 0;
+    if (hipGetDeviceCount(&n) != hipSuccess) return 0;
+    return n;
+}
+
+int vx_ctx_enter(vx27_hip_ctx *ctx) {
+    VX_REQUIRE(ctx != nullptr, "null context");
+    VX_HIP(hipSetDevice(ctx->device));
+    return 0;
+}
+
+extern "C" int vx27_hip_open(vx27_hip_ctx **out, int device, char *err, size_t errlen) {
+    auto fail = [&](void) {
+        if (err && errlen) snprintf(err, errlen, "%s", g_err);
+        return -1;
+    };
+    if (!out) {
+        vx_set_error("vx27_hip_open: null output pointer");
+        return fail();
+    }
+    *out = nullptr;
+    int n = 0;
+    hipError_t e = hipGetDeviceCount(&n);
+    if (e != hipSuccess || n <= 0) {
+        vx_set_error("vx27_hip_open: no HIP device (%s)", hipGetErrorString(e));
+        return fail();
+    }
+    if (device < 0 || device >= n) {
+        vx_set_error("vx27_hip_open: device %d out of range (have %d)", device, n);
+        return fail();
+    }
+    hipDeviceProp_t prop;
+    if (hipGetDeviceProperties(&prop, device) != hipSuccess) {
+        vx_set_error("vx27_hip_open: cannot query device %d", device);
+        return fail();
+    }
+    if (strncmp(prop.gcnArchName, "gfx950", 6) != 0) {
+        vx_set_error("vx27_hip_open: device %d is %s; this library is built for gfx950", device,
+                     prop.gcnArchName);
+        return fail();
+    }
+    vx27_hip_ctx *c = (vx27_hip_ctx *)calloc(1, sizeof(vx27_hip_ctx));
+    c->device = device;
+    if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
+        vx_set_error("vx27_hip_open: stream creation failed on device %d", device);
+        free(c);
+        return fail();
+    }
+    c->stream = c->own_stream;
+    *out = c;
+    return 0;
+}
+
+static void prof_clear(vx27_hip_ctx *ctx) {
+    for (int i = 0; i < ctx->prof_n; i++) {
+        (void)hipEventDestroy(ctx->prof[i].e0);
+        (void)hipEventDestroy(ctx->prof[i].e1);
+    }
+    ctx->prof_n = 0;
+}
+
+void vx_prof_begin(vx27_hip_ctx *ctx) {
+    if (!ctx->prof_on) return;
+    if (ctx->prof_n == ctx->prof_cap) {
+        int cap = ctx->prof_cap ? 2 * ctx->prof_cap : 256;
+        vx_prof_rec *p = (vx_prof_rec *)realloc(ctx->prof, sizeof(vx_prof_rec) * (size_t)cap);
+        if (!p) return;
+        ctx->prof = p;
+        ctx->prof_cap = cap;
+    }
+    vx_prof_rec *r = &ctx->prof[ctx->prof_n];
+    r->name = nullptr;
+    if (hipEventCreate(&r->e0) != hipSuccess) return;
+    if (hipEventCreate(&r->e1) != hipSuccess) {
+        (void)hipEventDestroy(r->e0);
+        return;
+    }
+    (void)hipEventRecord(r->e0, ctx->stream);
+    ctx->prof_n++;
+}
+
+void vx_prof_end(vx27_hip_ctx *ctx, const char *name) {
+    if (!ctx->prof_on || ctx->prof_n == 0) return;
+    vx_prof_rec *r = &ctx->prof[ctx->prof_n - 1];
+    if (r->name) return;   // begin failed
+    r->name = name;
+    (void)hipEventRecord(r->e1, ctx->stream);
+}
+
+extern "C" int vx27_hip_prof_enable(vx27_hip_ctx *ctx, int on) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_HIP(hipStreamSynchronize(ctx->stream));
+    prof_clear(ctx);
+    ctx->prof_on = on ? 1 : 0;
+    return 0;
+}
+
+extern "C" int vx27_hip_prof_read(vx27_hip_ctx *ctx, const char *name, int *count, double *total_ms) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(name && count && total_ms, "vx27_hip_prof_read: null argument");
+    VX_HIP(hipStreamSynchronize(ctx->stream));
+    int n = 0;
+    double tot = 0.0;
+    for (int i = 0; i < ctx->prof_n; i++) {
+        const vx_prof_rec *r = &ctx->prof[i];
+        if (!r->name || strcmp(r->name, name) != 0) continue;
+        float ms = 0.0f;
+        VX_HIP(hipEventElapsedTime(&ms, r->e0, r->e1));
+        tot += ms;
+        n++;
+    }
+    *count = n;
+    *total_ms = tot;
+    return 0;
+}
+
+extern "C" void vx27_hip_close(vx27_hip_ctx *ctx) {
+    if (!ctx) return;
+    (void)hipSetDevice(ctx->device);
+    (void)hipStreamSynchronize(ctx->stream);
+    prof_clear(ctx);
+    free(ctx->prof);
+    if (ctx->scratch) (void)hipFree(ctx->scratch);
+    if (ctx->stage) (void)hipFree(ctx->stage);
+    (void)hipStreamDestroy(ctx->own_stream);
+    free(ctx);
+}
+
+extern "C" int vx27_hip_sync(vx27_hip_ctx *ctx) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+
+extern "C" int vx27_hip_set_stream(vx27_hip_ctx *ctx, void *s) {
+    VX_REQUIRE(ctx != nullptr, "null context");
+    ctx->stream = s ? (hipStream_t)s : ctx->own_stream;
+    return 0;
+}
+
+extern "C" void *vx27_hip_get_stream(vx27_hip_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
+
+int vx_ctx_scratch(vx27_hip_ctx *ctx, size_t bytes, void **out) {
+    if (bytes > ctx->scratch_bytes) {
+        VX_HIP(hipStreamSynchronize(ctx->stream));
+        if (ctx->scratch) VX_HIP(hipFree(ctx->scratch));
+        ctx->scratch = nullptr;
+        ctx->scratch_bytes = 0;
+        size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+        VX_HIP(hipMalloc(&ctx->scratch, want));
+        ctx->scratch_bytes = want;
+    }
+    *out = ctx->scratch;
+    return 0;
+}
+
+int vx_ctx_stage(vx27_hip_ctx *ctx, size_t bytes, void **out) {
+    if (bytes > ctx->stage_bytes) {
+        VX_HIP(hipStreamSynchronize(ctx->stream));
+        if (ctx->stage) VX_HIP(hipFree(ctx->stage));
+        ctx->stage = nullptr;
+        ctx->stage_bytes = 0;
+        size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
+        VX_HIP(hipMalloc(&ctx->stage, want));
+        ctx->stage_bytes = want;
+    }
+    *out = ctx->stage;
+    return 0;
+}
+
+// ------------------------------------------------------------------ memory
+extern "C" int vx27_hip_alloc(vx27_hip_ctx *ctx, void **dptr, size_t bytes) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(dptr != nullptr, "vx27_hip_alloc: null output pointer");
+    *dptr = nullptr;
+    VX_HIP(hipMalloc(dptr, bytes ? bytes : 1));
+    return 0;
+}
+extern "C" int vx27_hip_free(vx27_hip_ctx *ctx, void *dptr) {
+    if (vx_ctx_enter(ctx)) return -1;
+    if (dptr) {
+        VX_HIP(hipStreamSynchronize(ctx->stream));
+        VX_HIP(hipFree(dptr));
+    }
+    return 0;
+}
+extern "C" int vx27_hip_h2d(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, ctx->stream));
+    VX_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+extern "C" int vx27_hip_d2h(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToHost, ctx->stream));
+    VX_HIP(hipStreamSynchronize(ctx->stream));
+    return 0;
+}
+extern "C" int vx27_hip_d2d(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
+    return 0;
+}
+extern "C" int vx27_hip_memset(vx27_hip_ctx *ctx, void *dst, int byte, size_t bytes) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_HIP(hipMemsetAsync(dst, byte, bytes, ctx->stream));
+    return 0;
+}
+
+// ------------------------------------------------ default (drop-in) context
+static vx27_hip_ctx *g_default = nullptr;
+static int g_errmode = VX27_HIP_ERR_ABORT;
+
+extern "C" void vx27_hip_set_error_mode(int mode) { g_errmode = mode; }
+extern "C" int vx27_hip_get_error_mode(void) { return g_errmode; }
+
+extern "C" vx27_hip_ctx *vx27_hip_default_ctx(void) {
+    if (g_default) return g_default;
+    const char *env = getenv("VX27_HIP_DEVICE");
+    int dev = env ? atoi(env) : 0;
+    char err[256];
+    if (vx27_hip_open(&g_default, dev, err, sizeof err) != 0) {
+        g_default = nullptr;
+        return nullptr;
+    }
+    return g_default;
+}
