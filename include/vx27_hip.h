@@ -143,11 +143,13 @@ typedef struct {
     size_t q_seq_stride, q_head_stride;
     const float *gate;       /* gate logits, same addressing with its own strides */
     size_t gate_seq_stride, gate_head_stride;
-    const float *k_new, *v_new;  /* [B][n_kv][hd] raw k (before norm/rope) and v */
+    const float *k_new, *v_new;  /* [B][n_kv][hd] raw k (before norm/rope) and v
+                                    (sequence stride kv_seq_stride) */
     const float *q_norm_w, *k_norm_w;  /* [hd] */
     uint16_t *k_cache, *v_cache;       /* bf16, format above; row pos is written */
     float *out;              /* [B][n_q][hd]: attention * sigmoid(gate) */
     int n_split;             /* key splits per (sequence, KV head); 0 = automatic */
+    size_t kv_seq_stride;    /* per-sequence stride of k_new / v_new in floats; 0 = n_kv*hd */
 } vx27_gqa_desc;
 
 /* One decode step of the gated GQA mixer core (vx27_qfwd.c:172-211):
@@ -170,6 +172,84 @@ int vx27_hip_kv_read(vx27_hip_ctx *ctx, const uint16_t *k_cache, const uint16_t 
  * float product; cos/sin are the device's float functions. */
 int vx27_hip_rope_table(vx27_hip_ctx *ctx, const int *pos, int n, int rope_dim,
                         float theta, float yarn, float *cosv, float *sinv);
+
+/* ------------------------------------------------ projections and layers */
+/* y[b*y_stride + n] = sum_k W[n][k] * x[b*x_stride + k] for B <= 5 vectors:
+ * W bf16 row-major [N][K] (N % 16 == 0, K % 32 == 0), x and y fp32.  The
+ * F32 matvec of the reference (vx27_pmat.c:98-101, 119-125) on bf16 weights;
+ * x enters the MFMA exactly (split into three bf16 parts), fp32 accumulation. */
+int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x,
+                       size_t x_stride, int B, float *y, size_t y_stride);
+
+/* The mixer of one Gated DeltaNet layer for one decode token of B <= 5
+ * sequences, from the layer input xn to the out_proj output (the DeltaNet
+ * branch of vx27_qlayer, vx27_qfwd.c:102-153):
+ *   [qkv | z | a | b] = W_in xn      (in_proj_qkv, in_proj_z, in_proj_a, in_proj_b
+ *                                      stacked row-wise: C + nv*hd + 2*nv rows)
+ *   causal conv + SiLU on qkv (state in place), gates from a, b,
+ *   rmsn(1+w) + l2norm on q,k, exact delta rule per value head,
+ *   rmsn_std(o)*w * silu(z), out = W_out o.
+ * hd = 128, C = 2*nqk*hd + nv*hd. */
+typedef struct {
+    int B, nqk, nv, hd, hidden;
+    const float *x;             /* [B][hidden] layer input (after input_layernorm) */
+    const uint16_t *x_packed;   /* optional: x already packed by vx27_hip_pack_x (or NULL) */
+    const uint16_t *w_in;       /* bf16 [C + nv*hd + 2*nv][hidden] */
+    const uint16_t *w_out;      /* bf16 [hidden][nv*hd] */
+    const void *conv_w;         /* [C][4] */
+    int conv_w_dtype;           /* VX27_F32 or VX27_BF16 */
+    const float *A_log, *dt_bias, *norm_w;  /* [nv], [nv], [hd] */
+    float *S;                   /* [B][nv][hd][hd] in/out */
+    float *conv_state;          /* [B][C][3] in/out */
+    float *out;                 /* [B][hidden] */
+} vx27_dn_layer_desc;
+int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_desc *d);
+
+/* The mixer of one gated GQA layer for one decode token of B <= 5 sequences
+ * (the attention branch of vx27_qlayer, vx27_qfwd.c:162-213):
+ *   [q|gate interleaved per head | k | v] = W_qkv xn  (q_proj, k_proj, v_proj
+ *                                      stacked: n_q*2*hd + 2*n_kv*hd rows),
+ *   vx27_hip_gqa_decode on them, out = W_o att. */
+typedef struct {
+    int B, n_q, n_kv, hd, hidden, rope_dim;
+    float rope_theta, rope_yarn;
+    int L;                      /* KV cache capacity */
+    const float *x;             /* [B][hidden] */
+    const uint16_t *x_packed;   /* optional pre-packed x (or NULL) */
+    const uint16_t *w_qkv;      /* bf16 [n_q*2*hd + 2*n_kv*hd][hidden] */
+    const uint16_t *w_o;        /* bf16 [hidden][n_q*hd] */
+    const float *q_norm_w, *k_norm_w;
+    const int *pos;             /* [B] device */
+    uint16_t *k_cache, *v_cache;
+    float *out;                 /* [B][hidden] */
+    int n_split;                /* 0 = automatic */
+} vx27_gqa_layer_desc;
+int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer_desc *d);
+
+/* Pack x [B][K] once for several layers that read the same input
+ * (x_packed of the layer descriptors); packed holds vx27_hip_pack_bytes(K). */
+size_t vx27_hip_pack_bytes(int K);
+int vx27_hip_pack_x(vx27_hip_ctx *ctx, const float *x, int B, int K, uint16_t *packed);
+
+/* pos[b] += 1 for b < B (advances decode positions inside a captured graph) */
+int vx27_hip_advance_pos(vx27_hip_ctx *ctx, int *pos, int B);
+
+/* --------------------------------------------------------- HIP graphs
+ * Capture the calls made on ctx between graph_begin and graph_end into an
+ * executable graph; graph_launch replays it on the context stream.  Calls
+ * that would grow the context scratch must have run once before capture. */
+int vx27_hip_graph_begin(vx27_hip_ctx *ctx);
+int vx27_hip_graph_end(vx27_hip_ctx *ctx, void **graph_exec);
+int vx27_hip_graph_launch(vx27_hip_ctx *ctx, void *graph_exec);
+int vx27_hip_graph_destroy(void *graph_exec);
+
+/* ---------------------------------------------- synthetic data on device
+ * Deterministic N(mean, std^2) values from a counter-based generator
+ * (splitmix64 of (seed, index), Box-Muller) -- for benchmarks and tests. */
+int vx27_hip_fill_normal_f32(vx27_hip_ctx *ctx, float *p, size_t n, uint64_t seed, float mean,
+                             float std);
+int vx27_hip_fill_normal_bf16(vx27_hip_ctx *ctx, uint16_t *p, size_t n, uint64_t seed, float mean,
+                              float std);
 
 /* ------------------------------------ device forms of the reference API
  * Same arguments, sizes and arithmetic as the reference function named, on

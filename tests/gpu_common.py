@@ -78,3 +78,64 @@ def oracle_gqa_decode(d, Lcap, threads=None):
         kr[b] = kc[pos]
         vr[b] = vc[pos]
     return outs, kr, vr
+
+
+def oracle_matvec_batch(W_bf16, x, threads=None):
+    """y[b] = W x[b] with the reference's F32 matvec (double serial sums) on
+    bf16 weights widened exactly; x [B][K] -> y [B][N]."""
+    W_bf16 = np.ascontiguousarray(W_bf16, np.uint16)
+    x = np.ascontiguousarray(x, np.float32)
+    B, K = x.shape
+    N = W_bf16.shape[0]
+    y = np.empty((B, N), np.float32)
+    O.lib().orc_matvec_batch(W_bf16.ctypes.data, 1, x, y, N, K, B, threads or O.default_threads())
+    return y
+
+
+def oracle_dn_layer(w, x, S, conv, nqk, nv, hd=128):
+    """The DeltaNet mixer of one layer (projections, all glue stages,
+    out_proj) for one token of each sequence; S [B][nv][hd][hd] and conv
+    [B][C][3] are updated in place.  w: w_in, w_out (bf16 bits), conv_w
+    (float), A_log, dt_bias, norm_w."""
+    B = x.shape[0]
+    qd, vd = nqk * hd, nv * hd
+    C_ = 2 * qd + vd
+    y = oracle_matvec_batch(w["w_in"], x)
+    keep = {k: np.ascontiguousarray(w[k], np.float32) for k in ("A_log", "dt_bias", "norm_w", "conv_w")}
+    cfg = O.DnCfg(nqk, nv, hd, O.DN_CONV | O.DN_PRE_RMS | O.DN_PRE_L2 | O.DN_OUT_GATE,
+                  keep["A_log"].ctypes.data, keep["dt_bias"].ctypes.data, keep["norm_w"].ctypes.data,
+                  keep["conv_w"].ctypes.data)
+    o = np.empty((B, vd), np.float32)
+    for b in range(B):
+        qkv = np.ascontiguousarray(y[b, :C_])
+        z = np.ascontiguousarray(y[b, C_:C_ + vd])
+        a = np.ascontiguousarray(y[b, C_ + vd:C_ + vd + nv])
+        bb = np.ascontiguousarray(y[b, C_ + vd + nv:])
+        Sb = np.ascontiguousarray(S[b]); cb = np.ascontiguousarray(conv[b])
+        O.lib().orc_dn_token(C.byref(cfg), qkv, a, bb, z.ctypes.data, Sb.reshape(-1), cb.ctypes.data, o[b])
+        S[b] = Sb; conv[b] = cb
+    return oracle_matvec_batch(w["w_out"], o)
+
+
+def oracle_gqa_layer(w, x, kc, vc, pos, n_q=24, n_kv=4, hd=256):
+    """The gated-GQA mixer of one layer for one token of each sequence; kc,
+    vc bf16 caches [B][Lcap][n_kv][hd] updated at pos[b]."""
+    B = x.shape[0]
+    y = oracle_matvec_batch(w["w_qkv"], x)
+    Nq = n_q * 2 * hd
+    qn = np.ascontiguousarray(w["q_norm_w"], np.float32)
+    kn = np.ascontiguousarray(w["k_norm_w"], np.float32)
+    att = np.empty((B, n_q * hd), np.float32)
+    for b in range(B):
+        p = int(pos[b])
+        qg = np.ascontiguousarray(y[b, :Nq])
+        k1 = np.ascontiguousarray(y[b, Nq:Nq + n_kv * hd])
+        v1 = np.ascontiguousarray(y[b, Nq + n_kv * hd:])
+        kb = np.ascontiguousarray(kc[b]); vb = np.ascontiguousarray(vc[b])
+        cs, sn = O.rope_cos_sin(p)
+        cfg = O.GqaCfg(n_q, n_kv, hd, 64, 1, qn.ctypes.data, kn.ctypes.data, kb.ctypes.data, vb.ctypes.data,
+                       n_kv * hd, hd, n_kv * hd, hd)
+        O.lib().orc_gqa_token(C.byref(cfg), qg, 2 * hd, qg.ctypes.data + hd * 4, 2 * hd, k1, v1, p, cs, sn,
+                              att[b])
+        kc[b] = kb; vc[b] = vb
+    return oracle_matvec_batch(w["w_o"], att)

@@ -1,0 +1,202 @@
+"""GPU parity of the whole-mixer layer steps (projections + mixer core +
+output projection) and of the projection GEMM, against the oracle's
+composition of the reference glue (vx27_qfwd.c:102-153, 162-213) with the
+reference's F32 matvec on bf16 weights.  Also: graph replay == eager.
+
+Tolerances: DeltaNet layer output and state 1e-5 (fp32 recurrence);
+gated-GQA layer output 2e-2 + 1e-2*|ref| (bf16 attention)."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from gpu_common import maxabs, oracle_dn_layer, oracle_gqa_layer, oracle_matvec_batch, say
+
+pytestmark = pytest.mark.gpu
+
+H = 5120
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from vx27_amd import lib as L
+    c = L.Ctx(0)
+    yield c
+    c.close()
+
+
+def bf16w(r, shape, std):
+    from vx27_amd import workloads as W
+    return W.bf16_bits(W.normal(r, shape, std))
+
+
+def test_gemv_bf16_vs_reference_matvec(ctx):
+    from vx27_amd import lib as L, workloads as W
+    r = W.rng(7, "gemv")
+    for N, K, B in ((16432, 5120, 4), (5120, 6144, 4), (1024, 5120, 1), (64, 96, 5)):
+        Wb = bf16w(r, (N, K), 0.02)
+        x = W.normal(r, (B, K))
+        y = np.empty((B, N), np.float32)
+        wb, xb, yb = ctx.put(Wb), ctx.put(x), ctx.buf(y.nbytes)
+        L.check(L.lib().vx27_hip_gemv_bf16(ctx.h, wb.ptr, N, K, xb.ptr, K, B, yb.ptr, N), "gemv")
+        y = yb.download((B, N), np.float32)
+        ref = oracle_matvec_batch(Wb, x)
+        e = maxabs(y, ref)
+        say(f"  gemv {N}x{K} B={B}: max|d|={e:.3e} (max|y|={np.abs(ref).max():.2f})")
+        assert e <= 1e-5
+        for bb in (wb, xb, yb):
+            bb.free()
+
+
+def dn_layer_inputs(r, B, nqk=16, nv=48, hd=128):
+    from vx27_amd import workloads as W
+    qd, vd = nqk * hd, nv * hd
+    C_ = 2 * qd + vd
+    w = {"w_in": bf16w(r, (C_ + vd + 2 * nv, H), 0.02), "w_out": bf16w(r, (H, vd), 0.02)}
+    w["conv_w_bf16"] = bf16w(r, (C_, 4), 0.2)
+    w["conv_w"] = W.bf16_to_f32(w["conv_w_bf16"])
+    w["A_log"] = r.uniform(-2, 1, nv).astype(np.float32)
+    w["dt_bias"] = W.normal(r, nv, 0.1)
+    w["norm_w"] = W.normal(r, hd, 0.1, 1.0)
+    S = W.normal(r, (B, nv, hd, hd), 0.02)
+    conv = W.normal(r, (B, C_, 3), 0.5)
+    return w, S, conv
+
+
+def test_dn_layer_decode(ctx):
+    """The real layer shape (nqk 16, nv 48, hidden 5120), batch 4, 3 tokens."""
+    from vx27_amd import lib as L, workloads as W
+    B, nqk, nv = 4, 16, 48
+    r = W.rng(8, "dn_layer")
+    w, S, conv = dn_layer_inputs(r, B, nqk, nv)
+    dev = {k: ctx.put(w[k]) for k in ("w_in", "w_out", "conv_w_bf16", "A_log", "dt_bias", "norm_w")}
+    Sd, cd = ctx.put(S), ctx.put(conv)
+    xb, ob = ctx.buf(B * H * 4), ctx.buf(B * H * 4)
+    d = L.DnLayerDesc(B, nqk, nv, 128, H, xb.ptr, None, dev["w_in"].ptr, dev["w_out"].ptr,
+                      dev["conv_w_bf16"].ptr, L.BF16, dev["A_log"].ptr, dev["dt_bias"].ptr,
+                      dev["norm_w"].ptr, Sd.ptr, cd.ptr, ob.ptr)
+    Sr, cr = S.copy(), conv.copy()
+    for t in range(3):
+        x = W.normal(r, (B, H))
+        xb.upload(x)
+        L.check(L.lib().vx27_hip_dn_layer_decode(ctx.h, C.byref(d)), "dn_layer")
+        out = ob.download((B, H), np.float32)
+        ref = oracle_dn_layer(w, x, Sr, cr, nqk, nv)
+        e = maxabs(out, ref)
+        say(f"  dn layer token {t}: max|d out|={e:.3e} (max|out|={np.abs(ref).max():.3f})")
+        assert e <= 1e-5
+    eS = maxabs(Sd.download(S.shape, np.float32), Sr)
+    say(f"  dn layer state max|d|={eS:.3e}")
+    assert eS <= 1e-5
+    # the conv state holds projection outputs: fp32 MFMA sums vs the oracle's double sums
+    assert maxabs(cd.download(conv.shape, np.float32), cr) <= 1e-5
+
+
+def gqa_layer_inputs(r, B, Lcap, n_ctx):
+    from vx27_amd import workloads as W
+    w = {"w_qkv": bf16w(r, (24 * 512 + 2 * 1024, H), 0.02), "w_o": bf16w(r, (H, 24 * 256), 0.02),
+         "q_norm_w": W.normal(r, 256, 0.1), "k_norm_w": W.normal(r, 256, 0.1)}
+    kc = np.zeros((B, Lcap, 4, 256), np.uint16)
+    vc = np.zeros((B, Lcap, 4, 256), np.uint16)
+    kc[:, :n_ctx] = bf16w(r, (B, n_ctx, 4, 256), 1.0)
+    vc[:, :n_ctx] = bf16w(r, (B, n_ctx, 4, 256), 1.0)
+    return w, kc, vc
+
+
+def test_gqa_layer_decode(ctx):
+    """Real layer shape (24Q/4KV hd 256, hidden 5120), batch 4 at ragged
+    positions, 2 tokens."""
+    from vx27_amd import lib as L, mixers as M, workloads as W
+    B, Lcap, n_ctx = 4, 768, 700
+    r = W.rng(9, "gqa_layer")
+    w, kc, vc = gqa_layer_inputs(r, B, Lcap, n_ctx)
+    lay = M.GatedGQALayer(ctx, B, Lcap, w["q_norm_w"], w["k_norm_w"])
+    for b in range(B):
+        lay.write_kv(b, 0, W.bf16_to_f32(kc[b, :n_ctx]), W.bf16_to_f32(vc[b, :n_ctx]))
+    wq, wo = ctx.put(w["w_qkv"]), ctx.put(w["w_o"])
+    pos = np.array([650, 0, 31, 699], np.int32)
+    pb = ctx.put(pos)
+    xb, ob = ctx.buf(B * H * 4), ctx.buf(B * H * 4)
+    d = L.GqaLayerDesc(B, 24, 4, 256, H, 64, 1e7, 1.0, Lcap, xb.ptr, None, wq.ptr, wo.ptr,
+                       lay.q_norm_w.ptr, lay.k_norm_w.ptr, pb.ptr, lay.k_cache.ptr, lay.v_cache.ptr, ob.ptr, 0)
+    for t in range(2):
+        x = W.normal(r, (B, H))
+        xb.upload(x)
+        L.check(L.lib().vx27_hip_gqa_layer_decode(ctx.h, C.byref(d)), "gqa_layer")
+        out = ob.download((B, H), np.float32)
+        ref = oracle_gqa_layer(w, x, kc, vc, pos)
+        err = np.abs(out.astype(np.float64) - ref)
+        lim = 2e-2 + 1e-2 * np.abs(ref)
+        say(f"  gqa layer token {t}: max|d|={err.max():.3e} (max|ref|={np.abs(ref).max():.3f})")
+        assert np.all(err <= lim)
+        L.check(L.lib().vx27_hip_advance_pos(ctx.h, pb.ptr, B), "advance")
+        pos = pos + 1
+
+
+def test_graph_replay_matches_eager(ctx):
+    """One DeltaNet + one GQA layer step captured in a HIP graph and replayed
+    three times (eager work and syncs in between) equals three eager steps."""
+    from vx27_amd import lib as L, mixers as M, workloads as W
+    B, Lcap, n_ctx = 4, 256, 200
+    r = W.rng(10, "graph")
+    w, S, conv = dn_layer_inputs(r, B)
+    gw, kc, vc = gqa_layer_inputs(r, B, Lcap, n_ctx)
+    xs = [W.normal(r, (B, H)) for _ in range(3)]
+
+    def setup():
+        dev = {k: ctx.put(w[k]) for k in ("w_in", "w_out", "conv_w_bf16", "A_log", "dt_bias", "norm_w")}
+        Sd, cd = ctx.put(S), ctx.put(conv)
+        lay = M.GatedGQALayer(ctx, B, Lcap, gw["q_norm_w"], gw["k_norm_w"])
+        for b in range(B):
+            lay.write_kv(b, 0, W.bf16_to_f32(kc[b, :n_ctx]), W.bf16_to_f32(vc[b, :n_ctx]))
+        wq, wo = ctx.put(gw["w_qkv"]), ctx.put(gw["w_o"])
+        pb = ctx.put(np.array([n_ctx, n_ctx - 5, 17, 64], np.int32))
+        xb, o1, o2 = ctx.buf(B * H * 4), ctx.buf(B * H * 4), ctx.buf(B * H * 4)
+        dd = L.DnLayerDesc(B, 16, 48, 128, H, xb.ptr, None, dev["w_in"].ptr, dev["w_out"].ptr,
+                           dev["conv_w_bf16"].ptr, L.BF16, dev["A_log"].ptr, dev["dt_bias"].ptr,
+                           dev["norm_w"].ptr, Sd.ptr, cd.ptr, o1.ptr)
+        gd = L.GqaLayerDesc(B, 24, 4, 256, H, 64, 1e7, 1.0, Lcap, xb.ptr, None, wq.ptr, wo.ptr,
+                            lay.q_norm_w.ptr, lay.k_norm_w.ptr, pb.ptr, lay.k_cache.ptr, lay.v_cache.ptr,
+                            o2.ptr, 0)
+
+        def step():
+            L.check(L.lib().vx27_hip_dn_layer_decode(ctx.h, C.byref(dd)), "dn_layer")
+            L.check(L.lib().vx27_hip_gqa_layer_decode(ctx.h, C.byref(gd)), "gqa_layer")
+            L.check(L.lib().vx27_hip_advance_pos(ctx.h, pb.ptr, B), "advance")
+        return xb, o1, o2, Sd, step
+
+    xb, o1, o2, Sd, step = setup()
+    eager = []
+    for t in range(3):
+        xb.upload(xs[t])
+        step()
+        eager.append((o1.download((B, H), np.float32), o2.download((B, H), np.float32)))
+    xb, o1, o2, Sd2, step = setup()
+    xb.upload(xs[0])
+    step()                                     # sizes the scratch before capture
+    ctx.sync()
+    xb, o1, o2, Sd2, step = setup()
+    ctx.graph_begin()
+    step()
+    g = ctx.graph_end()
+    try:
+        for t in range(3):
+            xb.upload(xs[t])
+            ctx.graph_launch(g)
+            ctx.sync()
+            a, b2 = o1.download((B, H), np.float32), o2.download((B, H), np.float32)
+            _ = np.abs(a).sum()                # eager host work between replays
+            assert np.array_equal(a, eager[t][0]), f"dn replay {t}"
+            assert np.array_equal(b2, eager[t][1]), f"gqa replay {t}"
+    finally:
+        L.lib().vx27_hip_graph_destroy(g)
+
+
+def test_fill_normal_deterministic(ctx):
+    n = 1 << 20
+    a, b = ctx.buf(n * 4), ctx.buf(n * 4)
+    ctx.fill_normal(a, n, 1234, std=2.0, mean=0.5)
+    ctx.fill_normal(b, n, 1234, std=2.0, mean=0.5)
+    x = a.download(n, np.float32)
+    assert np.array_equal(x, b.download(n, np.float32))
+    assert abs(x.mean() - 0.5) < 0.01 and abs(x.std() - 2.0) < 0.01

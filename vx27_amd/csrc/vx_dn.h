@@ -1,0 +1,65 @@
+// Internal interface of the DeltaNet recurrence kernel (vx_dn_decode.hip),
+// shared with the layer entry points (vx_layer.hip).
+#pragma once
+#include "vx_common.h"
+
+namespace {
+constexpr int HD = 128;
+
+// silu1 of vx27_qfwd.c:48 / vx27_deltanet.c:104
+__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
+
+// softplus with the reference's tails (vx27_deltanet.c:58-63)
+__device__ __forceinline__ double softplus_d(double x) {
+    if (x > 20.0) return x;
+    if (x < -20.0) return exp(x);
+    return log(1.0 + exp(x));
+}
+
+// one causal-conv step of a channel (vx27_deltanet.c:106-122): window
+// (c0 oldest, c1, c2, x), products summed left to right, then SiLU
+__device__ __forceinline__ float conv_step(float c[3], const float w[4], float x) {
+    float acc = w[0] * c[0];
+    acc = acc + w[1] * c[1];
+    acc = acc + w[2] * c[2];
+    acc = acc + w[3] * x;
+    c[0] = c[1];
+    c[1] = c[2];
+    c[2] = x;
+    return silu_f(acc);
+}
+
+__device__ __forceinline__ void load_conv_w(const void *w, int bf16, size_t ch, float out[4]) {
+    if (bf16) {
+        const uint16_t *p = (const uint16_t *)w + ch * 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++) out[t] = vx_bf16_to_f32(p[t]);
+    } else {
+        const float *p = (const float *)w + ch * 4;
+#pragma unroll
+        for (int t = 0; t < 4; t++) out[t] = p[t];
+    }
+}
+}  // namespace
+
+struct DnArgs {
+    int B, nqk, nv, steps;
+    unsigned flags;
+    int fused_conv;
+    float *S;
+    float *conv_state;
+    const void *conv_w;
+    int conv_bf16;
+    // activations: either x (fused conv) or q/k/v (already convolved or given)
+    const float *x;
+    const float *q, *k, *v;
+    size_t q_tok, k_tok, v_tok;   // per-(t,b) stride of q, k, v in floats
+    const double2 *gates;         // [steps][B][nv] (beta, decay)
+    const float *norm_w, *z;
+    size_t z_tok;                 // per-(t,b) stride of z
+    float *out;
+    size_t out_tok;               // per-(t,b) stride of out
+};
+
+// Launch the recurrence (one workgroup per (sequence, value head)).
+int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a);

@@ -20,36 +20,14 @@
 // a head's 128 elements are wave trees in double (the reference sums them
 // serially; the two can differ in the last bit of the double sum, far below
 // the float rounding that follows).
-#include "vx_common.h"
+#include "vx_dn.h"
 
 namespace {
 
-constexpr int HD = 128;
 
-struct DnArgs {
-    int B, nqk, nv, steps;
-    unsigned flags;
-    int fused_conv;
-    float *S;
-    float *conv_state;
-    const void *conv_w;
-    int conv_bf16;
-    // activations: either x (fused conv) or q/k/v (already convolved or given)
-    const float *x;
-    const float *q, *k, *v;
-    size_t q_tok, k_tok, v_tok;   // per-(t,b) stride of q, k, v in floats
-    const double2 *gates;         // [steps][B][nv] (beta, decay)
-    const float *norm_w, *z;
-    float *out;
-};
 
-__device__ __forceinline__ float silu_f(float v) { return v / (1.0f + expf(-v)); }
 
-__device__ __forceinline__ double softplus_d(double x) {
-    if (x > 20.0) return x;
-    if (x < -20.0) return exp(x);
-    return log(1.0 + exp(x));
-}
+
 
 // Gate mapping of vx27_deltanet.c:65-69 for every (token, sequence, value
 // head): beta = sigmoid(b), decay = exp(g_log) with g_log = -exp(A_log) *
@@ -66,29 +44,7 @@ __global__ __launch_bounds__(256) void dn_gate_kernel(int n, int nv, const float
     gates[e] = make_double2(beta, exp(glog));
 }
 
-// one causal-conv step of a channel: window (c0 oldest, c1, c2, x)
-__device__ __forceinline__ float conv_step(float c[3], const float w[4], float x) {
-    float acc = w[0] * c[0];
-    acc = acc + w[1] * c[1];
-    acc = acc + w[2] * c[2];
-    acc = acc + w[3] * x;
-    c[0] = c[1];
-    c[1] = c[2];
-    c[2] = x;
-    return silu_f(acc);
-}
 
-__device__ __forceinline__ void load_conv_w(const void *w, int bf16, size_t ch, float out[4]) {
-    if (bf16) {
-        const uint16_t *p = (const uint16_t *)w + ch * 4;
-#pragma unroll
-        for (int t = 0; t < 4; t++) out[t] = vx_bf16_to_f32(p[t]);
-    } else {
-        const float *p = (const float *)w + ch * 4;
-#pragma unroll
-        for (int t = 0; t < 4; t++) out[t] = p[t];
-    }
-}
 
 // Sum of two per-lane doubles over the block's 128 lanes (2 waves); every
 // thread must call it (barrier inside).  slot is private to one call site.
@@ -220,12 +176,12 @@ __global__ __launch_bounds__(HD) void dn_decode_kernel(DnArgs a) {
             double so = (double)of * (double)of, unused = 0.0;
             block_sum2(so, unused, s_red[3]);
             const float is = 1.0f / sqrtf((float)(so / HD) + 1e-6f);
-            const float zz = a.z[sb * vd + (size_t)vh * HD + j];
+            const float zz = a.z[sb * a.z_tok + (size_t)vh * HD + j];
             of = ((of * is) * nw) * silu_f(zz);
         } else {
             __syncthreads();   // s_qn/s_kn are rewritten by the next step
         }
-        a.out[sb * vd + (size_t)vh * HD + j] = of;
+        a.out[sb * a.out_tok + (size_t)vh * HD + j] = of;
     }
 
     // ---- write back state and conv state
@@ -267,6 +223,12 @@ __global__ __launch_bounds__(256) void dn_conv_kernel(ConvArgs a) {
 }
 
 }  // namespace
+
+int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a) {
+    VX_REQUIRE(!a.fused_conv || a.nv == a.nqk, "dn recurrence: fused conv needs nv == nqk");
+    VX_LAUNCH(ctx, dn_decode_kernel, dim3((unsigned)(a.B * a.nv)), dim3(HD), a);
+    return 0;
+}
 
 extern "C" int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d) {
     if (vx_ctx_enter(ctx)) return -1;
@@ -323,6 +285,7 @@ extern "C" int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d) {
         a.q = act; a.k = act + qd; a.v = act + 2 * qd;
         a.q_tok = a.k_tok = a.v_tok = (size_t)C;
     }
-    VX_LAUNCH(ctx, dn_decode_kernel, dim3((unsigned)(d->B * d->nv)), dim3(HD), a);
-    return 0;
+    a.z_tok = (size_t)vd;
+    a.out_tok = (size_t)vd;
+    return vx_dn_recurrence(ctx, a);
 }

@@ -69,6 +69,7 @@ struct PrepArgs {
     const float *q;
     size_t q_ss, q_hs;
     const float *k_new, *v_new, *q_norm_w, *k_norm_w;
+    size_t kv_ss;   // per-sequence stride of k_new / v_new
     uint16_t *k_cache, *v_cache;
     float *q_out;   // [B][n_q][256]
     RopeTab rope;
@@ -93,7 +94,7 @@ __global__ __launch_bounds__(256) void gqa_prep(PrepArgs a) {
     const bool is_q = h < a.n_q;
     const int hk = h - a.n_q;
     const float x = is_q ? a.q[(size_t)b * a.q_ss + (size_t)h * a.q_hs + i]
-                         : a.k_new[((size_t)b * a.n_kv + hk) * HDG + i];
+                         : a.k_new[(size_t)b * a.kv_ss + (size_t)hk * HDG + i];
     const float w = is_q ? a.q_norm_w[i] : a.k_norm_w[i];
     const double ss = block_sum256((double)x * (double)x, red);
     const float s = 1.0f / sqrtf((float)(ss / HDG) + 1e-6f);
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(256) void gqa_prep(PrepArgs a) {
         a.q_out[((size_t)b * a.n_q + h) * HDG + i] = r;
     } else {
         a.k_cache[k_index(a.B, a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(r);
-        const float vv = a.v_new[((size_t)b * a.n_kv + hk) * HDG + i];
+        const float vv = a.v_new[(size_t)b * a.kv_ss + (size_t)hk * HDG + i];
         a.v_cache[v_index(a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(vv);
     }
 }
@@ -321,8 +322,7 @@ int fill_rope(RopeTab &t, int rope_dim, float theta) {
 
 }  // namespace
 
-extern "C" int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d) {
-    if (vx_ctx_enter(ctx)) return -1;
+static int gqa_check(const vx27_gqa_desc *d) {
     VX_REQUIRE(d != nullptr, "vx27_hip_gqa_decode: null descriptor");
     VX_REQUIRE(d->hd == HDG, "vx27_hip_gqa_decode: hd must be 256 (got %d)", d->hd);
     VX_REQUIRE(d->B >= 1 && d->n_kv >= 1 && d->n_q >= d->n_kv && d->n_q % d->n_kv == 0 &&
@@ -333,10 +333,10 @@ extern "C" int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d) {
     VX_REQUIRE(d->pos && d->q && d->gate && d->k_new && d->v_new && d->q_norm_w && d->k_norm_w &&
                    d->k_cache && d->v_cache && d->out,
                "vx27_hip_gqa_decode: null pointer in descriptor");
-    RopeTab rt = {};
-    if (d->rope_dim > 0 && fill_rope(rt, d->rope_dim, d->rope_theta)) return -1;
-    const float yarn = d->rope_yarn < 1.0f ? 1.0f : d->rope_yarn;
-    const int qg = d->n_q / d->n_kv;
+    return 0;
+}
+
+static int gqa_n_split(const vx27_gqa_desc *d) {
     int n_split = d->n_split;
     if (n_split <= 0) {
         // ~4096 waves over all (sequence, KV head) pairs, at least 4 tiles per wave
@@ -345,12 +345,23 @@ extern "C" int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d) {
         if (n_split > (tiles + 3) / 4) n_split = (tiles + 3) / 4;
         if (n_split < 1) n_split = 1;
     }
+    return n_split;
+}
+
+size_t vx_gqa_scratch_bytes(const vx27_gqa_desc *d) {
+    const size_t n_part = (size_t)d->B * d->n_kv * gqa_n_split(d) * (d->n_q / d->n_kv);
+    return ((size_t)d->B * d->n_q * HDG + n_part * HDG + n_part * 2) * sizeof(float);
+}
+
+// The decode step with caller-provided scratch of vx_gqa_scratch_bytes(d).
+int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr) {
+    if (gqa_check(d)) return -1;
+    RopeTab rt = {};
+    if (d->rope_dim > 0 && fill_rope(rt, d->rope_dim, d->rope_theta)) return -1;
+    const float yarn = d->rope_yarn < 1.0f ? 1.0f : d->rope_yarn;
+    const int qg = d->n_q / d->n_kv;
+    const int n_split = gqa_n_split(d);
     const size_t n_part = (size_t)d->B * d->n_kv * n_split * qg;
-    const size_t qbytes = (size_t)d->B * d->n_q * HDG * sizeof(float);
-    const size_t obytes = n_part * HDG * sizeof(float);
-    const size_t mlbytes = n_part * 2 * sizeof(float);
-    void *scr;
-    if (vx_ctx_scratch(ctx, qbytes + obytes + mlbytes, &scr)) return -1;
     float *q_rot = (float *)scr;
     float *part_o = q_rot + (size_t)d->B * d->n_q * HDG;
     float *part_ml = part_o + n_part * HDG;
@@ -360,6 +371,7 @@ extern "C" int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d) {
     pa.flags = d->flags; pa.yarn = yarn; pa.pos = d->pos; pa.q = d->q;
     pa.q_ss = d->q_seq_stride; pa.q_hs = d->q_head_stride;
     pa.k_new = d->k_new; pa.v_new = d->v_new; pa.q_norm_w = d->q_norm_w; pa.k_norm_w = d->k_norm_w;
+    pa.kv_ss = d->kv_seq_stride ? d->kv_seq_stride : (size_t)d->n_kv * HDG;
     pa.k_cache = d->k_cache; pa.v_cache = d->v_cache; pa.q_out = q_rot; pa.rope = rt;
     VX_LAUNCH(ctx, gqa_prep, dim3(d->n_q + d->n_kv, d->B), dim3(256), pa);
 
@@ -375,6 +387,14 @@ extern "C" int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d) {
     ca.g_ss = d->gate_seq_stride; ca.g_hs = d->gate_head_stride; ca.out = d->out;
     VX_LAUNCH(ctx, gqa_combine, dim3(d->n_q, d->B), dim3(256), ca);
     return 0;
+}
+
+extern "C" int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d) {
+    if (vx_ctx_enter(ctx)) return -1;
+    if (gqa_check(d)) return -1;
+    void *scr;
+    if (vx_ctx_scratch(ctx, vx_gqa_scratch_bytes(d), &scr)) return -1;
+    return vx_gqa_decode_into(ctx, d, scr);
 }
 
 extern "C" int vx27_hip_kv_write(vx27_hip_ctx *ctx, uint16_t *k_cache, uint16_t *v_cache, int B_total,

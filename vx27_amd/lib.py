@@ -35,7 +35,22 @@ class GqaDesc(C.Structure):
                 ("q", VP), ("q_seq_stride", C.c_size_t), ("q_head_stride", C.c_size_t),
                 ("gate", VP), ("gate_seq_stride", C.c_size_t), ("gate_head_stride", C.c_size_t),
                 ("k_new", VP), ("v_new", VP), ("q_norm_w", VP), ("k_norm_w", VP),
-                ("k_cache", VP), ("v_cache", VP), ("out", VP), ("n_split", C.c_int)]
+                ("k_cache", VP), ("v_cache", VP), ("out", VP), ("n_split", C.c_int),
+                ("kv_seq_stride", C.c_size_t)]
+
+
+class DnLayerDesc(C.Structure):
+    _fields_ = [("B", C.c_int), ("nqk", C.c_int), ("nv", C.c_int), ("hd", C.c_int), ("hidden", C.c_int),
+                ("x", VP), ("x_packed", VP), ("w_in", VP), ("w_out", VP), ("conv_w", VP),
+                ("conv_w_dtype", C.c_int), ("A_log", VP), ("dt_bias", VP), ("norm_w", VP),
+                ("S", VP), ("conv_state", VP), ("out", VP)]
+
+
+class GqaLayerDesc(C.Structure):
+    _fields_ = [("B", C.c_int), ("n_q", C.c_int), ("n_kv", C.c_int), ("hd", C.c_int), ("hidden", C.c_int),
+                ("rope_dim", C.c_int), ("rope_theta", C.c_float), ("rope_yarn", C.c_float), ("L", C.c_int),
+                ("x", VP), ("x_packed", VP), ("w_qkv", VP), ("w_o", VP), ("q_norm_w", VP), ("k_norm_w", VP),
+                ("pos", VP), ("k_cache", VP), ("v_cache", VP), ("out", VP), ("n_split", C.c_int)]
 
 
 _SIGS = {
@@ -63,6 +78,18 @@ _SIGS = {
     "vx27_hip_kv_write": (C.c_int, [VP, VP, VP] + [C.c_int] * 7 + [VP, VP]),
     "vx27_hip_kv_read": (C.c_int, [VP, VP, VP] + [C.c_int] * 7 + [VP, VP]),
     "vx27_hip_rope_table": (C.c_int, [VP, VP, C.c_int, C.c_int, C.c_float, C.c_float, VP, VP]),
+    "vx27_hip_gemv_bf16": (C.c_int, [VP, VP, C.c_int, C.c_int, VP, C.c_size_t, C.c_int, VP, C.c_size_t]),
+    "vx27_hip_dn_layer_decode": (C.c_int, [VP, C.POINTER(DnLayerDesc)]),
+    "vx27_hip_gqa_layer_decode": (C.c_int, [VP, C.POINTER(GqaLayerDesc)]),
+    "vx27_hip_pack_bytes": (C.c_size_t, [C.c_int]),
+    "vx27_hip_pack_x": (C.c_int, [VP, VP, C.c_int, C.c_int, VP]),
+    "vx27_hip_advance_pos": (C.c_int, [VP, VP, C.c_int]),
+    "vx27_hip_graph_begin": (C.c_int, [VP]),
+    "vx27_hip_graph_end": (C.c_int, [VP, C.POINTER(VP)]),
+    "vx27_hip_graph_launch": (C.c_int, [VP, VP]),
+    "vx27_hip_graph_destroy": (C.c_int, [VP]),
+    "vx27_hip_fill_normal_f32": (C.c_int, [VP, VP, C.c_size_t, C.c_uint64, C.c_float, C.c_float]),
+    "vx27_hip_fill_normal_bf16": (C.c_int, [VP, VP, C.c_size_t, C.c_uint64, C.c_float, C.c_float]),
     "vx27_hip_step_exact": (C.c_int, [VP, VP, VP, VP, VP, C.c_double, C.c_double, VP, C.c_int]),
     "vx27_hip_update_simple": (C.c_int, [VP, VP, VP, VP, C.c_float, C.c_int, C.c_int]),
     "vx27_hip_retrieve_simple": (C.c_int, [VP, VP, VP, VP, C.c_int, C.c_int]),
@@ -199,6 +226,22 @@ class Ctx:
         n, ms = C.c_int(), C.c_double()
         check(lib().vx27_hip_prof_read(self.h, kernel.encode(), C.byref(n), C.byref(ms)), "prof_read")
         return n.value, ms.value
+
+    def fill_normal(self, buf, n, seed, std=1.0, mean=0.0, bf16=False):
+        fn = lib().vx27_hip_fill_normal_bf16 if bf16 else lib().vx27_hip_fill_normal_f32
+        check(fn(self.h, buf.ptr if isinstance(buf, DevBuf) else buf, int(n), int(seed), float(mean),
+                 float(std)), "fill_normal")
+
+    def graph_begin(self):
+        check(lib().vx27_hip_graph_begin(self.h), "graph_begin")
+
+    def graph_end(self):
+        g = VP()
+        check(lib().vx27_hip_graph_end(self.h, C.byref(g)), "graph_end")
+        return g.value
+
+    def graph_launch(self, g):
+        check(lib().vx27_hip_graph_launch(self.h, g), "graph_launch")
 
     def close(self):
         for b in self._bufs:
