@@ -66,12 +66,21 @@ class MixerStack:
         self.pos = ctx.put(np.full(B, Lctx, np.int32))
         self.layers = []
         self.kv_bytes = self.w_bytes = self.s_bytes = 0
+        tmp = ctx.buf((C_ + vd + 2 * nv) * H * 2)      # row-major staging for weight tiling
+        lib = L.lib()
+
+        def weight(N, K, seed):
+            """bf16 ~N(0, 0.02) [N][K] generated row-major, stored tiled."""
+            fill(tmp, N * K, seed, 0.02, bf16=True)
+            wt = ctx.buf(N * K * 2)
+            L.check(lib.vx27_hip_pack_weights_bf16(ctx.h, tmp.ptr, N, K, wt.ptr), "pack_weights")
+            return wt
         for li in range(n_layers):
             full = (li + 1) % 4 == 0
             s += 10
             if full:
-                wq = ctx.buf((24 * 2 * gq + 2 * 4 * gq) * H * 2); fill(wq, wq.nbytes // 2, s + 1, 0.02, bf16=True)
-                wo = ctx.buf(H * 24 * gq * 2); fill(wo, wo.nbytes // 2, s + 2, 0.02, bf16=True)
+                wq = weight(24 * 2 * gq + 2 * 4 * gq, H, s + 1)
+                wo = weight(H, 24 * gq, s + 2)
                 qn = ctx.put(W.normal(r, gq, 0.1)); kn = ctx.put(W.normal(r, gq, 0.1))
                 n = B * 4 * self.Lcap * gq
                 kc = ctx.buf(n * 2); fill(kc, n, s + 3, 1.0, bf16=True)
@@ -82,8 +91,8 @@ class MixerStack:
                 self.layers.append(("gqa", d))
                 self.w_bytes += wq.nbytes + wo.nbytes
             else:
-                wi = ctx.buf((C_ + vd + 2 * nv) * H * 2); fill(wi, wi.nbytes // 2, s + 1, 0.02, bf16=True)
-                wo = ctx.buf(H * vd * 2); fill(wo, wo.nbytes // 2, s + 2, 0.02, bf16=True)
+                wi = weight(C_ + vd + 2 * nv, H, s + 1)
+                wo = weight(H, vd, s + 2)
                 cw = ctx.buf(C_ * 4 * 2); fill(cw, C_ * 4, s + 3, 0.2, bf16=True)
                 A_log = ctx.put(r.uniform(-2, 1, nv).astype(np.float32))
                 dtb = ctx.put(W.normal(r, nv, 0.1))
@@ -96,6 +105,7 @@ class MixerStack:
                 self.w_bytes += wi.nbytes + wo.nbytes
                 self.s_bytes += 2 * S.nbytes + 2 * cs.nbytes
         ctx.sync()
+        tmp.free()
 
     def step(self):
         from vx27_amd import lib as L
@@ -135,8 +145,8 @@ def bench_c5(ctx, steps, warmup, B=4, Lctx=131072, cpu=True):
     st.step()
     ctx.sync()
     prof = {}
-    for k in ("gqa_split", "gqa_prep", "gqa_combine", "gemv_part", "gemv_reduce_store", "dn_in_epilogue",
-              "dn_decode_kernel", "pack_x"):
+    for k in ("gqa_split", "gqa_prep", "gqa_combine", "gemv_part_k<true>", "gemv_reduce_store",
+              "dn_in_epilogue", "dn_decode_kernel", "pack_x"):
         n, ms = ctx.prof_read(k)
         prof[k] = (n, ms)
     ctx.prof_enable(False)

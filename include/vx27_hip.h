@@ -181,6 +181,13 @@ int vx27_hip_rope_table(vx27_hip_ctx *ctx, const int *pos, int n, int rope_dim,
 int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x,
                        size_t x_stride, int B, float *y, size_t y_stride);
 
+/* Weight tiling for the layer entry points: row-major bf16 W [N][K] into the
+ * MFMA tile layout [N/16][K/32][64 lanes][8] (lane (g,m) of tile (rb, s)
+ * holds W[16rb + m][32s + 8g .. 8g+7]), so each wave loads 1 KiB of
+ * contiguous weights per tile.  Done once per weight, like the reference's
+ * offline forge of its packed weight format (src/vx_forge.c). */
+int vx27_hip_pack_weights_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, uint16_t *W_tiled);
+
 /* The mixer of one Gated DeltaNet layer for one decode token of B <= 5
  * sequences, from the layer input xn to the out_proj output (the DeltaNet
  * branch of vx27_qlayer, vx27_qfwd.c:102-153):
@@ -194,8 +201,8 @@ typedef struct {
     int B, nqk, nv, hd, hidden;
     const float *x;             /* [B][hidden] layer input (after input_layernorm) */
     const uint16_t *x_packed;   /* optional: x already packed by vx27_hip_pack_x (or NULL) */
-    const uint16_t *w_in;       /* bf16 [C + nv*hd + 2*nv][hidden] */
-    const uint16_t *w_out;      /* bf16 [hidden][nv*hd] */
+    const uint16_t *w_in;       /* bf16 [C + nv*hd + 2*nv][hidden], tiled (vx27_hip_pack_weights_bf16) */
+    const uint16_t *w_out;      /* bf16 [hidden][nv*hd], tiled */
     const void *conv_w;         /* [C][4] */
     int conv_w_dtype;           /* VX27_F32 or VX27_BF16 */
     const float *A_log, *dt_bias, *norm_w;  /* [nv], [nv], [hd] */
@@ -216,8 +223,8 @@ typedef struct {
     int L;                      /* KV cache capacity */
     const float *x;             /* [B][hidden] */
     const uint16_t *x_packed;   /* optional pre-packed x (or NULL) */
-    const uint16_t *w_qkv;      /* bf16 [n_q*2*hd + 2*n_kv*hd][hidden] */
-    const uint16_t *w_o;        /* bf16 [hidden][n_q*hd] */
+    const uint16_t *w_qkv;      /* bf16 [n_q*2*hd + 2*n_kv*hd][hidden], tiled */
+    const uint16_t *w_o;        /* bf16 [hidden][n_q*hd], tiled */
     const float *q_norm_w, *k_norm_w;
     const int *pos;             /* [B] device */
     uint16_t *k_cache, *v_cache;

@@ -69,7 +69,8 @@ def test_dn_layer_decode(ctx):
     B, nqk, nv = 4, 16, 48
     r = W.rng(8, "dn_layer")
     w, S, conv = dn_layer_inputs(r, B, nqk, nv)
-    dev = {k: ctx.put(w[k]) for k in ("w_in", "w_out", "conv_w_bf16", "A_log", "dt_bias", "norm_w")}
+    dev = {k: ctx.put(w[k]) for k in ("conv_w_bf16", "A_log", "dt_bias", "norm_w")}
+    dev["w_in"], dev["w_out"] = ctx.put_tiled(w["w_in"]), ctx.put_tiled(w["w_out"])
     Sd, cd = ctx.put(S), ctx.put(conv)
     xb, ob = ctx.buf(B * H * 4), ctx.buf(B * H * 4)
     d = L.DnLayerDesc(B, nqk, nv, 128, H, xb.ptr, None, dev["w_in"].ptr, dev["w_out"].ptr,
@@ -113,7 +114,7 @@ def test_gqa_layer_decode(ctx):
     lay = M.GatedGQALayer(ctx, B, Lcap, w["q_norm_w"], w["k_norm_w"])
     for b in range(B):
         lay.write_kv(b, 0, W.bf16_to_f32(kc[b, :n_ctx]), W.bf16_to_f32(vc[b, :n_ctx]))
-    wq, wo = ctx.put(w["w_qkv"]), ctx.put(w["w_o"])
+    wq, wo = ctx.put_tiled(w["w_qkv"]), ctx.put_tiled(w["w_o"])
     pos = np.array([650, 0, 31, 699], np.int32)
     pb = ctx.put(pos)
     xb, ob = ctx.buf(B * H * 4), ctx.buf(B * H * 4)
@@ -144,12 +145,13 @@ def test_graph_replay_matches_eager(ctx):
     xs = [W.normal(r, (B, H)) for _ in range(3)]
 
     def setup():
-        dev = {k: ctx.put(w[k]) for k in ("w_in", "w_out", "conv_w_bf16", "A_log", "dt_bias", "norm_w")}
+        dev = {k: ctx.put(w[k]) for k in ("conv_w_bf16", "A_log", "dt_bias", "norm_w")}
+        dev["w_in"], dev["w_out"] = ctx.put_tiled(w["w_in"]), ctx.put_tiled(w["w_out"])
         Sd, cd = ctx.put(S), ctx.put(conv)
         lay = M.GatedGQALayer(ctx, B, Lcap, gw["q_norm_w"], gw["k_norm_w"])
         for b in range(B):
             lay.write_kv(b, 0, W.bf16_to_f32(kc[b, :n_ctx]), W.bf16_to_f32(vc[b, :n_ctx]))
-        wq, wo = ctx.put(gw["w_qkv"]), ctx.put(gw["w_o"])
+        wq, wo = ctx.put_tiled(gw["w_qkv"]), ctx.put_tiled(gw["w_o"])
         pb = ctx.put(np.array([n_ctx, n_ctx - 5, 17, 64], np.int32))
         xb, o1, o2 = ctx.buf(B * H * 4), ctx.buf(B * H * 4), ctx.buf(B * H * 4)
         dd = L.DnLayerDesc(B, 16, 48, 128, H, xb.ptr, None, dev["w_in"].ptr, dev["w_out"].ptr,

@@ -57,8 +57,9 @@ struct DnArgs {
     const double2 *gates;         // [steps][B][nv] (beta, decay)
     const float *norm_w, *z;
     size_t z_tok;                 // per-(t,b) stride of z
-    float *out;
+    float *out;                   // may be NULL when out_packed is set
     size_t out_tok;               // per-(t,b) stride of out
+    uint16_t *out_packed;         // optional: out as the packed GEMV operand (steps == 1)
 };
 
 // Launch the recurrence (one workgroup per (sequence, value head)).

@@ -21,6 +21,7 @@
 // serially; the two can differ in the last bit of the double sum, far below
 // the float rounding that follows).
 #include "vx_dn.h"
+#include "vx_gemv.h"
 
 namespace {
 
@@ -181,7 +182,8 @@ __global__ __launch_bounds__(HD) void dn_decode_kernel(DnArgs a) {
         } else {
             __syncthreads();   // s_qn/s_kn are rewritten by the next step
         }
-        a.out[sb * a.out_tok + (size_t)vh * HD + j] = of;
+        if (a.out) a.out[sb * a.out_tok + (size_t)vh * HD + j] = of;
+        if (a.out_packed) vx_pack_store(a.out_packed, a.B, b, vh * HD + j, of);
     }
 
     // ---- write back state and conv state

@@ -1,30 +1,71 @@
 // Internal interface of the skinny bf16 GEMM (vx_gemv.hip), shared with the
-// layer kernels that fuse their own reduction epilogues.
+// kernels that produce its packed operand or fuse its reduction epilogue.
 #pragma once
 #include "vx_common.h"
 
-// Split-K plan for an N x K GEMV: n_seg K segments of ks_per 32-wide k-steps.
+// Split-K plan for an N x K GEMV: n_seg K segments of ks_per 32-wide k-steps;
+// segments are combined four at a time inside a workgroup, so
+// vx_gemv_pseg(n_seg) partial sets [N][16] fp32 are written.
 int vx_gemv_plan(int N, int K, int *n_seg, int *ks_per);
+int vx_gemv_pseg(int n_seg);
 size_t vx_gemv_part_bytes(int N, int n_seg);
 size_t vx_pack_bytes(int K);
-// x [B][K] (row stride x_stride) -> packed MFMA B operand with P bf16 parts.
-int vx_pack(vx27_hip_ctx *ctx, const float *x, size_t x_stride, int B, int P, int K, uint16_t *packed);
-// partial sums [n_seg][N][16] of W [N][K] bf16 times the packed operand
-int vx_gemv_part(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const uint16_t *packed, int n_seg,
-                 int ks_per, float *part);
-// y[b*y_stride + n] = sum of partials (P parts of vector b)
-int vx_gemv_reduce_store(vx27_hip_ctx *ctx, const float *part, int N, int B, int P, int n_seg, float *y,
+// x [B][K] (row stride x_stride) -> packed MFMA B operand (three bf16 parts).
+int vx_pack(vx27_hip_ctx *ctx, const float *x, size_t x_stride, int B, int K, uint16_t *packed);
+// partial sums of W [N][K] bf16 (tiled layout if `tiled`, else row-major)
+// times the packed operand
+int vx_gemv_part(vx27_hip_ctx *ctx, const uint16_t *W, int tiled, int N, int K, const uint16_t *packed,
+                 int n_seg, int ks_per, float *part);
+// y[b*y_stride + n] = sum of partials of vector b
+int vx_gemv_reduce_store(vx27_hip_ctx *ctx, const float *part, int N, int B, int n_seg, float *y,
                          size_t y_stride);
 
-// Sum of the partials of output (n, b): segments in order, parts in order
-// within a segment.
-__device__ __forceinline__ float vx_gemv_sum(const float *part, int N, int B, int P, int n_seg, int n, int b) {
-    float acc = 0.0f;
-    for (int s = 0; s < n_seg; s++) {
-        const float *p = part + ((size_t)s * N + n) * 16 + b;
-        float v = p[0];
-        for (int q = 1; q < P; q++) v += p[q * B];
-        acc += v;
+// Part p (0 = hi, 1 = mid, 2 = lo) of the exact three-way bf16 split of x:
+// hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid); each difference
+// is exact in fp32.
+__device__ __forceinline__ uint16_t vx_bf16_part(float x, int p) {
+    uint16_t h = vx_f32_to_bf16(x);
+    for (int q = 0; q < p; q++) {
+        x = x - vx_bf16_to_f32(h);
+        h = vx_f32_to_bf16(x);
     }
-    return acc;
+    return h;
+}
+
+// Element k of vector b (of B) as the three parts of the packed operand.
+__device__ __forceinline__ void vx_pack_store(uint16_t *packed, int B, int b, int k, float x) {
+    const size_t base = ((size_t)(k >> 5) * 64 + ((k >> 3) & 3) * 16) * 8 + (k & 7);
+    uint16_t h = vx_f32_to_bf16(x);
+    packed[base + (size_t)b * 8] = h;
+    x = x - vx_bf16_to_f32(h);
+    h = vx_f32_to_bf16(x);
+    packed[base + (size_t)(B + b) * 8] = h;
+    x = x - vx_bf16_to_f32(h);
+    packed[base + (size_t)(2 * B + b) * 8] = vx_f32_to_bf16(x);
+}
+
+// Sums of the partials of row n for each vector b < B (three parts):
+// partial sets in order, parts hi + mid + lo within a set.
+template <int B>
+__device__ __forceinline__ void vx_gemv_sum_row_t(const float *part, int N, int n_pseg, int n, float *acc) {
+#pragma unroll
+    for (int b = 0; b < B; b++) acc[b] = 0.0f;
+    for (int s = 0; s < n_pseg; s++) {
+        const float4 *p4 = (const float4 *)(part + ((size_t)s * N + n) * 16);
+        const float4 c0 = p4[0], c1 = p4[1], c2 = p4[2], c3 = p4[3];
+        const float c[16] = {c0.x, c0.y, c0.z, c0.w, c1.x, c1.y, c1.z, c1.w,
+                             c2.x, c2.y, c2.z, c2.w, c3.x, c3.y, c3.z, c3.w};
+#pragma unroll
+        for (int b = 0; b < B; b++) acc[b] += (c[b] + c[B + b]) + c[2 * B + b];
+    }
+}
+__device__ __forceinline__ void vx_gemv_sum_row(const float *part, int N, int B, int n_pseg, int n,
+                                                float *acc) {
+    switch (B) {
+        case 1: vx_gemv_sum_row_t<1>(part, N, n_pseg, n, acc); break;
+        case 2: vx_gemv_sum_row_t<2>(part, N, n_pseg, n, acc); break;
+        case 3: vx_gemv_sum_row_t<3>(part, N, n_pseg, n, acc); break;
+        case 4: vx_gemv_sum_row_t<4>(part, N, n_pseg, n, acc); break;
+        default: vx_gemv_sum_row_t<5>(part, N, n_pseg, n, acc); break;
+    }
 }

@@ -1,27 +1,30 @@
 // Skinny bf16 GEMM (the mixer projections) on gfx950 MFMA.
 //
 // y[b][n] = sum_k W[n][k] * x[b][k] for B <= 5 activation vectors (decode:
-// one token per sequence), W bf16 row-major [N][K] (the layout of the
-// reference's weight tensors, vx27_pmat.h:6-8), x and y fp32.
+// one token per sequence), W bf16 [N][K] (the reference's weight tensors,
+// vx27_pmat.h:6-8), x and y fp32.
 //
 // The fp32 activations enter the MFMA exactly: each x is split into three
 // bf16 parts hi + mid + lo (8 mantissa bits each, 24 in all), and the parts
-// of the B vectors are the columns of the MFMA's B operand (3*B <= 16 of the
+// of the B vectors are the columns of the MFMA's B operand (3*B <= 15 of the
 // 16 columns).  One v_mfma_f32_16x16x32_bf16 therefore multiplies 16 weight
-// rows by all parts of all vectors; the products are exact in fp32 and the
+// rows by every part of every vector; the products are exact in fp32 and the
 // only rounding is the fp32 accumulation, as in a plain fp32 dot product.
-// The part sums are formed in the reduction.  No cross-lane reduction is
-// needed: the MFMA accumulates over k.
+// Output column n of an MFMA depends only on operand column n, so operand
+// columns >= 3*B may hold anything: they feed output columns nobody reads.
 //
-// Kernels:
-//   pack_x     x [B][K] fp32 -> packed B operand [K/32][64 lanes][8] bf16
-//              (lane (g,n) of k-step s holds part n/B of vector n%B at
-//              k = 32s + 8g + 0..7; columns n >= P*B are zero)
-//   gemv_part  one wave per (64-row group, K segment): 4 row blocks x the
-//              segment's k-steps, partial sums [split][N][16] fp32
-//   reductions sum the partials in a fixed order (deterministic) and apply
-//              an epilogue: plain store, or the DeltaNet input projection's
-//              (causal conv + SiLU, z, gate mapping), see vx_layer.hip.
+// Layouts:
+//   packed activations  [K/32 k-steps][64 lanes][8] bf16: lane (g,n) of k-step
+//                       s holds part n/B of vector n%B at k = 32s + 8g + 0..7
+//   tiled weights       [N/16 row blocks][K/32 k-steps][64 lanes][8] bf16:
+//                       lane (g,m) holds W[16*rb + m][32s + 8g + 0..7], so a
+//                       wave's A operand is 1 KiB of contiguous memory
+//                       (vx27_hip_pack_weights_bf16 converts row-major W)
+//
+// gemv_part: a workgroup of 4 waves owns 64 rows (4 row blocks); its waves
+// take 4 consecutive K segments and are combined in LDS, so one partial
+// [N][16] fp32 is written per workgroup-segment; the reductions sum them in a
+// fixed order (deterministic) and apply an epilogue.
 #include "vx_gemv.h"
 
 namespace {
@@ -29,29 +32,18 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-__device__ __forceinline__ uint16_t bf16_bits(float x) { return vx_f32_to_bf16(x); }
+constexpr int RB = 4;   // 16-row MFMA blocks per workgroup
 
-// pack: grid (K/32), block 64; lane (g,n) writes its 8 elements of k-step s
-__global__ __launch_bounds__(64) void pack_x(const float *x, size_t x_stride, int B, int P, uint16_t *out) {
+// pack activations: grid (K/32), block 64; lane (g,n) writes its 8 elements
+__global__ __launch_bounds__(64) void pack_x(const float *x, size_t x_stride, int B, uint16_t *out) {
     const int s = blockIdx.x, lane = threadIdx.x, g = lane >> 4, n = lane & 15;
+    if (n >= 3 * B) return;   // padding columns feed unread output columns
+    const int p = n / B, b = n % B;
+    const float *xr = x + (size_t)b * x_stride + 32 * s + 8 * g;
     uint16_t v[8];
-    if (n < P * B) {
-        const int p = n / B, b = n % B;
-        const float *xr = x + (size_t)b * x_stride + 32 * s + 8 * g;
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            float r = xr[e];
-            uint16_t h = bf16_bits(r);
-            for (int q = 0; q < p; q++) {   // peel the leading parts
-                r = r - vx_bf16_to_f32(h);
-                h = bf16_bits(r);
-            }
-            v[e] = h;
-        }
-    } else {
-#pragma unroll
-        for (int e = 0; e < 8; e++) v[e] = 0;
-    }
+    for (int e = 0; e < 8; e++) v[e] = vx_bf16_part(xr[e], p);
+
     uint4 w;
     w.x = v[0] | ((uint32_t)v[1] << 16);
     w.y = v[2] | ((uint32_t)v[3] << 16);
@@ -60,59 +52,74 @@ __global__ __launch_bounds__(64) void pack_x(const float *x, size_t x_stride, in
     *(uint4 *)(out + ((size_t)s * 64 + lane) * 8) = w;
 }
 
-constexpr int RB = 4;   // 16-row MFMA blocks per wave
+// row-major W [N][K] -> tiled; grid (N/16, K/32), block 64
+__global__ __launch_bounds__(64) void pack_w(const uint16_t *W, int K, uint16_t *Wt) {
+    const int rb = blockIdx.x, s = blockIdx.y, lane = threadIdx.x, g = lane >> 4, m = lane & 15;
+    const int nks = K / 32;
+    const uint4 v = *(const uint4 *)(W + (size_t)(16 * rb + m) * K + 32 * s + 8 * g);
+    *(uint4 *)(Wt + (((size_t)rb * nks + s) * 64 + lane) * 8) = v;
+}
 
-// grid (ceil(N/64), ceil(n_seg/4)), block 256: wave w computes row group
-// blockIdx.x (64 rows) over K segment blockIdx.y*4 + w.
-__global__ __launch_bounds__(256) void gemv_part(const uint16_t *W, int N, int K, const uint16_t *xp,
-                                                 int ks_per, int n_seg, float *part) {
+// grid (ceil(N/64), ceil(n_seg/4)), block 256; wave w: K segment 4*blockIdx.y + w
+template <bool TILED>
+__global__ __launch_bounds__(256) void gemv_part_k(const uint16_t *W, int N, int K, const uint16_t *xp,
+                                                   int ks_per, int n_seg, float *part) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63, g = lane >> 4, m = lane & 15;
     const int seg = blockIdx.y * 4 + wave;
-    if (seg >= n_seg) return;
-    const int row0 = blockIdx.x * 16 * RB;
+    const int rb0 = blockIdx.x * RB;
     const int nks = K / 32;
-    const int s0 = seg * ks_per, s1 = min(nks, s0 + ks_per);
+    const int s0 = seg * ks_per, s1 = seg < n_seg ? min(nks, s0 + ks_per) : s0;
+    __shared__ floatx4_t red[4][RB][64];
     floatx4_t acc[RB];
 #pragma unroll
     for (int r = 0; r < RB; r++) acc[r] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
-    const uint16_t *wrow[RB];
     bool live[RB];
+    const uint16_t *wp[RB];
 #pragma unroll
     for (int r = 0; r < RB; r++) {
-        const int row = row0 + r * 16 + m;
-        live[r] = row0 + r * 16 < N;          // whole block in or out (N % 16 == 0)
-        wrow[r] = W + (size_t)(live[r] ? row : 0) * K + 8 * g;
+        live[r] = (rb0 + r) * 16 < N;          // whole 16-row block in or out (N % 16 == 0)
+        const int rb = live[r] ? rb0 + r : 0;
+        wp[r] = TILED ? W + ((size_t)rb * nks * 64 + lane) * 8
+                      : W + (size_t)(16 * rb + m) * K + 8 * g;
     }
     const bf16x8_t *xb = (const bf16x8_t *)xp + lane;
-#pragma unroll 2
+#pragma unroll 4
     for (int s = s0; s < s1; s++) {
         const bf16x8_t bop = xb[(size_t)s * 64];
         bf16x8_t aop[RB];
 #pragma unroll
-        for (int r = 0; r < RB; r++) aop[r] = *(const bf16x8_t *)(wrow[r] + 32 * s);
+        for (int r = 0; r < RB; r++)
+            aop[r] = *(const bf16x8_t *)(TILED ? wp[r] + (size_t)s * 512 : wp[r] + 32 * s);
 #pragma unroll
         for (int r = 0; r < RB; r++)
             if (live[r]) acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[r], bop, acc[r], 0, 0, 0);
     }
-    // lane (g,m) holds C[4g+i][m]: rows row0 + r*16 + 4g + i, column m
 #pragma unroll
-    for (int r = 0; r < RB; r++) {
-        if (!live[r]) continue;
+    for (int r = 0; r < RB; r++) red[wave][r][lane] = acc[r];
+    __syncthreads();
+    // wave w sums the four segments of row block w in segment order
+    const int r = wave;
+    if (!live[r]) return;
+    floatx4_t v = red[0][r][lane];
+    v += red[1][r][lane];
+    v += red[2][r][lane];
+    v += red[3][r][lane];
+    // lane (g,m) holds C[4g+i][m]: row 16*(rb0+r) + 4g + i, column m
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int row = row0 + r * 16 + 4 * g + i;
-            part[((size_t)seg * N + row) * 16 + m] = acc[r][i];
-        }
+    for (int i = 0; i < 4; i++) {
+        const int row = 16 * (rb0 + r) + 4 * g + i;
+        part[((size_t)blockIdx.y * N + row) * 16 + m] = v[i];
     }
 }
 
-// plain reduction: y[b*y_stride + n] = sum over segments and parts
-__global__ __launch_bounds__(256) void gemv_reduce_store(const float *part, int N, int B, int P, int n_seg,
+// plain reduction, one thread per row: y[b*y_stride + n] for b < B
+__global__ __launch_bounds__(256) void gemv_reduce_store(const float *part, int N, int B, int n_pseg,
                                                          float *y, size_t y_stride) {
-    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (id >= (size_t)N * B) return;
-    const int b = (int)(id / N), n = (int)(id % N);
-    y[(size_t)b * y_stride + n] = vx_gemv_sum(part, N, B, P, n_seg, n, b);
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= N) return;
+    float acc[5];
+    vx_gemv_sum_row(part, N, B, n_pseg, n, acc);
+    for (int b = 0; b < B; b++) y[(size_t)b * y_stride + n] = acc[b];
 }
 
 }  // namespace
@@ -133,19 +140,39 @@ int vx_gemv_plan(int N, int K, int *n_seg, int *ks_per) {
     return 0;
 }
 
-size_t vx_gemv_part_bytes(int N, int n_seg) { return (size_t)n_seg * N * 16 * sizeof(float); }
+int vx_gemv_pseg(int n_seg) { return (n_seg + 3) / 4; }
+size_t vx_gemv_part_bytes(int N, int n_seg) { return (size_t)vx_gemv_pseg(n_seg) * N * 16 * sizeof(float); }
 size_t vx_pack_bytes(int K) { return (size_t)(K / 32) * 64 * 8 * sizeof(uint16_t); }
 
-int vx_pack(vx27_hip_ctx *ctx, const float *x, size_t x_stride, int B, int P, int K, uint16_t *packed) {
-    VX_REQUIRE(B >= 1 && P >= 1 && P * B <= 16 && K % 32 == 0, "pack: need P*B <= 16, K %% 32 == 0");
-    VX_LAUNCH(ctx, pack_x, dim3(K / 32), dim3(64), x, x_stride, B, P, packed);
+int vx_pack(vx27_hip_ctx *ctx, const float *x, size_t x_stride, int B, int K, uint16_t *packed) {
+    VX_REQUIRE(B >= 1 && B <= 5 && K % 32 == 0, "pack: need B <= 5, K %% 32 == 0");
+    VX_LAUNCH(ctx, pack_x, dim3(K / 32), dim3(64), x, x_stride, B, packed);
     return 0;
 }
 
-int vx_gemv_part(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const uint16_t *packed, int n_seg,
-                 int ks_per, float *part) {
-    const int groups = (N + 16 * RB - 1) / (16 * RB);
-    VX_LAUNCH(ctx, gemv_part, dim3(groups, (n_seg + 3) / 4), dim3(256), W, N, K, packed, ks_per, n_seg, part);
+int vx_gemv_part(vx27_hip_ctx *ctx, const uint16_t *W, int tiled, int N, int K, const uint16_t *packed,
+                 int n_seg, int ks_per, float *part) {
+    const dim3 grid((N + 16 * RB - 1) / (16 * RB), vx_gemv_pseg(n_seg));
+    if (tiled)
+        VX_LAUNCH(ctx, gemv_part_k<true>, grid, dim3(256), W, N, K, packed, ks_per, n_seg, part);
+    else
+        VX_LAUNCH(ctx, gemv_part_k<false>, grid, dim3(256), W, N, K, packed, ks_per, n_seg, part);
+    return 0;
+}
+
+int vx_gemv_reduce_store(vx27_hip_ctx *ctx, const float *part, int N, int B, int n_seg, float *y,
+                         size_t y_stride) {
+    VX_LAUNCH(ctx, gemv_reduce_store, dim3((N + 255) / 256), dim3(256), part, N, B, vx_gemv_pseg(n_seg), y,
+              y_stride);
+    return 0;
+}
+
+extern "C" int vx27_hip_pack_weights_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, uint16_t *Wt) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(W && Wt && W != Wt, "vx27_hip_pack_weights_bf16: need distinct source and destination");
+    VX_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 32 == 0,
+               "vx27_hip_pack_weights_bf16: N must be a multiple of 16 and K of 32");
+    VX_LAUNCH(ctx, pack_w, dim3(N / 16, K / 32), dim3(64), W, K, Wt);
     return 0;
 }
 
@@ -161,18 +188,7 @@ extern "C" int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, i
     if (vx_ctx_scratch(ctx, pk + vx_gemv_part_bytes(N, n_seg), &scr)) return -1;
     uint16_t *packed = (uint16_t *)scr;
     float *part = (float *)((char *)scr + pk);
-    if (vx_pack(ctx, x, x_stride, B, 3, K, packed)) return -1;
-    if (vx_gemv_part(ctx, W, N, K, packed, n_seg, ks_per, part)) return -1;
-    const size_t n = (size_t)N * B;
-    VX_LAUNCH(ctx, gemv_reduce_store, dim3((unsigned)((n + 255) / 256)), dim3(256), part, N, B, 3, n_seg, y,
-              y_stride);
-    return 0;
-}
-
-int vx_gemv_reduce_store(vx27_hip_ctx *ctx, const float *part, int N, int B, int P, int n_seg, float *y,
-                         size_t y_stride) {
-    const size_t n = (size_t)N * B;
-    VX_LAUNCH(ctx, gemv_reduce_store, dim3((unsigned)((n + 255) / 256)), dim3(256), part, N, B, P, n_seg, y,
-              y_stride);
-    return 0;
+    if (vx_pack(ctx, x, x_stride, B, K, packed)) return -1;
+    if (vx_gemv_part(ctx, W, 0, N, K, packed, n_seg, ks_per, part)) return -1;
+    return vx_gemv_reduce_store(ctx, part, N, B, n_seg, y, y_stride);
 }

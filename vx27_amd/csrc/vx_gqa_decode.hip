@@ -28,7 +28,7 @@
 //                                           dim-major V block.
 #include <math.h>
 
-#include "vx_common.h"
+#include "vx_gemv.h"
 
 namespace {
 
@@ -248,27 +248,43 @@ struct CombArgs {
     const float *part_o, *part_ml;
     const float *gate;
     size_t g_ss, g_hs;
-    float *out;
+    float *out;                  // [B][n_q][256] or NULL
+    uint16_t *out_packed;        // optional packed GEMV operand of out (K = n_q*256)
 };
 
-// grid (n_q, B), block 256
+// grid (n_q, B, 4 dim chunks), block 256: wave w merges splits w, w+4, ...
+// for 64 dims, then the four waves are merged in LDS in wave order.
 __global__ __launch_bounds__(256) void gqa_combine(CombArgs a) {
-    const int h = blockIdx.x, b = blockIdx.y, i = threadIdx.x;
+    const int h = blockIdx.x, b = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int i = blockIdx.z * 64 + lane;
     const int qg = a.n_q / a.n_kv, kvh = h / qg, n = h % qg;
     const size_t base = ((size_t)b * a.n_kv + kvh) * a.n_split;
+    __shared__ float s_o[4][64], s_l[4];
+    // global max of the split maxima (every wave computes it)
     float M = -INFINITY;
-    for (int s = 0; s < a.n_split; s++) M = fmaxf(M, a.part_ml[((base + s) * qg + n) * 2]);
+    for (int s = lane; s < a.n_split; s += 64) M = fmaxf(M, a.part_ml[((base + s) * qg + n) * 2]);
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
     float L = 0.0f, O = 0.0f;
-#pragma unroll 4
-    for (int s = 0; s < a.n_split; s++) {
+#pragma unroll 8
+    for (int s = wave; s < a.n_split; s += 4) {
         const float m = a.part_ml[((base + s) * qg + n) * 2];
-        if (m == -INFINITY) continue;
-        const float w = exp2f(m - M);
-        L += a.part_ml[((base + s) * qg + n) * 2 + 1] * w;
-        O += a.part_o[((base + s) * qg + n) * HDG + i] * w;
+        const float l = a.part_ml[((base + s) * qg + n) * 2 + 1];
+        const float o = a.part_o[((base + s) * qg + n) * HDG + i];
+        const float w = (m == -INFINITY) ? 0.0f : exp2f(m - M);
+        L += l * w;
+        O += o * w;
     }
+    s_o[wave][lane] = O;
+    if (lane == 0) s_l[wave] = L;
+    __syncthreads();
+    if (wave != 0) return;
+    const float Lt = ((s_l[0] + s_l[1]) + s_l[2]) + s_l[3];
+    const float Ot = ((s_o[0][lane] + s_o[1][lane]) + s_o[2][lane]) + s_o[3][lane];
     const float gl = a.gate[(size_t)b * a.g_ss + (size_t)h * a.g_hs + i];
-    a.out[((size_t)b * a.n_q + h) * HDG + i] = (O / L) * (1.0f / (1.0f + expf(-gl)));
+    const float r = (Ot / Lt) * (1.0f / (1.0f + expf(-gl)));
+    if (a.out) a.out[((size_t)b * a.n_q + h) * HDG + i] = r;
+    if (a.out_packed) vx_pack_store(a.out_packed, a.B, b, h * HDG + i, r);
 }
 
 struct KvMoveArgs {
@@ -331,7 +347,7 @@ static int gqa_check(const vx27_gqa_desc *d) {
     VX_REQUIRE(d->L >= 64 && d->L % 64 == 0, "vx27_hip_gqa_decode: L must be a positive multiple of 64");
     VX_REQUIRE(d->rope_dim >= 0 && d->rope_dim <= HDG, "vx27_hip_gqa_decode: bad rope_dim");
     VX_REQUIRE(d->pos && d->q && d->gate && d->k_new && d->v_new && d->q_norm_w && d->k_norm_w &&
-                   d->k_cache && d->v_cache && d->out,
+                   d->k_cache && d->v_cache,
                "vx27_hip_gqa_decode: null pointer in descriptor");
     return 0;
 }
@@ -353,8 +369,9 @@ size_t vx_gqa_scratch_bytes(const vx27_gqa_desc *d) {
     return ((size_t)d->B * d->n_q * HDG + n_part * HDG + n_part * 2) * sizeof(float);
 }
 
-// The decode step with caller-provided scratch of vx_gqa_scratch_bytes(d).
-int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr) {
+// The decode step with caller-provided scratch of vx_gqa_scratch_bytes(d);
+// out_packed (optional) receives the output as the packed GEMV operand.
+int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uint16_t *out_packed) {
     if (gqa_check(d)) return -1;
     RopeTab rt = {};
     if (d->rope_dim > 0 && fill_rope(rt, d->rope_dim, d->rope_theta)) return -1;
@@ -385,16 +402,18 @@ int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr) {
     ca.B = d->B; ca.n_q = d->n_q; ca.n_kv = d->n_kv; ca.n_split = n_split;
     ca.part_o = part_o; ca.part_ml = part_ml; ca.gate = d->gate;
     ca.g_ss = d->gate_seq_stride; ca.g_hs = d->gate_head_stride; ca.out = d->out;
-    VX_LAUNCH(ctx, gqa_combine, dim3(d->n_q, d->B), dim3(256), ca);
+    ca.out_packed = out_packed;
+    VX_LAUNCH(ctx, gqa_combine, dim3(d->n_q, d->B, HDG / 64), dim3(256), ca);
     return 0;
 }
 
 extern "C" int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d) {
     if (vx_ctx_enter(ctx)) return -1;
     if (gqa_check(d)) return -1;
+    VX_REQUIRE(d->out != nullptr, "vx27_hip_gqa_decode: null output");
     void *scr;
     if (vx_ctx_scratch(ctx, vx_gqa_scratch_bytes(d), &scr)) return -1;
-    return vx_gqa_decode_into(ctx, d, scr);
+    return vx_gqa_decode_into(ctx, d, scr, nullptr);
 }
 
 extern "C" int vx27_hip_kv_write(vx27_hip_ctx *ctx, uint16_t *k_cache, uint16_t *v_cache, int B_total,

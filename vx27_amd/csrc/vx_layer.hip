@@ -17,7 +17,7 @@
 #include "vx_gemv.h"
 
 size_t vx_gqa_scratch_bytes(const vx27_gqa_desc *d);
-int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr);
+int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uint16_t *out_packed);
 
 namespace {
 
@@ -25,7 +25,7 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct DnInArgs {
     const float *part;
-    int N, B, P, n_seg, C, vd, nv;
+    int N, B, n_pseg, C, vd, nv;
     float *conv_state;
     const void *conv_w;
     int conv_bf16;
@@ -34,28 +34,32 @@ struct DnInArgs {
     double2 *gates;
 };
 
-// one thread per (row n, sequence b) of the stacked input projection
+// one thread per row n of the stacked input projection, all sequences
 __global__ __launch_bounds__(256) void dn_in_epilogue(DnInArgs a) {
-    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (id >= (size_t)a.N * a.B) return;
-    const int b = (int)(id / a.N), n = (int)(id % a.N);
-    const float v = vx_gemv_sum(a.part, a.N, a.B, a.P, a.n_seg, n, b);
+    const int n = blockIdx.x * blockDim.x + threadIdx.x;
+    if (n >= a.N) return;
+    float v[5];
+    vx_gemv_sum_row(a.part, a.N, a.B, a.n_pseg, n, v);
     if (n < a.C) {                       // q|k|v channel: causal conv + SiLU
-        float w[4], st[3];
+        float w[4];
         load_conv_w(a.conv_w, a.conv_bf16, (size_t)n, w);
-        float *sp = a.conv_state + ((size_t)b * a.C + n) * 3;
-        st[0] = sp[0]; st[1] = sp[1]; st[2] = sp[2];
-        a.act[(size_t)b * a.C + n] = conv_step(st, w, v);
-        sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
+        for (int b = 0; b < a.B; b++) {
+            float st[3];
+            float *sp = a.conv_state + ((size_t)b * a.C + n) * 3;
+            st[0] = sp[0]; st[1] = sp[1]; st[2] = sp[2];
+            a.act[(size_t)b * a.C + n] = conv_step(st, w, v[b]);
+            sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
+        }
     } else if (n < a.C + a.vd) {         // z
-        a.z[(size_t)b * a.vd + (n - a.C)] = v;
+        for (int b = 0; b < a.B; b++) a.z[(size_t)b * a.vd + (n - a.C)] = v[b];
     } else if (n < a.C + a.vd + a.nv) {  // a -> decay = exp(g_log), vx27_deltanet.c:68,82
         const int vh = n - a.C - a.vd;
-        const double glog = -exp((double)a.A_log[vh]) * softplus_d((double)v + (double)a.dt_bias[vh]);
-        a.gates[(size_t)b * a.nv + vh].y = exp(glog);
+        const double eA = exp((double)a.A_log[vh]), dtb = (double)a.dt_bias[vh];
+        for (int b = 0; b < a.B; b++)
+            a.gates[(size_t)b * a.nv + vh].y = exp(-eA * softplus_d((double)v[b] + dtb));
     } else {                             // b -> beta = sigmoid(b), vx27_deltanet.c:67
         const int vh = n - a.C - a.vd - a.nv;
-        a.gates[(size_t)b * a.nv + vh].x = 1.0 / (1.0 + exp(-(double)v));
+        for (int b = 0; b < a.B; b++) a.gates[(size_t)b * a.nv + vh].x = 1.0 / (1.0 + exp(-(double)v[b]));
     }
 }
 
@@ -93,7 +97,7 @@ extern "C" size_t vx27_hip_pack_bytes(int K) { return vx_pack_bytes(K); }
 extern "C" int vx27_hip_pack_x(vx27_hip_ctx *ctx, const float *x, int B, int K, uint16_t *packed) {
     if (vx_ctx_enter(ctx)) return -1;
     VX_REQUIRE(x && packed && B >= 1 && B <= 5, "vx27_hip_pack_x: bad arguments");
-    return vx_pack(ctx, x, (size_t)K, B, 3, K, packed);
+    return vx_pack(ctx, x, (size_t)K, B, K, packed);
 }
 
 extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_desc *d) {
@@ -118,10 +122,10 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     if (vx_gemv_part_bytes(H, seg_out) > part_b) part_b = vx_gemv_part_bytes(H, seg_out);
     part_b = align256(part_b);
     const size_t act_b = align256((size_t)B * C * 4), z_b = align256((size_t)B * vd * 4);
-    const size_t g_b = align256((size_t)B * nv * sizeof(double2)), o_b = align256((size_t)B * vd * 4);
+    const size_t g_b = align256((size_t)B * nv * sizeof(double2));
     const size_t pk_o = align256(vx_pack_bytes(vd));
     void *scr;
-    if (vx_ctx_scratch(ctx, pk_x + part_b + act_b + z_b + g_b + o_b + pk_o, &scr)) return -1;
+    if (vx_ctx_scratch(ctx, pk_x + part_b + act_b + z_b + g_b + pk_o, &scr)) return -1;
     char *p = (char *)scr;
     uint16_t *xp = d->x_packed ? (uint16_t *)d->x_packed : (uint16_t *)p;
     p += pk_x;
@@ -129,15 +133,13 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     float *act = (float *)p; p += act_b;
     float *z = (float *)p; p += z_b;
     double2 *gates = (double2 *)p; p += g_b;
-    float *o = (float *)p; p += o_b;
     uint16_t *op = (uint16_t *)p;
 
-    if (!d->x_packed && vx_pack(ctx, d->x, (size_t)H, B, 3, H, xp)) return -1;
-    if (vx_gemv_part(ctx, d->w_in, Nin, H, xp, seg_in, per_in, part)) return -1;
-    DnInArgs ea = {part, Nin, B, 3, seg_in, C, vd, nv, d->conv_state, d->conv_w,
+    if (!d->x_packed && vx_pack(ctx, d->x, (size_t)H, B, H, xp)) return -1;
+    if (vx_gemv_part(ctx, d->w_in, 1, Nin, H, xp, seg_in, per_in, part)) return -1;
+    DnInArgs ea = {part, Nin, B, vx_gemv_pseg(seg_in), C, vd, nv, d->conv_state, d->conv_w,
                    d->conv_w_dtype == VX27_BF16, d->A_log, d->dt_bias, act, z, gates};
-    const size_t ne = (size_t)Nin * B;
-    VX_LAUNCH(ctx, dn_in_epilogue, dim3((unsigned)((ne + 255) / 256)), dim3(256), ea);
+    VX_LAUNCH(ctx, dn_in_epilogue, dim3((unsigned)((Nin + 255) / 256)), dim3(256), ea);
 
     DnArgs ra = {};
     ra.B = B; ra.nqk = d->nqk; ra.nv = nv; ra.steps = 1;
@@ -146,12 +148,11 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     ra.q = act; ra.k = act + qd; ra.v = act + 2 * qd;
     ra.q_tok = ra.k_tok = ra.v_tok = (size_t)C;
     ra.gates = gates; ra.norm_w = d->norm_w; ra.z = z; ra.z_tok = (size_t)vd;
-    ra.out = o; ra.out_tok = (size_t)vd;
+    ra.out = nullptr; ra.out_tok = (size_t)vd; ra.out_packed = op;
     if (vx_dn_recurrence(ctx, ra)) return -1;
 
-    if (vx_pack(ctx, o, (size_t)vd, B, 3, vd, op)) return -1;
-    if (vx_gemv_part(ctx, d->w_out, H, vd, op, seg_out, per_out, part)) return -1;
-    return vx_gemv_reduce_store(ctx, part, H, B, 3, seg_out, d->out, (size_t)H);
+    if (vx_gemv_part(ctx, d->w_out, 1, H, vd, op, seg_out, per_out, part)) return -1;
+    return vx_gemv_reduce_store(ctx, part, H, B, seg_out, d->out, (size_t)H);
 }
 
 extern "C" int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer_desc *d) {
@@ -179,32 +180,29 @@ extern "C" int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer
     size_t part_b = vx_gemv_part_bytes(Nqkv, seg_in);
     if (vx_gemv_part_bytes(H, seg_out) > part_b) part_b = vx_gemv_part_bytes(H, seg_out);
     part_b = align256(part_b);
-    const size_t y_b = align256((size_t)B * Nqkv * 4), att_b = align256((size_t)B * Ka * 4);
+    const size_t y_b = align256((size_t)B * Nqkv * 4);
     const size_t pk_a = align256(vx_pack_bytes(Ka));
     // placeholders so the scratch size of the attention step can be planned
     g.q = g.gate = g.k_new = g.v_new = (const float *)1;
-    g.out = (float *)1;
     const size_t gq_b = align256(vx_gqa_scratch_bytes(&g));
     void *scr;
-    if (vx_ctx_scratch(ctx, pk_x + part_b + y_b + att_b + pk_a + gq_b, &scr)) return -1;
+    if (vx_ctx_scratch(ctx, pk_x + part_b + y_b + pk_a + gq_b, &scr)) return -1;
     char *p = (char *)scr;
     uint16_t *xp = d->x_packed ? (uint16_t *)d->x_packed : (uint16_t *)p;
     p += pk_x;
     float *part = (float *)p; p += part_b;
     float *y = (float *)p; p += y_b;
-    float *att = (float *)p; p += att_b;
     uint16_t *ap = (uint16_t *)p; p += pk_a;
     void *gscr = p;
 
-    if (!d->x_packed && vx_pack(ctx, d->x, (size_t)H, B, 3, H, xp)) return -1;
-    if (vx_gemv_part(ctx, d->w_qkv, Nqkv, H, xp, seg_in, per_in, part)) return -1;
-    if (vx_gemv_reduce_store(ctx, part, Nqkv, B, 3, seg_in, y, (size_t)Nqkv)) return -1;
+    if (!d->x_packed && vx_pack(ctx, d->x, (size_t)H, B, H, xp)) return -1;
+    if (vx_gemv_part(ctx, d->w_qkv, 1, Nqkv, H, xp, seg_in, per_in, part)) return -1;
+    if (vx_gemv_reduce_store(ctx, part, Nqkv, B, seg_in, y, (size_t)Nqkv)) return -1;
     g.q = y; g.gate = y + hd; g.k_new = y + Nq; g.v_new = y + Nq + (size_t)d->n_kv * hd;
-    g.out = att;
-    if (vx_gqa_decode_into(ctx, &g, gscr)) return -1;
-    if (vx_pack(ctx, att, (size_t)Ka, B, 3, Ka, ap)) return -1;
-    if (vx_gemv_part(ctx, d->w_o, H, Ka, ap, seg_out, per_out, part)) return -1;
-    return vx_gemv_reduce_store(ctx, part, H, B, 3, seg_out, d->out, (size_t)H);
+    g.out = nullptr;
+    if (vx_gqa_decode_into(ctx, &g, gscr, ap)) return -1;
+    if (vx_gemv_part(ctx, d->w_o, 1, H, Ka, ap, seg_out, per_out, part)) return -1;
+    return vx_gemv_reduce_store(ctx, part, H, B, seg_out, d->out, (size_t)H);
 }
 
 extern "C" int vx27_hip_advance_pos(vx27_hip_ctx *ctx, int *pos, int B) {

@@ -82,6 +82,7 @@ _SIGS = {
     "vx27_hip_dn_layer_decode": (C.c_int, [VP, C.POINTER(DnLayerDesc)]),
     "vx27_hip_gqa_layer_decode": (C.c_int, [VP, C.POINTER(GqaLayerDesc)]),
     "vx27_hip_pack_bytes": (C.c_size_t, [C.c_int]),
+    "vx27_hip_pack_weights_bf16": (C.c_int, [VP, VP, C.c_int, C.c_int, VP]),
     "vx27_hip_pack_x": (C.c_int, [VP, VP, C.c_int, C.c_int, VP]),
     "vx27_hip_advance_pos": (C.c_int, [VP, VP, C.c_int]),
     "vx27_hip_graph_begin": (C.c_int, [VP]),
@@ -231,6 +232,18 @@ class Ctx:
         fn = lib().vx27_hip_fill_normal_bf16 if bf16 else lib().vx27_hip_fill_normal_f32
         check(fn(self.h, buf.ptr if isinstance(buf, DevBuf) else buf, int(n), int(seed), float(mean),
                  float(std)), "fill_normal")
+
+    def put_tiled(self, W_bf16):
+        """Upload row-major bf16 weights [N][K] and return them in the MFMA
+        tile layout the layer entry points read."""
+        W_bf16 = np.ascontiguousarray(W_bf16, np.uint16)
+        N, K = W_bf16.shape
+        src = DevBuf(self, W_bf16.nbytes).upload(W_bf16)
+        dst = self.buf(W_bf16.nbytes)
+        check(lib().vx27_hip_pack_weights_bf16(self.h, src.ptr, N, K, dst.ptr), "pack_weights")
+        self.sync()
+        src.free()
+        return dst
 
     def graph_begin(self):
         check(lib().vx27_hip_graph_begin(self.h), "graph_begin")
