@@ -49,7 +49,8 @@ const char *vx27_hip_version(void);
 /* Kernel profiler: while enabled, the library records HIP events around
  * each of its kernel launches on the context stream; prof_read synchronises
  * and returns how many launches of `kernel` were recorded and their summed
- * duration.  Enabling (or disabling) clears the records. */
+ * duration; a template kernel's instances (name<...>) count under its
+ * name.  Enabling (or disabling) clears the records. */
 int vx27_hip_prof_enable(vx27_hip_ctx *ctx, int on);
 int vx27_hip_prof_read(vx27_hip_ctx *ctx, const char *kernel, int *count, double *total_ms);
 

@@ -1,13 +1,14 @@
 // Gated DeltaNet recurrent decode for gfx950.
 //
-// Work decomposition: one workgroup (128 lanes, 2 waves) per (sequence b,
-// value head vh).  Lane j owns column j of the head's 128x128 state S[i][j]
-// (i = key dim, j = value dim): the column lives in 128 VGPRs for all steps
-// of a call, so kv[j] = sum_i S[i][j] kn[i] and o[j] = sum_i S[i][j] qn[i] are
-// lane-local sums in the reference's row order (vx27_deltanet.c:84-101) with
-// no cross-lane reduction.  S is read and written once per call through a
-// buffer resource (one lane offset, scalar row offsets), coalesced 512 bytes
-// per row.
+// Work decomposition: one workgroup per (sequence b, value head vh) with
+// 128*R lanes.  Column j of the head's 128x128 state S[i][j] (i = key dim,
+// j = value dim) is held by R adjacent lanes, 128/R rows each, in VGPRs for
+// all steps of a call.  With R = 1 (large batches) kv[j] = sum_i S[i][j] kn[i]
+// and o[j] = sum_i S[i][j] qn[i] are lane-local sums in the reference's row
+// order (vx27_deltanet.c:84-101); with R = 2 or 4 (few heads, more lanes per
+// head to fill the chip) the R row-block partial sums are added by a
+// shuffle butterfly.  S is read and written once per call through a buffer
+// resource (one lane offset, scalar row offsets).
 //
 // The causal conv (vx27_deltanet.c:106-122) is fused when every workgroup
 // owns the conv channels it reads, i.e. nv == nqk (q_g, k_g, v_g all belong
@@ -47,8 +48,10 @@ __global__ __launch_bounds__(256) void dn_gate_kernel(int n, int nv, const float
 
 
 
-// Sum of two per-lane doubles over the block's 128 lanes (2 waves); every
-// thread must call it (barrier inside).  slot is private to one call site.
+// Sum of two per-lane doubles over all NW waves of the block (wave partials
+// added in wave order); every thread must call it (barrier inside).  slot is
+// private to one call site.
+template <int NW>
 __device__ __forceinline__ void block_sum2(double &u, double &v, double (*slot)[2]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const double su = vx_wave_sum_f64(u), sv = vx_wave_sum_f64(v);
@@ -57,145 +60,193 @@ __device__ __forceinline__ void block_sum2(double &u, double &v, double (*slot)[
         slot[wave][1] = sv;
     }
     __syncthreads();
-    u = slot[0][0] + slot[1][0];
-    v = slot[0][1] + slot[1][1];
+    double a0 = slot[0][0], a1 = slot[0][1];
+#pragma unroll
+    for (int w = 1; w < NW; w++) {
+        a0 = a0 + slot[w][0];
+        a1 = a1 + slot[w][1];
+    }
+    u = a0;
+    v = a1;
 }
 
-__global__ __launch_bounds__(HD) void dn_decode_kernel(DnArgs a) {
-    const int j = threadIdx.x;                 // owned column / channel
+// Sum over the R adjacent lanes that share a state column (butterfly; every
+// lane of the group ends with the same bits since each add is commutative).
+template <int R>
+__device__ __forceinline__ double part_sum(double x) {
+#pragma unroll
+    for (int off = 1; off < R; off <<= 1) x = x + __shfl_xor(x, off, 64);
+    return x;
+}
+
+// One workgroup per (sequence, value head) with 128*R lanes: lane (col, part)
+// = (tid / R, tid % R) holds rows part*128/R .. of state column col.  Lanes
+// tid < 128 own q/k element tid (and its conv channels); the part-0 lane of a
+// column owns the value channel and writes the column's output.
+template <int R>
+__global__ __launch_bounds__(HD * R) void dn_decode_kernel(DnArgs a) {
+    constexpr int RR = HD / R;                 // state rows per lane
+    constexpr int NW = 2 * R;                  // waves per block
+    const int tid = threadIdx.x;
+    const int part = tid % R, col = tid / R;
+    const int j = tid;                         // q/k element (qk lanes)
+    const bool qk_lane = tid < HD;
+    const bool v_lane = part == 0;
     const int b = blockIdx.x / a.nv;
     const int vh = blockIdx.x % a.nv;
     const int g = vh * a.nqk / a.nv;           // QK head (vx27_qfwd.c:137)
     const int qd = a.nqk * HD, vd = a.nv * HD, C = 2 * qd + vd;
 
     __shared__ float s_qn[HD], s_kn[HD];
-    __shared__ double s_red[4][2][2];
+    __shared__ double s_red[4][NW][2];
 
-    // ---- state column into registers
+    // ---- state rows of this lane into registers
     const __amdgpu_buffer_rsrc_t Sr = __builtin_amdgcn_make_buffer_rsrc(
         a.S + ((size_t)b * a.nv + vh) * HD * HD, 0, HD * HD * 4, 0x00020000);
-    float Sc[HD];
+    float Sc[RR];
 #pragma unroll
-    for (int i = 0; i < HD; i++)
-        Sc[i] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(Sr, j * 4, i * HD * 4, 0));
+    for (int u = 0; u < RR; u++)
+        Sc[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(Sr, col * 4, (part * RR + u) * HD * 4, 0));
 
     // ---- owned conv channels (fused conv: nv == nqk, so g == vh)
     const bool conv = a.fused_conv != 0;
     float cq[3] = {0, 0, 0}, ck[3] = {0, 0, 0}, cv[3] = {0, 0, 0};
     float wq[4] = {0, 0, 0, 0}, wk[4] = {0, 0, 0, 0}, wv[4] = {0, 0, 0, 0};
     const size_t chq = (size_t)g * HD + j, chk = (size_t)qd + g * HD + j,
-                 chv = (size_t)2 * qd + (size_t)vh * HD + j;
+                 chv = (size_t)2 * qd + (size_t)vh * HD + col;
     float *cst = conv ? a.conv_state + (size_t)b * C * 3 : nullptr;
     if (conv) {
-        load_conv_w(a.conv_w, a.conv_bf16, chq, wq);
-        load_conv_w(a.conv_w, a.conv_bf16, chk, wk);
-        load_conv_w(a.conv_w, a.conv_bf16, chv, wv);
+        if (qk_lane) {
+            load_conv_w(a.conv_w, a.conv_bf16, chq, wq);
+            load_conv_w(a.conv_w, a.conv_bf16, chk, wk);
 #pragma unroll
-        for (int t = 0; t < 3; t++) {
-            cq[t] = cst[chq * 3 + t];
-            ck[t] = cst[chk * 3 + t];
-            cv[t] = cst[chv * 3 + t];
+            for (int t = 0; t < 3; t++) {
+                cq[t] = cst[chq * 3 + t];
+                ck[t] = cst[chk * 3 + t];
+            }
+        }
+        if (v_lane) {
+            load_conv_w(a.conv_w, a.conv_bf16, chv, wv);
+#pragma unroll
+            for (int t = 0; t < 3; t++) cv[t] = cst[chv * 3 + t];
         }
     }
-    const float nw = a.norm_w ? a.norm_w[j] : 1.0f;
+    const float nwj = (a.norm_w && qk_lane) ? a.norm_w[j] : 1.0f;     // q/k element weight
+    const float nwc = a.norm_w ? a.norm_w[col] : 1.0f;                // output column weight
     const float qs = 1.0f / sqrtf((float)HD);
 
     for (int t = 0; t < a.steps; t++) {
         const size_t sb = (size_t)t * a.B + b;
         const double2 gt = a.gates[sb * a.nv + vh];   // uniform address: scalar load
         // ---- activations of this token
-        float qa, ka, va;
+        float qa = 0.0f, ka = 0.0f, va = 0.0f;
         if (conv) {
             const float *x = a.x + sb * C;
-            qa = conv_step(cq, wq, x[chq]);
-            ka = conv_step(ck, wk, x[chk]);
-            va = conv_step(cv, wv, x[chv]);
+            if (qk_lane) {
+                qa = conv_step(cq, wq, x[chq]);
+                ka = conv_step(ck, wk, x[chk]);
+            }
+            if (v_lane) va = conv_step(cv, wv, x[chv]);
         } else {
-            qa = a.q[sb * a.q_tok + (size_t)g * HD + j];
-            ka = a.k[sb * a.k_tok + (size_t)g * HD + j];
-            va = a.v[sb * a.v_tok + (size_t)vh * HD + j];
+            if (qk_lane) {
+                qa = a.q[sb * a.q_tok + (size_t)g * HD + j];
+                ka = a.k[sb * a.k_tok + (size_t)g * HD + j];
+            }
+            if (v_lane) va = a.v[sb * a.v_tok + (size_t)vh * HD + col];
         }
+        if (R > 1) va = __shfl(va, (tid & 63) - part, 64);   // from the column's part-0 lane
         // ---- q/k normalisation chain
         if (a.flags & VX27_DN_PRE_RMS) {       // rmsn(x)*(1+w), vx27_qfwd.c:32-39,123
             double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
-            block_sum2(sq, sk, s_red[0]);
+            block_sum2<NW>(sq, sk, s_red[0]);
             const float iq = 1.0f / sqrtf((float)(sq / HD) + 1e-6f);
             const float ik = 1.0f / sqrtf((float)(sk / HD) + 1e-6f);
-            qa = (qa * iq) * (nw + 1.0f);
-            ka = (ka * ik) * (nw + 1.0f);
+            qa = (qa * iq) * (nwj + 1.0f);
+            ka = (ka * ik) * (nwj + 1.0f);
         }
         if (a.flags & VX27_DN_PRE_L2) {        // l2norm + q/sqrt(hd), vx27_qfwd.c:124-130
             double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
-            block_sum2(sq, sk, s_red[1]);
+            block_sum2<NW>(sq, sk, s_red[1]);
             qa = qa * (1.0f / sqrtf((float)sq + 1e-6f));
             ka = ka * (1.0f / sqrtf((float)sk + 1e-6f));
             qa = qa * qs;
         }
         {                                       // inside step_exact, vx27_deltanet.c:77-80
             double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
-            block_sum2(sq, sk, s_red[2]);
-            const float qn = qa * (1.0f / sqrtf((float)sq + 1e-6f));
-            s_qn[j] = qn * qs;
-            s_kn[j] = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+            block_sum2<NW>(sq, sk, s_red[2]);
+            if (qk_lane) {
+                const float qn = qa * (1.0f / sqrtf((float)sq + 1e-6f));
+                s_qn[j] = qn * qs;
+                s_kn[j] = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+            }
         }
         __syncthreads();
         const double beta = gt.x, decay = gt.y;
-        // ---- S *= decay ; kv = S^T kn   (double, rows in order)
+        // ---- S *= decay ; kv = S^T kn   (double, rows in order within the lane)
         double kv = 0.0;
 #pragma unroll
-        for (int i = 0; i < HD; i += 4) {
-            const float4 kn4 = *(const float4 *)&s_kn[i];
+        for (int u = 0; u < RR; u += 4) {
+            const float4 kn4 = *(const float4 *)&s_kn[part * RR + u];
             const float knv[4] = {kn4.x, kn4.y, kn4.z, kn4.w};
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const float sd = (float)((double)Sc[i + u] * decay);
-                Sc[i + u] = sd;
-                kv = kv + (double)sd * (double)knv[u];
+            for (int e = 0; e < 4; e++) {
+                const float sd = (float)((double)Sc[u + e] * decay);
+                Sc[u + e] = sd;
+                kv = kv + (double)sd * (double)knv[e];
             }
         }
+        kv = part_sum<R>(kv);
         // ---- S += kn (x) (v - kv)*beta ; o = S^T qn
         // (compiler barrier: kn is re-read from LDS instead of held in registers)
         __asm__ volatile("" ::: "memory");
         const double dl = ((double)va - kv) * beta;
         double o = 0.0;
 #pragma unroll
-        for (int i = 0; i < HD; i += 4) {
-            const float4 kn4 = *(const float4 *)&s_kn[i];
-            const float4 qn4 = *(const float4 *)&s_qn[i];
+        for (int u = 0; u < RR; u += 4) {
+            const float4 kn4 = *(const float4 *)&s_kn[part * RR + u];
+            const float4 qn4 = *(const float4 *)&s_qn[part * RR + u];
             const float knv[4] = {kn4.x, kn4.y, kn4.z, kn4.w};
             const float qnv[4] = {qn4.x, qn4.y, qn4.z, qn4.w};
 #pragma unroll
-            for (int u = 0; u < 4; u++) {
-                const float su = (float)((double)Sc[i + u] + (double)knv[u] * dl);
-                Sc[i + u] = su;
-                o = o + (double)su * (double)qnv[u];
+            for (int e = 0; e < 4; e++) {
+                const float su = (float)((double)Sc[u + e] + (double)knv[e] * dl);
+                Sc[u + e] = su;
+                o = o + (double)su * (double)qnv[e];
             }
         }
+        o = part_sum<R>(o);
         float of = (float)o;
         // ---- gated output norm (vx27_qfwd.c:147-151)
         if (a.flags & VX27_DN_OUT_GATE) {
-            double so = (double)of * (double)of, unused = 0.0;
-            block_sum2(so, unused, s_red[3]);
+            double so = v_lane ? (double)of * (double)of : 0.0, unused = 0.0;
+            block_sum2<NW>(so, unused, s_red[3]);
             const float is = 1.0f / sqrtf((float)(so / HD) + 1e-6f);
-            const float zz = a.z[sb * a.z_tok + (size_t)vh * HD + j];
-            of = ((of * is) * nw) * silu_f(zz);
+            const float zz = a.z[sb * a.z_tok + (size_t)vh * HD + col];
+            of = ((of * is) * nwc) * silu_f(zz);
         } else {
             __syncthreads();   // s_qn/s_kn are rewritten by the next step
         }
-        if (a.out) a.out[sb * a.out_tok + (size_t)vh * HD + j] = of;
-        if (a.out_packed) vx_pack_store(a.out_packed, a.B, b, vh * HD + j, of);
+        if (v_lane) {
+            if (a.out) a.out[sb * a.out_tok + (size_t)vh * HD + col] = of;
+            if (a.out_packed) vx_pack_store(a.out_packed, a.B, b, vh * HD + col, of);
+        }
     }
 
     // ---- write back state and conv state
 #pragma unroll
-    for (int i = 0; i < HD; i++)
-        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Sc[i]), Sr, j * 4, i * HD * 4, 0);
+    for (int u = 0; u < RR; u++)
+        __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Sc[u]), Sr, col * 4, (part * RR + u) * HD * 4, 0);
     if (conv) {
+        if (qk_lane) {
 #pragma unroll
-        for (int t = 0; t < 3; t++) {
-            cst[chq * 3 + t] = cq[t];
-            cst[chk * 3 + t] = ck[t];
-            cst[chv * 3 + t] = cv[t];
+            for (int t = 0; t < 3; t++) {
+                cst[chq * 3 + t] = cq[t];
+                cst[chk * 3 + t] = ck[t];
+            }
+        }
+        if (v_lane) {
+#pragma unroll
+            for (int t = 0; t < 3; t++) cst[chv * 3 + t] = cv[t];
         }
     }
 }
@@ -228,7 +279,16 @@ __global__ __launch_bounds__(256) void dn_conv_kernel(ConvArgs a) {
 
 int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a) {
     VX_REQUIRE(!a.fused_conv || a.nv == a.nqk, "dn recurrence: fused conv needs nv == nqk");
-    VX_LAUNCH(ctx, dn_decode_kernel, dim3((unsigned)(a.B * a.nv)), dim3(HD), a);
+    // split each state column over R lanes when there are few heads to spread
+    // over the 256 CUs (one workgroup per head)
+    const int heads = a.B * a.nv;
+    const dim3 grid((unsigned)heads);
+    if (heads >= 1024)
+        VX_LAUNCH(ctx, dn_decode_kernel<1>, grid, dim3(HD * 1), a);
+    else if (heads >= 256)
+        VX_LAUNCH(ctx, dn_decode_kernel<2>, grid, dim3(HD * 2), a);
+    else
+        VX_LAUNCH(ctx, dn_decode_kernel<4>, grid, dim3(HD * 4), a);
     return 0;
 }
 

@@ -130,7 +130,7 @@ __device__ __forceinline__ bf16x8_t load_bf16x8(const uint16_t *p) {
 }
 
 // grid (n_split, n_kv, B), block 64 (one wave)
-__global__ __launch_bounds__(64) void gqa_split(SplitArgs a) {
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void gqa_split(SplitArgs a) {
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x, g = lane >> 4, n = lane & 15;
     const int qg = a.n_q / a.n_kv;

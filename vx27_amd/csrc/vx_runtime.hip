@@ -124,7 +124,10 @@ extern "C" int vx27_hip_prof_read(vx27_hip_ctx *ctx, const char *name, int *coun
     double tot = 0.0;
     for (int i = 0; i < ctx->prof_n; i++) {
         const vx_prof_rec *r = &ctx->prof[i];
-        if (!r->name || strcmp(r->name, name) != 0) continue;
+        // a template's instances (kernel<1>, kernel<4>, ...) count under its name
+        const size_t ln = strlen(name);
+        if (!r->name || strncmp(r->name, name, ln) != 0 || (r->name[ln] != '\0' && r->name[ln] != '<'))
+            continue;
         float ms = 0.0f;
         VX_HIP(hipEventElapsedTime(&ms, r->e0, r->e1));
         tot += ms;
