@@ -1,6 +1,7 @@
 """Token-mixer benchmark on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload NAME]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--workload c5|dn_conv]
+                    [--context L] [--no-extra] [--no-cpu]
 
 Prints ONE JSON line.  A "step" is one decode step of the workload (one token
 for every sequence of the batch), inputs already resident in HBM.  `value` is
@@ -8,18 +9,28 @@ mixer microseconds per token (whole job), lower is better.  The line also
 carries:
   roofline      the dominant kernel's algorithmic bytes per launch divided by
                 its average duration, measured with HIP events on the
-                library's stream over the timed region, against 8 TB/s
+                library's stream during one profiled step, against 8 TB/s;
+                `traffic` is the HBM bytes per launch that rocprofv3's
+                FETCH_SIZE and WRITE_SIZE counters read for that kernel at the
+                default workload (scaled by a copy-kernel calibration)
   cpu_baseline  the oracle (CPU restatement of the reference path) timed on
                 this host on a bounded sample of the same workload
   extra         the other decode configurations, measured the same way
 
 Workloads (synthetic, seeded, random-init):
+  c5        (default) one decode step of all 64 token mixers of the model:
+            48 Gated DeltaNet mixers (16 QK / 48 V heads, 128x128 fp32 state
+            per V head, conv, gates, gated norm) and 16 gated GQA mixers
+            (24 Q / 4 KV heads of 256, QK RMSNorm, partial RoPE, sigmoid gate)
+            with their input and output projections (bf16 weights, hidden
+            5120), batch 4 at context 131072 (bf16 KV cache); the 64 layers
+            are replayed as one HIP graph
   dn_conv   batched Gated DeltaNet decode with the fused causal conv:
             64 sequences x 16 heads x 128x128 fp32 state, 6144 conv channels
             (bf16 weights), l2norm q/k, exact delta rule; 256 steps
-  gqa8k     gated GQA decode, 24Q/4KV hd 256, bf16 KV cache of 8192
-            positions, batch 1 and 32
-  dn_recur  DeltaNet recurrence alone, 1 sequence x 16 heads, 2000 steps
+Extras (without --no-extra): dn_conv, gated GQA decode at 8192 positions
+(batch 1 and 32), and the DeltaNet recurrence alone (1 sequence x 16 heads,
+2000 steps).
 """
 from __future__ import annotations
 
@@ -36,6 +47,10 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK = 8.0e12           # bytes/s, MI355X
+# HBM bytes per gqa_split launch at batch 4, context 131072: FETCH_SIZE (x2, the
+# factor a plain copy kernel of known size gives) + WRITE_SIZE, rocprofv3 --pmc
+# runs of this script, summarised in profiles/c5_decode_step_pmc.txt
+GQA_SPLIT_TRAFFIC_B4_L131072 = 2.1754e9
 METRIC = "mixer µs/token decode (B=1..64) + % HBM roofline; prefill tok/s + MFMA util"
 
 
@@ -370,8 +385,8 @@ def main():
     ap.add_argument("--no-cpu", action="store_true")
     args = ap.parse_args()
     if args.gpus != 1:
-        print(f"bench.py: this build measures one GPU only (asked for {args.gpus}); the mixers "
-              "shard per (sequence, head) with no exchange -- see DESIGN.md", file=sys.stderr)
+        print(f"bench.py: measures one GPU only (asked for {args.gpus}); the mixers shard per "
+              "(sequence, head) with no exchange, so N GPUs run N independent shards", file=sys.stderr)
         sys.exit(2)
     sys.path.insert(0, os.path.join(ROOT, "tests"))
     from vx27_amd import lib as L
@@ -389,6 +404,7 @@ def main():
                   "deltanet_layers": 48, "gqa_layers": 16, "deltanet_v_heads": 48, "weights": "bf16",
                   "kv_cache": "bf16", "state": "fp32"}
         kbytes, kus = res["kernel_alg_bytes"], res["kernel_us"]
+        traffic = GQA_SPLIT_TRAFFIC_B4_L131072 if args.context == 131072 else None
         step_frac = res["step_GBs"] * 1e9 / HBM_PEAK
         extra["c5_step"] = {k: v for k, v in res.items() if k != "cpu"}
         extra["c5_step"]["step_roofline_frac"] = round(step_frac, 4)
@@ -399,6 +415,7 @@ def main():
         ms_step = res["us_per_step"] / 1e3
         config = {"workload": res["workload"], "batch": 64, "heads": 16, "head_dim": 128}
         kbytes, kus = res["alg_bytes"], res["kernel_us"]
+        traffic = None
         dtype = "fp32 (fp64 accumulation)"
     if not args.no_extra:
         if args.workload != "dn_conv":
@@ -426,7 +443,7 @@ def main():
         "dtype": dtype, "data": "synthetic (seeded random inputs and random-init weights)",
         "config": config,
         "roofline": {"bound": "hbm", "achieved": round(ach / 1e9, 1), "peak": HBM_PEAK / 1e9,
-                     "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4), "traffic": None,
+                     "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4), "traffic": traffic,
                      "kernel": res["kernel"], "kernel_us": round(kus, 2),
                      "alg_bytes_per_launch": kbytes},
         "cpu_baseline": res.get("cpu"),
