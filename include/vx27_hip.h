@@ -58,6 +58,15 @@ int vx27_hip_prof_read(vx27_hip_ctx *ctx, const char *kernel, int *count, double
  * device VX27_HIP_DEVICE from the environment, default 0). */
 vx27_hip_ctx *vx27_hip_default_ctx(void);
 
+/* Route switch for callers that keep their own CPU path, mirroring
+ * vx27_gpu_reg_on/off (vx27_gpu_reg.h:10-11): enable turns the route on only
+ * if the default context opens (returns 0, else -1 with last_error set);
+ * vx27_hip_enabled() is what the caller tests before taking the device path.
+ * Off by default.  The library's own functions do not consult it. */
+int vx27_hip_enable(void);
+void vx27_hip_disable(void);
+int vx27_hip_enabled(void);
+
 /* Error behaviour of the void drop-ins, which cannot return a status:
  * VX27_HIP_ERR_ABORT (default) prints the error and aborts the process;
  * VX27_HIP_ERR_POISON fills the outputs with NaN, records the error and

@@ -75,6 +75,9 @@ def test_entry_points_validate_without_device():
     if so.vx27_hip_device_count() == 0:
         assert so.vx27_hip_open(C.byref(h), 0, err, 256) == -1
         assert b"no HIP device" in err.value or b"device" in err.value
+        # the route switch stays off when no context can open
+        assert so.vx27_hip_enable() == -1
+    assert so.vx27_hip_enabled() == 0
 
 
 def test_product_never_imports_the_oracle():

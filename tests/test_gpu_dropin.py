@@ -115,3 +115,15 @@ def test_dropin_poison_mode(M):
         assert np.all(np.isnan(o))
     finally:
         lib.vx27_hip_set_error_mode(L.ERR_ABORT)
+
+
+def test_route_switch(M):
+    """vx27_hip_enable/disable mirror vx27_gpu_reg_on/off (vx27_gpu_reg.h:10-11):
+    off by default, on once the default context is open."""
+    from vx27_amd import lib as L
+    lib = L.lib()
+    assert lib.vx27_hip_enabled() == 0
+    assert lib.vx27_hip_enable() == 0
+    assert lib.vx27_hip_enabled() == 1
+    lib.vx27_hip_disable()
+    assert lib.vx27_hip_enabled() == 0

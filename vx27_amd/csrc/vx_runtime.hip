@@ -3,6 +3,8 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
+
 #include "vx_common.h"
 
 static thread_local char g_err[512] = "";
@@ -237,6 +239,16 @@ static int g_errmode = VX27_HIP_ERR_ABORT;
 
 extern "C" void vx27_hip_set_error_mode(int mode) { g_errmode = mode; }
 extern "C" int vx27_hip_get_error_mode(void) { return g_errmode; }
+
+static std::atomic<int> g_route_on{0};
+
+extern "C" int vx27_hip_enable(void) {
+    if (!vx27_hip_default_ctx()) return -1;
+    g_route_on.store(1);
+    return 0;
+}
+extern "C" void vx27_hip_disable(void) { g_route_on.store(0); }
+extern "C" int vx27_hip_enabled(void) { return g_route_on.load(); }
 
 extern "C" vx27_hip_ctx *vx27_hip_default_ctx(void) {
     if (g_default) return g_default;

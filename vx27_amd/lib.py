@@ -63,6 +63,9 @@ _SIGS = {
     "vx27_hip_device_count": (C.c_int, []),
     "vx27_hip_version": (C.c_char_p, []),
     "vx27_hip_default_ctx": (VP, []),
+    "vx27_hip_enable": (C.c_int, []),
+    "vx27_hip_disable": (None, []),
+    "vx27_hip_enabled": (C.c_int, []),
     "vx27_hip_prof_enable": (C.c_int, [VP, C.c_int]),
     "vx27_hip_prof_read": (C.c_int, [VP, C.c_char_p, C.POINTER(C.c_int), C.POINTER(C.c_double)]),
     "vx27_hip_set_error_mode": (None, [C.c_int]),
