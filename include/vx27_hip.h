@@ -129,6 +129,26 @@ typedef struct {
  * and write S once per call. */
 int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d);
 
+/* DeltaNet prefill: T tokens of B sequences through step_exact semantics
+ * (vx27_deltanet.c:71-102 token by token, as vx27_qlayer_batch applies it,
+ * vx27_qfwd.c:249-313), computed in chunks of 64 tokens with bf16 MFMA
+ * products and the fp32 state carried between chunks.  q and k are
+ * l2-normalised (and q scaled by 1/sqrt(hd)) inside, as step_exact does.
+ * Accuracy is that of bf16 products (not the fp32 recurrence's). */
+typedef struct {
+    int B, T;
+    int nqk, nv;    /* value head vh uses QK head vh*nqk/nv; nv a multiple of nqk */
+    int hd;         /* 128 */
+    unsigned flags; /* 0 */
+    float *S;       /* [B][nv][hd][hd] fp32: initial state in, final state out */
+    const uint16_t *q, *k;       /* bf16 [B][T][nqk][hd] */
+    const uint16_t *v;           /* bf16 [B][T][nv][hd] */
+    const float *a, *b;          /* [B][T][nv] gate projections */
+    const float *A_log, *dt_bias;/* [nv] */
+    float *out;                  /* [B][T][nv][hd] */
+} vx27_dn_prefill_desc;
+int vx27_hip_dn_prefill(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d);
+
 /* ---------------------------------------------------------- GQA decode */
 /* KV cache format (bf16), for B sequences x n_kv heads x L positions, hd 256:
  *   K: [B][n_kv][L][hd]            one row per position

@@ -1,0 +1,113 @@
+"""GPU parity of the prefill mixers through the C ABI against the oracle.
+
+DeltaNet prefill (vx27_hip_dn_prefill) is the chunked form of the exact delta
+rule with bf16 MFMA products; its oracle is the reference's own sequential
+step_exact (vx27_deltanet.c:71-102) applied token by token to the same bf16
+inputs widened to fp32 (orc_dn_run).  The chunked products are bf16, so the
+outputs are held to the bf16 bar (|gpu - oracle| <= 2e-2 + 1e-2 |oracle|), not
+to the fp32 recurrence's 1e-5; the final-state error is reported and held to
+the same bf16 bar.  The elementwise bar is loose next to the outputs'
+magnitude (|o| < 0.1 here), so the error is also held to 2% of max|oracle|,
+which a dropped or mis-decayed term of the chunked form exceeds.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from gpu_common import maxabs, oracle_dn, say
+
+pytestmark = pytest.mark.gpu
+
+ATOL, RTOL = 2e-2, 1e-2
+SCALE_TOL = 2e-2
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from vx27_amd import lib as L
+    c = L.Ctx(0)
+    yield c
+    c.close()
+
+
+def run_dn_prefill(ctx, d, S=None, t0=0, t1=None):
+    """Prefill tokens t0..t1-1 of workload d on the device; returns (out, S)."""
+    from vx27_amd import lib as L
+    B, T, nqk, hd = d["q"].shape
+    nv = d["v"].shape[2]
+    t1 = T if t1 is None else t1
+    sl = slice(t0, t1)
+    bufs = {k: ctx.put(np.ascontiguousarray(d[k][:, sl])) for k in ("q", "k", "v", "a", "b")}
+    bufs["A_log"], bufs["dt_bias"] = ctx.put(d["A_log"]), ctx.put(d["dt_bias"])
+    Sd = ctx.put(np.ascontiguousarray(d["S0"] if S is None else S, np.float32))
+    n = t1 - t0
+    ob = ctx.buf(B * n * nv * hd * 4)
+    desc = L.DnPrefillDesc(B, n, nqk, nv, hd, 0, Sd.ptr, bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr,
+                           bufs["a"].ptr, bufs["b"].ptr, bufs["A_log"].ptr, bufs["dt_bias"].ptr, ob.ptr)
+    L.check(L.lib().vx27_hip_dn_prefill(ctx.h, C.byref(desc)), "dn_prefill")
+    out = ob.download((B, n, nv, hd), np.float32)
+    Sn = Sd.download(d["S0"].shape, np.float32)
+    for bb in list(bufs.values()) + [Sd, ob]:
+        bb.free()
+    return out, Sn
+
+
+def oracle_dn_prefill(d):
+    """Sequential step_exact over the bf16 inputs widened to fp32."""
+    from vx27_amd import workloads as W
+    B, T, nqk, hd = d["q"].shape
+    nv = d["v"].shape[2]
+    seq = {k: np.ascontiguousarray(np.swapaxes(W.bf16_to_f32(d[k]), 0, 1)) for k in ("q", "k", "v")}
+    seq.update({k: np.ascontiguousarray(np.swapaxes(d[k], 0, 1)) for k in ("a", "b")})
+    seq.update(A_log=d["A_log"], dt_bias=d["dt_bias"], S0=d["S0"])
+    out, S, _, secs = oracle_dn(seq, 0, B, nqk, nv, T)
+    return np.swapaxes(out, 0, 1), S, secs
+
+
+def check_bf16(got, ref, tag):
+    err = np.abs(got.astype(np.float64) - ref)
+    lim = ATOL + RTOL * np.abs(ref)
+    worst = float((err / lim).max())
+    say(f"  {tag}: max|d|={err.max():.3e} (max|ref|={np.abs(ref).max():.3f}, worst/limit {worst:.3f})")
+    assert np.all(err <= lim), tag
+    assert err.max() <= SCALE_TOL * np.abs(ref).max(), tag
+
+
+def test_dn_prefill_4096(ctx):
+    """One 4096-token prompt, 16 heads, zero state (the prefill workload)."""
+    from vx27_amd import workloads as W
+    d = W.dn_prefill(B=1, T=4096)
+    say("dn_prefill: B=1 T=4096 nqk=nv=16")
+    out, S = run_dn_prefill(ctx, d)
+    ref, Sr, secs = oracle_dn_prefill(d)
+    say(f"  oracle {secs:.2f}s")
+    check_bf16(out, ref, "out")
+    say(f"  final state max|d|={maxabs(S, Sr):.3e} (max|S|={np.abs(Sr).max():.3f})")
+    check_bf16(S, Sr, "state")
+
+
+@pytest.mark.parametrize("B,T,nqk,nv,S0", [(2, 200, 4, 8, 0.02), (1, 193, 4, 12, 0.02), (3, 64, 2, 2, 0.0),
+                                           (1, 5, 16, 48, 0.02)])
+def test_dn_prefill_shapes(ctx, B, T, nqk, nv, S0):
+    """Ragged T (partial last chunk), several sequences, nv = 3 nqk (QK head
+    sharing), a nonzero initial state, and head counts off the XCD grouping."""
+    from vx27_amd import workloads as W
+    d = W.dn_prefill(B=B, T=T, nqk=nqk, nv=nv, S0_std=S0)
+    say(f"dn_prefill: B={B} T={T} nqk={nqk} nv={nv} S0_std={S0}")
+    out, S = run_dn_prefill(ctx, d)
+    ref, Sr, _ = oracle_dn_prefill(d)
+    check_bf16(out, ref, "out")
+    check_bf16(S, Sr, "state")
+
+
+def test_dn_prefill_split_prompt(ctx):
+    """A prompt prefilled in two calls at a chunk boundary (state carried in
+    global memory) equals the one-call result bit for bit."""
+    from vx27_amd import workloads as W
+    d = W.dn_prefill(B=2, T=384, nqk=4, nv=8, S0_std=0.02, config=41)
+    out, S = run_dn_prefill(ctx, d)
+    o1, S1 = run_dn_prefill(ctx, d, t0=0, t1=128)
+    o2, S2 = run_dn_prefill(ctx, d, S=S1, t0=128, t1=384)
+    assert np.array_equal(np.concatenate([o1, o2], axis=1), out)
+    assert np.array_equal(S2, S)

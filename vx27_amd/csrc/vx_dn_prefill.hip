@@ -1,0 +1,376 @@
+// Gated DeltaNet prefill on gfx950: the chunked (WY) form of the exact delta
+// rule, bf16 MFMA for the chunk products, fp32 state carried across chunks.
+//
+// Per token the reference (vx27_deltanet_step_exact, vx27_deltanet.c:71-102,
+// applied token by token by vx27_qlayer_batch, vx27_qfwd.c:249-313) does
+//   kn = l2norm(k), qn = l2norm(q)/sqrt(128), S <- e^g S,
+//   u = beta (v - S^T kn), S <- S + kn u^T, o = S^T qn.
+// Over a chunk of C = 64 tokens with state S0 at its start and cumulative
+// log-decay gam_t = g_1 + ... + g_t this is exactly
+//   U  = T (beta V) - T (beta e^gam K) S0 = Ut + NW S0,     T = (I + A)^-1,
+//   A[s][r] = beta_s e^(gam_s - gam_r) kn_s.kn_r   (r < s),
+//   O  = (e^gam Q) S0 + P U,   P[t][s] = e^(gam_t - gam_s) qn_t.kn_s (s <= t),
+//   S  = e^gam_C S0 + Kt^T U,  Kt[t] = e^(gam_C - gam_t) kn_t,
+// where every exponent is <= 0.  Only S0 couples the chunks.
+//
+// dnp_prep  (grid chunks x value heads x sequences, fully parallel): gates,
+//           norms, K K^T and Q K^T on MFMA, the triangular solve for Ut and
+//           NW = -T (beta e^gam K) by forward substitution in fp32 (one lane
+//           per column), and the chunk's MFMA operand tiles written to a
+//           record in scratch.
+// dnp_scan  (grid value heads x 8 column slices x sequences): walks the
+//           chunks in order; a workgroup owns 16 value columns of one head's
+//           state (columns are independent in all three products), keeps
+//           them in MFMA accumulators and runs 14 MFMAs per wave per chunk.
+//           The 8 slices of a head are placed on one XCD so the records they
+//           share are read from HBM once.
+//
+// Operand tiles ([rows/16][k/32][64 lanes][8] bf16) follow the MFMA operand
+// layout of v_mfma_f32_16x16x32_bf16: lane (g = l/16, m = l%16) of an A tile
+// holds A[m][8g..8g+7]; a wave's tile is 1 KiB of contiguous memory.
+#include "vx_dn.h"
+
+namespace {
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef float floatx4_t __attribute__((ext_vector_type(4)));
+
+constexpr int CH = 64;            // chunk length
+constexpr int NSLICE = 8;         // 16-column slices of a head's state
+constexpr int KP = HD + 4;        // padded fp32 row of kn in LDS
+constexpr int QP = HD + 8;        // padded bf16 row of qn in LDS
+constexpr int PP = CH + 8;        // padded bf16 row of P in LDS
+
+// chunk record (bytes)
+constexpr size_t R_NW = 0;                       // -W   [4][4][64][8] bf16
+constexpr size_t R_QE = R_NW + 4 * 4 * 512 * 2;  // e^gam qn  [4][4][64][8] bf16
+constexpr size_t R_KT = R_QE + 4 * 4 * 512 * 2;  // Kt^T [8][2][64][8] bf16
+constexpr size_t R_P = R_KT + 8 * 2 * 512 * 2;   // P    [4][2][64][8] bf16
+constexpr size_t R_UT = R_P + 4 * 2 * 512 * 2;   // Ut   [4 rb][8 cs][64][4] fp32
+constexpr size_t REC = R_UT + 4 * 8 * 64 * 4 * 4;
+
+struct PrepArgs {
+    int T, nqk, nv, NC;
+    const uint16_t *q, *k, *v;       // [B][T][nqk|nqk|nv][128] bf16
+    const float *a, *b;              // [B][T][nv]
+    const float *A_log, *dt_bias;    // [nv]
+    char *rec;                       // [B][nv][NC] records
+    float *gC;                       // [B][nv][NC] e^gam_C
+};
+
+__device__ __forceinline__ uint32_t pack2(float x, float y) {
+    return (uint32_t)vx_f32_to_bf16(x) | ((uint32_t)vx_f32_to_bf16(y) << 16);
+}
+__device__ __forceinline__ uint4 pack8(const float *f) {
+    return make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
+}
+__device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) {
+    bf16x8_t r;
+    __builtin_memcpy(&r, &u, 16);
+    return r;
+}
+
+__global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
+    const int c = blockIdx.x, vh = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, m = lane & 15;
+    const int qh = vh * p.nqk / p.nv;
+    const int t0 = c * CH;
+    const int nvalid = min(CH, p.T - t0);
+
+    __shared__ float kn_f[CH][KP];        // kn (fp32); later -W
+    __shared__ uint16_t qn_b[CH][QP];     // qn (bf16); later P (bf16, row stride PP)
+    __shared__ float A_s[CH][CH];
+    __shared__ double gam_s[CH];
+    __shared__ float beta_s[CH], eg_s[CH], egc_s[CH];   // beta, e^gam_t, e^(gam_C - gam_t)
+
+    // gates and the cumulative log-decay (wave 0, lane = token); masked
+    // tokens get beta = 0 and g = 0, which leaves U and S unchanged
+    if (wave == 0) {
+        double beta = 0.0, glog = 0.0;
+        if (lane < nvalid) {
+            const size_t e = ((size_t)b * p.T + t0 + lane) * p.nv + vh;
+            beta = 1.0 / (1.0 + exp(-(double)p.b[e]));
+            glog = -exp((double)p.A_log[vh]) * softplus_d((double)p.a[e] + (double)p.dt_bias[vh]);
+        }
+        double s = glog;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const double o = __shfl_up(s, off, 64);
+            if (lane >= off) s += o;
+        }
+        const double sC = __shfl(s, 63, 64);
+        gam_s[lane] = s;
+        beta_s[lane] = (float)beta;
+        eg_s[lane] = (float)exp(s);
+        egc_s[lane] = (float)exp(sC - s);
+    }
+
+    // q, k rows of this wave's 16 tokens: lane holds dims 2l, 2l+1
+    const float qscale = 1.0f / sqrtf((float)HD);
+    for (int r = 0; r < 16; r++) {
+        const int t = wave * 16 + r;
+        float k0 = 0.f, k1 = 0.f, q0 = 0.f, q1 = 0.f;
+        if (t < nvalid) {
+            const size_t row = ((size_t)b * p.T + t0 + t) * p.nqk + qh;
+            const uint32_t kw = *(const uint32_t *)(p.k + row * HD + 2 * lane);
+            const uint32_t qw = *(const uint32_t *)(p.q + row * HD + 2 * lane);
+            k0 = vx_bf16_to_f32((uint16_t)kw);
+            k1 = vx_bf16_to_f32((uint16_t)(kw >> 16));
+            q0 = vx_bf16_to_f32((uint16_t)qw);
+            q1 = vx_bf16_to_f32((uint16_t)(qw >> 16));
+        }
+        const double ssk = vx_wave_sum_f64((double)k0 * k0 + (double)k1 * k1);
+        const double ssq = vx_wave_sum_f64((double)q0 * q0 + (double)q1 * q1);
+        const float ik = 1.0f / sqrtf((float)ssk + 1e-6f);
+        const float iq = 1.0f / sqrtf((float)ssq + 1e-6f);
+        kn_f[t][2 * lane] = k0 * ik;
+        kn_f[t][2 * lane + 1] = k1 * ik;
+        *(uint32_t *)&qn_b[t][2 * lane] = pack2((q0 * iq) * qscale, (q1 * iq) * qscale);
+    }
+    __syncthreads();
+
+    char *rec = p.rec + (((size_t)b * p.nv + vh) * p.NC + c) * REC;
+    const double gamC = gam_s[CH - 1];
+    if (tid == 0) p.gC[((size_t)b * p.nv + vh) * p.NC + c] = (float)exp(gamC);
+
+    // K K^T and Q K^T for row block `wave`; Qe tiles on the way
+    floatx4_t acck[4], accq[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+        acck[nb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+        accq[nb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+    }
+    const int rowA = wave * 16 + m;
+    const float egA = eg_s[rowA];
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        const int d0 = 32 * ks + 8 * g;
+        const uint4 qa = *(const uint4 *)&qn_b[rowA][d0];
+        const bf16x8_t aq = as_bf16x8(qa);
+        const bf16x8_t ak = as_bf16x8(pack8(&kn_f[rowA][d0]));
+        {   // Qe tile (row block wave, k-step ks): e^gam_t * qn
+            const uint16_t *qs = (const uint16_t *)&qa;
+            float f[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) f[e] = egA * vx_bf16_to_f32(qs[e]);
+            *(uint4 *)(rec + R_QE + ((size_t)(wave * 4 + ks) * 64 + lane) * 16) = pack8(f);
+        }
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) {
+            const bf16x8_t bk = as_bf16x8(pack8(&kn_f[nb * 16 + m][d0]));
+            acck[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, bk, acck[nb], 0, 0, 0);
+            accq[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq, bk, accq[nb], 0, 0, 0);
+        }
+    }
+    // Kt^T tiles: rows = key dims (8 blocks), k = tokens (2 steps); 4 per wave
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int tile = wave * 4 + j, rb = tile >> 1, ks = tile & 1;
+        const int i = rb * 16 + m;
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int t = 32 * ks + 8 * g + e;
+            f[e] = egc_s[t] * kn_f[t][i];
+        }
+        *(uint4 *)(rec + R_KT + ((size_t)tile * 64 + lane) * 16) = pack8(f);
+    }
+    __syncthreads();   // qn_b is reused for P below
+
+    // A (fp32, for the solve) and P (bf16, staged for its operand tiles)
+    uint16_t *P_b = &qn_b[0][0];
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int s = wave * 16 + 4 * g + i, r = nb * 16 + m;
+            const float ed = r <= s ? expf((float)(gam_s[s] - gam_s[r])) : 0.0f;
+            A_s[s][r] = r < s ? beta_s[s] * ed * acck[nb][i] : 0.0f;
+            P_b[s * PP + r] = vx_f32_to_bf16(ed * accq[nb][i]);
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+        const uint4 v = *(const uint4 *)&P_b[rowA * PP + 32 * ks + 8 * g];
+        *(uint4 *)(rec + R_P + ((size_t)(wave * 2 + ks) * 64 + lane) * 16) = v;
+    }
+
+    // forward substitution x = (I + A)^-1 rhs, one column per thread:
+    // columns 0..127 of beta V (-> Ut), 128..255 of beta e^gam K (-> W)
+    float x[CH];
+    if (tid < HD) {
+#pragma unroll
+        for (int t = 0; t < CH; t++) {
+            float vv = 0.0f;
+            if (t < nvalid) vv = vx_bf16_to_f32(p.v[(((size_t)b * p.T + t0 + t) * p.nv + vh) * HD + tid]);
+            x[t] = beta_s[t] * vv;
+        }
+    } else {
+#pragma unroll
+        for (int t = 0; t < CH; t++) x[t] = (beta_s[t] * eg_s[t]) * kn_f[t][tid - HD];
+    }
+#pragma unroll
+    for (int i = 1; i < CH; i++) {
+        float acc = x[i];
+#pragma unroll
+        for (int k4 = 0; k4 < i; k4 += 4) {
+            const float4 a4 = *(const float4 *)&A_s[i][k4];   // A[i][k] = 0 for k >= i
+            acc -= a4.x * x[k4];
+            if (k4 + 1 < CH) acc -= a4.y * x[k4 + 1];
+            if (k4 + 2 < CH) acc -= a4.z * x[k4 + 2];
+            if (k4 + 3 < CH) acc -= a4.w * x[k4 + 3];
+        }
+        x[i] = acc;
+    }
+    if (tid < HD) {
+        // Ut column tid in C-layout tiles [rb][cs][lane (g,n)][i]
+        const int cs = tid >> 4, n = tid & 15;
+        float *ut = (float *)(rec + R_UT);
+#pragma unroll
+        for (int t = 0; t < CH; t++) {
+            const int rb = t >> 4, gg = (t & 15) >> 2, i = t & 3;
+            ut[(((size_t)rb * 8 + cs) * 64 + gg * 16 + n) * 4 + i] = x[t];
+        }
+    }
+    __syncthreads();   // every read of kn_f is done
+    if (tid >= HD) {
+#pragma unroll
+        for (int t = 0; t < CH; t++) kn_f[t][tid - HD] = -x[t];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++)
+        *(uint4 *)(rec + R_NW + ((size_t)(wave * 4 + ks) * 64 + lane) * 16) = pack8(&kn_f[rowA][32 * ks + 8 * g]);
+}
+
+struct ScanArgs {
+    int T, nv, NC, xcd_map;
+    const char *rec;
+    const float *gC;
+    float *S;        // [B][nv][128][128]
+    float *out;      // [B][T][nv][128]
+};
+
+struct ChunkOps {
+    uint4 nw[4], qe[4], kt[4], pp[2];
+    float4 ut;
+};
+
+__device__ __forceinline__ void load_ops(ChunkOps &o, const char *rec, int wave, int lane, int slice) {
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        o.nw[ks] = *(const uint4 *)(rec + R_NW + ((size_t)(wave * 4 + ks) * 64 + lane) * 16);
+        o.qe[ks] = *(const uint4 *)(rec + R_QE + ((size_t)(wave * 4 + ks) * 64 + lane) * 16);
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++)   // Kt^T tiles (rb 2w + j/2, ks j%2)
+        o.kt[j] = *(const uint4 *)(rec + R_KT + ((size_t)(wave * 4 + j) * 64 + lane) * 16);
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++)
+        o.pp[ks] = *(const uint4 *)(rec + R_P + ((size_t)(wave * 2 + ks) * 64 + lane) * 16);
+    o.ut = *(const float4 *)(rec + R_UT + (((size_t)wave * 8 + slice) * 64 + lane) * 16);
+}
+
+__global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
+    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int b = blockIdx.y, bid = blockIdx.x;
+    int vh, slice;
+    if (p.xcd_map) {   // the 8 slices of a head on one XCD (workgroups go round-robin over 8)
+        const int xcd = bid & 7, idx = bid >> 3;
+        slice = idx % NSLICE;
+        vh = (idx / NSLICE) * 8 + xcd;
+    } else {
+        vh = bid / NSLICE;
+        slice = bid % NSLICE;
+    }
+    const int col = slice * 16 + n;
+
+    __shared__ uint16_t S_l[16][HD + 8];   // S slice, bf16, [column][key dim]
+    __shared__ uint16_t U_l[16][CH + 8];   // U slice, bf16, [column][token]
+
+    // state rows 32w .. 32w+31 (row blocks 2w, 2w+1) of the slice, C layout
+    float *Sg = p.S + ((size_t)b * p.nv + vh) * HD * HD;
+    floatx4_t S[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) S[r][i] = Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + col];
+
+    const char *rec0 = p.rec + ((size_t)b * p.nv + vh) * p.NC * REC;
+    const float *gC = p.gC + ((size_t)b * p.nv + vh) * p.NC;
+    ChunkOps cur, nxt;
+    load_ops(cur, rec0, wave, lane, slice);
+    for (int c = 0; c < p.NC; c++) {
+        if (c + 1 < p.NC) load_ops(nxt, rec0 + (size_t)(c + 1) * REC, wave, lane, slice);
+        // S (bf16) -> LDS as [column][key dim]
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int d = (2 * wave + r) * 16 + 4 * g;
+            *(uint2 *)&S_l[n][d] = make_uint2(pack2(S[r][0], S[r][1]), pack2(S[r][2], S[r][3]));
+        }
+        __syncthreads();
+        bf16x8_t sb[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) sb[ks] = as_bf16x8(*(const uint4 *)&S_l[n][32 * ks + 8 * g]);
+        // U = Ut - W S for tokens 16w .. 16w+15
+        floatx4_t U = (floatx4_t){cur.ut.x, cur.ut.y, cur.ut.z, cur.ut.w};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) U = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.nw[ks]), sb[ks], U, 0, 0, 0);
+        *(uint2 *)&U_l[n][wave * 16 + 4 * g] = make_uint2(pack2(U[0], U[1]), pack2(U[2], U[3]));
+        __syncthreads();
+        bf16x8_t ub[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) ub[ks] = as_bf16x8(*(const uint4 *)&U_l[n][32 * ks + 8 * g]);
+        // O = (e^gam Q) S + P U
+        floatx4_t O = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) O = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.qe[ks]), sb[ks], O, 0, 0, 0);
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) O = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.pp[ks]), ub[ks], O, 0, 0, 0);
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int t = c * CH + wave * 16 + 4 * g + i;
+            if (t < p.T) p.out[(((size_t)b * p.T + t) * p.nv + vh) * HD + col] = O[i];
+        }
+        // S = e^gam_C S + Kt^T U
+        const float gc = gC[c];
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            S[r] *= gc;
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+                S[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.kt[2 * r + ks]), ub[ks], S[r], 0, 0, 0);
+        }
+        cur = nxt;
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + col] = S[r][i];
+}
+
+}  // namespace
+
+extern "C" int vx27_hip_dn_prefill(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(d, "vx27_hip_dn_prefill: null descriptor");
+    VX_REQUIRE(d->hd == HD, "vx27_hip_dn_prefill: head_dim must be 128 (got %d)", d->hd);
+    VX_REQUIRE(d->B >= 1 && d->T >= 1 && d->nqk >= 1 && d->nv >= d->nqk && d->nv % d->nqk == 0 && d->nv <= 4096,
+               "vx27_hip_dn_prefill: bad sizes B=%d T=%d nqk=%d nv=%d", d->B, d->T, d->nqk, d->nv);
+    VX_REQUIRE(d->flags == 0, "vx27_hip_dn_prefill: flags must be 0");
+    VX_REQUIRE(d->S && d->q && d->k && d->v && d->a && d->b && d->A_log && d->dt_bias && d->out,
+               "vx27_hip_dn_prefill: null pointer");
+    const int NC = (d->T + CH - 1) / CH;
+    const size_t n_rec = (size_t)d->B * d->nv * NC;
+    const size_t gc_off = (n_rec * REC + 255) & ~(size_t)255;
+    void *scr;
+    if (vx_ctx_scratch(ctx, gc_off + n_rec * sizeof(float), &scr)) return -1;
+    PrepArgs pa{d->T, d->nqk, d->nv, NC, d->q, d->k, d->v, d->a, d->b, d->A_log, d->dt_bias,
+                (char *)scr, (float *)((char *)scr + gc_off)};
+    VX_LAUNCH(ctx, dnp_prep, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B), dim3(256), pa);
+    ScanArgs sa{d->T, d->nv, NC, (d->nv % 8) == 0, (const char *)scr, (const float *)((char *)scr + gc_off),
+                d->S, d->out};
+    VX_LAUNCH(ctx, dnp_scan, dim3((unsigned)(d->nv * NSLICE), (unsigned)d->B), dim3(256), sa);
+    return 0;
+}

@@ -28,6 +28,12 @@ class DnDesc(C.Structure):
                 ("A_log", VP), ("dt_bias", VP), ("norm_w", VP), ("z", VP), ("out", VP)]
 
 
+class DnPrefillDesc(C.Structure):
+    _fields_ = [("B", C.c_int), ("T", C.c_int), ("nqk", C.c_int), ("nv", C.c_int), ("hd", C.c_int),
+                ("flags", C.c_uint), ("S", VP), ("q", VP), ("k", VP), ("v", VP), ("a", VP), ("b", VP),
+                ("A_log", VP), ("dt_bias", VP), ("out", VP)]
+
+
 class GqaDesc(C.Structure):
     _fields_ = [("B", C.c_int), ("n_q", C.c_int), ("n_kv", C.c_int), ("hd", C.c_int),
                 ("rope_dim", C.c_int), ("rope_theta", C.c_float), ("rope_yarn", C.c_float),
@@ -77,6 +83,7 @@ _SIGS = {
     "vx27_hip_d2d": (C.c_int, [VP, VP, VP, C.c_size_t]),
     "vx27_hip_memset": (C.c_int, [VP, VP, C.c_int, C.c_size_t]),
     "vx27_hip_dn_decode": (C.c_int, [VP, C.POINTER(DnDesc)]),
+    "vx27_hip_dn_prefill": (C.c_int, [VP, C.POINTER(DnPrefillDesc)]),
     "vx27_hip_gqa_decode": (C.c_int, [VP, C.POINTER(GqaDesc)]),
     "vx27_hip_kv_write": (C.c_int, [VP, VP, VP] + [C.c_int] * 7 + [VP, VP]),
     "vx27_hip_kv_read": (C.c_int, [VP, VP, VP] + [C.c_int] * 7 + [VP, VP]),

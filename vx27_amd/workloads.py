@@ -95,6 +95,23 @@ def dn_conv(B=64, H=16, steps=256, hd=128, config=3, S0_std=0.02, nv=None):
     return d
 
 
+def dn_prefill(B=1, T=4096, nqk=16, nv=16, hd=128, config=4, S0_std=0.0):
+    """Config: one prompt of T tokens; q,k,v ~N(0,1) stored bf16
+    [B][T][heads][128] (q and k are l2-normalised inside, as step_exact does);
+    a,b ~N(0,1) [B][T][nv]; A_log ~U(-2,1), dt_bias ~N(0,0.1); S0 zero."""
+    r = rng(config, "dn_prefill")
+    A_log, dt_bias = dn_heads(r, nv)
+    d = dict(A_log=A_log, dt_bias=dt_bias)
+    d["q"] = bf16_bits(normal(r, (B, T, nqk, hd)))
+    d["k"] = bf16_bits(normal(r, (B, T, nqk, hd)))
+    d["v"] = bf16_bits(normal(r, (B, T, nv, hd)))
+    d["a"] = normal(r, (B, T, nv))
+    d["b"] = normal(r, (B, T, nv))
+    d["S0"] = (normal(r, (B, nv, hd, hd), S0_std) if S0_std > 0
+               else np.zeros((B, nv, hd, hd), np.float32))
+    return d
+
+
 def gqa_decode(B=1, L=8192, n_q=24, n_kv=4, hd=256, config=2):
     """Config: bf16 KV cache of L positions with K,V ~N(0,1) (taken as already
     normed and roped), new token at position L; raw q ~N(0,1) and gate logits
