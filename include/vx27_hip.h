@@ -187,6 +187,34 @@ typedef struct {
  * over positions 0..pos -> * sigmoid(gate). */
 int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d);
 
+/* GQA prefill: T new tokens of each of B sequences at positions pos0..pos0+T-1
+ * (token by token as vx27_qlayer_batch runs the decode glue,
+ * vx27_qfwd.c:314-376): rmsn q,k -> RoPE -> k,v written to the cache (bf16,
+ * format above) -> causal attention of each token over positions 0..its own
+ * (earlier cache rows included) -> * sigmoid(gate).  bf16 MFMA products,
+ * fp32 softmax. */
+typedef struct {
+    int B, T;
+    int n_q, n_kv, hd;       /* 24, 4, 256 */
+    int rope_dim;
+    float rope_theta, rope_yarn;
+    int L;                   /* cache capacity, multiple of 64; pos0 + T <= L */
+    int pos0;                /* position of token 0 (same for every sequence) */
+    unsigned flags;          /* VX27_GQA_NORM_W */
+    /* bf16 raw q and gate logits: element (b, t, h, i) at
+     * q[(b*T + t)*q_tok_stride + h*q_head_stride + i]; 0 strides = dense
+     * [B][T][n_q][hd].  Interleaved q_proj output: head stride 2*hd, gate = q + hd. */
+    const uint16_t *q;
+    size_t q_tok_stride, q_head_stride;
+    const uint16_t *gate;
+    size_t gate_tok_stride, gate_head_stride;
+    const uint16_t *k_new, *v_new;   /* bf16 [B][T][n_kv][hd] raw k and v */
+    const float *q_norm_w, *k_norm_w;/* [hd] */
+    uint16_t *k_cache, *v_cache;
+    float *out;                      /* [B][T][n_q][hd] */
+} vx27_gqa_prefill_desc;
+int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d);
+
 /* Copy n rows of fp32 [n][n_kv][hd] K and V (positions p0..p0+n-1 of
  * sequence b) into / out of the cache format, rounding to bf16 on write. */
 int vx27_hip_kv_write(vx27_hip_ctx *ctx, uint16_t *k_cache, uint16_t *v_cache, int B_total,

@@ -72,6 +72,12 @@ class DnRunArgs(C.Structure):
                 ("A_log", VP), ("dt_bias", VP), ("norm_w", VP), ("z", VP), ("out", VP)]
 
 
+class GqaPrefillArgs(C.Structure):
+    _fields_ = [(n, C.c_int) for n in ("B", "T", "n_q", "n_kv", "hd", "rope_dim", "pos0", "L", "threads")] + \
+               [("rope_theta", C.c_float), ("rope_yarn", C.c_float)] + \
+               [(n, VP) for n in ("q", "gate", "k", "v", "q_norm_w", "k_norm_w", "k_cache", "v_cache", "out")]
+
+
 class DnLayerW(C.Structure):
     _fields_ = [(n, VP) for n in ("ln_w", "w_qkv", "w_z", "w_a", "w_b", "conv_w",
                                    "A_log", "dt_bias", "norm_w", "w_out")]
@@ -123,6 +129,7 @@ def lib():
         "orc_dn_run": (C.c_double, [C.POINTER(DnRunArgs)]),
         "orc_dn_run_avx2": (C.c_double, [C.c_int] * 5 + [F32P, F32P, F32P, F32P, F64P, F64P, F32P]),
         "orc_attend_batch": (C.c_double, [C.POINTER(AttendBatchArgs)]),
+        "orc_gqa_prefill": (C.c_double, [C.POINTER(GqaPrefillArgs)]),
         "orc_matvec_batch": (C.c_double, [VP, C.c_int, F32P, F32P, C.c_int, C.c_int, C.c_int, C.c_int]),
     }
     for name, (res, args) in sig.items():

@@ -223,6 +223,66 @@ double orc_attend_batch(const orc_attend_batch_args *a) {
     return orc_now() - t0;
 }
 
+/* -------------------------------------------------------- GQA prefill */
+typedef struct {
+    const orc_gqa_prefill_args *a;
+    const float *q_rot;     /* [B][T][n_q][hd] normed + roped */
+} orc_gp_ctx;
+
+static void orc_gp_worker(void *arg, int tid, int n) {
+    const orc_gp_ctx *c = (const orc_gp_ctx *)arg;
+    const orc_gqa_prefill_args *a = c->a;
+    const int hd = a->hd;
+    const long long units = (long long)a->B * a->T * a->n_q;
+    float *sc = (float *)malloc(sizeof(float) * (size_t)a->L);
+    float *one = (float *)malloc(sizeof(float) * (size_t)a->n_q * hd);
+    for (long long u = tid; u < units; u += n) {
+        const int h = (int)(u % a->n_q);
+        const long long bt = u / a->n_q;
+        const int t = (int)(bt % a->T), b = (int)(bt / a->T);
+        const size_t kvs = (size_t)a->n_kv * hd;
+        orc_attend_args s = {a->n_q, a->n_kv, hd, a->pos0 + t + 1, 1, 0,
+                             c->q_rot + (size_t)bt * a->n_q * hd,
+                             a->k_cache + (size_t)b * a->L * kvs, a->v_cache + (size_t)b * a->L * kvs,
+                             kvs, (size_t)hd, kvs, (size_t)hd, one};
+        orc_attend_one(&s, h, sc);
+        const size_t o = ((size_t)bt * a->n_q + h) * hd;
+        for (int i = 0; i < hd; i++)
+            a->out[o + i] = one[(size_t)h * hd + i] * (1.0f / (1.0f + expf(-a->gate[o + i])));
+    }
+    free(sc);
+    free(one);
+}
+
+double orc_gqa_prefill(const orc_gqa_prefill_args *a) {
+    const double t0 = orc_now();
+    const int hd = a->hd, half = a->rope_dim / 2;
+    float *q_rot = (float *)malloc(sizeof(float) * (size_t)a->B * a->T * a->n_q * hd);
+    float cosv[128], sinv[128];
+    for (int b = 0; b < a->B; b++)
+        for (int t = 0; t < a->T; t++) {
+            const size_t bt = (size_t)b * a->T + t;
+            const int pos = a->pos0 + t;
+            if (half > 0) orc_rope_cos_sin(pos, cosv, sinv, a->rope_dim, a->rope_theta, a->rope_yarn);
+            float *qr = q_rot + bt * a->n_q * hd;
+            for (int h = 0; h < a->n_q; h++)
+                orc_rmsn_1pw(a->q + (bt * a->n_q + h) * hd, a->q_norm_w, qr + (size_t)h * hd, hd);
+            float *kc = a->k_cache + ((size_t)b * a->L + pos) * a->n_kv * hd;
+            float *vc = a->v_cache + ((size_t)b * a->L + pos) * a->n_kv * hd;
+            for (int h = 0; h < a->n_kv; h++)
+                orc_rmsn_1pw(a->k + (bt * a->n_kv + h) * hd, a->k_norm_w, kc + (size_t)h * hd, hd);
+            if (half > 0) {
+                orc_rope_apply(qr, a->n_q, hd, a->rope_dim, cosv, sinv);
+                orc_rope_apply(kc, a->n_kv, hd, a->rope_dim, cosv, sinv);
+            }
+            memcpy(vc, a->v + bt * a->n_kv * hd, sizeof(float) * (size_t)a->n_kv * hd);
+        }
+    orc_gp_ctx c = {a, q_rot};
+    orc_tp_run(a->threads, orc_gp_worker, &c);
+    free(q_rot);
+    return orc_now() - t0;
+}
+
 /* --------------------------------------------------------- matvec runs */
 typedef struct { const void *W; int w_bf16; const float *x; float *y; int rows, cols, B; } orc_mv_args;
 

@@ -192,6 +192,23 @@ typedef struct {
 } orc_attend_batch_args;
 double orc_attend_batch(const orc_attend_batch_args *a);
 
+/* GQA prefill of T tokens per sequence in the order of vx27_qlayer_batch
+ * (vx27_qfwd.c:314-376): for each token, rmsn(1+w) on q and k, RoPE at
+ * pos0+t (orc_rope_cos_sin), k,v appended to a float cache
+ * [B][L][n_kv][hd] (rows < pos0 supplied by the caller), then the token's
+ * attention over positions 0..pos0+t (double dot, float softmax) times
+ * sigmoid(gate).  The attention units (b, t, h) run in parallel. */
+typedef struct {
+    int B, T, n_q, n_kv, hd, rope_dim, pos0, L, threads;
+    float rope_theta, rope_yarn;
+    const float *q, *gate;          /* [B][T][n_q][hd] */
+    const float *k, *v;             /* [B][T][n_kv][hd] raw */
+    const float *q_norm_w, *k_norm_w;
+    float *k_cache, *v_cache;       /* [B][L][n_kv][hd] */
+    float *out;                     /* [B][T][n_q][hd] */
+} orc_gqa_prefill_args;
+double orc_gqa_prefill(const orc_gqa_prefill_args *a);
+
 /* Row-parallel matvec for B vectors (W bf16 widened), double serial sums. */
 double orc_matvec_batch(const void *W, int w_bf16, const float *x, float *y,
                         int rows, int cols, int B, int threads);

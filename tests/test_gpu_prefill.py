@@ -111,3 +111,92 @@ def test_dn_prefill_split_prompt(ctx):
     o2, S2 = run_dn_prefill(ctx, d, S=S1, t0=128, t1=384)
     assert np.array_equal(np.concatenate([o1, o2], axis=1), out)
     assert np.array_equal(S2, S)
+
+
+# ------------------------------------------------------------------ GQA
+def run_gqa_prefill(ctx, d, L, prior=None, interleave=False):
+    """Prefill the workload's T tokens at positions pos0.. into a fresh cache of
+    capacity L (rows < pos0 from `prior` = (k, v) fp32 [B][pos0][n_kv][256]);
+    returns out [B][T][n_q][256]."""
+    from vx27_amd import lib as L_
+    lib = L_.lib()
+    B, T, n_q, hd = d["q"].shape
+    n_kv = d["k"].shape[2]
+    pos0 = d["pos0"]
+    kc = ctx.buf(B * n_kv * L * hd * 2)
+    vc = ctx.buf(B * n_kv * L * hd * 2)
+    lib.vx27_hip_memset(ctx.h, kc.ptr, 0xFF, kc.nbytes)       # stale rows hold NaN bit patterns
+    lib.vx27_hip_memset(ctx.h, vc.ptr, 0xFF, vc.nbytes)
+    keep = []
+    if prior is not None:
+        for b in range(B):
+            kb, vb = ctx.put(np.ascontiguousarray(prior[0][b])), ctx.put(np.ascontiguousarray(prior[1][b]))
+            L_.check(lib.vx27_hip_kv_write(ctx.h, kc.ptr, vc.ptr, B, n_kv, hd, L, b, 0, pos0, kb.ptr, vb.ptr),
+                     "kv_write")
+            keep += [kb, vb]
+    if interleave:
+        qg = np.empty((B, T, n_q, 2, hd), np.uint16)
+        qg[:, :, :, 0], qg[:, :, :, 1] = d["q"], d["gate"]
+        qb = ctx.put(qg)
+        qp, gp, ts, hs = qb.ptr, qb.ptr + hd * 2, n_q * 2 * hd, 2 * hd
+    else:
+        qb, gb = ctx.put(d["q"]), ctx.put(d["gate"])
+        keep.append(gb)
+        qp, gp, ts, hs = qb.ptr, gb.ptr, 0, 0
+    kn, vn = ctx.put(d["k"]), ctx.put(d["v"])
+    qw, kw = ctx.put(d["q_norm_w"]), ctx.put(d["k_norm_w"])
+    ob = ctx.buf(B * T * n_q * hd * 4)
+    desc = L_.GqaPrefillDesc(B, T, n_q, n_kv, hd, 64, 1e7, 1.0, L, pos0, 0, qp, ts, hs, gp, ts, hs,
+                             kn.ptr, vn.ptr, qw.ptr, kw.ptr, kc.ptr, vc.ptr, ob.ptr)
+    L_.check(lib.vx27_hip_gqa_prefill(ctx.h, C.byref(desc)), "gqa_prefill")
+    out = ob.download((B, T, n_q, hd), np.float32)
+    for bb in keep + [qb, kn, vn, qw, kw, ob, kc, vc]:
+        bb.free()
+    return out
+
+
+def oracle_gqa_prefill(d, L, prior=None):
+    from oracle import oracle as O
+    from vx27_amd import workloads as W
+    B, T, n_q, hd = d["q"].shape
+    n_kv = d["k"].shape[2]
+    f = {k: np.ascontiguousarray(W.bf16_to_f32(d[k])) for k in ("q", "gate", "k", "v")}
+    qw, kw = np.ascontiguousarray(d["q_norm_w"]), np.ascontiguousarray(d["k_norm_w"])
+    kc = np.zeros((B, L, n_kv, hd), np.float32)
+    vc = np.zeros((B, L, n_kv, hd), np.float32)
+    if prior is not None:
+        kc[:, :d["pos0"]], vc[:, :d["pos0"]] = prior
+    out = np.empty((B, T, n_q, hd), np.float32)
+    a = O.GqaPrefillArgs(B, T, n_q, n_kv, hd, 64, d["pos0"], L, O.default_threads(), 1e7, 1.0,
+                         f["q"].ctypes.data, f["gate"].ctypes.data, f["k"].ctypes.data, f["v"].ctypes.data,
+                         qw.ctypes.data, kw.ctypes.data, kc.ctypes.data, vc.ctypes.data, out.ctypes.data)
+    secs = O.lib().orc_gqa_prefill(C.byref(a))
+    return out, secs
+
+
+def test_gqa_prefill_4096(ctx):
+    """One 4096-token prompt, 24Q/4KV hd 256 (the prefill workload)."""
+    from vx27_amd import workloads as W
+    d = W.gqa_prefill(B=1, T=4096)
+    say("gqa_prefill: B=1 T=4096")
+    out = run_gqa_prefill(ctx, d, 4096)
+    ref, secs = oracle_gqa_prefill(d, 4096)
+    say(f"  oracle {secs:.2f}s")
+    check_bf16(out, ref, "out")
+
+
+@pytest.mark.parametrize("B,T,pos0,L,inter", [(2, 200, 100, 320, False), (1, 130, 0, 192, True),
+                                              (3, 1, 63, 64, False), (1, 300, 37, 384, True)])
+def test_gqa_prefill_shapes(ctx, B, T, pos0, L, inter):
+    """Ragged T, an earlier context in the cache (pos0 > 0, unaligned), one
+    token, the interleaved q_proj layout, and stale NaN rows past the end."""
+    from vx27_amd import workloads as W
+    d = W.gqa_prefill(B=B, T=T, pos0=pos0, config=51)
+    say(f"gqa_prefill: B={B} T={T} pos0={pos0} L={L} interleaved={inter}")
+    prior = None
+    if pos0:
+        r = W.rng(52, "gqa_prefill_prior")
+        prior = tuple(W.bf16_to_f32(W.bf16_bits(W.normal(r, (B, pos0, 4, 256)))) for _ in range(2))
+    out = run_gqa_prefill(ctx, d, L, prior, inter)
+    ref, _ = oracle_gqa_prefill(d, L, prior)
+    check_bf16(out, ref, "out")

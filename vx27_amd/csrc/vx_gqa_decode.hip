@@ -29,26 +29,25 @@
 #include <math.h>
 
 #include "vx_gemv.h"
+#include "vx_gqa.h"
 
 namespace {
 
-constexpr int HDG = 256;      // head dim of the gated GQA layers
-constexpr int TILE = 32;      // keys per tile (V block size)
-constexpr int MAXR = 128;     // max rope_dim/2 carried in kernel arguments
+constexpr int HDG = VX_GQA_HD;
+constexpr int TILE = VX_GQA_VBLK;    // keys per tile (V block size)
+constexpr int MAXR = VX_ROPE_MAXH;
 
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
-struct RopeTab {
-    float freq[MAXR];
-};
+typedef vx_rope_tab RopeTab;
 
 __device__ __forceinline__ size_t k_index(int B_unused, int n_kv, int L, int b, int h, int p, int i) {
     (void)B_unused;
-    return (((size_t)b * n_kv + h) * L + p) * HDG + i;
+    return vx_k_index(n_kv, L, b, h, p, i);
 }
 __device__ __forceinline__ size_t v_index(int n_kv, int L, int b, int h, int p, int i) {
-    return ((((size_t)b * n_kv + h) * (L / TILE) + p / TILE) * HDG + i) * TILE + (p % TILE);
+    return vx_v_index(n_kv, L, b, h, p, i);
 }
 
 // Block-wide double sum over 256 threads (4 waves); contains barriers.
@@ -325,8 +324,10 @@ __global__ void rope_table_kernel(RopeTabArgs a) {
     a.sinv[(size_t)r * a.half + i] = sinf(ang);
 }
 
+}  // namespace
+
 // freq_i = powf(theta, -2i/rope_dim) on the host, as vx27_rope.c:11
-int fill_rope(RopeTab &t, int rope_dim, float theta) {
+int vx_rope_fill(vx_rope_tab &t, int rope_dim, float theta) {
     VX_REQUIRE(rope_dim >= 2 && rope_dim % 2 == 0 && rope_dim / 2 <= MAXR,
                "rope_dim must be even and <= %d (got %d)", 2 * MAXR, rope_dim);
     for (int i = 0; i < rope_dim / 2; i++) {
@@ -335,8 +336,6 @@ int fill_rope(RopeTab &t, int rope_dim, float theta) {
     }
     return 0;
 }
-
-}  // namespace
 
 static int gqa_check(const vx27_gqa_desc *d) {
     VX_REQUIRE(d != nullptr, "vx27_hip_gqa_decode: null descriptor");
@@ -374,7 +373,7 @@ size_t vx_gqa_scratch_bytes(const vx27_gqa_desc *d) {
 int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uint16_t *out_packed) {
     if (gqa_check(d)) return -1;
     RopeTab rt = {};
-    if (d->rope_dim > 0 && fill_rope(rt, d->rope_dim, d->rope_theta)) return -1;
+    if (d->rope_dim > 0 && vx_rope_fill(rt, d->rope_dim, d->rope_theta)) return -1;
     const float yarn = d->rope_yarn < 1.0f ? 1.0f : d->rope_yarn;
     const int qg = d->n_q / d->n_kv;
     const int n_split = gqa_n_split(d);
@@ -447,7 +446,7 @@ extern "C" int vx27_hip_rope_table(vx27_hip_ctx *ctx, const int *pos, int n, int
     if (vx_ctx_enter(ctx)) return -1;
     VX_REQUIRE(pos && cosv && sinv && n >= 0, "vx27_hip_rope_table: bad arguments");
     RopeTab rt = {};
-    if (fill_rope(rt, rope_dim, theta)) return -1;
+    if (vx_rope_fill(rt, rope_dim, theta)) return -1;
     if (n == 0) return 0;
     RopeTabArgs a = {pos, n, rope_dim / 2, yarn < 1.0f ? 1.0f : yarn, cosv, sinv, rt};
     VX_LAUNCH(ctx, rope_table_kernel, dim3(n), dim3(MAXR), a);

@@ -15,9 +15,8 @@
 
 #include "vx_dn.h"
 #include "vx_gemv.h"
+#include "vx_gqa.h"
 
-size_t vx_gqa_scratch_bytes(const vx27_gqa_desc *d);
-int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uint16_t *out_packed);
 
 namespace {
 

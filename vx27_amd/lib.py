@@ -34,6 +34,16 @@ class DnPrefillDesc(C.Structure):
                 ("A_log", VP), ("dt_bias", VP), ("out", VP)]
 
 
+class GqaPrefillDesc(C.Structure):
+    _fields_ = [("B", C.c_int), ("T", C.c_int), ("n_q", C.c_int), ("n_kv", C.c_int), ("hd", C.c_int),
+                ("rope_dim", C.c_int), ("rope_theta", C.c_float), ("rope_yarn", C.c_float),
+                ("L", C.c_int), ("pos0", C.c_int), ("flags", C.c_uint),
+                ("q", VP), ("q_tok_stride", C.c_size_t), ("q_head_stride", C.c_size_t),
+                ("gate", VP), ("gate_tok_stride", C.c_size_t), ("gate_head_stride", C.c_size_t),
+                ("k_new", VP), ("v_new", VP), ("q_norm_w", VP), ("k_norm_w", VP),
+                ("k_cache", VP), ("v_cache", VP), ("out", VP)]
+
+
 class GqaDesc(C.Structure):
     _fields_ = [("B", C.c_int), ("n_q", C.c_int), ("n_kv", C.c_int), ("hd", C.c_int),
                 ("rope_dim", C.c_int), ("rope_theta", C.c_float), ("rope_yarn", C.c_float),
@@ -84,6 +94,7 @@ _SIGS = {
     "vx27_hip_memset": (C.c_int, [VP, VP, C.c_int, C.c_size_t]),
     "vx27_hip_dn_decode": (C.c_int, [VP, C.POINTER(DnDesc)]),
     "vx27_hip_dn_prefill": (C.c_int, [VP, C.POINTER(DnPrefillDesc)]),
+    "vx27_hip_gqa_prefill": (C.c_int, [VP, C.POINTER(GqaPrefillDesc)]),
     "vx27_hip_gqa_decode": (C.c_int, [VP, C.POINTER(GqaDesc)]),
     "vx27_hip_kv_write": (C.c_int, [VP, VP, VP] + [C.c_int] * 7 + [VP, VP]),
     "vx27_hip_kv_read": (C.c_int, [VP, VP, VP] + [C.c_int] * 7 + [VP, VP]),

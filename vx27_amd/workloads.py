@@ -112,6 +112,17 @@ def dn_prefill(B=1, T=4096, nqk=16, nv=16, hd=128, config=4, S0_std=0.0):
     return d
 
 
+def gqa_prefill(B=1, T=4096, n_q=24, n_kv=4, hd=256, pos0=0, config=5):
+    """Config: one prompt of T tokens, bf16 ~N(0,1) raw q [B][T][24][256],
+    gate logits [B][T][24][256], raw k, v [B][T][4][256]; q/k norm weights w
+    with (1+w) ~ 1+N(0,0.1); RoPE at positions pos0..pos0+T-1; causal."""
+    r = rng(config, "gqa_prefill")
+    d = {"q": bf16_bits(normal(r, (B, T, n_q, hd))), "gate": bf16_bits(normal(r, (B, T, n_q, hd))),
+         "k": bf16_bits(normal(r, (B, T, n_kv, hd))), "v": bf16_bits(normal(r, (B, T, n_kv, hd))),
+         "q_norm_w": normal(r, hd, 0.1), "k_norm_w": normal(r, hd, 0.1), "pos0": pos0}
+    return d
+
+
 def gqa_decode(B=1, L=8192, n_q=24, n_kv=4, hd=256, config=2):
     """Config: bf16 KV cache of L positions with K,V ~N(0,1) (taken as already
     normed and roped), new token at position L; raw q ~N(0,1) and gate logits
