@@ -29,8 +29,9 @@ Workloads (synthetic, seeded, random-init):
             64 sequences x 16 heads x 128x128 fp32 state, 6144 conv channels
             (bf16 weights), l2norm q/k, exact delta rule; 256 steps
 Extras (without --no-extra): dn_conv, gated GQA decode at 8192 positions
-(batch 1 and 32), and the DeltaNet recurrence alone (1 sequence x 16 heads,
-2000 steps).
+(batch 1 and 32), the two prefills of a 4096-token prompt (chunked DeltaNet,
+16 heads; causal gated GQA, 24Q/4KV hd 256) against the bf16 MFMA peak, and
+the DeltaNet recurrence alone (1 sequence x 16 heads, 2000 steps).
 """
 from __future__ import annotations
 
@@ -373,6 +374,106 @@ def bench_gqa(ctx, B, Lctx=8192, iters=20):
             "alg_bytes": alg, "achieved_GBs": alg / avg_s / 1e9}
 
 
+# ---------------------------------------------------------------- prefill
+MFMA_BF16_PEAK = 2.5e15     # flop/s, MI355X dense bf16
+
+
+def _time_calls(ctx, fn, kernels, iters):
+    """Run fn() iters times with the profiler on; wall time per call and the
+    summed kernel time per call (HIP events on the library stream)."""
+    ctx.sync()
+    ctx.prof_enable(True)
+    t0 = time.perf_counter()
+    for _ in range(iters):
+        fn()
+    ctx.sync()
+    wall = (time.perf_counter() - t0) / iters
+    per = {k: ctx.prof_read(k)[1] / iters * 1e3 for k in kernels}
+    ctx.prof_enable(False)
+    return wall * 1e6, per
+
+
+def bench_dn_prefill(ctx, T=4096, iters=20, cpu=True):
+    """Chunked Gated DeltaNet prefill: one T-token prompt, 16 heads of 128."""
+    from vx27_amd import lib as L, workloads as W
+    d = W.dn_prefill(B=1, T=T)
+    H, hd, C_ = 16, 128, 64
+    bufs = {k: ctx.put(d[k]) for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "S0")}
+    ob = ctx.buf(T * H * hd * 4)
+    desc = L.DnPrefillDesc(1, T, H, H, hd, 0, bufs["S0"].ptr, bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr,
+                           bufs["a"].ptr, bufs["b"].ptr, bufs["A_log"].ptr, bufs["dt_bias"].ptr, ob.ptr)
+
+    def run():
+        L.check(L.lib().vx27_hip_dn_prefill(ctx.h, C.byref(desc)), "dn_prefill")
+    for _ in range(3):
+        run()
+    wall_us, per = _time_calls(ctx, run, ("dnp_prep", "dnp_scan"), iters)
+    k_us = sum(per.values())
+    flops = H * (T // C_) * (10 * C_ * C_ * hd + 6 * C_ * hd * hd + 2 * C_ ** 3 / 3)
+    nbytes = T * H * hd * 2 * 3 + T * H * 8 + T * H * hd * 4 + 2 * H * hd * hd * 4
+    res = {"workload": f"dn_prefill B=1 T={T} heads=16 chunk=64", "us_per_call": wall_us,
+           "kernel_us": k_us, "kernels_us": per, "tokens_per_s": T / (k_us / 1e6),
+           "alg_flops": flops, "mfma_frac": flops / (k_us / 1e6) / MFMA_BF16_PEAK,
+           "alg_bytes": nbytes, "hbm_frac": nbytes / (k_us / 1e6) / HBM_PEAK}
+    if cpu:
+        from gpu_common import oracle_dn
+        seq = {k: np.ascontiguousarray(np.swapaxes(W.bf16_to_f32(d[k]), 0, 1)) for k in ("q", "k", "v")}
+        seq.update({k: np.ascontiguousarray(np.swapaxes(d[k], 0, 1)) for k in ("a", "b")})
+        seq.update(A_log=d["A_log"], dt_bias=d["dt_bias"], S0=d["S0"])
+        from oracle import oracle as O
+        _, _, _, secs = oracle_dn(seq, 0, 1, H, H, T)
+        res["cpu"] = {"value": T / secs, "unit": "tokens/s", "cores": min(H, O.default_threads()),
+                      "kind": "port", "sample": f"oracle sequential step_exact, {T} tokens x 16 heads"}
+    for b in bufs.values():
+        b.free()
+    ob.free()
+    return res
+
+
+def bench_gqa_prefill(ctx, T=4096, iters=10, cpu=True):
+    """Causal gated GQA prefill: one T-token prompt, 24Q/4KV hd 256."""
+    from vx27_amd import lib as L, workloads as W
+    d = W.gqa_prefill(B=1, T=T)
+    n_q, n_kv, hd = 24, 4, 256
+    Lc = (T + 63) // 64 * 64
+    kc, vc = ctx.buf(n_kv * Lc * hd * 2), ctx.buf(n_kv * Lc * hd * 2)
+    bufs = {k: ctx.put(d[k]) for k in ("q", "gate", "k", "v", "q_norm_w", "k_norm_w")}
+    ob = ctx.buf(T * n_q * hd * 4)
+    desc = L.GqaPrefillDesc(1, T, n_q, n_kv, hd, 64, 1e7, 1.0, Lc, 0, 0, bufs["q"].ptr, 0, 0,
+                            bufs["gate"].ptr, 0, 0, bufs["k"].ptr, bufs["v"].ptr, bufs["q_norm_w"].ptr,
+                            bufs["k_norm_w"].ptr, kc.ptr, vc.ptr, ob.ptr)
+
+    def run():
+        L.check(L.lib().vx27_hip_gqa_prefill(ctx.h, C.byref(desc)), "gqa_prefill")
+    for _ in range(3):
+        run()
+    wall_us, per = _time_calls(ctx, run, ("gqp_prep", "gqp_attn"), iters)
+    k_us = sum(per.values())
+    flops = 2 * hd * n_q * T * (T + 1)
+    res = {"workload": f"gqa_prefill B=1 T={T} 24Q/4KV hd256 causal", "us_per_call": wall_us,
+           "kernel_us": k_us, "kernels_us": per, "tokens_per_s": T / (k_us / 1e6),
+           "alg_flops": flops, "mfma_frac": flops / (k_us / 1e6) / MFMA_BF16_PEAK,
+           "attn_mfma_frac": flops / (per["gqp_attn"] / 1e6) / MFMA_BF16_PEAK}
+    if cpu:
+        # oracle on the first 1024 query rows (causal work 1/16 of the prompt's), scaled
+        from oracle import oracle as O
+        Ts = 1024
+        f = {k: np.ascontiguousarray(W.bf16_to_f32(d[k][:, :Ts])) for k in ("q", "gate", "k", "v")}
+        kco = np.zeros((1, Ts, n_kv, hd), np.float32); vco = np.zeros_like(kco)
+        out = np.empty((1, Ts, n_q, hd), np.float32)
+        qw, kw = np.ascontiguousarray(d["q_norm_w"]), np.ascontiguousarray(d["k_norm_w"])
+        a = O.GqaPrefillArgs(1, Ts, n_q, n_kv, hd, 64, 0, Ts, O.default_threads(), 1e7, 1.0,
+                             f["q"].ctypes.data, f["gate"].ctypes.data, f["k"].ctypes.data, f["v"].ctypes.data,
+                             qw.ctypes.data, kw.ctypes.data, kco.ctypes.data, vco.ctypes.data, out.ctypes.data)
+        secs = O.lib().orc_gqa_prefill(C.byref(a)) * (T * (T + 1)) / (Ts * (Ts + 1))
+        res["cpu"] = {"value": T / secs, "unit": "tokens/s", "cores": O.default_threads(), "kind": "port",
+                      "sample": f"oracle prefill of the first {Ts} tokens, time scaled by the causal "
+                                f"work ratio {T * (T + 1) / (Ts * (Ts + 1)):.1f}"}
+    for b in list(bufs.values()) + [kc, vc, ob]:
+        b.free()
+    return res
+
+
 # ------------------------------------------------------------------- main
 def main():
     ap = argparse.ArgumentParser()
@@ -428,6 +529,15 @@ def main():
             extra[f"gqa8k_B{B}"] = r
             log(f"  gqa B={B}: {r['us_per_step']:.1f} us/step, split kernel {r['kernel_us']:.1f} us, "
                 f"{r['achieved_GBs']:.0f} GB/s")
+        r = bench_dn_prefill(ctx, cpu=not args.no_cpu)
+        extra["dn_prefill_T4096"] = r
+        log(f"  dn_prefill: {r['kernel_us']:.1f} us ({r['tokens_per_s']:.3g} tok/s), "
+            f"MFMA {100 * r['mfma_frac']:.1f}%, HBM {100 * r['hbm_frac']:.1f}%  {r['kernels_us']}")
+        r = bench_gqa_prefill(ctx, cpu=not args.no_cpu)
+        extra["gqa_prefill_T4096"] = r
+        log(f"  gqa_prefill: {r['kernel_us']:.1f} us ({r['tokens_per_s']:.3g} tok/s), "
+            f"MFMA {100 * r['mfma_frac']:.1f}% (attention kernel {100 * r['attn_mfma_frac']:.1f}%)  "
+            f"{r['kernels_us']}")
         r = bench_dn_recurrent(ctx)
         extra["dn_recurrent"] = r
         log(f"  dn_recurrent: {r['us_per_step_multistep_call']:.2f} us/step (one call), "

@@ -11,7 +11,7 @@
  * restates.  Build with -std=c11 -ffp-contract=off (no FMA contraction),
  * exactly as the reference's own -std=c11 build evaluates.
  *
- * Pinning status (how each function is checked, in tests/test_oracle_*.py):
+ * Pinning status (how each function is checked, in tests/test_oracle.py):
  *   orc_gate_params, orc_l2norm, orc_step_exact, orc_conv1d_step,
  *   orc_update_simple / orc_retrieve_simple, orc_rmsnorm_w, orc_attn_1q,
  *   orc_rope_cos_sin, orc_rope_apply                -> golden vectors minted
@@ -20,10 +20,11 @@
  *   orc_dn_layer_token, orc_gqa_layer_token (the vx27_qlayer glue)
  *     -> golden vectors minted from the compiled reference vx27_qlayer with
  *        synthetic F32 weights and a zero FFN.
- *   orc_attend (bf16 KV, long context, batches) and orc_dn_prefill_seq
- *     (sequential prefill) are compositions of the pinned functions; they are
- *     additionally checked against closed forms (one key -> its value,
- *     identical keys -> mean of values, chunk-invariance).
+ *   orc_attend (bf16 KV, long context, batches) -> orc_gqa_token (pinned
+ *     above) + closed forms (one key -> its value, identical keys -> mean).
+ *   orc_dn_run (multi-token, batched; the DeltaNet prefill oracle) and
+ *   orc_gqa_prefill (token-ordered GQA prefill) -> bit-exact against chains
+ *     of the pinned per-token functions.
  */
 #ifndef VX27_ORACLE_H
 #define VX27_ORACLE_H

@@ -317,3 +317,62 @@ def test_live_vs_reference(O):
         c2 = np.empty(32, np.float32); s2 = np.empty(32, np.float32)
         R.vx27_rope_cos_sin(p, c2, s2, 64, 1e7, 1.0)
         assert np.array_equal(c1, c2) and np.array_equal(s1, s2), p
+
+
+# ------------------------------ compositions used as multi-token oracles
+def test_dn_run_equals_chained_steps(O):
+    """orc_dn_run (the batched / multi-token driver, also the DeltaNet prefill
+    oracle) equals chained orc_step_exact + orc_gate_params calls bit for bit,
+    including the QK-head sharing vh*nqk/nv (vx27_qfwd.c:136-137)."""
+    r = I.rng("dn_run_chain")
+    B, nqk, nv, hd, T = 2, 2, 4, 128, 5
+    q, k = I.normal(r, (T, B, nqk, hd)), I.normal(r, (T, B, nqk, hd))
+    v = I.normal(r, (T, B, nv, hd))
+    a, b = I.normal(r, (T, B, nv)), I.normal(r, (T, B, nv))
+    A_log, dt = f32(r.uniform(-2, 1, nv)), I.normal(r, nv, 0.1)
+    S0 = I.normal(r, (B, nv, hd, hd), 0.05)
+    S = S0.copy()
+    out = np.empty((T, B, nv, hd), np.float32)
+    args = O.DnRunArgs(B, nqk, nv, hd, T, 0, 3, S.ctypes.data, None, None, None, q.ctypes.data,
+                       k.ctypes.data, v.ctypes.data, a.ctypes.data, b.ctypes.data, A_log.ctypes.data,
+                       dt.ctypes.data, None, None, out.ctypes.data)
+    O.lib().orc_dn_run(C.byref(args))
+    Sr = S0.copy()
+    for t in range(T):
+        for bb in range(B):
+            for vh in range(nv):
+                g = vh * nqk // nv
+                beta, glog = O.gate_params(a[t, bb, vh], A_log[vh], b[t, bb, vh], dt[vh])
+                o = O.step_exact(Sr[bb, vh], q[t, bb, g], k[t, bb, g], v[t, bb, vh], beta, glog)
+                assert np.array_equal(o, out[t, bb, vh]), (t, bb, vh)
+    assert np.array_equal(S, Sr)
+
+
+def test_gqa_prefill_equals_token_chain(O):
+    """orc_gqa_prefill (the GQA prefill oracle, parallel over tokens and heads)
+    equals orc_gqa_token applied token by token (pinned to vx27_qlayer)
+    bit for bit, with an earlier context in the cache."""
+    r = I.rng("gqa_prefill_chain")
+    n_q, n_kv, hd, T, pos0, L = 24, 4, 256, 4, 3, 8
+    q, gate = I.normal(r, (1, T, n_q, hd)), I.normal(r, (1, T, n_q, hd))
+    k, v = I.normal(r, (1, T, n_kv, hd)), I.normal(r, (1, T, n_kv, hd))
+    qw, kw = I.normal(r, hd, 0.1), I.normal(r, hd, 0.1)
+    kc0 = np.zeros((1, L, n_kv, hd), np.float32); vc0 = np.zeros_like(kc0)
+    kc0[0, :pos0], vc0[0, :pos0] = I.normal(r, (pos0, n_kv, hd)), I.normal(r, (pos0, n_kv, hd))
+    kc, vc = kc0.copy(), vc0.copy()
+    out = np.empty((1, T, n_q, hd), np.float32)
+    a = O.GqaPrefillArgs(1, T, n_q, n_kv, hd, 64, pos0, L, 3, 1e7, 1.0, q.ctypes.data, gate.ctypes.data,
+                         k.ctypes.data, v.ctypes.data, qw.ctypes.data, kw.ctypes.data, kc.ctypes.data,
+                         vc.ctypes.data, out.ctypes.data)
+    O.lib().orc_gqa_prefill(C.byref(a))
+    kr, vr = kc0.copy(), vc0.copy()
+    cfg = O.GqaCfg(n_q, n_kv, hd, 64, 0, qw.ctypes.data, kw.ctypes.data, kr.ctypes.data, vr.ctypes.data,
+                   n_kv * hd, hd, n_kv * hd, hd)
+    for t in range(T):
+        c, s = O.rope_cos_sin(pos0 + t)
+        o = np.empty((n_q, hd), np.float32)
+        gt = f32(gate[0, t])
+        O.lib().orc_gqa_token(C.byref(cfg), f32(q[0, t]), hd, gt.ctypes.data, hd, f32(k[0, t]), f32(v[0, t]),
+                              pos0 + t, c, s, o)
+        assert np.array_equal(o, out[0, t]), t
+    assert np.array_equal(kc, kr) and np.array_equal(vc, vr)
