@@ -7,6 +7,9 @@ hipcc compiles every csrc/*.hip for --offload-arch=gfx950 with:
                                       kernels reproduce the reference's
                                       separate multiply/add roundings
   -target-feature -packed-fp32-ops    no packed FP32 instructions
+and, for the MFMA prefill kernels (FILE_FLAGS), -amdgpu-mfma-vgpr-form: their
+accumulators stay in arch VGPRs, where the online-softmax and state updates
+touch them with VALU ops, instead of being copied in and out of AGPRs.
 gcc compiles the C drop-in layer (-std=c11) against include/vx27_hip.h.
 Objects go to vx27_amd/_build/, the library to vx27_amd/libvx27_hip.so.
 """
@@ -31,6 +34,10 @@ HIPCC = os.environ.get("HIPCC", shutil.which("hipcc") or "/opt/rocm/bin/hipcc")
 HIP_FLAGS = ["-O3", f"--offload-arch={ARCH}", "-fPIC", "-std=c++17", "-ffp-contract=off",
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wno-unused-result", f"-I{INC}", f"-I{CSRC}"]
+FILE_FLAGS = {
+    "vx_gqa_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "vx_dn_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+}
 CC = os.environ.get("CC", "gcc")
 C_FLAGS = ["-std=c11", "-O2", "-fPIC", "-ffp-contract=off", "-Wall", f"-I{INC}"]
 
@@ -51,7 +58,7 @@ def build(verbose: bool = True, jobs: int = 8) -> str:
     jobs_list = []
     for src in hips:
         obj = os.path.join(BUILD, os.path.basename(src) + ".o")
-        jobs_list.append([HIPCC, *HIP_FLAGS, "-c", src, "-o", obj])
+        jobs_list.append([HIPCC, *HIP_FLAGS, *FILE_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj])
     for src in cs:
         obj = os.path.join(BUILD, os.path.basename(src) + ".o")
         jobs_list.append([CC, *C_FLAGS, "-c", src, "-o", obj])

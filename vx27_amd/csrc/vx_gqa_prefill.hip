@@ -34,8 +34,6 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 constexpr int HDG = VX_GQA_HD;
 constexpr int QT = 128;     // queries per workgroup
 constexpr int KT = 64;      // keys per tile
-constexpr int KROW = HDG + 8;   // padded LDS row of the K tile (bf16)
-constexpr int VROW = KT + 8;    // padded LDS row of the dim-major V tile (bf16)
 
 struct PrepArgs {
     int T, n_q, n_kv, rope_dim, L, pos0;
@@ -83,7 +81,8 @@ __global__ __launch_bounds__(256) void gqp_prep(PrepArgs a) {
     else if (i < 2 * half)
         r = row[i - half] * sn[i - half] + row[i] * cs[i - half];
     if (is_q) {
-        a.q_rot[(((size_t)b * a.n_q + h) * a.T + t) * HDG + i] = vx_f32_to_bf16(r);
+        // scores leave the MFMA in the exp2 domain: q * log2(e) / sqrt(256)
+        a.q_rot[(((size_t)b * a.n_q + h) * a.T + t) * HDG + i] = vx_f32_to_bf16(r * (1.4426950408889634f / 16.0f));
     } else {
         a.k_cache[vx_k_index(a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(r);
         a.v_cache[vx_v_index(a.n_kv, a.L, b, hk, pos, i)] = a.v[tok * a.kv_ts + (size_t)hk * HDG + i];
@@ -91,9 +90,8 @@ __global__ __launch_bounds__(256) void gqp_prep(PrepArgs a) {
 }
 
 struct AttnArgs {
-    int T, n_q, n_kv, L, pos0;
-    float scale_log2;             // log2(e) / sqrt(256)
-    const uint16_t *q_rot;        // [B][n_q][T][256]
+    int T, n_q, n_kv, L, pos0, xcd_map;
+    const uint16_t *q_rot;        // [B][n_q][T][256], pre-scaled by log2(e)/sqrt(256)
     const uint16_t *k_cache, *v_cache;
     const uint16_t *gate;
     size_t g_ts, g_hs;
@@ -105,29 +103,130 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) {
     __builtin_memcpy(&r, &u, 16);
     return r;
 }
+// hardware round-to-nearest-even pack (v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack2(float x, float y) {
-    return (uint32_t)vx_f32_to_bf16(x) | ((uint32_t)vx_f32_to_bf16(y) << 16);
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = (bf16x2_t){(__bf16)x, (__bf16)y};
+    return __builtin_bit_cast(uint32_t, v);
 }
 
-// grid (ceil(T/128), n_q, B), block 256
+
+// LDS tile buffer: K [64 keys][256 dims] then V [256 dims][64 keys], bf16,
+// 16-byte units XOR-swizzled so the MFMA operand reads are conflict-free:
+//   K unit u of key r at r*32 + (u ^ (r & 15))
+//   V unit u (8 keys) of dim d at d*8 + (u ^ ((d >> 1) & 7))
+constexpr int KBUF = KT * HDG * 2;          // bytes of the K part
+constexpr int TBUF = 2 * KBUF;              // bytes of one K+V tile buffer
+
+// Direct-to-LDS loads of one 64-key tile, K and V separately: 4 waves x 8
+// instructions of 64 lanes x 16 bytes each; every lane loads the global unit
+// that belongs at its swizzled LDS slot.
+// One 16-byte-per-lane load from global memory straight into LDS
+// (global_load_lds_dwordx4: lane L's 16 bytes land at lds + 16 L).  Issued
+// from inline asm so that the compiler does not track it: its own waits for
+// LDS DMA would drain the prefetch in flight before every LDS read.  The
+// kernels order it themselves with explicit vmcnt waits before the barriers
+// that publish a tile.  M0 (the LDS base) is saved and restored around it,
+// with the one wait state that an M0 write needs before the load.
+__device__ __forceinline__ void dma16(const void *base, uint32_t off, uint32_t lds) {
+    uint32_t saved;
+    __asm__ volatile(
+        "s_mov_b32 %0, m0\n\t"
+        "s_mov_b32 m0, %3\n\t"
+        "s_nop 0\n\t"
+        "global_load_lds_dwordx4 %1, %2\n\t"
+        "s_mov_b32 m0, %0"
+        : "=&s"(saved)
+        : "v"(off), "s"(base), "s"(lds)
+        : "memory");
+}
+__device__ __forceinline__ uint32_t lds_addr(const void *p) {
+    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
+}
+
+// Loads of one 64-key tile, K and V separately: 4 waves x 8 instructions of
+// 64 lanes x 16 bytes each; every lane loads the global unit that belongs at
+// its swizzled LDS slot.  The lane offsets are recomputed at each call (the
+// empty asm hides that they are loop-invariant, so they are not held in
+// registers across the tile loop).
+__device__ __forceinline__ void load_k(uint32_t kbuf, const char *Kt, int wave, int lane) {
+    __asm__ volatile("" : "+v"(lane));
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int r = (wave * 8 + j) * 2 + (lane >> 5), u = (lane & 31) ^ (r & 15);
+        dma16(Kt, (uint32_t)(r * HDG + u * 8) * 2, kbuf + (wave * 8 + j) * 1024);
+    }
+}
+__device__ __forceinline__ void load_v(uint32_t vbuf, const char *Vt, int wave, int lane) {
+    __asm__ volatile("" : "+v"(lane));
+#pragma unroll
+    for (int j = 0; j < 8; j++) {
+        const int d = (wave * 8 + j) * 8 + (lane >> 3), w = (lane & 7) ^ ((d >> 1) & 7);
+        dma16(Vt, (uint32_t)((((w >> 2) * HDG + d) * 32) + (w & 3) * 8) * 2, vbuf + (wave * 8 + j) * 1024);
+    }
+}
+
+// The workgroup's 128 query rows (row-major, same swizzle as K), once per
+// workgroup: 4 waves x 16 instructions; rows past T repeat row T-1.
+__device__ __forceinline__ void load_q(uint32_t qbuf, const uint16_t *Qh, int qrow0, int T, int wave, int lane) {
+#pragma unroll
+    for (int j = 0; j < 16; j++) {
+        const int r = (wave * 16 + j) * 2 + (lane >> 5), u = (lane & 31) ^ (r & 15);
+        const int t = min(qrow0 + r, T - 1);
+        dma16(Qh, (uint32_t)(t * HDG + u * 8) * 2, qbuf + (wave * 16 + j) * 1024);
+    }
+}
+
+// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
+// operations, not for its outstanding global loads (__syncthreads would also
+// drain the direct-to-LDS prefetch in flight; each wave waits for its own
+// tile loads with an explicit vmcnt before the barrier that publishes them).
+__device__ __forceinline__ void lds_barrier() {
+    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+    __builtin_amdgcn_s_barrier();
+    __asm__ volatile("" ::: "memory");
+}
+
+// grid (ceil(T/128) * n_q, B), block 256
 __global__ __launch_bounds__(256) void gqp_attn(AttnArgs a) {
-    const int qt = gridDim.x - 1 - blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+    // Workgroups go round-robin over the 8 XCDs (each with its own L2).  With
+    // xcd_map, XCD x takes the query heads of KV head x / (8 / n_kv), so an
+    // L2 holds one KV head's cache; heaviest (last) query tiles first.
+    const int n_qt = gridDim.x / a.n_q, b = blockIdx.y;
+    int qt, h;
+    if (a.xcd_map) {
+        const int id = blockIdx.x, xcd = id & 7, slot = id >> 3;
+        const int xpk = 8 / a.n_kv, hpx = a.n_q / 8;   // XCDs per KV head, Q heads per XCD
+        qt = n_qt - 1 - slot / hpx;
+        h = (xcd / xpk) * (a.n_q / a.n_kv) + (xcd % xpk) * hpx + slot % hpx;
+    } else {
+        qt = n_qt - 1 - (int)blockIdx.x / a.n_q;
+        h = blockIdx.x % a.n_q;
+    }
     const int kvh = h / (a.n_q / a.n_kv);
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: LDS bases go to M0
     const int r0 = qt * QT + wave * 32;                 // this wave's first query (token index)
 
-    __shared__ uint16_t K_l[KT][KROW];
-    __shared__ uint16_t V_l[HDG][VROW];
+    // K and V tiles as distinct LDS objects: the next K streams in while this
+    // tile's V is read, and the next V while the next K is read, and the
+    // compiler can see that these do not alias
+    __shared__ __attribute__((aligned(16))) char Kl[KBUF];
+    __shared__ __attribute__((aligned(16))) char Vl[KBUF];
+    __shared__ __attribute__((aligned(16))) char Ql[QT * HDG * 2];   // this workgroup's queries
 
-    // Q^T operands of the two 16-query blocks (rows past T clamped; never stored)
-    bf16x8_t qb[2][8];
-#pragma unroll
-    for (int rb = 0; rb < 2; rb++) {
-        const int t = min(r0 + rb * 16 + n, a.T - 1);
-        const uint16_t *qp = a.q_rot + (((size_t)b * a.n_q + h) * a.T + t) * HDG + 8 * g;
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) qb[rb][ks] = as_bf16x8(*(const uint4 *)(qp + 32 * ks));
-    }
+    const int n_keys = a.pos0 + a.T;                           // valid cache positions
+    const int wg_last = a.pos0 + min(qt * QT + QT, a.T) - 1;   // last key any row here sees
+    const int n_tiles = wg_last / KT + 1;
+    const int wave_last = a.pos0 + min(r0 + 31, a.T - 1);
+    // tile kt: K rows kt*64.. (32 KiB) and V blocks 2kt, 2kt+1 (2 x 16 KiB)
+    const char *Kc = (const char *)(a.k_cache + vx_k_index(a.n_kv, a.L, b, kvh, 0, 0));
+    const char *Vc = (const char *)(a.v_cache + vx_v_index(a.n_kv, a.L, b, kvh, 0, 0));
+    const uint32_t kl = lds_addr(Kl), vl = lds_addr(Vl);
+    load_q(lds_addr(Ql), a.q_rot + ((size_t)b * a.n_q + h) * a.T * HDG, qt * QT, a.T, wave, lane);
+    load_k(kl, Kc, wave, lane);
+    load_v(vl, Vc, wave, lane);
+
     floatx4_t O[2][16];
 #pragma unroll
     for (int rb = 0; rb < 2; rb++)
@@ -135,118 +234,145 @@ __global__ __launch_bounds__(256) void gqp_attn(AttnArgs a) {
         for (int db = 0; db < 16; db++) O[rb][db] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
     float mrow[2] = {-INFINITY, -INFINITY}, lrow[2] = {0.f, 0.f};
 
-    const int n_keys = a.pos0 + a.T;                           // valid cache positions
-    const int wg_last = a.pos0 + min(qt * QT + QT, a.T) - 1;   // last key any row here sees
-    const int n_tiles = wg_last / KT + 1;
-    const int wave_last = a.pos0 + min(r0 + 31, a.T - 1);
-    const uint16_t *Kc = a.k_cache + vx_k_index(a.n_kv, a.L, b, kvh, 0, 0);
-    const uint16_t *Vc = a.v_cache + vx_v_index(a.n_kv, a.L, b, kvh, 0, 0);
-
     for (int kt = 0; kt < n_tiles; kt++) {
         const int k0 = kt * KT;
-        __syncthreads();   // the previous tile's readers are done
-        // stage K rows k0..k0+63 and the two dim-major V blocks; V of
-        // positions past the valid keys is zeroed (masked P is 0, and 0 * a
-        // stale NaN would not be)
-#pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const int idx = it * 256 + tid;
-            const int kr = idx >> 5, c16 = idx & 31;
-            *(uint4 *)&K_l[kr][c16 * 8] = *(const uint4 *)(Kc + (size_t)(k0 + kr) * HDG + c16 * 8);
-        }
-#pragma unroll
-        for (int it = 0; it < 8; it++) {
-            const int idx = it * 256 + tid;
-            const int blk = idx >> 10, w = idx & 1023, dim = w >> 2, c = w & 3;
-            const int p = k0 + blk * 32 + c * 8;
-            uint4 v = *(const uint4 *)(Vc + ((size_t)(k0 / 32 + blk) * HDG + dim) * 32 + c * 8);
-            if (p + 8 > n_keys) {
-                uint16_t *e = (uint16_t *)&v;
-#pragma unroll
-                for (int j = 0; j < 8; j++)
-                    if (p + j >= n_keys) e[j] = 0;
-            }
-            *(uint4 *)&V_l[dim][blk * 32 + c * 8] = v;
-        }
-        __syncthreads();
-        if (k0 > wave_last) continue;   // wave-uniform: every key here is masked for this wave
-
+        const bool more = kt + 1 < n_tiles;
+        const bool live = k0 <= wave_last;   // wave-uniform: otherwise every key here is masked
+        // K(kt) (and Q) landed; V(kt), issued after it, may still be in flight
+        __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        lds_barrier();
         floatx4_t s[4][2];
 #pragma unroll
         for (int kb = 0; kb < 4; kb++)
 #pragma unroll
             for (int rb = 0; rb < 2; rb++) s[kb][rb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+        if (live) {
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-#pragma unroll
-            for (int kb = 0; kb < 4; kb++) {
-                const bf16x8_t ka = as_bf16x8(*(const uint4 *)&K_l[kb * 16 + n][32 * ks + 8 * g]);
+            for (int ks = 0; ks < 8; ks++) {
+                const int uo = ((4 * ks + g) ^ n) << 4;   // swizzled unit of rows = n (mod 16)
+                bf16x8_t qv[2];
 #pragma unroll
                 for (int rb = 0; rb < 2; rb++)
-                    s[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qb[rb][ks], s[kb][rb], 0, 0, 0);
+                    qv[rb] = as_bf16x8(*(const uint4 *)(Ql + (wave * 32 + rb * 16 + n) * 512 + uo));
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++) {
+                    const bf16x8_t ka = as_bf16x8(*(const uint4 *)(Kl + (kb * 16 + n) * 512 + uo));
+#pragma unroll
+                    for (int rb = 0; rb < 2; rb++)
+                        s[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qv[rb], s[kb][rb], 0, 0, 0);
+                }
             }
         }
-        const bool need_mask = k0 + KT - 1 > a.pos0 + r0;
+        lds_barrier();   // every wave is done with K(kt)
+        if (more) load_k(kl, Kc + (size_t)(kt + 1) * KBUF, wave, lane);
+
         bf16x8_t pa[2][2];
+        if (live) {
+            if (k0 + KT - 1 > a.pos0 + r0) {   // diagonal tile: causal mask
 #pragma unroll
-        for (int rb = 0; rb < 2; rb++) {
-            const int qpos = a.pos0 + r0 + rb * 16 + n;
-            float mx = -INFINITY;
+                for (int rb = 0; rb < 2; rb++) {
+                    const int qpos = a.pos0 + r0 + rb * 16 + n;
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++)
+                    for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    float x = s[kb][rb][i] * a.scale_log2;
-                    if (need_mask && k0 + kb * 16 + 4 * g + i > qpos) x = -INFINITY;
-                    s[kb][rb][i] = x;
-                    mx = fmaxf(mx, x);
+                        for (int i = 0; i < 4; i++)
+                            if (k0 + kb * 16 + 4 * g + i > qpos) s[kb][rb][i] = -INFINITY;
                 }
-            mx = fmaxf(mx, __shfl_xor(mx, 16, 64));
-            mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
-            const float mnew = fmaxf(mrow[rb], mx);
-            const float alpha = exp2f(mrow[rb] - mnew);
-            mrow[rb] = mnew;
-            float sum = 0.f;
+            }
+            // Lazy rescaling: P = exp2(s - m) against a reference max m per
+            // query that only moves when the tile's max exceeds it by more
+            // than 8 (so P <= 2^8, exact enough in bf16 and fp32); O and l are
+            // rescaled only then, which after the first tiles is rare.
+            float mx[2];
 #pragma unroll
-            for (int kb = 0; kb < 4; kb++)
+            for (int rb = 0; rb < 2; rb++) {
+                float m = -INFINITY;
 #pragma unroll
-                for (int i = 0; i < 4; i++) {
-                    const float pv = exp2f(s[kb][rb][i] - mnew);
-                    s[kb][rb][i] = pv;
-                    sum += pv;
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int i = 0; i < 4; i++) m = fmaxf(m, s[kb][rb][i]);
+                m = fmaxf(m, __shfl_xor(m, 16, 64));
+                mx[rb] = fmaxf(m, __shfl_xor(m, 32, 64));
+            }
+            if (__any(mx[0] > mrow[0] + 8.0f || mx[1] > mrow[1] + 8.0f)) {
+#pragma unroll
+                for (int rb = 0; rb < 2; rb++) {
+                    const float mnew = mx[rb] > mrow[rb] + 8.0f ? mx[rb] : mrow[rb];
+                    const float alpha = __builtin_amdgcn_exp2f(mrow[rb] - mnew);   // 0 on the first tile
+                    mrow[rb] = mnew;
+                    lrow[rb] *= alpha;
+                    float al[4];   // O rows 4g+i of this block take the factor of query 4g+i
+#pragma unroll
+                    for (int i = 0; i < 4; i++) al[i] = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+                    for (int db = 0; db < 16; db++)
+#pragma unroll
+                        for (int i = 0; i < 4; i++) O[rb][db][i] *= al[i];
                 }
-            sum += __shfl_xor(sum, 16, 64);
-            sum += __shfl_xor(sum, 32, 64);
-            lrow[rb] = lrow[rb] * alpha + sum;
-            // O rows 4g+i of this block take the factor of query 4g+i
-            float al[4];
+            }
 #pragma unroll
-            for (int i = 0; i < 4; i++) al[i] = __shfl(alpha, 4 * g + i, 64);
+            for (int rb = 0; rb < 2; rb++) {
+                float sum = 0.f;
 #pragma unroll
-            for (int db = 0; db < 16; db++)
+                for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-                for (int i = 0; i < 4; i++) O[rb][db][i] *= al[i];
+                    for (int i = 0; i < 4; i++) {
+                        const float pv = __builtin_amdgcn_exp2f(s[kb][rb][i] - mrow[rb]);
+                        s[kb][rb][i] = pv;
+                        sum += pv;
+                    }
+                sum += __shfl_xor(sum, 16, 64);
+                sum += __shfl_xor(sum, 32, 64);
+                lrow[rb] += sum;
+#pragma unroll
+                for (int ks = 0; ks < 2; ks++) {
+                    const uint4 u = make_uint4(pack2(s[2 * ks][rb][0], s[2 * ks][rb][1]),
+                                               pack2(s[2 * ks][rb][2], s[2 * ks][rb][3]),
+                                               pack2(s[2 * ks + 1][rb][0], s[2 * ks + 1][rb][1]),
+                                               pack2(s[2 * ks + 1][rb][2], s[2 * ks + 1][rb][3]));
+                    pa[rb][ks] = as_bf16x8(u);
+                }
+            }
+        }
+
+        // V(kt) landed; K(kt+1), issued after it, may still be in flight
+        if (more)
+            __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        else
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        lds_barrier();
+        if (k0 + KT > n_keys) {
+            // last tile: V of positions past the valid keys is zeroed (masked P
+            // is 0, and 0 * a stale NaN would not be)
+            uint16_t *V = (uint16_t *)Vl;
+            for (int e = tid; e < HDG * KT; e += 256) {
+                const int d = e >> 6, key = e & 63;
+                if (k0 + key >= n_keys) {
+                    const int u = (key >> 3) ^ ((d >> 1) & 7);
+                    V[d * KT + u * 8 + (key & 7)] = 0;
+                }
+            }
+            lds_barrier();
+        }
+        if (live) {
+            const int vsw = (n >> 1) & 7, vhalf = (g & 1) * 8;
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) {
-                const uint4 u = make_uint4(pack2(s[2 * ks][rb][0], s[2 * ks][rb][1]),
-                                           pack2(s[2 * ks][rb][2], s[2 * ks][rb][3]),
-                                           pack2(s[2 * ks + 1][rb][0], s[2 * ks + 1][rb][1]),
-                                           pack2(s[2 * ks + 1][rb][2], s[2 * ks + 1][rb][3]));
-                pa[rb][ks] = as_bf16x8(u);
+                const int u0 = ((4 * ks + (g >> 1)) ^ vsw) << 4, u1 = ((4 * ks + 2 + (g >> 1)) ^ vsw) << 4;
+#pragma unroll
+                for (int db = 0; db < 16; db++) {
+                    const char *vr = Vl + (db * 16 + n) * (KT * 2) + vhalf;
+                    const uint2 lo = *(const uint2 *)(vr + u0);
+                    const uint2 hi = *(const uint2 *)(vr + u1);
+                    const bf16x8_t vb = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+#pragma unroll
+                    for (int rb = 0; rb < 2; rb++)
+                        O[rb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rb][ks], vb, O[rb][db], 0, 0, 0);
+                }
             }
         }
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) {
-#pragma unroll
-            for (int db = 0; db < 16; db++) {
-                const uint2 lo = *(const uint2 *)&V_l[db * 16 + n][32 * ks + 4 * g];
-                const uint2 hi = *(const uint2 *)&V_l[db * 16 + n][32 * ks + 16 + 4 * g];
-                const bf16x8_t vb = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-#pragma unroll
-                for (int rb = 0; rb < 2; rb++)
-                    O[rb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rb][ks], vb, O[rb][db], 0, 0, 0);
-            }
-        }
+        lds_barrier();   // every wave is done with V(kt)
+        if (more) load_v(vl, Vc + (size_t)(kt + 1) * KBUF, wave, lane);
     }
 
     // out = O / l * sigmoid(gate)
@@ -303,12 +429,14 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
 
     AttnArgs aa;
     aa.T = d->T; aa.n_q = d->n_q; aa.n_kv = d->n_kv; aa.L = d->L; aa.pos0 = d->pos0;
-    aa.scale_log2 = 1.4426950408889634f / 16.0f;
     aa.q_rot = (const uint16_t *)scr; aa.k_cache = d->k_cache; aa.v_cache = d->v_cache;
     aa.gate = d->gate;
     aa.g_ts = d->gate_tok_stride ? d->gate_tok_stride : (size_t)d->n_q * HDG;
     aa.g_hs = d->gate_head_stride ? d->gate_head_stride : HDG;
     aa.out = d->out;
-    VX_LAUNCH(ctx, gqp_attn, dim3((unsigned)((d->T + QT - 1) / QT), (unsigned)d->n_q, (unsigned)d->B), dim3(256), aa);
+    // XCD grouping needs whole KV heads per XCD pair set: n_kv | 8 and 8 | n_q
+    aa.xcd_map = (8 % d->n_kv == 0) && (d->n_q % 8 == 0) && ((d->n_q / 8) * (8 / d->n_kv) == d->n_q / d->n_kv);
+    const int n_qt = (d->T + QT - 1) / QT;
+    VX_LAUNCH(ctx, gqp_attn, dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B), dim3(256), aa);
     return 0;
 }
