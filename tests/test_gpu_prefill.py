@@ -200,3 +200,18 @@ def test_gqa_prefill_shapes(ctx, B, T, pos0, L, inter):
     out = run_gqa_prefill(ctx, d, L, prior, inter)
     ref, _ = oracle_gqa_prefill(d, L, prior)
     check_bf16(out, ref, "out")
+
+
+def test_prefill_deterministic(ctx):
+    """Both prefills are deterministic: the same call twice gives identical
+    bits (the kernels use fixed reduction orders; a missed wait on an
+    asynchronous tile load would show up here as run-to-run differences)."""
+    from vx27_amd import workloads as W
+    d = W.gqa_prefill(B=1, T=2048, config=53)
+    a = run_gqa_prefill(ctx, d, 2048)
+    b = run_gqa_prefill(ctx, d, 2048)
+    assert np.array_equal(a, b), "gqa prefill differs between identical calls"
+    e = W.dn_prefill(B=1, T=2048, config=54)
+    o1, S1 = run_dn_prefill(ctx, e)
+    o2, S2 = run_dn_prefill(ctx, e)
+    assert np.array_equal(o1, o2) and np.array_equal(S1, S2), "dn prefill differs between identical calls"

@@ -71,6 +71,16 @@ void vx_prof_end(vx27_hip_ctx *ctx, const char *name);
         VX_LAUNCHED(#kernel);                                                     \
     } while (0)
 
+// The same with the profiler name given (for template instances whose
+// argument list needs parentheses in the macro call).
+#define VX_LAUNCH_NAMED(ctx, name, kernel, grid, block, ...)                       \
+    do {                                                                          \
+        vx_prof_begin(ctx);                                                       \
+        hipLaunchKernelGGL(kernel, grid, block, 0, (ctx)->stream, __VA_ARGS__);   \
+        vx_prof_end(ctx, name);                                                   \
+        VX_LAUNCHED(name);                                                        \
+    } while (0)
+
 // Make the context's device current (contexts may live on different devices).
 int vx_ctx_enter(vx27_hip_ctx *ctx);
 // Device scratch of at least `bytes`, owned by ctx (synchronises before growing).

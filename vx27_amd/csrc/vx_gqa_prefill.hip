@@ -10,9 +10,9 @@
 // same as causal attention of all T queries over the cache.
 //
 // Kernels per call:
-//   gqp_prep   one workgroup per (head, token, sequence): norm + RoPE of q
-//              (bf16, head-major scratch) and of k; k,v rounded to bf16 and
-//              stored at positions pos0..pos0+T-1 of the cache.
+//   gqp_prep   one workgroup per (token, sequence): norm + RoPE of every q
+//              head (bf16, head-major scratch) and k head; k,v rounded to
+//              bf16 and stored at positions pos0..pos0+T-1 of the cache.
 //   gqp_attn   one workgroup per (128-query tile, Q head, sequence), heaviest
 //              tiles first; 4 waves of 32 queries.  Per 64-key tile staged in
 //              LDS:  S^T[key][q] = K . Q^T (v_mfma_f32_16x16x32_bf16, 4 key
@@ -33,6 +33,10 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 constexpr int HDG = VX_GQA_HD;
 constexpr int QT = 128;     // queries per workgroup
+#ifndef GQP_NW
+#define GQP_NW 4            // waves per attention workgroup (32 queries each)
+#endif
+#define GQP_RB (QT / 16 / GQP_NW)
 constexpr int KT = 64;      // keys per tile
 
 struct PrepArgs {
@@ -47,45 +51,64 @@ struct PrepArgs {
     vx_rope_tab rope;
 };
 
-// grid (n_q + n_kv, T, B), block 256 (thread = dim)
+// grid (T, B), block 256: one workgroup per token, RoPE table once per
+// token, wave w handles heads w, w+4, ... of q then k; lane l holds dims
+// l, l+64, l+128, l+192
 __global__ __launch_bounds__(256) void gqp_prep(PrepArgs a) {
-    const int h = blockIdx.x, t = blockIdx.y, b = blockIdx.z, i = threadIdx.x;
-    const int wave = i >> 6, lane = i & 63;
-    __shared__ double red[4];
-    __shared__ float row[HDG];
+    const int t = blockIdx.x, b = blockIdx.y;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     __shared__ float cs[VX_ROPE_MAXH], sn[VX_ROPE_MAXH];
+    __shared__ float row[4][HDG];
     const int pos = a.pos0 + t;
     const int half = a.rope_dim / 2;
-    if (i < half) {
-        const float ang = ((float)pos / a.yarn) * a.rope.freq[i];
-        cs[i] = cosf(ang);
-        sn[i] = sinf(ang);
+    if (tid < half) {
+        const float ang = ((float)pos / a.yarn) * a.rope.freq[tid];
+        cs[tid] = cosf(ang);
+        sn[tid] = sinf(ang);
     }
-    const bool is_q = h < a.n_q;
-    const int hk = h - a.n_q;
+    __syncthreads();
     const size_t tok = (size_t)b * a.T + t;
-    const float x = vx_bf16_to_f32(is_q ? a.q[tok * a.q_ts + (size_t)h * a.q_hs + i]
-                                        : a.k[tok * a.kv_ts + (size_t)hk * HDG + i]);
-    const float w = is_q ? a.q_norm_w[i] : a.k_norm_w[i];
-    const double ws = vx_wave_sum_f64((double)x * (double)x);
-    if (lane == 0) red[wave] = ws;
-    __syncthreads();
-    const double ss = ((red[0] + red[1]) + red[2]) + red[3];
-    const float s = 1.0f / sqrtf((float)(ss / HDG) + 1e-6f);
-    const float y = (a.flags & VX27_GQA_NORM_W) ? (x * s) * w : (x * s) * (w + 1.0f);
-    row[i] = y;
-    __syncthreads();
-    float r = y;
-    if (i < half)
-        r = row[i] * cs[i] - row[i + half] * sn[i];
-    else if (i < 2 * half)
-        r = row[i - half] * sn[i - half] + row[i] * cs[i - half];
-    if (is_q) {
-        // scores leave the MFMA in the exp2 domain: q * log2(e) / sqrt(256)
-        a.q_rot[(((size_t)b * a.n_q + h) * a.T + t) * HDG + i] = vx_f32_to_bf16(r * (1.4426950408889634f / 16.0f));
-    } else {
-        a.k_cache[vx_k_index(a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(r);
-        a.v_cache[vx_v_index(a.n_kv, a.L, b, hk, pos, i)] = a.v[tok * a.kv_ts + (size_t)hk * HDG + i];
+    const int nh = a.n_q + a.n_kv;
+    float *rw = row[wave];
+    for (int h = wave; h < nh; h += 4) {
+        const bool is_q = h < a.n_q;
+        const int hk = h - a.n_q;
+        const uint16_t *src = is_q ? a.q + tok * a.q_ts + (size_t)h * a.q_hs : a.k + tok * a.kv_ts + (size_t)hk * HDG;
+        const float *wn = is_q ? a.q_norm_w : a.k_norm_w;
+        float x[4];
+        double ss = 0.0;
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            x[e] = vx_bf16_to_f32(src[lane + 64 * e]);
+            ss += (double)x[e] * (double)x[e];
+        }
+        ss = vx_wave_sum_f64(ss);
+        const float sc = 1.0f / sqrtf((float)(ss / HDG) + 1e-6f);
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const float w = wn[lane + 64 * e];
+            x[e] = (a.flags & VX27_GQA_NORM_W) ? (x[e] * sc) * w : (x[e] * sc) * (w + 1.0f);
+            rw[lane + 64 * e] = x[e];
+        }
+        __builtin_amdgcn_wave_barrier();   // this wave's row writes before its partner reads
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const int i = lane + 64 * e;
+            float r = x[e];
+            if (i < half)
+                r = rw[i] * cs[i] - rw[i + half] * sn[i];
+            else if (i < 2 * half)
+                r = rw[i - half] * sn[i - half] + rw[i] * cs[i - half];
+            if (is_q) {
+                // scores leave the MFMA in the exp2 domain: q * log2(e) / sqrt(256)
+                a.q_rot[(((size_t)b * a.n_q + h) * a.T + t) * HDG + i] = vx_f32_to_bf16(r * (1.4426950408889634f / 16.0f));
+            } else {
+                a.k_cache[vx_k_index(a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(r);
+                a.v_cache[vx_v_index(a.n_kv, a.L, b, hk, pos, i)] = a.v[tok * a.kv_ts + (size_t)hk * HDG + i];
+            }
+        }
+        __builtin_amdgcn_wave_barrier();   // reads of this row done before the next head's writes
     }
 }
 
@@ -149,31 +172,37 @@ __device__ __forceinline__ uint32_t lds_addr(const void *p) {
 // its swizzled LDS slot.  The lane offsets are recomputed at each call (the
 // empty asm hides that they are loop-invariant, so they are not held in
 // registers across the tile loop).
+template <int NW>
 __device__ __forceinline__ void load_k(uint32_t kbuf, const char *Kt, int wave, int lane) {
     __asm__ volatile("" : "+v"(lane));
+    constexpr int PER = 32 / NW;   // 1 KiB chunks per wave
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int r = (wave * 8 + j) * 2 + (lane >> 5), u = (lane & 31) ^ (r & 15);
-        dma16(Kt, (uint32_t)(r * HDG + u * 8) * 2, kbuf + (wave * 8 + j) * 1024);
+    for (int j = 0; j < PER; j++) {
+        const int r = (wave * PER + j) * 2 + (lane >> 5), u = (lane & 31) ^ (r & 15);
+        dma16(Kt, (uint32_t)(r * HDG + u * 8) * 2, kbuf + (wave * PER + j) * 1024);
     }
 }
+template <int NW>
 __device__ __forceinline__ void load_v(uint32_t vbuf, const char *Vt, int wave, int lane) {
     __asm__ volatile("" : "+v"(lane));
+    constexpr int PER = 32 / NW;
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int d = (wave * 8 + j) * 8 + (lane >> 3), w = (lane & 7) ^ ((d >> 1) & 7);
-        dma16(Vt, (uint32_t)((((w >> 2) * HDG + d) * 32) + (w & 3) * 8) * 2, vbuf + (wave * 8 + j) * 1024);
+    for (int j = 0; j < PER; j++) {
+        const int d = (wave * PER + j) * 8 + (lane >> 3), w = (lane & 7) ^ ((d >> 1) & 7);
+        dma16(Vt, (uint32_t)((((w >> 2) * HDG + d) * 32) + (w & 3) * 8) * 2, vbuf + (wave * PER + j) * 1024);
     }
 }
 
 // The workgroup's 128 query rows (row-major, same swizzle as K), once per
-// workgroup: 4 waves x 16 instructions; rows past T repeat row T-1.
+// workgroup: 64 chunks of 1 KiB over the waves; rows past T repeat row T-1.
+template <int NW>
 __device__ __forceinline__ void load_q(uint32_t qbuf, const uint16_t *Qh, int qrow0, int T, int wave, int lane) {
+    constexpr int PER = 64 / NW;
 #pragma unroll
-    for (int j = 0; j < 16; j++) {
-        const int r = (wave * 16 + j) * 2 + (lane >> 5), u = (lane & 31) ^ (r & 15);
+    for (int j = 0; j < PER; j++) {
+        const int r = (wave * PER + j) * 2 + (lane >> 5), u = (lane & 31) ^ (r & 15);
         const int t = min(qrow0 + r, T - 1);
-        dma16(Qh, (uint32_t)(t * HDG + u * 8) * 2, qbuf + (wave * 16 + j) * 1024);
+        dma16(Qh, (uint32_t)(t * HDG + u * 8) * 2, qbuf + (wave * PER + j) * 1024);
     }
 }
 
@@ -187,8 +216,11 @@ __device__ __forceinline__ void lds_barrier() {
     __asm__ volatile("" ::: "memory");
 }
 
-// grid (ceil(T/128) * n_q, B), block 256
-__global__ __launch_bounds__(256) void gqp_attn(AttnArgs a) {
+// grid (ceil(T/128) * n_q, B), block NW*64: NW waves of RB 16-query blocks
+template <int NW, int RB>
+__global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
+    static_assert(NW * RB * 16 == QT, "a workgroup covers QT queries");
+    constexpr int PER = 32 / NW;   // direct-to-LDS instructions per wave for one K or V tile
     // Workgroups go round-robin over the 8 XCDs (each with its own L2).  With
     // xcd_map, XCD x takes the query heads of KV head x / (8 / n_kv), so an
     // L2 holds one KV head's cache; heaviest (last) query tiles first.
@@ -206,7 +238,7 @@ __global__ __launch_bounds__(256) void gqp_attn(AttnArgs a) {
     const int kvh = h / (a.n_q / a.n_kv);
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: LDS bases go to M0
-    const int r0 = qt * QT + wave * 32;                 // this wave's first query (token index)
+    const int r0 = qt * QT + wave * (RB * 16);                 // this wave's first query (token index)
 
     // K and V tiles as distinct LDS objects: the next K streams in while this
     // tile's V is read, and the next V while the next K is read, and the
@@ -218,59 +250,65 @@ __global__ __launch_bounds__(256) void gqp_attn(AttnArgs a) {
     const int n_keys = a.pos0 + a.T;                           // valid cache positions
     const int wg_last = a.pos0 + min(qt * QT + QT, a.T) - 1;   // last key any row here sees
     const int n_tiles = wg_last / KT + 1;
-    const int wave_last = a.pos0 + min(r0 + 31, a.T - 1);
+    const int wave_last = a.pos0 + min(r0 + RB * 16 - 1, a.T - 1);
     // tile kt: K rows kt*64.. (32 KiB) and V blocks 2kt, 2kt+1 (2 x 16 KiB)
     const char *Kc = (const char *)(a.k_cache + vx_k_index(a.n_kv, a.L, b, kvh, 0, 0));
     const char *Vc = (const char *)(a.v_cache + vx_v_index(a.n_kv, a.L, b, kvh, 0, 0));
     const uint32_t kl = lds_addr(Kl), vl = lds_addr(Vl);
-    load_q(lds_addr(Ql), a.q_rot + ((size_t)b * a.n_q + h) * a.T * HDG, qt * QT, a.T, wave, lane);
-    load_k(kl, Kc, wave, lane);
-    load_v(vl, Vc, wave, lane);
+    load_q<NW>(lds_addr(Ql), a.q_rot + ((size_t)b * a.n_q + h) * a.T * HDG, qt * QT, a.T, wave, lane);
+    load_k<NW>(kl, Kc, wave, lane);
+    load_v<NW>(vl, Vc, wave, lane);
 
-    floatx4_t O[2][16];
+    floatx4_t O[RB][16];
 #pragma unroll
-    for (int rb = 0; rb < 2; rb++)
+    for (int rb = 0; rb < RB; rb++)
 #pragma unroll
         for (int db = 0; db < 16; db++) O[rb][db] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
-    float mrow[2] = {-INFINITY, -INFINITY}, lrow[2] = {0.f, 0.f};
+    float mrow[RB], lrow[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        mrow[rb] = -INFINITY;
+        lrow[rb] = 0.f;
+    }
 
     for (int kt = 0; kt < n_tiles; kt++) {
         const int k0 = kt * KT;
         const bool more = kt + 1 < n_tiles;
         const bool live = k0 <= wave_last;   // wave-uniform: otherwise every key here is masked
-        // K(kt) (and Q) landed; V(kt), issued after it, may still be in flight
-        __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+        // K(kt) (and Q) landed; V(kt), issued after it (PER instructions per
+        // wave), may still be in flight
+        __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
         lds_barrier();
-        floatx4_t s[4][2];
+        floatx4_t s[4][RB];
 #pragma unroll
         for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-            for (int rb = 0; rb < 2; rb++) s[kb][rb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+            for (int rb = 0; rb < RB; rb++) s[kb][rb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
         if (live) {
 #pragma unroll
             for (int ks = 0; ks < 8; ks++) {
                 const int uo = ((4 * ks + g) ^ n) << 4;   // swizzled unit of rows = n (mod 16)
-                bf16x8_t qv[2];
+                bf16x8_t qv[RB];
 #pragma unroll
-                for (int rb = 0; rb < 2; rb++)
-                    qv[rb] = as_bf16x8(*(const uint4 *)(Ql + (wave * 32 + rb * 16 + n) * 512 + uo));
+                for (int rb = 0; rb < RB; rb++)
+                    qv[rb] = as_bf16x8(*(const uint4 *)(Ql + (wave * (RB * 16) + rb * 16 + n) * 512 + uo));
 #pragma unroll
                 for (int kb = 0; kb < 4; kb++) {
                     const bf16x8_t ka = as_bf16x8(*(const uint4 *)(Kl + (kb * 16 + n) * 512 + uo));
 #pragma unroll
-                    for (int rb = 0; rb < 2; rb++)
+                    for (int rb = 0; rb < RB; rb++)
                         s[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qv[rb], s[kb][rb], 0, 0, 0);
                 }
             }
         }
         lds_barrier();   // every wave is done with K(kt)
-        if (more) load_k(kl, Kc + (size_t)(kt + 1) * KBUF, wave, lane);
+        if (more) load_k<NW>(kl, Kc + (size_t)(kt + 1) * KBUF, wave, lane);
 
-        bf16x8_t pa[2][2];
+        bf16x8_t pa[RB][2];
         if (live) {
             if (k0 + KT - 1 > a.pos0 + r0) {   // diagonal tile: causal mask
 #pragma unroll
-                for (int rb = 0; rb < 2; rb++) {
+                for (int rb = 0; rb < RB; rb++) {
                     const int qpos = a.pos0 + r0 + rb * 16 + n;
 #pragma unroll
                     for (int kb = 0; kb < 4; kb++)
@@ -283,9 +321,9 @@ __global__ __launch_bounds__(256) void gqp_attn(AttnArgs a) {
             // query that only moves when the tile's max exceeds it by more
             // than 8 (so P <= 2^8, exact enough in bf16 and fp32); O and l are
             // rescaled only then, which after the first tiles is rare.
-            float mx[2];
+            float mx[RB];
 #pragma unroll
-            for (int rb = 0; rb < 2; rb++) {
+            for (int rb = 0; rb < RB; rb++) {
                 float m = -INFINITY;
 #pragma unroll
                 for (int kb = 0; kb < 4; kb++)
@@ -294,9 +332,12 @@ __global__ __launch_bounds__(256) void gqp_attn(AttnArgs a) {
                 m = fmaxf(m, __shfl_xor(m, 16, 64));
                 mx[rb] = fmaxf(m, __shfl_xor(m, 32, 64));
             }
-            if (__any(mx[0] > mrow[0] + 8.0f || mx[1] > mrow[1] + 8.0f)) {
+            bool grow = false;
 #pragma unroll
-                for (int rb = 0; rb < 2; rb++) {
+            for (int rb = 0; rb < RB; rb++) grow = grow || mx[rb] > mrow[rb] + 8.0f;
+            if (__any(grow)) {
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) {
                     const float mnew = mx[rb] > mrow[rb] + 8.0f ? mx[rb] : mrow[rb];
                     const float alpha = __builtin_amdgcn_exp2f(mrow[rb] - mnew);   // 0 on the first tile
                     mrow[rb] = mnew;
@@ -311,7 +352,7 @@ __global__ __launch_bounds__(256) void gqp_attn(AttnArgs a) {
                 }
             }
 #pragma unroll
-            for (int rb = 0; rb < 2; rb++) {
+            for (int rb = 0; rb < RB; rb++) {
                 float sum = 0.f;
 #pragma unroll
                 for (int kb = 0; kb < 4; kb++)
@@ -337,7 +378,7 @@ __global__ __launch_bounds__(256) void gqp_attn(AttnArgs a) {
 
         // V(kt) landed; K(kt+1), issued after it, may still be in flight
         if (more)
-            __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
+            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
         else
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
         lds_barrier();
@@ -345,7 +386,7 @@ __global__ __launch_bounds__(256) void gqp_attn(AttnArgs a) {
             // last tile: V of positions past the valid keys is zeroed (masked P
             // is 0, and 0 * a stale NaN would not be)
             uint16_t *V = (uint16_t *)Vl;
-            for (int e = tid; e < HDG * KT; e += 256) {
+            for (int e = tid; e < HDG * KT; e += NW * 64) {
                 const int d = e >> 6, key = e & 63;
                 if (k0 + key >= n_keys) {
                     const int u = (key >> 3) ^ ((d >> 1) & 7);
@@ -366,18 +407,18 @@ __global__ __launch_bounds__(256) void gqp_attn(AttnArgs a) {
                     const uint2 hi = *(const uint2 *)(vr + u1);
                     const bf16x8_t vb = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
 #pragma unroll
-                    for (int rb = 0; rb < 2; rb++)
+                    for (int rb = 0; rb < RB; rb++)
                         O[rb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rb][ks], vb, O[rb][db], 0, 0, 0);
                 }
             }
         }
         lds_barrier();   // every wave is done with V(kt)
-        if (more) load_v(vl, Vc + (size_t)(kt + 1) * KBUF, wave, lane);
+        if (more) load_v<NW>(vl, Vc + (size_t)(kt + 1) * KBUF, wave, lane);
     }
 
     // out = O / l * sigmoid(gate)
 #pragma unroll
-    for (int rb = 0; rb < 2; rb++) {
+    for (int rb = 0; rb < RB; rb++) {
         float il[4];
 #pragma unroll
         for (int i = 0; i < 4; i++) il[i] = 1.0f / __shfl(lrow[rb], 4 * g + i, 64);
@@ -425,7 +466,7 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     pa.kv_ts = (size_t)d->n_kv * HDG;
     pa.q_norm_w = d->q_norm_w; pa.k_norm_w = d->k_norm_w;
     pa.k_cache = d->k_cache; pa.v_cache = d->v_cache; pa.q_rot = (uint16_t *)scr;
-    VX_LAUNCH(ctx, gqp_prep, dim3((unsigned)(d->n_q + d->n_kv), (unsigned)d->T, (unsigned)d->B), dim3(256), pa);
+    VX_LAUNCH(ctx, gqp_prep, dim3((unsigned)d->T, (unsigned)d->B), dim3(256), pa);
 
     AttnArgs aa;
     aa.T = d->T; aa.n_q = d->n_q; aa.n_kv = d->n_kv; aa.L = d->L; aa.pos0 = d->pos0;
@@ -437,6 +478,7 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     // XCD grouping needs whole KV heads per XCD pair set: n_kv | 8 and 8 | n_q
     aa.xcd_map = (8 % d->n_kv == 0) && (d->n_q % 8 == 0) && ((d->n_q / 8) * (8 / d->n_kv) == d->n_q / d->n_kv);
     const int n_qt = (d->T + QT - 1) / QT;
-    VX_LAUNCH(ctx, gqp_attn, dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B), dim3(256), aa);
+    VX_LAUNCH_NAMED(ctx, "gqp_attn", (gqp_attn<GQP_NW, GQP_RB>), dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B),
+                    dim3(GQP_NW * 64), aa);
     return 0;
 }
