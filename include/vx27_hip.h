@@ -240,10 +240,12 @@ int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const
                        size_t x_stride, int B, float *y, size_t y_stride);
 
 /* Weight tiling for the layer entry points: row-major bf16 W [N][K] into the
- * MFMA tile layout [N/16][K/32][64 lanes][8] (lane (g,m) of tile (rb, s)
- * holds W[16rb + m][32s + 8g .. 8g+7]), so each wave loads 1 KiB of
- * contiguous weights per tile.  Done once per weight, like the reference's
- * offline forge of its packed weight format (src/vx_forge.c). */
+ * MFMA tile layout [K/32][N/16][64 lanes][8] (lane (g,m) of tile (s, rb)
+ * holds W[16rb + m][32s + 8g .. 8g+7]): each wave loads 1 KiB of contiguous
+ * weights per tile, and the row blocks of one k-step are adjacent, so the
+ * workgroups of a launch stream one contiguous band at a time.  Done once
+ * per weight, like the reference's offline forge of its packed weight format
+ * (src/vx_forge.c). */
 int vx27_hip_pack_weights_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, uint16_t *W_tiled);
 
 /* The mixer of one Gated DeltaNet layer for one decode token of B <= 5

@@ -42,6 +42,10 @@ __device__ __forceinline__ void load_conv_w(const void *w, int bf16, size_t ch, 
 }
 }  // namespace
 
+// Internal flag: q and k are final (normalised and scaled as step_exact
+// leaves them); the recurrence skips every q/k normalisation.
+constexpr unsigned VX_DN_QK_READY = 1u << 16;
+
 struct DnArgs {
     int B, nqk, nv, steps;
     unsigned flags;
@@ -60,7 +64,17 @@ struct DnArgs {
     float *out;                   // may be NULL when out_packed is set
     size_t out_tok;               // per-(t,b) stride of out
     uint16_t *out_packed;         // optional: out as the packed GEMV operand (steps == 1)
+    // optional scratch [B][nv][128] for pre-norm outputs: lets a single-step
+    // call with VX27_DN_OUT_GATE split each head's columns over workgroups
+    // (the output norm then runs in a separate finish kernel)
+    float *o_pre;
 };
 
-// Launch the recurrence (one workgroup per (sequence, value head)).
+// Normalise q and k in place for the recurrence, one workgroup per
+// (sequence, QK head, q|k): the chain rmsn(1+w) (PRE_RMS), l2norm and
+// 1/sqrt(hd) (PRE_L2), then step_exact's own l2norm and 1/sqrt(hd) on q.
+// q_tok/k_tok are the per-sequence strides; flags select the first two steps.
+int vx_dn_qk_norm(vx27_hip_ctx *ctx, int B, int nqk, unsigned flags, float *q, float *k, size_t tok_stride,
+                  const float *norm_w);
+// Launch the recurrence (one or more workgroups per (sequence, value head)).
 int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a);

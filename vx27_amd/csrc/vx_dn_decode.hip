@@ -79,21 +79,29 @@ __device__ __forceinline__ double part_sum(double x) {
     return x;
 }
 
-// One workgroup per (sequence, value head) with 128*R lanes: lane (col, part)
-// = (tid / R, tid % R) holds rows part*128/R .. of state column col.  Lanes
-// tid < 128 own q/k element tid (and its conv channels); the part-0 lane of a
-// column owns the value channel and writes the column's output.
-template <int R>
-__global__ __launch_bounds__(HD * R) void dn_decode_kernel(DnArgs a) {
+// CS workgroups per (sequence, value head), each owning 128/CS state
+// columns with R lanes per column (128/CS * R >= 128 lanes): lane (lcol,
+// part) = (tid / R, tid % R) holds rows part*128/R .. of column
+// slice*128/CS + lcol.  Lanes tid < 128 own q/k element tid (and its conv
+// channels, CS == 1 only); the part-0 lane of a column owns the value channel
+// and writes the column's output.  The columns of a head are independent in
+// kv = S^T k, the rank-1 update and o = S^T q; the q/k normalisations are
+// recomputed by every slice.  With CS > 1 and VX27_DN_OUT_GATE (one step),
+// the pre-norm outputs go to o_pre and dn_out_gate finishes them.
+template <int R, int CS>
+__global__ __launch_bounds__(HD / CS * R) void dn_decode_kernel(DnArgs a) {
     constexpr int RR = HD / R;                 // state rows per lane
-    constexpr int NW = 2 * R;                  // waves per block
+    constexpr int NT = HD / CS * R;            // lanes per block
+    constexpr int NW = NT / 64;                // waves per block
+    static_assert(NT >= HD && NT % 64 == 0, "a block needs a lane per q/k element");
     const int tid = threadIdx.x;
-    const int part = tid % R, col = tid / R;
+    const int part = tid % R, col = (blockIdx.x % CS) * (HD / CS) + tid / R;
     const int j = tid;                         // q/k element (qk lanes)
     const bool qk_lane = tid < HD;
     const bool v_lane = part == 0;
-    const int b = blockIdx.x / a.nv;
-    const int vh = blockIdx.x % a.nv;
+    const int head = blockIdx.x / CS;
+    const int b = head / a.nv;
+    const int vh = head % a.nv;
     const int g = vh * a.nqk / a.nv;           // QK head (vx27_qfwd.c:137)
     const int qd = a.nqk * HD, vd = a.nv * HD, C = 2 * qd + vd;
 
@@ -108,8 +116,8 @@ __global__ __launch_bounds__(HD * R) void dn_decode_kernel(DnArgs a) {
     for (int u = 0; u < RR; u++)
         Sc[u] = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(Sr, col * 4, (part * RR + u) * HD * 4, 0));
 
-    // ---- owned conv channels (fused conv: nv == nqk, so g == vh)
-    const bool conv = a.fused_conv != 0;
+    // ---- owned conv channels (fused conv: nv == nqk, so g == vh; CS == 1)
+    const bool conv = CS == 1 && a.fused_conv != 0;
     float cq[3] = {0, 0, 0}, ck[3] = {0, 0, 0}, cv[3] = {0, 0, 0};
     float wq[4] = {0, 0, 0, 0}, wk[4] = {0, 0, 0, 0}, wv[4] = {0, 0, 0, 0};
     const size_t chq = (size_t)g * HD + j, chk = (size_t)qd + g * HD + j,
@@ -155,29 +163,36 @@ __global__ __launch_bounds__(HD * R) void dn_decode_kernel(DnArgs a) {
             if (v_lane) va = a.v[sb * a.v_tok + (size_t)vh * HD + col];
         }
         if (R > 1) va = __shfl(va, (tid & 63) - part, 64);   // from the column's part-0 lane
-        // ---- q/k normalisation chain
-        if (a.flags & VX27_DN_PRE_RMS) {       // rmsn(x)*(1+w), vx27_qfwd.c:32-39,123
-            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
-            block_sum2<NW>(sq, sk, s_red[0]);
-            const float iq = 1.0f / sqrtf((float)(sq / HD) + 1e-6f);
-            const float ik = 1.0f / sqrtf((float)(sk / HD) + 1e-6f);
-            qa = (qa * iq) * (nwj + 1.0f);
-            ka = (ka * ik) * (nwj + 1.0f);
-        }
-        if (a.flags & VX27_DN_PRE_L2) {        // l2norm + q/sqrt(hd), vx27_qfwd.c:124-130
-            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
-            block_sum2<NW>(sq, sk, s_red[1]);
-            qa = qa * (1.0f / sqrtf((float)sq + 1e-6f));
-            ka = ka * (1.0f / sqrtf((float)sk + 1e-6f));
-            qa = qa * qs;
-        }
-        {                                       // inside step_exact, vx27_deltanet.c:77-80
-            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
-            block_sum2<NW>(sq, sk, s_red[2]);
+        // ---- q/k normalisation chain (skipped when q, k arrive final)
+        if (a.flags & VX_DN_QK_READY) {
             if (qk_lane) {
-                const float qn = qa * (1.0f / sqrtf((float)sq + 1e-6f));
-                s_qn[j] = qn * qs;
-                s_kn[j] = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+                s_qn[j] = qa;
+                s_kn[j] = ka;
+            }
+        } else {
+            if (a.flags & VX27_DN_PRE_RMS) {       // rmsn(x)*(1+w), vx27_qfwd.c:32-39,123
+                double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+                block_sum2<NW>(sq, sk, s_red[0]);
+                const float iq = 1.0f / sqrtf((float)(sq / HD) + 1e-6f);
+                const float ik = 1.0f / sqrtf((float)(sk / HD) + 1e-6f);
+                qa = (qa * iq) * (nwj + 1.0f);
+                ka = (ka * ik) * (nwj + 1.0f);
+            }
+            if (a.flags & VX27_DN_PRE_L2) {        // l2norm + q/sqrt(hd), vx27_qfwd.c:124-130
+                double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+                block_sum2<NW>(sq, sk, s_red[1]);
+                qa = qa * (1.0f / sqrtf((float)sq + 1e-6f));
+                ka = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+                qa = qa * qs;
+            }
+            {                                       // inside step_exact, vx27_deltanet.c:77-80
+                double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+                block_sum2<NW>(sq, sk, s_red[2]);
+                if (qk_lane) {
+                    const float qn = qa * (1.0f / sqrtf((float)sq + 1e-6f));
+                    s_qn[j] = qn * qs;
+                    s_kn[j] = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+                }
             }
         }
         __syncthreads();
@@ -217,6 +232,11 @@ __global__ __launch_bounds__(HD * R) void dn_decode_kernel(DnArgs a) {
         o = part_sum<R>(o);
         float of = (float)o;
         // ---- gated output norm (vx27_qfwd.c:147-151)
+        if (CS > 1 && (a.flags & VX27_DN_OUT_GATE)) {   // finished by dn_out_gate
+            if (v_lane) a.o_pre[((size_t)b * a.nv + vh) * HD + col] = of;
+            __syncthreads();   // s_qn/s_kn are rewritten by the next step
+            continue;
+        }
         if (a.flags & VX27_DN_OUT_GATE) {
             double so = v_lane ? (double)of * (double)of : 0.0, unused = 0.0;
             block_sum2<NW>(so, unused, s_red[3]);
@@ -251,6 +271,53 @@ __global__ __launch_bounds__(HD * R) void dn_decode_kernel(DnArgs a) {
     }
 }
 
+// q/k normalisation chain ahead of the recurrence: block (b, g, which) of
+// 128 lanes normalises q (which = 0) or k (which = 1) of QK head g in place.
+// Same operations and reduction order as the in-kernel chain.
+__global__ __launch_bounds__(HD) void dn_qk_norm_kernel(int nqk, unsigned flags, float *q, float *k, size_t tok,
+                                                       const float *norm_w) {
+    const int which = blockIdx.x & 1, g = (blockIdx.x >> 1) % nqk, b = (blockIdx.x >> 1) / nqk;
+    const int j = threadIdx.x;
+    __shared__ double s_red[3][2][2];
+    float *p = (which ? k : q) + (size_t)b * tok + (size_t)g * HD + j;
+    float x = *p;
+    const float qs = 1.0f / sqrtf((float)HD);
+    double unused = 0.0;
+    if (flags & VX27_DN_PRE_RMS) {
+        double s = (double)x * (double)x;
+        block_sum2<2>(s, unused, s_red[0]);
+        x = (x * (1.0f / sqrtf((float)(s / HD) + 1e-6f))) * (norm_w[j] + 1.0f);
+    }
+    if (flags & VX27_DN_PRE_L2) {
+        double s = (double)x * (double)x;
+        block_sum2<2>(s, unused, s_red[1]);
+        x = x * (1.0f / sqrtf((float)s + 1e-6f));
+        if (!which) x = x * qs;
+    }
+    double s = (double)x * (double)x;
+    block_sum2<2>(s, unused, s_red[2]);
+    x = x * (1.0f / sqrtf((float)s + 1e-6f));
+    if (!which) x = x * qs;
+    *p = x;
+}
+
+// Gated output norm of one step for column-split heads: one block of 128
+// lanes per (sequence, value head); out = rmsn_std(o)*norm_w * silu(z)
+// (vx27_qfwd.c:147-151) from the pre-norm outputs in o_pre.
+__global__ __launch_bounds__(HD) void dn_out_gate(DnArgs a) {
+    const int head = blockIdx.x, col = threadIdx.x;
+    const int b = head / a.nv, vh = head % a.nv;
+    __shared__ double s_red[2][2];
+    float of = a.o_pre[(size_t)head * HD + col];
+    double so = (double)of * (double)of, unused = 0.0;
+    block_sum2<2>(so, unused, s_red);
+    const float is = 1.0f / sqrtf((float)(so / HD) + 1e-6f);
+    const float zz = a.z[(size_t)b * a.z_tok + (size_t)vh * HD + col];
+    of = ((of * is) * a.norm_w[col]) * silu_f(zz);
+    if (a.out) a.out[(size_t)b * a.out_tok + (size_t)vh * HD + col] = of;
+    if (a.out_packed) vx_pack_store(a.out_packed, a.B, b, vh * HD + col, of);
+}
+
 // Channel-parallel causal conv over `steps` tokens: one thread per (b, c),
 // state carried in registers; act [steps][B][C] receives silu(conv).
 struct ConvArgs {
@@ -277,18 +344,51 @@ __global__ __launch_bounds__(256) void dn_conv_kernel(ConvArgs a) {
 
 }  // namespace
 
+int vx_dn_qk_norm(vx27_hip_ctx *ctx, int B, int nqk, unsigned flags, float *q, float *k, size_t tok_stride,
+                  const float *norm_w) {
+    VX_LAUNCH(ctx, dn_qk_norm_kernel, dim3((unsigned)(B * nqk * 2)), dim3(HD), nqk, flags, q, k, tok_stride, norm_w);
+    return 0;
+}
+
 int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a) {
     VX_REQUIRE(!a.fused_conv || a.nv == a.nqk, "dn recurrence: fused conv needs nv == nqk");
-    // split each state column over R lanes when there are few heads to spread
-    // over the 256 CUs (one workgroup per head)
+    // Spread few heads over the 256 CUs: split each head's columns over CS
+    // workgroups (not with the fused conv, whose q/k channels one block owns,
+    // nor with a per-step output norm over several steps), else split each
+    // column's rows over R lanes of one workgroup.
     const int heads = a.B * a.nv;
-    const dim3 grid((unsigned)heads);
-    if (heads >= 1024)
-        VX_LAUNCH(ctx, dn_decode_kernel<1>, grid, dim3(HD * 1), a);
-    else if (heads >= 256)
-        VX_LAUNCH(ctx, dn_decode_kernel<2>, grid, dim3(HD * 2), a);
-    else
-        VX_LAUNCH(ctx, dn_decode_kernel<4>, grid, dim3(HD * 4), a);
+    const bool gate = (a.flags & VX27_DN_OUT_GATE) != 0;
+    int CS = 1;
+    if (!a.fused_conv && (!gate || (a.steps == 1 && a.o_pre)))
+        while (heads * CS < 512 && CS < 8) CS *= 2;
+#if defined(VX_DN_CS)
+    if (CS > 1) CS = VX_DN_CS;   // build-time override for tuning sweeps
+#endif
+    const dim3 grid((unsigned)(heads * CS));
+    switch (CS) {
+        case 1:
+            if (heads >= 1024)
+                VX_LAUNCH_NAMED(ctx, "dn_decode_kernel", (dn_decode_kernel<1, 1>), grid, dim3(HD), a);
+            else if (heads >= 256)
+                VX_LAUNCH_NAMED(ctx, "dn_decode_kernel", (dn_decode_kernel<2, 1>), grid, dim3(HD * 2), a);
+            else
+                VX_LAUNCH_NAMED(ctx, "dn_decode_kernel", (dn_decode_kernel<4, 1>), grid, dim3(HD * 4), a);
+            break;
+#ifndef VX_DN_RS
+#define VX_DN_RS 1   // lanes per column = CS * VX_DN_RS
+#endif
+        case 2:
+            VX_LAUNCH_NAMED(ctx, "dn_decode_kernel", (dn_decode_kernel<2 * VX_DN_RS, 2>), grid, dim3(HD * VX_DN_RS), a);
+            break;
+        case 4:
+            VX_LAUNCH_NAMED(ctx, "dn_decode_kernel", (dn_decode_kernel<4 * VX_DN_RS, 4>), grid, dim3(HD * VX_DN_RS), a);
+            break;
+        default:
+            VX_LAUNCH_NAMED(ctx, "dn_decode_kernel", (dn_decode_kernel<8 * VX_DN_RS, 8>), grid, dim3(HD * VX_DN_RS), a);
+            break;
+    }
+    DnArgs f = a;
+    if (CS > 1 && gate) VX_LAUNCH(ctx, dn_out_gate, dim3((unsigned)heads), dim3(HD), f);
     return 0;
 }
 
@@ -329,18 +429,21 @@ extern "C" int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d) {
         a.fused_conv = 1;
         a.x = d->x;
     }
-    // scratch: gates [steps][B][nv] double2, then (unfused conv) activations
+    // scratch: gates [steps][B][nv] double2, pre-norm outputs [B][nv][128],
+    // then (unfused conv) activations
     const size_t n_gate = (size_t)d->steps * d->B * d->nv;
     const size_t gate_bytes = (n_gate * sizeof(double2) + 255) & ~(size_t)255;
+    const size_t opre_bytes = ((size_t)d->B * vd * sizeof(float) + 255) & ~(size_t)255;
     const size_t act_elems = sep_conv ? (size_t)d->steps * d->B * C : 0;
     void *scr;
-    if (vx_ctx_scratch(ctx, gate_bytes + act_elems * sizeof(float), &scr)) return -1;
+    if (vx_ctx_scratch(ctx, gate_bytes + opre_bytes + act_elems * sizeof(float), &scr)) return -1;
     double2 *gates = (double2 *)scr;
+    a.o_pre = (float *)((char *)scr + gate_bytes);
     VX_LAUNCH(ctx, dn_gate_kernel, dim3((unsigned)((n_gate + 255) / 256)), dim3(256), (int)n_gate, d->nv, d->a, d->b, d->A_log, d->dt_bias, gates);
     a.gates = gates;
     if (sep_conv) {
         // shared q/k channels: convolve all channels first
-        float *act = (float *)((char *)scr + gate_bytes);
+        float *act = (float *)((char *)scr + gate_bytes + opre_bytes);
         ConvArgs ca = {d->B, C, d->steps, a.conv_bf16, d->conv_state, d->conv_w, d->x, act};
         const size_t nthr = (size_t)d->B * C;
         VX_LAUNCH(ctx, dn_conv_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), ca);

@@ -16,10 +16,13 @@
 // Layouts:
 //   packed activations  [K/32 k-steps][64 lanes][8] bf16: lane (g,n) of k-step
 //                       s holds part n/B of vector n%B at k = 32s + 8g + 0..7
-//   tiled weights       [N/16 row blocks][K/32 k-steps][64 lanes][8] bf16:
+//   tiled weights       [K/32 k-steps][N/16 row blocks][64 lanes][8] bf16:
 //                       lane (g,m) holds W[16*rb + m][32s + 8g + 0..7], so a
-//                       wave's A operand is 1 KiB of contiguous memory
-//                       (vx27_hip_pack_weights_bf16 converts row-major W)
+//                       wave's A operand is 1 KiB of contiguous memory and
+//                       the 4 row blocks of a workgroup at one k-step are
+//                       4 KiB contiguous; workgroups moving together read one
+//                       contiguous band of W (vx27_hip_pack_weights_bf16
+//                       converts row-major W)
 //
 // gemv_part: a workgroup of 4 waves owns 64 rows (4 row blocks); its waves
 // take 4 consecutive K segments and are combined in LDS, so one partial
@@ -33,6 +36,17 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 constexpr int RB = 4;   // 16-row MFMA blocks per workgroup
+#ifndef VX_GEMV_WAVES
+#define VX_GEMV_WAVES 2048   // target waves per launch
+#endif
+#ifndef VX_GEMV_MINKS
+#define VX_GEMV_MINKS 8      // at least this many 32-wide k-steps per wave
+#endif
+#ifndef VX_GEMV_UNROLL
+#define VX_GEMV_UNROLL 4     // k-steps in flight per wave (x RB loads each)
+#endif
+#define VX_PRAGMA(x) _Pragma(#x)
+#define VX_UNROLL(n) VX_PRAGMA(unroll n)
 
 // pack activations: grid (K/32), block 64; lane (g,n) writes its 8 elements
 __global__ __launch_bounds__(64) void pack_x(const float *x, size_t x_stride, int B, uint16_t *out) {
@@ -55,9 +69,9 @@ __global__ __launch_bounds__(64) void pack_x(const float *x, size_t x_stride, in
 // row-major W [N][K] -> tiled; grid (N/16, K/32), block 64
 __global__ __launch_bounds__(64) void pack_w(const uint16_t *W, int K, uint16_t *Wt) {
     const int rb = blockIdx.x, s = blockIdx.y, lane = threadIdx.x, g = lane >> 4, m = lane & 15;
-    const int nks = K / 32;
+    const int nb = gridDim.x;
     const uint4 v = *(const uint4 *)(W + (size_t)(16 * rb + m) * K + 32 * s + 8 * g);
-    *(uint4 *)(Wt + (((size_t)rb * nks + s) * 64 + lane) * 8) = v;
+    *(uint4 *)(Wt + (((size_t)s * nb + rb) * 64 + lane) * 8) = v;
 }
 
 // grid (ceil(N/64), ceil(n_seg/4)), block 256; wave w: K segment 4*blockIdx.y + w
@@ -79,17 +93,17 @@ __global__ __launch_bounds__(256) void gemv_part_k(const uint16_t *W, int N, int
     for (int r = 0; r < RB; r++) {
         live[r] = (rb0 + r) * 16 < N;          // whole 16-row block in or out (N % 16 == 0)
         const int rb = live[r] ? rb0 + r : 0;
-        wp[r] = TILED ? W + ((size_t)rb * nks * 64 + lane) * 8
+        wp[r] = TILED ? W + ((size_t)rb * 64 + lane) * 8
                       : W + (size_t)(16 * rb + m) * K + 8 * g;
     }
     const bf16x8_t *xb = (const bf16x8_t *)xp + lane;
-#pragma unroll 4
+    VX_UNROLL(VX_GEMV_UNROLL)
     for (int s = s0; s < s1; s++) {
         const bf16x8_t bop = xb[(size_t)s * 64];
         bf16x8_t aop[RB];
 #pragma unroll
         for (int r = 0; r < RB; r++)
-            aop[r] = *(const bf16x8_t *)(TILED ? wp[r] + (size_t)s * 512 : wp[r] + 32 * s);
+            aop[r] = *(const bf16x8_t *)(TILED ? wp[r] + (size_t)s * (N / 16) * 512 : wp[r] + 32 * s);
 #pragma unroll
         for (int r = 0; r < RB; r++)
             if (live[r]) acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[r], bop, acc[r], 0, 0, 0);
@@ -129,9 +143,9 @@ int vx_gemv_plan(int N, int K, int *n_seg, int *ks_per) {
                "gemv: N must be a multiple of 16 and K of 32 (N=%d K=%d)", N, K);
     const int groups = (N + 16 * RB - 1) / (16 * RB);
     const int nks = K / 32;
-    // about 2048 waves in all, at least 8 k-steps per wave
-    int seg = (2048 + groups - 1) / groups;
-    if (seg > nks / 8) seg = nks / 8;
+    // about VX_GEMV_WAVES waves in all, at least VX_GEMV_MINKS k-steps per wave
+    int seg = (VX_GEMV_WAVES + groups - 1) / groups;
+    if (seg > nks / VX_GEMV_MINKS) seg = nks / VX_GEMV_MINKS;
     if (seg < 1) seg = 1;
     int per = (nks + seg - 1) / seg;
     seg = (nks + per - 1) / per;

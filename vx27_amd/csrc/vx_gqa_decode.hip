@@ -129,15 +129,18 @@ __device__ __forceinline__ bf16x8_t load_bf16x8(const uint16_t *p) {
 }
 
 // grid (n_split, n_kv, B), block 64 (one wave)
-__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void gqa_split(SplitArgs a) {
+#ifndef VX_SPLIT_WPE
+#define VX_SPLIT_WPE 2       // waves per SIMD the split kernel is compiled for
+#endif
+#ifndef VX_SPLIT_WAVES
+#define VX_SPLIT_WAVES 2048  // target split waves per launch
+#endif
+__global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(VX_SPLIT_WPE))) void gqa_split(SplitArgs a) {
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x, g = lane >> 4, n = lane & 15;
     const int qg = a.n_q / a.n_kv;
     const int n_keys = min(max(a.pos[b], 0), a.L - 1) + 1;
     const int n_tiles = (n_keys + TILE - 1) / TILE;
-    const int per = (n_tiles + a.n_split - 1) / a.n_split;
-    const int t0 = split * per;
-    const int t1 = min(n_tiles, t0 + per);
 
     // Q^T operand: lane (g,n) holds dims 32s + 8g + 0..7 of query head n
     bf16x8_t qB[8];
@@ -164,7 +167,10 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(2))) void gq
     // A-operand row m of block r holds key 8(m/4) + 4r + m%4
     const int krow0 = 8 * (n >> 2) + (n & 3);
 
-    for (int tile = t0; tile < t1; tile++) {
+    // split s takes tiles s, s + n_split, ...: at any moment the splits in
+    // flight read one contiguous window of the cache (rather than n_split
+    // streams a fixed distance apart, which land on the same HBM channels)
+    for (int tile = split; tile < n_tiles; tile += a.n_split) {
         const int key0 = tile * TILE;
         // ---- scores S^T (two 16-key blocks)
         floatx4_t sc0 = {0.f, 0.f, 0.f, 0.f}, sc1 = {0.f, 0.f, 0.f, 0.f};
@@ -354,9 +360,9 @@ static int gqa_check(const vx27_gqa_desc *d) {
 static int gqa_n_split(const vx27_gqa_desc *d) {
     int n_split = d->n_split;
     if (n_split <= 0) {
-        // ~4096 waves over all (sequence, KV head) pairs, at least 4 tiles per wave
+        // ~VX_SPLIT_WAVES waves over all (sequence, KV head) pairs, at least 4 tiles per wave
         const int tiles = d->L / TILE;
-        n_split = (4096 + d->B * d->n_kv - 1) / (d->B * d->n_kv);
+        n_split = (VX_SPLIT_WAVES + d->B * d->n_kv - 1) / (d->B * d->n_kv);
         if (n_split > (tiles + 3) / 4) n_split = (tiles + 3) / 4;
         if (n_split < 1) n_split = 1;
     }

@@ -123,8 +123,9 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     const size_t act_b = align256((size_t)B * C * 4), z_b = align256((size_t)B * vd * 4);
     const size_t g_b = align256((size_t)B * nv * sizeof(double2));
     const size_t pk_o = align256(vx_pack_bytes(vd));
+    const size_t opre_b = align256((size_t)B * vd * 4);
     void *scr;
-    if (vx_ctx_scratch(ctx, pk_x + part_b + act_b + z_b + g_b + pk_o, &scr)) return -1;
+    if (vx_ctx_scratch(ctx, pk_x + part_b + act_b + z_b + g_b + pk_o + opre_b, &scr)) return -1;
     char *p = (char *)scr;
     uint16_t *xp = d->x_packed ? (uint16_t *)d->x_packed : (uint16_t *)p;
     p += pk_x;
@@ -132,7 +133,8 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     float *act = (float *)p; p += act_b;
     float *z = (float *)p; p += z_b;
     double2 *gates = (double2 *)p; p += g_b;
-    uint16_t *op = (uint16_t *)p;
+    uint16_t *op = (uint16_t *)p; p += pk_o;
+    float *o_pre = (float *)p;
 
     if (!d->x_packed && vx_pack(ctx, d->x, (size_t)H, B, H, xp)) return -1;
     if (vx_gemv_part(ctx, d->w_in, 1, Nin, H, xp, seg_in, per_in, part)) return -1;
@@ -140,14 +142,17 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
                    d->conv_w_dtype == VX27_BF16, d->A_log, d->dt_bias, act, z, gates};
     VX_LAUNCH(ctx, dn_in_epilogue, dim3((unsigned)((Nin + 255) / 256)), dim3(256), ea);
 
+    // q/k normalisation once per QK head (nv/nqk value heads share it)
+    if (vx_dn_qk_norm(ctx, B, d->nqk, VX27_DN_PRE_RMS | VX27_DN_PRE_L2, act, act + qd, (size_t)C, d->norm_w))
+        return -1;
     DnArgs ra = {};
     ra.B = B; ra.nqk = d->nqk; ra.nv = nv; ra.steps = 1;
-    ra.flags = VX27_DN_PRE_RMS | VX27_DN_PRE_L2 | VX27_DN_OUT_GATE;
+    ra.flags = VX_DN_QK_READY | VX27_DN_OUT_GATE;
     ra.S = d->S;
     ra.q = act; ra.k = act + qd; ra.v = act + 2 * qd;
     ra.q_tok = ra.k_tok = ra.v_tok = (size_t)C;
     ra.gates = gates; ra.norm_w = d->norm_w; ra.z = z; ra.z_tok = (size_t)vd;
-    ra.out = nullptr; ra.out_tok = (size_t)vd; ra.out_packed = op;
+    ra.out = nullptr; ra.out_tok = (size_t)vd; ra.out_packed = op; ra.o_pre = o_pre;
     if (vx_dn_recurrence(ctx, ra)) return -1;
 
     if (vx_gemv_part(ctx, d->w_out, 1, H, vd, op, seg_out, per_out, part)) return -1;
