@@ -40,6 +40,30 @@ __device__ __forceinline__ void load_conv_w(const void *w, int bf16, size_t ch, 
         for (int t = 0; t < 4; t++) out[t] = p[t];
     }
 }
+// Sum of two per-lane doubles over all NW waves of the block (wave partials
+// added in wave order); every thread must call it (barrier inside).  slot is
+// private to one call site.
+template <int NW>
+__device__ __forceinline__ void block_sum2(double &u, double &v, double (*slot)[2]) {
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const double su = vx_wave_sum_f64(u), sv = vx_wave_sum_f64(v);
+    if (lane == 0) {
+        slot[wave][0] = su;
+        slot[wave][1] = sv;
+    }
+    __syncthreads();
+    double a0 = slot[0][0], a1 = slot[0][1];
+#pragma unroll
+    for (int w = 1; w < NW; w++) {
+        a0 = a0 + slot[w][0];
+        a1 = a1 + slot[w][1];
+    }
+    u = a0;
+    v = a1;
+}
+
+// Sum over the R adjacent lanes that share a state column (butterfly; every
+// lane of the group ends with the same bits since each add is commutative).
 }  // namespace
 
 // Internal flag: q and k are final (normalised and scaled as step_exact
@@ -70,11 +94,5 @@ struct DnArgs {
     float *o_pre;
 };
 
-// Normalise q and k in place for the recurrence, one workgroup per
-// (sequence, QK head, q|k): the chain rmsn(1+w) (PRE_RMS), l2norm and
-// 1/sqrt(hd) (PRE_L2), then step_exact's own l2norm and 1/sqrt(hd) on q.
-// q_tok/k_tok are the per-sequence strides; flags select the first two steps.
-int vx_dn_qk_norm(vx27_hip_ctx *ctx, int B, int nqk, unsigned flags, float *q, float *k, size_t tok_stride,
-                  const float *norm_w);
 // Launch the recurrence (one or more workgroups per (sequence, value head)).
 int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a);

@@ -48,30 +48,6 @@ __global__ __launch_bounds__(256) void dn_gate_kernel(int n, int nv, const float
 
 
 
-// Sum of two per-lane doubles over all NW waves of the block (wave partials
-// added in wave order); every thread must call it (barrier inside).  slot is
-// private to one call site.
-template <int NW>
-__device__ __forceinline__ void block_sum2(double &u, double &v, double (*slot)[2]) {
-    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const double su = vx_wave_sum_f64(u), sv = vx_wave_sum_f64(v);
-    if (lane == 0) {
-        slot[wave][0] = su;
-        slot[wave][1] = sv;
-    }
-    __syncthreads();
-    double a0 = slot[0][0], a1 = slot[0][1];
-#pragma unroll
-    for (int w = 1; w < NW; w++) {
-        a0 = a0 + slot[w][0];
-        a1 = a1 + slot[w][1];
-    }
-    u = a0;
-    v = a1;
-}
-
-// Sum over the R adjacent lanes that share a state column (butterfly; every
-// lane of the group ends with the same bits since each add is commutative).
 template <int R>
 __device__ __forceinline__ double part_sum(double x) {
 #pragma unroll
@@ -271,36 +247,6 @@ __global__ __launch_bounds__(HD / CS * R) void dn_decode_kernel(DnArgs a) {
     }
 }
 
-// q/k normalisation chain ahead of the recurrence: block (b, g, which) of
-// 128 lanes normalises q (which = 0) or k (which = 1) of QK head g in place.
-// Same operations and reduction order as the in-kernel chain.
-__global__ __launch_bounds__(HD) void dn_qk_norm_kernel(int nqk, unsigned flags, float *q, float *k, size_t tok,
-                                                       const float *norm_w) {
-    const int which = blockIdx.x & 1, g = (blockIdx.x >> 1) % nqk, b = (blockIdx.x >> 1) / nqk;
-    const int j = threadIdx.x;
-    __shared__ double s_red[3][2][2];
-    float *p = (which ? k : q) + (size_t)b * tok + (size_t)g * HD + j;
-    float x = *p;
-    const float qs = 1.0f / sqrtf((float)HD);
-    double unused = 0.0;
-    if (flags & VX27_DN_PRE_RMS) {
-        double s = (double)x * (double)x;
-        block_sum2<2>(s, unused, s_red[0]);
-        x = (x * (1.0f / sqrtf((float)(s / HD) + 1e-6f))) * (norm_w[j] + 1.0f);
-    }
-    if (flags & VX27_DN_PRE_L2) {
-        double s = (double)x * (double)x;
-        block_sum2<2>(s, unused, s_red[1]);
-        x = x * (1.0f / sqrtf((float)s + 1e-6f));
-        if (!which) x = x * qs;
-    }
-    double s = (double)x * (double)x;
-    block_sum2<2>(s, unused, s_red[2]);
-    x = x * (1.0f / sqrtf((float)s + 1e-6f));
-    if (!which) x = x * qs;
-    *p = x;
-}
-
 // Gated output norm of one step for column-split heads: one block of 128
 // lanes per (sequence, value head); out = rmsn_std(o)*norm_w * silu(z)
 // (vx27_qfwd.c:147-151) from the pre-norm outputs in o_pre.
@@ -344,12 +290,6 @@ __global__ __launch_bounds__(256) void dn_conv_kernel(ConvArgs a) {
 
 }  // namespace
 
-int vx_dn_qk_norm(vx27_hip_ctx *ctx, int B, int nqk, unsigned flags, float *q, float *k, size_t tok_stride,
-                  const float *norm_w) {
-    VX_LAUNCH(ctx, dn_qk_norm_kernel, dim3((unsigned)(B * nqk * 2)), dim3(HD), nqk, flags, q, k, tok_stride, norm_w);
-    return 0;
-}
-
 int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a) {
     VX_REQUIRE(!a.fused_conv || a.nv == a.nqk, "dn recurrence: fused conv needs nv == nqk");
     // Spread few heads over the 256 CUs: split each head's columns over CS
@@ -358,11 +298,14 @@ int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a) {
     // column's rows over R lanes of one workgroup.
     const int heads = a.B * a.nv;
     const bool gate = (a.flags & VX27_DN_OUT_GATE) != 0;
+    // (With the output gate, one workgroup per head keeps the norm in the
+    // kernel; splitting would need the dn_out_gate launch, which costs more
+    // than the split gains.)
     int CS = 1;
-    if (!a.fused_conv && (!gate || (a.steps == 1 && a.o_pre)))
+    if (!a.fused_conv && !gate)
         while (heads * CS < 512 && CS < 8) CS *= 2;
 #if defined(VX_DN_CS)
-    if (CS > 1) CS = VX_DN_CS;   // build-time override for tuning sweeps
+    if (CS > 1 || VX_DN_CS == 1) CS = VX_DN_CS;   // build-time override for tuning sweeps
 #endif
     const dim3 grid((unsigned)(heads * CS));
     switch (CS) {

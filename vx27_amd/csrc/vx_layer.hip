@@ -4,9 +4,11 @@
 // DeltaNet layer (vx27_qfwd.c:102-153), one decode token of B sequences:
 //   gemv_part(W_in)          [qkv | z | a | b] partial sums
 //   dn_in_epilogue           reduce + causal conv/SiLU on qkv (state in place),
-//                            z, decay from a, beta from b
-//   dn_decode_kernel         rmsn(1+w), l2norm, exact step, gated output norm
-//   pack_x(o) + gemv_part(W_out) + reduce   -> out
+//                            the q/k normalisation chain, z, decay from a,
+//                            beta from b
+//   dn_decode_kernel         exact step on the final q/k, gated output norm,
+//                            output written as the packed operand of W_out
+//   gemv_part(W_out) + reduce   -> out
 // Gated GQA layer (vx27_qfwd.c:162-213):
 //   gemv_part(W_qkv) + reduce  -> [q|gate interleaved | k | v]
 //   gqa_prep / gqa_split / gqa_combine (vx_gqa_decode.hip)
@@ -24,22 +26,58 @@ size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct DnInArgs {
     const float *part;
-    int N, B, n_pseg, C, vd, nv;
+    int N, B, n_pseg, C, vd, nv, nqk;
     float *conv_state;
     const void *conv_w;
     int conv_bf16;
-    const float *A_log, *dt_bias;
+    const float *A_log, *dt_bias, *norm_w;
     float *act, *z;
     double2 *gates;
 };
 
-// one thread per row n of the stacked input projection, all sequences
-__global__ __launch_bounds__(256) void dn_in_epilogue(DnInArgs a) {
-    const int n = blockIdx.x * blockDim.x + threadIdx.x;
-    if (n >= a.N) return;
+// One block of 128 lanes per 128-row group of the stacked input projection
+// (one row per lane, all sequences): the split-K sum, then
+//   q|k|v rows: causal conv + SiLU (conv state in place); the q and k groups
+//               are whole heads, and run the normalisation chain of
+//               vx27_qfwd.c:119-130 plus step_exact's own (vx27_deltanet.c:
+//               77-80): rmsn(1+w), l2norm (q /= sqrt(hd)), l2norm (q /= sqrt(hd))
+//   z rows:     copied out; a rows: decay = exp(g_log); b rows: beta
+__global__ __launch_bounds__(HD) void dn_in_epilogue(DnInArgs a) {
+    const int n = blockIdx.x * HD + threadIdx.x;
+    const bool live = n < a.N;
     float v[5];
-    vx_gemv_sum_row(a.part, a.N, a.B, a.n_pseg, n, v);
-    if (n < a.C) {                       // q|k|v channel: causal conv + SiLU
+    if (live) vx_gemv_sum_row(a.part, a.N, a.B, a.n_pseg, live ? n : 0, v);
+    const int qd = a.nqk * HD;
+    if ((int)blockIdx.x < 2 * a.nqk) {   // a q or k head: conv, then the norm chain per sequence
+        __shared__ double s_red[3][2][2];
+        float w[4];
+        load_conv_w(a.conv_w, a.conv_bf16, (size_t)n, w);
+        const bool is_q = n < qd;
+        const float nw = a.norm_w[threadIdx.x] + 1.0f;
+        const float qs = 1.0f / sqrtf((float)HD);
+        for (int b = 0; b < a.B; b++) {
+            float st[3];
+            float *sp = a.conv_state + ((size_t)b * a.C + n) * 3;
+            st[0] = sp[0]; st[1] = sp[1]; st[2] = sp[2];
+            float x = conv_step(st, w, v[b]);
+            sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
+            double unused = 0.0, ss = (double)x * (double)x;
+            block_sum2<2>(ss, unused, s_red[0]);
+            x = (x * (1.0f / sqrtf((float)(ss / HD) + 1e-6f))) * nw;
+            ss = (double)x * (double)x;
+            block_sum2<2>(ss, unused, s_red[1]);
+            x = x * (1.0f / sqrtf((float)ss + 1e-6f));
+            if (is_q) x = x * qs;
+            ss = (double)x * (double)x;
+            block_sum2<2>(ss, unused, s_red[2]);
+            x = x * (1.0f / sqrtf((float)ss + 1e-6f));
+            if (is_q) x = x * qs;
+            a.act[(size_t)b * a.C + n] = x;
+        }
+        return;
+    }
+    if (!live) return;
+    if (n < a.C) {                       // v channel: causal conv + SiLU
         float w[4];
         load_conv_w(a.conv_w, a.conv_bf16, (size_t)n, w);
         for (int b = 0; b < a.B; b++) {
@@ -123,9 +161,8 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     const size_t act_b = align256((size_t)B * C * 4), z_b = align256((size_t)B * vd * 4);
     const size_t g_b = align256((size_t)B * nv * sizeof(double2));
     const size_t pk_o = align256(vx_pack_bytes(vd));
-    const size_t opre_b = align256((size_t)B * vd * 4);
     void *scr;
-    if (vx_ctx_scratch(ctx, pk_x + part_b + act_b + z_b + g_b + pk_o + opre_b, &scr)) return -1;
+    if (vx_ctx_scratch(ctx, pk_x + part_b + act_b + z_b + g_b + pk_o, &scr)) return -1;
     char *p = (char *)scr;
     uint16_t *xp = d->x_packed ? (uint16_t *)d->x_packed : (uint16_t *)p;
     p += pk_x;
@@ -133,18 +170,14 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     float *act = (float *)p; p += act_b;
     float *z = (float *)p; p += z_b;
     double2 *gates = (double2 *)p; p += g_b;
-    uint16_t *op = (uint16_t *)p; p += pk_o;
-    float *o_pre = (float *)p;
+    uint16_t *op = (uint16_t *)p;
 
     if (!d->x_packed && vx_pack(ctx, d->x, (size_t)H, B, H, xp)) return -1;
     if (vx_gemv_part(ctx, d->w_in, 1, Nin, H, xp, seg_in, per_in, part)) return -1;
-    DnInArgs ea = {part, Nin, B, vx_gemv_pseg(seg_in), C, vd, nv, d->conv_state, d->conv_w,
-                   d->conv_w_dtype == VX27_BF16, d->A_log, d->dt_bias, act, z, gates};
-    VX_LAUNCH(ctx, dn_in_epilogue, dim3((unsigned)((Nin + 255) / 256)), dim3(256), ea);
+    DnInArgs ea = {part, Nin, B, vx_gemv_pseg(seg_in), C, vd, nv, d->nqk, d->conv_state, d->conv_w,
+                   d->conv_w_dtype == VX27_BF16, d->A_log, d->dt_bias, d->norm_w, act, z, gates};
+    VX_LAUNCH(ctx, dn_in_epilogue, dim3((unsigned)((Nin + HD - 1) / HD)), dim3(HD), ea);
 
-    // q/k normalisation once per QK head (nv/nqk value heads share it)
-    if (vx_dn_qk_norm(ctx, B, d->nqk, VX27_DN_PRE_RMS | VX27_DN_PRE_L2, act, act + qd, (size_t)C, d->norm_w))
-        return -1;
     DnArgs ra = {};
     ra.B = B; ra.nqk = d->nqk; ra.nv = nv; ra.steps = 1;
     ra.flags = VX_DN_QK_READY | VX27_DN_OUT_GATE;
@@ -152,7 +185,7 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     ra.q = act; ra.k = act + qd; ra.v = act + 2 * qd;
     ra.q_tok = ra.k_tok = ra.v_tok = (size_t)C;
     ra.gates = gates; ra.norm_w = d->norm_w; ra.z = z; ra.z_tok = (size_t)vd;
-    ra.out = nullptr; ra.out_tok = (size_t)vd; ra.out_packed = op; ra.o_pre = o_pre;
+    ra.out = nullptr; ra.out_tok = (size_t)vd; ra.out_packed = op;
     if (vx_dn_recurrence(ctx, ra)) return -1;
 
     if (vx_gemv_part(ctx, d->w_out, 1, H, vd, op, seg_out, per_out, part)) return -1;
