@@ -240,12 +240,13 @@ int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const
                        size_t x_stride, int B, float *y, size_t y_stride);
 
 /* Weight tiling for the layer entry points: row-major bf16 W [N][K] into the
- * MFMA tile layout [K/32][N/16][64 lanes][8] (lane (g,m) of tile (s, rb)
- * holds W[16rb + m][32s + 8g .. 8g+7]): each wave loads 1 KiB of contiguous
- * weights per tile, and the row blocks of one k-step are adjacent, so the
- * workgroups of a launch stream one contiguous band at a time.  Done once
- * per weight, like the reference's offline forge of its packed weight format
- * (src/vx_forge.c). */
+ * MFMA tile layout [K/(32*KG)][N/16][KG][64 lanes][8], KG = 4 k-steps when
+ * K/32 is a multiple of 4 (else 2 or 1); lane (g,m) of tile (k-step s, row
+ * block rb) holds W[16rb + m][32s + 8g .. 8g+7].  Each wave loads 1 KiB of
+ * contiguous weights per tile, a row block's KG k-steps are adjacent, and
+ * the row blocks of one k-group are adjacent, so a launch streams long
+ * contiguous runs.  Done once per weight, like the reference's offline forge
+ * of its packed weight format (src/vx_forge.c). */
 int vx27_hip_pack_weights_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, uint16_t *W_tiled);
 
 /* The mixer of one Gated DeltaNet layer for one decode token of B <= 5

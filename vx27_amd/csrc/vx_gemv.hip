@@ -16,13 +16,15 @@
 // Layouts:
 //   packed activations  [K/32 k-steps][64 lanes][8] bf16: lane (g,n) of k-step
 //                       s holds part n/B of vector n%B at k = 32s + 8g + 0..7
-//   tiled weights       [K/32 k-steps][N/16 row blocks][64 lanes][8] bf16:
-//                       lane (g,m) holds W[16*rb + m][32s + 8g + 0..7], so a
-//                       wave's A operand is 1 KiB of contiguous memory and
-//                       the 4 row blocks of a workgroup at one k-step are
-//                       4 KiB contiguous; workgroups moving together read one
-//                       contiguous band of W (vx27_hip_pack_weights_bf16
-//                       converts row-major W)
+//   tiled weights       [K/(32 KG) k-groups][N/16 row blocks][KG][64 lanes][8]
+//                       bf16 (KG = 4 k-steps when K/32 allows): lane (g,m) of
+//                       tile (s, rb) holds W[16*rb + m][32s + 8g + 0..7].  A
+//                       wave's A operand is 1 KiB contiguous, a row block's KG
+//                       k-steps are adjacent, and so are the row blocks of a
+//                       workgroup: one wave's batch of KG k-steps over its 4
+//                       row blocks is one 16 KiB run, and neighbouring
+//                       workgroups read neighbouring runs
+//                       (vx27_hip_pack_weights_bf16 converts row-major W)
 //
 // gemv_part: a workgroup of 4 waves owns 64 rows (4 row blocks); its waves
 // take 4 consecutive K segments and are combined in LDS, so one partial
@@ -42,11 +44,7 @@ constexpr int RB = 4;   // 16-row MFMA blocks per workgroup
 #ifndef VX_GEMV_MINKS
 #define VX_GEMV_MINKS 8      // at least this many 32-wide k-steps per wave
 #endif
-#ifndef VX_GEMV_UNROLL
-#define VX_GEMV_UNROLL 4     // k-steps in flight per wave (x RB loads each)
-#endif
-#define VX_PRAGMA(x) _Pragma(#x)
-#define VX_UNROLL(n) VX_PRAGMA(unroll n)
+
 
 // pack activations: grid (K/32), block 64; lane (g,n) writes its 8 elements
 __global__ __launch_bounds__(64) void pack_x(const float *x, size_t x_stride, int B, uint16_t *out) {
@@ -66,12 +64,30 @@ __global__ __launch_bounds__(64) void pack_x(const float *x, size_t x_stride, in
     *(uint4 *)(out + ((size_t)s * 64 + lane) * 8) = w;
 }
 
+#ifndef VX_GEMV_KG
+#define VX_GEMV_KG 1         // k-steps per group of the tiled layout (1, 2 or 4)
+#endif
+#ifndef VX_GEMV_U
+#define VX_GEMV_U 1          // k-steps per load batch of a wave
+#endif
+#ifndef VX_GEMV_STRIDED
+#define VX_GEMV_STRIDED 0    // K segments interleaved (segment s: k-steps s, s + n_seg, ...)
+#endif
+// k-steps per group of the tiled weight layout
+__host__ __device__ __forceinline__ int gemv_kg(int K) {
+    const int nks = K / 32;
+    return nks % VX_GEMV_KG == 0 ? VX_GEMV_KG : 1;
+}
+// element offset of tile (k-step s, row block rb) in the tiled layout
+__device__ __forceinline__ size_t tile_off(int s, int rb, int nb, int kg) {
+    return ((size_t)(s / kg) * nb + rb) * kg * 512 + (size_t)(s % kg) * 512;
+}
+
 // row-major W [N][K] -> tiled; grid (N/16, K/32), block 64
 __global__ __launch_bounds__(64) void pack_w(const uint16_t *W, int K, uint16_t *Wt) {
     const int rb = blockIdx.x, s = blockIdx.y, lane = threadIdx.x, g = lane >> 4, m = lane & 15;
-    const int nb = gridDim.x;
     const uint4 v = *(const uint4 *)(W + (size_t)(16 * rb + m) * K + 32 * s + 8 * g);
-    *(uint4 *)(Wt + (((size_t)s * nb + rb) * 64 + lane) * 8) = v;
+    *(uint4 *)(Wt + tile_off(s, rb, gridDim.x, gemv_kg(K)) + lane * 8) = v;
 }
 
 // grid (ceil(N/64), ceil(n_seg/4)), block 256; wave w: K segment 4*blockIdx.y + w
@@ -93,20 +109,49 @@ __global__ __launch_bounds__(256) void gemv_part_k(const uint16_t *W, int N, int
     for (int r = 0; r < RB; r++) {
         live[r] = (rb0 + r) * 16 < N;          // whole 16-row block in or out (N % 16 == 0)
         const int rb = live[r] ? rb0 + r : 0;
-        wp[r] = TILED ? W + ((size_t)rb * 64 + lane) * 8
+        wp[r] = TILED ? W + tile_off(0, rb, N / 16, gemv_kg(K)) + lane * 8
                       : W + (size_t)(16 * rb + m) * K + 8 * g;
     }
     const bf16x8_t *xb = (const bf16x8_t *)xp + lane;
-    VX_UNROLL(VX_GEMV_UNROLL)
-    for (int s = s0; s < s1; s++) {
+    // k-steps of this wave: a contiguous segment [s0, s1), or (strided) the
+    // k-steps seg, seg + n_seg, ...; loads of U k-steps are issued before the
+    // first MFMA of the batch consumes them
+    constexpr int U = VX_GEMV_U;
+    const int kg = TILED ? gemv_kg(K) : 1;
+    const size_t gstride = (size_t)(N / 16) * kg * 512;
+    auto woff = [&](int st) -> size_t {
+        return TILED ? (size_t)(st / kg) * gstride + (size_t)(st % kg) * 512 : (size_t)st * 32;
+    };
+    const int sbeg = VX_GEMV_STRIDED ? (seg < n_seg ? seg : nks) : s0;
+    const int send = VX_GEMV_STRIDED ? nks : s1;
+    const int sinc = VX_GEMV_STRIDED ? n_seg : 1;
+    int s = sbeg;
+    for (; s + (U - 1) * sinc < send; s += U * sinc) {
+        bf16x8_t bop[U], aop[U][RB];
+#pragma unroll
+        for (int u = 0; u < U; u++) {
+            const int st = s + u * sinc;
+            bop[u] = xb[(size_t)st * 64];
+            const size_t off = woff(st);
+#pragma unroll
+            for (int r = 0; r < RB; r++) aop[u][r] = *(const bf16x8_t *)(wp[r] + off);
+        }
+        // dead row blocks (past N in the last workgroup) multiply row block 0
+        // and are never stored: no branch in the streaming loop
+#pragma unroll
+        for (int u = 0; u < U; u++)
+#pragma unroll
+            for (int r = 0; r < RB; r++)
+                acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[u][r], bop[u], acc[r], 0, 0, 0);
+    }
+    for (; s < send; s += sinc) {
         const bf16x8_t bop = xb[(size_t)s * 64];
+        const size_t off = woff(s);
         bf16x8_t aop[RB];
 #pragma unroll
-        for (int r = 0; r < RB; r++)
-            aop[r] = *(const bf16x8_t *)(TILED ? wp[r] + (size_t)s * (N / 16) * 512 : wp[r] + 32 * s);
+        for (int r = 0; r < RB; r++) aop[r] = *(const bf16x8_t *)(wp[r] + off);
 #pragma unroll
-        for (int r = 0; r < RB; r++)
-            if (live[r]) acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[r], bop, acc[r], 0, 0, 0);
+        for (int r = 0; r < RB; r++) acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[r], bop, acc[r], 0, 0, 0);
     }
 #pragma unroll
     for (int r = 0; r < RB; r++) red[wave][r][lane] = acc[r];
@@ -148,6 +193,8 @@ int vx_gemv_plan(int N, int K, int *n_seg, int *ks_per) {
     if (seg > nks / VX_GEMV_MINKS) seg = nks / VX_GEMV_MINKS;
     if (seg < 1) seg = 1;
     int per = (nks + seg - 1) / seg;
+    const int kg = gemv_kg(K);
+    per = (per + kg - 1) / kg * kg;   // segments start at k-group boundaries
     seg = (nks + per - 1) / per;
     *n_seg = seg;
     *ks_per = per;
