@@ -78,7 +78,7 @@ __global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
     const int nvalid = min(CH, p.T - t0);
 
     __shared__ float kn_f[CH][KP];        // kn (fp32); later -W
-    __shared__ uint16_t qn_b[CH][QP];     // qn (bf16); later P (bf16, row stride PP)
+    __shared__ uint16_t qn_b[CH][QP];     // qn (bf16); later P (bf16, row stride PP); later v
     __shared__ float A_s[CH][CH];
     __shared__ double gam_s[CH];
     __shared__ float beta_s[CH], eg_s[CH], egc_s[CH];   // beta, e^gam_t, e^(gam_C - gam_t)
@@ -105,27 +105,70 @@ __global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
         egc_s[lane] = (float)exp(sC - s);
     }
 
-    // q, k rows of this wave's 16 tokens: lane holds dims 2l, 2l+1
+    // q and k rows, one token per lane (wave 1: k, wave 2: q): the lane reads
+    // its token's 256 bytes and sums the squares itself, so no cross-lane
+    // reduction is needed
     const float qscale = 1.0f / sqrtf((float)HD);
-    for (int r = 0; r < 16; r++) {
-        const int t = wave * 16 + r;
-        float k0 = 0.f, k1 = 0.f, q0 = 0.f, q1 = 0.f;
-        if (t < nvalid) {
-            const size_t row = ((size_t)b * p.T + t0 + t) * p.nqk + qh;
-            const uint32_t kw = *(const uint32_t *)(p.k + row * HD + 2 * lane);
-            const uint32_t qw = *(const uint32_t *)(p.q + row * HD + 2 * lane);
-            k0 = vx_bf16_to_f32((uint16_t)kw);
-            k1 = vx_bf16_to_f32((uint16_t)(kw >> 16));
-            q0 = vx_bf16_to_f32((uint16_t)qw);
-            q1 = vx_bf16_to_f32((uint16_t)(qw >> 16));
+    uint4 vrow[16];   // wave 3: v row of token `lane`, parked in LDS once qn_b is free
+    if (wave == 3) {
+        if (lane < nvalid) {
+            const uint16_t *src = p.v + (((size_t)b * p.T + t0 + lane) * p.nv + vh) * HD;
+#pragma unroll
+            for (int j = 0; j < 16; j++) vrow[j] = *(const uint4 *)(src + 8 * j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; j++) vrow[j] = make_uint4(0u, 0u, 0u, 0u);
         }
-        const double ssk = vx_wave_sum_f64((double)k0 * k0 + (double)k1 * k1);
-        const double ssq = vx_wave_sum_f64((double)q0 * q0 + (double)q1 * q1);
-        const float ik = 1.0f / sqrtf((float)ssk + 1e-6f);
-        const float iq = 1.0f / sqrtf((float)ssq + 1e-6f);
-        kn_f[t][2 * lane] = k0 * ik;
-        kn_f[t][2 * lane + 1] = k1 * ik;
-        *(uint32_t *)&qn_b[t][2 * lane] = pack2((q0 * iq) * qscale, (q1 * iq) * qscale);
+    }
+    if (wave == 1 || wave == 2) {
+        const int t = lane;
+        uint4 raw[16];
+        if (t < nvalid) {
+            const uint16_t *src = (wave == 1 ? p.k : p.q) + (((size_t)b * p.T + t0 + t) * p.nqk + qh) * HD;
+#pragma unroll
+            for (int j = 0; j < 16; j++) raw[j] = *(const uint4 *)(src + 8 * j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; j++) raw[j] = make_uint4(0u, 0u, 0u, 0u);
+        }
+        double ss = 0.0;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const double lo = (double)vx_bf16_to_f32((uint16_t)w4[e]);
+                const double hi = (double)vx_bf16_to_f32((uint16_t)(w4[e] >> 16));
+                ss = ss + lo * lo;
+                ss = ss + hi * hi;
+            }
+        }
+        const float inv = 1.0f / sqrtf((float)ss + 1e-6f);
+        if (wave == 1) {
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+                float f[8];
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    f[2 * e] = vx_bf16_to_f32((uint16_t)w4[e]) * inv;
+                    f[2 * e + 1] = vx_bf16_to_f32((uint16_t)(w4[e] >> 16)) * inv;
+                }
+                *(float4 *)&kn_f[t][8 * j] = make_float4(f[0], f[1], f[2], f[3]);
+                *(float4 *)&kn_f[t][8 * j + 4] = make_float4(f[4], f[5], f[6], f[7]);
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+                uint32_t o4[4];
+#pragma unroll
+                for (int e = 0; e < 4; e++)
+                    o4[e] = pack2((vx_bf16_to_f32((uint16_t)w4[e]) * inv) * qscale,
+                                  (vx_bf16_to_f32((uint16_t)(w4[e] >> 16)) * inv) * qscale);
+                *(uint4 *)&qn_b[t][8 * j] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
+            }
+        }
     }
     __syncthreads();
 
@@ -195,6 +238,12 @@ __global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
         const uint4 v = *(const uint4 *)&P_b[rowA * PP + 32 * ks + 8 * g];
         *(uint4 *)(rec + R_P + ((size_t)(wave * 2 + ks) * 64 + lane) * 16) = v;
     }
+    __syncthreads();   // P is read out; qn_b now holds v (bf16 rows)
+    if (wave == 3) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) *(uint4 *)&qn_b[lane][8 * j] = vrow[j];
+    }
+    __syncthreads();
 
     // forward substitution x = (I + A)^-1 rhs, one column per thread:
     // columns 0..127 of beta V (-> Ut), 128..255 of beta e^gam K (-> W)
@@ -202,26 +251,41 @@ __global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
     if (tid < HD) {
 #pragma unroll
         for (int t = 0; t < CH; t++) {
-            float vv = 0.0f;
-            if (t < nvalid) vv = vx_bf16_to_f32(p.v[(((size_t)b * p.T + t0 + t) * p.nv + vh) * HD + tid]);
-            x[t] = beta_s[t] * vv;
+            x[t] = beta_s[t] * vx_bf16_to_f32(qn_b[t][tid]);
         }
     } else {
 #pragma unroll
         for (int t = 0; t < CH; t++) x[t] = (beta_s[t] * eg_s[t]) * kn_f[t][tid - HD];
     }
+    // blocked forward substitution over four 16-row blocks: first the rows of
+    // a block against every earlier block (four independent partial sums per
+    // row, so the rows proceed in parallel), then the 16-row triangle
 #pragma unroll
-    for (int i = 1; i < CH; i++) {
-        float acc = x[i];
+    for (int blk = 0; blk < 4; blk++) {
+        if (blk > 0) {
 #pragma unroll
-        for (int k4 = 0; k4 < i; k4 += 4) {
-            const float4 a4 = *(const float4 *)&A_s[i][k4];   // A[i][k] = 0 for k >= i
-            acc -= a4.x * x[k4];
-            if (k4 + 1 < CH) acc -= a4.y * x[k4 + 1];
-            if (k4 + 2 < CH) acc -= a4.z * x[k4 + 2];
-            if (k4 + 3 < CH) acc -= a4.w * x[k4 + 3];
+            for (int ii = 0; ii < 16; ii++) {
+                const int i = 16 * blk + ii;
+                float a0 = x[i], a1 = 0.f, a2 = 0.f, a3 = 0.f;
+#pragma unroll
+                for (int k4 = 0; k4 < 16 * blk; k4 += 4) {
+                    const float4 a4 = *(const float4 *)&A_s[i][k4];
+                    a0 -= a4.x * x[k4];
+                    a1 -= a4.y * x[k4 + 1];
+                    a2 -= a4.z * x[k4 + 2];
+                    a3 -= a4.w * x[k4 + 3];
+                }
+                x[i] = (a0 + a1) + (a2 + a3);
+            }
         }
-        x[i] = acc;
+#pragma unroll
+        for (int ii = 1; ii < 16; ii++) {
+            const int i = 16 * blk + ii;
+            float acc = x[i];
+#pragma unroll
+            for (int k = 16 * blk; k < i; k++) acc -= A_s[i][k] * x[k];
+            x[i] = acc;
+        }
     }
     if (tid < HD) {
         // Ut column tid in C-layout tiles [rb][cs][lane (g,n)][i]
