@@ -47,7 +47,8 @@ constexpr size_t R_QE = R_NW + 4 * 4 * 512 * 2;  // e^gam qn  [4][4][64][8] bf16
 constexpr size_t R_KT = R_QE + 4 * 4 * 512 * 2;  // Kt^T [8][2][64][8] bf16
 constexpr size_t R_P = R_KT + 8 * 2 * 512 * 2;   // P    [4][2][64][8] bf16
 constexpr size_t R_UT = R_P + 4 * 2 * 512 * 2;   // Ut   [4 rb][8 cs][64][4] fp32
-constexpr size_t REC = R_UT + 4 * 8 * 64 * 4 * 4;
+constexpr size_t R_GC = R_UT + 4 * 8 * 64 * 4 * 4; // e^gam_C, one float
+constexpr size_t REC = R_GC + 256;
 
 struct PrepArgs {
     int T, nqk, nv, NC;
@@ -174,7 +175,7 @@ __global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
 
     char *rec = p.rec + (((size_t)b * p.nv + vh) * p.NC + c) * REC;
     const double gamC = gam_s[CH - 1];
-    if (tid == 0) p.gC[((size_t)b * p.nv + vh) * p.NC + c] = (float)exp(gamC);
+    if (tid == 0) *(float *)(rec + R_GC) = (float)exp(gamC);
 
     // K K^T and Q K^T for row block `wave`; Qe tiles on the way
     floatx4_t acck[4], accq[4];
@@ -319,6 +320,7 @@ struct ScanArgs {
 struct ChunkOps {
     uint4 nw[4], qe[4], kt[4], pp[2];
     float4 ut;
+    float gc;
 };
 
 __device__ __forceinline__ void load_ops(ChunkOps &o, const char *rec, int wave, int lane, int slice) {
@@ -334,6 +336,7 @@ __device__ __forceinline__ void load_ops(ChunkOps &o, const char *rec, int wave,
     for (int ks = 0; ks < 2; ks++)
         o.pp[ks] = *(const uint4 *)(rec + R_P + ((size_t)(wave * 2 + ks) * 64 + lane) * 16);
     o.ut = *(const float4 *)(rec + R_UT + (((size_t)wave * 8 + slice) * 64 + lane) * 16);
+    o.gc = *(const float *)(rec + R_GC);
 }
 
 __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
@@ -362,10 +365,9 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
         for (int i = 0; i < 4; i++) S[r][i] = Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + col];
 
     const char *rec0 = p.rec + ((size_t)b * p.nv + vh) * p.NC * REC;
-    const float *gC = p.gC + ((size_t)b * p.nv + vh) * p.NC;
-    ChunkOps cur, nxt;
-    load_ops(cur, rec0, wave, lane, slice);
-    for (int c = 0; c < p.NC; c++) {
+    // one chunk from `cur` while the next chunk's operands load into `nxt`;
+    // unrolled by two with the operand sets swapping roles (no copies)
+    auto step = [&](int c, const ChunkOps &cur, ChunkOps &nxt) {
         if (c + 1 < p.NC) load_ops(nxt, rec0 + (size_t)(c + 1) * REC, wave, lane, slice);
         // S (bf16) -> LDS as [column][key dim]
 #pragma unroll
@@ -377,36 +379,49 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
         bf16x8_t sb[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) sb[ks] = as_bf16x8(*(const uint4 *)&S_l[n][32 * ks + 8 * g]);
-        // U = Ut - W S for tokens 16w .. 16w+15
-        floatx4_t U = (floatx4_t){cur.ut.x, cur.ut.y, cur.ut.z, cur.ut.w};
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) U = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.nw[ks]), sb[ks], U, 0, 0, 0);
+        // U = Ut - W S for tokens 16w .. 16w+15, and the e^gam Q S part of O,
+        // as independent two-MFMA chains (the dependent-MFMA latency, not the
+        // issue rate, bounds this loop)
+        floatx4_t U0 = (floatx4_t){cur.ut.x, cur.ut.y, cur.ut.z, cur.ut.w}, U1 = {0.f, 0.f, 0.f, 0.f};
+        floatx4_t O0 = {0.f, 0.f, 0.f, 0.f}, O1 = {0.f, 0.f, 0.f, 0.f};
+        U0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.nw[0]), sb[0], U0, 0, 0, 0);
+        U1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.nw[1]), sb[1], U1, 0, 0, 0);
+        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.qe[0]), sb[0], O0, 0, 0, 0);
+        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.qe[1]), sb[1], O1, 0, 0, 0);
+        U0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.nw[2]), sb[2], U0, 0, 0, 0);
+        U1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.nw[3]), sb[3], U1, 0, 0, 0);
+        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.qe[2]), sb[2], O0, 0, 0, 0);
+        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.qe[3]), sb[3], O1, 0, 0, 0);
+        const floatx4_t U = U0 + U1;
         *(uint2 *)&U_l[n][wave * 16 + 4 * g] = make_uint2(pack2(U[0], U[1]), pack2(U[2], U[3]));
         __syncthreads();
         bf16x8_t ub[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) ub[ks] = as_bf16x8(*(const uint4 *)&U_l[n][32 * ks + 8 * g]);
-        // O = (e^gam Q) S + P U
-        floatx4_t O = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+        // O += P U (two more independent MFMAs), then the two chains merge
+        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.pp[0]), ub[0], O0, 0, 0, 0);
+        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.pp[1]), ub[1], O1, 0, 0, 0);
+        // S = e^gam_C S + Kt^T U: per row block, two independent MFMAs
+        const float gc = cur.gc;
 #pragma unroll
-        for (int ks = 0; ks < 4; ks++) O = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.qe[ks]), sb[ks], O, 0, 0, 0);
-#pragma unroll
-        for (int ks = 0; ks < 2; ks++) O = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.pp[ks]), ub[ks], O, 0, 0, 0);
+        for (int r = 0; r < 2; r++) {
+            floatx4_t Sa = S[r] * gc, Sb = {0.f, 0.f, 0.f, 0.f};
+            Sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.kt[2 * r]), ub[0], Sa, 0, 0, 0);
+            Sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.kt[2 * r + 1]), ub[1], Sb, 0, 0, 0);
+            S[r] = Sa + Sb;
+        }
+        const floatx4_t O = O0 + O1;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int t = c * CH + wave * 16 + 4 * g + i;
             if (t < p.T) p.out[(((size_t)b * p.T + t) * p.nv + vh) * HD + col] = O[i];
         }
-        // S = e^gam_C S + Kt^T U
-        const float gc = gC[c];
-#pragma unroll
-        for (int r = 0; r < 2; r++) {
-            S[r] *= gc;
-#pragma unroll
-            for (int ks = 0; ks < 2; ks++)
-                S[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.kt[2 * r + ks]), ub[ks], S[r], 0, 0, 0);
-        }
-        cur = nxt;
+    };
+    ChunkOps opa, opb;
+    load_ops(opa, rec0, wave, lane, slice);
+    for (int c = 0; c < p.NC; c += 2) {
+        step(c, opa, opb);
+        if (c + 1 < p.NC) step(c + 1, opb, opa);
     }
 #pragma unroll
     for (int r = 0; r < 2; r++)
