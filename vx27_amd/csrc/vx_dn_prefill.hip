@@ -22,13 +22,16 @@
 //           chunks in order; a workgroup owns 16 value columns of one head's
 //           state (columns are independent in all three products), keeps
 //           them in MFMA accumulators and runs 14 MFMAs per wave per chunk.
-//           The 8 slices of a head are placed on one XCD so the records they
+//           Each wave streams its own operand tiles of the chunk two ahead
+//           straight into LDS (two slots, explicit vmcnt waits, no barrier
+//           for the hand-off).  The 8 slices of a head are placed on one XCD so the records they
 //           share are read from HBM once.
 //
 // Operand tiles ([rows/16][k/32][64 lanes][8] bf16) follow the MFMA operand
 // layout of v_mfma_f32_16x16x32_bf16: lane (g = l/16, m = l%16) of an A tile
 // holds A[m][8g..8g+7]; a wave's tile is 1 KiB of contiguous memory.
 #include "vx_dn.h"
+#include "vx_lds.h"
 
 namespace {
 
@@ -59,8 +62,13 @@ struct PrepArgs {
     float *gC;                       // [B][nv][NC] e^gam_C
 };
 
+// round-to-nearest-even pair (v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack2(float x, float y) {
-    return (uint32_t)vx_f32_to_bf16(x) | ((uint32_t)vx_f32_to_bf16(y) << 16);
+    typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+    const bf16x2_t v = (bf16x2_t){(__bf16)x, (__bf16)y};
+    uint32_t r;
+    __builtin_memcpy(&r, &v, 4);
+    return r;
 }
 __device__ __forceinline__ uint4 pack8(const float *f) {
     return make_uint4(pack2(f[0], f[1]), pack2(f[2], f[3]), pack2(f[4], f[5]), pack2(f[6], f[7]));
@@ -320,27 +328,52 @@ struct ScanArgs {
 struct ChunkOps {
     uint4 nw[4], qe[4], kt[4], pp[2];
     float4 ut;
-    float gc;
 };
 
-__device__ __forceinline__ void load_ops(ChunkOps &o, const char *rec, int wave, int lane, int slice) {
+// A wave's operands of one chunk: 15 tiles of 1 KiB in its record, staged in
+// LDS in this order: -W (rows 16w..16w+15, 4 k-steps), e^gam Q (same rows),
+// Kt^T (row blocks 2w, 2w+1, 2 k-steps each), P (rows 16w.., 2 k-steps) and
+// the wave's Ut block of the slice; then the record's last 256 bytes, whose
+// first float is e^gam_C.
+constexpr int OPS_TILES = 15;
+constexpr int OPS_LOADS = OPS_TILES + 1;   // load instructions per wave and chunk
+constexpr uint32_t OPS_WAVE = OPS_TILES * 1024 + 256;
+constexpr uint32_t OPS_BUF = 4 * OPS_WAVE;
+
+__device__ __forceinline__ uint32_t ops_src(int j, int wave, int slice) {
+    return j < 4    ? (uint32_t)(R_NW + (wave * 4 + j) * 1024)
+           : j < 8  ? (uint32_t)(R_QE + (wave * 4 + j - 4) * 1024)
+           : j < 12 ? (uint32_t)(R_KT + (wave * 4 + j - 8) * 1024)
+           : j < 14 ? (uint32_t)(R_P + (wave * 2 + j - 12) * 1024)
+                    : (uint32_t)(R_UT + (wave * 8 + slice) * 1024);
+}
+
+// Starts the wave's 15 direct-to-LDS tile loads of record `rec` into its
+// slot at LDS address `lds`.  Each wave reads back only what it loaded
+// itself, so the hand-off needs this wave's vmcnt wait and no barrier.
+__device__ __forceinline__ void fetch_ops(const char *rec, uint32_t lds, int wave, int slice, int lane) {
+#pragma unroll
+    for (int j = 0; j < OPS_TILES; j++)
+        vx_dma16(rec, ops_src(j, wave, slice) + (uint32_t)lane * 16, lds + (uint32_t)j * 1024);
+    vx_dma4(rec, (uint32_t)R_GC + (uint32_t)lane * 4, lds + OPS_TILES * 1024);
+}
+
+__device__ __forceinline__ void read_ops(ChunkOps &o, const uint4 *t) {
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
-        o.nw[ks] = *(const uint4 *)(rec + R_NW + ((size_t)(wave * 4 + ks) * 64 + lane) * 16);
-        o.qe[ks] = *(const uint4 *)(rec + R_QE + ((size_t)(wave * 4 + ks) * 64 + lane) * 16);
+        o.nw[ks] = t[ks * 64];
+        o.qe[ks] = t[(4 + ks) * 64];
+        o.kt[ks] = t[(8 + ks) * 64];
     }
-#pragma unroll
-    for (int j = 0; j < 4; j++)   // Kt^T tiles (rb 2w + j/2, ks j%2)
-        o.kt[j] = *(const uint4 *)(rec + R_KT + ((size_t)(wave * 4 + j) * 64 + lane) * 16);
-#pragma unroll
-    for (int ks = 0; ks < 2; ks++)
-        o.pp[ks] = *(const uint4 *)(rec + R_P + ((size_t)(wave * 2 + ks) * 64 + lane) * 16);
-    o.ut = *(const float4 *)(rec + R_UT + (((size_t)wave * 8 + slice) * 64 + lane) * 16);
-    o.gc = *(const float *)(rec + R_GC);
+    o.pp[0] = t[12 * 64];
+    o.pp[1] = t[13 * 64];
+    const uint4 u = t[14 * 64];
+    o.ut = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
 }
 
 __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int b = blockIdx.y, bid = blockIdx.x;
     int vh, slice;
     if (p.xcd_map) {   // the 8 slices of a head on one XCD (workgroups go round-robin over 8)
@@ -353,8 +386,14 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
     }
     const int col = slice * 16 + n;
 
+    __shared__ __align__(16) char ops_l[2][OPS_BUF];   // chunk operands, two chunks in flight
     __shared__ uint16_t S_l[16][HD + 8];   // S slice, bf16, [column][key dim]
     __shared__ uint16_t U_l[16][CH + 8];   // U slice, bf16, [column][token]
+
+    const char *rec0 = vx_uniform_ptr(p.rec + ((size_t)b * p.nv + vh) * p.NC * REC);
+    const uint32_t ops_w = vx_lds_addr(ops_l) + (uint32_t)wave * OPS_WAVE;
+    fetch_ops(rec0, ops_w, wave, slice, lane);
+    if (p.NC > 1) fetch_ops(rec0 + REC, ops_w + OPS_BUF, wave, slice, lane);
 
     // state rows 32w .. 32w+31 (row blocks 2w, 2w+1) of the slice, C layout
     float *Sg = p.S + ((size_t)b * p.nv + vh) * HD * HD;
@@ -363,19 +402,31 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
     for (int r = 0; r < 2; r++)
 #pragma unroll
         for (int i = 0; i < 4; i++) S[r][i] = Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + col];
+    // take the state loads' wait here, once, rather than inside the loop
+    __asm__ volatile("" ::"v"(S[0]), "v"(S[1]));
 
-    const char *rec0 = p.rec + ((size_t)b * p.nv + vh) * p.NC * REC;
-    // one chunk from `cur` while the next chunk's operands load into `nxt`;
-    // unrolled by two with the operand sets swapping roles (no copies)
-    auto step = [&](int c, const ChunkOps &cur, ChunkOps &nxt) {
-        if (c + 1 < p.NC) load_ops(nxt, rec0 + (size_t)(c + 1) * REC, wave, lane, slice);
+    for (int c = 0; c < p.NC; c++) {
+        // chunk c's loads have landed once at most the loads of chunk c+1 are
+        // still outstanding (loads complete in issue order)
+        if (c + 1 < p.NC)
+            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(OPS_LOADS) : "memory");
+        else
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        ChunkOps cur;
+        const char *slot = &ops_l[c & 1][wave * OPS_WAVE];
+        read_ops(cur, (const uint4 *)slot + lane);
+        const float gc = *(const float *)(slot + OPS_TILES * 1024);
+        // the slot is free once the reads have returned: refill it with chunk c+2
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (c + 2 < p.NC) fetch_ops(rec0 + (size_t)(c + 2) * REC, ops_w + (uint32_t)(c & 1) * OPS_BUF, wave, slice, lane);
+
         // S (bf16) -> LDS as [column][key dim]
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int d = (2 * wave + r) * 16 + 4 * g;
             *(uint2 *)&S_l[n][d] = make_uint2(pack2(S[r][0], S[r][1]), pack2(S[r][2], S[r][3]));
         }
-        __syncthreads();
+        vx_lds_barrier();
         bf16x8_t sb[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) sb[ks] = as_bf16x8(*(const uint4 *)&S_l[n][32 * ks + 8 * g]);
@@ -394,7 +445,7 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
         O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.qe[3]), sb[3], O1, 0, 0, 0);
         const floatx4_t U = U0 + U1;
         *(uint2 *)&U_l[n][wave * 16 + 4 * g] = make_uint2(pack2(U[0], U[1]), pack2(U[2], U[3]));
-        __syncthreads();
+        vx_lds_barrier();
         bf16x8_t ub[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) ub[ks] = as_bf16x8(*(const uint4 *)&U_l[n][32 * ks + 8 * g]);
@@ -402,7 +453,6 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
         O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.pp[0]), ub[0], O0, 0, 0, 0);
         O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.pp[1]), ub[1], O1, 0, 0, 0);
         // S = e^gam_C S + Kt^T U: per row block, two independent MFMAs
-        const float gc = cur.gc;
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             floatx4_t Sa = S[r] * gc, Sb = {0.f, 0.f, 0.f, 0.f};
@@ -416,12 +466,6 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
             const int t = c * CH + wave * 16 + 4 * g + i;
             if (t < p.T) p.out[(((size_t)b * p.T + t) * p.nv + vh) * HD + col] = O[i];
         }
-    };
-    ChunkOps opa, opb;
-    load_ops(opa, rec0, wave, lane, slice);
-    for (int c = 0; c < p.NC; c += 2) {
-        step(c, opa, opb);
-        if (c + 1 < p.NC) step(c + 1, opb, opa);
     }
 #pragma unroll
     for (int r = 0; r < 2; r++)

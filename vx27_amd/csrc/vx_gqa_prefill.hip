@@ -25,6 +25,7 @@
 #include <math.h>
 
 #include "vx_gqa.h"
+#include "vx_lds.h"
 
 namespace {
 
@@ -144,29 +145,6 @@ constexpr int TBUF = 2 * KBUF;              // bytes of one K+V tile buffer
 // Direct-to-LDS loads of one 64-key tile, K and V separately: 4 waves x 8
 // instructions of 64 lanes x 16 bytes each; every lane loads the global unit
 // that belongs at its swizzled LDS slot.
-// One 16-byte-per-lane load from global memory straight into LDS
-// (global_load_lds_dwordx4: lane L's 16 bytes land at lds + 16 L).  Issued
-// from inline asm so that the compiler does not track it: its own waits for
-// LDS DMA would drain the prefetch in flight before every LDS read.  The
-// kernels order it themselves with explicit vmcnt waits before the barriers
-// that publish a tile.  M0 (the LDS base) is saved and restored around it,
-// with the one wait state that an M0 write needs before the load.
-__device__ __forceinline__ void dma16(const void *base, uint32_t off, uint32_t lds) {
-    uint32_t saved;
-    __asm__ volatile(
-        "s_mov_b32 %0, m0\n\t"
-        "s_mov_b32 m0, %3\n\t"
-        "s_nop 0\n\t"
-        "global_load_lds_dwordx4 %1, %2\n\t"
-        "s_mov_b32 m0, %0"
-        : "=&s"(saved)
-        : "v"(off), "s"(base), "s"(lds)
-        : "memory");
-}
-__device__ __forceinline__ uint32_t lds_addr(const void *p) {
-    return (uint32_t)(uintptr_t)(__attribute__((address_space(3))) const void *)p;
-}
-
 // Loads of one 64-key tile, K and V separately: 4 waves x 8 instructions of
 // 64 lanes x 16 bytes each; every lane loads the global unit that belongs at
 // its swizzled LDS slot.  The lane offsets are recomputed at each call (the
@@ -179,7 +157,7 @@ __device__ __forceinline__ void load_k(uint32_t kbuf, const char *Kt, int wave, 
 #pragma unroll
     for (int j = 0; j < PER; j++) {
         const int r = (wave * PER + j) * 2 + (lane >> 5), u = (lane & 31) ^ (r & 15);
-        dma16(Kt, (uint32_t)(r * HDG + u * 8) * 2, kbuf + (wave * PER + j) * 1024);
+        vx_dma16(Kt, (uint32_t)(r * HDG + u * 8) * 2, kbuf + (wave * PER + j) * 1024);
     }
 }
 template <int NW>
@@ -189,7 +167,7 @@ __device__ __forceinline__ void load_v(uint32_t vbuf, const char *Vt, int wave, 
 #pragma unroll
     for (int j = 0; j < PER; j++) {
         const int d = (wave * PER + j) * 8 + (lane >> 3), w = (lane & 7) ^ ((d >> 1) & 7);
-        dma16(Vt, (uint32_t)((((w >> 2) * HDG + d) * 32) + (w & 3) * 8) * 2, vbuf + (wave * PER + j) * 1024);
+        vx_dma16(Vt, (uint32_t)((((w >> 2) * HDG + d) * 32) + (w & 3) * 8) * 2, vbuf + (wave * PER + j) * 1024);
     }
 }
 
@@ -202,18 +180,8 @@ __device__ __forceinline__ void load_q(uint32_t qbuf, const uint16_t *Qh, int qr
     for (int j = 0; j < PER; j++) {
         const int r = (wave * PER + j) * 2 + (lane >> 5), u = (lane & 31) ^ (r & 15);
         const int t = min(qrow0 + r, T - 1);
-        dma16(Qh, (uint32_t)(t * HDG + u * 8) * 2, qbuf + (wave * PER + j) * 1024);
+        vx_dma16(Qh, (uint32_t)(t * HDG + u * 8) * 2, qbuf + (wave * PER + j) * 1024);
     }
-}
-
-// Workgroup barrier for LDS hand-offs only: waits for this wave's LDS
-// operations, not for its outstanding global loads (__syncthreads would also
-// drain the direct-to-LDS prefetch in flight; each wave waits for its own
-// tile loads with an explicit vmcnt before the barrier that publishes them).
-__device__ __forceinline__ void lds_barrier() {
-    __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-    __builtin_amdgcn_s_barrier();
-    __asm__ volatile("" ::: "memory");
 }
 
 // grid (ceil(T/128) * n_q, B), block NW*64: NW waves of RB 16-query blocks
@@ -254,8 +222,8 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
     // tile kt: K rows kt*64.. (32 KiB) and V blocks 2kt, 2kt+1 (2 x 16 KiB)
     const char *Kc = (const char *)(a.k_cache + vx_k_index(a.n_kv, a.L, b, kvh, 0, 0));
     const char *Vc = (const char *)(a.v_cache + vx_v_index(a.n_kv, a.L, b, kvh, 0, 0));
-    const uint32_t kl = lds_addr(Kl), vl = lds_addr(Vl);
-    load_q<NW>(lds_addr(Ql), a.q_rot + ((size_t)b * a.n_q + h) * a.T * HDG, qt * QT, a.T, wave, lane);
+    const uint32_t kl = vx_lds_addr(Kl), vl = vx_lds_addr(Vl);
+    load_q<NW>(vx_lds_addr(Ql), a.q_rot + ((size_t)b * a.n_q + h) * a.T * HDG, qt * QT, a.T, wave, lane);
     load_k<NW>(kl, Kc, wave, lane);
     load_v<NW>(vl, Vc, wave, lane);
 
@@ -278,7 +246,7 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
         // K(kt) (and Q) landed; V(kt), issued after it (PER instructions per
         // wave), may still be in flight
         __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
-        lds_barrier();
+        vx_lds_barrier();
         floatx4_t s[4][RB];
 #pragma unroll
         for (int kb = 0; kb < 4; kb++)
@@ -301,7 +269,7 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
                 }
             }
         }
-        lds_barrier();   // every wave is done with K(kt)
+        vx_lds_barrier();   // every wave is done with K(kt)
         if (more) load_k<NW>(kl, Kc + (size_t)(kt + 1) * KBUF, wave, lane);
 
         bf16x8_t pa[RB][2];
@@ -381,7 +349,7 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
             __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
         else
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        lds_barrier();
+        vx_lds_barrier();
         if (k0 + KT > n_keys) {
             // last tile: V of positions past the valid keys is zeroed (masked P
             // is 0, and 0 * a stale NaN would not be)
@@ -393,7 +361,7 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
                     V[d * KT + u * 8 + (key & 7)] = 0;
                 }
             }
-            lds_barrier();
+            vx_lds_barrier();
         }
         if (live) {
             const int vsw = (n >> 1) & 7, vhalf = (g & 1) * 8;
@@ -412,7 +380,7 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
                 }
             }
         }
-        lds_barrier();   // every wave is done with V(kt)
+        vx_lds_barrier();   // every wave is done with V(kt)
         if (more) load_v<NW>(vl, Vc + (size_t)(kt + 1) * KBUF, wave, lane);
     }
 
