@@ -247,6 +247,140 @@ __global__ __launch_bounds__(HD / CS * R) void dn_decode_kernel(DnArgs a) {
     }
 }
 
+// One step with final q and k (VX_DN_QK_READY, no fused conv): one block of
+// 512 lanes per (sequence, value head).  Lane (part = tid / 32, c4 = tid % 32)
+// holds state rows 8 part .. 8 part + 7 of columns 4 c4 .. 4 c4 + 3, so each
+// wave reads and writes two whole 512-byte state rows per instruction, and
+// all of a lane's state loads are in flight before any other work.  The
+// per-element arithmetic is the general kernel's (decay and the rank-1
+// update through double, float state); kv and o are summed in double per
+// lane over its rows, then over the 16 parts.  Wave 0 finishes the gated
+// output norm (vx27_qfwd.c:147-151) for the whole head.
+__global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int part = tid >> 5, c4 = tid & 31;
+    const int head = blockIdx.x, b = head / a.nv, vh = head % a.nv;
+    const int g = vh * a.nqk / a.nv;           // QK head (vx27_qfwd.c:137)
+
+    __shared__ float s_qn[HD], s_kn[HD], s_v[HD];
+    __shared__ double s_red[8][HD];           // per-wave partial kv, then o
+    __shared__ double s_dl[HD];
+
+    float va = 0.0f, qa = 0.0f, ka = 0.0f;
+    if (tid < HD) {
+        qa = a.q[(size_t)b * a.q_tok + (size_t)g * HD + tid];
+        ka = a.k[(size_t)b * a.k_tok + (size_t)g * HD + tid];
+        va = a.v[(size_t)b * a.v_tok + (size_t)vh * HD + tid];
+    }
+    const bool gate = (a.flags & VX27_DN_OUT_GATE) != 0;
+    float z0 = 0.f, z1 = 0.f, w0 = 1.f, w1 = 1.f;
+    if (wave == 0 && gate) {
+        z0 = a.z[(size_t)b * a.z_tok + (size_t)vh * HD + lane];
+        z1 = a.z[(size_t)b * a.z_tok + (size_t)vh * HD + lane + 64];
+        if (a.norm_w) {
+            w0 = a.norm_w[lane];
+            w1 = a.norm_w[lane + 64];
+        }
+    }
+    const double2 gt = a.gates[(size_t)b * a.nv + vh];   // uniform address: scalar load
+    const double beta = gt.x, decay = gt.y;
+    // state loads after the small ones: those return first (loads complete in
+    // order), so the q/k hand-off below overlaps the state's arrival
+    float *Sg = a.S + ((size_t)b * a.nv + vh) * HD * HD + (size_t)(8 * part) * HD + 4 * c4;
+    float4 S4[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) S4[r] = *(const float4 *)(Sg + (size_t)r * HD);
+    if (tid < HD) {   // v goes through LDS too, so its use waits on nothing late
+        s_qn[tid] = qa;
+        s_kn[tid] = ka;
+        s_v[tid] = va;
+    }
+    __syncthreads();
+
+    float kn[8], qn[8];
+    {
+        const float4 k0 = *(const float4 *)&s_kn[8 * part], k1 = *(const float4 *)&s_kn[8 * part + 4];
+        const float4 q0 = *(const float4 *)&s_qn[8 * part], q1 = *(const float4 *)&s_qn[8 * part + 4];
+        kn[0] = k0.x; kn[1] = k0.y; kn[2] = k0.z; kn[3] = k0.w;
+        kn[4] = k1.x; kn[5] = k1.y; kn[6] = k1.z; kn[7] = k1.w;
+        qn[0] = q0.x; qn[1] = q0.y; qn[2] = q0.z; qn[3] = q0.w;
+        qn[4] = q1.x; qn[5] = q1.y; qn[6] = q1.z; qn[7] = q1.w;
+    }
+    // ---- S *= decay ; kv = S^T kn
+    double kv[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        float *e = (float *)&S4[r];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float sd = (float)((double)e[c] * decay);
+            e[c] = sd;
+            kv[c] = kv[c] + (double)sd * (double)kn[r];
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) kv[c] = kv[c] + __shfl_xor(kv[c], 32, 64);
+    if (lane < 32) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) s_red[wave][4 * c4 + c] = kv[c];
+    }
+    __syncthreads();
+    if (tid < HD) {
+        double s = s_red[0][tid];
+#pragma unroll
+        for (int w = 1; w < 8; w++) s = s + s_red[w][tid];
+        s_dl[tid] = ((double)s_v[tid] - s) * beta;
+    }
+    __syncthreads();
+    // ---- S += kn (x) dl ; o = S^T qn
+    double dl[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) dl[c] = s_dl[4 * c4 + c];
+    double o[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        float *e = (float *)&S4[r];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float su = (float)((double)e[c] + (double)kn[r] * dl[c]);
+            e[c] = su;
+            o[c] = o[c] + (double)su * (double)qn[r];
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < 8; r++) *(float4 *)(Sg + (size_t)r * HD) = S4[r];
+#pragma unroll
+    for (int c = 0; c < 4; c++) o[c] = o[c] + __shfl_xor(o[c], 32, 64);
+    if (lane < 32) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) s_red[wave][4 * c4 + c] = o[c];
+    }
+    __syncthreads();
+    if (wave != 0) return;
+    // ---- wave 0: columns lane and lane + 64
+    double oa = s_red[0][lane], ob = s_red[0][lane + 64];
+#pragma unroll
+    for (int w = 1; w < 8; w++) {
+        oa = oa + s_red[w][lane];
+        ob = ob + s_red[w][lane + 64];
+    }
+    float f0 = (float)oa, f1 = (float)ob;
+    if (gate) {
+        const double so = vx_wave_sum_f64((double)f0 * (double)f0 + (double)f1 * (double)f1);
+        const float is = 1.0f / sqrtf((float)(so / HD) + 1e-6f);
+        f0 = ((f0 * is) * w0) * silu_f(z0);
+        f1 = ((f1 * is) * w1) * silu_f(z1);
+    }
+    if (a.out) {
+        a.out[(size_t)b * a.out_tok + (size_t)vh * HD + lane] = f0;
+        a.out[(size_t)b * a.out_tok + (size_t)vh * HD + lane + 64] = f1;
+    }
+    if (a.out_packed) {
+        vx_pack_store(a.out_packed, a.B, b, vh * HD + lane, f0);
+        vx_pack_store(a.out_packed, a.B, b, vh * HD + lane + 64, f1);
+    }
+}
+
 // Gated output norm of one step for column-split heads: one block of 128
 // lanes per (sequence, value head); out = rmsn_std(o)*norm_w * silu(z)
 // (vx27_qfwd.c:147-151) from the pre-norm outputs in o_pre.
@@ -298,6 +432,14 @@ int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a) {
     // column's rows over R lanes of one workgroup.
     const int heads = a.B * a.nv;
     const bool gate = (a.flags & VX27_DN_OUT_GATE) != 0;
+#ifndef VX_DN_STEP
+#define VX_DN_STEP 1
+#endif
+    if (VX_DN_STEP && a.steps == 1 && (a.flags & VX_DN_QK_READY) && !a.fused_conv &&
+        ((uintptr_t)a.S & 15) == 0) {
+        VX_LAUNCH(ctx, dn_step_kernel, dim3((unsigned)heads), dim3(512), a);
+        return 0;
+    }
     // (With the output gate, one workgroup per head keeps the norm in the
     // kernel; splitting would need the dn_out_gate launch, which costs more
     // than the split gains.)
