@@ -90,6 +90,14 @@ __global__ __launch_bounds__(64) void pack_w(const uint16_t *W, int K, uint16_t 
     *(uint4 *)(Wt + tile_off(s, rb, gridDim.x, gemv_kg(K)) + lane * 8) = v;
 }
 
+#ifndef VX_GEMV_NT
+#define VX_GEMV_NT 1         // streaming (nontemporal) weight loads
+#endif
+__device__ __forceinline__ bf16x8_t wload(const bf16x8_t *p) {
+    if (VX_GEMV_NT) return __builtin_nontemporal_load(p);
+    return *p;
+}
+
 // grid (ceil(N/64), ceil(n_seg/4)), block 256; wave w: K segment 4*blockIdx.y + w
 template <bool TILED>
 __global__ __launch_bounds__(256) void gemv_part_k(const uint16_t *W, int N, int K, const uint16_t *xp,
@@ -134,7 +142,7 @@ __global__ __launch_bounds__(256) void gemv_part_k(const uint16_t *W, int N, int
             bop[u] = xb[(size_t)st * 64];
             const size_t off = woff(st);
 #pragma unroll
-            for (int r = 0; r < RB; r++) aop[u][r] = *(const bf16x8_t *)(wp[r] + off);
+            for (int r = 0; r < RB; r++) aop[u][r] = wload((const bf16x8_t *)(wp[r] + off));
         }
         // dead row blocks (past N in the last workgroup) multiply row block 0
         // and are never stored: no branch in the streaming loop
@@ -149,7 +157,7 @@ __global__ __launch_bounds__(256) void gemv_part_k(const uint16_t *W, int N, int
         const size_t off = woff(s);
         bf16x8_t aop[RB];
 #pragma unroll
-        for (int r = 0; r < RB; r++) aop[r] = *(const bf16x8_t *)(wp[r] + off);
+        for (int r = 0; r < RB; r++) aop[r] = wload((const bf16x8_t *)(wp[r] + off));
 #pragma unroll
         for (int r = 0; r < RB; r++) acc[r] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aop[r], bop, acc[r], 0, 0, 0);
     }

@@ -124,7 +124,11 @@ struct SplitArgs {
     float *part_ml;              // [B][n_kv][n_split][qg][2]
 };
 
+#ifndef VX_SPLIT_NT
+#define VX_SPLIT_NT 1        // streaming (nontemporal) loads of the KV cache
+#endif
 __device__ __forceinline__ bf16x8_t load_bf16x8(const uint16_t *p) {
+    if (VX_SPLIT_NT) return __builtin_nontemporal_load((const bf16x8_t *)p);
     return *(const bf16x8_t *)p;
 }
 
