@@ -161,8 +161,8 @@ def bench_c5(ctx, steps, warmup, B=4, Lctx=131072, cpu=True):
     st.step()
     ctx.sync()
     prof = {}
-    for k in ("gqa_split", "gqa_prep", "gqa_combine", "gemv_part_k<true>", "gemv_reduce_store",
-              "dn_in_epilogue", "dn_step_kernel", "dn_decode_kernel", "pack_x"):
+    for k in ("gqa_split", "gqa_prep", "gqa_combine", "gemv_dn_in", "gemv_wk_store", "dn_step_kernel",
+              "dn_decode_kernel", "pack_x"):
         n, ms = ctx.prof_read(k)
         prof[k] = (n, ms)
     ctx.prof_enable(False)

@@ -22,6 +22,7 @@ struct vx27_hip_ctx {
     // small staging for the drop-ins (host-pointer API)
     void *stage;
     size_t stage_bytes;
+    int n_cu;                // compute units of the device
     // kernel profiler (vx27_hip_prof_*): off unless enabled
     int prof_on;
     vx_prof_rec *prof;

@@ -23,6 +23,7 @@
 // the float rounding that follows).
 #include "vx_dn.h"
 #include "vx_gemv.h"
+#include "vx_lds.h"
 
 namespace {
 
@@ -247,8 +248,9 @@ __global__ __launch_bounds__(HD / CS * R) void dn_decode_kernel(DnArgs a) {
     }
 }
 
-// One step with final q and k (VX_DN_QK_READY, no fused conv): one block of
-// 512 lanes per (sequence, value head).  Lane (part = tid / 32, c4 = tid % 32)
+// One step without the fused conv (q, k given: final with VX_DN_QK_READY,
+// else normalised here per the flags): one block of 512 lanes per (sequence,
+// value head).  Lane (part = tid / 32, c4 = tid % 32)
 // holds state rows 8 part .. 8 part + 7 of columns 4 c4 .. 4 c4 + 3, so each
 // wave reads and writes two whole 512-byte state rows per instruction, and
 // all of a lane's state loads are in flight before any other work.  The
@@ -290,6 +292,49 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
     float4 S4[8];
 #pragma unroll
     for (int r = 0; r < 8; r++) S4[r] = *(const float4 *)(Sg + (size_t)r * HD);
+    if (!(a.flags & VX_DN_QK_READY)) {
+        // q/k normalisation chain (vx27_qfwd.c:119-130 per flags, then
+        // step_exact's own l2norm, vx27_deltanet.c:77-80) on lanes < 128
+        // (waves 0 and 1); sums of squares in double, wave partials added in
+        // wave order.  The barriers only order LDS (the state loads stay in
+        // flight).
+        __shared__ double s_nrm[3][2][2];
+        const float nwj = (a.norm_w && tid < HD) ? a.norm_w[tid] : 1.0f;
+        const float qs = 1.0f / sqrtf((float)HD);
+        auto sum2 = [&](double &u, double &v, double (*slot)[2]) {
+            if (wave < 2) {
+                const double su = vx_wave_sum_f64(u), sv = vx_wave_sum_f64(v);
+                if (lane == 0) {
+                    slot[wave][0] = su;
+                    slot[wave][1] = sv;
+                }
+            }
+            vx_lds_barrier();
+            u = slot[0][0] + slot[1][0];
+            v = slot[0][1] + slot[1][1];
+        };
+        if (a.flags & VX27_DN_PRE_RMS) {       // rmsn(x)*(1+w), vx27_qfwd.c:32-39,123
+            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+            sum2(sq, sk, s_nrm[0]);
+            const float iq = 1.0f / sqrtf((float)(sq / HD) + 1e-6f);
+            const float ik = 1.0f / sqrtf((float)(sk / HD) + 1e-6f);
+            qa = (qa * iq) * (nwj + 1.0f);
+            ka = (ka * ik) * (nwj + 1.0f);
+        }
+        if (a.flags & VX27_DN_PRE_L2) {        // l2norm + q/sqrt(hd), vx27_qfwd.c:124-130
+            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+            sum2(sq, sk, s_nrm[1]);
+            qa = qa * (1.0f / sqrtf((float)sq + 1e-6f));
+            ka = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+            qa = qa * qs;
+        }
+        {                                       // inside step_exact, vx27_deltanet.c:77-80
+            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+            sum2(sq, sk, s_nrm[2]);
+            qa = (qa * (1.0f / sqrtf((float)sq + 1e-6f))) * qs;
+            ka = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+        }
+    }
     if (tid < HD) {   // v goes through LDS too, so its use waits on nothing late
         s_qn[tid] = qa;
         s_kn[tid] = ka;
@@ -435,8 +480,7 @@ int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a) {
 #ifndef VX_DN_STEP
 #define VX_DN_STEP 1
 #endif
-    if (VX_DN_STEP && a.steps == 1 && (a.flags & VX_DN_QK_READY) && !a.fused_conv &&
-        ((uintptr_t)a.S & 15) == 0) {
+    if (VX_DN_STEP && a.steps == 1 && !a.fused_conv && ((uintptr_t)a.S & 15) == 0) {
         VX_LAUNCH(ctx, dn_step_kernel, dim3((unsigned)heads), dim3(512), a);
         return 0;
     }

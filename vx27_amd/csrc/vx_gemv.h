@@ -3,22 +3,18 @@
 #pragma once
 #include "vx_common.h"
 
-// Split-K plan for an N x K GEMV: n_seg K segments of ks_per 32-wide k-steps;
-// segments are combined four at a time inside a workgroup, so
-// vx_gemv_pseg(n_seg) partial sets [N][16] fp32 are written.
+// Split-K plan of the row-major path for an N x K GEMV: n_seg K segments of
+// ks_per 32-wide k-steps; segments are combined four at a time inside a
+// workgroup, so vx_gemv_pseg(n_seg) partial sets [N][16] fp32 are written.
 int vx_gemv_plan(int N, int K, int *n_seg, int *ks_per);
 int vx_gemv_pseg(int n_seg);
 size_t vx_gemv_part_bytes(int N, int n_seg);
 size_t vx_pack_bytes(int K);
 // x [B][K] (row stride x_stride) -> packed MFMA B operand (three bf16 parts).
 int vx_pack(vx27_hip_ctx *ctx, const float *x, size_t x_stride, int B, int K, uint16_t *packed);
-// partial sums of W [N][K] bf16 (tiled layout if `tiled`, else row-major)
-// times the packed operand
-int vx_gemv_part(vx27_hip_ctx *ctx, const uint16_t *W, int tiled, int N, int K, const uint16_t *packed,
-                 int n_seg, int ks_per, float *part);
-// y[b*y_stride + n] = sum of partials of vector b
-int vx_gemv_reduce_store(vx27_hip_ctx *ctx, const float *part, int N, int B, int n_seg, float *y,
-                         size_t y_stride);
+// y[b*y_stride + n] = sum over k of W[n][k] x_b[k] for tiled W and a packed x
+int vx_gemv_store(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const uint16_t *packed, int B, float *y,
+                  size_t y_stride);
 
 // Part p (0 = hi, 1 = mid, 2 = lo) of the exact three-way bf16 split of x:
 // hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid); each difference

@@ -2,21 +2,24 @@
 // device-side synthetic fills and HIP-graph capture.
 //
 // DeltaNet layer (vx27_qfwd.c:102-153), one decode token of B sequences:
-//   gemv_part(W_in)          [qkv | z | a | b] partial sums
-//   dn_in_epilogue           reduce + causal conv/SiLU on qkv (state in place),
-//                            the q/k normalisation chain, z, decay from a,
-//                            beta from b
-//   dn_decode_kernel         exact step on the final q/k, gated output norm,
-//                            output written as the packed operand of W_out
-//   gemv_part(W_out) + reduce   -> out
+//   gemv_dn_in               [qkv | z | a | b] projection with its epilogue
+//                            (DnInEpi): causal conv/SiLU on qkv (state in
+//                            place), z, decay from a, beta from b
+//   dn_step_kernel           q/k normalisation chain, exact step, gated
+//                            output norm, output written as the packed
+//                            operand of W_out
+//   gemv_wk_store(W_out)     -> out
 // Gated GQA layer (vx27_qfwd.c:162-213):
-//   gemv_part(W_qkv) + reduce  -> [q|gate interleaved | k | v]
-//   gqa_prep / gqa_split / gqa_combine (vx_gqa_decode.hip)
-//   pack_x(att) + gemv_part(W_o) + reduce   -> out
+//   gemv_wk_store(W_qkv)     -> [q|gate interleaved | k | v]
+//   gqa_prep / gqa_split / gqa_combine (vx_gqa_decode.hip; the combine
+//                            writes the packed operand of W_o)
+//   gemv_wk_store(W_o)       -> out
+// (the GEMVs are whole-K workgroups with the reduction in LDS:
+// vx_gemv_body.h)
 #include <math.h>
 
 #include "vx_dn.h"
-#include "vx_gemv.h"
+#include "vx_gemv_body.h"
 #include "vx_gqa.h"
 
 
@@ -25,79 +28,56 @@ namespace {
 size_t align256(size_t x) { return (x + 255) & ~(size_t)255; }
 
 struct DnInArgs {
-    const float *part;
-    int N, B, n_pseg, C, vd, nv, nqk;
+    int B, C, vd, nv;
     float *conv_state;
     const void *conv_w;
     int conv_bf16;
-    const float *A_log, *dt_bias, *norm_w;
+    const float *A_log, *dt_bias;
     float *act, *z;
     double2 *gates;
 };
 
-// One block of 128 lanes per 128-row group of the stacked input projection
-// (one row per lane, all sequences): the split-K sum, then
-//   q|k|v rows: causal conv + SiLU (conv state in place); the q and k groups
-//               are whole heads, and run the normalisation chain of
-//               vx27_qfwd.c:119-130 plus step_exact's own (vx27_deltanet.c:
-//               77-80): rmsn(1+w), l2norm (q /= sqrt(hd)), l2norm (q /= sqrt(hd))
+// Epilogue of the stacked DeltaNet input projection [qkv | z | a | b]
+// (vx27_qfwd.c:102-117), one thread per row, all sequences:
+//   q|k|v rows: causal conv + SiLU (conv state in place) -> act; the q/k
+//               normalisation chain runs in the recurrence kernel, which
+//               has whole heads
 //   z rows:     copied out; a rows: decay = exp(g_log); b rows: beta
-__global__ __launch_bounds__(HD) void dn_in_epilogue(DnInArgs a) {
-    const int n = blockIdx.x * HD + threadIdx.x;
-    const bool live = n < a.N;
-    float v[5];
-    if (live) vx_gemv_sum_row(a.part, a.N, a.B, a.n_pseg, live ? n : 0, v);
-    const int qd = a.nqk * HD;
-    if ((int)blockIdx.x < 2 * a.nqk) {   // a q or k head: conv, then the norm chain per sequence
-        __shared__ double s_red[3][2][2];
-        float w[4];
-        load_conv_w(a.conv_w, a.conv_bf16, (size_t)n, w);
-        const bool is_q = n < qd;
-        const float nw = a.norm_w[threadIdx.x] + 1.0f;
-        const float qs = 1.0f / sqrtf((float)HD);
-        for (int b = 0; b < a.B; b++) {
-            float st[3];
-            float *sp = a.conv_state + ((size_t)b * a.C + n) * 3;
-            st[0] = sp[0]; st[1] = sp[1]; st[2] = sp[2];
-            float x = conv_step(st, w, v[b]);
-            sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
-            double unused = 0.0, ss = (double)x * (double)x;
-            block_sum2<2>(ss, unused, s_red[0]);
-            x = (x * (1.0f / sqrtf((float)(ss / HD) + 1e-6f))) * nw;
-            ss = (double)x * (double)x;
-            block_sum2<2>(ss, unused, s_red[1]);
-            x = x * (1.0f / sqrtf((float)ss + 1e-6f));
-            if (is_q) x = x * qs;
-            ss = (double)x * (double)x;
-            block_sum2<2>(ss, unused, s_red[2]);
-            x = x * (1.0f / sqrtf((float)ss + 1e-6f));
-            if (is_q) x = x * qs;
-            a.act[(size_t)b * a.C + n] = x;
+struct DnInEpi {
+    DnInArgs a;
+    template <int RB>
+    __device__ __forceinline__ void operator()(int row0, int rows, const WkRows<RB> &c, int tid) const {
+        if (tid >= rows) return;
+        const int n = row0 + tid;
+        float v[5];
+        for (int b = 0; b < a.B; b++) v[b] = c.y(tid, b);
+        if (n < a.C) {                       // q, k or v channel: causal conv + SiLU
+            float w[4];
+            load_conv_w(a.conv_w, a.conv_bf16, (size_t)n, w);
+            for (int b = 0; b < a.B; b++) {
+                float *sp = a.conv_state + ((size_t)b * a.C + n) * 3;
+                float st[3] = {sp[0], sp[1], sp[2]};
+                a.act[(size_t)b * a.C + n] = conv_step(st, w, v[b]);
+                sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
+            }
+        } else if (n < a.C + a.vd) {         // z
+            for (int b = 0; b < a.B; b++) a.z[(size_t)b * a.vd + (n - a.C)] = v[b];
+        } else if (n < a.C + a.vd + a.nv) {  // a -> decay = exp(g_log), vx27_deltanet.c:68,82
+            const int vh = n - a.C - a.vd;
+            const double eA = exp((double)a.A_log[vh]), dtb = (double)a.dt_bias[vh];
+            for (int b = 0; b < a.B; b++)
+                a.gates[(size_t)b * a.nv + vh].y = exp(-eA * softplus_d((double)v[b] + dtb));
+        } else {                             // b -> beta = sigmoid(b), vx27_deltanet.c:67
+            const int vh = n - a.C - a.vd - a.nv;
+            for (int b = 0; b < a.B; b++) a.gates[(size_t)b * a.nv + vh].x = 1.0 / (1.0 + exp(-(double)v[b]));
         }
-        return;
     }
-    if (!live) return;
-    if (n < a.C) {                       // v channel: causal conv + SiLU
-        float w[4];
-        load_conv_w(a.conv_w, a.conv_bf16, (size_t)n, w);
-        for (int b = 0; b < a.B; b++) {
-            float st[3];
-            float *sp = a.conv_state + ((size_t)b * a.C + n) * 3;
-            st[0] = sp[0]; st[1] = sp[1]; st[2] = sp[2];
-            a.act[(size_t)b * a.C + n] = conv_step(st, w, v[b]);
-            sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
-        }
-    } else if (n < a.C + a.vd) {         // z
-        for (int b = 0; b < a.B; b++) a.z[(size_t)b * a.vd + (n - a.C)] = v[b];
-    } else if (n < a.C + a.vd + a.nv) {  // a -> decay = exp(g_log), vx27_deltanet.c:68,82
-        const int vh = n - a.C - a.vd;
-        const double eA = exp((double)a.A_log[vh]), dtb = (double)a.dt_bias[vh];
-        for (int b = 0; b < a.B; b++)
-            a.gates[(size_t)b * a.nv + vh].y = exp(-eA * softplus_d((double)v[b] + dtb));
-    } else {                             // b -> beta = sigmoid(b), vx27_deltanet.c:67
-        const int vh = n - a.C - a.vd - a.nv;
-        for (int b = 0; b < a.B; b++) a.gates[(size_t)b * a.nv + vh].x = 1.0 / (1.0 + exp(-(double)v[b]));
-    }
+};
+
+template <int RBW, bool NT>
+__global__ __launch_bounds__(1024) void gemv_dn_in(const uint16_t *W, int N, int K, const uint16_t *xp, int B,
+                                                   DnInEpi epi) {
+    vx_gemv_wk_body<RBW, NT>(W, N, K, xp, B, epi);
 }
 
 __global__ void advance_pos_kernel(int *pos, int B) {
@@ -152,35 +132,31 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
                "vx27_hip_dn_layer_decode: conv_w_dtype must be VX27_F32 or VX27_BF16");
     const int B = d->B, nv = d->nv, qd = d->nqk * HD, vd = nv * HD, C = 2 * qd + vd, H = d->hidden;
     const int Nin = C + vd + 2 * nv;
-    int seg_in, per_in, seg_out, per_out;
-    if (vx_gemv_plan(Nin, H, &seg_in, &per_in) || vx_gemv_plan(H, vd, &seg_out, &per_out)) return -1;
     const size_t pk_x = d->x_packed ? 0 : align256(vx_pack_bytes(H));
-    size_t part_b = vx_gemv_part_bytes(Nin, seg_in);
-    if (vx_gemv_part_bytes(H, seg_out) > part_b) part_b = vx_gemv_part_bytes(H, seg_out);
-    part_b = align256(part_b);
     const size_t act_b = align256((size_t)B * C * 4), z_b = align256((size_t)B * vd * 4);
     const size_t g_b = align256((size_t)B * nv * sizeof(double2));
     const size_t pk_o = align256(vx_pack_bytes(vd));
     void *scr;
-    if (vx_ctx_scratch(ctx, pk_x + part_b + act_b + z_b + g_b + pk_o, &scr)) return -1;
+    if (vx_ctx_scratch(ctx, pk_x + act_b + z_b + g_b + pk_o, &scr)) return -1;
     char *p = (char *)scr;
     uint16_t *xp = d->x_packed ? (uint16_t *)d->x_packed : (uint16_t *)p;
     p += pk_x;
-    float *part = (float *)p; p += part_b;
     float *act = (float *)p; p += act_b;
     float *z = (float *)p; p += z_b;
     double2 *gates = (double2 *)p; p += g_b;
     uint16_t *op = (uint16_t *)p;
 
     if (!d->x_packed && vx_pack(ctx, d->x, (size_t)H, B, H, xp)) return -1;
-    if (vx_gemv_part(ctx, d->w_in, 1, Nin, H, xp, seg_in, per_in, part)) return -1;
-    DnInArgs ea = {part, Nin, B, vx_gemv_pseg(seg_in), C, vd, nv, d->nqk, d->conv_state, d->conv_w,
-                   d->conv_w_dtype == VX27_BF16, d->A_log, d->dt_bias, d->norm_w, act, z, gates};
-    VX_LAUNCH(ctx, dn_in_epilogue, dim3((unsigned)((Nin + HD - 1) / HD)), dim3(HD), ea);
+    {
+        const DnInArgs ea = {B, C, vd, nv, d->conv_state, d->conv_w, d->conv_w_dtype == VX27_BF16,
+                             d->A_log, d->dt_bias, act, z, gates};
+        const WkPlan wp = vx_gemv_wk_plan(Nin, H, ctx->n_cu);
+        VX_WK_DISPATCH(ctx, gemv_dn_in, wp, d->w_in, Nin, H, xp, B, (DnInEpi{ea}));
+    }
 
     DnArgs ra = {};
     ra.B = B; ra.nqk = d->nqk; ra.nv = nv; ra.steps = 1;
-    ra.flags = VX_DN_QK_READY | VX27_DN_OUT_GATE;
+    ra.flags = VX27_DN_PRE_RMS | VX27_DN_PRE_L2 | VX27_DN_OUT_GATE;
     ra.S = d->S;
     ra.q = act; ra.k = act + qd; ra.v = act + 2 * qd;
     ra.q_tok = ra.k_tok = ra.v_tok = (size_t)C;
@@ -188,8 +164,7 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     ra.out = nullptr; ra.out_tok = (size_t)vd; ra.out_packed = op;
     if (vx_dn_recurrence(ctx, ra)) return -1;
 
-    if (vx_gemv_part(ctx, d->w_out, 1, H, vd, op, seg_out, per_out, part)) return -1;
-    return vx_gemv_reduce_store(ctx, part, H, B, seg_out, d->out, (size_t)H);
+    return vx_gemv_store(ctx, d->w_out, H, vd, op, B, d->out, (size_t)H);
 }
 
 extern "C" int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer_desc *d) {
@@ -201,8 +176,6 @@ extern "C" int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer
     VX_REQUIRE(d->x && d->w_qkv && d->w_o && d->out, "vx27_hip_gqa_layer_decode: null pointer in descriptor");
     const int B = d->B, H = d->hidden, hd = d->hd;
     const int Nq = d->n_q * 2 * hd, Nqkv = Nq + 2 * d->n_kv * hd, Ka = d->n_q * hd;
-    int seg_in, per_in, seg_out, per_out;
-    if (vx_gemv_plan(Nqkv, H, &seg_in, &per_in) || vx_gemv_plan(H, Ka, &seg_out, &per_out)) return -1;
 
     vx27_gqa_desc g = {};
     g.B = B; g.n_q = d->n_q; g.n_kv = d->n_kv; g.hd = hd; g.rope_dim = d->rope_dim;
@@ -214,32 +187,26 @@ extern "C" int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer
     g.k_cache = d->k_cache; g.v_cache = d->v_cache; g.n_split = d->n_split;
 
     const size_t pk_x = d->x_packed ? 0 : align256(vx_pack_bytes(H));
-    size_t part_b = vx_gemv_part_bytes(Nqkv, seg_in);
-    if (vx_gemv_part_bytes(H, seg_out) > part_b) part_b = vx_gemv_part_bytes(H, seg_out);
-    part_b = align256(part_b);
     const size_t y_b = align256((size_t)B * Nqkv * 4);
     const size_t pk_a = align256(vx_pack_bytes(Ka));
     // placeholders so the scratch size of the attention step can be planned
     g.q = g.gate = g.k_new = g.v_new = (const float *)1;
     const size_t gq_b = align256(vx_gqa_scratch_bytes(&g));
     void *scr;
-    if (vx_ctx_scratch(ctx, pk_x + part_b + y_b + pk_a + gq_b, &scr)) return -1;
+    if (vx_ctx_scratch(ctx, pk_x + y_b + pk_a + gq_b, &scr)) return -1;
     char *p = (char *)scr;
     uint16_t *xp = d->x_packed ? (uint16_t *)d->x_packed : (uint16_t *)p;
     p += pk_x;
-    float *part = (float *)p; p += part_b;
     float *y = (float *)p; p += y_b;
     uint16_t *ap = (uint16_t *)p; p += pk_a;
     void *gscr = p;
 
     if (!d->x_packed && vx_pack(ctx, d->x, (size_t)H, B, H, xp)) return -1;
-    if (vx_gemv_part(ctx, d->w_qkv, 1, Nqkv, H, xp, seg_in, per_in, part)) return -1;
-    if (vx_gemv_reduce_store(ctx, part, Nqkv, B, seg_in, y, (size_t)Nqkv)) return -1;
+    if (vx_gemv_store(ctx, d->w_qkv, Nqkv, H, xp, B, y, (size_t)Nqkv)) return -1;
     g.q = y; g.gate = y + hd; g.k_new = y + Nq; g.v_new = y + Nq + (size_t)d->n_kv * hd;
     g.out = nullptr;
     if (vx_gqa_decode_into(ctx, &g, gscr, ap)) return -1;
-    if (vx_gemv_part(ctx, d->w_o, 1, H, Ka, ap, seg_out, per_out, part)) return -1;
-    return vx_gemv_reduce_store(ctx, part, H, B, seg_out, d->out, (size_t)H);
+    return vx_gemv_store(ctx, d->w_o, H, Ka, ap, B, d->out, (size_t)H);
 }
 
 extern "C" int vx27_hip_advance_pos(vx27_hip_ctx *ctx, int *pos, int B) {

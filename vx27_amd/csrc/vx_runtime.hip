@@ -70,6 +70,7 @@ extern "C" int vx27_hip_open(vx27_hip_ctx **out, int device, char *err, size_t e
         return fail();
     }
     c->stream = c->own_stream;
+    c->n_cu = prop.multiProcessorCount > 0 ? prop.multiProcessorCount : 256;
     *out = c;
     return 0;
 }
