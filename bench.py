@@ -447,7 +447,7 @@ def bench_gqa_prefill(ctx, T=4096, iters=10, cpu=True):
         L.check(L.lib().vx27_hip_gqa_prefill(ctx.h, C.byref(desc)), "gqa_prefill")
     for _ in range(3):
         run()
-    wall_us, per = _time_calls(ctx, run, ("gqp_prep", "gqp_attn"), iters)
+    wall_us, per = _time_calls(ctx, run, ("gqp_kv", "gqp_attn"), iters)
     k_us = sum(per.values())
     flops = 2 * hd * n_q * T * (T + 1)
     res = {"workload": f"gqa_prefill B=1 T={T} 24Q/4KV hd256 causal", "us_per_call": wall_us,

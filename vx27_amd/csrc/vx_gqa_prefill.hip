@@ -10,19 +10,27 @@
 // same as causal attention of all T queries over the cache.
 //
 // Kernels per call:
-//   gqp_prep   one workgroup per (token, sequence): norm + RoPE of every q
-//              head (bf16, head-major scratch) and k head; k,v rounded to
-//              bf16 and stored at positions pos0..pos0+T-1 of the cache.
+//   gqp_kv     one workgroup per (token, sequence): rmsn + RoPE of every k
+//              head; k,v rounded to bf16 and stored at positions
+//              pos0..pos0+T-1 of the cache.
 //   gqp_attn   one workgroup per (128-query tile, Q head, sequence), heaviest
-//              tiles first; 4 waves of 32 queries.  Per 64-key tile staged in
-//              LDS:  S^T[key][q] = K . Q^T (v_mfma_f32_16x16x32_bf16, 4 key
-//              blocks x 2 query blocks x 8 k-steps), causal mask, online
-//              softmax; the C layout of S^T (lane (g,n): keys 4g..4g+3 of a
-//              16-key block, query n) is, for key blocks 2s and 2s+1, the A
-//              operand of O += P V with the keys of k-step s in the order
-//              (4g..4g+3, 16+4g..16+4g+3); the V operand takes the keys in
-//              the same order from the dim-major V tile.
+//              tiles first; 4 waves of 32 queries.  Each wave normalises,
+//              rotates and scales its own 32 query rows into MFMA operand
+//              registers (the B operand layout puts both halves of a RoPE
+//              pair in one lane when rope_dim is a multiple of 64).  64-key
+//              K and V tiles arrive in LDS by direct-to-LDS loads, double
+//              buffered: tile kt+1 streams in while tile kt is used.  Per
+//              tile:  S^T[key][q] = K . Q^T (v_mfma_f32_16x16x32_bf16, 4 key
+//              blocks x query blocks x 8 k-steps), causal mask, online
+//              softmax.  Row m of key block kb holds key 32(kb/2) + 8(m/4)
+//              + 4(kb%2) + m%4, so in the C layout of S^T lane (g,n) of key
+//              blocks 2s and 2s+1 holds keys 32s + 8g + 0..7 of query n:
+//              that is the A operand of O^T += V^T P^T for k-step s as it
+//              stands, and the matching V operand is one 16-byte unit (8
+//              consecutive keys) of a dim row of the dim-major V tile.
 #include <math.h>
+
+#include <type_traits>
 
 #include "vx_gqa.h"
 #include "vx_lds.h"
@@ -35,27 +43,27 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 constexpr int HDG = VX_GQA_HD;
 constexpr int QT = 128;     // queries per workgroup
 #ifndef GQP_NW
-#define GQP_NW 4            // waves per attention workgroup (32 queries each)
+#define GQP_NW 8            // waves per attention workgroup (128/NW queries each)
 #endif
 #define GQP_RB (QT / 16 / GQP_NW)
 constexpr int KT = 64;      // keys per tile
 
-struct PrepArgs {
-    int T, n_q, n_kv, rope_dim, L, pos0;
+struct KvArgs {
+    int T, n_kv, rope_dim, L, pos0;
     unsigned flags;
     float yarn;
-    const uint16_t *q, *k, *v;
-    size_t q_ts, q_hs, kv_ts;     // token / head strides (elements); k,v head stride 256
-    const float *q_norm_w, *k_norm_w;
+    const uint16_t *k, *v;
+    size_t kv_ts;                 // token stride (elements); head stride 256
+    const float *k_norm_w;
     uint16_t *k_cache, *v_cache;
-    uint16_t *q_rot;              // [B][n_q][T][256]
+    float2 *cs_tab;               // [T][rope_dim/2] (cos, sin) of each token's angles, for gqp_attn
     vx_rope_tab rope;
 };
 
 // grid (T, B), block 256: one workgroup per token, RoPE table once per
-// token, wave w handles heads w, w+4, ... of q then k; lane l holds dims
-// l, l+64, l+128, l+192
-__global__ __launch_bounds__(256) void gqp_prep(PrepArgs a) {
+// token, wave w handles KV heads w, w+4, ...; lane l holds dims l, l+64,
+// l+128, l+192
+__global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
     const int t = blockIdx.x, b = blockIdx.y;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -67,16 +75,13 @@ __global__ __launch_bounds__(256) void gqp_prep(PrepArgs a) {
         const float ang = ((float)pos / a.yarn) * a.rope.freq[tid];
         cs[tid] = cosf(ang);
         sn[tid] = sinf(ang);
+        if (b == 0) a.cs_tab[(size_t)t * half + tid] = make_float2(cs[tid], sn[tid]);
     }
     __syncthreads();
     const size_t tok = (size_t)b * a.T + t;
-    const int nh = a.n_q + a.n_kv;
     float *rw = row[wave];
-    for (int h = wave; h < nh; h += 4) {
-        const bool is_q = h < a.n_q;
-        const int hk = h - a.n_q;
-        const uint16_t *src = is_q ? a.q + tok * a.q_ts + (size_t)h * a.q_hs : a.k + tok * a.kv_ts + (size_t)hk * HDG;
-        const float *wn = is_q ? a.q_norm_w : a.k_norm_w;
+    for (int hk = wave; hk < a.n_kv; hk += 4) {
+        const uint16_t *src = a.k + tok * a.kv_ts + (size_t)hk * HDG;
         float x[4];
         double ss = 0.0;
 #pragma unroll
@@ -88,7 +93,7 @@ __global__ __launch_bounds__(256) void gqp_prep(PrepArgs a) {
         const float sc = 1.0f / sqrtf((float)(ss / HDG) + 1e-6f);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            const float w = wn[lane + 64 * e];
+            const float w = a.k_norm_w[lane + 64 * e];
             x[e] = (a.flags & VX27_GQA_NORM_W) ? (x[e] * sc) * w : (x[e] * sc) * (w + 1.0f);
             rw[lane + 64 * e] = x[e];
         }
@@ -101,25 +106,25 @@ __global__ __launch_bounds__(256) void gqp_prep(PrepArgs a) {
                 r = rw[i] * cs[i] - rw[i + half] * sn[i];
             else if (i < 2 * half)
                 r = rw[i - half] * sn[i - half] + rw[i] * cs[i - half];
-            if (is_q) {
-                // scores leave the MFMA in the exp2 domain: q * log2(e) / sqrt(256)
-                a.q_rot[(((size_t)b * a.n_q + h) * a.T + t) * HDG + i] = vx_f32_to_bf16(r * (1.4426950408889634f / 16.0f));
-            } else {
-                a.k_cache[vx_k_index(a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(r);
-                a.v_cache[vx_v_index(a.n_kv, a.L, b, hk, pos, i)] = a.v[tok * a.kv_ts + (size_t)hk * HDG + i];
-            }
+            a.k_cache[vx_k_index(a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(r);
+            a.v_cache[vx_v_index(a.n_kv, a.L, b, hk, pos, i)] = a.v[tok * a.kv_ts + (size_t)hk * HDG + i];
         }
         __builtin_amdgcn_wave_barrier();   // reads of this row done before the next head's writes
     }
 }
 
 struct AttnArgs {
-    int T, n_q, n_kv, L, pos0, xcd_map;
-    const uint16_t *q_rot;        // [B][n_q][T][256], pre-scaled by log2(e)/sqrt(256)
+    int T, n_q, n_kv, L, pos0, xcd_map, rope_dim;
+    unsigned flags;
+    float yarn;
+    const uint16_t *q;            // raw q: q[(b*T + t)*q_ts + h*q_hs + i]
+    size_t q_ts, q_hs;
+    const float *q_norm_w;
     const uint16_t *k_cache, *v_cache;
     const uint16_t *gate;
     size_t g_ts, g_hs;
     float *out;                   // [B][T][n_q][256]
+    const float2 *cs_tab;         // [T][rope_dim/2] (cos, sin), written by gqp_kv
 };
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) {
@@ -135,9 +140,10 @@ __device__ __forceinline__ uint32_t pack2(float x, float y) {
 }
 
 
-// LDS tile buffer: K [64 keys][256 dims] then V [256 dims][64 keys], bf16,
+// LDS tile buffers: K [64 keys][256 dims] and V [256 dims][64 keys], bf16,
 // 16-byte units XOR-swizzled so the MFMA operand reads are conflict-free:
-//   K unit u of key r at r*32 + (u ^ (r & 15))
+//   K unit u of key r at r*32 + (u ^ kswz(r)), kswz(r) = (r & 3) | ((r >> 1) & 12)
+//     (the 16 rows one key block reads are distinct in kswz)
 //   V unit u (8 keys) of dim d at d*8 + (u ^ ((d >> 1) & 7))
 constexpr int KBUF = KT * HDG * 2;          // bytes of the K part
 constexpr int TBUF = 2 * KBUF;              // bytes of one K+V tile buffer
@@ -150,13 +156,15 @@ constexpr int TBUF = 2 * KBUF;              // bytes of one K+V tile buffer
 // its swizzled LDS slot.  The lane offsets are recomputed at each call (the
 // empty asm hides that they are loop-invariant, so they are not held in
 // registers across the tile loop).
+__device__ __forceinline__ int kswz(int r) { return (r & 3) | ((r >> 1) & 12); }
+
 template <int NW>
 __device__ __forceinline__ void load_k(uint32_t kbuf, const char *Kt, int wave, int lane) {
     __asm__ volatile("" : "+v"(lane));
     constexpr int PER = 32 / NW;   // 1 KiB chunks per wave
 #pragma unroll
     for (int j = 0; j < PER; j++) {
-        const int r = (wave * PER + j) * 2 + (lane >> 5), u = (lane & 31) ^ (r & 15);
+        const int r = (wave * PER + j) * 2 + (lane >> 5), u = (lane & 31) ^ kswz(r);
         vx_dma16(Kt, (uint32_t)(r * HDG + u * 8) * 2, kbuf + (wave * PER + j) * 1024);
     }
 }
@@ -168,19 +176,6 @@ __device__ __forceinline__ void load_v(uint32_t vbuf, const char *Vt, int wave, 
     for (int j = 0; j < PER; j++) {
         const int d = (wave * PER + j) * 8 + (lane >> 3), w = (lane & 7) ^ ((d >> 1) & 7);
         vx_dma16(Vt, (uint32_t)((((w >> 2) * HDG + d) * 32) + (w & 3) * 8) * 2, vbuf + (wave * PER + j) * 1024);
-    }
-}
-
-// The workgroup's 128 query rows (row-major, same swizzle as K), once per
-// workgroup: 64 chunks of 1 KiB over the waves; rows past T repeat row T-1.
-template <int NW>
-__device__ __forceinline__ void load_q(uint32_t qbuf, const uint16_t *Qh, int qrow0, int T, int wave, int lane) {
-    constexpr int PER = 64 / NW;
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int r = (wave * PER + j) * 2 + (lane >> 5), u = (lane & 31) ^ (r & 15);
-        const int t = min(qrow0 + r, T - 1);
-        vx_dma16(Qh, (uint32_t)(t * HDG + u * 8) * 2, qbuf + (wave * PER + j) * 1024);
     }
 }
 
@@ -208,12 +203,10 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: LDS bases go to M0
     const int r0 = qt * QT + wave * (RB * 16);                 // this wave's first query (token index)
 
-    // K and V tiles as distinct LDS objects: the next K streams in while this
-    // tile's V is read, and the next V while the next K is read, and the
-    // compiler can see that these do not alias
-    __shared__ __attribute__((aligned(16))) char Kl[KBUF];
-    __shared__ __attribute__((aligned(16))) char Vl[KBUF];
-    __shared__ __attribute__((aligned(16))) char Ql[QT * HDG * 2];   // this workgroup's queries
+    // two K and two V tile buffers: tile kt+1 streams into one pair while
+    // tile kt is read from the other
+    __shared__ __attribute__((aligned(16))) char Kl[2][KBUF];
+    __shared__ __attribute__((aligned(16))) char Vl[2][KBUF];
 
     const int n_keys = a.pos0 + a.T;                           // valid cache positions
     const int wg_last = a.pos0 + min(qt * QT + QT, a.T) - 1;   // last key any row here sees
@@ -222,10 +215,79 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
     // tile kt: K rows kt*64.. (32 KiB) and V blocks 2kt, 2kt+1 (2 x 16 KiB)
     const char *Kc = (const char *)(a.k_cache + vx_k_index(a.n_kv, a.L, b, kvh, 0, 0));
     const char *Vc = (const char *)(a.v_cache + vx_v_index(a.n_kv, a.L, b, kvh, 0, 0));
-    const uint32_t kl = vx_lds_addr(Kl), vl = vx_lds_addr(Vl);
-    load_q<NW>(vx_lds_addr(Ql), a.q_rot + ((size_t)b * a.n_q + h) * a.T * HDG, qt * QT, a.T, wave, lane);
-    load_k<NW>(kl, Kc, wave, lane);
-    load_v<NW>(vl, Vc, wave, lane);
+    const uint32_t kl0 = vx_lds_addr(Kl[0]), vl0 = vx_lds_addr(Vl[0]);
+    load_k<NW>(kl0, Kc, wave, lane);
+    load_v<NW>(vl0, Vc, wave, lane);
+
+    // ---- this wave's queries as the B operand of S^T = K Q^T: lane (g,n)
+    // of k-step ks holds dims 32ks + 8g + 0..7 of query row n of block rb.
+    // rmsn (1+w, or w with VX27_GQA_NORM_W; sum of squares in double over
+    // the 4 lanes of the row), RoPE (pair (i, i + half) sits in one lane:
+    // k-steps ks and ks + half/32), then the log2(e)/sqrt(256) score scale.
+    bf16x8_t qv[RB][8];
+    {
+        const int hq = a.rope_dim / 64;   // k-steps holding the first half of the pairs
+        // one query block with a constant index (qv and x stay in registers)
+        auto prep_block = [&](auto rbc) {
+            constexpr int rb = decltype(rbc)::value;
+            const int t = min(r0 + rb * 16 + n, a.T - 1);   // rows past T repeat row T-1
+            const uint16_t *src = a.q + ((size_t)b * a.T + t) * a.q_ts + (size_t)h * a.q_hs + 8 * g;
+            float x[8][8];
+            double ss = 0.0;
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                const uint4 u = *(const uint4 *)(src + 32 * ks);
+                const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    x[ks][2 * e] = __uint_as_float(w4[e] << 16);
+                    x[ks][2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u);
+                }
+#pragma unroll
+                for (int e = 0; e < 8; e++) ss += (double)x[ks][e] * (double)x[ks][e];
+            }
+            ss += __shfl_xor(ss, 16, 64);
+            ss += __shfl_xor(ss, 32, 64);
+            const float sc = 1.0f / sqrtf((float)(ss / HDG) + 1e-6f);
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float w = a.q_norm_w[32 * ks + 8 * g + e];
+                    x[ks][e] = (a.flags & VX27_GQA_NORM_W) ? (x[ks][e] * sc) * w : (x[ks][e] * sc) * (w + 1.0f);
+                }
+            // the pair offset as a constant, so x stays in registers; cos and
+            // sin of the token's angles from the table gqp_kv wrote
+            const float2 *ct = a.cs_tab + (size_t)t * (32 * hq) + 8 * g;
+            auto rope = [&](auto hqc) {
+                constexpr int HQ = decltype(hqc)::value;
+#pragma unroll
+                for (int ks = 0; ks < HQ; ks++)
+#pragma unroll
+                    for (int e = 0; e < 8; e++) {
+                        const float2 c = ct[32 * ks + e];
+                        const float x0 = x[ks][e], x1 = x[ks + HQ][e];
+                        x[ks][e] = x0 * c.x - x1 * c.y;
+                        x[ks + HQ][e] = x0 * c.y + x1 * c.x;
+                    }
+            };
+            switch (hq) {
+                case 1: rope(std::integral_constant<int, 1>{}); break;
+                case 2: rope(std::integral_constant<int, 2>{}); break;
+                case 3: rope(std::integral_constant<int, 3>{}); break;
+                case 4: rope(std::integral_constant<int, 4>{}); break;
+                default: break;
+            }
+            constexpr float QS = 1.4426950408889634f / 16.0f;   // scores in the exp2 domain
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+                qv[rb][ks] = as_bf16x8(make_uint4(pack2(x[ks][0] * QS, x[ks][1] * QS), pack2(x[ks][2] * QS, x[ks][3] * QS),
+                                                  pack2(x[ks][4] * QS, x[ks][5] * QS), pack2(x[ks][6] * QS, x[ks][7] * QS)));
+        };
+        prep_block(std::integral_constant<int, 0>{});
+        if constexpr (RB > 1) prep_block(std::integral_constant<int, 1>{});
+        static_assert(RB <= 2, "the query prologue covers at most two blocks");
+    }
 
     floatx4_t O[RB][16];
 #pragma unroll
@@ -240,37 +302,49 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
     }
 
     for (int kt = 0; kt < n_tiles; kt++) {
-        const int k0 = kt * KT;
+        const int k0 = kt * KT, cur = kt & 1;
         const bool more = kt + 1 < n_tiles;
         const bool live = k0 <= wave_last;   // wave-uniform: otherwise every key here is masked
-        // K(kt) (and Q) landed; V(kt), issued after it (PER instructions per
-        // wave), may still be in flight
+        const char *Kt = Kl[cur], *Vt = Vl[cur];
+        // K(kt) landed: issued after it is only V(kt) (PER instructions per
+        // wave); the barrier also means every wave is done with tile kt-1,
+        // whose buffers take tile kt+1 now
         __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
         vx_lds_barrier();
+        if (more) {
+            load_k<NW>(vx_lds_addr(Kl[cur ^ 1]), Kc + (size_t)(kt + 1) * KBUF, wave, lane);
+            load_v<NW>(vx_lds_addr(Vl[cur ^ 1]), Vc + (size_t)(kt + 1) * KBUF, wave, lane);
+        }
         floatx4_t s[4][RB];
 #pragma unroll
         for (int kb = 0; kb < 4; kb++)
 #pragma unroll
             for (int rb = 0; rb < RB; rb++) s[kb][rb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
         if (live) {
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                const int uo = ((4 * ks + g) ^ n) << 4;   // swizzled unit of rows = n (mod 16)
-                bf16x8_t qv[RB];
-#pragma unroll
-                for (int rb = 0; rb < RB; rb++)
-                    qv[rb] = as_bf16x8(*(const uint4 *)(Ql + (wave * (RB * 16) + rb * 16 + n) * 512 + uo));
+            // the K operands of k-step ks+1 are read while the MFMAs of ks run
+            // (the scheduling barriers keep that order)
+            bf16x8_t kf[2][4];
+            auto kload = [&](int ks, bf16x8_t *dst) {
 #pragma unroll
                 for (int kb = 0; kb < 4; kb++) {
-                    const bf16x8_t ka = as_bf16x8(*(const uint4 *)(Kl + (kb * 16 + n) * 512 + uo));
+                    const int kr = 32 * (kb >> 1) + 8 * (n >> 2) + 4 * (kb & 1) + (n & 3);   // key row of A row n
+                    const int uo = ((4 * ks + g) ^ kswz(kr)) << 4;
+                    dst[kb] = as_bf16x8(*(const uint4 *)(Kt + kr * 512 + uo));
+                }
+            };
+            kload(0, kf[0]);
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++) {
+                if (ks + 1 < 8) kload(ks + 1, kf[(ks + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                     for (int rb = 0; rb < RB; rb++)
-                        s[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ka, qv[rb], s[kb][rb], 0, 0, 0);
-                }
+                        s[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks & 1][kb], qv[rb][ks], s[kb][rb], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        vx_lds_barrier();   // every wave is done with K(kt)
-        if (more) load_k<NW>(kl, Kc + (size_t)(kt + 1) * KBUF, wave, lane);
 
         bf16x8_t pa[RB][2];
         if (live) {
@@ -282,7 +356,7 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
                     for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                         for (int i = 0; i < 4; i++)
-                            if (k0 + kb * 16 + 4 * g + i > qpos) s[kb][rb][i] = -INFINITY;
+                            if (k0 + 32 * (kb >> 1) + 8 * g + 4 * (kb & 1) + i > qpos) s[kb][rb][i] = -INFINITY;
                 }
             }
             // Lazy rescaling: P = exp2(s - m) against a reference max m per
@@ -344,16 +418,17 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
             }
         }
 
-        // V(kt) landed; K(kt+1), issued after it, may still be in flight
+        // V(kt) landed: issued after it are K(kt+1) and V(kt+1) when there is
+        // a next tile
         if (more)
-            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
+            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PER) : "memory");
         else
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
         vx_lds_barrier();
         if (k0 + KT > n_keys) {
             // last tile: V of positions past the valid keys is zeroed (masked P
             // is 0, and 0 * a stale NaN would not be)
-            uint16_t *V = (uint16_t *)Vl;
+            uint16_t *V = (uint16_t *)Vl[cur];
             for (int e = tid; e < HDG * KT; e += NW * 64) {
                 const int d = e >> 6, key = e & 63;
                 if (k0 + key >= n_keys) {
@@ -364,24 +439,31 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
             vx_lds_barrier();
         }
         if (live) {
-            const int vsw = (n >> 1) & 7, vhalf = (g & 1) * 8;
+            // groups of 4 dim blocks: the V operands of group j+1 are read
+            // while the MFMAs of group j run
+            const int vsw = (n >> 1) & 7;
+            bf16x8_t vf[2][4];
+            auto vload = [&](int grp, bf16x8_t *dst) {
+                const int ks = grp >> 2, db0 = (grp & 3) * 4;
+                const int uo = ((4 * ks + g) ^ vsw) << 4;   // keys 32ks + 8g .. +7
 #pragma unroll
-            for (int ks = 0; ks < 2; ks++) {
-                const int u0 = ((4 * ks + (g >> 1)) ^ vsw) << 4, u1 = ((4 * ks + 2 + (g >> 1)) ^ vsw) << 4;
+                for (int j = 0; j < 4; j++)
+                    dst[j] = as_bf16x8(*(const uint4 *)(Vt + ((db0 + j) * 16 + n) * (KT * 2) + uo));
+            };
+            vload(0, vf[0]);
 #pragma unroll
-                for (int db = 0; db < 16; db++) {
-                    const char *vr = Vl + (db * 16 + n) * (KT * 2) + vhalf;
-                    const uint2 lo = *(const uint2 *)(vr + u0);
-                    const uint2 hi = *(const uint2 *)(vr + u1);
-                    const bf16x8_t vb = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+            for (int grp = 0; grp < 8; grp++) {
+                if (grp + 1 < 8) vload(grp + 1, vf[(grp + 1) & 1]);
+                __builtin_amdgcn_sched_barrier(0);
+                const int ks = grp >> 2, db0 = (grp & 3) * 4;
+#pragma unroll
+                for (int j = 0; j < 4; j++)
 #pragma unroll
                     for (int rb = 0; rb < RB; rb++)
-                        O[rb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rb][ks], vb, O[rb][db], 0, 0, 0);
-                }
+                        O[rb][db0 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rb][ks], vf[grp & 1][j], O[rb][db0 + j], 0, 0, 0);
+                __builtin_amdgcn_sched_barrier(0);
             }
         }
-        vx_lds_barrier();   // every wave is done with V(kt)
-        if (more) load_v<NW>(vl, Vc + (size_t)(kt + 1) * KBUF, wave, lane);
     }
 
     // out = O / l * sigmoid(gate)
@@ -418,27 +500,33 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     VX_REQUIRE(d->L >= 64 && d->L % 64 == 0, "vx27_hip_gqa_prefill: L must be a positive multiple of 64");
     VX_REQUIRE(d->pos0 >= 0 && (long long)d->pos0 + d->T <= d->L,
                "vx27_hip_gqa_prefill: positions [%d, %d) outside the cache (L=%d)", d->pos0, d->pos0 + d->T, d->L);
-    VX_REQUIRE(d->rope_dim >= 0 && d->rope_dim <= HDG, "vx27_hip_gqa_prefill: bad rope_dim");
+    VX_REQUIRE(d->rope_dim >= 0 && d->rope_dim <= HDG && d->rope_dim % 64 == 0,
+               "vx27_hip_gqa_prefill: rope_dim must be a multiple of 64 in [0, 256] (got %d)", d->rope_dim);
+    VX_REQUIRE((d->q_tok_stride == 0 || d->q_tok_stride % 8 == 0) && (d->q_head_stride == 0 || d->q_head_stride % 8 == 0) &&
+                   ((uintptr_t)d->q & 15) == 0,
+               "vx27_hip_gqa_prefill: q must be 16-byte aligned with strides that are multiples of 8 elements");
     VX_REQUIRE(d->q && d->gate && d->k_new && d->v_new && d->q_norm_w && d->k_norm_w && d->k_cache &&
                    d->v_cache && d->out,
                "vx27_hip_gqa_prefill: null pointer in descriptor");
-    PrepArgs pa = {};
-    if (d->rope_dim > 0 && vx_rope_fill(pa.rope, d->rope_dim, d->rope_theta)) return -1;
+    KvArgs ka = {};
+    if (d->rope_dim > 0 && vx_rope_fill(ka.rope, d->rope_dim, d->rope_theta)) return -1;
+    ka.T = d->T; ka.n_kv = d->n_kv; ka.rope_dim = d->rope_dim; ka.L = d->L; ka.pos0 = d->pos0;
+    ka.flags = d->flags; ka.yarn = d->rope_yarn < 1.0f ? 1.0f : d->rope_yarn;
+    ka.k = d->k_new; ka.v = d->v_new; ka.kv_ts = (size_t)d->n_kv * HDG;
+    ka.k_norm_w = d->k_norm_w; ka.k_cache = d->k_cache; ka.v_cache = d->v_cache;
     void *scr;
-    if (vx_ctx_scratch(ctx, (size_t)d->B * d->n_q * d->T * HDG * sizeof(uint16_t), &scr)) return -1;
-    pa.T = d->T; pa.n_q = d->n_q; pa.n_kv = d->n_kv; pa.rope_dim = d->rope_dim; pa.L = d->L;
-    pa.pos0 = d->pos0; pa.flags = d->flags; pa.yarn = d->rope_yarn < 1.0f ? 1.0f : d->rope_yarn;
-    pa.q = d->q; pa.k = d->k_new; pa.v = d->v_new;
-    pa.q_ts = d->q_tok_stride ? d->q_tok_stride : (size_t)d->n_q * HDG;
-    pa.q_hs = d->q_head_stride ? d->q_head_stride : HDG;
-    pa.kv_ts = (size_t)d->n_kv * HDG;
-    pa.q_norm_w = d->q_norm_w; pa.k_norm_w = d->k_norm_w;
-    pa.k_cache = d->k_cache; pa.v_cache = d->v_cache; pa.q_rot = (uint16_t *)scr;
-    VX_LAUNCH(ctx, gqp_prep, dim3((unsigned)d->T, (unsigned)d->B), dim3(256), pa);
+    if (vx_ctx_scratch(ctx, (size_t)d->T * (d->rope_dim / 2 + 1) * sizeof(float2), &scr)) return -1;
+    ka.cs_tab = (float2 *)scr;
+    VX_LAUNCH(ctx, gqp_kv, dim3((unsigned)d->T, (unsigned)d->B), dim3(256), ka);
 
     AttnArgs aa;
     aa.T = d->T; aa.n_q = d->n_q; aa.n_kv = d->n_kv; aa.L = d->L; aa.pos0 = d->pos0;
-    aa.q_rot = (const uint16_t *)scr; aa.k_cache = d->k_cache; aa.v_cache = d->v_cache;
+    aa.rope_dim = d->rope_dim; aa.flags = d->flags; aa.yarn = ka.yarn; aa.cs_tab = ka.cs_tab;
+    aa.q = d->q;
+    aa.q_ts = d->q_tok_stride ? d->q_tok_stride : (size_t)d->n_q * HDG;
+    aa.q_hs = d->q_head_stride ? d->q_head_stride : HDG;
+    aa.q_norm_w = d->q_norm_w;
+    aa.k_cache = d->k_cache; aa.v_cache = d->v_cache;
     aa.gate = d->gate;
     aa.g_ts = d->gate_tok_stride ? d->gate_tok_stride : (size_t)d->n_q * HDG;
     aa.g_hs = d->gate_head_stride ? d->gate_head_stride : HDG;
