@@ -52,7 +52,7 @@ struct KvArgs {
     int T, n_kv, rope_dim, L, pos0;
     unsigned flags;
     float yarn;
-    const uint16_t *k, *v;
+    const uint16_t *k, *v;        // [B][T][n_kv][256] (16-byte aligned rows)
     size_t kv_ts;                 // token stride (elements); head stride 256
     const float *k_norm_w;
     uint16_t *k_cache, *v_cache;
@@ -60,33 +60,78 @@ struct KvArgs {
     vx_rope_tab rope;
 };
 
-// grid (T, B), block 256: one workgroup per token, RoPE table once per
-// token, wave w handles KV heads w, w+4, ...; lane l holds dims l, l+64,
-// l+128, l+192
+// grid (32-position blocks touched, n_kv, B), block 256: one workgroup per
+// 32-position block of one KV head (the V cache's block: written as whole
+// 16-byte runs, element by element only at partial blocks, so positions
+// outside [pos0, pos0+T) keep their contents).  k: wave w takes the block's
+// tokens w, w+4, ...; lane l holds dims l, l+64, l+128, l+192.
+constexpr int VB = VX_GQA_VBLK;
 __global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
-    const int t = blockIdx.x, b = blockIdx.y;
+    const int hk = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    __shared__ float cs[VX_ROPE_MAXH], sn[VX_ROPE_MAXH];
-    __shared__ float row[4][HDG];
-    const int pos = a.pos0 + t;
+    const int p0 = (a.pos0 / VB + (int)blockIdx.x) * VB;        // first position of the block
+    const int lo = max(p0, a.pos0), hi = min(p0 + VB, a.pos0 + a.T);   // valid positions [lo, hi)
     const int half = a.rope_dim / 2;
-    if (tid < half) {
-        const float ang = ((float)pos / a.yarn) * a.rope.freq[tid];
-        cs[tid] = cosf(ang);
-        sn[tid] = sinf(ang);
-        if (b == 0) a.cs_tab[(size_t)t * half + tid] = make_float2(cs[tid], sn[tid]);
+    __shared__ float cs[VB][VX_ROPE_MAXH / 2], sn[VB][VX_ROPE_MAXH / 2];   // rope_dim <= 128 here
+    __shared__ __attribute__((aligned(16))) uint16_t vt[VB][HDG];         // the block's v rows
+    __shared__ float row[4][HDG];
+    // cos/sin of every (position, frequency) of the block
+    for (int e = tid; e < VB * half; e += 256) {
+        const int j = e / half, i = e % half, pos = p0 + j;
+        if (pos < lo || pos >= hi) continue;
+        const float ang = ((float)pos / a.yarn) * a.rope.freq[i];
+        cs[j][i] = cosf(ang);
+        sn[j][i] = sinf(ang);
+        if (b == 0 && hk == 0) a.cs_tab[(size_t)(pos - a.pos0) * half + i] = make_float2(cs[j][i], sn[j][i]);
+    }
+    // v rows of the block's tokens into LDS (16-byte chunks)
+    for (int e = tid; e < VB * (HDG / 8); e += 256) {
+        const int j = e / (HDG / 8), c = e % (HDG / 8), pos = p0 + j;
+        if (pos < lo || pos >= hi) continue;
+        const size_t tok = (size_t)b * a.T + (pos - a.pos0);
+        *(uint4 *)&vt[j][c * 8] = *(const uint4 *)(a.v + tok * a.kv_ts + (size_t)hk * HDG + c * 8);
     }
     __syncthreads();
-    const size_t tok = (size_t)b * a.T + t;
+    // V block [256 dims][32 positions]: thread -> (dim, 8 positions)
+    {
+        uint16_t *vb = a.v_cache + vx_v_index(a.n_kv, a.L, b, hk, p0, 0);
+        for (int e = tid; e < HDG * (VB / 8); e += 256) {
+            const int d = e / (VB / 8), c = e % (VB / 8);
+            const int q0 = p0 + c * 8;
+            if (q0 >= lo && q0 + 8 <= hi) {
+                uint16_t v8[8];
+#pragma unroll
+                for (int k = 0; k < 8; k++) v8[k] = vt[c * 8 + k][d];
+                *(uint4 *)(vb + (size_t)d * VB + c * 8) = make_uint4(v8[0] | ((uint32_t)v8[1] << 16), v8[2] | ((uint32_t)v8[3] << 16),
+                                                                     v8[4] | ((uint32_t)v8[5] << 16), v8[6] | ((uint32_t)v8[7] << 16));
+            } else {
+                for (int k = 0; k < 8; k++)
+                    if (q0 + k >= lo && q0 + k < hi) vb[(size_t)d * VB + c * 8 + k] = vt[c * 8 + k][d];
+            }
+        }
+    }
+    // k: rmsn + RoPE per token, one wave per token; the wave's 8 rows are
+    // loaded up front
     float *rw = row[wave];
-    for (int hk = wave; hk < a.n_kv; hk += 4) {
-        const uint16_t *src = a.k + tok * a.kv_ts + (size_t)hk * HDG;
+    uint16_t kraw[VB / 4][4];
+#pragma unroll
+    for (int jj = 0; jj < VB / 4; jj++) {
+        const int pos = p0 + wave + 4 * jj;
+        if (pos < lo || pos >= hi) continue;
+        const uint16_t *src = a.k + ((size_t)b * a.T + (pos - a.pos0)) * a.kv_ts + (size_t)hk * HDG;
+#pragma unroll
+        for (int e = 0; e < 4; e++) kraw[jj][e] = src[lane + 64 * e];
+    }
+#pragma unroll
+    for (int jj = 0; jj < VB / 4; jj++) {
+        const int j = wave + 4 * jj, pos = p0 + j;
+        if (pos < lo || pos >= hi) continue;   // wave-uniform
         float x[4];
         double ss = 0.0;
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            x[e] = vx_bf16_to_f32(src[lane + 64 * e]);
+            x[e] = vx_bf16_to_f32(kraw[jj][e]);
             ss += (double)x[e] * (double)x[e];
         }
         ss = vx_wave_sum_f64(ss);
@@ -98,18 +143,18 @@ __global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
             rw[lane + 64 * e] = x[e];
         }
         __builtin_amdgcn_wave_barrier();   // this wave's row writes before its partner reads
+        uint16_t *kc = a.k_cache + vx_k_index(a.n_kv, a.L, b, hk, pos, 0);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
             const int i = lane + 64 * e;
             float r = x[e];
             if (i < half)
-                r = rw[i] * cs[i] - rw[i + half] * sn[i];
+                r = rw[i] * cs[j][i] - rw[i + half] * sn[j][i];
             else if (i < 2 * half)
-                r = rw[i - half] * sn[i - half] + rw[i] * cs[i - half];
-            a.k_cache[vx_k_index(a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(r);
-            a.v_cache[vx_v_index(a.n_kv, a.L, b, hk, pos, i)] = a.v[tok * a.kv_ts + (size_t)hk * HDG + i];
+                r = rw[i - half] * sn[j][i - half] + rw[i] * cs[j][i - half];
+            kc[i] = vx_f32_to_bf16(r);
         }
-        __builtin_amdgcn_wave_barrier();   // reads of this row done before the next head's writes
+        __builtin_amdgcn_wave_barrier();   // reads of this row done before the next token's writes
     }
 }
 
@@ -500,11 +545,12 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     VX_REQUIRE(d->L >= 64 && d->L % 64 == 0, "vx27_hip_gqa_prefill: L must be a positive multiple of 64");
     VX_REQUIRE(d->pos0 >= 0 && (long long)d->pos0 + d->T <= d->L,
                "vx27_hip_gqa_prefill: positions [%d, %d) outside the cache (L=%d)", d->pos0, d->pos0 + d->T, d->L);
-    VX_REQUIRE(d->rope_dim >= 0 && d->rope_dim <= HDG && d->rope_dim % 64 == 0,
-               "vx27_hip_gqa_prefill: rope_dim must be a multiple of 64 in [0, 256] (got %d)", d->rope_dim);
+    VX_REQUIRE(d->rope_dim >= 0 && d->rope_dim <= VX_ROPE_MAXH && d->rope_dim % 64 == 0,
+               "vx27_hip_gqa_prefill: rope_dim must be a multiple of 64 in [0, %d] (got %d)", VX_ROPE_MAXH, d->rope_dim);
     VX_REQUIRE((d->q_tok_stride == 0 || d->q_tok_stride % 8 == 0) && (d->q_head_stride == 0 || d->q_head_stride % 8 == 0) &&
                    ((uintptr_t)d->q & 15) == 0,
                "vx27_hip_gqa_prefill: q must be 16-byte aligned with strides that are multiples of 8 elements");
+    VX_REQUIRE(((uintptr_t)d->v_new & 15) == 0, "vx27_hip_gqa_prefill: v_new must be 16-byte aligned");
     VX_REQUIRE(d->q && d->gate && d->k_new && d->v_new && d->q_norm_w && d->k_norm_w && d->k_cache &&
                    d->v_cache && d->out,
                "vx27_hip_gqa_prefill: null pointer in descriptor");
@@ -517,7 +563,10 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     void *scr;
     if (vx_ctx_scratch(ctx, (size_t)d->T * (d->rope_dim / 2 + 1) * sizeof(float2), &scr)) return -1;
     ka.cs_tab = (float2 *)scr;
-    VX_LAUNCH(ctx, gqp_kv, dim3((unsigned)d->T, (unsigned)d->B), dim3(256), ka);
+    {
+        const int nblk = (d->pos0 + d->T - 1) / VX_GQA_VBLK - d->pos0 / VX_GQA_VBLK + 1;
+        VX_LAUNCH(ctx, gqp_kv, dim3((unsigned)nblk, (unsigned)d->n_kv, (unsigned)d->B), dim3(256), ka);
+    }
 
     AttnArgs aa;
     aa.T = d->T; aa.n_q = d->n_q; aa.n_kv = d->n_kv; aa.L = d->L; aa.pos0 = d->pos0;
