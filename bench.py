@@ -269,7 +269,11 @@ def bench_dn_conv(ctx, steps, warmup, B=64, H=16, cpu=True):
         L.check(fn(ctx.h, C.byref(descs[t])), "dn_decode")
     ctx.sync()
     wall = time.perf_counter() - t0
-    n, ms = ctx.prof_read("dn_decode_kernel")
+    kname = "dn_step_kernel"   # one step per call: the single-step kernel (conv and gates fused)
+    n, ms = ctx.prof_read(kname)
+    if n == 0:
+        kname = "dn_decode_kernel"
+        n, ms = ctx.prof_read(kname)
     ng, msg = ctx.prof_read("dn_gate_kernel")
     ctx.prof_enable(False)
     # algorithmic bytes of the decode kernel per launch (one step of B sequences)
@@ -283,7 +287,7 @@ def bench_dn_conv(ctx, steps, warmup, B=64, H=16, cpu=True):
         "workload": f"dn_conv B={B} heads={H} hd=128 conv=6144ch bf16w, {steps} steps",
         "us_per_step": wall / steps * 1e6,
         "us_per_token": wall / steps / B * 1e6,
-        "kernel": "dn_decode_kernel", "kernel_us": avg_s * 1e6,
+        "kernel": kname, "kernel_us": avg_s * 1e6,
         "gate_kernel_us": msg / max(ng, 1) * 1e3,
         "alg_bytes": alg, "achieved_GBs": alg / avg_s / 1e9,
     }

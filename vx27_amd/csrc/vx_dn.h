@@ -82,7 +82,10 @@ struct DnArgs {
     const float *x;
     const float *q, *k, *v;
     size_t q_tok, k_tok, v_tok;   // per-(t,b) stride of q, k, v in floats
-    const double2 *gates;         // [steps][B][nv] (beta, decay)
+    const double2 *gates;         // [steps][B][nv] (beta, decay); NULL: the step kernel
+                                  // maps ga, gb (one step) itself
+    const float *ga, *gb;         // raw gate inputs [B][nv] (vx27_deltanet_gate_params's a, b)
+    const float *A_log, *dt_bias; // [nv]
     const float *norm_w, *z;
     size_t z_tok;                 // per-(t,b) stride of z
     float *out;                   // may be NULL when out_packed is set
@@ -96,3 +99,6 @@ struct DnArgs {
 
 // Launch the recurrence (one or more workgroups per (sequence, value head)).
 int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a);
+// Whether vx_dn_recurrence runs a call as one single-step kernel (which can
+// also map the gates itself, with gates == NULL).
+bool vx_dn_single_step(const DnArgs &a);

@@ -248,9 +248,10 @@ __global__ __launch_bounds__(HD / CS * R) void dn_decode_kernel(DnArgs a) {
     }
 }
 
-// One step without the fused conv (q, k given: final with VX_DN_QK_READY,
-// else normalised here per the flags): one block of 512 lanes per (sequence,
-// value head).  Lane (part = tid / 32, c4 = tid % 32)
+// One step (q, k given or, with the fused conv (nv == nqk), convolved here
+// from x; final with VX_DN_QK_READY, else normalised here per the flags;
+// gates given, or mapped here from a, b): one block of 512 lanes per
+// (sequence, value head).  Lane (part = tid / 32, c4 = tid % 32)
 // holds state rows 8 part .. 8 part + 7 of columns 4 c4 .. 4 c4 + 3, so each
 // wave reads and writes two whole 512-byte state rows per instruction, and
 // all of a lane's state loads are in flight before any other work.  The
@@ -270,9 +271,36 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
 
     float va = 0.0f, qa = 0.0f, ka = 0.0f;
     if (tid < HD) {
-        qa = a.q[(size_t)b * a.q_tok + (size_t)g * HD + tid];
-        ka = a.k[(size_t)b * a.k_tok + (size_t)g * HD + tid];
-        va = a.v[(size_t)b * a.v_tok + (size_t)vh * HD + tid];
+        if (a.fused_conv) {   // causal conv + SiLU of this head's q, k, v channels (nv == nqk: g == vh)
+            const int qd = a.nqk * HD, C = 2 * qd + a.nv * HD;
+            const size_t chq = (size_t)g * HD + tid, chk = (size_t)qd + g * HD + tid,
+                         chv = (size_t)2 * qd + (size_t)vh * HD + tid;
+            const float *x = a.x + (size_t)b * C;
+            float *cst = a.conv_state + (size_t)b * C * 3;
+            float wq[4], wk[4], wv[4], cq[3], ck[3], cv[3];
+            load_conv_w(a.conv_w, a.conv_bf16, chq, wq);
+            load_conv_w(a.conv_w, a.conv_bf16, chk, wk);
+            load_conv_w(a.conv_w, a.conv_bf16, chv, wv);
+#pragma unroll
+            for (int t = 0; t < 3; t++) {
+                cq[t] = cst[chq * 3 + t];
+                ck[t] = cst[chk * 3 + t];
+                cv[t] = cst[chv * 3 + t];
+            }
+            qa = conv_step(cq, wq, x[chq]);
+            ka = conv_step(ck, wk, x[chk]);
+            va = conv_step(cv, wv, x[chv]);
+#pragma unroll
+            for (int t = 0; t < 3; t++) {
+                cst[chq * 3 + t] = cq[t];
+                cst[chk * 3 + t] = ck[t];
+                cst[chv * 3 + t] = cv[t];
+            }
+        } else {
+            qa = a.q[(size_t)b * a.q_tok + (size_t)g * HD + tid];
+            ka = a.k[(size_t)b * a.k_tok + (size_t)g * HD + tid];
+            va = a.v[(size_t)b * a.v_tok + (size_t)vh * HD + tid];
+        }
     }
     const bool gate = (a.flags & VX27_DN_OUT_GATE) != 0;
     float z0 = 0.f, z1 = 0.f, w0 = 1.f, w1 = 1.f;
@@ -284,8 +312,16 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
             w1 = a.norm_w[lane + 64];
         }
     }
-    const double2 gt = a.gates[(size_t)b * a.nv + vh];   // uniform address: scalar load
-    const double beta = gt.x, decay = gt.y;
+    double beta, decay;
+    if (a.gates) {
+        const double2 gt = a.gates[(size_t)b * a.nv + vh];   // uniform address: scalar load
+        beta = gt.x;
+        decay = gt.y;
+    } else {   // vx27_deltanet_gate_params (vx27_deltanet.c:65-69), decay = exp(g_log)
+        const size_t e = (size_t)b * a.nv + vh;
+        beta = 1.0 / (1.0 + exp(-(double)a.gb[e]));
+        decay = exp(-exp((double)a.A_log[vh]) * softplus_d((double)a.ga[e] + (double)a.dt_bias[vh]));
+    }
     // state loads after the small ones: those return first (loads complete in
     // order), so the q/k hand-off below overlaps the state's arrival
     float *Sg = a.S + ((size_t)b * a.nv + vh) * HD * HD + (size_t)(8 * part) * HD + 4 * c4;
@@ -469,6 +505,13 @@ __global__ __launch_bounds__(256) void dn_conv_kernel(ConvArgs a) {
 
 }  // namespace
 
+bool vx_dn_single_step(const DnArgs &a) {
+#ifndef VX_DN_STEP
+#define VX_DN_STEP 1
+#endif
+    return VX_DN_STEP && a.steps == 1 && ((uintptr_t)a.S & 15) == 0;
+}
+
 int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a) {
     VX_REQUIRE(!a.fused_conv || a.nv == a.nqk, "dn recurrence: fused conv needs nv == nqk");
     // Spread few heads over the 256 CUs: split each head's columns over CS
@@ -477,13 +520,11 @@ int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a) {
     // column's rows over R lanes of one workgroup.
     const int heads = a.B * a.nv;
     const bool gate = (a.flags & VX27_DN_OUT_GATE) != 0;
-#ifndef VX_DN_STEP
-#define VX_DN_STEP 1
-#endif
-    if (VX_DN_STEP && a.steps == 1 && !a.fused_conv && ((uintptr_t)a.S & 15) == 0) {
+    if (vx_dn_single_step(a)) {
         VX_LAUNCH(ctx, dn_step_kernel, dim3((unsigned)heads), dim3(512), a);
         return 0;
     }
+    VX_REQUIRE(a.gates != nullptr, "internal: the multi-step recurrence needs mapped gates");
     // (With the output gate, one workgroup per head keeps the norm in the
     // kernel; splitting would need the dn_out_gate launch, which costs more
     // than the split gains.)
@@ -568,8 +609,12 @@ extern "C" int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d) {
     if (vx_ctx_scratch(ctx, gate_bytes + opre_bytes + act_elems * sizeof(float), &scr)) return -1;
     double2 *gates = (double2 *)scr;
     a.o_pre = (float *)((char *)scr + gate_bytes);
-    VX_LAUNCH(ctx, dn_gate_kernel, dim3((unsigned)((n_gate + 255) / 256)), dim3(256), (int)n_gate, d->nv, d->a, d->b, d->A_log, d->dt_bias, gates);
-    a.gates = gates;
+    a.ga = d->a; a.gb = d->b; a.A_log = d->A_log; a.dt_bias = d->dt_bias;
+    if (!vx_dn_single_step(a)) {
+        VX_LAUNCH(ctx, dn_gate_kernel, dim3((unsigned)((n_gate + 255) / 256)), dim3(256), (int)n_gate, d->nv, d->a,
+                  d->b, d->A_log, d->dt_bias, gates);
+        a.gates = gates;
+    }
     if (sep_conv) {
         // shared q/k channels: convolve all channels first
         float *act = (float *)((char *)scr + gate_bytes + opre_bytes);
