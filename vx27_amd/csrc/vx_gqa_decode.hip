@@ -139,6 +139,9 @@ __device__ __forceinline__ bf16x8_t load_bf16x8(const uint16_t *p) {
 #ifndef VX_SPLIT_WAVES
 #define VX_SPLIT_WAVES 2048  // target split waves per launch
 #endif
+#ifndef VX_SPLIT_MINT
+#define VX_SPLIT_MINT 4      // at least this many key tiles per split wave
+#endif
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(VX_SPLIT_WPE))) void gqa_split(SplitArgs a) {
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
     const int lane = threadIdx.x, g = lane >> 4, n = lane & 15;
@@ -364,10 +367,11 @@ static int gqa_check(const vx27_gqa_desc *d) {
 static int gqa_n_split(const vx27_gqa_desc *d) {
     int n_split = d->n_split;
     if (n_split <= 0) {
-        // ~VX_SPLIT_WAVES waves over all (sequence, KV head) pairs, at least 4 tiles per wave
+        // ~VX_SPLIT_WAVES waves over all (sequence, KV head) pairs, at least
+        // VX_SPLIT_MINT tiles per wave
         const int tiles = d->L / TILE;
         n_split = (VX_SPLIT_WAVES + d->B * d->n_kv - 1) / (d->B * d->n_kv);
-        if (n_split > (tiles + 3) / 4) n_split = (tiles + 3) / 4;
+        if (n_split > (tiles + VX_SPLIT_MINT - 1) / VX_SPLIT_MINT) n_split = (tiles + VX_SPLIT_MINT - 1) / VX_SPLIT_MINT;
         if (n_split < 1) n_split = 1;
     }
     return n_split;
