@@ -351,10 +351,10 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
         const bool more = kt + 1 < n_tiles;
         const bool live = k0 <= wave_last;   // wave-uniform: otherwise every key here is masked
         const char *Kt = Kl[cur], *Vt = Vl[cur];
-        // K(kt) landed: issued after it is only V(kt) (PER instructions per
-        // wave); the barrier also means every wave is done with tile kt-1,
-        // whose buffers take tile kt+1 now
-        __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(PER) : "memory");
+        // K(kt) and V(kt) landed (nothing is issued after them yet); the
+        // barrier also means every wave is done with tile kt-1, whose buffers
+        // take tile kt+1 now
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
         vx_lds_barrier();
         if (more) {
             load_k<NW>(vx_lds_addr(Kl[cur ^ 1]), Kc + (size_t)(kt + 1) * KBUF, wave, lane);
@@ -463,13 +463,6 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
             }
         }
 
-        // V(kt) landed: issued after it are K(kt+1) and V(kt+1) when there is
-        // a next tile
-        if (more)
-            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PER) : "memory");
-        else
-            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        vx_lds_barrier();
         if (k0 + KT > n_keys) {
             // last tile: V of positions past the valid keys is zeroed (masked P
             // is 0, and 0 * a stale NaN would not be)
@@ -481,7 +474,7 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
                     V[d * KT + u * 8 + (key & 7)] = 0;
                 }
             }
-            vx_lds_barrier();
+            vx_lds_barrier();   // (workgroup-uniform: every wave takes this branch)
         }
         if (live) {
             // groups of 4 dim blocks: the V operands of group j+1 are read
