@@ -41,11 +41,15 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 constexpr int HDG = VX_GQA_HD;
-constexpr int QT = 128;     // queries per workgroup
 #ifndef GQP_NW
-#define GQP_NW 8            // waves per attention workgroup (128/NW queries each)
+#define GQP_NW 8            // waves per attention workgroup
 #endif
-#define GQP_RB (QT / 16 / GQP_NW)
+#ifndef GQP_RB
+#define GQP_RB 1            // 16-query blocks per wave
+#endif
+#ifndef GQP_DB
+#define GQP_DB 1            // double-buffered K/V tiles (else one buffer, two workgroups per CU)
+#endif
 constexpr int KT = 64;      // keys per tile
 
 struct KvArgs {
@@ -225,9 +229,9 @@ __device__ __forceinline__ void load_v(uint32_t vbuf, const char *Vt, int wave, 
 }
 
 // grid (ceil(T/128) * n_q, B), block NW*64: NW waves of RB 16-query blocks
-template <int NW, int RB>
+template <int NW, int RB, bool DB>
 __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
-    static_assert(NW * RB * 16 == QT, "a workgroup covers QT queries");
+    constexpr int QT = NW * RB * 16;   // queries per workgroup
     constexpr int PER = 32 / NW;   // direct-to-LDS instructions per wave for one K or V tile
     // Workgroups go round-robin over the 8 XCDs (each with its own L2).  With
     // xcd_map, XCD x takes the query heads of KV head x / (8 / n_kv), so an
@@ -248,10 +252,12 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: LDS bases go to M0
     const int r0 = qt * QT + wave * (RB * 16);                 // this wave's first query (token index)
 
-    // two K and two V tile buffers: tile kt+1 streams into one pair while
-    // tile kt is read from the other
-    __shared__ __attribute__((aligned(16))) char Kl[2][KBUF];
-    __shared__ __attribute__((aligned(16))) char Vl[2][KBUF];
+    // DB: two K and two V tile buffers, tile kt+1 streams into one pair while
+    // tile kt is read from the other.  Otherwise one pair (64 KiB, so two
+    // workgroups share a CU and one's softmax overlaps the other's MFMAs),
+    // refilled once every wave is done with it.
+    __shared__ __attribute__((aligned(16))) char Kl[DB ? 2 : 1][KBUF];
+    __shared__ __attribute__((aligned(16))) char Vl[DB ? 2 : 1][KBUF];
 
     const int n_keys = a.pos0 + a.T;                           // valid cache positions
     const int wg_last = a.pos0 + min(qt * QT + QT, a.T) - 1;   // last key any row here sees
@@ -347,7 +353,7 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
     }
 
     for (int kt = 0; kt < n_tiles; kt++) {
-        const int k0 = kt * KT, cur = kt & 1;
+        const int k0 = kt * KT, cur = DB ? (kt & 1) : 0;
         const bool more = kt + 1 < n_tiles;
         const bool live = k0 <= wave_last;   // wave-uniform: otherwise every key here is masked
         const char *Kt = Kl[cur], *Vt = Vl[cur];
@@ -356,7 +362,7 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
         // take tile kt+1 now
         __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
         vx_lds_barrier();
-        if (more) {
+        if (DB && more) {
             load_k<NW>(vx_lds_addr(Kl[cur ^ 1]), Kc + (size_t)(kt + 1) * KBUF, wave, lane);
             load_v<NW>(vx_lds_addr(Vl[cur ^ 1]), Vc + (size_t)(kt + 1) * KBUF, wave, lane);
         }
@@ -502,6 +508,11 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
                 __builtin_amdgcn_sched_barrier(0);
             }
         }
+        if (!DB && more) {   // every wave is done with the one buffer pair: refill it
+            vx_lds_barrier();
+            load_k<NW>(vx_lds_addr(Kl[0]), Kc + (size_t)(kt + 1) * KBUF, wave, lane);
+            load_v<NW>(vx_lds_addr(Vl[0]), Vc + (size_t)(kt + 1) * KBUF, wave, lane);
+        }
     }
 
     // out = O / l * sigmoid(gate)
@@ -575,8 +586,9 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     aa.out = d->out;
     // XCD grouping needs whole KV heads per XCD pair set: n_kv | 8 and 8 | n_q
     aa.xcd_map = (8 % d->n_kv == 0) && (d->n_q % 8 == 0) && ((d->n_q / 8) * (8 / d->n_kv) == d->n_q / d->n_kv);
+    constexpr int QT = GQP_NW * GQP_RB * 16;
     const int n_qt = (d->T + QT - 1) / QT;
-    VX_LAUNCH_NAMED(ctx, "gqp_attn", (gqp_attn<GQP_NW, GQP_RB>), dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B),
+    VX_LAUNCH_NAMED(ctx, "gqp_attn", (gqp_attn<GQP_NW, GQP_RB, GQP_DB != 0>), dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B),
                     dim3(GQP_NW * 64), aa);
     return 0;
 }
