@@ -325,11 +325,6 @@ struct ScanArgs {
     float *out;      // [B][T][nv][128]
 };
 
-struct ChunkOps {
-    uint4 nw[4], qe[4], kt[4], pp[2];
-    float4 ut;
-};
-
 // A wave's operands of one chunk: 15 tiles of 1 KiB in its record, staged in
 // LDS in this order: -W (rows 16w..16w+15, 4 k-steps), e^gam Q (same rows),
 // Kt^T (row blocks 2w, 2w+1, 2 k-steps each), P (rows 16w.., 2 k-steps) and
@@ -356,19 +351,6 @@ __device__ __forceinline__ void fetch_ops(const char *rec, uint32_t lds, int wav
     for (int j = 0; j < OPS_TILES; j++)
         vx_dma16(rec, ops_src(j, wave, slice) + (uint32_t)lane * 16, lds + (uint32_t)j * 1024);
     vx_dma4(rec, (uint32_t)R_GC + (uint32_t)lane * 4, lds + OPS_TILES * 1024);
-}
-
-__device__ __forceinline__ void read_ops(ChunkOps &o, const uint4 *t) {
-#pragma unroll
-    for (int ks = 0; ks < 4; ks++) {
-        o.nw[ks] = t[ks * 64];
-        o.qe[ks] = t[(4 + ks) * 64];
-        o.kt[ks] = t[(8 + ks) * 64];
-    }
-    o.pp[0] = t[12 * 64];
-    o.pp[1] = t[13 * 64];
-    const uint4 u = t[14 * 64];
-    o.ut = make_float4(__uint_as_float(u.x), __uint_as_float(u.y), __uint_as_float(u.z), __uint_as_float(u.w));
 }
 
 __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
@@ -406,65 +388,78 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
     __asm__ volatile("" ::"v"(S[0]), "v"(S[1]));
 
     for (int c = 0; c < p.NC; c++) {
-        // chunk c's loads have landed once at most the loads of chunk c+1 are
-        // still outstanding (loads complete in issue order)
-        if (c + 1 < p.NC)
-            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(OPS_LOADS) : "memory");
-        else
-            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        ChunkOps cur;
-        const char *slot = &ops_l[c & 1][wave * OPS_WAVE];
-        read_ops(cur, (const uint4 *)slot + lane);
-        const float gc = *(const float *)(slot + OPS_TILES * 1024);
-        // the slot is free once the reads have returned: refill it with chunk c+2
-        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (c + 2 < p.NC) fetch_ops(rec0 + (size_t)(c + 2) * REC, ops_w + (uint32_t)(c & 1) * OPS_BUF, wave, slice, lane);
-
+        // The chunk's dependent chain S -> U -> S' starts at once; the operand
+        // reads go into its shadow (before the barrier whose far side needs
+        // them), and chunk c+2's loads start once this slot is read out.
         // S (bf16) -> LDS as [column][key dim]
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int d = (2 * wave + r) * 16 + 4 * g;
             *(uint2 *)&S_l[n][d] = make_uint2(pack2(S[r][0], S[r][1]), pack2(S[r][2], S[r][3]));
         }
-        vx_lds_barrier();
+        // chunk c's loads have landed once at most the loads of chunk c+1 are
+        // still outstanding (loads complete in issue order)
+        if (c + 1 < p.NC)
+            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(OPS_LOADS) : "memory");
+        else
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        const char *slot = &ops_l[c & 1][wave * OPS_WAVE];
+        const uint4 *t = (const uint4 *)slot + lane;
+        uint4 nw[4], qe[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            nw[ks] = t[ks * 64];
+            qe[ks] = t[(4 + ks) * 64];
+        }
+        const uint4 utu = t[14 * 64];
+        const float gc = *(const float *)(slot + OPS_TILES * 1024);
+        vx_lds_barrier();   // S_l complete (and this wave's operand reads returned)
         bf16x8_t sb[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) sb[ks] = as_bf16x8(*(const uint4 *)&S_l[n][32 * ks + 8 * g]);
         // U = Ut - W S for tokens 16w .. 16w+15, and the e^gam Q S part of O,
         // as independent two-MFMA chains (the dependent-MFMA latency, not the
         // issue rate, bounds this loop)
-        floatx4_t U0 = (floatx4_t){cur.ut.x, cur.ut.y, cur.ut.z, cur.ut.w}, U1 = {0.f, 0.f, 0.f, 0.f};
+        floatx4_t U0 = (floatx4_t){__uint_as_float(utu.x), __uint_as_float(utu.y), __uint_as_float(utu.z), __uint_as_float(utu.w)};
+        floatx4_t U1 = {0.f, 0.f, 0.f, 0.f};
         floatx4_t O0 = {0.f, 0.f, 0.f, 0.f}, O1 = {0.f, 0.f, 0.f, 0.f};
-        U0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.nw[0]), sb[0], U0, 0, 0, 0);
-        U1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.nw[1]), sb[1], U1, 0, 0, 0);
-        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.qe[0]), sb[0], O0, 0, 0, 0);
-        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.qe[1]), sb[1], O1, 0, 0, 0);
-        U0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.nw[2]), sb[2], U0, 0, 0, 0);
-        U1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.nw[3]), sb[3], U1, 0, 0, 0);
-        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.qe[2]), sb[2], O0, 0, 0, 0);
-        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.qe[3]), sb[3], O1, 0, 0, 0);
+        U0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(nw[0]), sb[0], U0, 0, 0, 0);
+        U1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(nw[1]), sb[1], U1, 0, 0, 0);
+        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qe[0]), sb[0], O0, 0, 0, 0);
+        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qe[1]), sb[1], O1, 0, 0, 0);
+        U0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(nw[2]), sb[2], U0, 0, 0, 0);
+        U1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(nw[3]), sb[3], U1, 0, 0, 0);
+        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qe[2]), sb[2], O0, 0, 0, 0);
+        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qe[3]), sb[3], O1, 0, 0, 0);
         const floatx4_t U = U0 + U1;
         *(uint2 *)&U_l[n][wave * 16 + 4 * g] = make_uint2(pack2(U[0], U[1]), pack2(U[2], U[3]));
-        vx_lds_barrier();
+        uint4 kt[4], pp[2];
+#pragma unroll
+        for (int j = 0; j < 4; j++) kt[j] = t[(8 + j) * 64];
+        pp[0] = t[12 * 64];
+        pp[1] = t[13 * 64];
+        vx_lds_barrier();   // U_l complete; every read of this slot has returned
+        // the slot is free: refill it with chunk c+2
+        if (c + 2 < p.NC) fetch_ops(rec0 + (size_t)(c + 2) * REC, ops_w + (uint32_t)(c & 1) * OPS_BUF, wave, slice, lane);
         bf16x8_t ub[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) ub[ks] = as_bf16x8(*(const uint4 *)&U_l[n][32 * ks + 8 * g]);
         // O += P U (two more independent MFMAs), then the two chains merge
-        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.pp[0]), ub[0], O0, 0, 0, 0);
-        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.pp[1]), ub[1], O1, 0, 0, 0);
+        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pp[0]), ub[0], O0, 0, 0, 0);
+        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pp[1]), ub[1], O1, 0, 0, 0);
         // S = e^gam_C S + Kt^T U: per row block, two independent MFMAs
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             floatx4_t Sa = S[r] * gc, Sb = {0.f, 0.f, 0.f, 0.f};
-            Sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.kt[2 * r]), ub[0], Sa, 0, 0, 0);
-            Sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(cur.kt[2 * r + 1]), ub[1], Sb, 0, 0, 0);
+            Sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kt[2 * r]), ub[0], Sa, 0, 0, 0);
+            Sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kt[2 * r + 1]), ub[1], Sb, 0, 0, 0);
             S[r] = Sa + Sb;
         }
         const floatx4_t O = O0 + O1;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            const int t = c * CH + wave * 16 + 4 * g + i;
-            if (t < p.T) p.out[(((size_t)b * p.T + t) * p.nv + vh) * HD + col] = O[i];
+            const int tt = c * CH + wave * 16 + 4 * g + i;
+            if (tt < p.T) p.out[(((size_t)b * p.T + tt) * p.nv + vh) * HD + col] = O[i];
         }
     }
 #pragma unroll
