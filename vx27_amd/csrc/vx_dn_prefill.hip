@@ -343,14 +343,22 @@ __device__ __forceinline__ uint32_t ops_src(int j, int wave, int slice) {
                     : (uint32_t)(R_UT + (wave * 8 + slice) * 1024);
 }
 
-// Starts the wave's 15 direct-to-LDS tile loads of record `rec` into its
-// slot at LDS address `lds`.  Each wave reads back only what it loaded
-// itself, so the hand-off needs this wave's vmcnt wait and no barrier.
+// Starts group q (0..3) of the wave's 16 direct-to-LDS loads of record
+// `rec` into its slot at LDS address `lds` (tiles 4q .. 4q+3, the last
+// group ending with the record's final 256 bytes).  Each wave reads back only
+// what it loaded itself, so the hand-off needs this wave's vmcnt wait and no
+// barrier.  The groups are issued at spread-out points of a chunk step: the
+// load path drains 60 KiB per chunk per CU, and issuing all of it at once
+// stalls the wave.
+__device__ __forceinline__ void fetch_ops(const char *rec, uint32_t lds, int wave, int slice, int lane, int q) {
+#pragma unroll
+    for (int j = 4 * q; j < 4 * q + 4 && j < OPS_TILES; j++)
+        vx_dma16(rec, ops_src(j, wave, slice) + (uint32_t)lane * 16, lds + (uint32_t)j * 1024);
+    if (q == 3) vx_dma4(rec, (uint32_t)R_GC + (uint32_t)lane * 4, lds + OPS_TILES * 1024);
+}
 __device__ __forceinline__ void fetch_ops(const char *rec, uint32_t lds, int wave, int slice, int lane) {
 #pragma unroll
-    for (int j = 0; j < OPS_TILES; j++)
-        vx_dma16(rec, ops_src(j, wave, slice) + (uint32_t)lane * 16, lds + (uint32_t)j * 1024);
-    vx_dma4(rec, (uint32_t)R_GC + (uint32_t)lane * 4, lds + OPS_TILES * 1024);
+    for (int q = 0; q < 4; q++) fetch_ops(rec, lds, wave, slice, lane, q);
 }
 
 __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
@@ -397,12 +405,18 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
             const int d = (2 * wave + r) * 16 + 4 * g;
             *(uint2 *)&S_l[n][d] = make_uint2(pack2(S[r][0], S[r][1]), pack2(S[r][2], S[r][3]));
         }
-        // chunk c's loads have landed once at most the loads of chunk c+1 are
-        // still outstanding (loads complete in issue order)
+        // chunk c's loads have landed once at most the loads issued after its
+        // last group are still outstanding: groups 0 and 1 of chunk c+1 (8
+        // loads; loads complete in issue order)
         if (c + 1 < p.NC)
-            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(OPS_LOADS) : "memory");
+            __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
         else
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // groups 2 and 3 of chunk c+1 go out in this step's first half
+        const bool fill1 = c >= 1 && c + 1 < p.NC;   // (chunks 0 and 1 are loaded whole up front)
+        const char *rec1 = rec0 + (size_t)(c + 1) * REC;
+        const uint32_t slot1 = ops_w + (uint32_t)((c + 1) & 1) * OPS_BUF;
+        if (fill1) fetch_ops(rec1, slot1, wave, slice, lane, 2);
         const char *slot = &ops_l[c & 1][wave * OPS_WAVE];
         const uint4 *t = (const uint4 *)slot + lane;
         uint4 nw[4], qe[4];
@@ -414,6 +428,7 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
         const uint4 utu = t[14 * 64];
         const float gc = *(const float *)(slot + OPS_TILES * 1024);
         vx_lds_barrier();   // S_l complete (and this wave's operand reads returned)
+        if (fill1) fetch_ops(rec1, slot1, wave, slice, lane, 3);
         bf16x8_t sb[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) sb[ks] = as_bf16x8(*(const uint4 *)&S_l[n][32 * ks + 8 * g]);
@@ -439,14 +454,19 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
         pp[0] = t[12 * 64];
         pp[1] = t[13 * 64];
         vx_lds_barrier();   // U_l complete; every read of this slot has returned
-        // the slot is free: refill it with chunk c+2
-        if (c + 2 < p.NC) fetch_ops(rec0 + (size_t)(c + 2) * REC, ops_w + (uint32_t)(c & 1) * OPS_BUF, wave, slice, lane);
+        // the slot is free: refill it with chunk c+2, groups 0 and 1 in this
+        // step, 2 and 3 in the next
+        const bool refill = c + 2 < p.NC;
+        const char *rec2 = rec0 + (size_t)(c + 2) * REC;
+        const uint32_t slot2 = ops_w + (uint32_t)(c & 1) * OPS_BUF;
+        if (refill) fetch_ops(rec2, slot2, wave, slice, lane, 0);
         bf16x8_t ub[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) ub[ks] = as_bf16x8(*(const uint4 *)&U_l[n][32 * ks + 8 * g]);
         // O += P U (two more independent MFMAs), then the two chains merge
         O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pp[0]), ub[0], O0, 0, 0, 0);
         O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pp[1]), ub[1], O1, 0, 0, 0);
+        if (refill) fetch_ops(rec2, slot2, wave, slice, lane, 1);
         // S = e^gam_C S + Kt^T U: per row block, two independent MFMAs
 #pragma unroll
         for (int r = 0; r < 2; r++) {
