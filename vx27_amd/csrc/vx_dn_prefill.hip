@@ -40,9 +40,6 @@ typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 constexpr int CH = 64;            // chunk length
 constexpr int NSLICE = 8;         // 16-column slices of a head's state
-constexpr int KP = HD + 4;        // padded fp32 row of kn in LDS
-constexpr int QP = HD + 8;        // padded bf16 row of qn in LDS
-constexpr int PP = CH + 8;        // padded bf16 row of P in LDS
 
 // chunk record (bytes)
 constexpr size_t R_NW = 0;                       // -W   [4][4][64][8] bf16
@@ -79,19 +76,62 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 u) {
     return r;
 }
 
+// LDS of dnp_prep, one byte array carved into regions whose contents change
+// with the phase:
+//   R1: raw q rows [64][RP] bf16  -> P staging [64][TP] bf16 -> T [64][64] fp32
+//   R2: raw k rows [64][RP] bf16  -> V^T [128][TP] bf16     -> -W staging [64][RP] bf16
+//   KTR: K^T [128][TP] bf16 (raw k, dims x tokens)
+//   AS: A [64][AP] fp32; MT: level products [3][16][16] fp32; then per-token scalars
+constexpr int RP = HD + 8;     // padded bf16 row of 128 elements
+constexpr int TP = CH + 8;     // padded bf16 row of 64 elements
+constexpr int AP = CH + 4;     // padded fp32 row of A
+constexpr int L_R1 = 0;
+constexpr int L_R2 = L_R1 + CH * RP * 2;
+constexpr int L_KT = L_R2 + HD * TP * 2;
+constexpr int L_AS = L_KT + HD * TP * 2;
+constexpr int L_MT = L_AS + CH * AP * 4;
+constexpr int L_GAM = L_MT + 3 * 256 * 4;
+constexpr int L_SC = L_GAM + CH * 8;            // 5 float[64]: beta, e^gam, e^(gamC-gam), 1/|q|, 1/|k|
+constexpr int L_TOTAL = L_SC + 5 * CH * 4;
+static_assert(CH * 64 * 4 <= CH * RP * 2, "T fits region R1");
+
+// One workgroup per (chunk of 64 tokens, value head, sequence):
+//   phase 1  gates and the cumulative log-decay (wave 0); raw k rows, K^T and
+//            1/|k| (wave 1); raw q rows and 1/|q| (wave 2); v rows (wave 3)
+//   phase 2  K K^T and Q K^T on MFMA (raw bf16 rows, norms applied after);
+//            e^gam Q and Kt^T operand tiles
+//   phase 3  A = beta e^(gam_s - gam_r) kn_s.kn_r (r < s), P operand tiles;
+//            V^T in LDS
+//   phase 4  T = (I + A)^-1, blocked: the four 16x16 diagonal blocks by
+//            forward substitution, then T_ij = -T_ii sum_k A_ik T_kj level by
+//            level (fp32)
+//   phase 5  [Ut | W] = T [beta V | beta e^gam kn] on MFMA, as
+//            (T diag(beta)) V and (T diag(beta e^gam /|k|)) K with V, K the
+//            raw bf16 inputs (exact operands) and the scaled T split into
+//            bf16 hi + lo (a 16-bit-significand product, fp32 sums)
 __global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
     const int c = blockIdx.x, vh = blockIdx.y, b = blockIdx.z;
-    const int tid = threadIdx.x, wave = tid >> 6, lane = tid & 63, g = lane >> 4, m = lane & 15;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, m = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int qh = vh * p.nqk / p.nv;
     const int t0 = c * CH;
     const int nvalid = min(CH, p.T - t0);
 
-    __shared__ float kn_f[CH][KP];        // kn (fp32); later -W
-    __shared__ uint16_t qn_b[CH][QP];     // qn (bf16); later P (bf16, row stride PP); later v
-    __shared__ float A_s[CH][CH];
-    __shared__ double gam_s[CH];
-    __shared__ float beta_s[CH], eg_s[CH], egc_s[CH];   // beta, e^gam_t, e^(gam_C - gam_t)
+    __shared__ __attribute__((aligned(16))) char smem[L_TOTAL];
+    uint16_t *q_rows = (uint16_t *)(smem + L_R1);   // [64][RP]
+    uint16_t *P_b = (uint16_t *)(smem + L_R1);      // [64][TP]
+    float *T_s = (float *)(smem + L_R1);            // [64][64]
+    uint16_t *k_rows = (uint16_t *)(smem + L_R2);   // [64][RP]
+    uint16_t *V_t = (uint16_t *)(smem + L_R2);      // [128][TP]
+    uint16_t *W_b = (uint16_t *)(smem + L_R2);      // [64][RP]
+    uint16_t *K_t = (uint16_t *)(smem + L_KT);      // [128][TP]
+    float *A_s = (float *)(smem + L_AS);            // [64][AP]
+    float *M_t = (float *)(smem + L_MT);            // [3][16][16]
+    double *gam_s = (double *)(smem + L_GAM);
+    float *beta_s = (float *)(smem + L_SC), *eg_s = beta_s + CH, *egc_s = eg_s + CH;
+    float *iq_s = egc_s + CH, *ik_s = iq_s + CH;
 
+    // ---- phase 1
     // gates and the cumulative log-decay (wave 0, lane = token); masked
     // tokens get beta = 0 and g = 0, which leaves U and S unchanged
     if (wave == 0) {
@@ -101,45 +141,34 @@ __global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
             beta = 1.0 / (1.0 + exp(-(double)p.b[e]));
             glog = -exp((double)p.A_log[vh]) * softplus_d((double)p.a[e] + (double)p.dt_bias[vh]);
         }
-        double s = glog;
+        double sc = glog;
 #pragma unroll
         for (int off = 1; off < 64; off <<= 1) {
-            const double o = __shfl_up(s, off, 64);
-            if (lane >= off) s += o;
+            const double o = __shfl_up(sc, off, 64);
+            if (lane >= off) sc += o;
         }
-        const double sC = __shfl(s, 63, 64);
-        gam_s[lane] = s;
+        const double sC = __shfl(sc, 63, 64);
+        gam_s[lane] = sc;
         beta_s[lane] = (float)beta;
-        eg_s[lane] = (float)exp(s);
-        egc_s[lane] = (float)exp(sC - s);
+        eg_s[lane] = (float)exp(sc);
+        egc_s[lane] = (float)exp(sC - sc);
     }
-
-    // q and k rows, one token per lane (wave 1: k, wave 2: q): the lane reads
-    // its token's 256 bytes and sums the squares itself, so no cross-lane
-    // reduction is needed
-    const float qscale = 1.0f / sqrtf((float)HD);
-    uint4 vrow[16];   // wave 3: v row of token `lane`, parked in LDS once qn_b is free
-    if (wave == 3) {
+    // rows of one token per lane (wave 1: k, wave 2: q, wave 3: v); the lane
+    // sums its own squares (double), so no cross-lane reduction is needed
+    uint4 raw[16];
+    if (wave >= 1) {
+        const uint16_t *src = wave == 1 ? p.k + (((size_t)b * p.T + t0 + lane) * p.nqk + qh) * HD
+                            : wave == 2 ? p.q + (((size_t)b * p.T + t0 + lane) * p.nqk + qh) * HD
+                                        : p.v + (((size_t)b * p.T + t0 + lane) * p.nv + vh) * HD;
         if (lane < nvalid) {
-            const uint16_t *src = p.v + (((size_t)b * p.T + t0 + lane) * p.nv + vh) * HD;
-#pragma unroll
-            for (int j = 0; j < 16; j++) vrow[j] = *(const uint4 *)(src + 8 * j);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 16; j++) vrow[j] = make_uint4(0u, 0u, 0u, 0u);
-        }
-    }
-    if (wave == 1 || wave == 2) {
-        const int t = lane;
-        uint4 raw[16];
-        if (t < nvalid) {
-            const uint16_t *src = (wave == 1 ? p.k : p.q) + (((size_t)b * p.T + t0 + t) * p.nqk + qh) * HD;
 #pragma unroll
             for (int j = 0; j < 16; j++) raw[j] = *(const uint4 *)(src + 8 * j);
         } else {
 #pragma unroll
             for (int j = 0; j < 16; j++) raw[j] = make_uint4(0u, 0u, 0u, 0u);
         }
+    }
+    if (wave == 1 || wave == 2) {
         double ss = 0.0;
 #pragma unroll
         for (int j = 0; j < 16; j++) {
@@ -152,31 +181,24 @@ __global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
                 ss = ss + hi * hi;
             }
         }
-        const float inv = 1.0f / sqrtf((float)ss + 1e-6f);
+        const float inv = 1.0f / sqrtf((float)ss + 1e-6f);   // l2norm, vx27_deltanet.c:51-56
+        uint16_t *rows = wave == 1 ? k_rows : q_rows;
+#pragma unroll
+        for (int j = 0; j < 16; j++) *(uint4 *)&rows[lane * RP + 8 * j] = raw[j];
         if (wave == 1) {
+            ik_s[lane] = inv;
+            // K^T: dim d of every token, one 128-byte row per instruction
 #pragma unroll
             for (int j = 0; j < 16; j++) {
                 const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
-                float f[8];
 #pragma unroll
                 for (int e = 0; e < 4; e++) {
-                    f[2 * e] = vx_bf16_to_f32((uint16_t)w4[e]) * inv;
-                    f[2 * e + 1] = vx_bf16_to_f32((uint16_t)(w4[e] >> 16)) * inv;
+                    K_t[(8 * j + 2 * e) * TP + lane] = (uint16_t)w4[e];
+                    K_t[(8 * j + 2 * e + 1) * TP + lane] = (uint16_t)(w4[e] >> 16);
                 }
-                *(float4 *)&kn_f[t][8 * j] = make_float4(f[0], f[1], f[2], f[3]);
-                *(float4 *)&kn_f[t][8 * j + 4] = make_float4(f[4], f[5], f[6], f[7]);
             }
         } else {
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
-                uint32_t o4[4];
-#pragma unroll
-                for (int e = 0; e < 4; e++)
-                    o4[e] = pack2((vx_bf16_to_f32((uint16_t)w4[e]) * inv) * qscale,
-                                  (vx_bf16_to_f32((uint16_t)(w4[e] >> 16)) * inv) * qscale);
-                *(uint4 *)&qn_b[t][8 * j] = make_uint4(o4[0], o4[1], o4[2], o4[3]);
-            }
+            iq_s[lane] = inv;
         }
     }
     __syncthreads();
@@ -184,8 +206,9 @@ __global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
     char *rec = p.rec + (((size_t)b * p.nv + vh) * p.NC + c) * REC;
     const double gamC = gam_s[CH - 1];
     if (tid == 0) *(float *)(rec + R_GC) = (float)exp(gamC);
+    const float qscale = 1.0f / sqrtf((float)HD);
 
-    // K K^T and Q K^T for row block `wave`; Qe tiles on the way
+    // ---- phase 2: raw K K^T and Q K^T for row block `wave`; e^gam qn tiles
     floatx4_t acck[4], accq[4];
 #pragma unroll
     for (int nb = 0; nb < 4; nb++) {
@@ -193,23 +216,23 @@ __global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
         accq[nb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
     }
     const int rowA = wave * 16 + m;
-    const float egA = eg_s[rowA];
+    const float qeA = eg_s[rowA] * (iq_s[rowA] * qscale);
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
         const int d0 = 32 * ks + 8 * g;
-        const uint4 qa = *(const uint4 *)&qn_b[rowA][d0];
+        const uint4 qa = *(const uint4 *)&q_rows[rowA * RP + d0];
         const bf16x8_t aq = as_bf16x8(qa);
-        const bf16x8_t ak = as_bf16x8(pack8(&kn_f[rowA][d0]));
-        {   // Qe tile (row block wave, k-step ks): e^gam_t * qn
+        const bf16x8_t ak = as_bf16x8(*(const uint4 *)&k_rows[rowA * RP + d0]);
+        {   // e^gam qn tile (row block wave, k-step ks)
             const uint16_t *qs = (const uint16_t *)&qa;
             float f[8];
 #pragma unroll
-            for (int e = 0; e < 8; e++) f[e] = egA * vx_bf16_to_f32(qs[e]);
+            for (int e = 0; e < 8; e++) f[e] = qeA * vx_bf16_to_f32(qs[e]);
             *(uint4 *)(rec + R_QE + ((size_t)(wave * 4 + ks) * 64 + lane) * 16) = pack8(f);
         }
 #pragma unroll
         for (int nb = 0; nb < 4; nb++) {
-            const bf16x8_t bk = as_bf16x8(pack8(&kn_f[nb * 16 + m][d0]));
+            const bf16x8_t bk = as_bf16x8(*(const uint4 *)&k_rows[(nb * 16 + m) * RP + d0]);
             acck[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ak, bk, acck[nb], 0, 0, 0);
             accq[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(aq, bk, accq[nb], 0, 0, 0);
         }
@@ -218,103 +241,151 @@ __global__ __launch_bounds__(256) void dnp_prep(PrepArgs p) {
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int tile = wave * 4 + j, rb = tile >> 1, ks = tile & 1;
-        const int i = rb * 16 + m;
+        const int i = rb * 16 + m, tb = 32 * ks + 8 * g;
+        const uint4 kr = *(const uint4 *)&K_t[i * TP + tb];
+        const uint16_t *kv = (const uint16_t *)&kr;
         float f[8];
 #pragma unroll
-        for (int e = 0; e < 8; e++) {
-            const int t = 32 * ks + 8 * g + e;
-            f[e] = egc_s[t] * kn_f[t][i];
-        }
+        for (int e = 0; e < 8; e++) f[e] = (egc_s[tb + e] * ik_s[tb + e]) * vx_bf16_to_f32(kv[e]);
         *(uint4 *)(rec + R_KT + ((size_t)tile * 64 + lane) * 16) = pack8(f);
     }
-    __syncthreads();   // qn_b is reused for P below
+    __syncthreads();   // q and k rows are no longer read
 
-    // A (fp32, for the solve) and P (bf16, staged for its operand tiles)
-    uint16_t *P_b = &qn_b[0][0];
+    // ---- phase 3: A (fp32, for the inverse), P (bf16 staging), V^T
 #pragma unroll
     for (int nb = 0; nb < 4; nb++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int s = wave * 16 + 4 * g + i, r = nb * 16 + m;
             const float ed = r <= s ? expf((float)(gam_s[s] - gam_s[r])) : 0.0f;
-            A_s[s][r] = r < s ? beta_s[s] * ed * acck[nb][i] : 0.0f;
-            P_b[s * PP + r] = vx_f32_to_bf16(ed * accq[nb][i]);
+            A_s[s * AP + r] = r < s ? beta_s[s] * ed * ((ik_s[s] * ik_s[r]) * acck[nb][i]) : 0.0f;
+            P_b[s * TP + r] = vx_f32_to_bf16(ed * (((iq_s[s] * qscale) * ik_s[r]) * accq[nb][i]));
+        }
+    }
+    if (wave == 3) {   // V^T: dim d of every token
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                V_t[(8 * j + 2 * e) * TP + lane] = (uint16_t)w4[e];
+                V_t[(8 * j + 2 * e + 1) * TP + lane] = (uint16_t)(w4[e] >> 16);
+            }
         }
     }
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
-        const uint4 v = *(const uint4 *)&P_b[rowA * PP + 32 * ks + 8 * g];
+        const uint4 v = *(const uint4 *)&P_b[rowA * TP + 32 * ks + 8 * g];
         *(uint4 *)(rec + R_P + ((size_t)(wave * 2 + ks) * 64 + lane) * 16) = v;
     }
-    __syncthreads();   // P is read out; qn_b now holds v (bf16 rows)
-    if (wave == 3) {
+    __syncthreads();   // P staging is read out; R1 takes T
+
+    // ---- phase 4: T = (I + A)^-1
+    if (tid < 64) {   // diagonal blocks: thread (block bi, column cc)
+        const int bi = tid >> 4, cc = tid & 15, o = 16 * bi;
+        float t[16];
 #pragma unroll
-        for (int j = 0; j < 16; j++) *(uint4 *)&qn_b[lane][8 * j] = vrow[j];
+        for (int r = 0; r < 16; r++) {
+            float acc = r == cc ? 1.0f : 0.0f;
+#pragma unroll
+            for (int k = 0; k < r; k++) acc -= A_s[(o + r) * AP + o + k] * t[k];
+            t[r] = acc;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) T_s[(o + r) * 64 + o + cc] = t[r];
     }
     __syncthreads();
-
-    // forward substitution x = (I + A)^-1 rhs, one column per thread:
-    // columns 0..127 of beta V (-> Ut), 128..255 of beta e^gam K (-> W)
-    float x[CH];
-    if (tid < HD) {
+    // off-diagonal blocks, level by level: T[j+lev][j] = -T[i][i] M,
+    // M = sum_{kb=j}^{i-1} A[i][kb] T[kb][j] (i = j + lev), one block per wave
+    // on the fp32 MFMA (v_mfma_f32_16x16x4_f32: lane l holds A[l%16][k0 + l/16]
+    // and B[k0 + l/16][l%16]; exact fp32 products)
+    float *Mw = M_t + (wave < 3 ? wave : 0) * 256;   // this wave's 16x16 scratch
 #pragma unroll
-        for (int t = 0; t < CH; t++) {
-            x[t] = beta_s[t] * vx_bf16_to_f32(qn_b[t][tid]);
-        }
-    } else {
+    for (int lev = 1; lev < 4; lev++) {
+        if (wave < 4 - lev) {
+            const int j = wave, i = j + lev;
+            floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+            for (int kb = j; kb < i; kb++) {
 #pragma unroll
-        for (int t = 0; t < CH; t++) x[t] = (beta_s[t] * eg_s[t]) * kn_f[t][tid - HD];
-    }
-    // blocked forward substitution over four 16-row blocks: first the rows of
-    // a block against every earlier block (four independent partial sums per
-    // row, so the rows proceed in parallel), then the 16-row triangle
-#pragma unroll
-    for (int blk = 0; blk < 4; blk++) {
-        if (blk > 0) {
-#pragma unroll
-            for (int ii = 0; ii < 16; ii++) {
-                const int i = 16 * blk + ii;
-                float a0 = x[i], a1 = 0.f, a2 = 0.f, a3 = 0.f;
-#pragma unroll
-                for (int k4 = 0; k4 < 16 * blk; k4 += 4) {
-                    const float4 a4 = *(const float4 *)&A_s[i][k4];
-                    a0 -= a4.x * x[k4];
-                    a1 -= a4.y * x[k4 + 1];
-                    a2 -= a4.z * x[k4 + 2];
-                    a3 -= a4.w * x[k4 + 3];
+                for (int k0 = 0; k0 < 16; k0 += 4) {
+                    const float av = A_s[(16 * i + m) * AP + 16 * kb + k0 + g];
+                    const float bv = T_s[(16 * kb + k0 + g) * 64 + 16 * j + m];
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
                 }
-                x[i] = (a0 + a1) + (a2 + a3);
             }
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) Mw[(4 * g + ii) * 16 + m] = acc[ii];
+            asm volatile("" ::: "memory");   // LDS ops of one wave stay in order
+            floatx4_t tacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k0 = 0; k0 < 16; k0 += 4) {
+                const float av = T_s[(16 * i + m) * 64 + 16 * i + k0 + g];
+                const float bv = Mw[(k0 + g) * 16 + m];
+                tacc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, tacc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) T_s[(16 * i + 4 * g + ii) * 64 + 16 * j + m] = -tacc[ii];
         }
+        __syncthreads();
+    }
+
+    // ---- phase 5: [Ut | W] rows of block `wave` = T_V V | T_K K (MFMA)
+    bf16x8_t tv[2][2], tk[2][2];   // [k-step][hi, lo]
 #pragma unroll
-        for (int ii = 1; ii < 16; ii++) {
-            const int i = 16 * blk + ii;
-            float acc = x[i];
+    for (int ks = 0; ks < 2; ks++) {
+        const int s = wave * 16 + m, r0 = 32 * ks + 8 * g;
+        float fv[8], fk[8];
 #pragma unroll
-            for (int k = 16 * blk; k < i; k++) acc -= A_s[i][k] * x[k];
-            x[i] = acc;
+        for (int e = 0; e < 8; e++) {
+            const int r = r0 + e;
+            const float tsr = r <= s ? T_s[s * 64 + r] : 0.0f;   // upper blocks are never written
+            fv[e] = tsr * beta_s[r];
+            fk[e] = tsr * ((beta_s[r] * eg_s[r]) * ik_s[r]);
+        }
+        float lv[8], lk[8];
+        const uint4 hv = pack8(fv), hk = pack8(fk);
+        const uint16_t *hvs = (const uint16_t *)&hv, *hks = (const uint16_t *)&hk;
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            lv[e] = fv[e] - vx_bf16_to_f32(hvs[e]);
+            lk[e] = fk[e] - vx_bf16_to_f32(hks[e]);
+        }
+        tv[ks][0] = as_bf16x8(hv);
+        tv[ks][1] = as_bf16x8(pack8(lv));
+        tk[ks][0] = as_bf16x8(hk);
+        tk[ks][1] = as_bf16x8(pack8(lk));
+    }
+    floatx4_t wacc[8];
+    float *ut = (float *)(rec + R_UT);
+#pragma unroll
+    for (int cb = 0; cb < 16; cb++) {
+        const bool isv = cb < 8;
+        const uint16_t *src = isv ? V_t : K_t;
+        const int col = (cb & 7) * 16 + m;
+        floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const bf16x8_t bop = as_bf16x8(*(const uint4 *)&src[col * TP + 32 * ks + 8 * g]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(isv ? tv[ks][0] : tk[ks][0], bop, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(isv ? tv[ks][1] : tk[ks][1], bop, acc, 0, 0, 0);
+        }
+        if (isv) {   // Ut: C layout tile (rb = wave, cs = cb), as the scan reads it
+            *(floatx4_t *)&ut[(((size_t)wave * 8 + cb) * 64 + lane) * 4] = acc;
+        } else {
+            wacc[cb - 8] = acc;
         }
     }
-    if (tid < HD) {
-        // Ut column tid in C-layout tiles [rb][cs][lane (g,n)][i]
-        const int cs = tid >> 4, n = tid & 15;
-        float *ut = (float *)(rec + R_UT);
+    __syncthreads();   // every read of V^T is done: R2 takes the -W staging
+    // -W rows (token 16 wave + 4g + i, dim 16 cb + m) -> bf16 staging
 #pragma unroll
-        for (int t = 0; t < CH; t++) {
-            const int rb = t >> 4, gg = (t & 15) >> 2, i = t & 3;
-            ut[(((size_t)rb * 8 + cs) * 64 + gg * 16 + n) * 4 + i] = x[t];
-        }
-    }
-    __syncthreads();   // every read of kn_f is done
-    if (tid >= HD) {
+    for (int cb = 0; cb < 8; cb++)
 #pragma unroll
-        for (int t = 0; t < CH; t++) kn_f[t][tid - HD] = -x[t];
-    }
+        for (int i = 0; i < 4; i++) W_b[(wave * 16 + 4 * g + i) * RP + cb * 16 + m] = vx_f32_to_bf16(-wacc[cb][i]);
     __syncthreads();
 #pragma unroll
     for (int ks = 0; ks < 4; ks++)
-        *(uint4 *)(rec + R_NW + ((size_t)(wave * 4 + ks) * 64 + lane) * 16) = pack8(&kn_f[rowA][32 * ks + 8 * g]);
+        *(uint4 *)(rec + R_NW + ((size_t)(wave * 4 + ks) * 64 + lane) * 16) = *(const uint4 *)&W_b[rowA * RP + 32 * ks + 8 * g];
 }
 
 struct ScanArgs {
