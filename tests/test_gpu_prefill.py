@@ -202,6 +202,34 @@ def test_gqa_prefill_shapes(ctx, B, T, pos0, L, inter):
     check_bf16(out, ref, "out")
 
 
+def test_gqa_prefill_wide_scores(ctx):
+    """Scores hundreds of log2 units apart, exact in bf16: raw q and k rows
+    one-hot (+-1) in an unrotated dim 64..127 whose norm weight has 1+w = 4,
+    so after rmsn every score is 0 or +-(64*64/16)*log2(e), and equal scores
+    stay equal after rounding.  A query whose matching key first appears
+    after its first key tile overflows fp32 against that tile's max: the
+    attention kernel's overflow check must catch it and redo the query with
+    the rescaling (online) softmax.  Ragged T, stale NaN rows past the end."""
+    from vx27_amd import workloads as W
+    B, T, L, n_q, n_kv = 1, 300, 320, 24, 4
+    d = W.gqa_prefill(B=B, T=T, config=55)
+    r = W.rng(56, "gqa_wide")
+    def one_hot(shape):
+        x = np.zeros(shape + (256,), np.float32)
+        dim = r.integers(64, 128, size=shape)
+        sgn = np.where(r.random(shape) < 0.5, -1.0, 1.0)
+        np.put_along_axis(x, dim[..., None], sgn[..., None], axis=-1)
+        return W.bf16_bits(x)
+    d["q"], d["k"] = one_hot((B, T, n_q)), one_hot((B, T, n_kv))
+    w = np.zeros(256, np.float32)
+    w[64:128] = 3.0
+    d["q_norm_w"], d["k_norm_w"] = w.copy(), w.copy()
+    say("gqa_prefill: B=1 T=300 L=320, one-hot q/k with scores 0 or +-369 (log2 units)")
+    out = run_gqa_prefill(ctx, d, L)
+    ref, _ = oracle_gqa_prefill(d, L)
+    check_bf16(out, ref, "out")
+
+
 def test_prefill_deterministic(ctx):
     """Both prefills are deterministic: the same call twice gives identical
     bits (the kernels use fixed reduction orders; a missed wait on an

@@ -7,9 +7,11 @@ hipcc compiles every csrc/*.hip for --offload-arch=gfx950 with:
                                       kernels reproduce the reference's
                                       separate multiply/add roundings
   -target-feature -packed-fp32-ops    no packed FP32 instructions
-and, for the MFMA prefill kernels (FILE_FLAGS), -amdgpu-mfma-vgpr-form: their
-accumulators stay in arch VGPRs, where the online-softmax and state updates
-touch them with VALU ops, instead of being copied in and out of AGPRs.
+and, for the DeltaNet prefill kernels (FILE_FLAGS), -amdgpu-mfma-vgpr-form:
+their accumulators stay in arch VGPRs, where the state updates touch them
+with VALU ops, instead of being copied in and out of AGPRs.  (The attention
+kernel's O accumulators are only ever touched by MFMAs in its loop, so they
+live in AGPRs.)
 gcc compiles the C drop-in layer (-std=c11) against include/vx27_hip.h.
 Objects go to vx27_amd/_build/, the library to vx27_amd/libvx27_hip.so.
 """
@@ -35,7 +37,6 @@ HIP_FLAGS = ["-O3", f"--offload-arch={ARCH}", "-fPIC", "-std=c++17", "-ffp-contr
              "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
              "-Wno-unused-result", f"-I{INC}", f"-I{CSRC}"]
 FILE_FLAGS = {
-    "vx_gqa_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "vx_dn_prefill.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 CC = os.environ.get("CC", "gcc")

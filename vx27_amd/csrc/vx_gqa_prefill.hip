@@ -10,24 +10,30 @@
 // same as causal attention of all T queries over the cache.
 //
 // Kernels per call:
-//   gqp_kv     one workgroup per (token, sequence): rmsn + RoPE of every k
-//              head; k,v rounded to bf16 and stored at positions
-//              pos0..pos0+T-1 of the cache.
-//   gqp_attn   one workgroup per (128-query tile, Q head, sequence), heaviest
-//              tiles first; 4 waves of 32 queries.  Each wave normalises,
-//              rotates and scales its own 32 query rows into MFMA operand
-//              registers (the B operand layout puts both halves of a RoPE
-//              pair in one lane when rope_dim is a multiple of 64).  64-key
-//              K and V tiles arrive in LDS by direct-to-LDS loads, double
-//              buffered: tile kt+1 streams in while tile kt is used.  Per
-//              tile:  S^T[key][q] = K . Q^T (v_mfma_f32_16x16x32_bf16, 4 key
-//              blocks x query blocks x 8 k-steps), causal mask, online
-//              softmax.  Row m of key block kb holds key 32(kb/2) + 8(m/4)
-//              + 4(kb%2) + m%4, so in the C layout of S^T lane (g,n) of key
-//              blocks 2s and 2s+1 holds keys 32s + 8g + 0..7 of query n:
-//              that is the A operand of O^T += V^T P^T for k-step s as it
-//              stands, and the matching V operand is one 16-byte unit (8
-//              consecutive keys) of a dim row of the dim-major V tile.
+//   gqp_kv       one workgroup per 32-position V block of one KV head: rmsn +
+//                RoPE of k; k,v rounded to bf16 and stored at positions
+//                pos0..pos0+T-1 of the cache; the (cos, sin) table of the
+//                new positions for the query prologue.
+//   gqp_attn_pp  one workgroup per (128-query tile, Q head, sequence),
+//                heaviest tiles first; 4 waves of 32 queries (one wave per
+//                SIMD).  Each wave normalises, rotates and scales its 32
+//                query rows into MFMA operand registers (the B operand layout
+//                puts both halves of a RoPE pair in one lane when rope_dim is
+//                a multiple of 64).  64-key K and V tiles arrive in LDS by
+//                direct-to-LDS loads.  Per tile: S^T[key][q] = K . Q^T
+//                (v_mfma_f32_16x16x32_bf16, 4 key blocks x 2 query blocks x
+//                8 k-steps), causal mask, softmax.  Row m of key block kb
+//                holds key 32(kb/2) + 8(m/4) + 4(kb%2) + m%4, so in the C
+//                layout of S^T lane (g,n) of key blocks 2s and 2s+1 holds
+//                keys 32s + 8g + 0..7 of query n: that is the A operand of
+//                O += P V for k-step s as it stands, and the matching V
+//                operand is one 16-byte unit (8 consecutive keys) of a dim
+//                row of the dim-major V tile.  The S of tile kt+1 runs on the
+//                MFMA pipe while the VALU does the softmax of tile kt (see
+//                the kernel's comment for the schedule and the softmax
+//                reference).
+//   gqp_attn     the earlier one-tile-at-a-time form (8 waves of 16
+//                queries, online softmax), kept as a build option (GQP_PP=0).
 #include <math.h>
 
 #include <type_traits>
@@ -46,6 +52,9 @@ constexpr int HDG = VX_GQA_HD;
 #endif
 #ifndef GQP_RB
 #define GQP_RB 1            // 16-query blocks per wave
+#endif
+#ifndef GQP_PP
+#define GQP_PP 1            // software-pipelined attention kernel (4 waves x 32 queries)
 #endif
 #ifndef GQP_DB
 #define GQP_DB 1            // double-buffered K/V tiles (else one buffer, two workgroups per CU)
@@ -228,6 +237,96 @@ __device__ __forceinline__ void load_v(uint32_t vbuf, const char *Vt, int wave, 
     }
 }
 
+// NB 16-query blocks as the B operand of S^T = K Q^T: lane (g,n) of k-step
+// ks gets dims 32ks + 8g + 0..7 of token row t[blk] (the block's row n).
+// rmsn (1+w, or w with VX27_GQA_NORM_W; sum of squares in double over the 4
+// lanes of the row), RoPE (pair (i, i + half) sits in one lane: k-steps ks
+// and ks + half/32; cos and sin from the table gqp_kv wrote), then the
+// log2(e)/sqrt(256) score scale, so scores come out in the exp2 domain.
+// Every global load (rows, norm weights, cos/sin) is issued before any of
+// them is used: one round trip.
+constexpr int HQ_MAX = VX_ROPE_MAXH / 64;   // k-steps holding the first half of the pairs, at most
+template <int NB>
+__device__ __forceinline__ void q_prep(const AttnArgs &a, int b, int h, const int (&t)[NB], int g,
+                                       bf16x8_t (&qv)[NB][8]) {
+    const int hq = a.rope_dim / 64;
+    uint4 u[NB][8];
+    float4 w[8][2];
+    float4 cs[NB][HQ_MAX][4];
+#pragma unroll
+    for (int blk = 0; blk < NB; blk++) {
+        const uint16_t *src = a.q + ((size_t)b * a.T + t[blk]) * a.q_ts + (size_t)h * a.q_hs + 8 * g;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) u[blk][ks] = *(const uint4 *)(src + 32 * ks);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        w[ks][0] = *(const float4 *)(a.q_norm_w + 32 * ks + 8 * g);
+        w[ks][1] = *(const float4 *)(a.q_norm_w + 32 * ks + 8 * g + 4);
+    }
+#pragma unroll
+    for (int blk = 0; blk < NB; blk++) {
+        const float4 *ct = (const float4 *)(a.cs_tab + (size_t)t[blk] * (32 * hq) + 8 * g);
+#pragma unroll
+        for (int ks = 0; ks < HQ_MAX; ks++)
+#pragma unroll
+            for (int e = 0; e < 4; e++)
+                cs[blk][ks][e] = ks < hq ? ct[16 * ks + e] : make_float4(1.f, 0.f, 1.f, 0.f);
+    }
+    const bool wdirect = (a.flags & VX27_GQA_NORM_W) != 0;
+#pragma unroll
+    for (int blk = 0; blk < NB; blk++) {
+        float x[8][8];
+        double ss = 0.0;
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            const uint32_t w4[4] = {u[blk][ks].x, u[blk][ks].y, u[blk][ks].z, u[blk][ks].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                x[ks][2 * e] = __uint_as_float(w4[e] << 16);
+                x[ks][2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u);
+            }
+#pragma unroll
+            for (int e = 0; e < 8; e++) ss += (double)x[ks][e] * (double)x[ks][e];
+        }
+        ss += __shfl_xor(ss, 16, 64);
+        ss += __shfl_xor(ss, 32, 64);
+        const float sc = 1.0f / sqrtf((float)(ss / HDG) + 1e-6f);
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            const float wv[8] = {w[ks][0].x, w[ks][0].y, w[ks][0].z, w[ks][0].w,
+                                 w[ks][1].x, w[ks][1].y, w[ks][1].z, w[ks][1].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) x[ks][e] = wdirect ? (x[ks][e] * sc) * wv[e] : (x[ks][e] * sc) * (wv[e] + 1.0f);
+        }
+        // the pair offset as a constant, so x stays in registers
+        auto rope = [&](auto hqc) {
+            constexpr int HQ = decltype(hqc)::value;
+#pragma unroll
+            for (int ks = 0; ks < HQ; ks++)
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    const float4 c4 = cs[blk][ks][e >> 1];
+                    const float cx = (e & 1) ? c4.z : c4.x, cy = (e & 1) ? c4.w : c4.y;
+                    const float x0 = x[ks][e], x1 = x[ks + HQ][e];
+                    x[ks][e] = x0 * cx - x1 * cy;
+                    x[ks + HQ][e] = x0 * cy + x1 * cx;
+                }
+        };
+        static_assert(HQ_MAX == 2, "RoPE cases below cover rope_dim 64 and 128");
+        switch (hq) {
+            case 1: rope(std::integral_constant<int, 1>{}); break;
+            case 2: rope(std::integral_constant<int, 2>{}); break;
+            default: break;
+        }
+        constexpr float QS = 1.4426950408889634f / 16.0f;   // scores in the exp2 domain
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++)
+            qv[blk][ks] = as_bf16x8(make_uint4(pack2(x[ks][0] * QS, x[ks][1] * QS), pack2(x[ks][2] * QS, x[ks][3] * QS),
+                                               pack2(x[ks][4] * QS, x[ks][5] * QS), pack2(x[ks][6] * QS, x[ks][7] * QS)));
+    }
+}
+
 // grid (ceil(T/128) * n_q, B), block NW*64: NW waves of RB 16-query blocks
 template <int NW, int RB, bool DB>
 __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
@@ -270,74 +369,13 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
     load_k<NW>(kl0, Kc, wave, lane);
     load_v<NW>(vl0, Vc, wave, lane);
 
-    // ---- this wave's queries as the B operand of S^T = K Q^T: lane (g,n)
-    // of k-step ks holds dims 32ks + 8g + 0..7 of query row n of block rb.
-    // rmsn (1+w, or w with VX27_GQA_NORM_W; sum of squares in double over
-    // the 4 lanes of the row), RoPE (pair (i, i + half) sits in one lane:
-    // k-steps ks and ks + half/32), then the log2(e)/sqrt(256) score scale.
+    // ---- this wave's queries as MFMA operands
     bf16x8_t qv[RB][8];
     {
-        const int hq = a.rope_dim / 64;   // k-steps holding the first half of the pairs
-        // one query block with a constant index (qv and x stay in registers)
-        auto prep_block = [&](auto rbc) {
-            constexpr int rb = decltype(rbc)::value;
-            const int t = min(r0 + rb * 16 + n, a.T - 1);   // rows past T repeat row T-1
-            const uint16_t *src = a.q + ((size_t)b * a.T + t) * a.q_ts + (size_t)h * a.q_hs + 8 * g;
-            float x[8][8];
-            double ss = 0.0;
+        int tq[RB];   // rows past T repeat row T-1
 #pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                const uint4 u = *(const uint4 *)(src + 32 * ks);
-                const uint32_t w4[4] = {u.x, u.y, u.z, u.w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    x[ks][2 * e] = __uint_as_float(w4[e] << 16);
-                    x[ks][2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u);
-                }
-#pragma unroll
-                for (int e = 0; e < 8; e++) ss += (double)x[ks][e] * (double)x[ks][e];
-            }
-            ss += __shfl_xor(ss, 16, 64);
-            ss += __shfl_xor(ss, 32, 64);
-            const float sc = 1.0f / sqrtf((float)(ss / HDG) + 1e-6f);
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++)
-#pragma unroll
-                for (int e = 0; e < 8; e++) {
-                    const float w = a.q_norm_w[32 * ks + 8 * g + e];
-                    x[ks][e] = (a.flags & VX27_GQA_NORM_W) ? (x[ks][e] * sc) * w : (x[ks][e] * sc) * (w + 1.0f);
-                }
-            // the pair offset as a constant, so x stays in registers; cos and
-            // sin of the token's angles from the table gqp_kv wrote
-            const float2 *ct = a.cs_tab + (size_t)t * (32 * hq) + 8 * g;
-            auto rope = [&](auto hqc) {
-                constexpr int HQ = decltype(hqc)::value;
-#pragma unroll
-                for (int ks = 0; ks < HQ; ks++)
-#pragma unroll
-                    for (int e = 0; e < 8; e++) {
-                        const float2 c = ct[32 * ks + e];
-                        const float x0 = x[ks][e], x1 = x[ks + HQ][e];
-                        x[ks][e] = x0 * c.x - x1 * c.y;
-                        x[ks + HQ][e] = x0 * c.y + x1 * c.x;
-                    }
-            };
-            switch (hq) {
-                case 1: rope(std::integral_constant<int, 1>{}); break;
-                case 2: rope(std::integral_constant<int, 2>{}); break;
-                case 3: rope(std::integral_constant<int, 3>{}); break;
-                case 4: rope(std::integral_constant<int, 4>{}); break;
-                default: break;
-            }
-            constexpr float QS = 1.4426950408889634f / 16.0f;   // scores in the exp2 domain
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++)
-                qv[rb][ks] = as_bf16x8(make_uint4(pack2(x[ks][0] * QS, x[ks][1] * QS), pack2(x[ks][2] * QS, x[ks][3] * QS),
-                                                  pack2(x[ks][4] * QS, x[ks][5] * QS), pack2(x[ks][6] * QS, x[ks][7] * QS)));
-        };
-        prep_block(std::integral_constant<int, 0>{});
-        if constexpr (RB > 1) prep_block(std::integral_constant<int, 1>{});
-        static_assert(RB <= 2, "the query prologue covers at most two blocks");
+        for (int rb = 0; rb < RB; rb++) tq[rb] = min(r0 + 16 * rb + n, a.T - 1);
+        q_prep<RB>(a, b, h, tq, g, qv);
     }
 
     floatx4_t O[RB][16];
@@ -538,6 +576,432 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
     }
 }
 
+
+// Software-pipelined attention: 4 waves of 32 queries (two 16-query blocks,
+// so every K and V operand read from LDS feeds two MFMAs).  The stretch
+// between two barriers, interval kt, runs the S MFMAs of tile kt+1 with the
+// softmax of tile kt interleaved on the VALU, then O += P V of tile kt; row
+// sums come out of the MFMA pipe as P times a ones operand, in the C layout
+// of O.  Two K and two V tile buffers: interval kt streams K(kt+2) and
+// V(kt+1) into the buffers that K(kt) and V(kt-1) left (a clamped tile index
+// past the end reloads a valid tile into a buffer nobody reads again, so the
+// loads carry no branch).
+//
+// Softmax reference: each query's max over its first tile, fixed for the
+// whole pass, so P = exp2(s - m0) needs no running max and O no rescale.
+// That is exact in fp32 (the reference cancels in O / l) unless a later
+// score exceeds m0 by more than fp32 range allows: then O or l is no longer
+// finite, and the wave redoes its queries with the online (rescaling)
+// softmax, reading K and V straight from the cache.  grid (ceil(T/128) *
+// n_q, B), block 256.
+constexpr int PP_RB = 2, PP_QT = 4 * PP_RB * 16, PP_PER = 8;
+
+__global__ __launch_bounds__(256) void gqp_attn_pp(AttnArgs a) {
+    constexpr int RB = PP_RB, QT = PP_QT, PER = PP_PER;
+    const int n_qt = gridDim.x / a.n_q, b = blockIdx.y;
+    int qt, h;
+    if (a.xcd_map) {   // as in gqp_attn: one KV head's query heads per XCD group, heaviest tiles first
+        const int id = blockIdx.x, xcd = id & 7, slot = id >> 3;
+        const int xpk = 8 / a.n_kv, hpx = a.n_q / 8;
+        qt = n_qt - 1 - slot / hpx;
+        h = (xcd / xpk) * (a.n_q / a.n_kv) + (xcd % xpk) * hpx + slot % hpx;
+    } else {
+        qt = n_qt - 1 - (int)blockIdx.x / a.n_q;
+        h = blockIdx.x % a.n_q;
+    }
+    const int kvh = h / (a.n_q / a.n_kv);
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int r0 = qt * QT + wave * (RB * 16);
+
+    // K tile buffers, then V tile buffers, in one array (the epilogue reuses
+    // all 128 KiB)
+    __shared__ __attribute__((aligned(16))) char smem[4 * KBUF];
+    char (*Kl)[KBUF] = (char (*)[KBUF])smem;
+    char (*Vl)[KBUF] = (char (*)[KBUF])(smem + 2 * KBUF);
+
+    const int n_keys = a.pos0 + a.T;
+    const int wg_last = a.pos0 + min(qt * QT + QT, a.T) - 1;
+    const int n_tiles = wg_last / KT + 1;
+    const int wave_tiles = (a.pos0 + min(r0 + RB * 16 - 1, a.T - 1)) / KT + 1;   // tiles with a key this wave sees
+    const int n_main = min((a.pos0 + r0 + 1) / KT, n_tiles);   // tiles with no key past any query of this wave
+    const char *Kc = (const char *)(a.k_cache + vx_k_index(a.n_kv, a.L, b, kvh, 0, 0));
+    const char *Vc = (const char *)(a.v_cache + vx_v_index(a.n_kv, a.L, b, kvh, 0, 0));
+
+    // this wave's share of a tile: PER 1 KiB units of K and of V; per-lane
+    // source offsets of the swizzled LDS slots (loop-invariant)
+    uint32_t ko[PER], vo[PER];
+#pragma unroll
+    for (int j = 0; j < PER; j++) {
+        const int r = (wave * PER + j) * 2 + (lane >> 5), u = (lane & 31) ^ kswz(r);
+        ko[j] = (uint32_t)(r * HDG + u * 8) * 2;
+        const int d = (wave * PER + j) * 8 + (lane >> 3), w = (lane & 7) ^ ((d >> 1) & 7);
+        vo[j] = (uint32_t)((((w >> 2) * HDG + d) * 32) + (w & 3) * 8) * 2;
+    }
+    const uint32_t kl0 = vx_lds_addr(Kl[0]), vl0 = vx_lds_addr(Vl[0]);
+    // (tile and buf are wave-uniform; vx_uniform_ptr keeps the source base
+    // in scalar registers where the compiler would not know it)
+    auto dma_k = [&](int tile, int buf, int j) {
+        vx_dma16(vx_uniform_ptr(Kc + (size_t)tile * KBUF), ko[j], kl0 + buf * KBUF + (wave * PER + j) * 1024);
+    };
+    auto dma_v = [&](int tile, int buf, int j) {
+        vx_dma16(vx_uniform_ptr(Vc + (size_t)tile * KBUF), vo[j], vl0 + buf * KBUF + (wave * PER + j) * 1024);
+    };
+#pragma unroll
+    for (int j = 0; j < PER; j++) dma_k(0, 0, j);
+#pragma unroll
+    for (int j = 0; j < PER; j++) dma_v(0, 0, j);
+#pragma unroll
+    for (int j = 0; j < PER; j++) dma_k(min(1, n_tiles - 1), 1, j);
+
+    bf16x8_t qv[RB][8];
+    {
+        const int tq[RB] = {min(r0 + n, a.T - 1), min(r0 + 16 + n, a.T - 1)};   // rows past T repeat row T-1
+        q_prep<RB>(a, b, h, tq, g, qv);
+    }
+
+    floatx4_t O[RB][16], Ol[RB];
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        Ol[rb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int db = 0; db < 16; db++) O[rb][db] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+    }
+    const bf16x8_t ones = as_bf16x8(make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u));
+
+    // key row held by row n of key block kb (see kswz): in the C layout of
+    // S^T, lane (g,n) of blocks 2s, 2s+1 holds keys 32s + 8g + 0..7
+    auto key_of = [&](int kb, int i) { return 32 * (kb >> 1) + 8 * g + 4 * (kb & 1) + i; };
+    auto kload = [&](const char *Kt, int ks, bf16x8_t *dst) {
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++) {
+            const int kr = 32 * (kb >> 1) + 8 * (n >> 2) + 4 * (kb & 1) + (n & 3);
+            const int uo = ((4 * ks + g) ^ kswz(kr)) << 4;
+            dst[kb] = as_bf16x8(*(const uint4 *)(Kt + kr * 512 + uo));
+        }
+    };
+    auto zero_s = [&](floatx4_t (&x)[4][RB]) {
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) x[kb][rb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+    };
+    auto s_tile = [&](const char *Kt, floatx4_t (&x)[4][RB]) {   // S without interleaved work
+        bf16x8_t kf[2][4];
+        kload(Kt, 0, kf[0]);
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            if (ks + 1 < 8) kload(Kt, ks + 1, kf[(ks + 1) & 1]);
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++)
+                    x[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks & 1][kb], qv[rb][ks], x[kb][rb], 0, 0, 0);
+        }
+    };
+    auto mask = [&](int k0, floatx4_t (&x)[4][RB]) {   // causal: keys past the query's position
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            const int qpos = a.pos0 + r0 + rb * 16 + n;
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int i = 0; i < 4; i++)
+                    if (k0 + key_of(kb, i) > qpos) x[kb][rb][i] = -INFINITY;
+        }
+    };
+    auto row_max = [&](floatx4_t (&x)[4][RB], int rb) {   // over the 4 lanes of query n
+        float m = -INFINITY;
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) m = fmaxf(m, x[kb][rb][i]);
+        m = fmaxf(m, __shfl_xor(m, 16, 64));
+        return fmaxf(m, __shfl_xor(m, 32, 64));
+    };
+
+    // softmax of one tile in 8 pieces (piece p runs beside k-step p of the
+    // next tile's S): P = exp2(s - m0) for one key block of one query block,
+    // packed to bf16 as the A operand of P V once both blocks of a k-step
+    // are done.  The main intervals start the S accumulators at -m0 (mq),
+    // so their S already is s - m0 (sub = false).
+    float m0[RB];
+    floatx4_t mq[RB];
+    bf16x8_t pa[RB][2];
+    auto sm_piece = [&](int piece, floatx4_t (&x)[4][RB], bool sub) {
+        const int rb = piece >> 2, kb = piece & 3;
+#pragma unroll
+        for (int i = 0; i < 4; i++) x[kb][rb][i] = __builtin_amdgcn_exp2f(sub ? x[kb][rb][i] - m0[rb] : x[kb][rb][i]);
+        if (kb & 1)
+            pa[rb][kb >> 1] = as_bf16x8(make_uint4(pack2(x[kb - 1][rb][0], x[kb - 1][rb][1]),
+                                                   pack2(x[kb - 1][rb][2], x[kb - 1][rb][3]),
+                                                   pack2(x[kb][rb][0], x[kb][rb][1]), pack2(x[kb][rb][2], x[kb][rb][3])));
+    };
+    // O += P V: groups of 4 dim blocks, the V operands of group j+1 read while
+    // the MFMAs of group j run; row sums from P times ones
+    auto pv_tile = [&](const char *Vt) {
+        const int vsw = (n >> 1) & 7;
+        bf16x8_t vf[2][4];
+        auto vload = [&](int grp, bf16x8_t *dst) {
+            const int ks = grp >> 2, db0 = (grp & 3) * 4;
+            const int uo = ((4 * ks + g) ^ vsw) << 4;
+#pragma unroll
+            for (int j = 0; j < 4; j++) dst[j] = as_bf16x8(*(const uint4 *)(Vt + ((db0 + j) * 16 + n) * (KT * 2) + uo));
+        };
+        vload(0, vf[0]);
+#pragma unroll
+        for (int grp = 0; grp < 8; grp++) {
+            if (grp + 1 < 8) vload(grp + 1, vf[(grp + 1) & 1]);
+            __builtin_amdgcn_sched_barrier(0);
+            const int ks = grp >> 2, db0 = (grp & 3) * 4;
+#pragma unroll
+            for (int j = 0; j < 4; j++)
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++)
+                    O[rb][db0 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rb][ks], vf[grp & 1][j], O[rb][db0 + j], 0, 0, 0);
+            if ((grp & 3) == 3)
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) Ol[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rb][ks], ones, Ol[rb], 0, 0, 0);
+            __builtin_amdgcn_sched_barrier(0);
+        }
+    };
+    // wait for K(kt+1) and V(kt) (every wave's share), then one barrier:
+    // every wave is done with interval kt-1, whose buffers take K(kt+2) and
+    // V(kt+1); sources clamped to a valid tile
+    auto enter = [&](int kt, int &tk, int &tv) {
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        vx_lds_barrier();
+        tk = min(kt + 2, n_tiles - 1);
+        tv = min(kt + 1, n_tiles - 1);
+    };
+
+    // Main interval: tile kt has no key past any query of this wave (no
+    // mask); S(kt+1) on the MFMA pipe, the softmax of tile kt beside it,
+    // this wave's loads of K(kt+2) and V(kt+1) spread over the k-steps, then
+    // P V(kt).  One straight-line body.
+    auto main_iv = [&](int kt, floatx4_t (&sc)[4][RB], floatx4_t (&sn)[4][RB]) {
+        int tk, tv;
+        enter(kt, tk, tv);
+        const int bk = kt & 1, bv = bk ^ 1;
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) sn[kb][rb] = mq[rb];
+        const char *Kt = Kl[(kt + 1) & 1];
+        bf16x8_t kf[2][4];
+        kload(Kt, 0, kf[0]);
+#pragma unroll
+        for (int ks = 0; ks < 8; ks++) {
+            if (ks + 1 < 8) kload(Kt, ks + 1, kf[(ks + 1) & 1]);
+            dma_k(tk, bk, ks);
+            dma_v(tv, bv, ks);
+#pragma unroll
+            for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++)
+                    sn[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks & 1][kb], qv[rb][ks], sn[kb][rb], 0, 0, 0);
+            sm_piece(ks, sc, false);
+#pragma unroll
+            for (int x = 0; x < 8; x++) {
+                __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
+                __builtin_amdgcn_sched_group_barrier(0x002, 2, 0);   // up to two VALU
+            }
+            __builtin_amdgcn_sched_barrier(0);
+        }
+        pv_tile(Vl[kt & 1]);
+    };
+    // Tail interval (the few tiles that straddle this wave's queries, and
+    // those past them): causal mask; the last tile's V past the valid keys
+    // zeroed (masked P is 0, and 0 * a stale NaN would not be); tiles past
+    // this wave's last query only take part in the loads.
+    auto tail_iv = [&](int kt, floatx4_t (&sc)[4][RB], floatx4_t (&sn)[4][RB]) {
+        int tk, tv;
+        enter(kt, tk, tv);
+        const int k0 = kt * KT;
+#pragma unroll
+        for (int j = 0; j < PER; j++) dma_k(tk, kt & 1, j);
+#pragma unroll
+        for (int j = 0; j < PER; j++) dma_v(tv, (kt & 1) ^ 1, j);
+        if (k0 + KT > n_keys) {
+            uint16_t *V = (uint16_t *)Vl[kt & 1];
+            for (int e = tid; e < HDG * KT; e += 256) {
+                const int d = e >> 6, key = e & 63;
+                if (k0 + key >= n_keys) V[d * KT + (((key >> 3) ^ ((d >> 1) & 7)) * 8) + (key & 7)] = 0;
+            }
+            vx_lds_barrier();   // (workgroup-uniform)
+        }
+        if (kt < wave_tiles) {
+            mask(k0, sc);
+#pragma unroll
+            for (int piece = 0; piece < 8; piece++) sm_piece(piece, sc, false);
+            if (kt + 1 < wave_tiles) {
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+                    for (int rb = 0; rb < RB; rb++) sn[kb][rb] = mq[rb];
+                s_tile(Kl[(kt + 1) & 1], sn);
+            }
+            pv_tile(Vl[kt & 1]);
+        }
+    };
+
+    // S(0) and the reference maxima, then the main intervals two at a time
+    // (the S buffers swap roles), then the tail
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+    vx_lds_barrier();
+    floatx4_t sA[4][RB], sB[4][RB];
+    zero_s(sA);
+    s_tile(Kl[0], sA);
+    if (KT - 1 > a.pos0 + r0) mask(0, sA);
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++) {
+        m0[rb] = row_max(sA, rb);
+        mq[rb] = (floatx4_t){-m0[rb], -m0[rb], -m0[rb], -m0[rb]};
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) sA[kb][rb][i] -= m0[rb];   // tile 0 relative to m0, as the others
+    }
+    int kt = 0;
+    for (; kt + 2 <= n_main; kt += 2) {
+        main_iv(kt, sA, sB);
+        main_iv(kt + 1, sB, sA);
+    }
+    auto copy_s = [&](floatx4_t (&dst)[4][RB], floatx4_t (&src)[4][RB]) {
+#pragma unroll
+        for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) dst[kb][rb] = src[kb][rb];
+    };
+    if (kt < n_main) {
+        main_iv(kt, sA, sB);
+        kt++;
+        copy_s(sA, sB);
+    }
+    for (; kt < n_tiles; kt++) {
+        tail_iv(kt, sA, sB);
+        copy_s(sA, sB);
+    }
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");   // the last (unused) tile loads
+
+    // Overflow past the fixed reference: redo this wave's queries with the
+    // online softmax (running max per query, O and l rescaled when it moves
+    // by more than 16), K and V operands read from the cache.
+    bool bad = false;
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            bad = bad || !__builtin_isfinite(Ol[rb][i]);
+#pragma unroll
+            for (int db = 0; db < 16; db++) bad = bad || !__builtin_isfinite(O[rb][db][i]);
+        }
+    if (__any(bad)) {
+        float mrow[RB];
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) {
+            mrow[rb] = -INFINITY;
+            Ol[rb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int db = 0; db < 16; db++) O[rb][db] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+        }
+        for (int t = 0; t < wave_tiles; t++) {
+            const int k0 = t * KT;
+            floatx4_t x[4][RB];
+            zero_s(x);
+#pragma unroll
+            for (int ks = 0; ks < 8; ks++)
+#pragma unroll
+                for (int kb = 0; kb < 4; kb++) {
+                    const int kr = 32 * (kb >> 1) + 8 * (n >> 2) + 4 * (kb & 1) + (n & 3);
+                    const bf16x8_t kf = as_bf16x8(*(const uint4 *)(Kc + ((size_t)(k0 + kr) * HDG + 32 * ks + 8 * g) * 2));
+#pragma unroll
+                    for (int rb = 0; rb < RB; rb++) x[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf, qv[rb][ks], x[kb][rb], 0, 0, 0);
+                }
+            mask(k0, x);
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) {
+                const float m = row_max(x, rb);
+                const float mnew = m > mrow[rb] + 16.0f ? m : mrow[rb];
+                const float alpha = __builtin_amdgcn_exp2f(mrow[rb] - mnew);   // 0 on the first tile
+                mrow[rb] = mnew;
+                m0[rb] = mnew;
+                float al[4];
+#pragma unroll
+                for (int i = 0; i < 4; i++) al[i] = __shfl(alpha, 4 * g + i, 64);
+#pragma unroll
+                for (int i = 0; i < 4; i++) {
+                    Ol[rb][i] *= al[i];
+#pragma unroll
+                    for (int db = 0; db < 16; db++) O[rb][db][i] *= al[i];
+                }
+            }
+#pragma unroll
+            for (int piece = 0; piece < 8; piece++) sm_piece(piece, x, true);
+            // V operands: keys 32ks + 8g .. +7 of dim 16db + n, zero past the valid keys
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                const int key = k0 + 32 * ks + 8 * g;
+#pragma unroll
+                for (int db = 0; db < 16; db++) {
+                    const int d = db * 16 + n;
+                    uint4 u = *(const uint4 *)(Vc + ((((size_t)(key / 32) * HDG + d) * 32) + (key % 32)) * 2);
+                    uint32_t w4[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+                    for (int e = 0; e < 4; e++) {
+                        if (key + 2 * e >= n_keys) w4[e] &= 0xffff0000u;
+                        if (key + 2 * e + 1 >= n_keys) w4[e] &= 0x0000ffffu;
+                    }
+                    const bf16x8_t vf = as_bf16x8(make_uint4(w4[0], w4[1], w4[2], w4[3]));
+#pragma unroll
+                    for (int rb = 0; rb < RB; rb++) O[rb][db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rb][ks], vf, O[rb][db], 0, 0, 0);
+                }
+#pragma unroll
+                for (int rb = 0; rb < RB; rb++) Ol[rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rb][ks], ones, Ol[rb], 0, 0, 0);
+            }
+        }
+    }
+
+    // out = O / l * sigmoid(gate), one query row (256 dims) per instruction:
+    // this wave's O rows, scaled by 1/l, go through its 32 KiB of the (now
+    // idle) tile buffers, so every gate load and output store is one whole
+    // row across the wave (lane L: dims 4L..4L+3).  Row r's 16-dim groups are
+    // XOR-swizzled by (r / 4) % 4, so the four rows one C-layout store
+    // touches fall on distinct banks.  The gate rows are loaded first, to
+    // overlap their latency with the transposition.
+    uint2 gv[RB * 16];
+#pragma unroll
+    for (int q = 0; q < RB * 16; q++) {
+        const int t = min(r0 + q, a.T - 1);
+        gv[q] = *(const uint2 *)(a.gate + ((size_t)b * a.T + t) * a.g_ts + (size_t)h * a.g_hs + 4 * lane);
+    }
+    vx_lds_barrier();   // every wave is done with the tile buffers
+    float *Ow = (float *)smem + wave * (RB * 16 * HDG);
+#pragma unroll
+    for (int rb = 0; rb < RB; rb++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float il = __builtin_amdgcn_rcpf(Ol[rb][i]);
+#pragma unroll
+            for (int db = 0; db < 16; db++) Ow[(rb * 16 + 4 * g + i) * HDG + ((db ^ g) * 16) + n] = O[rb][db][i] * il;
+        }
+    __builtin_amdgcn_wave_barrier();   // (one wave's LDS operations complete in order)
+    constexpr float L2E = 1.4426950408889634f;
+#pragma unroll
+    for (int q = 0; q < RB * 16; q++) {
+        const int t = r0 + q, sw = (q >> 2) & 3;
+        const float4 o = *(const float4 *)&Ow[q * HDG + (((lane >> 2) ^ sw) * 16) + 4 * (lane & 3)];
+        const float g0 = __uint_as_float(gv[q].x << 16), g1 = __uint_as_float(gv[q].x & 0xffff0000u);
+        const float g2 = __uint_as_float(gv[q].y << 16), g3 = __uint_as_float(gv[q].y & 0xffff0000u);
+        float4 r;
+        r.x = o.x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g0 * L2E));
+        r.y = o.y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g1 * L2E));
+        r.z = o.z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g2 * L2E));
+        r.w = o.w * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g3 * L2E));
+        if (t < a.T) *(float4 *)(a.out + (((size_t)b * a.T + t) * a.n_q + h) * HDG + 4 * lane) = r;
+    }
+}
+
 }  // namespace
 
 extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d) {
@@ -555,6 +1019,11 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
                    ((uintptr_t)d->q & 15) == 0,
                "vx27_hip_gqa_prefill: q must be 16-byte aligned with strides that are multiples of 8 elements");
     VX_REQUIRE(((uintptr_t)d->v_new & 15) == 0, "vx27_hip_gqa_prefill: v_new must be 16-byte aligned");
+    VX_REQUIRE((d->gate_tok_stride == 0 || d->gate_tok_stride % 4 == 0) &&
+                   (d->gate_head_stride == 0 || d->gate_head_stride % 4 == 0) && ((uintptr_t)d->gate & 7) == 0,
+               "vx27_hip_gqa_prefill: gate must be 8-byte aligned with strides that are multiples of 4 elements");
+    VX_REQUIRE(((uintptr_t)d->out & 15) == 0, "vx27_hip_gqa_prefill: out must be 16-byte aligned");
+    VX_REQUIRE(((uintptr_t)d->q_norm_w & 15) == 0, "vx27_hip_gqa_prefill: q_norm_w must be 16-byte aligned");
     VX_REQUIRE(d->q && d->gate && d->k_new && d->v_new && d->q_norm_w && d->k_norm_w && d->k_cache &&
                    d->v_cache && d->out,
                "vx27_hip_gqa_prefill: null pointer in descriptor");
@@ -586,9 +1055,14 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     aa.out = d->out;
     // XCD grouping needs whole KV heads per XCD pair set: n_kv | 8 and 8 | n_q
     aa.xcd_map = (8 % d->n_kv == 0) && (d->n_q % 8 == 0) && ((d->n_q / 8) * (8 / d->n_kv) == d->n_q / d->n_kv);
+#if GQP_PP
+    const int n_qt = (d->T + PP_QT - 1) / PP_QT;
+    VX_LAUNCH_NAMED(ctx, "gqp_attn", gqp_attn_pp, dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B), dim3(256), aa);
+#else
     constexpr int QT = GQP_NW * GQP_RB * 16;
     const int n_qt = (d->T + QT - 1) / QT;
     VX_LAUNCH_NAMED(ctx, "gqp_attn", (gqp_attn<GQP_NW, GQP_RB, GQP_DB != 0>), dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B),
                     dim3(GQP_NW * 64), aa);
+#endif
     return 0;
 }
