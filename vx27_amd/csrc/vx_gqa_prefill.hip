@@ -239,12 +239,15 @@ __device__ __forceinline__ void load_v(uint32_t vbuf, const char *Vt, int wave, 
 
 // NB 16-query blocks as the B operand of S^T = K Q^T: lane (g,n) of k-step
 // ks gets dims 32ks + 8g + 0..7 of token row t[blk] (the block's row n).
-// rmsn (1+w, or w with VX27_GQA_NORM_W; sum of squares in double over the 4
-// lanes of the row), RoPE (pair (i, i + half) sits in one lane: k-steps ks
-// and ks + half/32; cos and sin from the table gqp_kv wrote), then the
-// log2(e)/sqrt(256) score scale, so scores come out in the exp2 domain.
-// Every global load (rows, norm weights, cos/sin) is issued before any of
-// them is used: one round trip.
+// rmsn (1+w, or w with VX27_GQA_NORM_W), RoPE (pair (i, i + half) sits in
+// one lane: k-steps ks and ks + half/32; cos and sin from the table gqp_kv
+// wrote) and the log2(e)/sqrt(256) score scale, so scores come out in the
+// exp2 domain.  The scale commutes with the rotation, so it is folded into
+// the per-dim norm factor (1+w) log2(e)/16, computed once for both blocks.
+// The squares of the bf16 inputs are exact in fp32; the sum of squares is
+// fp32 per lane and double across the row's 4 lanes.  Every global load
+// (rows, norm weights, cos/sin) is issued before any of them is used: one
+// round trip.
 constexpr int HQ_MAX = VX_ROPE_MAXH / 64;   // k-steps holding the first half of the pairs, at most
 template <int NB>
 __device__ __forceinline__ void q_prep(const AttnArgs &a, int b, int h, const int (&t)[NB], int g,
@@ -273,11 +276,20 @@ __device__ __forceinline__ void q_prep(const AttnArgs &a, int b, int h, const in
             for (int e = 0; e < 4; e++)
                 cs[blk][ks][e] = ks < hq ? ct[16 * ks + e] : make_float4(1.f, 0.f, 1.f, 0.f);
     }
+    constexpr float QS = 1.4426950408889634f / 16.0f;   // scores in the exp2 domain
     const bool wdirect = (a.flags & VX27_GQA_NORM_W) != 0;
+    float wq[8][8];
+#pragma unroll
+    for (int ks = 0; ks < 8; ks++) {
+        const float wv[8] = {w[ks][0].x, w[ks][0].y, w[ks][0].z, w[ks][0].w,
+                             w[ks][1].x, w[ks][1].y, w[ks][1].z, w[ks][1].w};
+#pragma unroll
+        for (int e = 0; e < 8; e++) wq[ks][e] = (wdirect ? wv[e] : wv[e] + 1.0f) * QS;
+    }
 #pragma unroll
     for (int blk = 0; blk < NB; blk++) {
         float x[8][8];
-        double ss = 0.0;
+        float ssf = 0.f;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
             const uint32_t w4[4] = {u[blk][ks].x, u[blk][ks].y, u[blk][ks].z, u[blk][ks].w};
@@ -287,18 +299,16 @@ __device__ __forceinline__ void q_prep(const AttnArgs &a, int b, int h, const in
                 x[ks][2 * e + 1] = __uint_as_float(w4[e] & 0xffff0000u);
             }
 #pragma unroll
-            for (int e = 0; e < 8; e++) ss += (double)x[ks][e] * (double)x[ks][e];
+            for (int e = 0; e < 8; e++) ssf += x[ks][e] * x[ks][e];
         }
+        double ss = (double)ssf;
         ss += __shfl_xor(ss, 16, 64);
         ss += __shfl_xor(ss, 32, 64);
         const float sc = 1.0f / sqrtf((float)(ss / HDG) + 1e-6f);
 #pragma unroll
-        for (int ks = 0; ks < 8; ks++) {
-            const float wv[8] = {w[ks][0].x, w[ks][0].y, w[ks][0].z, w[ks][0].w,
-                                 w[ks][1].x, w[ks][1].y, w[ks][1].z, w[ks][1].w};
+        for (int ks = 0; ks < 8; ks++)
 #pragma unroll
-            for (int e = 0; e < 8; e++) x[ks][e] = wdirect ? (x[ks][e] * sc) * wv[e] : (x[ks][e] * sc) * (wv[e] + 1.0f);
-        }
+            for (int e = 0; e < 8; e++) x[ks][e] = (x[ks][e] * sc) * wq[ks][e];
         // the pair offset as a constant, so x stays in registers
         auto rope = [&](auto hqc) {
             constexpr int HQ = decltype(hqc)::value;
@@ -319,11 +329,10 @@ __device__ __forceinline__ void q_prep(const AttnArgs &a, int b, int h, const in
             case 2: rope(std::integral_constant<int, 2>{}); break;
             default: break;
         }
-        constexpr float QS = 1.4426950408889634f / 16.0f;   // scores in the exp2 domain
 #pragma unroll
         for (int ks = 0; ks < 8; ks++)
-            qv[blk][ks] = as_bf16x8(make_uint4(pack2(x[ks][0] * QS, x[ks][1] * QS), pack2(x[ks][2] * QS, x[ks][3] * QS),
-                                               pack2(x[ks][4] * QS, x[ks][5] * QS), pack2(x[ks][6] * QS, x[ks][7] * QS)));
+            qv[blk][ks] = as_bf16x8(make_uint4(pack2(x[ks][0], x[ks][1]), pack2(x[ks][2], x[ks][3]),
+                                               pack2(x[ks][4], x[ks][5]), pack2(x[ks][6], x[ks][7])));
     }
 }
 
