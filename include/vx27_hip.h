@@ -192,11 +192,16 @@ int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d);
  * vx27_qfwd.c:314-376): rmsn q,k -> RoPE -> k,v written to the cache (bf16,
  * format above) -> causal attention of each token over positions 0..its own
  * (earlier cache rows included) -> * sigmoid(gate).  bf16 MFMA products,
- * fp32 softmax. */
+ * fp32 softmax.
+ * Requirements (checked; -1 with a message otherwise): hd == 256; rope_dim a
+ * multiple of 64, at most 128; q 16-byte aligned with q strides multiples of
+ * 8 elements; gate 8-byte aligned with gate strides multiples of 4 elements;
+ * v_new, q_norm_w and out 16-byte aligned.  Buffers from hipMalloc and the
+ * interleaved q_proj layout (gate = q + 256) meet all of them. */
 typedef struct {
     int B, T;
     int n_q, n_kv, hd;       /* 24, 4, 256 */
-    int rope_dim;
+    int rope_dim;            /* 64 (0 = no rotation) */
     float rope_theta, rope_yarn;
     int L;                   /* cache capacity, multiple of 64; pos0 + T <= L */
     int pos0;                /* position of token 0 (same for every sequence) */
