@@ -23,6 +23,8 @@ struct vx27_hip_ctx {
     void *stage;
     size_t stage_bytes;
     int n_cu;                // compute units of the device
+    // prefill attention work schedule, cached per shape (vx_gqa_prefill.hip)
+    void *gqp_sched;
     // kernel profiler (vx27_hip_prof_*): off unless enabled
     int prof_on;
     vx_prof_rec *prof;
@@ -86,6 +88,8 @@ void vx_prof_end(vx27_hip_ctx *ctx, const char *name);
 int vx_ctx_enter(vx27_hip_ctx *ctx);
 // Device scratch of at least `bytes`, owned by ctx (synchronises before growing).
 int vx_ctx_scratch(vx27_hip_ctx *ctx, size_t bytes, void **out);
+// frees the cached prefill attention schedule (vx_gqa_prefill.hip)
+void vx_gqp_sched_free(vx27_hip_ctx *ctx);
 // Host-pointer staging buffer of at least `bytes` (device memory).
 int vx_ctx_stage(vx27_hip_ctx *ctx, size_t bytes, void **out);
 

@@ -147,6 +147,7 @@ extern "C" void vx27_hip_close(vx27_hip_ctx *ctx) {
     (void)hipStreamSynchronize(ctx->stream);
     prof_clear(ctx);
     free(ctx->prof);
+    vx_gqp_sched_free(ctx);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->stage) (void)hipFree(ctx->stage);
     (void)hipStreamDestroy(ctx->own_stream);
