@@ -230,6 +230,55 @@ def test_gqa_prefill_wide_scores(ctx):
     check_bf16(out, ref, "out")
 
 
+def test_gqa_prefill_graph():
+    """gqa_prefill captured in a HIP graph on a fresh context, for a shape not
+    seen outside the capture: the attention kernel then runs as one workgroup
+    per item instead of from a per-CU schedule (which is built and uploaded
+    outside captures only).  Every replay, with eager work between replays,
+    must equal the eager (scheduled) call bit for bit."""
+    from vx27_amd import lib as L_, workloads as W
+    lib = L_.lib()
+    c = L_.Ctx(0)
+    try:
+        def make(T, Lc):
+            d = W.gqa_prefill(B=1, T=T, config=57)
+            kc, vc = c.buf(4 * Lc * 256 * 2), c.buf(4 * Lc * 256 * 2)
+            bufs = {k: c.put(d[k]) for k in ("q", "gate", "k", "v", "q_norm_w", "k_norm_w")}
+            ob = c.buf(T * 24 * 256 * 4)
+            desc = L_.GqaPrefillDesc(1, T, 24, 4, 256, 64, 1e7, 1.0, Lc, 0, 0, bufs["q"].ptr, 0, 0,
+                                     bufs["gate"].ptr, 0, 0, bufs["k"].ptr, bufs["v"].ptr, bufs["q_norm_w"].ptr,
+                                     bufs["k_norm_w"].ptr, kc.ptr, vc.ptr, ob.ptr)
+            return d, desc, ob, list(bufs.values()) + [kc, vc, ob]
+        _, big, _, keep_big = make(300, 320)       # sizes the scratch (and caches its own schedule)
+        L_.check(lib.vx27_hip_gqa_prefill(c.h, C.byref(big)), "gqa_prefill")
+        c.sync()
+        d, desc, ob, keep = make(200, 256)
+        c.graph_begin()
+        L_.check(lib.vx27_hip_gqa_prefill(c.h, C.byref(desc)), "gqa_prefill (capture)")
+        g = c.graph_end()
+        try:
+            replays = []
+            for _ in range(3):
+                c.graph_launch(g)
+                c.sync()
+                replays.append(ob.download((1, 200, 24, 256), np.float32))
+                L_.check(lib.vx27_hip_gqa_prefill(c.h, C.byref(big)), "gqa_prefill")   # eager work between
+                c.sync()
+        finally:
+            lib.vx27_hip_graph_destroy(g)
+        L_.check(lib.vx27_hip_gqa_prefill(c.h, C.byref(desc)), "gqa_prefill")       # eager, scheduled
+        c.sync()
+        eager = ob.download((1, 200, 24, 256), np.float32)
+        for i, r in enumerate(replays):
+            assert np.array_equal(r, eager), f"graph replay {i} differs from the eager call"
+        ref, _ = oracle_gqa_prefill(d, 256)
+        check_bf16(eager, ref, "out")
+        for bb in keep + keep_big:
+            bb.free()
+    finally:
+        c.close()
+
+
 def test_prefill_deterministic(ctx):
     """Both prefills are deterministic: the same call twice gives identical
     bits (the kernels use fixed reduction orders; a missed wait on an
