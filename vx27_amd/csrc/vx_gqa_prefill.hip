@@ -610,9 +610,13 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
 // finite, and the wave redoes its queries with the online (rescaling)
 // softmax, reading K and V straight from the cache.  grid (ceil(T/128) *
 // n_q, B), block 256.
-constexpr int PP_RB = 2, PP_QT = 4 * PP_RB * 16, PP_PER = 8;
+#ifndef GQP_PP_NW
+#define GQP_PP_NW 4         // waves per pipelined-attention workgroup: 4 x 32 queries or 8 x 16
+#endif
+constexpr int PP_NW = GQP_PP_NW, PP_RB = 8 / PP_NW, PP_QT = PP_NW * PP_RB * 16, PP_PER = 32 / PP_NW;
+static_assert(PP_NW == 4 || PP_NW == 8, "4 waves of 32 queries or 8 of 16");
 
-__global__ __launch_bounds__(256) void gqp_attn_pp(AttnArgs a) {
+__global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
     constexpr int RB = PP_RB, QT = PP_QT, PER = PP_PER;
     const int n_items = a.sched ? a.sched_len : 1;
     for (int item = 0; item < n_items; item++) {
@@ -683,7 +687,9 @@ __global__ __launch_bounds__(256) void gqp_attn_pp(AttnArgs a) {
 
     bf16x8_t qv[RB][8];
     {
-        const int tq[RB] = {min(r0 + n, a.T - 1), min(r0 + 16 + n, a.T - 1)};   // rows past T repeat row T-1
+        int tq[RB];   // rows past T repeat row T-1
+#pragma unroll
+        for (int rb = 0; rb < RB; rb++) tq[rb] = min(r0 + 16 * rb + n, a.T - 1);
         q_prep<RB>(a, b, h, tq, g, qv);
     }
 
@@ -834,14 +840,16 @@ __global__ __launch_bounds__(256) void gqp_attn_pp(AttnArgs a) {
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) {
             if (ks + 1 < 8) kload(Kt, ks + 1, kf[(ks + 1) & 1]);
-            dma_k(tk, bk, ks);
-            dma_v(tv, bv, ks);
+            if (ks < PER) {
+                dma_k(tk, bk, ks);
+                dma_v(tv, bv, ks);
+            }
 #pragma unroll
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
                 for (int rb = 0; rb < RB; rb++)
                     sn[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks & 1][kb], qv[rb][ks], sn[kb][rb], 0, 0, 0);
-            sm_piece(ks, sc, false);
+            if (ks < 4 * RB) sm_piece(ks, sc, false);
 #pragma unroll
             for (int x = 0; x < 8; x++) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
@@ -876,7 +884,7 @@ __global__ __launch_bounds__(256) void gqp_attn_pp(AttnArgs a) {
         if (kt < wave_tiles) {
             mask(k0, sc);
 #pragma unroll
-            for (int piece = 0; piece < 8; piece++) sm_piece(piece, sc, false);
+            for (int piece = 0; piece < 4 * RB; piece++) sm_piece(piece, sc, false);
             if (kt + 1 < wave_tiles) {
 #pragma unroll
                 for (int kb = 0; kb < 4; kb++)
@@ -962,7 +970,7 @@ __global__ __launch_bounds__(256) void gqp_attn_pp(AttnArgs a) {
                 }
             }
 #pragma unroll
-            for (int piece = 0; piece < 8; piece++) sm_piece(piece, x, true);
+            for (int piece = 0; piece < 4 * RB; piece++) sm_piece(piece, x, true);
             // V operands: keys 32ks + 8g .. +7 of dim 16db + n, zero past the valid keys
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) {
@@ -1213,9 +1221,9 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     if (sc) {   // persistent: one workgroup per CU over its list
         aa.sched = sc->dev;
         aa.sched_len = sc->len;
-        VX_LAUNCH_NAMED(ctx, "gqp_attn", gqp_attn_pp, dim3((unsigned)sc->n_wg), dim3(256), aa);
+        VX_LAUNCH_NAMED(ctx, "gqp_attn", gqp_attn_pp, dim3((unsigned)sc->n_wg), dim3(PP_NW * 64), aa);
     } else {    // (inside a stream capture, first call of a shape) one workgroup per item
-        VX_LAUNCH_NAMED(ctx, "gqp_attn", gqp_attn_pp, dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B), dim3(256), aa);
+        VX_LAUNCH_NAMED(ctx, "gqp_attn", gqp_attn_pp, dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B), dim3(PP_NW * 64), aa);
     }
 #else
     constexpr int QT = GQP_NW * GQP_RB * 16;
