@@ -156,6 +156,8 @@ int vx27_hip_dn_prefill(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d);
  * L (the capacity) must be a multiple of 64.  Use vx27_hip_kv_write /
  * vx27_hip_kv_read to move rows in or out of this layout. */
 #define VX27_GQA_NORM_W 1u  /* q/k norm as x*s*w (vx27_gqa.c:10-15) instead of x*s*(1+w) */
+#define VX27_GQA_NO_GATE 2u /* no output gate: out = attention (the MTP drafter's use_gate = 0,
+                               vx27_mtp.c:258); gate may be NULL */
 
 typedef struct {
     int B;
@@ -177,7 +179,7 @@ typedef struct {
                                     (sequence stride kv_seq_stride) */
     const float *q_norm_w, *k_norm_w;  /* [hd] */
     uint16_t *k_cache, *v_cache;       /* bf16, format above; row pos is written */
-    float *out;              /* [B][n_q][hd]: attention * sigmoid(gate) */
+    float *out;              /* [B][n_q][hd]: attention * sigmoid(gate) (attention alone with VX27_GQA_NO_GATE) */
     int n_split;             /* key splits per (sequence, KV head); 0 = automatic */
     size_t kv_seq_stride;    /* per-sequence stride of k_new / v_new in floats; 0 = n_kv*hd */
 } vx27_gqa_desc;
@@ -205,7 +207,7 @@ typedef struct {
     float rope_theta, rope_yarn;
     int L;                   /* cache capacity, multiple of 64; pos0 + T <= L */
     int pos0;                /* position of token 0 (same for every sequence) */
-    unsigned flags;          /* VX27_GQA_NORM_W */
+    unsigned flags;          /* VX27_GQA_NORM_W, VX27_GQA_NO_GATE */
     /* bf16 raw q and gate logits: element (b, t, h, i) at
      * q[(b*T + t)*q_tok_stride + h*q_head_stride + i]; 0 strides = dense
      * [B][T][n_q][hd].  Interleaved q_proj output: head stride 2*hd, gate = q + hd. */

@@ -45,7 +45,7 @@ class GqaCfg(C.Structure):
                 ("kv_bf16", C.c_int), ("q_norm_w", VP), ("k_norm_w", VP),
                 ("k_cache", VP), ("v_cache", VP),
                 ("k_pos_stride", C.c_size_t), ("k_head_stride", C.c_size_t),
-                ("v_pos_stride", C.c_size_t), ("v_head_stride", C.c_size_t)]
+                ("v_pos_stride", C.c_size_t), ("v_head_stride", C.c_size_t), ("no_gate", C.c_int)]
 
 
 class AttendArgs(C.Structure):
@@ -75,7 +75,8 @@ class DnRunArgs(C.Structure):
 class GqaPrefillArgs(C.Structure):
     _fields_ = [(n, C.c_int) for n in ("B", "T", "n_q", "n_kv", "hd", "rope_dim", "pos0", "L", "threads")] + \
                [("rope_theta", C.c_float), ("rope_yarn", C.c_float)] + \
-               [(n, VP) for n in ("q", "gate", "k", "v", "q_norm_w", "k_norm_w", "k_cache", "v_cache", "out")]
+               [(n, VP) for n in ("q", "gate", "k", "v", "q_norm_w", "k_norm_w", "k_cache", "v_cache", "out")] + \
+               [("no_gate", C.c_int)]
 
 
 class DnLayerW(C.Structure):

@@ -248,7 +248,8 @@ static void orc_gp_worker(void *arg, int tid, int n) {
         orc_attend_one(&s, h, sc);
         const size_t o = ((size_t)bt * a->n_q + h) * hd;
         for (int i = 0; i < hd; i++)
-            a->out[o + i] = one[(size_t)h * hd + i] * (1.0f / (1.0f + expf(-a->gate[o + i])));
+            a->out[o + i] = a->no_gate ? one[(size_t)h * hd + i]
+                                       : one[(size_t)h * hd + i] * (1.0f / (1.0f + expf(-a->gate[o + i])));
     }
     free(sc);
     free(one);

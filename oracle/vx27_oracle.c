@@ -366,6 +366,10 @@ void orc_gqa_token(const orc_gqa_cfg *c, const float *q_raw, size_t q_head_strid
     orc_attend(&a);
     for (int h = 0; h < nq; h++)
         for (int i = 0; i < hd; i++) {
+            if (c->no_gate) {   /* vx27_mtp.c:258 with use_gate = 0 */
+                out[(size_t)h * hd + i] = att[(size_t)h * hd + i];
+                continue;
+            }
             const float gl = gate[(size_t)h * gate_head_stride + i];
             out[(size_t)h * hd + i] = att[(size_t)h * hd + i] * (1.0f / (1.0f + expf(-gl)));
         }

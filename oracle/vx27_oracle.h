@@ -124,12 +124,14 @@ void orc_dn_token(const orc_dn_cfg *c, const float *qkv, const float *a, const f
  * k1, v1 [n_kv][hd] raw projections; rmsn(1+w) on q and k; RoPE with the
  * given table; append k,v at position pos of the caller's cache (layout by
  * strides, float or bf16 storage); attend over 0..pos (double dot);
- * out [n_q][hd] = attention * sigmoid(gate). */
+ * out [n_q][hd] = attention * sigmoid(gate), or attention alone with no_gate
+ * (the MTP drafter's use_gate = 0, vx27_mtp.c:258). */
 typedef struct {
     int n_q, n_kv, hd, rope_dim, kv_bf16;
     const float *q_norm_w, *k_norm_w;      /* [hd] each, (1+w) form */
     void *k_cache, *v_cache;
     size_t k_pos_stride, k_head_stride, v_pos_stride, v_head_stride;
+    int no_gate;
 } orc_gqa_cfg;
 void orc_gqa_token(const orc_gqa_cfg *c, const float *q_raw, size_t q_head_stride,
                    const float *gate, size_t gate_head_stride,
@@ -198,7 +200,8 @@ double orc_attend_batch(const orc_attend_batch_args *a);
  * pos0+t (orc_rope_cos_sin), k,v appended to a float cache
  * [B][L][n_kv][hd] (rows < pos0 supplied by the caller), then the token's
  * attention over positions 0..pos0+t (double dot, float softmax) times
- * sigmoid(gate).  The attention units (b, t, h) run in parallel. */
+ * sigmoid(gate) (or not, with no_gate).  The attention units (b, t, h) run
+ * in parallel. */
 typedef struct {
     int B, T, n_q, n_kv, hd, rope_dim, pos0, L, threads;
     float rope_theta, rope_yarn;
@@ -207,6 +210,7 @@ typedef struct {
     const float *q_norm_w, *k_norm_w;
     float *k_cache, *v_cache;       /* [B][L][n_kv][hd] */
     float *out;                     /* [B][T][n_q][hd] */
+    int no_gate;
 } orc_gqa_prefill_args;
 double orc_gqa_prefill(const orc_gqa_prefill_args *a);
 

@@ -44,7 +44,7 @@ def bitexact_frac(a, b):
     return float(np.mean(np.asarray(a) == np.asarray(b)))
 
 
-def oracle_gqa_decode(d, Lcap, threads=None):
+def oracle_gqa_decode(d, Lcap, threads=None, no_gate=False):
     """Oracle for one gated-GQA decode step of every sequence of workload d
     (gqa_decode): bf16 cache [B][Lcap][n_kv][hd] holding the prefix, append at
     pos, attend 0..pos (double dot), gate.  Returns (out [B][n_q][hd],
@@ -67,7 +67,7 @@ def oracle_gqa_decode(d, Lcap, threads=None):
         vc[:nk] = d["V"][b]
         cs, sn = O.rope_cos_sin(pos)
         cfg = O.GqaCfg(n_q, n_kv, hd, 64, 1, qn.ctypes.data, kn.ctypes.data, kc.ctypes.data,
-                       vc.ctypes.data, n_kv * hd, hd, n_kv * hd, hd)
+                       vc.ctypes.data, n_kv * hd, hd, n_kv * hd, hd, int(no_gate))
         out = np.empty((n_q, hd), np.float32)
         k1 = np.ascontiguousarray(d["k_new"][b], np.float32)
         v1 = np.ascontiguousarray(d["v_new"][b], np.float32)

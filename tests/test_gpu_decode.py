@@ -135,6 +135,21 @@ def test_gqa_decode_8k(ctx, B):
         assert np.all(kd <= np.abs(W.bf16_to_f32(kr[b])) * 2 ** -7 + 1e-30)
 
 
+def test_gqa_decode_no_gate(ctx):
+    """VX27_GQA_NO_GATE: the attention without the output gate, as the MTP
+    drafter's decoder layer runs with use_gate = 0 (vx27_mtp.c:219-258)."""
+    from vx27_amd import lib as L, workloads as W
+    d = W.gqa_decode(B=2, L=300, config=23)
+    Lcap = 320
+    lay = _gqa_layer(ctx, d, 2, Lcap)
+    lay.flags |= L.GQA_NO_GATE
+    out = lay.decode(d["pos"], d["qg"], d["k_new"], d["v_new"])
+    ref, _, _ = oracle_gqa_decode(d, Lcap, no_gate=True)
+    _check_gqa(out, ref, "no gate")
+    gated, _, _ = oracle_gqa_decode(d, Lcap)
+    assert np.abs(ref - gated).max() > 0.1   # the flag changes the answer
+
+
 def test_gqa_edges_and_splits(ctx):
     """Ragged positions across tile edges (0, 1, 31, 32, 33, 63, 64, 100), and
     the same answer for every split count."""

@@ -376,3 +376,41 @@ def test_gqa_prefill_equals_token_chain(O):
                               pos0 + t, c, s, o)
         assert np.array_equal(o, out[0, t]), t
     assert np.array_equal(kc, kr) and np.array_equal(vc, vr)
+
+
+def test_gqa_no_gate_pinned(O):
+    """The no-gate branch (vx27_mtp.c:258 with use_gate = 0) equals the gated
+    path (pinned to vx27_qlayer) with gate logits of 100, whose sigmoid is
+    1.0f exactly, bit for bit: for one token and for the prefill."""
+    r = I.rng("gqa_no_gate")
+    n_q, n_kv, hd, T, pos0, L = 24, 4, 256, 3, 2, 8
+    q = I.normal(r, (1, T, n_q, hd))
+    k, v = I.normal(r, (1, T, n_kv, hd)), I.normal(r, (1, T, n_kv, hd))
+    qw, kw = I.normal(r, hd, 0.1), I.normal(r, hd, 0.1)
+    big = np.full((1, T, n_q, hd), 100.0, np.float32)
+    assert np.float32(1.0) / (np.float32(1.0) + np.exp(np.float32(-100.0))) == np.float32(1.0)
+    kc0 = np.zeros((1, L, n_kv, hd), np.float32)
+    kc0[0, :pos0] = I.normal(r, (pos0, n_kv, hd))
+    outs = []
+    for no_gate in (0, 1):
+        kc, vc = kc0.copy(), kc0.copy()
+        out = np.empty((1, T, n_q, hd), np.float32)
+        a = O.GqaPrefillArgs(1, T, n_q, n_kv, hd, 64, pos0, L, 3, 1e7, 1.0, q.ctypes.data, big.ctypes.data,
+                             k.ctypes.data, v.ctypes.data, qw.ctypes.data, kw.ctypes.data, kc.ctypes.data,
+                             vc.ctypes.data, out.ctypes.data, no_gate)
+        O.lib().orc_gqa_prefill(C.byref(a))
+        outs.append(out)
+    assert np.array_equal(outs[0], outs[1])
+    tok = []
+    for no_gate in (0, 1):
+        kr, vr = kc0.copy(), kc0.copy()
+        cfg = O.GqaCfg(n_q, n_kv, hd, 64, 0, qw.ctypes.data, kw.ctypes.data, kr.ctypes.data, vr.ctypes.data,
+                       n_kv * hd, hd, n_kv * hd, hd, no_gate)
+        c, s_ = O.rope_cos_sin(pos0)
+        o = np.empty((n_q, hd), np.float32)
+        gt = f32(big[0, 0])
+        O.lib().orc_gqa_token(C.byref(cfg), f32(q[0, 0]), hd, gt.ctypes.data, hd, f32(k[0, 0]), f32(v[0, 0]),
+                              pos0, c, s_, o)
+        tok.append(o)
+    assert np.array_equal(tok[0], tok[1])
+    assert np.array_equal(tok[1], outs[1][0, 0])

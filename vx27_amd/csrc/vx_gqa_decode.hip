@@ -2,7 +2,8 @@
 //
 // Reference semantics (vx27_qfwd.c:172-211): rmsn(q)*(1+w) and rmsn(k)*(1+w)
 // per head, NeoX RoPE on the first rope_dim dims, append k,v at position pos,
-// softmax(q.k / sqrt(hd)) over positions 0..pos, P.V, then * sigmoid(gate).
+// softmax(q.k / sqrt(hd)) over positions 0..pos, P.V, then * sigmoid(gate)
+// (no gate with VX27_GQA_NO_GATE, as the MTP drafter's use_gate = 0).
 //
 // Kernels per call:
 //   gqa_prep     one workgroup per (sequence, head): norm + RoPE of q (kept
@@ -12,7 +13,8 @@
 //                the cache once for all n_q/n_kv query heads of the group with
 //                v_mfma_f32_16x16x32_bf16, online softmax in fp32, writes a
 //                partial (m, l, O) per query head.
-//   gqa_combine  merges the partials, divides by l, applies sigmoid(gate).
+//   gqa_combine  merges the partials, divides by l, applies sigmoid(gate)
+//                (unless there is no gate).
 //
 // Tile algebra (32 keys per tile, query heads padded to 16):
 //   S^T[key][q] = K[key][:] . Q^T[:][q]    two 16-row MFMA blocks r=0,1 over
@@ -258,7 +260,7 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(VX_SPLIT_WPE
 struct CombArgs {
     int B, n_q, n_kv, n_split;
     const float *part_o, *part_ml;
-    const float *gate;
+    const float *gate;           // NULL: no output gate
     size_t g_ss, g_hs;
     float *out;                  // [B][n_q][256] or NULL
     uint16_t *out_packed;        // optional packed GEMV operand of out (K = n_q*256)
@@ -293,8 +295,11 @@ __global__ __launch_bounds__(256) void gqa_combine(CombArgs a) {
     if (wave != 0) return;
     const float Lt = ((s_l[0] + s_l[1]) + s_l[2]) + s_l[3];
     const float Ot = ((s_o[0][lane] + s_o[1][lane]) + s_o[2][lane]) + s_o[3][lane];
-    const float gl = a.gate[(size_t)b * a.g_ss + (size_t)h * a.g_hs + i];
-    const float r = (Ot / Lt) * (1.0f / (1.0f + expf(-gl)));
+    float r = Ot / Lt;
+    if (a.gate) {
+        const float gl = a.gate[(size_t)b * a.g_ss + (size_t)h * a.g_hs + i];
+        r = r * (1.0f / (1.0f + expf(-gl)));
+    }
     if (a.out) a.out[((size_t)b * a.n_q + h) * HDG + i] = r;
     if (a.out_packed) vx_pack_store(a.out_packed, a.B, b, h * HDG + i, r);
 }
@@ -358,7 +363,8 @@ static int gqa_check(const vx27_gqa_desc *d) {
                "vx27_hip_gqa_decode: need n_q = k*n_kv with k <= 16 (n_q=%d n_kv=%d)", d->n_q, d->n_kv);
     VX_REQUIRE(d->L >= 64 && d->L % 64 == 0, "vx27_hip_gqa_decode: L must be a positive multiple of 64");
     VX_REQUIRE(d->rope_dim >= 0 && d->rope_dim <= HDG, "vx27_hip_gqa_decode: bad rope_dim");
-    VX_REQUIRE(d->pos && d->q && d->gate && d->k_new && d->v_new && d->q_norm_w && d->k_norm_w &&
+    VX_REQUIRE(d->pos && d->q && (d->gate || (d->flags & VX27_GQA_NO_GATE)) && d->k_new && d->v_new &&
+                   d->q_norm_w && d->k_norm_w &&
                    d->k_cache && d->v_cache,
                "vx27_hip_gqa_decode: null pointer in descriptor");
     return 0;
@@ -413,7 +419,7 @@ int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uin
 
     CombArgs ca;
     ca.B = d->B; ca.n_q = d->n_q; ca.n_kv = d->n_kv; ca.n_split = n_split;
-    ca.part_o = part_o; ca.part_ml = part_ml; ca.gate = d->gate;
+    ca.part_o = part_o; ca.part_ml = part_ml; ca.gate = (d->flags & VX27_GQA_NO_GATE) ? nullptr : d->gate;
     ca.g_ss = d->gate_seq_stride; ca.g_hs = d->gate_head_stride; ca.out = d->out;
     ca.out_packed = out_packed;
     VX_LAUNCH(ctx, gqa_combine, dim3(d->n_q, d->B, HDG / 64), dim3(256), ca);

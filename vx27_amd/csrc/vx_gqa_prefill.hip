@@ -182,7 +182,7 @@ struct AttnArgs {
     size_t q_ts, q_hs;
     const float *q_norm_w;
     const uint16_t *k_cache, *v_cache;
-    const uint16_t *gate;
+    const uint16_t *gate;         // NULL: no output gate
     size_t g_ts, g_hs;
     float *out;                   // [B][T][n_q][256]
     const float2 *cs_tab;         // [T][rope_dim/2] (cos, sin), written by gqp_kv
@@ -585,8 +585,8 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
 #pragma unroll
             for (int db = 0; db < 16; db++) {
                 const int dim = db * 16 + n;
-                const float gl = vx_bf16_to_f32(gp[dim]);
-                op[dim] = (O[rb][db][i] * il[i]) * (1.0f / (1.0f + expf(-gl)));
+                const float gl = a.gate ? vx_bf16_to_f32(gp[dim]) : 0.0f;
+                op[dim] = a.gate ? (O[rb][db][i] * il[i]) * (1.0f / (1.0f + expf(-gl))) : O[rb][db][i] * il[i];
             }
         }
     }
@@ -1003,10 +1003,12 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
     // touches fall on distinct banks.  The gate rows are loaded first, to
     // overlap their latency with the transposition.
     uint2 gv[RB * 16];
+    const bool gated = a.gate != nullptr;
 #pragma unroll
     for (int q = 0; q < RB * 16; q++) {
         const int t = min(r0 + q, a.T - 1);
-        gv[q] = *(const uint2 *)(a.gate + ((size_t)b * a.T + t) * a.g_ts + (size_t)h * a.g_hs + 4 * lane);
+        gv[q] = gated ? *(const uint2 *)(a.gate + ((size_t)b * a.T + t) * a.g_ts + (size_t)h * a.g_hs + 4 * lane)
+                      : make_uint2(0u, 0u);
     }
     vx_lds_barrier();   // every wave is done with the tile buffers
     float *Ow = (float *)smem + wave * (RB * 16 * HDG);
@@ -1026,11 +1028,13 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
         const float4 o = *(const float4 *)&Ow[q * HDG + (((lane >> 2) ^ sw) * 16) + 4 * (lane & 3)];
         const float g0 = __uint_as_float(gv[q].x << 16), g1 = __uint_as_float(gv[q].x & 0xffff0000u);
         const float g2 = __uint_as_float(gv[q].y << 16), g3 = __uint_as_float(gv[q].y & 0xffff0000u);
-        float4 r;
-        r.x = o.x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g0 * L2E));
-        r.y = o.y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g1 * L2E));
-        r.z = o.z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g2 * L2E));
-        r.w = o.w * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g3 * L2E));
+        float4 r = o;
+        if (gated) {
+            r.x = o.x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g0 * L2E));
+            r.y = o.y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g1 * L2E));
+            r.z = o.z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g2 * L2E));
+            r.w = o.w * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g3 * L2E));
+        }
         if (t < a.T) *(float4 *)(a.out + (((size_t)b * a.T + t) * a.n_q + h) * HDG + 4 * lane) = r;
     }
     }   // items
@@ -1176,12 +1180,13 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
                    ((uintptr_t)d->q & 15) == 0,
                "vx27_hip_gqa_prefill: q must be 16-byte aligned with strides that are multiples of 8 elements");
     VX_REQUIRE(((uintptr_t)d->v_new & 15) == 0, "vx27_hip_gqa_prefill: v_new must be 16-byte aligned");
-    VX_REQUIRE((d->gate_tok_stride == 0 || d->gate_tok_stride % 4 == 0) &&
-                   (d->gate_head_stride == 0 || d->gate_head_stride % 4 == 0) && ((uintptr_t)d->gate & 7) == 0,
+    const bool gated = !(d->flags & VX27_GQA_NO_GATE);
+    VX_REQUIRE(!gated || ((d->gate_tok_stride == 0 || d->gate_tok_stride % 4 == 0) &&
+                          (d->gate_head_stride == 0 || d->gate_head_stride % 4 == 0) && ((uintptr_t)d->gate & 7) == 0),
                "vx27_hip_gqa_prefill: gate must be 8-byte aligned with strides that are multiples of 4 elements");
     VX_REQUIRE(((uintptr_t)d->out & 15) == 0, "vx27_hip_gqa_prefill: out must be 16-byte aligned");
     VX_REQUIRE(((uintptr_t)d->q_norm_w & 15) == 0, "vx27_hip_gqa_prefill: q_norm_w must be 16-byte aligned");
-    VX_REQUIRE(d->q && d->gate && d->k_new && d->v_new && d->q_norm_w && d->k_norm_w && d->k_cache &&
+    VX_REQUIRE(d->q && (d->gate || !gated) && d->k_new && d->v_new && d->q_norm_w && d->k_norm_w && d->k_cache &&
                    d->v_cache && d->out,
                "vx27_hip_gqa_prefill: null pointer in descriptor");
     KvArgs ka = {};
@@ -1206,7 +1211,7 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     aa.q_hs = d->q_head_stride ? d->q_head_stride : HDG;
     aa.q_norm_w = d->q_norm_w;
     aa.k_cache = d->k_cache; aa.v_cache = d->v_cache;
-    aa.gate = d->gate;
+    aa.gate = gated ? d->gate : nullptr;
     aa.g_ts = d->gate_tok_stride ? d->gate_tok_stride : (size_t)d->n_q * HDG;
     aa.g_hs = d->gate_head_stride ? d->gate_head_stride : HDG;
     aa.out = d->out;

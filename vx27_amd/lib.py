@@ -17,6 +17,7 @@ VP = C.c_void_p
 F32, BF16 = 0, 1
 DN_CONV, DN_PRE_RMS, DN_PRE_L2, DN_OUT_GATE = 1, 2, 4, 8
 GQA_NORM_W = 1
+GQA_NO_GATE = 2
 ERR_ABORT, ERR_POISON = 0, 1
 
 
