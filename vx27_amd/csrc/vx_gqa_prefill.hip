@@ -613,8 +613,12 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
 #ifndef GQP_PP_NW
 #define GQP_PP_NW 4         // waves per pipelined-attention workgroup: 4 x 32 queries or 8 x 16
 #endif
-constexpr int PP_NW = GQP_PP_NW, PP_RB = 8 / PP_NW, PP_QT = PP_NW * PP_RB * 16, PP_PER = 32 / PP_NW;
-static_assert(PP_NW == 4 || PP_NW == 8, "4 waves of 32 queries or 8 of 16");
+#ifndef GQP_PP_RB
+#define GQP_PP_RB (8 / GQP_PP_NW)   // 16-query blocks per wave
+#endif
+constexpr int PP_NW = GQP_PP_NW, PP_RB = GQP_PP_RB, PP_QT = PP_NW * PP_RB * 16, PP_PER = 32 / PP_NW;
+static_assert((PP_NW == 4 && (PP_RB == 2 || PP_RB == 3)) || (PP_NW == 8 && PP_RB == 1),
+              "4 waves of 32 or 48 queries, or 8 of 16");
 
 __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
     constexpr int RB = PP_RB, QT = PP_QT, PER = PP_PER;
@@ -849,7 +853,8 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
 #pragma unroll
                 for (int rb = 0; rb < RB; rb++)
                     sn[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks & 1][kb], qv[rb][ks], sn[kb][rb], 0, 0, 0);
-            if (ks < 4 * RB) sm_piece(ks, sc, false);
+#pragma unroll
+            for (int p = ks; p < 4 * RB; p += 8) sm_piece(p, sc, false);
 #pragma unroll
             for (int x = 0; x < 8; x++) {
                 __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // one MFMA
@@ -996,9 +1001,9 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
     }
 
     // out = O / l * sigmoid(gate), one query row (256 dims) per instruction:
-    // this wave's O rows, scaled by 1/l, go through its 32 KiB of the (now
-    // idle) tile buffers, so every gate load and output store is one whole
-    // row across the wave (lane L: dims 4L..4L+3).  Row r's 16-dim groups are
+    // this wave's O rows, scaled by 1/l, go 16 at a time through its 16 KiB
+    // of the (now idle) tile buffers, so every gate load and output store is
+    // one whole row across the wave (lane L: dims 4L..4L+3).  Row r's 16-dim groups are
     // XOR-swizzled by (r / 4) % 4, so the four rows one C-layout store
     // touches fall on distinct banks.  The gate rows are loaded first, to
     // overlap their latency with the transposition.
@@ -1011,31 +1016,33 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
                       : make_uint2(0u, 0u);
     }
     vx_lds_barrier();   // every wave is done with the tile buffers
-    float *Ow = (float *)smem + wave * (RB * 16 * HDG);
+    float *Ow = (float *)smem + wave * (16 * HDG);   // 16 rows at a time
+    constexpr float L2E = 1.4426950408889634f;
 #pragma unroll
-    for (int rb = 0; rb < RB; rb++)
+    for (int rb = 0; rb < RB; rb++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const float il = __builtin_amdgcn_rcpf(Ol[rb][i]);
 #pragma unroll
-            for (int db = 0; db < 16; db++) Ow[(rb * 16 + 4 * g + i) * HDG + ((db ^ g) * 16) + n] = O[rb][db][i] * il;
+            for (int db = 0; db < 16; db++) Ow[(4 * g + i) * HDG + ((db ^ g) * 16) + n] = O[rb][db][i] * il;
         }
-    __builtin_amdgcn_wave_barrier();   // (one wave's LDS operations complete in order)
-    constexpr float L2E = 1.4426950408889634f;
+        __builtin_amdgcn_wave_barrier();   // (one wave's LDS operations complete in order)
 #pragma unroll
-    for (int q = 0; q < RB * 16; q++) {
-        const int t = r0 + q, sw = (q >> 2) & 3;
-        const float4 o = *(const float4 *)&Ow[q * HDG + (((lane >> 2) ^ sw) * 16) + 4 * (lane & 3)];
-        const float g0 = __uint_as_float(gv[q].x << 16), g1 = __uint_as_float(gv[q].x & 0xffff0000u);
-        const float g2 = __uint_as_float(gv[q].y << 16), g3 = __uint_as_float(gv[q].y & 0xffff0000u);
-        float4 r = o;
-        if (gated) {
-            r.x = o.x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g0 * L2E));
-            r.y = o.y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g1 * L2E));
-            r.z = o.z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g2 * L2E));
-            r.w = o.w * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g3 * L2E));
+        for (int qq = 0; qq < 16; qq++) {
+            const int q = rb * 16 + qq, t = r0 + q, sw = (qq >> 2) & 3;
+            const float4 o = *(const float4 *)&Ow[qq * HDG + (((lane >> 2) ^ sw) * 16) + 4 * (lane & 3)];
+            const float g0 = __uint_as_float(gv[q].x << 16), g1 = __uint_as_float(gv[q].x & 0xffff0000u);
+            const float g2 = __uint_as_float(gv[q].y << 16), g3 = __uint_as_float(gv[q].y & 0xffff0000u);
+            float4 r = o;
+            if (gated) {
+                r.x = o.x * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g0 * L2E));
+                r.y = o.y * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g1 * L2E));
+                r.z = o.z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g2 * L2E));
+                r.w = o.w * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g3 * L2E));
+            }
+            if (t < a.T) *(float4 *)(a.out + (((size_t)b * a.T + t) * a.n_q + h) * HDG + 4 * lane) = r;
         }
-        if (t < a.T) *(float4 *)(a.out + (((size_t)b * a.T + t) * a.n_q + h) * HDG + 4 * lane) = r;
+        __builtin_amdgcn_wave_barrier();   // this pass's reads before the next pass's writes
     }
     }   // items
 }
