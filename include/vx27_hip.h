@@ -198,7 +198,8 @@ int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d);
  * Requirements (checked; -1 with a message otherwise): hd == 256; rope_dim a
  * multiple of 64, at most 128; q 16-byte aligned with q strides multiples of
  * 8 elements; gate 8-byte aligned with gate strides multiples of 4 elements;
- * v_new, q_norm_w and out 16-byte aligned.  Buffers from hipMalloc and the
+ * k_new 8-byte aligned; v_new, q_norm_w, out, k_cache and v_cache 16-byte
+ * aligned.  Buffers from hipMalloc and the
  * interleaved q_proj layout (gate = q + 256) meet all of them. */
 typedef struct {
     int B, T;
@@ -247,13 +248,13 @@ int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const
                        size_t x_stride, int B, float *y, size_t y_stride);
 
 /* Weight tiling for the layer entry points: row-major bf16 W [N][K] into the
- * MFMA tile layout [K/(32*KG)][N/16][KG][64 lanes][8], KG = 4 k-steps when
- * K/32 is a multiple of 4 (else 2 or 1); lane (g,m) of tile (k-step s, row
- * block rb) holds W[16rb + m][32s + 8g .. 8g+7].  Each wave loads 1 KiB of
- * contiguous weights per tile, a row block's KG k-steps are adjacent, and
- * the row blocks of one k-group are adjacent, so a launch streams long
- * contiguous runs.  Done once per weight, like the reference's offline forge
- * of its packed weight format (src/vx_forge.c). */
+ * MFMA tile layout [K/32][N/16][64 lanes][8]: lane (g,m) of tile (k-step s,
+ * row block rb) holds W[16rb + m][32s + 8g .. 8g+7].  Each wave loads 1 KiB
+ * of contiguous weights per tile and the row blocks of one k-step are
+ * adjacent, so a launch streams long contiguous runs.  (A build option,
+ * VX_GEMV_KG = 2 or 4, groups that many k-steps of a row block together.)
+ * Done once per weight, like the reference's offline forge of its packed
+ * weight format (src/vx_forge.c). */
 int vx27_hip_pack_weights_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, uint16_t *W_tiled);
 
 /* The mixer of one Gated DeltaNet layer for one decode token of B <= 5
@@ -271,7 +272,7 @@ typedef struct {
     const uint16_t *x_packed;   /* optional: x already packed by vx27_hip_pack_x (or NULL) */
     const uint16_t *w_in;       /* bf16 [C + nv*hd + 2*nv][hidden], tiled (vx27_hip_pack_weights_bf16) */
     const uint16_t *w_out;      /* bf16 [hidden][nv*hd], tiled */
-    const void *conv_w;         /* [C][4] */
+    const void *conv_w;         /* [C][4], 16-byte aligned */
     int conv_w_dtype;           /* VX27_F32 or VX27_BF16 */
     const float *A_log, *dt_bias, *norm_w;  /* [nv], [nv], [hd] */
     float *S;                   /* [B][nv][hd][hd] in/out */

@@ -114,7 +114,7 @@ def test_dn_prefill_split_prompt(ctx):
 
 
 # ------------------------------------------------------------------ GQA
-def run_gqa_prefill(ctx, d, L, prior=None, interleave=False, flags=0):
+def run_gqa_prefill(ctx, d, L, prior=None, interleave=False, flags=0, rope_dim=64):
     """Prefill the workload's T tokens at positions pos0.. into a fresh cache of
     capacity L (rows < pos0 from `prior` = (k, v) fp32 [B][pos0][n_kv][256]);
     returns out [B][T][n_q][256]."""
@@ -146,7 +146,7 @@ def run_gqa_prefill(ctx, d, L, prior=None, interleave=False, flags=0):
     kn, vn = ctx.put(d["k"]), ctx.put(d["v"])
     qw, kw = ctx.put(d["q_norm_w"]), ctx.put(d["k_norm_w"])
     ob = ctx.buf(B * T * n_q * hd * 4)
-    desc = L_.GqaPrefillDesc(B, T, n_q, n_kv, hd, 64, 1e7, 1.0, L, pos0, flags, qp, ts, hs, gp, ts, hs,
+    desc = L_.GqaPrefillDesc(B, T, n_q, n_kv, hd, rope_dim, 1e7, 1.0, L, pos0, flags, qp, ts, hs, gp, ts, hs,
                              kn.ptr, vn.ptr, qw.ptr, kw.ptr, kc.ptr, vc.ptr, ob.ptr)
     L_.check(lib.vx27_hip_gqa_prefill(ctx.h, C.byref(desc)), "gqa_prefill")
     out = ob.download((B, T, n_q, hd), np.float32)
@@ -155,7 +155,7 @@ def run_gqa_prefill(ctx, d, L, prior=None, interleave=False, flags=0):
     return out
 
 
-def oracle_gqa_prefill(d, L, prior=None, no_gate=False):
+def oracle_gqa_prefill(d, L, prior=None, no_gate=False, rope_dim=64):
     from oracle import oracle as O
     from vx27_amd import workloads as W
     B, T, n_q, hd = d["q"].shape
@@ -167,7 +167,7 @@ def oracle_gqa_prefill(d, L, prior=None, no_gate=False):
     if prior is not None:
         kc[:, :d["pos0"]], vc[:, :d["pos0"]] = prior
     out = np.empty((B, T, n_q, hd), np.float32)
-    a = O.GqaPrefillArgs(B, T, n_q, n_kv, hd, 64, d["pos0"], L, O.default_threads(), 1e7, 1.0,
+    a = O.GqaPrefillArgs(B, T, n_q, n_kv, hd, rope_dim, d["pos0"], L, O.default_threads(), 1e7, 1.0,
                          f["q"].ctypes.data, f["gate"].ctypes.data, f["k"].ctypes.data, f["v"].ctypes.data,
                          qw.ctypes.data, kw.ctypes.data, kc.ctypes.data, vc.ctypes.data, out.ctypes.data,
                          int(no_gate))
@@ -200,6 +200,21 @@ def test_gqa_prefill_shapes(ctx, B, T, pos0, L, inter):
         prior = tuple(W.bf16_to_f32(W.bf16_bits(W.normal(r, (B, pos0, 4, 256)))) for _ in range(2))
     out = run_gqa_prefill(ctx, d, L, prior, inter)
     ref, _ = oracle_gqa_prefill(d, L, prior)
+    check_bf16(out, ref, "out")
+
+
+@pytest.mark.parametrize("rope_dim", [0, 128])
+def test_gqa_prefill_rope_dims(ctx, rope_dim):
+    """rope_dim 0 (no rotation) and 128 (RoPE pairs 64 dims apart) over an
+    unaligned earlier context."""
+    from vx27_amd import workloads as W
+    B, T, pos0, L = 2, 150, 21, 192
+    d = W.gqa_prefill(B=B, T=T, pos0=pos0, config=61)
+    r = W.rng(62, "gqa_prefill_prior")
+    prior = tuple(W.bf16_to_f32(W.bf16_bits(W.normal(r, (B, pos0, 4, 256)))) for _ in range(2))
+    say(f"gqa_prefill: B={B} T={T} pos0={pos0} rope_dim={rope_dim}")
+    out = run_gqa_prefill(ctx, d, L, prior, rope_dim=rope_dim)
+    ref, _ = oracle_gqa_prefill(d, L, prior, rope_dim=rope_dim)
     check_bf16(out, ref, "out")
 
 

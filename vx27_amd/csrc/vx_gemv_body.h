@@ -41,8 +41,12 @@ struct WkRows {
     }
 };
 
-// Epilogue interface: void operator()(int row0, int rows, const WkRows<RB> &, int tid) const,
-// called by all 1024 threads (rows = valid rows from row0, <= 16 RB).
+// Epilogue interface, both called by all 1024 threads (rows = valid rows
+// from row0, <= 16 RB):
+//   Pre prefetch(int row0, int rows, int tid) const      before the K loop:
+//       issues the loads the epilogue needs besides the sums (their latency
+//       then hides under the loop instead of trailing it)
+//   void operator()(int row0, int rows, const WkRows<RB> &, int tid, const Pre &) const
 template <int RB, bool NT, class Epi>
 __device__ __forceinline__ void vx_gemv_wk_body(const uint16_t *W, int N, int K, const uint16_t *xp, int B,
                                                 const Epi &epi) {
@@ -51,6 +55,9 @@ __device__ __forceinline__ void vx_gemv_wk_body(const uint16_t *W, int N, int K,
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
     const int rb0 = blockIdx.x * RB, nb = N / 16;
     const int nks = K / 32, kg = vx_gemv_kg(K);
+    const int row0 = rb0 * 16;
+    const int rows = min(16 * RB, N - row0);
+    const auto pre = epi.prefetch(row0, rows, tid);
     vx_floatx4_t acc[RB];
 #pragma unroll
     for (int r = 0; r < RB; r++) acc[r] = (vx_floatx4_t){0.f, 0.f, 0.f, 0.f};
@@ -89,17 +96,17 @@ __device__ __forceinline__ void vx_gemv_wk_body(const uint16_t *W, int N, int K,
         for (int i = 0; i < 4; i++) ct[16 * r + 4 * g + i][m] = v[i];
     }
     __syncthreads();
-    const int row0 = rb0 * 16;
-    const int rows = min(16 * RB, N - row0);
-    epi(row0, rows, WkRows<RB>{ct, B}, tid);
+    epi(row0, rows, WkRows<RB>{ct, B}, tid, pre);
 }
 
 // Epilogue: y[b*y_stride + n] for every row n of the workgroup.
 struct WkStore {
     float *y;
     size_t y_stride;
+    struct Pre {};
+    __device__ __forceinline__ Pre prefetch(int, int, int) const { return {}; }
     template <int RB>
-    __device__ __forceinline__ void operator()(int row0, int rows, const WkRows<RB> &c, int tid) const {
+    __device__ __forceinline__ void operator()(int row0, int rows, const WkRows<RB> &c, int tid, const Pre &) const {
         for (int t = tid; t < rows * c.B; t += blockDim.x) {
             const int r = t % rows, b = t / rows;
             y[(size_t)b * y_stride + row0 + r] = c.y(r, b);

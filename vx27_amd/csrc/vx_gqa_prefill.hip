@@ -80,8 +80,12 @@ struct KvArgs {
 // 32-position block of one KV head (the V cache's block: written as whole
 // 16-byte runs, element by element only at partial blocks, so positions
 // outside [pos0, pos0+T) keep their contents).  k: wave w takes the block's
-// tokens w, w+4, ...; lane l holds dims l, l+64, l+128, l+192.
+// tokens w, w+4, ..., w+28; lane l holds dims 4l..4l+3 of each, so the two
+// halves of a RoPE pair (dims i and i+half, half = 32 or 64) sit in lanes l
+// and l ^ (half/4).  Every global load is issued before any of the work, and
+// the eight tokens' sums of squares are reduced side by side.
 constexpr int VB = VX_GQA_VBLK;
+constexpr int KV_VLD = VB * (HDG / 8) / 256;   // 16-byte v loads per thread
 __global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
     const int hk = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -89,26 +93,63 @@ __global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
     const int p0 = (a.pos0 / VB + (int)blockIdx.x) * VB;        // first position of the block
     const int lo = max(p0, a.pos0), hi = min(p0 + VB, a.pos0 + a.T);   // valid positions [lo, hi)
     const int half = a.rope_dim / 2;
-    __shared__ float cs[VB][VX_ROPE_MAXH / 2], sn[VB][VX_ROPE_MAXH / 2];   // rope_dim <= 128 here
+    __shared__ float2 csn[VB][VX_ROPE_MAXH / 2];                          // rope_dim <= 128 here
     __shared__ __attribute__((aligned(16))) uint16_t vt[VB][HDG];         // the block's v rows
-    __shared__ float row[4][HDG];
+
+    uint4 vr[KV_VLD];
+#pragma unroll
+    for (int r = 0; r < KV_VLD; r++) {
+        const int e = tid + 256 * r, j = e / (HDG / 8), c = e % (HDG / 8), pos = p0 + j;
+        if (pos >= lo && pos < hi)
+            vr[r] = *(const uint4 *)(a.v + ((size_t)b * a.T + (pos - a.pos0)) * a.kv_ts + (size_t)hk * HDG + c * 8);
+    }
+    uint2 kr[VB / 4];
+#pragma unroll
+    for (int jj = 0; jj < VB / 4; jj++) {
+        const int pos = p0 + wave + 4 * jj;
+        if (pos >= lo && pos < hi)
+            kr[jj] = *(const uint2 *)(a.k + ((size_t)b * a.T + (pos - a.pos0)) * a.kv_ts + (size_t)hk * HDG + 4 * lane);
+    }
+    float w[4];
+#pragma unroll
+    for (int e = 0; e < 4; e++) w[e] = a.k_norm_w[4 * lane + e];
+
     // cos/sin of every (position, frequency) of the block
     for (int e = tid; e < VB * half; e += 256) {
         const int j = e / half, i = e % half, pos = p0 + j;
         if (pos < lo || pos >= hi) continue;
         const float ang = ((float)pos / a.yarn) * a.rope.freq[i];
-        cs[j][i] = cosf(ang);
-        sn[j][i] = sinf(ang);
-        if (b == 0 && hk == 0) a.cs_tab[(size_t)(pos - a.pos0) * half + i] = make_float2(cs[j][i], sn[j][i]);
+        const float2 v = make_float2(cosf(ang), sinf(ang));
+        csn[j][i] = v;
+        if (b == 0 && hk == 0) a.cs_tab[(size_t)(pos - a.pos0) * half + i] = v;
     }
-    // v rows of the block's tokens into LDS (16-byte chunks)
-    for (int e = tid; e < VB * (HDG / 8); e += 256) {
-        const int j = e / (HDG / 8), c = e % (HDG / 8), pos = p0 + j;
-        if (pos < lo || pos >= hi) continue;
-        const size_t tok = (size_t)b * a.T + (pos - a.pos0);
-        *(uint4 *)&vt[j][c * 8] = *(const uint4 *)(a.v + tok * a.kv_ts + (size_t)hk * HDG + c * 8);
+#pragma unroll
+    for (int r = 0; r < KV_VLD; r++) {
+        const int e = tid + 256 * r, j = e / (HDG / 8), c = e % (HDG / 8), pos = p0 + j;
+        if (pos >= lo && pos < hi) *(uint4 *)&vt[j][c * 8] = vr[r];
     }
-    __syncthreads();
+
+    // k: rmsn (sum of squares in double) of the wave's 8 tokens
+    float x[VB / 4][4];
+    double ss[VB / 4];
+#pragma unroll
+    for (int jj = 0; jj < VB / 4; jj++) {
+        const int pos = p0 + wave + 4 * jj;
+        ss[jj] = 0.0;
+        if (pos < lo || pos >= hi) continue;   // wave-uniform
+        const uint32_t u[2] = {kr[jj].x, kr[jj].y};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            x[jj][e] = vx_bf16_to_f32((uint16_t)(u[e >> 1] >> (16 * (e & 1))));
+            ss[jj] += (double)x[jj][e] * (double)x[jj][e];
+        }
+    }
+#pragma unroll
+    for (int off = 32; off >= 1; off >>= 1)
+#pragma unroll
+        for (int jj = 0; jj < VB / 4; jj++) ss[jj] += __shfl_xor(ss[jj], off, 64);
+    __syncthreads();   // csn and vt complete
+
     // V block [256 dims][32 positions]: thread -> (dim, 8 positions)
     {
         uint16_t *vb = a.v_cache + vx_v_index(a.n_kv, a.L, b, hk, p0, 0);
@@ -127,50 +168,35 @@ __global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
             }
         }
     }
-    // k: rmsn + RoPE per token, one wave per token; the wave's 8 rows are
-    // loaded up front
-    float *rw = row[wave];
-    uint16_t kraw[VB / 4][4];
-#pragma unroll
-    for (int jj = 0; jj < VB / 4; jj++) {
-        const int pos = p0 + wave + 4 * jj;
-        if (pos < lo || pos >= hi) continue;
-        const uint16_t *src = a.k + ((size_t)b * a.T + (pos - a.pos0)) * a.kv_ts + (size_t)hk * HDG;
-#pragma unroll
-        for (int e = 0; e < 4; e++) kraw[jj][e] = src[lane + 64 * e];
-    }
+
+    // k: scale, RoPE with the partner lane's values, one 8-byte store per lane
+    const int partner = lane ^ (half / 4);
 #pragma unroll
     for (int jj = 0; jj < VB / 4; jj++) {
         const int j = wave + 4 * jj, pos = p0 + j;
         if (pos < lo || pos >= hi) continue;   // wave-uniform
-        float x[4];
-        double ss = 0.0;
+        const float sc = 1.0f / sqrtf((float)(ss[jj] / HDG) + 1e-6f);
+        float xn[4], xp[4], r[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++)
+            xn[e] = (a.flags & VX27_GQA_NORM_W) ? (x[jj][e] * sc) * w[e] : (x[jj][e] * sc) * (w[e] + 1.0f);
+#pragma unroll
+        for (int e = 0; e < 4; e++) xp[e] = __shfl(xn[e], partner, 64);
 #pragma unroll
         for (int e = 0; e < 4; e++) {
-            x[e] = vx_bf16_to_f32(kraw[jj][e]);
-            ss += (double)x[e] * (double)x[e];
+            const int i = 4 * lane + e;
+            r[e] = xn[e];
+            if (i < half) {
+                const float2 t = csn[j][i];
+                r[e] = xn[e] * t.x - xp[e] * t.y;
+            } else if (i < 2 * half) {
+                const float2 t = csn[j][i - half];
+                r[e] = xp[e] * t.y + xn[e] * t.x;
+            }
         }
-        ss = vx_wave_sum_f64(ss);
-        const float sc = 1.0f / sqrtf((float)(ss / HDG) + 1e-6f);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const float w = a.k_norm_w[lane + 64 * e];
-            x[e] = (a.flags & VX27_GQA_NORM_W) ? (x[e] * sc) * w : (x[e] * sc) * (w + 1.0f);
-            rw[lane + 64 * e] = x[e];
-        }
-        __builtin_amdgcn_wave_barrier();   // this wave's row writes before its partner reads
-        uint16_t *kc = a.k_cache + vx_k_index(a.n_kv, a.L, b, hk, pos, 0);
-#pragma unroll
-        for (int e = 0; e < 4; e++) {
-            const int i = lane + 64 * e;
-            float r = x[e];
-            if (i < half)
-                r = rw[i] * cs[j][i] - rw[i + half] * sn[j][i];
-            else if (i < 2 * half)
-                r = rw[i - half] * sn[j][i - half] + rw[i] * cs[j][i - half];
-            kc[i] = vx_f32_to_bf16(r);
-        }
-        __builtin_amdgcn_wave_barrier();   // reads of this row done before the next token's writes
+        *(uint2 *)(a.k_cache + vx_k_index(a.n_kv, a.L, b, hk, pos, 4 * lane)) =
+            make_uint2((uint32_t)vx_f32_to_bf16(r[0]) | ((uint32_t)vx_f32_to_bf16(r[1]) << 16),
+                       (uint32_t)vx_f32_to_bf16(r[2]) | ((uint32_t)vx_f32_to_bf16(r[3]) << 16));
     }
 }
 
@@ -1187,6 +1213,9 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
                    ((uintptr_t)d->q & 15) == 0,
                "vx27_hip_gqa_prefill: q must be 16-byte aligned with strides that are multiples of 8 elements");
     VX_REQUIRE(((uintptr_t)d->v_new & 15) == 0, "vx27_hip_gqa_prefill: v_new must be 16-byte aligned");
+    VX_REQUIRE(((uintptr_t)d->k_new & 7) == 0, "vx27_hip_gqa_prefill: k_new must be 8-byte aligned");
+    VX_REQUIRE((((uintptr_t)d->k_cache | (uintptr_t)d->v_cache) & 15) == 0,
+               "vx27_hip_gqa_prefill: k_cache and v_cache must be 16-byte aligned");
     const bool gated = !(d->flags & VX27_GQA_NO_GATE);
     VX_REQUIRE(!gated || ((d->gate_tok_stride == 0 || d->gate_tok_stride % 4 == 0) &&
                           (d->gate_head_stride == 0 || d->gate_head_stride % 4 == 0) && ((uintptr_t)d->gate & 7) == 0),

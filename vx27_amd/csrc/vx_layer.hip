@@ -43,33 +43,84 @@ struct DnInArgs {
 //               normalisation chain runs in the recurrence kernel, which
 //               has whole heads
 //   z rows:     copied out; a rows: decay = exp(g_log); b rows: beta
+// The conv weights (raw bits, converted after the loop so that nothing
+// waits on them) and the conv state of a q|k|v row are loaded before the
+// projection's K loop.
+constexpr int DN_MAXB = 5;
 struct DnInEpi {
     DnInArgs a;
+    struct Pre {
+        uint32_t w[4];   // bf16: 4 values in w[0..1]; f32: 4 values
+        float st[DN_MAXB][3];
+    };
+    __device__ __forceinline__ Pre prefetch(int row0, int rows, int tid) const {
+        Pre p;
+        const int n = row0 + tid;
+        if (tid < rows && n < a.C) {
+            if (a.conv_bf16) {
+                const uint2 u = *((const uint2 *)a.conv_w + n);
+                p.w[0] = u.x;
+                p.w[1] = u.y;
+            } else {
+                const uint4 u = *((const uint4 *)a.conv_w + n);
+                p.w[0] = u.x;
+                p.w[1] = u.y;
+                p.w[2] = u.z;
+                p.w[3] = u.w;
+            }
+#pragma unroll
+            for (int b = 0; b < DN_MAXB; b++)
+                if (b < a.B) {
+                    const float *sp = a.conv_state + ((size_t)b * a.C + n) * 3;
+                    p.st[b][0] = sp[0];
+                    p.st[b][1] = sp[1];
+                    p.st[b][2] = sp[2];
+                }
+        }
+        return p;
+    }
     template <int RB>
-    __device__ __forceinline__ void operator()(int row0, int rows, const WkRows<RB> &c, int tid) const {
+    __device__ __forceinline__ void operator()(int row0, int rows, const WkRows<RB> &c, int tid, const Pre &p) const {
         if (tid >= rows) return;
         const int n = row0 + tid;
-        float v[5];
-        for (int b = 0; b < a.B; b++) v[b] = c.y(tid, b);
+        float v[DN_MAXB];
+#pragma unroll
+        for (int b = 0; b < DN_MAXB; b++)
+            if (b < a.B) v[b] = c.y(tid, b);
         if (n < a.C) {                       // q, k or v channel: causal conv + SiLU
             float w[4];
-            load_conv_w(a.conv_w, a.conv_bf16, (size_t)n, w);
-            for (int b = 0; b < a.B; b++) {
-                float *sp = a.conv_state + ((size_t)b * a.C + n) * 3;
-                float st[3] = {sp[0], sp[1], sp[2]};
-                a.act[(size_t)b * a.C + n] = conv_step(st, w, v[b]);
-                sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
+            if (a.conv_bf16) {
+                w[0] = __uint_as_float(p.w[0] << 16);
+                w[1] = __uint_as_float(p.w[0] & 0xffff0000u);
+                w[2] = __uint_as_float(p.w[1] << 16);
+                w[3] = __uint_as_float(p.w[1] & 0xffff0000u);
+            } else {
+#pragma unroll
+                for (int t = 0; t < 4; t++) w[t] = __uint_as_float(p.w[t]);
             }
+#pragma unroll
+            for (int b = 0; b < DN_MAXB; b++)
+                if (b < a.B) {
+                    float *sp = a.conv_state + ((size_t)b * a.C + n) * 3;
+                    float st[3] = {p.st[b][0], p.st[b][1], p.st[b][2]};
+                    a.act[(size_t)b * a.C + n] = conv_step(st, w, v[b]);
+                    sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
+                }
         } else if (n < a.C + a.vd) {         // z
-            for (int b = 0; b < a.B; b++) a.z[(size_t)b * a.vd + (n - a.C)] = v[b];
+#pragma unroll
+            for (int b = 0; b < DN_MAXB; b++)
+                if (b < a.B) a.z[(size_t)b * a.vd + (n - a.C)] = v[b];
         } else if (n < a.C + a.vd + a.nv) {  // a -> decay = exp(g_log), vx27_deltanet.c:68,82
             const int vh = n - a.C - a.vd;
             const double eA = exp((double)a.A_log[vh]), dtb = (double)a.dt_bias[vh];
-            for (int b = 0; b < a.B; b++)
-                a.gates[(size_t)b * a.nv + vh].y = exp(-eA * softplus_d((double)v[b] + dtb));
+#pragma unroll
+            for (int b = 0; b < DN_MAXB; b++)
+                if (b < a.B) a.gates[(size_t)b * a.nv + vh].y = exp(-eA * softplus_d((double)v[b] + dtb));
         } else {                             // b -> beta = sigmoid(b), vx27_deltanet.c:67
             const int vh = n - a.C - a.vd - a.nv;
-            for (int b = 0; b < a.B; b++) a.gates[(size_t)b * a.nv + vh].x = 1.0 / (1.0 + exp(-(double)v[b]));
+#pragma unroll
+            for (int b = 0; b < DN_MAXB; b++)
+                if (b < a.B) a.gates[(size_t)b * a.nv + vh].x = 1.0 / (1.0 + exp(-(double)v[b]));
         }
     }
 };
@@ -130,6 +181,7 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
                "vx27_hip_dn_layer_decode: null pointer in descriptor");
     VX_REQUIRE(d->conv_w_dtype == VX27_F32 || d->conv_w_dtype == VX27_BF16,
                "vx27_hip_dn_layer_decode: conv_w_dtype must be VX27_F32 or VX27_BF16");
+    VX_REQUIRE(((uintptr_t)d->conv_w & 15) == 0, "vx27_hip_dn_layer_decode: conv_w must be 16-byte aligned");
     const int B = d->B, nv = d->nv, qd = d->nqk * HD, vd = nv * HD, C = 2 * qd + vd, H = d->hidden;
     const int Nin = C + vd + 2 * nv;
     const size_t pk_x = d->x_packed ? 0 : align256(vx_pack_bytes(H));
