@@ -116,3 +116,27 @@ __device__ __forceinline__ float vx_wave_sum_f32(float v) {
     for (int off = 32; off >= 1; off >>= 1) v += __shfl_xor(v, off, 64);
     return v;
 }
+// The same sum on the VALU's DPP paths, without the LDS crossbar that the
+// shuffles go through: a butterfly inside each quad, row rotations by 4 and
+// 8 (every lane of a 16-lane row then holds the row sum), the row
+// broadcasts 15 and 31 (lane 63 then holds the wave sum), and lane 63 read
+// back.  A fixed tree, so the result is the same on every call.
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double vx_dpp_f64(double x) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)u, CTRL, ROW_MASK, 0xF, false);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROW_MASK, 0xF, false);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double vx_wave_sum_f64_dpp(double v) {
+    v = v + vx_dpp_f64<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v = v + vx_dpp_f64<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v = v + vx_dpp_f64<0x124, 0xF>(v);   // row_ror:4
+    v = v + vx_dpp_f64<0x128, 0xF>(v);   // row_ror:8
+    v = v + vx_dpp_f64<0x142, 0xA>(v);   // row_bcast:15 into rows 1 and 3 (others add +0)
+    v = v + vx_dpp_f64<0x143, 0xC>(v);   // row_bcast:31 into rows 2 and 3
+    const uint64_t u = __builtin_bit_cast(uint64_t, v);
+    const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, 63);
+    const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), 63);
+    return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}

@@ -257,8 +257,10 @@ __global__ __launch_bounds__(HD / CS * R) void dn_decode_kernel(DnArgs a) {
 // all of a lane's state loads are in flight before any other work.  The
 // per-element arithmetic is the general kernel's (decay and the rank-1
 // update through double, float state); kv and o are summed in double per
-// lane over its rows, then over the 16 parts.  Wave 0 finishes the gated
-// output norm (vx27_qfwd.c:147-151) for the whole head.
+// lane over its rows, then over the 16 parts.  Wave 0 runs the q/k
+// normalisation chain for the whole head (two elements per lane, wave sums
+// on the DPP paths, no barrier) while the state loads are in flight, and
+// finishes the gated output norm (vx27_qfwd.c:147-151).
 __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int part = tid >> 5, c4 = tid & 31;
@@ -269,44 +271,51 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
     __shared__ double s_red[8][HD];           // per-wave partial kv, then o
     __shared__ double s_dl[HD];
 
-    float va = 0.0f, qa = 0.0f, ka = 0.0f;
-    if (tid < HD) {
-        if (a.fused_conv) {   // causal conv + SiLU of this head's q, k, v channels (nv == nqk: g == vh)
-            const int qd = a.nqk * HD, C = 2 * qd + a.nv * HD;
-            const size_t chq = (size_t)g * HD + tid, chk = (size_t)qd + g * HD + tid,
-                         chv = (size_t)2 * qd + (size_t)vh * HD + tid;
-            const float *x = a.x + (size_t)b * C;
-            float *cst = a.conv_state + (size_t)b * C * 3;
-            float wq[4], wk[4], wv[4], cq[3], ck[3], cv[3];
-            load_conv_w(a.conv_w, a.conv_bf16, chq, wq);
-            load_conv_w(a.conv_w, a.conv_bf16, chk, wk);
-            load_conv_w(a.conv_w, a.conv_bf16, chv, wv);
+    // wave 0 owns the head's q, k and v: elements lane and lane + 64
+    float qa[2] = {0.f, 0.f}, ka[2] = {0.f, 0.f}, va[2] = {0.f, 0.f};
+    if (wave == 0) {
 #pragma unroll
-            for (int t = 0; t < 3; t++) {
-                cq[t] = cst[chq * 3 + t];
-                ck[t] = cst[chk * 3 + t];
-                cv[t] = cst[chv * 3 + t];
-            }
-            qa = conv_step(cq, wq, x[chq]);
-            ka = conv_step(ck, wk, x[chk]);
-            va = conv_step(cv, wv, x[chv]);
+        for (int h = 0; h < 2; h++) {
+            const int i = lane + 64 * h;
+            if (a.fused_conv) {   // causal conv + SiLU of this head's q, k, v channels (nv == nqk: g == vh)
+                const int qd = a.nqk * HD, C = 2 * qd + a.nv * HD;
+                const size_t chq = (size_t)g * HD + i, chk = (size_t)qd + g * HD + i,
+                             chv = (size_t)2 * qd + (size_t)vh * HD + i;
+                const float *x = a.x + (size_t)b * C;
+                float *cst = a.conv_state + (size_t)b * C * 3;
+                float wq[4], wk[4], wv[4], cq[3], ck[3], cv[3];
+                load_conv_w(a.conv_w, a.conv_bf16, chq, wq);
+                load_conv_w(a.conv_w, a.conv_bf16, chk, wk);
+                load_conv_w(a.conv_w, a.conv_bf16, chv, wv);
 #pragma unroll
-            for (int t = 0; t < 3; t++) {
-                cst[chq * 3 + t] = cq[t];
-                cst[chk * 3 + t] = ck[t];
-                cst[chv * 3 + t] = cv[t];
+                for (int t = 0; t < 3; t++) {
+                    cq[t] = cst[chq * 3 + t];
+                    ck[t] = cst[chk * 3 + t];
+                    cv[t] = cst[chv * 3 + t];
+                }
+                qa[h] = conv_step(cq, wq, x[chq]);
+                ka[h] = conv_step(ck, wk, x[chk]);
+                va[h] = conv_step(cv, wv, x[chv]);
+#pragma unroll
+                for (int t = 0; t < 3; t++) {
+                    cst[chq * 3 + t] = cq[t];
+                    cst[chk * 3 + t] = ck[t];
+                    cst[chv * 3 + t] = cv[t];
+                }
+            } else {
+                qa[h] = a.q[(size_t)b * a.q_tok + (size_t)g * HD + i];
+                ka[h] = a.k[(size_t)b * a.k_tok + (size_t)g * HD + i];
+                va[h] = a.v[(size_t)b * a.v_tok + (size_t)vh * HD + i];
             }
-        } else {
-            qa = a.q[(size_t)b * a.q_tok + (size_t)g * HD + tid];
-            ka = a.k[(size_t)b * a.k_tok + (size_t)g * HD + tid];
-            va = a.v[(size_t)b * a.v_tok + (size_t)vh * HD + tid];
         }
     }
     const bool gate = (a.flags & VX27_DN_OUT_GATE) != 0;
     float z0 = 0.f, z1 = 0.f, w0 = 1.f, w1 = 1.f;
-    if (wave == 0 && gate) {
-        z0 = a.z[(size_t)b * a.z_tok + (size_t)vh * HD + lane];
-        z1 = a.z[(size_t)b * a.z_tok + (size_t)vh * HD + lane + 64];
+    if (wave == 0 && (gate || !(a.flags & VX_DN_QK_READY))) {
+        if (gate) {
+            z0 = a.z[(size_t)b * a.z_tok + (size_t)vh * HD + lane];
+            z1 = a.z[(size_t)b * a.z_tok + (size_t)vh * HD + lane + 64];
+        }
         if (a.norm_w) {
             w0 = a.norm_w[lane];
             w1 = a.norm_w[lane + 64];
@@ -323,58 +332,60 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
         decay = exp(-exp((double)a.A_log[vh]) * softplus_d((double)a.ga[e] + (double)a.dt_bias[vh]));
     }
     // state loads after the small ones: those return first (loads complete in
-    // order), so the q/k hand-off below overlaps the state's arrival
+    // order), so the q/k chain below overlaps the state's arrival
     float *Sg = a.S + ((size_t)b * a.nv + vh) * HD * HD + (size_t)(8 * part) * HD + 4 * c4;
     float4 S4[8];
 #pragma unroll
     for (int r = 0; r < 8; r++) S4[r] = *(const float4 *)(Sg + (size_t)r * HD);
-    if (!(a.flags & VX_DN_QK_READY)) {
+    if (wave == 0 && !(a.flags & VX_DN_QK_READY)) {
         // q/k normalisation chain (vx27_qfwd.c:119-130 per flags, then
-        // step_exact's own l2norm, vx27_deltanet.c:77-80) on lanes < 128
-        // (waves 0 and 1); sums of squares in double, wave partials added in
-        // wave order.  The barriers only order LDS (the state loads stay in
-        // flight).
-        __shared__ double s_nrm[3][2][2];
-        const float nwj = (a.norm_w && tid < HD) ? a.norm_w[tid] : 1.0f;
+        // step_exact's own l2norm, vx27_deltanet.c:77-80), all in wave 0:
+        // sums of squares in double, each lane's two elements, then the
+        // wave's DPP tree; no barriers, and the state loads stay in flight.
         const float qs = 1.0f / sqrtf((float)HD);
-        auto sum2 = [&](double &u, double &v, double (*slot)[2]) {
-            if (wave < 2) {
-                const double su = vx_wave_sum_f64(u), sv = vx_wave_sum_f64(v);
-                if (lane == 0) {
-                    slot[wave][0] = su;
-                    slot[wave][1] = sv;
-                }
-            }
-            vx_lds_barrier();
-            u = slot[0][0] + slot[1][0];
-            v = slot[0][1] + slot[1][1];
+        const float nw[2] = {w0, w1};
+        auto sums = [&](double &sq, double &sk) {
+            sq = vx_wave_sum_f64_dpp((double)qa[0] * (double)qa[0] + (double)qa[1] * (double)qa[1]);
+            sk = vx_wave_sum_f64_dpp((double)ka[0] * (double)ka[0] + (double)ka[1] * (double)ka[1]);
         };
+        double sq, sk;
         if (a.flags & VX27_DN_PRE_RMS) {       // rmsn(x)*(1+w), vx27_qfwd.c:32-39,123
-            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
-            sum2(sq, sk, s_nrm[0]);
+            sums(sq, sk);
             const float iq = 1.0f / sqrtf((float)(sq / HD) + 1e-6f);
             const float ik = 1.0f / sqrtf((float)(sk / HD) + 1e-6f);
-            qa = (qa * iq) * (nwj + 1.0f);
-            ka = (ka * ik) * (nwj + 1.0f);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                qa[h] = (qa[h] * iq) * (nw[h] + 1.0f);
+                ka[h] = (ka[h] * ik) * (nw[h] + 1.0f);
+            }
         }
         if (a.flags & VX27_DN_PRE_L2) {        // l2norm + q/sqrt(hd), vx27_qfwd.c:124-130
-            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
-            sum2(sq, sk, s_nrm[1]);
-            qa = qa * (1.0f / sqrtf((float)sq + 1e-6f));
-            ka = ka * (1.0f / sqrtf((float)sk + 1e-6f));
-            qa = qa * qs;
+            sums(sq, sk);
+            const float iq = 1.0f / sqrtf((float)sq + 1e-6f), ik = 1.0f / sqrtf((float)sk + 1e-6f);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                qa[h] = qa[h] * iq;
+                ka[h] = ka[h] * ik;
+                qa[h] = qa[h] * qs;
+            }
         }
         {                                       // inside step_exact, vx27_deltanet.c:77-80
-            double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
-            sum2(sq, sk, s_nrm[2]);
-            qa = (qa * (1.0f / sqrtf((float)sq + 1e-6f))) * qs;
-            ka = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+            sums(sq, sk);
+            const float iq = 1.0f / sqrtf((float)sq + 1e-6f), ik = 1.0f / sqrtf((float)sk + 1e-6f);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                qa[h] = (qa[h] * iq) * qs;
+                ka[h] = ka[h] * ik;
+            }
         }
     }
-    if (tid < HD) {   // v goes through LDS too, so its use waits on nothing late
-        s_qn[tid] = qa;
-        s_kn[tid] = ka;
-        s_v[tid] = va;
+    if (wave == 0) {   // v goes through LDS too, so its use waits on nothing late
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            s_qn[lane + 64 * h] = qa[h];
+            s_kn[lane + 64 * h] = ka[h];
+            s_v[lane + 64 * h] = va[h];
+        }
     }
     __syncthreads();
 
@@ -447,7 +458,7 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
     }
     float f0 = (float)oa, f1 = (float)ob;
     if (gate) {
-        const double so = vx_wave_sum_f64((double)f0 * (double)f0 + (double)f1 * (double)f1);
+        const double so = vx_wave_sum_f64_dpp((double)f0 * (double)f0 + (double)f1 * (double)f1);
         const float is = 1.0f / sqrtf((float)(so / HD) + 1e-6f);
         f0 = ((f0 * is) * w0) * silu_f(z0);
         f1 = ((f1 * is) * w1) * silu_f(z1);
