@@ -128,6 +128,17 @@ __device__ __forceinline__ double vx_dpp_f64(double x) {
     const uint32_t hi = (uint32_t)__builtin_amdgcn_update_dpp(0, (int)(uint32_t)(u >> 32), CTRL, ROW_MASK, 0xF, false);
     return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
+// The value of lane l ^ 32 (gfx950 v_permlane32_swap: a VALU exchange of
+// the wave's two 32-lane halves).
+__device__ __forceinline__ uint32_t vx_xor32_u32(uint32_t x) {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    return (threadIdx.x & 32) ? r[0] : r[1];
+}
+__device__ __forceinline__ double vx_xor32_f64(double x) {
+    const uint64_t u = __builtin_bit_cast(uint64_t, x);
+    const uint64_t lo = vx_xor32_u32((uint32_t)u), hi = vx_xor32_u32((uint32_t)(u >> 32));
+    return __builtin_bit_cast(double, (hi << 32) | lo);
+}
 __device__ __forceinline__ double vx_wave_sum_f64_dpp(double v) {
     v = v + vx_dpp_f64<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
     v = v + vx_dpp_f64<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]

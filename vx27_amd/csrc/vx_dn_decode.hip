@@ -407,11 +407,12 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
         for (int c = 0; c < 4; c++) {
             const float sd = (float)((double)e[c] * decay);
             e[c] = sd;
-            kv[c] = kv[c] + (double)sd * (double)kn[r];
+            // (a product of two floats is exact in double: the fused form rounds once, like mul + add)
+            kv[c] = __builtin_fma((double)sd, (double)kn[r], kv[c]);
         }
     }
 #pragma unroll
-    for (int c = 0; c < 4; c++) kv[c] = kv[c] + __shfl_xor(kv[c], 32, 64);
+    for (int c = 0; c < 4; c++) kv[c] = kv[c] + vx_xor32_f64(kv[c]);
     if (lane < 32) {
 #pragma unroll
         for (int c = 0; c < 4; c++) s_red[wave][4 * c4 + c] = kv[c];
@@ -436,13 +437,13 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
         for (int c = 0; c < 4; c++) {
             const float su = (float)((double)e[c] + (double)kn[r] * dl[c]);
             e[c] = su;
-            o[c] = o[c] + (double)su * (double)qn[r];
+            o[c] = __builtin_fma((double)su, (double)qn[r], o[c]);
         }
     }
 #pragma unroll
     for (int r = 0; r < 8; r++) *(float4 *)(Sg + (size_t)r * HD) = S4[r];
 #pragma unroll
-    for (int c = 0; c < 4; c++) o[c] = o[c] + __shfl_xor(o[c], 32, 64);
+    for (int c = 0; c < 4; c++) o[c] = o[c] + vx_xor32_f64(o[c]);
     if (lane < 32) {
 #pragma unroll
         for (int c = 0; c < 4; c++) s_red[wave][4 * c4 + c] = o[c];
