@@ -280,21 +280,25 @@ __device__ __forceinline__ void load_v(uint32_t vbuf, const char *Vt, int wave, 
 // The squares of the bf16 inputs are exact in fp32; the sum of squares is
 // fp32 per lane and double across the row's 4 lanes.  Every global load
 // (rows, norm weights, cos/sin) is issued before any of them is used: one
-// round trip.
+// round trip.  The raw rows come in as u (q_rows loads them from global
+// memory; the pipelined kernel may have staged them in LDS instead).
 constexpr int HQ_MAX = VX_ROPE_MAXH / 64;   // k-steps holding the first half of the pairs, at most
 template <int NB>
-__device__ __forceinline__ void q_prep(const AttnArgs &a, int b, int h, const int (&t)[NB], int g,
-                                       bf16x8_t (&qv)[NB][8]) {
-    const int hq = a.rope_dim / 64;
-    uint4 u[NB][8];
-    float4 w[8][2];
-    float4 cs[NB][HQ_MAX][4];
+__device__ __forceinline__ void q_rows(const AttnArgs &a, int b, int h, const int (&t)[NB], int g,
+                                       uint4 (&u)[NB][8]) {
 #pragma unroll
     for (int blk = 0; blk < NB; blk++) {
         const uint16_t *src = a.q + ((size_t)b * a.T + t[blk]) * a.q_ts + (size_t)h * a.q_hs + 8 * g;
 #pragma unroll
         for (int ks = 0; ks < 8; ks++) u[blk][ks] = *(const uint4 *)(src + 32 * ks);
     }
+}
+template <int NB>
+__device__ __forceinline__ void q_prep_rows(const AttnArgs &a, const int (&t)[NB], int g, const uint4 (&u)[NB][8],
+                                            bf16x8_t (&qv)[NB][8]) {
+    const int hq = a.rope_dim / 64;
+    float4 w[8][2];
+    float4 cs[NB][HQ_MAX][4];
 #pragma unroll
     for (int ks = 0; ks < 8; ks++) {
         w[ks][0] = *(const float4 *)(a.q_norm_w + 32 * ks + 8 * g);
@@ -367,6 +371,13 @@ __device__ __forceinline__ void q_prep(const AttnArgs &a, int b, int h, const in
             qv[blk][ks] = as_bf16x8(make_uint4(pack2(x[ks][0], x[ks][1]), pack2(x[ks][2], x[ks][3]),
                                                pack2(x[ks][4], x[ks][5]), pack2(x[ks][6], x[ks][7])));
     }
+}
+template <int NB>
+__device__ __forceinline__ void q_prep(const AttnArgs &a, int b, int h, const int (&t)[NB], int g,
+                                       bf16x8_t (&qv)[NB][8]) {
+    uint4 u[NB][8];
+    q_rows<NB>(a, b, h, t, g, u);
+    q_prep_rows<NB>(a, t, g, u, qv);
 }
 
 // grid (ceil(T/128) * n_q, B), block NW*64: NW waves of RB 16-query blocks
@@ -643,41 +654,79 @@ __global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
 #define GQP_PP_RB (8 / GQP_PP_NW)   // 16-query blocks per wave
 #endif
 constexpr int PP_NW = GQP_PP_NW, PP_RB = GQP_PP_RB, PP_QT = PP_NW * PP_RB * 16, PP_PER = 32 / PP_NW;
+#ifndef GQP_QSTAGE
+#define GQP_QSTAGE 1        // the epilogue stages the next item's query rows in LDS
+#endif
+// (a wave's 16 RB query rows fill its two V-buffer slots exactly: 4 x 32 or 8 x 16 queries)
+constexpr bool QSTAGE = GQP_QSTAGE && PP_RB * 8 == 2 * PP_PER;
 static_assert((PP_NW == 4 && (PP_RB == 2 || PP_RB == 3)) || (PP_NW == 8 && PP_RB == 1),
               "4 waves of 32 or 48 queries, or 8 of 16");
 
 __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
     constexpr int RB = PP_RB, QT = PP_QT, PER = PP_PER;
     const int n_items = a.sched ? a.sched_len : 1;
-    for (int item = 0; item < n_items; item++) {
-    int qt, h, b;
-    if (a.sched) {   // persistent: this workgroup's list (wave-uniform scalar loads)
-        const int code = a.sched[blockIdx.x * a.sched_len + item];
-        if (code < 0) break;
-        qt = code % a.n_qt;
-        h = (code / a.n_qt) % a.n_q;
-        b = code / (a.n_qt * a.n_q);
-        if (item > 0) vx_lds_barrier();   // the previous item's epilogue is done with LDS
-    } else if (a.xcd_map) {   // one item per workgroup: one KV head's query heads per XCD group, heaviest first
-        const int n_qt = gridDim.x / a.n_q, id = blockIdx.x, xcd = id & 7, slot = id >> 3;
-        const int xpk = 8 / a.n_kv, hpx = a.n_q / 8;
-        b = blockIdx.y;
-        qt = n_qt - 1 - slot / hpx;
-        h = (xcd / xpk) * (a.n_q / a.n_kv) + (xcd % xpk) * hpx + slot % hpx;
-    } else {
-        const int n_qt = gridDim.x / a.n_q;
-        b = blockIdx.y;
-        qt = n_qt - 1 - (int)blockIdx.x / a.n_q;
-        h = blockIdx.x % a.n_q;
-    }
-    const int kvh = h / (a.n_q / a.n_kv);
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int r0 = qt * QT + wave * (RB * 16);
-
     // K tile buffers, then V tile buffers, in one array (the epilogue reuses
     // all 128 KiB)
     __shared__ __attribute__((aligned(16))) char smem[4 * KBUF];
+
+    // (qt, h, b) of this workgroup's item `it`; false past the end of its list
+    auto item_of = [&](int it, int &qt, int &h, int &b) -> bool {
+        if (a.sched) {   // persistent: this workgroup's list (wave-uniform scalar loads)
+            const int code = a.sched[blockIdx.x * a.sched_len + it];
+            if (code < 0) return false;
+            qt = code % a.n_qt;
+            h = (code / a.n_qt) % a.n_q;
+            b = code / (a.n_qt * a.n_q);
+        } else if (a.xcd_map) {   // one item per workgroup: one KV head's query heads per XCD group, heaviest first
+            const int n_qt = gridDim.x / a.n_q, id = blockIdx.x, xcd = id & 7, slot = id >> 3;
+            const int xpk = 8 / a.n_kv, hpx = a.n_q / 8;
+            b = blockIdx.y;
+            qt = n_qt - 1 - slot / hpx;
+            h = (xcd / xpk) * (a.n_q / a.n_kv) + (xcd % xpk) * hpx + slot % hpx;
+        } else {
+            const int n_qt = gridDim.x / a.n_q;
+            b = blockIdx.y;
+            qt = n_qt - 1 - (int)blockIdx.x / a.n_q;
+            h = blockIdx.x % a.n_q;
+        }
+        return true;
+    };
+    // Stage this wave's 16 RB query rows of item (sqt, sh, sb) in its slots
+    // of the V buffers, by direct-to-LDS loads: rows 0 .. 8 RB - 1 in its
+    // PER KiB of V buffer 0, the rest in its PER KiB of V buffer 1 (exactly
+    // the slots its own loads of V(0) and V(1) fill later), 16-byte unit u
+    // of row q at position u ^ (q % 16) so that the reads of 16 rows at one
+    // unit fall on distinct banks.
+    auto stage_q = [&](int sqt, int sh, int sb) {
+        const int nr0 = sqt * QT + wave * (RB * 16), tf = min(nr0, a.T - 1);
+        const uint16_t *qb = vx_uniform_ptr(a.q + ((size_t)sb * a.T + tf) * a.q_ts + (size_t)sh * a.q_hs);
+        // (an opaque copy of the lane index: the per-lane offsets below are
+        // the same for every item, and hoisted out of the item loop they
+        // would hold registers through the main loop)
+        int ln = lane;
+        __asm__ volatile("" : "+v"(ln));
+        const uint32_t vb = vx_lds_addr(smem + 2 * KBUF) + wave * PER * 1024;
+#pragma unroll
+        for (int j = 0; j < RB * 8; j++) {   // rows 2j and 2j + 1
+            const int q = 2 * j + (ln >> 5), t = min(nr0 + q, a.T - 1);
+            const uint32_t off = (uint32_t)((t - tf) * a.q_ts * 2) + (uint32_t)(((ln & 31) ^ (q & 15)) << 4);
+            vx_dma16(qb, off, vb + ((2 * j) / (RB * 8)) * KBUF + ((2 * j) % (RB * 8)) * 512);
+        }
+    };
+    if (QSTAGE) {
+        int qt0, h0, b0;
+        if (item_of(0, qt0, h0, b0)) stage_q(qt0, h0, b0);
+    }
+
+    for (int item = 0; item < n_items; item++) {
+    int qt, h, b;
+    if (!item_of(item, qt, h, b)) break;
+    if (item > 0) vx_lds_barrier();   // the previous item's epilogue is done with LDS
+    const int kvh = h / (a.n_q / a.n_kv);
+    const int r0 = qt * QT + wave * (RB * 16);
+
     char (*Kl)[KBUF] = (char (*)[KBUF])smem;
     char (*Vl)[KBUF] = (char (*)[KBUF])(smem + 2 * KBUF);
 
@@ -708,19 +757,46 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
     auto dma_v = [&](int tile, int buf, int j) {
         vx_dma16(vx_uniform_ptr(Vc + (size_t)tile * KBUF), vo[j], vl0 + buf * KBUF + (wave * PER + j) * 1024);
     };
-#pragma unroll
-    for (int j = 0; j < PER; j++) dma_k(0, 0, j);
-#pragma unroll
-    for (int j = 0; j < PER; j++) dma_v(0, 0, j);
-#pragma unroll
-    for (int j = 0; j < PER; j++) dma_k(min(1, n_tiles - 1), 1, j);
-
+    // Prologue: K(0) and K(1) into LDS; the query rows (staged in this
+    // wave's V-buffer slots before the item loop or by the previous item's
+    // epilogue) read out; then V(0) into those slots, and the rows' norm and
+    // rotation, whose loads are L2 hits.
     bf16x8_t qv[RB][8];
     {
         int tq[RB];   // rows past T repeat row T-1
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) tq[rb] = min(r0 + 16 * rb + n, a.T - 1);
-        q_prep<RB>(a, b, h, tq, g, qv);
+        uint4 u[RB][8];
+        if (QSTAGE) {
+#pragma unroll
+            for (int j = 0; j < PER; j++) dma_k(0, 0, j);
+#pragma unroll
+            for (int j = 0; j < PER; j++) dma_k(min(1, n_tiles - 1), 1, j);
+            // the staging loads and everything issued before K(0) have landed
+            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PER) : "memory");
+            int ln = lane;   // (opaque, as in stage_q)
+            __asm__ volatile("" : "+v"(ln));
+            const int gg = ln >> 4, nn = ln & 15;
+#pragma unroll
+            for (int rb = 0; rb < RB; rb++) {
+                const int q = 16 * rb + nn;
+                const char *rp = smem + (2 + q / (RB * 8)) * KBUF + wave * PER * 1024 + (q % (RB * 8)) * 512;
+#pragma unroll
+                for (int ks = 0; ks < 8; ks++) u[rb][ks] = *(const uint4 *)(rp + (((4 * ks + gg) ^ (q & 15)) << 4));
+            }
+            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read out before V(0) lands there
+#pragma unroll
+            for (int j = 0; j < PER; j++) dma_v(0, 0, j);
+        } else {
+#pragma unroll
+            for (int j = 0; j < PER; j++) dma_k(0, 0, j);
+#pragma unroll
+            for (int j = 0; j < PER; j++) dma_v(0, 0, j);
+#pragma unroll
+            for (int j = 0; j < PER; j++) dma_k(min(1, n_tiles - 1), 1, j);
+            q_rows<RB>(a, b, h, tq, g, u);
+        }
+        q_prep_rows<RB>(a, tq, g, u, qv);
     }
 
     floatx4_t O[RB][16], Ol[RB];
@@ -1042,6 +1118,12 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
                       : make_uint2(0u, 0u);
     }
     vx_lds_barrier();   // every wave is done with the tile buffers
+    // the next item's query rows go into this wave's V-buffer slots while
+    // this epilogue runs (the transposition below uses only the K buffers)
+    if (QSTAGE && item + 1 < n_items) {
+        int nqt, nh, nb;
+        if (item_of(item + 1, nqt, nh, nb)) stage_q(nqt, nh, nb);
+    }
     float *Ow = (float *)smem + wave * (16 * HDG);   // 16 rows at a time
     constexpr float L2E = 1.4426950408889634f;
 #pragma unroll
