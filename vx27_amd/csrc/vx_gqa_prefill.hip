@@ -86,6 +86,12 @@ struct KvArgs {
 // the eight tokens' sums of squares are reduced side by side.
 constexpr int VB = VX_GQA_VBLK;
 constexpr int KV_VLD = VB * (HDG / 8) / 256;   // 16-byte v loads per thread
+#ifndef GQP_KV_NT
+#define GQP_KV_NT 1         // streaming (nontemporal) stores of the new cache rows
+#endif
+constexpr bool KV_NT = GQP_KV_NT;
+typedef uint32_t u32x4_t __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2_t __attribute__((ext_vector_type(2)));
 __global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
     const int hk = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63;
@@ -160,8 +166,11 @@ __global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
                 uint16_t v8[8];
 #pragma unroll
                 for (int k = 0; k < 8; k++) v8[k] = vt[c * 8 + k][d];
-                *(uint4 *)(vb + (size_t)d * VB + c * 8) = make_uint4(v8[0] | ((uint32_t)v8[1] << 16), v8[2] | ((uint32_t)v8[3] << 16),
-                                                                     v8[4] | ((uint32_t)v8[5] << 16), v8[6] | ((uint32_t)v8[7] << 16));
+                const uint4 w = make_uint4(v8[0] | ((uint32_t)v8[1] << 16), v8[2] | ((uint32_t)v8[3] << 16),
+                                           v8[4] | ((uint32_t)v8[5] << 16), v8[6] | ((uint32_t)v8[7] << 16));
+                u32x4_t *dst = (u32x4_t *)(vb + (size_t)d * VB + c * 8);
+                const u32x4_t wv = {w.x, w.y, w.z, w.w};
+                if (KV_NT) __builtin_nontemporal_store(wv, dst); else *dst = wv;
             } else {
                 for (int k = 0; k < 8; k++)
                     if (q0 + k >= lo && q0 + k < hi) vb[(size_t)d * VB + c * 8 + k] = vt[c * 8 + k][d];
@@ -194,9 +203,11 @@ __global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
                 r[e] = xp[e] * t.y + xn[e] * t.x;
             }
         }
-        *(uint2 *)(a.k_cache + vx_k_index(a.n_kv, a.L, b, hk, pos, 4 * lane)) =
-            make_uint2((uint32_t)vx_f32_to_bf16(r[0]) | ((uint32_t)vx_f32_to_bf16(r[1]) << 16),
-                       (uint32_t)vx_f32_to_bf16(r[2]) | ((uint32_t)vx_f32_to_bf16(r[3]) << 16));
+        const uint2 kw = make_uint2((uint32_t)vx_f32_to_bf16(r[0]) | ((uint32_t)vx_f32_to_bf16(r[1]) << 16),
+                                    (uint32_t)vx_f32_to_bf16(r[2]) | ((uint32_t)vx_f32_to_bf16(r[3]) << 16));
+        u32x2_t *kdst = (u32x2_t *)(a.k_cache + vx_k_index(a.n_kv, a.L, b, hk, pos, 4 * lane));
+        const u32x2_t kv2 = {kw.x, kw.y};
+        if (KV_NT) __builtin_nontemporal_store(kv2, kdst); else *kdst = kv2;
     }
 }
 
