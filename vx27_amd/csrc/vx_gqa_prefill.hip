@@ -670,6 +670,10 @@ constexpr int PP_NW = GQP_PP_NW, PP_RB = GQP_PP_RB, PP_QT = PP_NW * PP_RB * 16, 
 #endif
 // (a wave's 16 RB query rows fill its two V-buffer slots exactly: 4 x 32 or 8 x 16 queries)
 constexpr bool QSTAGE = GQP_QSTAGE && PP_RB * 8 == 2 * PP_PER;
+#ifndef GQP_OUT_NT
+#define GQP_OUT_NT 1        // streaming (nontemporal) stores of the attention output
+#endif
+constexpr bool OUT_NT = GQP_OUT_NT;
 static_assert((PP_NW == 4 && (PP_RB == 2 || PP_RB == 3)) || (PP_NW == 8 && PP_RB == 1),
               "4 waves of 32 or 48 queries, or 8 of 16");
 
@@ -1159,7 +1163,11 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
                 r.z = o.z * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g2 * L2E));
                 r.w = o.w * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(-g3 * L2E));
             }
-            if (t < a.T) *(float4 *)(a.out + (((size_t)b * a.T + t) * a.n_q + h) * HDG + 4 * lane) = r;
+            if (t < a.T) {
+                floatx4_t *dst = (floatx4_t *)(a.out + (((size_t)b * a.T + t) * a.n_q + h) * HDG + 4 * lane);
+                const floatx4_t rv = {r.x, r.y, r.z, r.w};
+                if (OUT_NT) __builtin_nontemporal_store(rv, dst); else *dst = rv;
+            }
         }
         __builtin_amdgcn_wave_barrier();   // this pass's reads before the next pass's writes
     }
