@@ -261,6 +261,12 @@ __global__ __launch_bounds__(HD / CS * R) void dn_decode_kernel(DnArgs a) {
 // normalisation chain for the whole head (two elements per lane, wave sums
 // on the DPP paths, no barrier) while the state loads are in flight, and
 // finishes the gated output norm (vx27_qfwd.c:147-151).
+#ifndef DN_STATE_NT_LD
+#define DN_STATE_NT_LD 1    // streaming loads of the state (read once per step)
+#endif
+#ifndef DN_STATE_NT_ST
+#define DN_STATE_NT_ST 1    // streaming stores of the state
+#endif
 __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
     const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
     const int part = tid >> 5, c4 = tid & 31;
@@ -336,7 +342,12 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
     float *Sg = a.S + ((size_t)b * a.nv + vh) * HD * HD + (size_t)(8 * part) * HD + 4 * c4;
     float4 S4[8];
 #pragma unroll
-    for (int r = 0; r < 8; r++) S4[r] = *(const float4 *)(Sg + (size_t)r * HD);
+    for (int r = 0; r < 8; r++) {
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        const f4v *sp = (const f4v *)(Sg + (size_t)r * HD);
+        const f4v v = DN_STATE_NT_LD ? __builtin_nontemporal_load(sp) : *sp;
+        S4[r] = make_float4(v.x, v.y, v.z, v.w);
+    }
     if (wave == 0 && !(a.flags & VX_DN_QK_READY)) {
         // q/k normalisation chain (vx27_qfwd.c:119-130 per flags, then
         // step_exact's own l2norm, vx27_deltanet.c:77-80), all in wave 0:
@@ -441,7 +452,12 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
         }
     }
 #pragma unroll
-    for (int r = 0; r < 8; r++) *(float4 *)(Sg + (size_t)r * HD) = S4[r];
+    for (int r = 0; r < 8; r++) {
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        f4v *sp = (f4v *)(Sg + (size_t)r * HD);
+        const f4v v = {S4[r].x, S4[r].y, S4[r].z, S4[r].w};
+        if (DN_STATE_NT_ST) __builtin_nontemporal_store(v, sp); else *sp = v;
+    }
 #pragma unroll
     for (int c = 0; c < 4; c++) o[c] = o[c] + vx_xor32_f64(o[c]);
     if (lane < 32) {
