@@ -128,6 +128,9 @@ __global__ __launch_bounds__(256) void gemv_reduce_store(const float *part, int 
 
 }  // namespace
 
+#ifndef VX_GEMV_NT_MIB
+#define VX_GEMV_NT_MIB 32   // matrices of at least this many MiB are read with streaming loads
+#endif
 WkPlan vx_gemv_wk_plan(int N, int K, int n_cu) {
     const int nb = N / 16;
     WkPlan p;
@@ -138,8 +141,9 @@ WkPlan vx_gemv_wk_plan(int N, int K, int n_cu) {
             break;
         }
     p.grid = (nb + p.rb - 1) / p.rb;
-    // streaming loads pay off on the large matrices and cost on small ones
-    p.nt = (size_t)N * K * 2 >= ((size_t)96 << 20);
+    // streaming loads pay off on matrices read once between other traffic
+    // (every projection of a decode step); small ones may stay cached
+    p.nt = (size_t)N * K * 2 >= ((size_t)VX_GEMV_NT_MIB << 20);
     return p;
 }
 
