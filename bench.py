@@ -51,7 +51,7 @@ HBM_PEAK = 8.0e12           # bytes/s, MI355X
 # HBM bytes per gqa_split launch at batch 4, context 131072: FETCH_SIZE (x2, the
 # factor a plain copy kernel of known size gives) + WRITE_SIZE, rocprofv3 --pmc
 # runs of this script, summarised in profiles/c5_decode_step_pmc.txt
-GQA_SPLIT_TRAFFIC_B4_L131072 = 2.1834e9
+GQA_SPLIT_TRAFFIC_B4_L131072 = 2.1851e9
 METRIC = "mixer µs/token decode (B=1..64) + % HBM roofline; prefill tok/s + MFMA util"
 
 
