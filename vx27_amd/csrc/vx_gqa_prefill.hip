@@ -668,8 +668,10 @@ constexpr int PP_NW = GQP_PP_NW, PP_RB = GQP_PP_RB, PP_QT = PP_NW * PP_RB * 16, 
 #ifndef GQP_QSTAGE
 #define GQP_QSTAGE 1        // the epilogue stages the next item's query rows in LDS
 #endif
-// (a wave's 16 RB query rows fill its two V-buffer slots exactly: 4 x 32 or 8 x 16 queries)
-constexpr bool QSTAGE = GQP_QSTAGE && PP_RB * 8 == 2 * PP_PER;
+// (a wave's 16 RB query rows fill its two V-buffer slots exactly, and the
+// epilogue's transposition, 16 KiB per wave, stays in the K buffers: 4 x 32
+// queries; with 8 waves it covers the V buffers too)
+constexpr bool QSTAGE = GQP_QSTAGE && PP_RB * 8 == 2 * PP_PER && PP_NW * 16 * HDG * 4 <= 2 * (int)KBUF;
 #ifndef GQP_OUT_NT
 #define GQP_OUT_NT 1        // streaming (nontemporal) stores of the attention output
 #endif
