@@ -142,7 +142,7 @@ __device__ __forceinline__ bf16x8_t load_bf16x8(const uint16_t *p) {
 #define VX_SPLIT_WAVES 2048  // target split waves per launch
 #endif
 #ifndef VX_SPLIT_MINT
-#define VX_SPLIT_MINT 4      // at least this many key tiles per split wave
+#define VX_SPLIT_MINT 2      // at least this many key tiles per split wave
 #endif
 __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(VX_SPLIT_WPE))) void gqa_split(SplitArgs a) {
     const int split = blockIdx.x, kvh = blockIdx.y, b = blockIdx.z;
