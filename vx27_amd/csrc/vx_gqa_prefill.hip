@@ -11,13 +11,17 @@
 //
 // Kernels per call:
 //   gqp_kv       one workgroup per 32-position V block of one KV head: rmsn +
-//                RoPE of k; k,v rounded to bf16 and stored at positions
-//                pos0..pos0+T-1 of the cache; the (cos, sin) table of the
-//                new positions for the query prologue.
-//   gqp_attn_pp  one workgroup per (128-query tile, Q head, sequence),
-//                heaviest tiles first; 4 waves of 32 queries (one wave per
-//                SIMD).  Each wave normalises, rotates and scales its 32
-//                query rows into MFMA operand registers (the B operand layout
+//                RoPE of k; k,v rounded to bf16 and stored (streaming) at
+//                positions pos0..pos0+T-1 of the cache; the (cos, sin) table
+//                of the new positions for the query prologue.
+//   gqp_attn_pp  items of (128-query tile, Q head, sequence): one
+//                workgroup per CU walking a balanced per-XCD list built on
+//                the host (or, inside a stream capture for a shape not yet
+//                scheduled, one workgroup per item, heaviest first); 4 waves
+//                of 32 queries (one wave per SIMD).  Each wave's query rows
+//                of an item are staged in LDS by direct-to-LDS loads while
+//                the previous item's epilogue runs; the wave normalises,
+//                rotates and scales them into MFMA operand registers (the B operand layout
 //                puts both halves of a RoPE pair in one lane when rope_dim is
 //                a multiple of 64).  64-key K and V tiles arrive in LDS by
 //                direct-to-LDS loads.  Per tile: S^T[key][q] = K . Q^T
