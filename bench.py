@@ -60,87 +60,9 @@ def log(*a):
 
 
 # ------------------------------------------------- full 64-mixer decode step
-class MixerStack:
-    """48 Gated DeltaNet + 16 gated GQA mixers (every 4th layer attention,
-    vx27_config.h:10-12), B sequences at context Lctx, random-init bf16
-    weights (std 0.02) and states filled on the device."""
-
-    def __init__(self, ctx, B=4, Lctx=131072, extra_pos=64, n_layers=64, nqk=16, nv=48, seed=5):
-        from vx27_amd import lib as L, workloads as W
-        self.ctx, self.B, self.Lctx, self.nv, self.nqk = ctx, B, Lctx, nv, nqk
-        H, hd, gq = 5120, 128, 256
-        self.H = H
-        qd, vd = nqk * hd, nv * hd
-        C_ = 2 * qd + vd
-        self.Lcap = (Lctx + extra_pos + 63) // 64 * 64
-        r = W.rng(5, "mixer_stack")
-        s = seed * 1000
-        fill = ctx.fill_normal
-        self.x = ctx.buf(B * H * 4)
-        self.xp = ctx.buf(L.lib().vx27_hip_pack_bytes(H))
-        self.out = ctx.buf(n_layers * B * H * 4)
-        self.pos = ctx.put(np.full(B, Lctx, np.int32))
-        self.layers = []
-        self.kv_bytes = self.w_bytes = self.s_bytes = 0
-        tmp = ctx.buf((C_ + vd + 2 * nv) * H * 2)      # row-major staging for weight tiling
-        lib = L.lib()
-
-        def weight(N, K, seed):
-            """bf16 ~N(0, 0.02) [N][K] generated row-major, stored tiled."""
-            fill(tmp, N * K, seed, 0.02, bf16=True)
-            wt = ctx.buf(N * K * 2)
-            L.check(lib.vx27_hip_pack_weights_bf16(ctx.h, tmp.ptr, N, K, wt.ptr), "pack_weights")
-            return wt
-        for li in range(n_layers):
-            full = (li + 1) % 4 == 0
-            s += 10
-            if full:
-                wq = weight(24 * 2 * gq + 2 * 4 * gq, H, s + 1)
-                wo = weight(H, 24 * gq, s + 2)
-                qn = ctx.put(W.normal(r, gq, 0.1)); kn = ctx.put(W.normal(r, gq, 0.1))
-                n = B * 4 * self.Lcap * gq
-                kc = ctx.buf(n * 2); fill(kc, n, s + 3, 1.0, bf16=True)
-                vc = ctx.buf(n * 2); fill(vc, n, s + 4, 1.0, bf16=True)
-                d = L.GqaLayerDesc(B, 24, 4, gq, H, 64, 1e7, 1.0, self.Lcap, self.x.ptr, self.xp.ptr,
-                                   wq.ptr, wo.ptr, qn.ptr, kn.ptr, self.pos.ptr, kc.ptr, vc.ptr,
-                                   self.out.ptr + li * B * H * 4, 0)
-                self.layers.append(("gqa", d))
-                self.w_bytes += wq.nbytes + wo.nbytes
-            else:
-                wi = weight(C_ + vd + 2 * nv, H, s + 1)
-                wo = weight(H, vd, s + 2)
-                cw = ctx.buf(C_ * 4 * 2); fill(cw, C_ * 4, s + 3, 0.2, bf16=True)
-                A_log = ctx.put(r.uniform(-2, 1, nv).astype(np.float32))
-                dtb = ctx.put(W.normal(r, nv, 0.1))
-                nw = ctx.put(W.normal(r, hd, 0.1, 1.0))
-                S = ctx.buf(B * nv * hd * hd * 4); fill(S, B * nv * hd * hd, s + 4, 0.02)
-                cs = ctx.buf(B * C_ * 3 * 4); fill(cs, B * C_ * 3, s + 5, 0.5)
-                d = L.DnLayerDesc(B, nqk, nv, hd, H, self.x.ptr, self.xp.ptr, wi.ptr, wo.ptr, cw.ptr, L.BF16,
-                                  A_log.ptr, dtb.ptr, nw.ptr, S.ptr, cs.ptr, self.out.ptr + li * B * H * 4)
-                self.layers.append(("dn", d))
-                self.w_bytes += wi.nbytes + wo.nbytes
-                self.s_bytes += 2 * S.nbytes + 2 * cs.nbytes
-        ctx.sync()
-        tmp.free()
-
-    def step(self):
-        from vx27_amd import lib as L
-        lib = L.lib()
-        L.check(lib.vx27_hip_pack_x(self.ctx.h, self.x.ptr, self.B, self.H, self.xp.ptr), "pack_x")
-        for kind, d in self.layers:
-            fn = lib.vx27_hip_gqa_layer_decode if kind == "gqa" else lib.vx27_hip_dn_layer_decode
-            L.check(fn(self.ctx.h, C.byref(d)), kind)
-        L.check(lib.vx27_hip_advance_pos(self.ctx.h, self.pos.ptr, self.B), "advance_pos")
-
-    def alg_bytes(self, pos):
-        """Algorithmic HBM bytes of one step at key count pos+1: KV of every
-        attended position, all weights, DeltaNet state and conv state r+w."""
-        kv = 16 * self.B * 4 * (pos + 1) * 256 * 2 * 2
-        return kv + self.w_bytes + self.s_bytes
-
-
 def bench_c5(ctx, steps, warmup, B=4, Lctx=131072, cpu=True):
-    from vx27_amd import lib as L, workloads as W
+    from vx27_amd import lib as L
+    from vx27_amd.stack import MixerStack
     t0 = time.perf_counter()
     st = MixerStack(ctx, B=B, Lctx=Lctx, extra_pos=steps + warmup + 8)
     log(f"  c5: setup {time.perf_counter() - t0:.1f}s, weights {st.w_bytes / 1e9:.2f} GB, "

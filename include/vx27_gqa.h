@@ -23,7 +23,8 @@ void vx27_rmsnorm(const float *x, const float *w, float *y, int n, float eps);
 /* Single-query attention of one layer (vx27_gqa.c:17-45): q [24*256],
  * caches [n_pos][4][256] fp32, out [24*256], scale 1/16, float dot products.
  * The reference's 1024-position cap and static scratch are lifted here: any
- * n_pos >= 1, and the call is reentrant per context. */
+ * n_pos >= 1, and the function is thread-safe (the library serialises
+ * concurrent drop-in calls on its default context). */
 void vx27_attn_1q(const float *q, const float *kcache, const float *vcache, int n_pos,
                   float *out);
 

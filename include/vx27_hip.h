@@ -36,6 +36,10 @@ typedef struct vx27_hip_ctx vx27_hip_ctx;
  * init convention (int status + caller message buffer, vx27_gpu_reg.h:9). */
 int vx27_hip_open(vx27_hip_ctx **ctx, int device, char *err, size_t errlen);
 void vx27_hip_close(vx27_hip_ctx *ctx);
+/* Waits for the context stream.  Also returns -1 if a GQA decode call since
+ * the last sync was given a position outside its KV cache (pos < 0 or
+ * pos >= L: the kernels clamp it so no access leaves the cache, and flag it
+ * for this call to report; that call's outputs are undefined). */
 int vx27_hip_sync(vx27_hip_ctx *ctx);
 /* Use a caller stream (hipStream_t) for subsequent calls; NULL restores the
  * context's own stream. */
@@ -312,8 +316,17 @@ int vx27_hip_advance_pos(vx27_hip_ctx *ctx, int *pos, int B);
 
 /* --------------------------------------------------------- HIP graphs
  * Capture the calls made on ctx between graph_begin and graph_end into an
- * executable graph; graph_launch replays it on the context stream.  Calls
- * that would grow the context scratch must have run once before capture. */
+ * executable graph; graph_launch replays it on the context stream.
+ *   - A call that needs more context scratch than the context holds fails
+ *     inside a capture (-1): run the same call once before capturing.
+ *   - A captured graph keeps the addresses of the scratch buffer and the
+ *     prefill schedules it was captured with.  While any graph captured on
+ *     a context is alive, the context frees none of them: a later call that
+ *     grows the scratch, or a prefill of a new shape, leaves the graph's
+ *     memory in place until graph_destroy of the last live graph (or
+ *     vx27_hip_close).  So eager calls of any size may run between replays.
+ *   - The graph and the eager calls share that scratch: replays and eager
+ *     calls must be ordered on one stream (the context's), never overlapped. */
 int vx27_hip_graph_begin(vx27_hip_ctx *ctx);
 int vx27_hip_graph_end(vx27_hip_ctx *ctx, void **graph_exec);
 int vx27_hip_graph_launch(vx27_hip_ctx *ctx, void *graph_exec);
@@ -350,7 +363,8 @@ int vx27_hip_conv1d_step(vx27_hip_ctx *ctx, float *state, const float *x, const 
                          float *y, int C, int apply_silu);               /* vx27_deltanet.c:106-122 */
 int vx27_hip_rope_apply(vx27_hip_ctx *ctx, float *v, int n_heads, int head_dim, int rope_dim,
                         const float *cosv, const float *sinv);           /* vx27_rope.c:18-29 */
-/* vx27_attn_1q (vx27_gqa.c:17-45) without its 1024-position cap, reentrant. */
+/* vx27_attn_1q (vx27_gqa.c:17-45) without its 1024-position cap; its scratch
+ * is the context's, so concurrent calls need distinct contexts. */
 int vx27_hip_attn_1q(vx27_hip_ctx *ctx, const float *q, const float *kcache,
                      const float *vcache, int n_pos, float *out);
 /* Context-owned device staging buffer of at least `bytes` for host-pointer

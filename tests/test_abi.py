@@ -60,6 +60,12 @@ def test_scalar_dropins_match_reference_golden():
     for i, p in enumerate(r["pos"]):
         c, s = M.rope_cos_sin(int(p))
         assert np.array_equal(c, r["cos"][i]) and np.array_equal(s, r["sin"][i])
+    # the product's vx27_mrope_cos_sin_text (vx27_rope.c:31-33) and the YaRN factor
+    c = np.empty(32, np.float32); s = np.empty(32, np.float32)
+    so.vx27_mrope_cos_sin_text(8192, c.ctypes.data, s.ctypes.data)
+    assert np.array_equal(c, r["mrope_cos"]) and np.array_equal(s, r["mrope_sin"])
+    c, s = M.rope_cos_sin(32, yarn=4.0)
+    assert np.array_equal(c, r["yarn_cos"]) and np.array_equal(s, r["yarn_sin"])
 
 
 def test_entry_points_validate_without_device():

@@ -100,6 +100,25 @@ def test_dropin_rmsnorm_attn_rope(M):
     assert np.array_equal(v, r["vout"])
 
 
+def test_dropin_attn_1q_long(M):
+    """vx27_attn_1q past the reference's 1024-position cap (n_pos 3000)
+    against the oracle's restatement without the cap (float dots, as
+    vx27_gqa.c:30-31)."""
+    from oracle import oracle as O
+    from vx27_amd import workloads as W
+    r = W.rng(61, "attn_1q_long")
+    n_pos = 3000
+    q = W.normal(r, 24 * 256)
+    kc = W.normal(r, n_pos * 4 * 256)
+    vc = W.normal(r, n_pos * 4 * 256)
+    o = M.attn_1q(q, kc, vc, n_pos)
+    ref = np.empty(24 * 256, np.float32)
+    O.lib().orc_attn_1q(q, kc, vc, n_pos, ref)
+    e = maxabs(o, ref)
+    say(f"  attn_1q n_pos={n_pos}: max|d|={e:.3e} (max|ref|={np.abs(ref).max():.3f})")
+    assert e <= 1e-5
+
+
 def test_dropin_poison_mode(M):
     """Error path without a host fallback: an unsupported size poisons the
     outputs with NaN in poison mode."""

@@ -1,0 +1,126 @@
+"""Captured HIP graphs and the context's scratch memory.
+
+A captured graph keeps the raw addresses of the context scratch and of the
+prefill schedules it was captured with.  The context must not free them
+while the graph can still be replayed, even when a later eager call grows
+the scratch or prefills a prompt of a new shape.  Regression test: eager(A),
+capture(A), eager calls that grow the scratch and add a schedule, new
+allocations that could take the freed memory, replay(A) == eager(A) bit for
+bit; then a capture of a call whose scratch is not sized yet fails cleanly.
+"""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from gpu_common import say
+
+pytestmark = pytest.mark.gpu
+
+
+def test_graph_survives_scratch_growth():
+    from vx27_amd import lib as L, mixers as M, workloads as W
+    lib = L.lib()
+    with L.Ctx(0) as ctx:
+        # A: a gated GQA decode step of 2 sequences (scratch: q, split partials)
+        d = W.gqa_decode(B=2, L=300, config=41)
+        Lcap = 320
+        lay = M.GatedGQALayer(ctx, 2, Lcap, d["q_norm_w"], d["k_norm_w"])
+        for b in range(2):
+            lay.write_kv(b, 0, W.bf16_to_f32(d["K"][b]), W.bf16_to_f32(d["V"][b]))
+        hd, n_q = 256, 24
+        qb, kb, vb = ctx.put(d["qg"]), ctx.put(d["k_new"]), ctx.put(d["v_new"])
+        pb, ob = ctx.put(d["pos"]), ctx.buf(2 * n_q * hd * 4)
+        desc = lay.desc(pb.ptr, qb.ptr, (n_q * 2 * hd, 2 * hd), qb.ptr + hd * 4, (n_q * 2 * hd, 2 * hd),
+                        kb.ptr, vb.ptr, ob.ptr)
+
+        def run_a():
+            L.check(lib.vx27_hip_gqa_decode(ctx.h, C.byref(desc)), "gqa_decode")
+
+        run_a()
+        eager = ob.download((2, n_q, hd), np.float32)
+        ctx.graph_begin()
+        run_a()
+        g = ctx.graph_end()
+        say("  captured A")
+        # B: a 2048-token DeltaNet prefill (tens of MB of chunk records: the
+        # scratch grows) and a GQA prefill of a shape not seen (a new schedule)
+        dp = W.dn_prefill(B=1, T=2048, config=42)
+        bufs = {k: ctx.put(dp[k]) for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "S0")}
+        po = ctx.buf(2048 * 16 * 128 * 4)
+        pd = L.DnPrefillDesc(1, 2048, 16, 16, 128, 0, bufs["S0"].ptr, bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr,
+                             bufs["a"].ptr, bufs["b"].ptr, bufs["A_log"].ptr, bufs["dt_bias"].ptr, po.ptr)
+        L.check(lib.vx27_hip_dn_prefill(ctx.h, C.byref(pd)), "dn_prefill")
+        gp = W.gqa_prefill(B=1, T=200, config=43)
+        gb = {k: ctx.put(gp[k]) for k in ("q", "gate", "k", "v", "q_norm_w", "k_norm_w")}
+        kc, vc, go = ctx.buf(4 * 256 * 256 * 2), ctx.buf(4 * 256 * 256 * 2), ctx.buf(200 * 24 * 256 * 4)
+        gd = L.GqaPrefillDesc(1, 200, 24, 4, 256, 64, 1e7, 1.0, 256, 0, 0, gb["q"].ptr, 0, 0, gb["gate"].ptr, 0, 0,
+                              gb["k"].ptr, gb["v"].ptr, gb["q_norm_w"].ptr, gb["k_norm_w"].ptr, kc.ptr, vc.ptr,
+                              go.ptr)
+        L.check(lib.vx27_hip_gqa_prefill(ctx.h, C.byref(gd)), "gqa_prefill")
+        ctx.sync()
+        say("  eager B calls done (scratch grown, new schedule)")
+        # new allocations that would take freed memory, filled with garbage
+        junk = [ctx.buf(1 << 20) for _ in range(8)]
+        for j, bj in enumerate(junk):
+            ctx.fill_normal(bj, (1 << 20) // 4, 900 + j, 1e30)
+        ob.zero()
+        try:
+            for rep in range(3):
+                ctx.graph_launch(g)
+                ctx.sync()
+                got = ob.download((2, n_q, hd), np.float32)
+                say(f"  replay {rep}: equal to eager = {np.array_equal(got, eager)}")
+                assert np.array_equal(got, eager), rep
+                run_a()                       # eager A between replays, same answer
+                ctx.sync()
+                assert np.array_equal(ob.download((2, n_q, hd), np.float32), eager)
+        finally:
+            L.check(lib.vx27_hip_graph_destroy(g), "graph_destroy")
+        # after the last graph is gone the retired memory is released; calls still work
+        L.check(lib.vx27_hip_dn_prefill(ctx.h, C.byref(pd)), "dn_prefill")
+        run_a()
+        ctx.sync()
+        assert np.array_equal(ob.download((2, n_q, hd), np.float32), eager)
+
+
+def test_capture_needing_scratch_fails_cleanly():
+    """Inside a capture, a call whose scratch is not yet sized returns -1
+    with a message (no allocation in the capture); the capture still ends."""
+    from vx27_amd import lib as L, workloads as W
+    lib = L.lib()
+    with L.Ctx(0) as ctx:
+        dp = W.dn_prefill(B=1, T=512, config=44)
+        bufs = {k: ctx.put(dp[k]) for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "S0")}
+        po = ctx.buf(512 * 16 * 128 * 4)
+        pd = L.DnPrefillDesc(1, 512, 16, 16, 128, 0, bufs["S0"].ptr, bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr,
+                             bufs["a"].ptr, bufs["b"].ptr, bufs["A_log"].ptr, bufs["dt_bias"].ptr, po.ptr)
+        pos = ctx.put(np.zeros(4, np.int32))
+        ctx.graph_begin()
+        L.check(lib.vx27_hip_advance_pos(ctx.h, pos.ptr, 4), "advance_pos")   # one node in the graph
+        rc = lib.vx27_hip_dn_prefill(ctx.h, C.byref(pd))
+        msg = lib.vx27_hip_last_error().decode()
+        g = ctx.graph_end()
+        L.check(lib.vx27_hip_graph_destroy(g), "graph_destroy")
+        say(f"  rc={rc}: {msg}")
+        assert rc == -1 and "before capturing" in msg
+        # the same call outside a capture sizes the scratch and runs
+        L.check(lib.vx27_hip_dn_prefill(ctx.h, C.byref(pd)), "dn_prefill")
+        ctx.sync()
+
+
+def test_sync_reports_position_outside_cache():
+    """A decode position past the cache is clamped on the device (no access
+    leaves the cache) and reported by the next vx27_hip_sync."""
+    from vx27_amd import lib as L, mixers as M, workloads as W
+    lib = L.lib()
+    with L.Ctx(0) as ctx:
+        d = W.gqa_decode(B=1, L=60, config=45)
+        lay = M.GatedGQALayer(ctx, 1, 64, d["q_norm_w"], d["k_norm_w"])
+        lay.decode(np.array([63], np.int32), d["qg"], d["k_new"], d["v_new"])
+        ctx.sync()                                    # in range: no report
+        lay.decode(np.array([64], np.int32), d["qg"], d["k_new"], d["v_new"])
+        with pytest.raises(L.HipError, match="outside its KV cache"):
+            ctx.sync()
+        # the flag is cleared by the report
+        L.check(lib.vx27_hip_sync(ctx.h), "sync")

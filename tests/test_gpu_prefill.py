@@ -322,3 +322,25 @@ def test_prefill_deterministic(ctx):
     o1, S1 = run_dn_prefill(ctx, e)
     o2, S2 = run_dn_prefill(ctx, e)
     assert np.array_equal(o1, o2) and np.array_equal(S1, S2), "dn prefill differs between identical calls"
+
+
+def test_gqa_prefill_norm_w(ctx):
+    """VX27_GQA_NORM_W: q/k norm as x*s*w (vx27_gqa.c:10-15's form).  The
+    oracle runs the (1+w) form with w - 1: for w in [0.5, 2] the difference
+    is exact (Sterbenz) and (w - 1) + 1 == w, so both forms multiply by the
+    same float."""
+    from vx27_amd import lib as L_, workloads as W
+    B, T, pos0, L = 1, 300, 0, 320
+    d = W.gqa_prefill(B=B, T=T, pos0=pos0, config=60)
+    r = W.rng(60, "norm_w")
+    w_q = np.clip(W.normal(r, 256, 0.1, 1.0), 0.5, 2.0).astype(np.float32)
+    w_k = np.clip(W.normal(r, 256, 0.1, 1.0), 0.5, 2.0).astype(np.float32)
+    dev = dict(d, q_norm_w=w_q, k_norm_w=w_k)
+    orc = dict(d, q_norm_w=(w_q - np.float32(1)).astype(np.float32), k_norm_w=(w_k - np.float32(1)).astype(np.float32))
+    assert np.array_equal(orc["q_norm_w"] + np.float32(1), w_q)
+    out = run_gqa_prefill(ctx, dev, L, None, flags=L_.GQA_NORM_W)
+    ref, _ = oracle_gqa_prefill(orc, L)
+    check_bf16(out, ref, "norm_w prefill")
+    # the flag changes the answer (the (1+w) form with the same w differs)
+    alt, _ = oracle_gqa_prefill(dev, L)
+    assert np.abs(alt - ref).max() > 1e-2

@@ -4,6 +4,8 @@
 #include <stdint.h>
 #include <stdio.h>
 
+#include <vector>
+
 #include "vx27_hip.h"
 
 // one profiled launch: events recorded around it on the context stream
@@ -16,15 +18,26 @@ struct vx27_hip_ctx {
     int device;
     hipStream_t stream;      // stream used for every enqueue
     hipStream_t own_stream;  // created by vx27_hip_open
-    // grow-only device scratch (split-K partials, staging), owned by the context
+    // grow-only device scratch (split-K partials, prefill chunk records),
+    // owned by the context
     void *scratch;
     size_t scratch_bytes;
     // small staging for the drop-ins (host-pointer API)
     void *stage;
     size_t stage_bytes;
     int n_cu;                // compute units of the device
-    // prefill attention work schedule, cached per shape (vx_gqa_prefill.hip)
-    void *gqp_sched;
+    // prefill attention work schedules, one per shape (vx_gqa_prefill.hip)
+    std::vector<void *> gqp_scheds;
+    // Executable graphs captured on this context that are not yet destroyed.
+    // A captured graph keeps the raw addresses of the scratch buffer and of
+    // the schedules it was captured with, so while any is alive a buffer
+    // that scratch growth replaces is kept here (not freed) until the last
+    // graph is destroyed or the context is closed.
+    int live_graphs;
+    std::vector<void *> retired;
+    // device flag set by a decode kernel that saw a position outside its KV
+    // cache; read back and cleared by vx27_hip_sync
+    int *err_flag;
     // kernel profiler (vx27_hip_prof_*): off unless enabled
     int prof_on;
     vx_prof_rec *prof;
@@ -88,8 +101,13 @@ void vx_prof_end(vx27_hip_ctx *ctx, const char *name);
 int vx_ctx_enter(vx27_hip_ctx *ctx);
 // Device scratch of at least `bytes`, owned by ctx (synchronises before growing).
 int vx_ctx_scratch(vx27_hip_ctx *ctx, size_t bytes, void **out);
-// frees the cached prefill attention schedule (vx_gqa_prefill.hip)
+// frees the cached prefill attention schedules (vx_gqa_prefill.hip)
 void vx_gqp_sched_free(vx27_hip_ctx *ctx);
+// Device memory owned by the context: freed now, or (while a captured graph
+// that may reference it is alive) kept until the last such graph is gone.
+void vx_ctx_release(vx27_hip_ctx *ctx, void *dptr);
+// Nonzero while the context stream is capturing a graph.
+bool vx_ctx_capturing(vx27_hip_ctx *ctx);
 // Host-pointer staging buffer of at least `bytes` (device memory).
 int vx_ctx_stage(vx27_hip_ctx *ctx, size_t bytes, void **out);
 

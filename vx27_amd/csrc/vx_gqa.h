@@ -24,8 +24,18 @@ struct vx_rope_tab {
 };
 int vx_rope_fill(vx_rope_tab &t, int rope_dim, float theta);
 
+// cos and sin of frequency i at position pos: angle = ((float)pos / yarn) *
+// freq_i in float, then the device's float cosf/sinf (vx27_rope.c:11-14).
+// Every kernel that rotates (decode prep, prefill k/v and query prologues
+// through the prefill's table, vx27_hip_rope_table) evaluates it here.
+__device__ __forceinline__ float2 vx_rope_cs(const vx_rope_tab &t, int pos, float yarn, int i) {
+    const float ang = ((float)pos / yarn) * t.freq[i];
+    return make_float2(cosf(ang), sinf(ang));
+}
+
 size_t vx_gqa_scratch_bytes(const vx27_gqa_desc *d);
 // The decode step with caller-provided scratch of vx_gqa_scratch_bytes(d);
 // out_packed (optional) receives the gated attention as the packed operand of
 // the output projection.
 int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uint16_t *out_packed);
+

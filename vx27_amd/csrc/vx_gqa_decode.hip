@@ -73,6 +73,7 @@ struct PrepArgs {
     size_t kv_ss;   // per-sequence stride of k_new / v_new
     uint16_t *k_cache, *v_cache;
     float *q_out;   // [B][n_q][256]
+    int *err_flag;  // set to 1 when pos is outside [0, L)
     RopeTab rope;
 };
 
@@ -82,15 +83,17 @@ __global__ __launch_bounds__(256) void gqa_prep(PrepArgs a) {
     __shared__ double red[4];
     __shared__ float row[HDG];
     __shared__ float cs[MAXR], sn[MAXR];
-    // positions outside the cache are clamped so no access leaves the buffers;
-    // the host contract is 0 <= pos < L
-    const int pos = min(max(a.pos[b], 0), a.L - 1);
+    // positions outside the cache are clamped so no access leaves the
+    // buffers, and flagged for vx27_hip_sync to report (the host contract is
+    // 0 <= pos < L)
+    const int pos_in = a.pos[b];
+    const int pos = min(max(pos_in, 0), a.L - 1);
+    if (pos != pos_in && h == 0 && i == 0) *a.err_flag = 1;
     const int half = a.rope_dim / 2;
     if (i < half) {
-        const float ps = (float)pos / a.yarn;
-        const float ang = ps * a.rope.freq[i];
-        cs[i] = cosf(ang);
-        sn[i] = sinf(ang);
+        const float2 c = vx_rope_cs(a.rope, pos, a.yarn, i);
+        cs[i] = c.x;
+        sn[i] = c.y;
     }
     const bool is_q = h < a.n_q;
     const int hk = h - a.n_q;
@@ -336,10 +339,9 @@ struct RopeTabArgs {
 __global__ void rope_table_kernel(RopeTabArgs a) {
     const int r = blockIdx.x, i = threadIdx.x;
     if (i >= a.half) return;
-    const float ps = (float)a.pos[r] / a.yarn;
-    const float ang = ps * a.rope.freq[i];
-    a.cosv[(size_t)r * a.half + i] = cosf(ang);
-    a.sinv[(size_t)r * a.half + i] = sinf(ang);
+    const float2 c = vx_rope_cs(a.rope, a.pos[r], a.yarn, i);
+    a.cosv[(size_t)r * a.half + i] = c.x;
+    a.sinv[(size_t)r * a.half + i] = c.y;
 }
 
 }  // namespace
@@ -409,6 +411,7 @@ int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uin
     pa.k_new = d->k_new; pa.v_new = d->v_new; pa.q_norm_w = d->q_norm_w; pa.k_norm_w = d->k_norm_w;
     pa.kv_ss = d->kv_seq_stride ? d->kv_seq_stride : (size_t)d->n_kv * HDG;
     pa.k_cache = d->k_cache; pa.v_cache = d->v_cache; pa.q_out = q_rot; pa.rope = rt;
+    pa.err_flag = ctx->err_flag;
     VX_LAUNCH(ctx, gqa_prep, dim3(d->n_q + d->n_kv, d->B), dim3(256), pa);
 
     SplitArgs sa;

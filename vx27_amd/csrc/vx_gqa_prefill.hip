@@ -36,8 +36,6 @@
 //                MFMA pipe while the VALU does the softmax of tile kt (see
 //                the kernel's comment for the schedule and the softmax
 //                reference).
-//   gqp_attn     the earlier one-tile-at-a-time form (8 waves of 16
-//                queries, online softmax), kept as a build option (GQP_PP=0).
 #include <math.h>
 
 #include <algorithm>
@@ -54,18 +52,6 @@ typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float floatx4_t __attribute__((ext_vector_type(4)));
 
 constexpr int HDG = VX_GQA_HD;
-#ifndef GQP_NW
-#define GQP_NW 8            // waves per attention workgroup
-#endif
-#ifndef GQP_RB
-#define GQP_RB 1            // 16-query blocks per wave
-#endif
-#ifndef GQP_PP
-#define GQP_PP 1            // software-pipelined attention kernel (4 waves x 32 queries)
-#endif
-#ifndef GQP_DB
-#define GQP_DB 1            // double-buffered K/V tiles (else one buffer, two workgroups per CU)
-#endif
 constexpr int KT = 64;      // keys per tile
 
 struct KvArgs {
@@ -128,8 +114,7 @@ __global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
     for (int e = tid; e < VB * half; e += 256) {
         const int j = e / half, i = e % half, pos = p0 + j;
         if (pos < lo || pos >= hi) continue;
-        const float ang = ((float)pos / a.yarn) * a.rope.freq[i];
-        const float2 v = make_float2(cosf(ang), sinf(ang));
+        const float2 v = vx_rope_cs(a.rope, pos, a.yarn, i);
         csn[j][i] = v;
         if (b == 0 && hk == 0) a.cs_tab[(size_t)(pos - a.pos0) * half + i] = v;
     }
@@ -257,33 +242,8 @@ constexpr int TBUF = 2 * KBUF;              // bytes of one K+V tile buffer
 // Direct-to-LDS loads of one 64-key tile, K and V separately: 4 waves x 8
 // instructions of 64 lanes x 16 bytes each; every lane loads the global unit
 // that belongs at its swizzled LDS slot.
-// Loads of one 64-key tile, K and V separately: 4 waves x 8 instructions of
-// 64 lanes x 16 bytes each; every lane loads the global unit that belongs at
-// its swizzled LDS slot.  The lane offsets are recomputed at each call (the
-// empty asm hides that they are loop-invariant, so they are not held in
-// registers across the tile loop).
+// XOR swizzle of K row r's 16-byte units in the LDS tile.
 __device__ __forceinline__ int kswz(int r) { return (r & 3) | ((r >> 1) & 12); }
-
-template <int NW>
-__device__ __forceinline__ void load_k(uint32_t kbuf, const char *Kt, int wave, int lane) {
-    __asm__ volatile("" : "+v"(lane));
-    constexpr int PER = 32 / NW;   // 1 KiB chunks per wave
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int r = (wave * PER + j) * 2 + (lane >> 5), u = (lane & 31) ^ kswz(r);
-        vx_dma16(Kt, (uint32_t)(r * HDG + u * 8) * 2, kbuf + (wave * PER + j) * 1024);
-    }
-}
-template <int NW>
-__device__ __forceinline__ void load_v(uint32_t vbuf, const char *Vt, int wave, int lane) {
-    __asm__ volatile("" : "+v"(lane));
-    constexpr int PER = 32 / NW;
-#pragma unroll
-    for (int j = 0; j < PER; j++) {
-        const int d = (wave * PER + j) * 8 + (lane >> 3), w = (lane & 7) ^ ((d >> 1) & 7);
-        vx_dma16(Vt, (uint32_t)((((w >> 2) * HDG + d) * 32) + (w & 3) * 8) * 2, vbuf + (wave * PER + j) * 1024);
-    }
-}
 
 // NB 16-query blocks as the B operand of S^T = K Q^T: lane (g,n) of k-step
 // ks gets dims 32ks + 8g + 0..7 of token row t[blk] (the block's row n).
@@ -394,256 +354,6 @@ __device__ __forceinline__ void q_prep(const AttnArgs &a, int b, int h, const in
     q_rows<NB>(a, b, h, t, g, u);
     q_prep_rows<NB>(a, t, g, u, qv);
 }
-
-// grid (ceil(T/128) * n_q, B), block NW*64: NW waves of RB 16-query blocks
-template <int NW, int RB, bool DB>
-__global__ __launch_bounds__(NW * 64) void gqp_attn(AttnArgs a) {
-    constexpr int QT = NW * RB * 16;   // queries per workgroup
-    constexpr int PER = 32 / NW;   // direct-to-LDS instructions per wave for one K or V tile
-    // Workgroups go round-robin over the 8 XCDs (each with its own L2).  With
-    // xcd_map, XCD x takes the query heads of KV head x / (8 / n_kv), so an
-    // L2 holds one KV head's cache; heaviest (last) query tiles first.
-    const int n_qt = gridDim.x / a.n_q, b = blockIdx.y;
-    int qt, h;
-    if (a.xcd_map) {
-        const int id = blockIdx.x, xcd = id & 7, slot = id >> 3;
-        const int xpk = 8 / a.n_kv, hpx = a.n_q / 8;   // XCDs per KV head, Q heads per XCD
-        qt = n_qt - 1 - slot / hpx;
-        h = (xcd / xpk) * (a.n_q / a.n_kv) + (xcd % xpk) * hpx + slot % hpx;
-    } else {
-        qt = n_qt - 1 - (int)blockIdx.x / a.n_q;
-        h = blockIdx.x % a.n_q;
-    }
-    const int kvh = h / (a.n_q / a.n_kv);
-    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
-    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // scalar: LDS bases go to M0
-    const int r0 = qt * QT + wave * (RB * 16);                 // this wave's first query (token index)
-
-    // DB: two K and two V tile buffers, tile kt+1 streams into one pair while
-    // tile kt is read from the other.  Otherwise one pair (64 KiB, so two
-    // workgroups share a CU and one's softmax overlaps the other's MFMAs),
-    // refilled once every wave is done with it.
-    __shared__ __attribute__((aligned(16))) char Kl[DB ? 2 : 1][KBUF];
-    __shared__ __attribute__((aligned(16))) char Vl[DB ? 2 : 1][KBUF];
-
-    const int n_keys = a.pos0 + a.T;                           // valid cache positions
-    const int wg_last = a.pos0 + min(qt * QT + QT, a.T) - 1;   // last key any row here sees
-    const int n_tiles = wg_last / KT + 1;
-    const int wave_last = a.pos0 + min(r0 + RB * 16 - 1, a.T - 1);
-    // tile kt: K rows kt*64.. (32 KiB) and V blocks 2kt, 2kt+1 (2 x 16 KiB)
-    const char *Kc = (const char *)(a.k_cache + vx_k_index(a.n_kv, a.L, b, kvh, 0, 0));
-    const char *Vc = (const char *)(a.v_cache + vx_v_index(a.n_kv, a.L, b, kvh, 0, 0));
-    const uint32_t kl0 = vx_lds_addr(Kl[0]), vl0 = vx_lds_addr(Vl[0]);
-    load_k<NW>(kl0, Kc, wave, lane);
-    load_v<NW>(vl0, Vc, wave, lane);
-
-    // ---- this wave's queries as MFMA operands
-    bf16x8_t qv[RB][8];
-    {
-        int tq[RB];   // rows past T repeat row T-1
-#pragma unroll
-        for (int rb = 0; rb < RB; rb++) tq[rb] = min(r0 + 16 * rb + n, a.T - 1);
-        q_prep<RB>(a, b, h, tq, g, qv);
-    }
-
-    floatx4_t O[RB][16];
-#pragma unroll
-    for (int rb = 0; rb < RB; rb++)
-#pragma unroll
-        for (int db = 0; db < 16; db++) O[rb][db] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
-    float mrow[RB], lrow[RB];
-#pragma unroll
-    for (int rb = 0; rb < RB; rb++) {
-        mrow[rb] = -INFINITY;
-        lrow[rb] = 0.f;
-    }
-
-    for (int kt = 0; kt < n_tiles; kt++) {
-        const int k0 = kt * KT, cur = DB ? (kt & 1) : 0;
-        const bool more = kt + 1 < n_tiles;
-        const bool live = k0 <= wave_last;   // wave-uniform: otherwise every key here is masked
-        const char *Kt = Kl[cur], *Vt = Vl[cur];
-        // K(kt) and V(kt) landed (nothing is issued after them yet); the
-        // barrier also means every wave is done with tile kt-1, whose buffers
-        // take tile kt+1 now
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        vx_lds_barrier();
-        if (DB && more) {
-            load_k<NW>(vx_lds_addr(Kl[cur ^ 1]), Kc + (size_t)(kt + 1) * KBUF, wave, lane);
-            load_v<NW>(vx_lds_addr(Vl[cur ^ 1]), Vc + (size_t)(kt + 1) * KBUF, wave, lane);
-        }
-        floatx4_t s[4][RB];
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-            for (int rb = 0; rb < RB; rb++) s[kb][rb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
-        if (live) {
-            // the K operands of k-step ks+1 are read while the MFMAs of ks run
-            // (the scheduling barriers keep that order)
-            bf16x8_t kf[2][4];
-            auto kload = [&](int ks, bf16x8_t *dst) {
-#pragma unroll
-                for (int kb = 0; kb < 4; kb++) {
-                    const int kr = 32 * (kb >> 1) + 8 * (n >> 2) + 4 * (kb & 1) + (n & 3);   // key row of A row n
-                    const int uo = ((4 * ks + g) ^ kswz(kr)) << 4;
-                    dst[kb] = as_bf16x8(*(const uint4 *)(Kt + kr * 512 + uo));
-                }
-            };
-            kload(0, kf[0]);
-#pragma unroll
-            for (int ks = 0; ks < 8; ks++) {
-                if (ks + 1 < 8) kload(ks + 1, kf[(ks + 1) & 1]);
-                __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-                for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                    for (int rb = 0; rb < RB; rb++)
-                        s[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks & 1][kb], qv[rb][ks], s[kb][rb], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-
-        bf16x8_t pa[RB][2];
-        if (live) {
-            if (k0 + KT - 1 > a.pos0 + r0) {   // diagonal tile: causal mask
-#pragma unroll
-                for (int rb = 0; rb < RB; rb++) {
-                    const int qpos = a.pos0 + r0 + rb * 16 + n;
-#pragma unroll
-                    for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++)
-                            if (k0 + 32 * (kb >> 1) + 8 * g + 4 * (kb & 1) + i > qpos) s[kb][rb][i] = -INFINITY;
-                }
-            }
-            // Lazy rescaling: P = exp2(s - m) against a reference max m per
-            // query that only moves when the tile's max exceeds it by more
-            // than 8 (so P <= 2^8, exact enough in bf16 and fp32); O and l are
-            // rescaled only then, which after the first tiles is rare.
-            float mx[RB];
-#pragma unroll
-            for (int rb = 0; rb < RB; rb++) {
-                float m = -INFINITY;
-#pragma unroll
-                for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) m = fmaxf(m, s[kb][rb][i]);
-                m = fmaxf(m, __shfl_xor(m, 16, 64));
-                mx[rb] = fmaxf(m, __shfl_xor(m, 32, 64));
-            }
-            bool grow = false;
-#pragma unroll
-            for (int rb = 0; rb < RB; rb++) grow = grow || mx[rb] > mrow[rb] + 8.0f;
-            if (__any(grow)) {
-#pragma unroll
-                for (int rb = 0; rb < RB; rb++) {
-                    const float mnew = mx[rb] > mrow[rb] + 8.0f ? mx[rb] : mrow[rb];
-                    const float alpha = __builtin_amdgcn_exp2f(mrow[rb] - mnew);   // 0 on the first tile
-                    mrow[rb] = mnew;
-                    lrow[rb] *= alpha;
-                    float al[4];   // O rows 4g+i of this block take the factor of query 4g+i
-#pragma unroll
-                    for (int i = 0; i < 4; i++) al[i] = __shfl(alpha, 4 * g + i, 64);
-#pragma unroll
-                    for (int db = 0; db < 16; db++)
-#pragma unroll
-                        for (int i = 0; i < 4; i++) O[rb][db][i] *= al[i];
-                }
-            }
-#pragma unroll
-            for (int rb = 0; rb < RB; rb++) {
-                float sum = 0.f;
-#pragma unroll
-                for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-                    for (int i = 0; i < 4; i++) {
-                        const float pv = __builtin_amdgcn_exp2f(s[kb][rb][i] - mrow[rb]);
-                        s[kb][rb][i] = pv;
-                        sum += pv;
-                    }
-                sum += __shfl_xor(sum, 16, 64);
-                sum += __shfl_xor(sum, 32, 64);
-                lrow[rb] += sum;
-#pragma unroll
-                for (int ks = 0; ks < 2; ks++) {
-                    const uint4 u = make_uint4(pack2(s[2 * ks][rb][0], s[2 * ks][rb][1]),
-                                               pack2(s[2 * ks][rb][2], s[2 * ks][rb][3]),
-                                               pack2(s[2 * ks + 1][rb][0], s[2 * ks + 1][rb][1]),
-                                               pack2(s[2 * ks + 1][rb][2], s[2 * ks + 1][rb][3]));
-                    pa[rb][ks] = as_bf16x8(u);
-                }
-            }
-        }
-
-        if (k0 + KT > n_keys) {
-            // last tile: V of positions past the valid keys is zeroed (masked P
-            // is 0, and 0 * a stale NaN would not be)
-            uint16_t *V = (uint16_t *)Vl[cur];
-            for (int e = tid; e < HDG * KT; e += NW * 64) {
-                const int d = e >> 6, key = e & 63;
-                if (k0 + key >= n_keys) {
-                    const int u = (key >> 3) ^ ((d >> 1) & 7);
-                    V[d * KT + u * 8 + (key & 7)] = 0;
-                }
-            }
-            vx_lds_barrier();   // (workgroup-uniform: every wave takes this branch)
-        }
-        if (live) {
-            // groups of 4 dim blocks: the V operands of group j+1 are read
-            // while the MFMAs of group j run
-            const int vsw = (n >> 1) & 7;
-            bf16x8_t vf[2][4];
-            auto vload = [&](int grp, bf16x8_t *dst) {
-                const int ks = grp >> 2, db0 = (grp & 3) * 4;
-                const int uo = ((4 * ks + g) ^ vsw) << 4;   // keys 32ks + 8g .. +7
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-                    dst[j] = as_bf16x8(*(const uint4 *)(Vt + ((db0 + j) * 16 + n) * (KT * 2) + uo));
-            };
-            vload(0, vf[0]);
-#pragma unroll
-            for (int grp = 0; grp < 8; grp++) {
-                if (grp + 1 < 8) vload(grp + 1, vf[(grp + 1) & 1]);
-                __builtin_amdgcn_sched_barrier(0);
-                const int ks = grp >> 2, db0 = (grp & 3) * 4;
-#pragma unroll
-                for (int j = 0; j < 4; j++)
-#pragma unroll
-                    for (int rb = 0; rb < RB; rb++)
-                        O[rb][db0 + j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pa[rb][ks], vf[grp & 1][j], O[rb][db0 + j], 0, 0, 0);
-                __builtin_amdgcn_sched_barrier(0);
-            }
-        }
-        if (!DB && more) {   // every wave is done with the one buffer pair: refill it
-            vx_lds_barrier();
-            load_k<NW>(vx_lds_addr(Kl[0]), Kc + (size_t)(kt + 1) * KBUF, wave, lane);
-            load_v<NW>(vx_lds_addr(Vl[0]), Vc + (size_t)(kt + 1) * KBUF, wave, lane);
-        }
-    }
-
-    // out = O / l * sigmoid(gate)
-#pragma unroll
-    for (int rb = 0; rb < RB; rb++) {
-        float il[4];
-#pragma unroll
-        for (int i = 0; i < 4; i++) il[i] = 1.0f / __shfl(lrow[rb], 4 * g + i, 64);
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int t = r0 + rb * 16 + 4 * g + i;
-            if (t >= a.T) continue;
-            const size_t tok = (size_t)b * a.T + t;
-            float *op = a.out + (tok * a.n_q + h) * HDG;
-            const uint16_t *gp = a.gate + tok * a.g_ts + (size_t)h * a.g_hs;
-#pragma unroll
-            for (int db = 0; db < 16; db++) {
-                const int dim = db * 16 + n;
-                const float gl = a.gate ? vx_bf16_to_f32(gp[dim]) : 0.0f;
-                op[dim] = a.gate ? (O[rb][db][i] * il[i]) * (1.0f / (1.0f + expf(-gl))) : O[rb][db][i] * il[i];
-            }
-        }
-    }
-}
-
 
 // Software-pipelined attention: 4 waves of 32 queries (two 16-query blocks,
 // so every K and V operand read from LDS feeds two MFMAs).  The stretch
@@ -1244,15 +954,26 @@ void gqp_pack(std::vector<CostItem> items, int nb, std::vector<std::vector<CostI
         std::sort(bn.begin(), bn.end(), [](const CostItem &x, const CostItem &y) { return x.first > y.first; });
 }
 
-// The schedule for this call's shape (built and uploaded once per shape);
+// The schedule for this call's shape (built and uploaded once per shape and
+// kept until the context closes: a captured graph holds its address);
 // nullptr when it would have to be uploaded inside a stream capture.
 const GqpSched *gqp_schedule(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d, int xcd_map) {
     const int n_qt = (d->T + PP_QT - 1) / PP_QT;
     const int key[7] = {d->T, d->pos0, d->n_q, d->n_kv, d->B, ctx->n_cu, xcd_map};
-    GqpSched *sc = (GqpSched *)ctx->gqp_sched;
-    if (sc && std::equal(key, key + 7, sc->key)) return sc;
-    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
-    if (hipStreamIsCapturing(ctx->stream, &cs) != hipSuccess || cs != hipStreamCaptureStatusNone) return nullptr;
+    for (void *p : ctx->gqp_scheds) {
+        const GqpSched *c = (const GqpSched *)p;
+        if (std::equal(key, key + 7, c->key)) return c;
+    }
+    if (vx_ctx_capturing(ctx)) return nullptr;
+    if (ctx->gqp_scheds.size() >= 64) {   // many shapes seen: start the cache afresh
+        if (hipStreamSynchronize(ctx->stream) != hipSuccess) return nullptr;
+        for (void *p : ctx->gqp_scheds) {
+            GqpSched *old = (GqpSched *)p;
+            vx_ctx_release(ctx, old->dev);   // kept while a captured graph may use it
+            free(old);
+        }
+        ctx->gqp_scheds.clear();
+    }
     const int n_groups = xcd_map ? 8 : 1;
     const int per = xcd_map ? std::max(1, ctx->n_cu / 8) : std::max(1, ctx->n_cu);
     std::vector<std::vector<CostItem>> group(n_groups);
@@ -1280,8 +1001,7 @@ const GqpSched *gqp_schedule(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d, 
         const auto &bn = bins[w % n_groups][w / n_groups];
         for (size_t i = 0; i < bn.size(); i++) tab[(size_t)w * len + i] = bn[i].second;
     }
-    vx_gqp_sched_free(ctx);
-    sc = (GqpSched *)calloc(1, sizeof(GqpSched));
+    GqpSched *sc = (GqpSched *)calloc(1, sizeof(GqpSched));
     if (!sc) return nullptr;
     if (hipMalloc(&sc->dev, tab.size() * sizeof(int)) != hipSuccess) { free(sc); return nullptr; }
     if (hipMemcpy(sc->dev, tab.data(), tab.size() * sizeof(int), hipMemcpyHostToDevice) != hipSuccess) {
@@ -1292,17 +1012,18 @@ const GqpSched *gqp_schedule(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d, 
     std::copy(key, key + 7, sc->key);
     sc->len = len;
     sc->n_wg = n_wg;
-    ctx->gqp_sched = sc;
+    ctx->gqp_scheds.push_back(sc);
     return sc;
 }
 }  // namespace
 
 void vx_gqp_sched_free(vx27_hip_ctx *ctx) {
-    GqpSched *sc = (GqpSched *)ctx->gqp_sched;
-    if (!sc) return;
-    (void)hipFree(sc->dev);
-    free(sc);
-    ctx->gqp_sched = nullptr;
+    for (void *p : ctx->gqp_scheds) {
+        GqpSched *sc = (GqpSched *)p;
+        (void)hipFree(sc->dev);
+        free(sc);
+    }
+    ctx->gqp_scheds.clear();
 }
 
 extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d) {
@@ -1360,7 +1081,6 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     aa.out = d->out;
     // XCD grouping needs whole KV heads per XCD pair set: n_kv | 8 and 8 | n_q
     aa.xcd_map = (8 % d->n_kv == 0) && (d->n_q % 8 == 0) && ((d->n_q / 8) * (8 / d->n_kv) == d->n_q / d->n_kv);
-#if GQP_PP
     const int n_qt = (d->T + PP_QT - 1) / PP_QT;
     aa.n_qt = n_qt;
     aa.sched = nullptr;
@@ -1373,11 +1093,5 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     } else {    // (inside a stream capture, first call of a shape) one workgroup per item
         VX_LAUNCH_NAMED(ctx, "gqp_attn", gqp_attn_pp, dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B), dim3(PP_NW * 64), aa);
     }
-#else
-    constexpr int QT = GQP_NW * GQP_RB * 16;
-    const int n_qt = (d->T + QT - 1) / QT;
-    VX_LAUNCH_NAMED(ctx, "gqp_attn", (gqp_attn<GQP_NW, GQP_RB, GQP_DB != 0>), dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B),
-                    dim3(GQP_NW * 64), aa);
-#endif
     return 0;
 }

@@ -268,38 +268,6 @@ extern "C" int vx27_hip_advance_pos(vx27_hip_ctx *ctx, int *pos, int B) {
     return 0;
 }
 
-extern "C" int vx27_hip_graph_begin(vx27_hip_ctx *ctx) {
-    if (vx_ctx_enter(ctx)) return -1;
-    VX_REQUIRE(!ctx->prof_on, "vx27_hip_graph_begin: disable the profiler before capturing");
-    VX_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
-    return 0;
-}
-
-extern "C" int vx27_hip_graph_end(vx27_hip_ctx *ctx, void **graph_exec) {
-    if (vx_ctx_enter(ctx)) return -1;
-    VX_REQUIRE(graph_exec != nullptr, "vx27_hip_graph_end: null output");
-    hipGraph_t g = nullptr;
-    VX_HIP(hipStreamEndCapture(ctx->stream, &g));
-    hipGraphExec_t e = nullptr;
-    const hipError_t rc = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
-    (void)hipGraphDestroy(g);
-    VX_HIP(rc);
-    *graph_exec = (void *)e;
-    return 0;
-}
-
-extern "C" int vx27_hip_graph_launch(vx27_hip_ctx *ctx, void *graph_exec) {
-    if (vx_ctx_enter(ctx)) return -1;
-    VX_REQUIRE(graph_exec != nullptr, "vx27_hip_graph_launch: null graph");
-    VX_HIP(hipGraphLaunch((hipGraphExec_t)graph_exec, ctx->stream));
-    return 0;
-}
-
-extern "C" int vx27_hip_graph_destroy(void *graph_exec) {
-    if (graph_exec) VX_HIP(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
-    return 0;
-}
-
 extern "C" int vx27_hip_fill_normal_f32(vx27_hip_ctx *ctx, float *p, size_t n, uint64_t seed, float mean,
                                         float std) {
     if (vx_ctx_enter(ctx)) return -1;

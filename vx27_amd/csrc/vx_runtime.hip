@@ -4,6 +4,8 @@
 #include <string.h>
 
 #include <atomic>
+#include <mutex>
+#include <unordered_map>
 
 #include "vx_common.h"
 
@@ -62,11 +64,17 @@ extern "C" int vx27_hip_open(vx27_hip_ctx **out, int device, char *err, size_t e
                      prop.gcnArchName);
         return fail();
     }
-    vx27_hip_ctx *c = (vx27_hip_ctx *)calloc(1, sizeof(vx27_hip_ctx));
+    vx27_hip_ctx *c = new vx27_hip_ctx();
     c->device = device;
     if (hipSetDevice(device) != hipSuccess || hipStreamCreateWithFlags(&c->own_stream, hipStreamNonBlocking) != hipSuccess) {
         vx_set_error("vx27_hip_open: stream creation failed on device %d", device);
-        free(c);
+        delete c;
+        return fail();
+    }
+    if (hipMalloc((void **)&c->err_flag, 256) != hipSuccess || hipMemset(c->err_flag, 0, 256) != hipSuccess) {
+        vx_set_error("vx27_hip_open: cannot allocate the error flag on device %d", device);
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
         return fail();
     }
     c->stream = c->own_stream;
@@ -141,22 +149,34 @@ extern "C" int vx27_hip_prof_read(vx27_hip_ctx *ctx, const char *name, int *coun
     return 0;
 }
 
+static void graphs_forget(vx27_hip_ctx *ctx);
+
 extern "C" void vx27_hip_close(vx27_hip_ctx *ctx) {
     if (!ctx) return;
     (void)hipSetDevice(ctx->device);
     (void)hipStreamSynchronize(ctx->stream);
+    graphs_forget(ctx);
     prof_clear(ctx);
     free(ctx->prof);
     vx_gqp_sched_free(ctx);
+    for (void *p : ctx->retired) (void)hipFree(p);
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->stage) (void)hipFree(ctx->stage);
+    if (ctx->err_flag) (void)hipFree(ctx->err_flag);
     (void)hipStreamDestroy(ctx->own_stream);
-    free(ctx);
+    delete ctx;
 }
 
 extern "C" int vx27_hip_sync(vx27_hip_ctx *ctx) {
     if (vx_ctx_enter(ctx)) return -1;
     VX_HIP(hipStreamSynchronize(ctx->stream));
+    int flag = 0;
+    VX_HIP(hipMemcpy(&flag, ctx->err_flag, sizeof flag, hipMemcpyDeviceToHost));
+    if (flag) {
+        VX_HIP(hipMemset(ctx->err_flag, 0, sizeof flag));
+        VX_REQUIRE(false, "vx27_hip_sync: a decode call since the last sync had a position outside its KV cache "
+                          "(pos < 0 or pos >= L); its outputs are undefined");
+    }
     return 0;
 }
 
@@ -168,10 +188,31 @@ extern "C" int vx27_hip_set_stream(vx27_hip_ctx *ctx, void *s) {
 
 extern "C" void *vx27_hip_get_stream(vx27_hip_ctx *ctx) { return ctx ? (void *)ctx->stream : nullptr; }
 
+bool vx_ctx_capturing(vx27_hip_ctx *ctx) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(ctx->stream, &cs) != hipSuccess) return true;
+    return cs != hipStreamCaptureStatusNone;
+}
+
+static std::mutex g_graph_mu;   // guards live_graphs and the owner map below
+
+void vx_ctx_release(vx27_hip_ctx *ctx, void *dptr) {
+    if (!dptr) return;
+    std::lock_guard<std::mutex> lk(g_graph_mu);
+    if (ctx->live_graphs > 0)
+        ctx->retired.push_back(dptr);
+    else
+        (void)hipFree(dptr);
+}
+
 int vx_ctx_scratch(vx27_hip_ctx *ctx, size_t bytes, void **out) {
     if (bytes > ctx->scratch_bytes) {
+        VX_REQUIRE(!vx_ctx_capturing(ctx),
+                   "scratch of %zu bytes needed inside a graph capture (have %zu): run the same call once "
+                   "before capturing",
+                   bytes, ctx->scratch_bytes);
         VX_HIP(hipStreamSynchronize(ctx->stream));
-        if (ctx->scratch) VX_HIP(hipFree(ctx->scratch));
+        vx_ctx_release(ctx, ctx->scratch);
         ctx->scratch = nullptr;
         ctx->scratch_bytes = 0;
         size_t want = bytes < ((size_t)1 << 20) ? ((size_t)1 << 20) : bytes;
@@ -179,6 +220,77 @@ int vx_ctx_scratch(vx27_hip_ctx *ctx, size_t bytes, void **out) {
         ctx->scratch_bytes = want;
     }
     *out = ctx->scratch;
+    return 0;
+}
+
+// ------------------------------------------------------------- HIP graphs
+// Which context captured each live executable graph (graph_destroy has no
+// context argument).
+static std::unordered_map<void *, vx27_hip_ctx *> g_graph_owner;
+
+static void graphs_forget(vx27_hip_ctx *ctx) {
+    std::lock_guard<std::mutex> lk(g_graph_mu);
+    for (auto &kv : g_graph_owner)
+        if (kv.second == ctx) kv.second = nullptr;
+}
+
+extern "C" int vx27_hip_graph_begin(vx27_hip_ctx *ctx) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(!ctx->prof_on, "vx27_hip_graph_begin: disable the profiler before capturing");
+    VX_HIP(hipStreamBeginCapture(ctx->stream, hipStreamCaptureModeThreadLocal));
+    return 0;
+}
+
+extern "C" int vx27_hip_graph_end(vx27_hip_ctx *ctx, void **graph_exec) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(graph_exec != nullptr, "vx27_hip_graph_end: null output");
+    hipGraph_t g = nullptr;
+    VX_HIP(hipStreamEndCapture(ctx->stream, &g));
+    hipGraphExec_t e = nullptr;
+    const hipError_t rc = hipGraphInstantiate(&e, g, nullptr, nullptr, 0);
+    (void)hipGraphDestroy(g);
+    VX_HIP(rc);
+    {
+        std::lock_guard<std::mutex> lk(g_graph_mu);
+        g_graph_owner[(void *)e] = ctx;
+        ctx->live_graphs++;
+    }
+    *graph_exec = (void *)e;
+    return 0;
+}
+
+extern "C" int vx27_hip_graph_launch(vx27_hip_ctx *ctx, void *graph_exec) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(graph_exec != nullptr, "vx27_hip_graph_launch: null graph");
+    VX_HIP(hipGraphLaunch((hipGraphExec_t)graph_exec, ctx->stream));
+    return 0;
+}
+
+extern "C" int vx27_hip_graph_destroy(void *graph_exec) {
+    if (!graph_exec) return 0;
+    vx27_hip_ctx *owner = nullptr;
+    {
+        std::lock_guard<std::mutex> lk(g_graph_mu);
+        auto it = g_graph_owner.find(graph_exec);
+        if (it != g_graph_owner.end()) {
+            owner = it->second;
+            g_graph_owner.erase(it);
+        }
+    }
+    if (owner) {
+        VX_HIP(hipSetDevice(owner->device));
+        // a replay of this graph may still be running on the stream
+        VX_HIP(hipStreamSynchronize(owner->stream));
+    }
+    VX_HIP(hipGraphExecDestroy((hipGraphExec_t)graph_exec));
+    if (owner) {
+        std::vector<void *> drop;
+        {
+            std::lock_guard<std::mutex> lk(g_graph_mu);
+            if (--owner->live_graphs == 0) drop.swap(owner->retired);
+        }
+        for (void *p : drop) VX_HIP(hipFree(p));
+    }
     return 0;
 }
 
@@ -252,14 +364,16 @@ extern "C" int vx27_hip_enable(void) {
 extern "C" void vx27_hip_disable(void) { g_route_on.store(0); }
 extern "C" int vx27_hip_enabled(void) { return g_route_on.load(); }
 
+// Opened once, by the first caller, whichever thread that is.
+static std::once_flag g_default_once;
+
 extern "C" vx27_hip_ctx *vx27_hip_default_ctx(void) {
-    if (g_default) return g_default;
-    const char *env = getenv("VX27_HIP_DEVICE");
-    int dev = env ? atoi(env) : 0;
-    char err[256];
-    if (vx27_hip_open(&g_default, dev, err, sizeof err) != 0) {
-        g_default = nullptr;
-        return nullptr;
-    }
+    std::call_once(g_default_once, [] {
+        const char *env = getenv("VX27_HIP_DEVICE");
+        int dev = env ? atoi(env) : 0;
+        char err[256];
+        if (vx27_hip_open(&g_default, dev, err, sizeof err) != 0) g_default = nullptr;
+    });
+    if (!g_default) vx_set_error("vx27_hip_default_ctx: no context could be opened on the default device");
     return g_default;
 }
