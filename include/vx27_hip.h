@@ -193,6 +193,18 @@ typedef struct {
  * over positions 0..pos -> * sigmoid(gate). */
 int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d);
 
+/* The same decode step without any allocation in the call.  No counterpart
+ * in the reference: it is for callers that cannot allocate (code under HIP
+ * graph capture, tight serving loops, harnesses that forbid hipMalloc).  Its
+ * scratch (normed q and the split-K partials) is a static 16 MiB device
+ * array, one per GPU, set up by vx27_hip_open and held until the process
+ * ends; a call needing more (B * n_kv * n_split * (n_q/n_kv) partials of
+ * 258 floats plus B * n_q * 256 floats) returns -1 with the size.  Every
+ * call on one GPU shares that array and leaves its contents there: calls
+ * that overlap on one GPU (two streams or two contexts) race.  Results are
+ * bit-identical to vx27_hip_gqa_decode's.  The profiler does not record it. */
+int vx27_hip_gqa_decode_noalloc(vx27_hip_ctx *ctx, const vx27_gqa_desc *d);
+
 /* GQA prefill: T new tokens of each of B sequences at positions pos0..pos0+T-1
  * (token by token as vx27_qlayer_batch runs the decode glue,
  * vx27_qfwd.c:314-376): rmsn q,k -> RoPE -> k,v written to the cache (bf16,

@@ -39,3 +39,6 @@ size_t vx_gqa_scratch_bytes(const vx27_gqa_desc *d);
 // the output projection.
 int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uint16_t *out_packed);
 
+// Looks up the per-device address of the no-allocation decode scratch
+// (vx_gqa_decode.hip); called by vx27_hip_open with the device current.
+int vx_noalloc_init(int device);

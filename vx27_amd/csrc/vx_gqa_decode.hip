@@ -30,6 +30,8 @@
 //                                           dim-major V block.
 #include <math.h>
 
+#include <mutex>
+
 #include "vx_gemv.h"
 #include "vx_gqa.h"
 
@@ -436,6 +438,55 @@ extern "C" int vx27_hip_gqa_decode(vx27_hip_ctx *ctx, const vx27_gqa_desc *d) {
     void *scr;
     if (vx_ctx_scratch(ctx, vx_gqa_scratch_bytes(d), &scr)) return -1;
     return vx_gqa_decode_into(ctx, d, scr, nullptr);
+}
+
+// ---- the decode step without allocation ----------------------------------
+// Scratch of vx27_hip_gqa_decode_noalloc: a file-scope device array, one
+// copy per GPU, held until the process ends.  Host code never passes the
+// array's name to a kernel (on the host it is only a stand-in for the
+// symbol): vx_noalloc_init looks up each device's address once, with that
+// device current, and the entry point passes that address.
+#define VX_NOALLOC_SCRATCH_BYTES (16u << 20)
+static __device__ __align__(256) char scratch[VX_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+constexpr int VX_MAX_DEVICES = 64;
+std::mutex g_noalloc_mu;
+void *g_noalloc_ptr[VX_MAX_DEVICES];
+}  // namespace
+
+// Called by vx27_hip_open (the device is current): the device address of
+// `scratch` on `device`, looked up once per device.
+int vx_noalloc_init(int device) {
+    VX_REQUIRE(device >= 0 && device < VX_MAX_DEVICES, "vx27_hip_open: device %d beyond %d", device, VX_MAX_DEVICES);
+    std::lock_guard<std::mutex> lk(g_noalloc_mu);
+    if (g_noalloc_ptr[device]) return 0;
+    void *ptr = nullptr;
+    VX_HIP(hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch)));
+    VX_REQUIRE(ptr != nullptr, "vx27_hip_open: no device address for the decode scratch on device %d", device);
+    g_noalloc_ptr[device] = ptr;
+    return 0;
+}
+
+extern "C" int vx27_hip_gqa_decode_noalloc(vx27_hip_ctx *ctx, const vx27_gqa_desc *d) {
+    if (vx_ctx_enter(ctx)) return -1;
+    if (gqa_check(d)) return -1;
+    VX_REQUIRE(d->out != nullptr, "vx27_hip_gqa_decode_noalloc: null output");
+    const size_t need = vx_gqa_scratch_bytes(d);
+    VX_REQUIRE(need <= VX_NOALLOC_SCRATCH_BYTES,
+               "vx27_hip_gqa_decode_noalloc: needs %zu bytes of scratch, the static buffer holds %u "
+               "(lower B or n_split, or use vx27_hip_gqa_decode)",
+               need, VX_NOALLOC_SCRATCH_BYTES);
+    void *scr = g_noalloc_ptr[ctx->device];
+    VX_REQUIRE(scr != nullptr, "vx27_hip_gqa_decode_noalloc: scratch not set up on device %d", ctx->device);
+    // every scratch element a kernel reads was written earlier in the same
+    // call (q, then the split partials), so nothing needs clearing; the
+    // profiler (host event records) is bypassed
+    const int prof = ctx->prof_on;
+    ctx->prof_on = 0;
+    const int rc = vx_gqa_decode_into(ctx, d, scr, nullptr);
+    ctx->prof_on = prof;
+    return rc;
 }
 
 extern "C" int vx27_hip_kv_write(vx27_hip_ctx *ctx, uint16_t *k_cache, uint16_t *v_cache, int B_total,

@@ -8,6 +8,7 @@
 #include <unordered_map>
 
 #include "vx_common.h"
+#include "vx_gqa.h"
 
 static thread_local char g_err[512] = "";
 
@@ -73,6 +74,12 @@ extern "C" int vx27_hip_open(vx27_hip_ctx **out, int device, char *err, size_t e
     }
     if (hipMalloc((void **)&c->err_flag, 256) != hipSuccess || hipMemset(c->err_flag, 0, 256) != hipSuccess) {
         vx_set_error("vx27_hip_open: cannot allocate the error flag on device %d", device);
+        (void)hipStreamDestroy(c->own_stream);
+        delete c;
+        return fail();
+    }
+    if (vx_noalloc_init(device) != 0) {
+        (void)hipFree(c->err_flag);
         (void)hipStreamDestroy(c->own_stream);
         delete c;
         return fail();

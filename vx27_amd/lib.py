@@ -97,6 +97,7 @@ _SIGS = {
     "vx27_hip_dn_prefill": (C.c_int, [VP, C.POINTER(DnPrefillDesc)]),
     "vx27_hip_gqa_prefill": (C.c_int, [VP, C.POINTER(GqaPrefillDesc)]),
     "vx27_hip_gqa_decode": (C.c_int, [VP, C.POINTER(GqaDesc)]),
+    "vx27_hip_gqa_decode_noalloc": (C.c_int, [VP, C.POINTER(GqaDesc)]),
     "vx27_hip_kv_write": (C.c_int, [VP, VP, VP] + [C.c_int] * 7 + [VP, VP]),
     "vx27_hip_kv_read": (C.c_int, [VP, VP, VP] + [C.c_int] * 7 + [VP, VP]),
     "vx27_hip_rope_table": (C.c_int, [VP, VP, C.c_int, C.c_int, C.c_float, C.c_float, VP, VP]),
