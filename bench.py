@@ -28,10 +28,21 @@ Workloads (synthetic, seeded, random-init):
   dn_conv   batched Gated DeltaNet decode with the fused causal conv:
             64 sequences x 16 heads x 128x128 fp32 state, 6144 conv channels
             (bf16 weights), l2norm q/k, exact delta rule; 256 steps
-Extras (without --no-extra): dn_conv, gated GQA decode at 8192 positions
-(batch 1 and 32), the two prefills of a 4096-token prompt (chunked DeltaNet,
-16 heads; causal gated GQA, 24Q/4KV hd 256) against the bf16 MFMA peak, and
-the DeltaNet recurrence alone (1 sequence x 16 heads, 2000 steps).
+Extras (without --no-extra), each with its algorithmic bytes (or flops)
+and roofline fraction, and the oracle timed on this host where noted:
+  c1_dn_recurrent   DeltaNet recurrence, 1 sequence x 16 heads, 2000 steps:
+                    one multi-step call (state resident) and per-step calls
+                    (state streamed, 2,130,048 B/step); CPU-exact and
+                    CPU-AVX2 (the compiled reference's AVX2 primitives when
+                    oracle/_ref is built), 16 threads and 1 thread
+  c2_gqa8k_B{1,4,32}  gated GQA decode at 8192 cached positions
+                    (33,640,448 B per sequence); CPU at B=1 and 32
+  c3_dn_conv_B{1,4,16,64}  batched DeltaNet decode with the fused conv;
+                    CPU at B=64 (16 threads and 1 thread)
+  c4a/c4b           the two prefills of a 4096-token prompt (chunked
+                    DeltaNet, 16 heads; causal gated GQA, 24Q/4KV hd 256)
+                    against the bf16 MFMA peak
+  host              nproc, usable CPUs, CPU model, threads of the CPU legs
 """
 from __future__ import annotations
 
@@ -165,7 +176,17 @@ def cpu_c5(B, ctx_sample=8192):
 
 
 # --------------------------------------------------------------- DeltaNet
+def dn_conv_alg_bytes(B, H=16, hd=128):
+    """Algorithmic bytes of one batched DeltaNet + conv decode step: state
+    r+w, conv state r+w, x, o, conv weights (bf16) and gate inputs."""
+    C_ = 3 * H * hd
+    return (2 * B * H * hd * hd * 4 + 2 * B * C_ * 3 * 4 + B * C_ * 4 + B * H * hd * 4 + C_ * 4 * 2
+            + B * H * 2 * 4)
+
+
 def bench_dn_conv(ctx, steps, warmup, B=64, H=16, cpu=True):
+    """Batched DeltaNet decode with the fused conv, one step per call (one
+    launch: conv, gates, norms, exact step)."""
     from vx27_amd import lib as L, mixers as M, workloads as W
     hd, C_ = 128, 3 * 16 * 128
     total = steps + warmup
@@ -201,46 +222,52 @@ def bench_dn_conv(ctx, steps, warmup, B=64, H=16, cpu=True):
     if n == 0:
         kname = "dn_decode_kernel"
         n, ms = ctx.prof_read(kname)
-    ng, msg = ctx.prof_read("dn_gate_kernel")
     ctx.prof_enable(False)
-    # algorithmic bytes of the decode kernel per launch (one step of B sequences)
-    alg = (2 * B * H * hd * hd * 4        # S read + write
-           + 2 * B * C_ * 3 * 4           # conv state read + write
-           + B * C_ * 4                   # x
-           + B * H * hd * 4               # out
-           + C_ * 4 * 2)                  # conv weights (bf16)
+    alg = dn_conv_alg_bytes(B, H, hd)
     avg_s = ms / n / 1e3
+    step_s = wall / steps
     res = {
         "workload": f"dn_conv B={B} heads={H} hd=128 conv=6144ch bf16w, {steps} steps",
-        "us_per_step": wall / steps * 1e6,
-        "us_per_token": wall / steps / B * 1e6,
+        "us_per_step": step_s * 1e6, "us_per_token": step_s / B * 1e6,
         "kernel": kname, "kernel_us": avg_s * 1e6,
-        "gate_kernel_us": msg / max(ng, 1) * 1e3,
-        "alg_bytes": alg, "achieved_GBs": alg / avg_s / 1e9,
+        "alg_bytes_per_step": alg, "achieved_GBs": alg / avg_s / 1e9,
+        "hbm_frac_kernel": alg / avg_s / HBM_PEAK, "hbm_frac_step": alg / step_s / HBM_PEAK,
     }
     if cpu:
         res["cpu"] = cpu_dn_conv(d, B, H)
+    for bb in (x, a, b, out, lay.S, lay.conv_state):
+        bb.free()
     return res
 
 
-def cpu_dn_conv(d, B, H, steps=96):
+def cpu_dn_conv(d, B, H, steps=96, steps_1t=8):
     """Oracle (CPU restatement, CPU-exact semantics) on the first `steps`
-    steps of the same workload, all B x H units in parallel."""
+    steps of the same workload, all B x H units in parallel; and on the
+    first `steps_1t` steps on one thread."""
     from oracle import oracle as O
-    from gpu_common import oracle_dn  # noqa: F401  (same driver as the tests)
-    sub = dict(d)
-    for k in ("x", "a", "b"):
-        sub[k] = np.ascontiguousarray(d[k][:steps])
+    from gpu_common import oracle_dn
     from vx27_amd import lib as L
     th = O.default_threads()
-    _, _, _, secs = oracle_dn(sub, L.DN_CONV | L.DN_PRE_L2, B, H, H, steps, threads=th)
-    return {"value": secs / (steps * B) * 1e6, "unit": "us/token", "cores": th, "kind": "port",
-            "sample": f"oracle step_exact path, {B} seq x {H} heads x {steps} of the steps, {th} threads"}
+    res = {}
+    for nth, ns in ((th, steps), (1, steps_1t)):
+        sub = dict(d)
+        for k in ("x", "a", "b"):
+            sub[k] = np.ascontiguousarray(d[k][:ns])
+        _, _, _, secs = oracle_dn(sub, L.DN_CONV | L.DN_PRE_L2, B, H, H, ns, threads=nth)
+        res[nth] = secs / (ns * B) * 1e6
+    return {"value": res[th], "unit": "us/token", "cores": th, "kind": "port",
+            "value_1thread": res[1],
+            "sample": f"oracle step_exact path (conv, l2 pre-norm), {B} seq x {H} heads: the first {steps} "
+                      f"steps on {th} threads, the first {steps_1t} on 1 thread"}
 
 
-def bench_dn_recurrent(ctx, steps=2000):
-    """16 heads x 2000 steps, one sequence: per-step launches and one
-    multi-step launch (state resident in registers)."""
+C1_BYTES_PER_STEP = 2130048   # S r+w 2,097,152 + q,k,v 24,576 + a,b 128 + o 8,192 (16 heads)
+
+
+def bench_dn_recurrent(ctx, steps=2000, cpu=True):
+    """16 heads x 2000 steps, one sequence: one multi-step launch (state
+    resident in registers: µs/step only) and per-step launches (the state
+    streamed from HBM and back every step: %HBM against 2,130,048 B/step)."""
     from vx27_amd import lib as L, mixers as M, workloads as W
     H, hd = 16, 128
     d = W.dn_recurrent(B=1, H=H, steps=steps)
@@ -261,19 +288,98 @@ def bench_dn_recurrent(ctx, steps=2000):
         per.append(lay.desc(1, 0, out.ptr + t * H * hd * 4, bufs["a"].ptr + t * H * 4,
                             bufs["b"].ptr + t * H * 4, q=bufs["q"].ptr + t * H * hd * 4,
                             k=bufs["k"].ptr + t * H * hd * 4, v=bufs["v"].ptr + t * H * hd * 4))
+    for t in range(8):
+        L.check(fn(ctx.h, C.byref(per[t])), "dn_decode")
     ctx.sync()
     t0 = time.perf_counter()
     for t in range(steps):
         L.check(fn(ctx.h, C.byref(per[t])), "dn_decode")
     ctx.sync()
     single = time.perf_counter() - t0
-    return {"workload": f"dn_recurrent B=1 heads=16 {steps} steps",
-            "us_per_step_multistep_call": multi / steps * 1e6,
-            "us_per_step_per_step_calls": single / steps * 1e6}
+    ctx.prof_enable(True)
+    for t in range(200):
+        L.check(fn(ctx.h, C.byref(per[t])), "dn_decode")
+    ctx.sync()
+    kern = {k: ctx.prof_read(k) for k in ("dn_step_kernel", "dn_decode_kernel", "dn_gate_kernel")}
+    ctx.prof_enable(False)
+    k_us = sum(ms for _, ms in kern.values()) / 200 * 1e3
+    res = {"workload": f"dn_recurrent B=1 heads=16 {steps} steps",
+           "us_per_step_resident": multi / steps * 1e6,
+           "us_per_step_streamed": single / steps * 1e6,
+           "kernel_us_streamed": k_us,
+           "kernels_streamed": {k: v[0] / 200 for k, v in kern.items() if v[0]},
+           "alg_bytes_per_step_streamed": C1_BYTES_PER_STEP,
+           "hbm_frac_streamed_kernel": C1_BYTES_PER_STEP / (k_us / 1e6) / HBM_PEAK,
+           "hbm_frac_streamed_step": C1_BYTES_PER_STEP / (single / steps) / HBM_PEAK}
+    if cpu:
+        res.update(cpu_dn_recurrent(d, steps))
+    for bb in list(bufs.values()) + [out, lay.S]:
+        bb.free()
+    return res
+
+
+def cpu_dn_recurrent(d, steps, steps_1t=250):
+    """C1 on the host: CPU-exact (the oracle's step_exact, 16 heads in
+    parallel) and CPU-AVX2 (the reference's AVX2 update/retrieve composed
+    into the gated delta rule: the compiled reference's own functions when
+    oracle/_ref is built, else their pinned restatement), each on 16 threads
+    over the 2000 steps and on 1 thread over the first 250."""
+    from oracle import oracle as O
+    from gpu_common import oracle_dn
+    H, hd = 16, 128
+    th = min(H, O.default_threads())
+    exact = {}
+    for nth, ns in ((th, steps), (1, steps_1t)):
+        sub = dict(d)
+        for k in ("q", "k", "v", "a", "b"):
+            sub[k] = np.ascontiguousarray(d[k][:ns])
+        _, _, _, secs = oracle_dn(sub, 0, 1, H, H, ns, threads=nth)
+        exact[nth] = secs / ns * 1e6
+    # the AVX2 composition takes normalised q (with the 1/sqrt(hd) scale) and k,
+    # beta and the decay exp(g) per (step, head) (vx27_deltanet.c:58-69)
+    q = np.ascontiguousarray(np.stack([O.l2norm(r) for r in d["q"].reshape(-1, hd)]).reshape(d["q"].shape)
+                             * np.float32(1.0 / np.sqrt(np.float32(hd))), np.float32)
+    k = np.ascontiguousarray(np.stack([O.l2norm(r) for r in d["k"].reshape(-1, hd)]).reshape(d["k"].shape))
+    a = d["a"].astype(np.float64)
+    b = d["b"].astype(np.float64)
+    x = a + d["dt_bias"].astype(np.float64)
+    sp = np.where(x > 20, x, np.where(x < -20, np.exp(x), np.log1p(np.exp(np.minimum(x, 20)))))
+    decay = np.ascontiguousarray(np.exp(-np.exp(d["A_log"].astype(np.float64)) * sp))
+    beta = np.ascontiguousarray(1.0 / (1.0 + np.exp(-b)))
+    v = np.ascontiguousarray(d["v"])
+    upd, ret = O.ref_avx2_fns()
+    kind = "reference" if upd is not None else "port"
+    avx = {}
+    for nth, ns in ((th, steps), (1, steps_1t)):
+        S = np.zeros((H, hd, hd), np.float32)
+        out = np.empty((ns, H, hd), np.float32)
+        secs = O.lib().orc_dn_run_avx2(1, H, hd, ns, nth, S.reshape(-1), q[:ns].reshape(-1), k[:ns].reshape(-1),
+                                       v[:ns].reshape(-1), beta[:ns].reshape(-1), decay[:ns].reshape(-1),
+                                       out.reshape(-1), upd, ret)
+        avx[nth] = secs / ns * 1e6
+    return {"cpu_exact": {"value": exact[th], "unit": "us/step", "cores": th, "kind": "port",
+                          "value_1thread": exact[1],
+                          "sample": f"oracle step_exact, 16 heads x {steps} steps on {th} threads; "
+                                    f"first {steps_1t} steps on 1 thread"},
+            "cpu_avx2": {"value": avx[th], "unit": "us/step", "cores": th, "kind": kind,
+                         "value_1thread": avx[1],
+                         "sample": ("compiled reference vx27_deltanet_update_avx2/retrieve_avx2"
+                                    if kind == "reference" else "restated AVX2 update/retrieve")
+                                   + f" composed into the gated delta rule, 16 heads x {steps} steps on {th} "
+                                   f"threads; first {steps_1t} steps on 1 thread"}}
 
 
 # -------------------------------------------------------------------- GQA
-def bench_gqa(ctx, B, Lctx=8192, iters=20):
+GQA_SEQ_EXTRA_BYTES = 24 * 256 * 4 * 3 + 2 * 4 * 256 * 4   # q, gate, out fp32 + k_new, v_new
+
+
+def gqa_alg_bytes(B, n_keys):
+    """K and V (bf16) of every attended position plus the per-sequence q,
+    gate, out and new k,v rows: 33,640,448 B per sequence at 8193 keys."""
+    return B * (4 * n_keys * 256 * 2 * 2 + GQA_SEQ_EXTRA_BYTES)
+
+
+def bench_gqa(ctx, B, Lctx=8192, iters=20, cpu=False):
     from vx27_amd import lib as L, mixers as M, workloads as W
     d = W.gqa_decode(B=B, L=Lctx)
     Lcap = (Lctx + 1 + 63) // 64 * 64
@@ -299,14 +405,46 @@ def bench_gqa(ctx, B, Lctx=8192, iters=20):
     for _ in range(iters):
         L.check(fn(ctx.h, C.byref(desc)), "gqa_decode")
     ctx.sync()
-    n, ms = ctx.prof_read("gqa_split")
+    kern = {k: ctx.prof_read(k) for k in ("gqa_prep", "gqa_split", "gqa_combine")}
     ctx.prof_enable(False)
     nk = Lctx + 1
-    alg = B * 4 * nk * hd * 2 * 2          # K and V bf16 of every attended position
-    avg_s = ms / n / 1e3
-    return {"workload": f"gqa_decode B={B} L={Lctx}", "us_per_step": wall * 1e6,
-            "us_per_token": wall / B * 1e6, "kernel": "gqa_split", "kernel_us": avg_s * 1e6,
-            "alg_bytes": alg, "achieved_GBs": alg / avg_s / 1e9}
+    kv = B * 4 * nk * hd * 2 * 2          # K and V bf16 of every attended position
+    alg = gqa_alg_bytes(B, nk)
+    split_s = kern["gqa_split"][1] / kern["gqa_split"][0] / 1e3
+    kern_s = sum(ms for _, ms in kern.values()) / iters / 1e3
+    res = {"workload": f"gqa_decode B={B} L={Lctx}", "us_per_step": wall * 1e6,
+           "us_per_token": wall / B * 1e6, "kernels_us": {k: v[1] / v[0] * 1e3 for k, v in kern.items()},
+           "kernel": "gqa_split", "kernel_us": split_s * 1e6,
+           "alg_bytes_per_step": alg, "kernel_alg_bytes": kv, "achieved_GBs": kv / split_s / 1e9,
+           "hbm_frac_kernel": kv / split_s / HBM_PEAK, "hbm_frac_kernels": alg / kern_s / HBM_PEAK,
+           "hbm_frac_step": alg / wall / HBM_PEAK}
+    if cpu:
+        res["cpu"] = cpu_gqa(d, B, nk)
+    for bb in (qb, kb, vb, pb, ob, lay.k_cache, lay.v_cache):
+        bb.free()
+    return res
+
+
+def cpu_gqa(d, B, nk):
+    """The oracle's attention (the vx27_qlayer loop: double dot, float
+    softmax and P.V) over the same bf16 cache, B x 24 (sequence, head)
+    units in parallel, median of 3 runs (the raw q rows stand in for the
+    normed ones: the time does not depend on the values)."""
+    from oracle import oracle as O
+    th = O.default_threads()
+    kv_k = np.ascontiguousarray(d["K"])     # [B][L][4][256] bf16 (the new row is not appended here)
+    kv_v = np.ascontiguousarray(d["V"])
+    L_ = kv_k.shape[1]
+    q = np.ascontiguousarray(d["qg"][:, :, :256])
+    n_keys = np.full(B, min(nk, L_), np.int32)
+    out = np.empty((B, 24, 256), np.float32)
+    a = O.AttendBatchArgs(B, 24, 4, 256, th, 1, 1, n_keys.ctypes.data, q.ctypes.data, kv_k.ctypes.data,
+                          kv_v.ctypes.data, L_ * 1024, 1024, 256, 1024, 256, out.ctypes.data)
+    O.lib().orc_attend_batch(C.byref(a))
+    t = sorted(O.lib().orc_attend_batch(C.byref(a)) for _ in range(3))[1]
+    return {"value": t / B * 1e6, "unit": "us/token", "cores": th, "kind": "port",
+            "sample": f"oracle attention over {int(n_keys[0])} bf16 keys, B={B} x 24 heads on {th} threads, "
+                      "median of 3"}
 
 
 # ---------------------------------------------------------------- prefill
@@ -419,6 +557,8 @@ def main():
     ap.add_argument("--context", type=int, default=131072)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4"],
+                    help="run one extra configuration alone and print its figures (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: measures one GPU only (asked for {args.gpus}); the mixers shard per "
@@ -428,6 +568,17 @@ def main():
     from vx27_amd import lib as L
     ctx = L.Ctx(0)
     log(f"bench: {L.lib().vx27_hip_version().decode()} workload={args.workload}")
+    if args.only:
+        cpu = not args.no_cpu
+        runs = {"c1": lambda: {"c1_dn_recurrent": bench_dn_recurrent(ctx, cpu=cpu)},
+                "c2": lambda: {f"c2_gqa8k_B{B}": bench_gqa(ctx, B, cpu=cpu) for B in (1, 4, 32)},
+                "c3": lambda: {f"c3_dn_conv_B{B}": bench_dn_conv(ctx, 256, 8, B=B, cpu=cpu and B == 64)
+                               for B in (1, 4, 16, 64)},
+                "c4": lambda: {"c4a_dn_prefill_T4096": bench_dn_prefill(ctx, cpu=cpu),
+                               "c4b_gqa_prefill_T4096": bench_gqa_prefill(ctx, cpu=cpu)}}
+        print(json.dumps({"only": args.only, "extra": runs[args.only]()}), flush=True)
+        ctx.close()
+        return
     extra = {}
     if args.workload == "c5":
         res = bench_c5(ctx, args.steps, args.warmup, Lctx=args.context, cpu=not args.no_cpu)
@@ -447,6 +598,7 @@ def main():
         dtype = "bf16 weights/KV, fp32 state (fp64 recurrence accumulation)"
     else:
         res = bench_dn_conv(ctx, args.steps, args.warmup, cpu=not args.no_cpu)
+        extra["c3_dn_conv_B64"] = {k: v for k, v in res.items() if k != "cpu"}
         value, unit = res["us_per_token"], "us/token"
         ms_step = res["us_per_step"] / 1e3
         config = {"workload": res["workload"], "batch": 64, "heads": 16, "head_dim": 128}
@@ -454,29 +606,40 @@ def main():
         traffic = None
         dtype = "fp32 (fp64 accumulation)"
     if not args.no_extra:
-        if args.workload != "dn_conv":
-            r = bench_dn_conv(ctx, 256, 8, cpu=False)
-            extra["dn_conv_B64"] = r
-            log(f"  dn_conv: {r['us_per_token']:.3f} us/token, kernel {r['kernel_us']:.1f} us, "
-                f"{r['achieved_GBs']:.0f} GB/s")
-        for B in (1, 32):
-            r = bench_gqa(ctx, B)
-            extra[f"gqa8k_B{B}"] = r
+        cpu = not args.no_cpu
+        for B in (1, 4, 16, 64):
+            if args.workload == "dn_conv" and B == 64:
+                continue
+            r = bench_dn_conv(ctx, 256, 8, B=B, cpu=cpu and B == 64)
+            extra[f"c3_dn_conv_B{B}"] = r
+            log(f"  dn_conv B={B}: {r['us_per_token']:.3f} us/token, kernel {r['kernel_us']:.1f} us, "
+                f"{r['achieved_GBs']:.0f} GB/s ({100 * r['hbm_frac_kernel']:.1f}% HBM)")
+        for B in (1, 4, 32):
+            r = bench_gqa(ctx, B, cpu=cpu and B in (1, 32))
+            extra[f"c2_gqa8k_B{B}"] = r
             log(f"  gqa B={B}: {r['us_per_step']:.1f} us/step, split kernel {r['kernel_us']:.1f} us, "
-                f"{r['achieved_GBs']:.0f} GB/s")
-        r = bench_dn_prefill(ctx, cpu=not args.no_cpu)
-        extra["dn_prefill_T4096"] = r
+                f"{r['achieved_GBs']:.0f} GB/s ({100 * r['hbm_frac_kernel']:.1f}% HBM), "
+                f"step {100 * r['hbm_frac_step']:.1f}% HBM")
+        r = bench_dn_prefill(ctx, cpu=cpu)
+        extra["c4a_dn_prefill_T4096"] = r
         log(f"  dn_prefill: {r['kernel_us']:.1f} us ({r['tokens_per_s']:.3g} tok/s), "
             f"MFMA {100 * r['mfma_frac']:.1f}%, HBM {100 * r['hbm_frac']:.1f}%  {r['kernels_us']}")
-        r = bench_gqa_prefill(ctx, cpu=not args.no_cpu)
-        extra["gqa_prefill_T4096"] = r
+        r = bench_gqa_prefill(ctx, cpu=cpu)
+        extra["c4b_gqa_prefill_T4096"] = r
         log(f"  gqa_prefill: {r['kernel_us']:.1f} us ({r['tokens_per_s']:.3g} tok/s), "
             f"MFMA {100 * r['mfma_frac']:.1f}% (attention kernel {100 * r['attn_mfma_frac']:.1f}%)  "
             f"{r['kernels_us']}")
-        r = bench_dn_recurrent(ctx)
-        extra["dn_recurrent"] = r
-        log(f"  dn_recurrent: {r['us_per_step_multistep_call']:.2f} us/step (one call), "
-            f"{r['us_per_step_per_step_calls']:.2f} us/step (per-step calls)")
+        r = bench_dn_recurrent(ctx, cpu=cpu)
+        extra["c1_dn_recurrent"] = r
+        log(f"  dn_recurrent: {r['us_per_step_resident']:.2f} us/step (state resident, one call), "
+            f"{r['us_per_step_streamed']:.2f} us/step (per-step calls; kernel {r['kernel_us_streamed']:.2f} us, "
+            f"{100 * r['hbm_frac_streamed_kernel']:.1f}% HBM)")
+        if cpu:
+            log(f"  dn_recurrent cpu: exact {r['cpu_exact']['value']:.1f} us/step, avx2 "
+                f"{r['cpu_avx2']['value']:.1f} us/step ({r['cpu_avx2']['kind']})")
+    if not args.no_cpu:
+        from oracle import oracle as O
+        extra["host"] = dict(O.host_info(), cpu_baseline_threads=O.default_threads())
     ach = kbytes / (kus / 1e6)
     line = {
         "metric": METRIC,

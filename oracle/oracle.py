@@ -128,7 +128,9 @@ def lib():
         "orc_dn_layer_token": (None, [C.POINTER(DnLayerW), F32P, F32P, F32P, F32P]),
         "orc_gqa_layer_token": (None, [C.POINTER(GqaLayerW), F32P, C.c_int, F32P, F32P, F32P]),
         "orc_dn_run": (C.c_double, [C.POINTER(DnRunArgs)]),
-        "orc_dn_run_avx2": (C.c_double, [C.c_int] * 5 + [F32P, F32P, F32P, F32P, F64P, F64P, F32P]),
+        "orc_dn_run_avx2": (C.c_double, [C.c_int] * 5 + [F32P, F32P, F32P, F32P, F64P, F64P, F32P, VP, VP]),
+        "orc_update_avx2_pub": (None, [F32P, F32P, F32P, C.c_float, C.c_int]),
+        "orc_retrieve_avx2_pub": (None, [F32P, F32P, F32P, C.c_int]),
         "orc_attend_batch": (C.c_double, [C.POINTER(AttendBatchArgs)]),
         "orc_gqa_prefill": (C.c_double, [C.POINTER(GqaPrefillArgs)]),
         "orc_matvec_batch": (C.c_double, [VP, C.c_int, F32P, F32P, C.c_int, C.c_int, C.c_int, C.c_int]),
@@ -256,9 +258,38 @@ def attend(q, k, v, n_keys, k_strides, v_strides, n_kv, dot_double=1, kv_bf16=0)
 
 
 def default_threads():
-    """Threads for the CPU baseline: the host's cores, capped at 16."""
+    """Threads for the CPU baseline: the CPUs this process may run on, at
+    most 16 (the host CPU share of one GPU on the GPU machines, whatever
+    nproc reports there)."""
     try:
         n = len(os.sched_getaffinity(0))
     except AttributeError:
         n = os.cpu_count() or 1
     return max(1, min(16, n))
+
+
+def host_info():
+    """nproc, usable CPUs, and the CPU model name of this host."""
+    model = "unknown"
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                model = line.split(":", 1)[1].strip()
+                break
+    except OSError:
+        pass
+    try:
+        usable = len(os.sched_getaffinity(0))
+    except AttributeError:
+        usable = os.cpu_count() or 1
+    return {"nproc": os.cpu_count(), "usable_cpus": usable, "cpu_model": model}
+
+
+def ref_avx2_fns():
+    """(update, retrieve) function pointers of the compiled reference's
+    vx27_deltanet_update_avx2 / retrieve_avx2, or (None, None) if
+    oracle/_ref was not built."""
+    R = ref()
+    if R is None:
+        return None, None
+    return (C.cast(R.vx27_deltanet_update_avx2, VP).value, C.cast(R.vx27_deltanet_retrieve_avx2, VP).value)

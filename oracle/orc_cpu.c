@@ -157,12 +157,21 @@ static void orc_retrieve_avx2(const float *S, const float *q, float *o, int hd) 
     for (int c = 0; c < hd / 8; c++) _mm256_storeu_ps(o + 8 * c, acc[c]);
 }
 
+void orc_update_avx2_pub(float *S, const float *k, const float *v, float decay, int hd) {
+    orc_update_avx2(S, k, v, decay, hd);
+}
+void orc_retrieve_avx2_pub(const float *S, const float *q, float *o, int hd) {
+    orc_retrieve_avx2(S, q, o, hd);
+}
+
 typedef struct {
     int B, nv, hd, steps;
     float *S;
     const float *qn, *kn, *v;
     const double *beta, *decay;
     float *out;
+    orc_update_fn upd;
+    orc_retrieve_fn ret;
 } orc_avx2_args;
 
 static void orc_avx2_worker(void *arg, int tid, int n) {
@@ -175,18 +184,20 @@ static void orc_avx2_worker(void *arg, int tid, int n) {
             const size_t e = (size_t)t * units + u;
             const float *q = a->qn + e * hd, *k = a->kn + e * hd, *v = a->v + e * hd;
             const float dec = (float)a->decay[e], bt = (float)a->beta[e];
-            orc_retrieve_avx2(S, k, kv, hd);
+            a->ret(S, k, kv, hd);
             for (int c = 0; c < hd; c++) d[c] = bt * (v[c] - dec * kv[c]);
-            orc_update_avx2(S, k, d, dec, hd);
-            orc_retrieve_avx2(S, q, a->out + e * hd, hd);
+            a->upd(S, k, d, dec, hd);
+            a->ret(S, q, a->out + e * hd, hd);
         }
     }
 }
 
 double orc_dn_run_avx2(int B, int nv, int hd, int steps, int threads, float *S,
                        const float *qn, const float *kn, const float *v,
-                       const double *beta, const double *decay, float *out) {
-    orc_avx2_args a = {B, nv, hd, steps, S, qn, kn, v, beta, decay, out};
+                       const double *beta, const double *decay, float *out,
+                       orc_update_fn upd, orc_retrieve_fn ret) {
+    orc_avx2_args a = {B, nv, hd, steps, S, qn, kn, v, beta, decay, out,
+                       upd ? upd : orc_update_avx2, ret ? ret : orc_retrieve_avx2};
     const double t0 = orc_now();
     orc_tp_run(threads, orc_avx2_worker, &a);
     return orc_now() - t0;

@@ -25,6 +25,10 @@
  *   orc_dn_run (multi-token, batched; the DeltaNet prefill oracle) and
  *   orc_gqa_prefill (token-ordered GQA prefill) -> bit-exact against chains
  *     of the pinned per-token functions.
+ *   orc_update_avx2_pub / orc_retrieve_avx2_pub -> bit-exact against the
+ *     compiled reference's AVX2 outputs (simple_update fixture);
+ *     orc_dn_run_avx2 (a CPU timing baseline, not a checker) -> equal to a
+ *     chain of those two on one head.
  */
 #ifndef VX27_ORACLE_H
 #define VX27_ORACLE_H
@@ -177,12 +181,24 @@ typedef struct {
 } orc_dn_run_args;
 double orc_dn_run(const orc_dn_run_args *r);
 
-/* The reference AVX2 primitives composed into the gated delta rule
+/* The reference AVX2 primitives vx27_deltanet_update_avx2 /
+ * retrieve_avx2 (vx27_deltanet_avx2.c:6-45), restated: row r of S becomes
+ * fma(S, decay, k[r]*v); o accumulates fma(S_row, q[r], o) over rows. */
+void orc_update_avx2_pub(float *S, const float *k, const float *v, float decay, int hd);
+void orc_retrieve_avx2_pub(const float *S, const float *q, float *o, int hd);
+typedef void (*orc_update_fn)(float *S, const float *k, const float *v, float decay, int hd);
+typedef void (*orc_retrieve_fn)(const float *S, const float *q, float *o, int hd);
+
+/* The AVX2 primitives composed into the gated delta rule
  * (decay*retrieve(S,k) -> d=beta(v-kv) -> update(S,k,d,decay) -> retrieve(S,q)),
- * q/k/v already normalised.  Float arithmetic, FMA, as vx27_deltanet_avx2.c. */
+ * q/k/v already normalised.  Float arithmetic, FMA, as vx27_deltanet_avx2.c.
+ * upd/ret: the primitives to call -- the compiled reference's own
+ * vx27_deltanet_update_avx2 / retrieve_avx2 when given, else the
+ * restatement above. */
 double orc_dn_run_avx2(int B, int nv, int hd, int steps, int threads, float *S,
                        const float *qn, const float *kn, const float *v,
-                       const double *beta, const double *decay, float *out);
+                       const double *beta, const double *decay, float *out,
+                       orc_update_fn upd, orc_retrieve_fn ret);
 
 /* GQA decode for B sequences over caches with per-sequence key counts. */
 typedef struct {

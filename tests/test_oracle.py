@@ -166,6 +166,57 @@ def test_simple_update_golden(O):
     assert np.abs(g["o_avx2"] - g["o_ref"]).max() < 1e-4
 
 
+def test_avx2_primitives_golden(O):
+    """The restated AVX2 update/retrieve (the CPU-AVX2 baseline's
+    primitives) are bit-exact to the compiled reference's
+    vx27_deltanet_update_avx2 / retrieve_avx2 outputs."""
+    g = golden("simple_update")
+    S = g["S0"].copy()
+    O.lib().orc_update_avx2_pub(S.reshape(-1), g["k"], g["v"], 0.9, 128)
+    o = np.empty(128, np.float32)
+    O.lib().orc_retrieve_avx2_pub(S.reshape(-1), g["q"], o, 128)
+    assert np.array_equal(S, g["S_avx2"]) and np.array_equal(o, g["o_avx2"])
+
+
+def test_avx2_run_is_the_primitive_chain(O):
+    """orc_dn_run_avx2 (2 heads x 5 steps, 2 threads) equals the chain
+    retrieve(S,k) -> d = beta (v - decay kv) -> update(S,k,d,decay) ->
+    retrieve(S,q) of the pinned primitives; with the compiled reference's
+    own primitives (where oracle/_ref is built) the run is the same bit for
+    bit."""
+    r = np.random.default_rng(5)
+    H, T, hd = 2, 5, 128
+    q = r.standard_normal((T, H, hd), dtype=np.float32)
+    k = r.standard_normal((T, H, hd), dtype=np.float32) / np.float32(11.3)
+    v = r.standard_normal((T, H, hd), dtype=np.float32)
+    beta = r.uniform(0.1, 0.9, (T, H))
+    decay = r.uniform(0.5, 1.0, (T, H))
+    S0 = r.standard_normal((H, hd, hd), dtype=np.float32) * np.float32(0.02)
+    S = S0.copy()
+    out = np.empty((T, H, hd), np.float32)
+    O.lib().orc_dn_run_avx2(1, H, hd, T, 2, S.reshape(-1), q.reshape(-1), k.reshape(-1), v.reshape(-1),
+                            beta.reshape(-1), decay.reshape(-1), out.reshape(-1), None, None)
+    Sw = S0.copy()
+    for t in range(T):
+        for h in range(H):
+            kv = np.empty(hd, np.float32)
+            O.lib().orc_retrieve_avx2_pub(Sw[h].reshape(-1), k[t, h], kv, hd)
+            dec, bt = np.float32(decay[t, h]), np.float32(beta[t, h])
+            dd = (bt * (v[t, h] - dec * kv)).astype(np.float32)
+            O.lib().orc_update_avx2_pub(Sw[h].reshape(-1), k[t, h], dd, dec, hd)
+            o = np.empty(hd, np.float32)
+            O.lib().orc_retrieve_avx2_pub(Sw[h].reshape(-1), q[t, h], o, hd)
+            assert np.array_equal(o, out[t, h]), (t, h)
+    assert np.array_equal(Sw, S)
+    upd, ret = O.ref_avx2_fns()
+    if upd is not None:
+        S2 = S0.copy()
+        out2 = np.empty_like(out)
+        O.lib().orc_dn_run_avx2(1, H, hd, T, 2, S2.reshape(-1), q.reshape(-1), k.reshape(-1), v.reshape(-1),
+                                beta.reshape(-1), decay.reshape(-1), out2.reshape(-1), upd, ret)
+        assert np.array_equal(out2, out) and np.array_equal(S2, S)
+
+
 # ------------------------------------------------------------- GQA pieces
 def test_rmsnorm_golden(O):
     g = golden("gqa")
