@@ -466,28 +466,41 @@ def _time_calls(ctx, fn, kernels, iters):
     return wall * 1e6, per
 
 
+DNP_KERNELS = ("dnp_glue_in", "dnp_conv_state", "dnp_prep3", "dnp_scan3", "dnp_prep", "dnp_scan", "dnp_out_gate")
+
+
+def dn_prefill_flops(T, H, hd=128, C_=64):
+    """Algorithmic flops of the chunked form: H (T/C) (10 C^2 d + 6 C d^2 + 2 C^3 / 3)."""
+    return H * (T // C_) * (10 * C_ * C_ * hd + 6 * C_ * hd * hd + 2 * C_ ** 3 / 3)
+
+
 def bench_dn_prefill(ctx, T=4096, iters=20, cpu=True):
-    """Chunked Gated DeltaNet prefill: one T-token prompt, 16 heads of 128."""
+    """Chunked Gated DeltaNet prefill: one T-token prompt, 16 heads of 128,
+    bf16 q/k/v in: the default split-precision products, and the bf16 form
+    (VX27_DN_BF16) beside it."""
     from vx27_amd import lib as L, workloads as W
     d = W.dn_prefill(B=1, T=T)
-    H, hd, C_ = 16, 128, 64
+    H, hd = 16, 128
     bufs = {k: ctx.put(d[k]) for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "S0")}
     ob = ctx.buf(T * H * hd * 4)
-    desc = L.DnPrefillDesc(1, T, H, H, hd, 0, bufs["S0"].ptr, bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr,
-                           bufs["a"].ptr, bufs["b"].ptr, bufs["A_log"].ptr, bufs["dt_bias"].ptr, ob.ptr)
-
-    def run():
-        L.check(L.lib().vx27_hip_dn_prefill(ctx.h, C.byref(desc)), "dn_prefill")
-    for _ in range(3):
-        run()
-    wall_us, per = _time_calls(ctx, run, ("dnp_prep", "dnp_scan"), iters)
-    k_us = sum(per.values())
-    flops = H * (T // C_) * (10 * C_ * C_ * hd + 6 * C_ * hd * hd + 2 * C_ ** 3 / 3)
+    flops = dn_prefill_flops(T, H)
     nbytes = T * H * hd * 2 * 3 + T * H * 8 + T * H * hd * 4 + 2 * H * hd * hd * 4
-    res = {"workload": f"dn_prefill B=1 T={T} heads=16 chunk=64", "us_per_call": wall_us,
-           "kernel_us": k_us, "kernels_us": per, "tokens_per_s": T / (k_us / 1e6),
-           "alg_flops": flops, "mfma_frac": flops / (k_us / 1e6) / MFMA_BF16_PEAK,
-           "alg_bytes": nbytes, "hbm_frac": nbytes / (k_us / 1e6) / HBM_PEAK}
+    res = {"workload": f"dn_prefill B=1 T={T} heads=16 chunk=64 (split-precision products)",
+           "alg_flops": flops, "alg_bytes": nbytes}
+    for tag, flags in (("", 0), ("bf16_", L.DN_BF16)):
+        desc = L.DnPrefillDesc(1, T, H, H, hd, flags, bufs["S0"].ptr, bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr,
+                               bufs["a"].ptr, bufs["b"].ptr, bufs["A_log"].ptr, bufs["dt_bias"].ptr, ob.ptr)
+
+        def run():
+            L.check(L.lib().vx27_hip_dn_prefill(ctx.h, C.byref(desc)), "dn_prefill")
+        for _ in range(3):
+            run()
+        wall_us, per = _time_calls(ctx, run, DNP_KERNELS, iters)
+        per = {k: v for k, v in per.items() if v > 0}
+        k_us = sum(per.values())
+        res.update({tag + "us_per_call": wall_us, tag + "kernel_us": k_us, tag + "kernels_us": per,
+                    tag + "tokens_per_s": T / (k_us / 1e6), tag + "mfma_frac": flops / (k_us / 1e6) / MFMA_BF16_PEAK,
+                    tag + "hbm_frac": nbytes / (k_us / 1e6) / HBM_PEAK})
     if cpu:
         from gpu_common import oracle_dn
         seq = {k: np.ascontiguousarray(np.swapaxes(W.bf16_to_f32(d[k]), 0, 1)) for k in ("q", "k", "v")}
@@ -500,6 +513,41 @@ def bench_dn_prefill(ctx, T=4096, iters=20, cpu=True):
     for b in bufs.values():
         b.free()
     ob.free()
+    return res
+
+
+def bench_dn_prefill_glue(ctx, T=4096, iters=10):
+    """The DeltaNet branch of vx27_qlayer_batch for one T-token prompt at
+    the real layer's shape (16 QK / 48 V heads): conv over 10240 channels,
+    rmsn(1+w) + l2 pre-norms, the chunked core (split precision), gated
+    output norm."""
+    from vx27_amd import lib as L, workloads as W
+    nqk, nv, hd = 16, 48, 128
+    d = W.dn_prefill_glue(B=1, T=T, nqk=nqk, nv=nv)
+    bufs = {k: ctx.put(d[k]) for k in ("x", "a", "b", "A_log", "dt_bias", "S0", "conv0", "conv_w_bf16", "norm_w",
+                                       "z")}
+    ob = ctx.buf(T * nv * hd * 4)
+    desc = L.DnPrefillDesc()
+    desc.B, desc.T, desc.nqk, desc.nv, desc.hd, desc.flags = 1, T, nqk, nv, hd, 15
+    desc.S, desc.out, desc.a, desc.b = bufs["S0"].ptr, ob.ptr, bufs["a"].ptr, bufs["b"].ptr
+    desc.A_log, desc.dt_bias, desc.x, desc.conv_state = bufs["A_log"].ptr, bufs["dt_bias"].ptr, bufs["x"].ptr, \
+        bufs["conv0"].ptr
+    desc.conv_w, desc.conv_w_dtype, desc.norm_w, desc.z = bufs["conv_w_bf16"].ptr, L.BF16, bufs["norm_w"].ptr, \
+        bufs["z"].ptr
+
+    def run():
+        L.check(L.lib().vx27_hip_dn_prefill(ctx.h, C.byref(desc)), "dn_prefill")
+    for _ in range(2):
+        run()
+    wall_us, per = _time_calls(ctx, run, DNP_KERNELS, iters)
+    per = {k: v for k, v in per.items() if v > 0}
+    k_us = sum(per.values())
+    flops = dn_prefill_flops(T, nv)
+    res = {"workload": f"dn_prefill with conv, pre-norms, gated norm: B=1 T={T} nqk=16 nv=48",
+           "us_per_call": wall_us, "kernel_us": k_us, "kernels_us": per, "tokens_per_s": T / (k_us / 1e6),
+           "alg_flops": flops, "mfma_frac": flops / (k_us / 1e6) / MFMA_BF16_PEAK}
+    for b in list(bufs.values()) + [ob]:
+        b.free()
     return res
 
 
@@ -575,6 +623,7 @@ def main():
                 "c3": lambda: {f"c3_dn_conv_B{B}": bench_dn_conv(ctx, 256, 8, B=B, cpu=cpu and B == 64)
                                for B in (1, 4, 16, 64)},
                 "c4": lambda: {"c4a_dn_prefill_T4096": bench_dn_prefill(ctx, cpu=cpu),
+                               "c4a_dn_prefill_layer_T4096": bench_dn_prefill_glue(ctx),
                                "c4b_gqa_prefill_T4096": bench_gqa_prefill(ctx, cpu=cpu)}}
         print(json.dumps({"only": args.only, "extra": runs[args.only]()}), flush=True)
         ctx.close()
@@ -623,7 +672,12 @@ def main():
         r = bench_dn_prefill(ctx, cpu=cpu)
         extra["c4a_dn_prefill_T4096"] = r
         log(f"  dn_prefill: {r['kernel_us']:.1f} us ({r['tokens_per_s']:.3g} tok/s), "
-            f"MFMA {100 * r['mfma_frac']:.1f}%, HBM {100 * r['hbm_frac']:.1f}%  {r['kernels_us']}")
+            f"MFMA {100 * r['mfma_frac']:.1f}%, HBM {100 * r['hbm_frac']:.1f}%  {r['kernels_us']}; bf16 products "
+            f"{r['bf16_kernel_us']:.1f} us")
+        r = bench_dn_prefill_glue(ctx)
+        extra["c4a_dn_prefill_layer_T4096"] = r
+        log(f"  dn_prefill layer (nv=48, glue): {r['kernel_us']:.1f} us, MFMA {100 * r['mfma_frac']:.1f}%  "
+            f"{r['kernels_us']}")
         r = bench_gqa_prefill(ctx, cpu=cpu)
         extra["c4b_gqa_prefill_T4096"] = r
         log(f"  gqa_prefill: {r['kernel_us']:.1f} us ({r['tokens_per_s']:.3g} tok/s), "

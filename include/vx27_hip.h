@@ -36,10 +36,12 @@ typedef struct vx27_hip_ctx vx27_hip_ctx;
  * init convention (int status + caller message buffer, vx27_gpu_reg.h:9). */
 int vx27_hip_open(vx27_hip_ctx **ctx, int device, char *err, size_t errlen);
 void vx27_hip_close(vx27_hip_ctx *ctx);
-/* Waits for the context stream.  Also returns -1 if a GQA decode call since
- * the last sync was given a position outside its KV cache (pos < 0 or
- * pos >= L: the kernels clamp it so no access leaves the cache, and flag it
- * for this call to report; that call's outputs are undefined). */
+/* Waits for the context stream.  Also returns -1 if a call since the last
+ * sync was given a device-side index outside its range: a GQA decode
+ * position outside its KV cache (pos < 0 or pos >= L: the kernels clamp it
+ * so no access leaves the cache) or a vx27_hip_dn_commit index past its
+ * checkpoints (nothing is copied for it).  That call's outputs are
+ * undefined. */
 int vx27_hip_sync(vx27_hip_ctx *ctx);
 /* Use a caller stream (hipStream_t) for subsequent calls; NULL restores the
  * context's own stream. */
@@ -133,25 +135,70 @@ typedef struct {
  * and write S once per call. */
 int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d);
 
-/* DeltaNet prefill: T tokens of B sequences through step_exact semantics
- * (vx27_deltanet.c:71-102 token by token, as vx27_qlayer_batch applies it,
- * vx27_qfwd.c:249-313), computed in chunks of 64 tokens with bf16 MFMA
- * products and the fp32 state carried between chunks.  q and k are
- * l2-normalised (and q scaled by 1/sqrt(hd)) inside, as step_exact does.
- * Accuracy is that of bf16 products (not the fp32 recurrence's). */
+/* DeltaNet prefill: T tokens of each of B sequences, in order, as
+ * vx27_qlayer_batch runs the DeltaNet branch token by token
+ * (vx27_qfwd.c:276-308): optional conv with carried state, optional
+ * rmsn(1+w) + l2norm pre-norm, step_exact (vx27_deltanet.c:71-102, which
+ * l2-normalises q,k and scales q again), optional gated output norm, and
+ * optional per-token state checkpoints (Sckpt/Cckpt, vx27_qfwd.c:306-307).
+ * The flags are the decode's (VX27_DN_CONV, _PRE_RMS, _PRE_L2, _OUT_GATE).
+ *
+ * Two algorithms:
+ *   chunked (default): the chunked WY form over chunks of 64 tokens, the
+ *     fp32 state carried between chunks, the chunk products on bf16 MFMA
+ *     with every operand split into a bf16 pair hi + lo (hi*hi + lo*hi +
+ *     hi*lo: ~16 significand bits per operand, results within ~1e-5
+ *     relative of the fp32 recurrence); the glue stages run in fp32 and
+ *     hand q, k, v over as such pairs.  VX27_DN_BF16 uses single bf16
+ *     operands instead (about 2x faster, bf16 accuracy).
+ *   exact (VX27_DN_EXACT, or whenever a checkpoint is asked for): the
+ *     decode kernels' fp32 recurrence token by token, the reference's own
+ *     arithmetic (bit-identical to vx27_hip_dn_decode called token by
+ *     token when checkpoints are written).  Meant for short windows such as
+ *     an MTP verify batch (the reference's batch is at most 8 tokens).
+ * Inputs are [B][T][...] (token t of sequence b at row b*T + t). */
+#define VX27_DN_EXACT 16u
+#define VX27_DN_BF16 32u
+
 typedef struct {
     int B, T;
     int nqk, nv;    /* value head vh uses QK head vh*nqk/nv; nv a multiple of nqk */
     int hd;         /* 128 */
-    unsigned flags; /* 0 */
+    unsigned flags; /* VX27_DN_CONV | _PRE_RMS | _PRE_L2 | _OUT_GATE | _EXACT | _BF16 */
     float *S;       /* [B][nv][hd][hd] fp32: initial state in, final state out */
-    const uint16_t *q, *k;       /* bf16 [B][T][nqk][hd] */
-    const uint16_t *v;           /* bf16 [B][T][nv][hd] */
+    /* without VX27_DN_CONV: bf16 q,k [B][T][nqk][hd], v [B][T][nv][hd] */
+    const uint16_t *q, *k;
+    const uint16_t *v;
     const float *a, *b;          /* [B][T][nv] gate projections */
     const float *A_log, *dt_bias;/* [nv] */
     float *out;                  /* [B][T][nv][hd] */
+    /* VX27_DN_CONV: fp32 projection output x [B][T][C], C = 2*nqk*hd + nv*hd,
+     * channels q|k|v; the conv state [B][C][3] (oldest first) is read and
+     * left as after token T-1; conv_w [C][4] as in vx27_dn_desc */
+    const float *x;
+    float *conv_state;
+    const void *conv_w;
+    int conv_w_dtype;
+    const float *norm_w;         /* [hd] (PRE_RMS uses 1+w, OUT_GATE uses w) */
+    const float *z;              /* [B][T][nv][hd] (OUT_GATE) */
+    /* optional checkpoints (either selects the exact algorithm):
+     * S_ckpt [B][T][nv][hd][hd] the state after each token,
+     * conv_ckpt [B][T][C][3] the conv state after each token (VX27_DN_CONV) */
+    float *S_ckpt;
+    float *conv_ckpt;
 } vx27_dn_prefill_desc;
 int vx27_hip_dn_prefill(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d);
+
+/* Make checkpoint m[b] of sequence b its live state (the device form of
+ * vx27_engine_commit_ckpt, vx27_run.c:250-255: a partial commit after a
+ * verify batch, the drafts past m rejected).  S [B][nv][hd][hd] and
+ * conv_state [B][C][3] take S_ckpt[b][m[b]] and conv_ckpt[b][m[b]] (layouts
+ * of vx27_dn_prefill_desc, T checkpoints per sequence); m is a device int
+ * array [B]; m[b] < 0 leaves sequence b unchanged, m[b] >= T is an error
+ * flagged like a position outside the cache (reported by vx27_hip_sync).
+ * Either checkpoint array may be NULL (its state is then not touched). */
+int vx27_hip_dn_commit(vx27_hip_ctx *ctx, int B, int T, int nv, int hd, int C, const int *m,
+                       const float *S_ckpt, const float *conv_ckpt, float *S, float *conv_state);
 
 /* ---------------------------------------------------------- GQA decode */
 /* KV cache format (bf16), for B sequences x n_kv heads x L positions, hd 256:

@@ -34,7 +34,7 @@ int main(void) {
         REF(vx27_hip_prof_enable), REF(vx27_hip_prof_read), REF(vx27_hip_default_ctx), REF(vx27_hip_enable),
         REF(vx27_hip_disable), REF(vx27_hip_enabled), REF(vx27_hip_set_error_mode), REF(vx27_hip_alloc),
         REF(vx27_hip_free), REF(vx27_hip_h2d), REF(vx27_hip_d2h), REF(vx27_hip_d2d), REF(vx27_hip_memset),
-        REF(vx27_hip_dn_decode), REF(vx27_hip_dn_prefill), REF(vx27_hip_gqa_decode), REF(vx27_hip_gqa_decode_noalloc), REF(vx27_hip_gqa_prefill),
+        REF(vx27_hip_dn_decode), REF(vx27_hip_dn_prefill), REF(vx27_hip_dn_commit), REF(vx27_hip_gqa_decode), REF(vx27_hip_gqa_decode_noalloc), REF(vx27_hip_gqa_prefill),
         REF(vx27_hip_kv_write), REF(vx27_hip_kv_read), REF(vx27_hip_rope_table), REF(vx27_hip_gemv_bf16),
         REF(vx27_hip_pack_weights_bf16), REF(vx27_hip_dn_layer_decode), REF(vx27_hip_gqa_layer_decode),
         REF(vx27_hip_pack_bytes), REF(vx27_hip_pack_x), REF(vx27_hip_advance_pos), REF(vx27_hip_graph_begin),

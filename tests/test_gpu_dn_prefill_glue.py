@@ -1,0 +1,194 @@
+"""GPU parity of the DeltaNet prefill with the glue of vx27_qlayer_batch
+(vx27_qfwd.c:276-308): conv with carried state, rmsn(1+w) + l2norm pre-norm
+(then step_exact's own normalisation: the double normalisation), gated output
+norm, per-token state checkpoints, and the partial commit of
+vx27_engine_commit_ckpt (vx27_run.c:250-255).
+
+Oracle: orc_dn_run with the same flags (the restated vx27_qlayer glue,
+pinned bit-exact to the compiled reference's vx27_qlayer), fed the same fp32
+inputs in token order.
+Bars: the exact path (fp32 recurrence token by token) 1e-5; the chunked path
+(q, k, v enter bf16 MFMA products) the bf16 bar 2e-2 + 1e-2|ref| and max|d|
+<= 2% of max|ref|; conv states bit-exact (they are copies of inputs); the
+checkpointed path bit-exact against vx27_hip_dn_decode called token by
+token."""
+import ctypes as C
+
+import numpy as np
+import pytest
+
+from gpu_common import maxabs, oracle_dn, say
+
+pytestmark = pytest.mark.gpu
+
+ALL = 1 | 2 | 4 | 8   # CONV | PRE_RMS | PRE_L2 | OUT_GATE
+
+
+@pytest.fixture(scope="module")
+def ctx():
+    from vx27_amd import lib as L
+    c = L.Ctx(0)
+    yield c
+    c.close()
+
+
+def run_prefill(ctx, d, nqk, flags, ckpt=False, bf16_qkv=None):
+    """vx27_hip_dn_prefill on workload d (dn_prefill_glue layout); returns
+    dict(out, S, conv[, S_ckpt, conv_ckpt])."""
+    from vx27_amd import lib as L
+    B, T, C_ = d["x"].shape
+    nv = d["a"].shape[2]
+    hd = 128
+    keep = []
+
+    def put(a):
+        b = ctx.put(np.ascontiguousarray(a))
+        keep.append(b)
+        return b.ptr
+    Sd, cd = ctx.put(d["S0"]), ctx.put(d["conv0"])
+    ob = ctx.buf(B * T * nv * hd * 4)
+    desc = L.DnPrefillDesc()
+    desc.B, desc.T, desc.nqk, desc.nv, desc.hd, desc.flags = B, T, nqk, nv, hd, flags
+    desc.S, desc.out = Sd.ptr, ob.ptr
+    desc.a, desc.b, desc.A_log, desc.dt_bias = put(d["a"]), put(d["b"]), put(d["A_log"]), put(d["dt_bias"])
+    if flags & L.DN_CONV:
+        desc.x, desc.conv_state, desc.conv_w, desc.conv_w_dtype = put(d["x"]), cd.ptr, put(d["conv_w_bf16"]), L.BF16
+    else:
+        desc.q, desc.k, desc.v = (put(a) for a in bf16_qkv)
+    desc.norm_w, desc.z = put(d["norm_w"]), put(d["z"])
+    sk = ck = None
+    if ckpt:
+        sk = ctx.buf(B * T * nv * hd * hd * 4)
+        ck = ctx.buf(B * T * C_ * 3 * 4)
+        desc.S_ckpt, desc.conv_ckpt = sk.ptr, ck.ptr
+    L.check(L.lib().vx27_hip_dn_prefill(ctx.h, C.byref(desc)), "dn_prefill")
+    ctx.sync()
+    res = {"out": ob.download((B, T, nv, hd), np.float32), "S": Sd.download(d["S0"].shape, np.float32),
+           "conv": cd.download(d["conv0"].shape, np.float32)}
+    if ckpt:
+        res["S_ckpt"] = sk.download((B, T, nv, hd, hd), np.float32)
+        res["conv_ckpt"] = ck.download((B, T, C_, 3), np.float32)
+        for bb in (sk, ck):
+            bb.free()
+    for bb in keep + [Sd, cd, ob]:
+        bb.free()
+    return res
+
+
+def oracle(d, nqk, flags):
+    """orc_dn_run over the prompt in token order; returns (out [B][T][nv][hd], S, conv)."""
+    B, T, _ = d["x"].shape
+    nv = d["a"].shape[2]
+    seq = {k: np.ascontiguousarray(np.swapaxes(d[k], 0, 1)) for k in ("x", "a", "b", "z")}
+    seq.update({k: d[k] for k in ("S0", "conv0", "conv_w", "A_log", "dt_bias", "norm_w")})
+    out, S, conv, secs = oracle_dn(seq, flags, B, nqk, nv, T)
+    return np.swapaxes(out, 0, 1), S, conv
+
+
+def check_bf16(got, ref, tag):
+    err = np.abs(got.astype(np.float64) - ref)
+    lim = 2e-2 + 1e-2 * np.abs(ref)
+    big = np.abs(ref).max()
+    say(f"  {tag}: max|d|={err.max():.3e} max|ref|={big:.3f} (d/limit {float((err / lim).max()):.3f}, "
+        f"d/scale {err.max() / (0.02 * big):.3f})")
+    assert np.all(np.isfinite(got))
+    assert np.all(err <= lim) and err.max() <= 0.02 * big, tag
+
+
+def test_dn_prefill_glue_chunked_4096(ctx):
+    """The real layer's shape (nqk 16, nv 48), one 4096-token prompt, every
+    glue stage, chunked algorithm."""
+    from vx27_amd import workloads as W
+    d = W.dn_prefill_glue(B=1, T=4096, nqk=16, nv=48)
+    say("dn prefill glue: B=1 T=4096 nqk=16 nv=48 all stages, chunked")
+    g = run_prefill(ctx, d, 16, ALL)
+    ref, S, conv = oracle(d, 16, ALL)
+    check_bf16(g["out"], ref, "out")
+    eS = maxabs(g["S"], S)
+    say(f"  final state max|d|={eS:.3e} (max|S|={np.abs(S).max():.3f})")
+    check_bf16(g["S"], S, "final state")
+    assert np.array_equal(g["conv"], conv)
+
+
+@pytest.mark.parametrize("flags", [1 | 4, 2 | 4 | 8, 1 | 2 | 4])
+def test_dn_prefill_glue_chunked_flags(ctx, flags):
+    """Subsets of the stages (with and without conv), ragged T, nv 32."""
+    from vx27_amd import workloads as W
+    d = W.dn_prefill_glue(B=2, T=333, nqk=16, nv=32, config=7)
+    bq = None
+    if not flags & 1:   # bf16 q, k, v inputs (the conv output given)
+        x = W.bf16_to_f32(W.bf16_bits(d["x"]))
+        d["x"] = x
+        qd = 16 * 128
+        bq = (W.bf16_bits(x[..., :qd]).reshape(2, 333, 16, 128), W.bf16_bits(x[..., qd:2 * qd]).reshape(2, 333, 16, 128),
+              W.bf16_bits(x[..., 2 * qd:]).reshape(2, 333, 32, 128))
+    g = run_prefill(ctx, d, 16, flags, bf16_qkv=bq)
+    if not flags & 1:
+        # the oracle's conv-less input is q|k|v per token; orc_dn_run reads
+        # q, k, v separately, so feed x's slices
+        from gpu_common import oracle_dn as od
+        seq = {"q": np.ascontiguousarray(np.swapaxes(x[..., :qd], 0, 1)),
+               "k": np.ascontiguousarray(np.swapaxes(x[..., qd:2 * qd], 0, 1)),
+               "v": np.ascontiguousarray(np.swapaxes(x[..., 2 * qd:], 0, 1))}
+        seq.update({k: np.ascontiguousarray(np.swapaxes(d[k], 0, 1)) for k in ("a", "b", "z")})
+        seq.update({k: d[k] for k in ("S0", "A_log", "dt_bias", "norm_w")})
+        ref, S, _, _ = od(seq, flags, 2, 16, 32, 333)
+        ref = np.swapaxes(ref, 0, 1)
+    else:
+        ref, S, conv = oracle(d, 16, flags)
+        assert np.array_equal(g["conv"], conv)
+    check_bf16(g["out"], ref, f"flags={flags}")
+    check_bf16(g["S"], S, f"flags={flags} final state")
+
+
+def test_dn_prefill_exact_path(ctx):
+    """VX27_DN_EXACT: the fp32 recurrence token by token (nqk 16, nv 48,
+    every stage), B = 2, T = 100: within 1e-5 of the oracle."""
+    from vx27_amd import lib as L, workloads as W
+    d = W.dn_prefill_glue(B=2, T=100, nqk=16, nv=48, config=8)
+    g = run_prefill(ctx, d, 16, ALL | L.DN_EXACT)
+    ref, S, conv = oracle(d, 16, ALL)
+    eo, es = maxabs(g["out"], ref), maxabs(g["S"], S)
+    say(f"  exact: max|d out|={eo:.3e} max|d S|={es:.3e}")
+    assert eo <= 1e-5 and es <= 1e-5
+    assert np.array_equal(g["conv"], conv)
+
+
+def test_dn_prefill_checkpoints_and_commit(ctx):
+    """A verify window of 8 tokens with per-token checkpoints (the
+    reference's Sckpt/Cckpt): equal bit for bit to vx27_hip_dn_decode called
+    token by token; then vx27_hip_dn_commit makes checkpoint m[b] live."""
+    from vx27_amd import lib as L, mixers as M, workloads as W
+    B, T, nqk, nv, hd = 2, 8, 16, 48, 128
+    d = W.dn_prefill_glue(B=B, T=T, nqk=nqk, nv=nv, config=9)
+    C_ = d["x"].shape[2]
+    g = run_prefill(ctx, d, nqk, ALL, ckpt=True)
+    # token-by-token decode of the same inputs
+    lay = M.DeltaNetLayer(ctx, B, nqk, nv, d["A_log"], d["dt_bias"], norm_w=d["norm_w"], conv_w=d["conv_w_bf16"],
+                          conv_w_dtype=L.BF16, S0=d["S0"], conv0=d["conv0"])
+    for t in range(T):
+        o = lay.decode(1, ALL, np.ascontiguousarray(d["a"][:, t][None]), np.ascontiguousarray(d["b"][:, t][None]),
+                       x=np.ascontiguousarray(d["x"][:, t][None]), z=np.ascontiguousarray(d["z"][:, t][None]))
+        assert np.array_equal(o[0], g["out"][:, t]), f"out token {t}"
+        assert np.array_equal(lay.state(), g["S_ckpt"][:, t]), f"S checkpoint {t}"
+        assert np.array_equal(lay.conv(), g["conv_ckpt"][:, t]), f"conv checkpoint {t}"
+    assert np.array_equal(lay.state(), g["S"]) and np.array_equal(lay.conv(), g["conv"])
+    ref, S, _ = oracle(d, nqk, ALL)
+    say(f"  checkpointed: bit-exact to the decode; max|d out| vs oracle {maxabs(g['out'], ref):.3e}")
+    assert maxabs(g["out"], ref) <= 1e-5 and maxabs(g["S"], S) <= 1e-5
+    # commit: sequence 0 keeps token 3's state, sequence 1 is left as is
+    Sd, cd = ctx.put(g["S"]), ctx.put(g["conv"])
+    sk, ck = ctx.put(g["S_ckpt"]), ctx.put(g["conv_ckpt"])
+    m = ctx.put(np.array([3, -1], np.int32))
+    L.check(L.lib().vx27_hip_dn_commit(ctx.h, B, T, nv, hd, C_, m.ptr, sk.ptr, ck.ptr, Sd.ptr, cd.ptr), "commit")
+    ctx.sync()
+    Sn, cn = Sd.download(g["S"].shape, np.float32), cd.download(g["conv"].shape, np.float32)
+    assert np.array_equal(Sn[0], g["S_ckpt"][0, 3]) and np.array_equal(cn[0], g["conv_ckpt"][0, 3])
+    assert np.array_equal(Sn[1], g["S"][1]) and np.array_equal(cn[1], g["conv"][1])
+    # an index past the window is reported, and nothing is copied for it
+    m.upload(np.array([T, 0], np.int32))
+    L.check(L.lib().vx27_hip_dn_commit(ctx.h, B, T, nv, hd, C_, m.ptr, sk.ptr, ck.ptr, Sd.ptr, cd.ptr), "commit")
+    with pytest.raises(L.HipError, match="outside"):
+        ctx.sync()
+    Sn = Sd.download(g["S"].shape, np.float32)
+    assert np.array_equal(Sn[0], g["S_ckpt"][0, 3]) and np.array_equal(Sn[1], g["S_ckpt"][1, 0])

@@ -72,6 +72,12 @@ constexpr unsigned VX_DN_QK_READY = 1u << 16;
 
 struct DnArgs {
     int B, nqk, nv, steps;
+    // per-token arrays (x, q, k, v, gates, ga/gb, z, out) hold token t of
+    // sequence b at index t * t_step + b * b_step (times the array's own
+    // stride): t_step = B, b_step = 1 is the decode layout [steps][B];
+    // t_step = 1, b_step = T the prefill layout [B][T].  0 means the decode
+    // layout.
+    int t_step, b_step;
     unsigned flags;
     int fused_conv;
     float *S;
@@ -96,6 +102,22 @@ struct DnArgs {
     // (the output norm then runs in a separate finish kernel)
     float *o_pre;
 };
+
+// Channel-parallel causal conv over `steps` tokens (dn_conv_kernel): one
+// thread per (b, c), the state carried in registers; act receives silu(conv).
+struct ConvArgs {
+    int B, C, steps, w_bf16;
+    float *state;         // [B][C][3], oldest first; left as after the last token
+    const void *w;
+    const float *x;
+    float *act;
+    int t_step, b_step;   // token (t, b) of x and act at row t * t_step + b * b_step
+    float *ckpt;          // optional: the state after each token, [rows][C][3] in the same row order
+};
+int vx_dn_conv(vx27_hip_ctx *ctx, const ConvArgs &ca);
+// (beta, exp(g_log)) of n gate inputs (vx27_deltanet_gate_params), value head e % nv
+int vx_dn_gates(vx27_hip_ctx *ctx, size_t n, int nv, const float *ga, const float *gb, const float *A_log,
+                const float *dt_bias, double2 *gates);
 
 // Launch the recurrence (one or more workgroups per (sequence, value head)).
 int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a);

@@ -121,7 +121,7 @@ __global__ __launch_bounds__(HD / CS * R) void dn_decode_kernel(DnArgs a) {
     const float qs = 1.0f / sqrtf((float)HD);
 
     for (int t = 0; t < a.steps; t++) {
-        const size_t sb = (size_t)t * a.B + b;
+        const size_t sb = (size_t)t * a.t_step + (size_t)b * a.b_step;
         const double2 gt = a.gates[sb * a.nv + vh];   // uniform address: scalar load
         // ---- activations of this token
         float qa = 0.0f, ka = 0.0f, va = 0.0f;
@@ -287,7 +287,7 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
                 const int qd = a.nqk * HD, C = 2 * qd + a.nv * HD;
                 const size_t chq = (size_t)g * HD + i, chk = (size_t)qd + g * HD + i,
                              chv = (size_t)2 * qd + (size_t)vh * HD + i;
-                const float *x = a.x + (size_t)b * C;
+                const float *x = a.x + (size_t)b * a.b_step * C;
                 float *cst = a.conv_state + (size_t)b * C * 3;
                 float wq[4], wk[4], wv[4], cq[3], ck[3], cv[3];
                 load_conv_w(a.conv_w, a.conv_bf16, chq, wq);
@@ -309,9 +309,10 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
                     cst[chv * 3 + t] = cv[t];
                 }
             } else {
-                qa[h] = a.q[(size_t)b * a.q_tok + (size_t)g * HD + i];
-                ka[h] = a.k[(size_t)b * a.k_tok + (size_t)g * HD + i];
-                va[h] = a.v[(size_t)b * a.v_tok + (size_t)vh * HD + i];
+                const size_t bs = (size_t)b * a.b_step;
+                qa[h] = a.q[bs * a.q_tok + (size_t)g * HD + i];
+                ka[h] = a.k[bs * a.k_tok + (size_t)g * HD + i];
+                va[h] = a.v[bs * a.v_tok + (size_t)vh * HD + i];
             }
         }
     }
@@ -319,8 +320,8 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
     float z0 = 0.f, z1 = 0.f, w0 = 1.f, w1 = 1.f;
     if (wave == 0 && (gate || !(a.flags & VX_DN_QK_READY))) {
         if (gate) {
-            z0 = a.z[(size_t)b * a.z_tok + (size_t)vh * HD + lane];
-            z1 = a.z[(size_t)b * a.z_tok + (size_t)vh * HD + lane + 64];
+            z0 = a.z[(size_t)b * a.b_step * a.z_tok + (size_t)vh * HD + lane];
+            z1 = a.z[(size_t)b * a.b_step * a.z_tok + (size_t)vh * HD + lane + 64];
         }
         if (a.norm_w) {
             w0 = a.norm_w[lane];
@@ -329,11 +330,11 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
     }
     double beta, decay;
     if (a.gates) {
-        const double2 gt = a.gates[(size_t)b * a.nv + vh];   // uniform address: scalar load
+        const double2 gt = a.gates[(size_t)b * a.b_step * a.nv + vh];   // uniform address: scalar load
         beta = gt.x;
         decay = gt.y;
     } else {   // vx27_deltanet_gate_params (vx27_deltanet.c:65-69), decay = exp(g_log)
-        const size_t e = (size_t)b * a.nv + vh;
+        const size_t e = (size_t)b * a.b_step * a.nv + vh;
         beta = 1.0 / (1.0 + exp(-(double)a.gb[e]));
         decay = exp(-exp((double)a.A_log[vh]) * softplus_d((double)a.ga[e] + (double)a.dt_bias[vh]));
     }
@@ -481,8 +482,8 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
         f1 = ((f1 * is) * w1) * silu_f(z1);
     }
     if (a.out) {
-        a.out[(size_t)b * a.out_tok + (size_t)vh * HD + lane] = f0;
-        a.out[(size_t)b * a.out_tok + (size_t)vh * HD + lane + 64] = f1;
+        a.out[(size_t)b * a.b_step * a.out_tok + (size_t)vh * HD + lane] = f0;
+        a.out[(size_t)b * a.b_step * a.out_tok + (size_t)vh * HD + lane + 64] = f1;
     }
     if (a.out_packed) {
         vx_pack_store(a.out_packed, a.B, b, vh * HD + lane, f0);
@@ -501,21 +502,14 @@ __global__ __launch_bounds__(HD) void dn_out_gate(DnArgs a) {
     double so = (double)of * (double)of, unused = 0.0;
     block_sum2<2>(so, unused, s_red);
     const float is = 1.0f / sqrtf((float)(so / HD) + 1e-6f);
-    const float zz = a.z[(size_t)b * a.z_tok + (size_t)vh * HD + col];
+    const float zz = a.z[(size_t)b * a.b_step * a.z_tok + (size_t)vh * HD + col];
     of = ((of * is) * a.norm_w[col]) * silu_f(zz);
-    if (a.out) a.out[(size_t)b * a.out_tok + (size_t)vh * HD + col] = of;
+    if (a.out) a.out[(size_t)b * a.b_step * a.out_tok + (size_t)vh * HD + col] = of;
     if (a.out_packed) vx_pack_store(a.out_packed, a.B, b, vh * HD + col, of);
 }
 
 // Channel-parallel causal conv over `steps` tokens: one thread per (b, c),
 // state carried in registers; act [steps][B][C] receives silu(conv).
-struct ConvArgs {
-    int B, C, steps, w_bf16;
-    float *state;
-    const void *w;
-    const float *x;
-    float *act;
-};
 __global__ __launch_bounds__(256) void dn_conv_kernel(ConvArgs a) {
     const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (id >= (size_t)a.B * a.C) return;
@@ -525,8 +519,13 @@ __global__ __launch_bounds__(256) void dn_conv_kernel(ConvArgs a) {
     float *sp = a.state + ((size_t)b * a.C + c) * 3;
     st[0] = sp[0]; st[1] = sp[1]; st[2] = sp[2];
     for (int t = 0; t < a.steps; t++) {
-        const size_t e = ((size_t)t * a.B + b) * a.C + c;
+        const size_t row = (size_t)t * a.t_step + (size_t)b * a.b_step;
+        const size_t e = row * a.C + c;
         a.act[e] = conv_step(st, w, a.x[e]);
+        if (a.ckpt) {
+            float *ck = a.ckpt + e * 3;
+            ck[0] = st[0]; ck[1] = st[1]; ck[2] = st[2];
+        }
     }
     sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
 }
@@ -540,7 +539,12 @@ bool vx_dn_single_step(const DnArgs &a) {
     return VX_DN_STEP && a.steps == 1 && ((uintptr_t)a.S & 15) == 0;
 }
 
-int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a) {
+int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a_in) {
+    DnArgs a = a_in;
+    if (a.t_step == 0 && a.b_step == 0) {   // decode layout [steps][B]
+        a.t_step = a.B;
+        a.b_step = 1;
+    }
     VX_REQUIRE(!a.fused_conv || a.nv == a.nqk, "dn recurrence: fused conv needs nv == nqk");
     // Spread few heads over the 256 CUs: split each head's columns over CS
     // workgroups (not with the fused conv, whose q/k channels one block owns,
@@ -646,7 +650,7 @@ extern "C" int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d) {
     if (sep_conv) {
         // shared q/k channels: convolve all channels first
         float *act = (float *)((char *)scr + gate_bytes + opre_bytes);
-        ConvArgs ca = {d->B, C, d->steps, a.conv_bf16, d->conv_state, d->conv_w, d->x, act};
+        ConvArgs ca = {d->B, C, d->steps, a.conv_bf16, d->conv_state, d->conv_w, d->x, act, d->B, 1, nullptr};
         const size_t nthr = (size_t)d->B * C;
         VX_LAUNCH(ctx, dn_conv_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), ca);
         a.q = act; a.k = act + qd; a.v = act + 2 * qd;
@@ -655,4 +659,17 @@ extern "C" int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d) {
     a.z_tok = (size_t)vd;
     a.out_tok = (size_t)vd;
     return vx_dn_recurrence(ctx, a);
+}
+
+int vx_dn_gates(vx27_hip_ctx *ctx, size_t n, int nv, const float *ga, const float *gb, const float *A_log,
+                const float *dt_bias, double2 *gates) {
+    VX_LAUNCH(ctx, dn_gate_kernel, dim3((unsigned)((n + 255) / 256)), dim3(256), (int)n, nv, ga, gb, A_log, dt_bias,
+              gates);
+    return 0;
+}
+
+int vx_dn_conv(vx27_hip_ctx *ctx, const ConvArgs &ca) {
+    const size_t nthr = (size_t)ca.B * ca.C;
+    VX_LAUNCH(ctx, dn_conv_kernel, dim3((unsigned)((nthr + 255) / 256)), dim3(256), ca);
+    return 0;
 }

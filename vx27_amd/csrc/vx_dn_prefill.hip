@@ -30,6 +30,8 @@
 // Operand tiles ([rows/16][k/32][64 lanes][8] bf16) follow the MFMA operand
 // layout of v_mfma_f32_16x16x32_bf16: lane (g = l/16, m = l%16) of an A tile
 // holds A[m][8g..8g+7]; a wave's tile is 1 KiB of contiguous memory.
+#include <algorithm>
+
 #include "vx_dn.h"
 #include "vx_lds.h"
 
@@ -559,7 +561,716 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
         for (int i = 0; i < 4; i++) Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + col] = S[r][i];
 }
 
+// ---- split precision (bf16x3) ----------------------------------------------
+// The default chunked form: every operand of the chunk products enters the
+// MFMAs as a pair of bf16 values, hi = bf16(x) and lo = bf16(x - hi), and
+// each product is hi*hi + lo*hi + hi*lo (the lo*lo term, ~2^-16 of the
+// product, is dropped): about 16 significand bits per operand, so the
+// chunked result stays within ~1e-5 of the fp32 recurrence instead of
+// bf16's ~1e-2.  Inputs q, k, v come as hi/lo pairs too (lo = NULL: the
+// inputs are exact in bf16).  The record holds each operand tile as a hi
+// tile and a lo tile.
+constexpr size_t X_NW = 0;                    // -W        hi, lo: 2 x [4][4][64][8] bf16
+constexpr size_t X_QE = X_NW + 2 * 16384;     // e^gam qn  hi, lo
+constexpr size_t X_KT = X_QE + 2 * 16384;     // Kt^T      hi, lo: 2 x [8][2][64][8]
+constexpr size_t X_P = X_KT + 2 * 16384;      // P         hi, lo: 2 x [4][2][64][8]
+constexpr size_t X_UT = X_P + 2 * 8192;       // Ut fp32 [4 rb][8 cs][64][4]
+constexpr size_t X_GC = X_UT + 32768;         // e^gam_C
+constexpr size_t XREC = X_GC + 256;
+
+struct Prep3Args {
+    int T, nqk, nv, NC;
+    const uint16_t *q, *k, *v;          // hi parts [B][T][nqk|nqk|nv][128] bf16
+    const uint16_t *ql, *kl, *vl;       // lo parts, or NULL
+    const float *a, *b;
+    const float *A_log, *dt_bias;
+    char *rec;                          // [B][nv][NC] records of XREC bytes
+};
+
+// bf16 hi and lo of 8 floats
+__device__ __forceinline__ void split8(const float *f, uint4 &hi, uint4 &lo) {
+    hi = pack8(f);
+    const uint16_t *h = (const uint16_t *)&hi;
+    float r[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) r[e] = f[e] - vx_bf16_to_f32(h[e]);
+    lo = pack8(r);
+}
+
+// LDS of dnp_prep3 (phases as dnp_prep's; every bf16 array has a lo twin)
+constexpr int X3_QH = 0;                                  // q rows hi -> P hi staging -> T fp32
+constexpr int X3_QL = X3_QH + CH * RP * 2;                // q rows lo -> P lo staging
+constexpr int X3_KH = X3_QL + CH * RP * 2;                // k rows hi -> V^T hi -> -W hi staging
+constexpr int X3_KL = X3_KH + HD * TP * 2;                // k rows lo -> V^T lo -> -W lo staging
+constexpr int X3_TH = X3_KL + HD * TP * 2;                // K^T hi
+constexpr int X3_TL = X3_TH + HD * TP * 2;                // K^T lo
+constexpr int X3_AS = X3_TL + HD * TP * 2;                // A fp32
+constexpr int X3_MT = X3_AS + CH * AP * 4;
+constexpr int X3_GAM = X3_MT + 3 * 256 * 4;
+constexpr int X3_SC = X3_GAM + CH * 8;
+constexpr int X3_TOTAL = X3_SC + 5 * CH * 4;
+static_assert(CH * RP * 2 <= HD * TP * 2, "k rows fit the V^T region");
+
+__global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
+    const int c = blockIdx.x, vh = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, m = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int qh = vh * p.nqk / p.nv;
+    const int t0 = c * CH;
+    const int nvalid = min(CH, p.T - t0);
+    const bool has_lo = p.ql != nullptr;
+
+    __shared__ __attribute__((aligned(16))) char smem[X3_TOTAL];
+    uint16_t *q_rows = (uint16_t *)(smem + X3_QH), *q_lo = (uint16_t *)(smem + X3_QL);
+    uint16_t *P_h = (uint16_t *)(smem + X3_QH), *P_l = (uint16_t *)(smem + X3_QL);   // [64][TP]
+    float *T_s = (float *)(smem + X3_QH);                                              // [64][64]
+    uint16_t *k_rows = (uint16_t *)(smem + X3_KH), *k_lo = (uint16_t *)(smem + X3_KL);
+    uint16_t *V_h = (uint16_t *)(smem + X3_KH), *V_l = (uint16_t *)(smem + X3_KL);   // [128][TP]
+    uint16_t *W_h = (uint16_t *)(smem + X3_KH), *W_l = (uint16_t *)(smem + X3_KL);   // [64][RP]
+    uint16_t *K_h = (uint16_t *)(smem + X3_TH), *K_l = (uint16_t *)(smem + X3_TL);   // [128][TP]
+    float *A_s = (float *)(smem + X3_AS);
+    float *M_t = (float *)(smem + X3_MT);
+    double *gam_s = (double *)(smem + X3_GAM);
+    float *beta_s = (float *)(smem + X3_SC), *eg_s = beta_s + CH, *egc_s = eg_s + CH;
+    float *iq_s = egc_s + CH, *ik_s = iq_s + CH;
+
+    // ---- phase 1: gates (wave 0); k, q, v rows (waves 1, 2, 3), hi and lo
+    if (wave == 0) {
+        double beta = 0.0, glog = 0.0;
+        if (lane < nvalid) {
+            const size_t e = ((size_t)b * p.T + t0 + lane) * p.nv + vh;
+            beta = 1.0 / (1.0 + exp(-(double)p.b[e]));
+            glog = -exp((double)p.A_log[vh]) * softplus_d((double)p.a[e] + (double)p.dt_bias[vh]);
+        }
+        double sc = glog;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const double o = __shfl_up(sc, off, 64);
+            if (lane >= off) sc += o;
+        }
+        const double sC = __shfl(sc, 63, 64);
+        gam_s[lane] = sc;
+        beta_s[lane] = (float)beta;
+        eg_s[lane] = (float)exp(sc);
+        egc_s[lane] = (float)exp(sC - sc);
+    }
+    uint4 raw[16], rawl[16];
+    if (wave >= 1) {
+        const size_t row = wave == 3 ? (((size_t)b * p.T + t0 + lane) * p.nv + vh) * HD
+                                     : (((size_t)b * p.T + t0 + lane) * p.nqk + qh) * HD;
+        const uint16_t *src = wave == 1 ? p.k : wave == 2 ? p.q : p.v;
+        const uint16_t *srl = wave == 1 ? p.kl : wave == 2 ? p.ql : p.vl;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            raw[j] = lane < nvalid ? *(const uint4 *)(src + row + 8 * j) : make_uint4(0u, 0u, 0u, 0u);
+            rawl[j] = (has_lo && lane < nvalid) ? *(const uint4 *)(srl + row + 8 * j) : make_uint4(0u, 0u, 0u, 0u);
+        }
+    }
+    if (wave == 1 || wave == 2) {
+        double ss = 0.0;   // of the value hi + lo (exact in double)
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+            const uint32_t l4[4] = {rawl[j].x, rawl[j].y, rawl[j].z, rawl[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                const double x0 = (double)vx_bf16_to_f32((uint16_t)w4[e]) + (double)vx_bf16_to_f32((uint16_t)l4[e]);
+                const double x1 = (double)vx_bf16_to_f32((uint16_t)(w4[e] >> 16)) +
+                                  (double)vx_bf16_to_f32((uint16_t)(l4[e] >> 16));
+                ss = ss + x0 * x0;
+                ss = ss + x1 * x1;
+            }
+        }
+        const float inv = 1.0f / sqrtf((float)ss + 1e-6f);   // l2norm, vx27_deltanet.c:51-56
+        uint16_t *rows = wave == 1 ? k_rows : q_rows, *rowl = wave == 1 ? k_lo : q_lo;
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            *(uint4 *)&rows[lane * RP + 8 * j] = raw[j];
+            *(uint4 *)&rowl[lane * RP + 8 * j] = rawl[j];
+        }
+        if (wave == 1) {
+            ik_s[lane] = inv;
+#pragma unroll
+            for (int j = 0; j < 16; j++) {
+                const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+                const uint32_t l4[4] = {rawl[j].x, rawl[j].y, rawl[j].z, rawl[j].w};
+#pragma unroll
+                for (int e = 0; e < 4; e++) {
+                    K_h[(8 * j + 2 * e) * TP + lane] = (uint16_t)w4[e];
+                    K_h[(8 * j + 2 * e + 1) * TP + lane] = (uint16_t)(w4[e] >> 16);
+                    K_l[(8 * j + 2 * e) * TP + lane] = (uint16_t)l4[e];
+                    K_l[(8 * j + 2 * e + 1) * TP + lane] = (uint16_t)(l4[e] >> 16);
+                }
+            }
+        } else {
+            iq_s[lane] = inv;
+        }
+    }
+    __syncthreads();
+
+    char *rec = p.rec + (((size_t)b * p.nv + vh) * p.NC + c) * XREC;
+    const double gamC = gam_s[CH - 1];
+    if (tid == 0) *(float *)(rec + X_GC) = (float)exp(gamC);
+    const float qscale = 1.0f / sqrtf((float)HD);
+
+    // ---- phase 2: K K^T and Q K^T (hi*hi + lo*hi + hi*lo); e^gam qn tiles
+    floatx4_t acck[4], accq[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+        acck[nb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+        accq[nb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+    }
+    const int rowA = wave * 16 + m;
+    const float qeA = eg_s[rowA] * (iq_s[rowA] * qscale);
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        const int d0 = 32 * ks + 8 * g;
+        const uint4 qa = *(const uint4 *)&q_rows[rowA * RP + d0], qal = *(const uint4 *)&q_lo[rowA * RP + d0];
+        const uint4 ka = *(const uint4 *)&k_rows[rowA * RP + d0], kal = *(const uint4 *)&k_lo[rowA * RP + d0];
+        {   // e^gam qn tile (row block wave, k-step ks), hi and lo
+            const uint16_t *qs = (const uint16_t *)&qa, *qsl = (const uint16_t *)&qal;
+            float f[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) f[e] = qeA * (vx_bf16_to_f32(qs[e]) + vx_bf16_to_f32(qsl[e]));
+            uint4 h, l;
+            split8(f, h, l);
+            *(uint4 *)(rec + X_QE + ((size_t)(wave * 4 + ks) * 64 + lane) * 16) = h;
+            *(uint4 *)(rec + X_QE + 16384 + ((size_t)(wave * 4 + ks) * 64 + lane) * 16) = l;
+        }
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) {
+            const bf16x8_t bk = as_bf16x8(*(const uint4 *)&k_rows[(nb * 16 + m) * RP + d0]);
+            acck[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka), bk, acck[nb], 0, 0, 0);
+            accq[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa), bk, accq[nb], 0, 0, 0);
+            if (has_lo) {
+                const bf16x8_t bkl = as_bf16x8(*(const uint4 *)&k_lo[(nb * 16 + m) * RP + d0]);
+                acck[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kal), bk, acck[nb], 0, 0, 0);
+                acck[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka), bkl, acck[nb], 0, 0, 0);
+                accq[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qal), bk, accq[nb], 0, 0, 0);
+                accq[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa), bkl, accq[nb], 0, 0, 0);
+            }
+        }
+    }
+    // Kt^T tiles (hi, lo): rows = key dims (8 blocks), k = tokens (2 steps); 4 per wave
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int tile = wave * 4 + j, rb = tile >> 1, ks = tile & 1;
+        const int i = rb * 16 + m, tb = 32 * ks + 8 * g;
+        const uint4 kr = *(const uint4 *)&K_h[i * TP + tb], krl = *(const uint4 *)&K_l[i * TP + tb];
+        const uint16_t *kv = (const uint16_t *)&kr, *kvl = (const uint16_t *)&krl;
+        float f[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++)
+            f[e] = (egc_s[tb + e] * ik_s[tb + e]) * (vx_bf16_to_f32(kv[e]) + vx_bf16_to_f32(kvl[e]));
+        uint4 h, l;
+        split8(f, h, l);
+        *(uint4 *)(rec + X_KT + ((size_t)tile * 64 + lane) * 16) = h;
+        *(uint4 *)(rec + X_KT + 16384 + ((size_t)tile * 64 + lane) * 16) = l;
+    }
+    __syncthreads();   // q and k rows are no longer read
+
+    // ---- phase 3: A (fp32), P hi/lo staging, V^T hi/lo
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int s = wave * 16 + 4 * g + i, r = nb * 16 + m;
+            const float ed = r <= s ? expf((float)(gam_s[s] - gam_s[r])) : 0.0f;
+            A_s[s * AP + r] = r < s ? beta_s[s] * ed * ((ik_s[s] * ik_s[r]) * acck[nb][i]) : 0.0f;
+            const float pv = ed * (((iq_s[s] * qscale) * ik_s[r]) * accq[nb][i]);
+            const uint16_t ph = vx_f32_to_bf16(pv);
+            P_h[s * TP + r] = ph;
+            P_l[s * TP + r] = vx_f32_to_bf16(pv - vx_bf16_to_f32(ph));
+        }
+    }
+    if (wave == 3) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
+            const uint32_t l4[4] = {rawl[j].x, rawl[j].y, rawl[j].z, rawl[j].w};
+#pragma unroll
+            for (int e = 0; e < 4; e++) {
+                V_h[(8 * j + 2 * e) * TP + lane] = (uint16_t)w4[e];
+                V_h[(8 * j + 2 * e + 1) * TP + lane] = (uint16_t)(w4[e] >> 16);
+                V_l[(8 * j + 2 * e) * TP + lane] = (uint16_t)l4[e];
+                V_l[(8 * j + 2 * e + 1) * TP + lane] = (uint16_t)(l4[e] >> 16);
+            }
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+        const size_t o = ((size_t)(wave * 2 + ks) * 64 + lane) * 16;
+        *(uint4 *)(rec + X_P + o) = *(const uint4 *)&P_h[rowA * TP + 32 * ks + 8 * g];
+        *(uint4 *)(rec + X_P + 8192 + o) = *(const uint4 *)&P_l[rowA * TP + 32 * ks + 8 * g];
+    }
+    __syncthreads();   // P staging is read out; the q region takes T
+
+    // ---- phase 4: T = (I + A)^-1 (as dnp_prep)
+    if (tid < 64) {
+        const int bi = tid >> 4, cc = tid & 15, o = 16 * bi;
+        float t[16];
+#pragma unroll
+        for (int r = 0; r < 16; r++) {
+            float acc = r == cc ? 1.0f : 0.0f;
+#pragma unroll
+            for (int k = 0; k < r; k++) acc -= A_s[(o + r) * AP + o + k] * t[k];
+            t[r] = acc;
+        }
+#pragma unroll
+        for (int r = 0; r < 16; r++) T_s[(o + r) * 64 + o + cc] = t[r];
+    }
+    __syncthreads();
+    float *Mw = M_t + (wave < 3 ? wave : 0) * 256;
+#pragma unroll
+    for (int lev = 1; lev < 4; lev++) {
+        if (wave < 4 - lev) {
+            const int j = wave, i = j + lev;
+            floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+            for (int kb = j; kb < i; kb++) {
+#pragma unroll
+                for (int k0 = 0; k0 < 16; k0 += 4) {
+                    const float av = A_s[(16 * i + m) * AP + 16 * kb + k0 + g];
+                    const float bv = T_s[(16 * kb + k0 + g) * 64 + 16 * j + m];
+                    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+                }
+            }
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) Mw[(4 * g + ii) * 16 + m] = acc[ii];
+            asm volatile("" ::: "memory");
+            floatx4_t tacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int k0 = 0; k0 < 16; k0 += 4) {
+                const float av = T_s[(16 * i + m) * 64 + 16 * i + k0 + g];
+                const float bv = Mw[(k0 + g) * 16 + m];
+                tacc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, tacc, 0, 0, 0);
+            }
+#pragma unroll
+            for (int ii = 0; ii < 4; ii++) T_s[(16 * i + 4 * g + ii) * 64 + 16 * j + m] = -tacc[ii];
+        }
+        __syncthreads();
+    }
+
+    // ---- phase 5: [Ut | W] rows of block `wave` = T_V V | T_K K, all pairs
+    bf16x8_t tv[2][2], tk[2][2];   // [k-step][hi, lo]
+#pragma unroll
+    for (int ks = 0; ks < 2; ks++) {
+        const int s = wave * 16 + m, r0 = 32 * ks + 8 * g;
+        float fv[8], fk[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) {
+            const int r = r0 + e;
+            const float tsr = r <= s ? T_s[s * 64 + r] : 0.0f;
+            fv[e] = tsr * beta_s[r];
+            fk[e] = tsr * ((beta_s[r] * eg_s[r]) * ik_s[r]);
+        }
+        uint4 hv, lv, hk, lk;
+        split8(fv, hv, lv);
+        split8(fk, hk, lk);
+        tv[ks][0] = as_bf16x8(hv);
+        tv[ks][1] = as_bf16x8(lv);
+        tk[ks][0] = as_bf16x8(hk);
+        tk[ks][1] = as_bf16x8(lk);
+    }
+    floatx4_t wacc[8];
+    float *ut = (float *)(rec + X_UT);
+#pragma unroll
+    for (int cb = 0; cb < 16; cb++) {
+        const bool isv = cb < 8;
+        const uint16_t *src = isv ? V_h : K_h, *srl = isv ? V_l : K_l;
+        const int col = (cb & 7) * 16 + m;
+        floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const bf16x8_t bop = as_bf16x8(*(const uint4 *)&src[col * TP + 32 * ks + 8 * g]);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(isv ? tv[ks][0] : tk[ks][0], bop, acc, 0, 0, 0);
+            acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(isv ? tv[ks][1] : tk[ks][1], bop, acc, 0, 0, 0);
+            if (has_lo) {
+                const bf16x8_t bol = as_bf16x8(*(const uint4 *)&srl[col * TP + 32 * ks + 8 * g]);
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(isv ? tv[ks][0] : tk[ks][0], bol, acc, 0, 0, 0);
+            }
+        }
+        if (isv) {
+            *(floatx4_t *)&ut[(((size_t)wave * 8 + cb) * 64 + lane) * 4] = acc;
+        } else {
+            wacc[cb - 8] = acc;
+        }
+    }
+    __syncthreads();   // every read of V^T is done: the k region takes the -W staging
+#pragma unroll
+    for (int cb = 0; cb < 8; cb++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const float w = -wacc[cb][i];
+            const uint16_t h = vx_f32_to_bf16(w);
+            W_h[(wave * 16 + 4 * g + i) * RP + cb * 16 + m] = h;
+            W_l[(wave * 16 + 4 * g + i) * RP + cb * 16 + m] = vx_f32_to_bf16(w - vx_bf16_to_f32(h));
+        }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        const size_t o = ((size_t)(wave * 4 + ks) * 64 + lane) * 16;
+        *(uint4 *)(rec + X_NW + o) = *(const uint4 *)&W_h[rowA * RP + 32 * ks + 8 * g];
+        *(uint4 *)(rec + X_NW + 16384 + o) = *(const uint4 *)&W_l[rowA * RP + 32 * ks + 8 * g];
+    }
+}
+
+// dnp_scan3: the chunk walk of dnp_scan with every operand as a hi/lo pair.
+// A wave's operands of one chunk (29 tiles of 1 KiB + the record's last 256
+// bytes) are staged in one LDS slot per wave: at the top of a chunk step the
+// wave reads the whole slot into registers and at once starts the next
+// chunk's direct-to-LDS loads into it, so they have a whole step to land.
+// The output rows of a chunk are stored at the top of the next step.
+constexpr int X3_TILES = 29;
+constexpr uint32_t X3_WAVE = X3_TILES * 1024 + 256;
+
+__device__ __forceinline__ uint32_t x3_src(int j, int wave, int slice) {
+    // slot order: NW hi 0-3, NW lo 4-7, QE hi 8-11, QE lo 12-15, KT hi 16-19,
+    // KT lo 20-23, P hi 24-25, P lo 26-27, Ut 28
+    return j < 8    ? (uint32_t)(X_NW + (j >> 2) * 16384 + (wave * 4 + (j & 3)) * 1024)
+           : j < 16 ? (uint32_t)(X_QE + ((j - 8) >> 2) * 16384 + (wave * 4 + (j & 3)) * 1024)
+           : j < 24 ? (uint32_t)(X_KT + ((j - 16) >> 2) * 16384 + (wave * 4 + (j & 3)) * 1024)
+           : j < 28 ? (uint32_t)(X_P + ((j - 24) >> 1) * 8192 + (wave * 2 + (j & 1)) * 1024)
+                    : (uint32_t)(X_UT + (wave * 8 + slice) * 1024);
+}
+__device__ __forceinline__ void x3_fetch(const char *rec, uint32_t lds, int wave, int slice, int lane) {
+#pragma unroll
+    for (int j = 0; j < X3_TILES; j++)
+        vx_dma16(rec, x3_src(j, wave, slice) + (uint32_t)lane * 16, lds + (uint32_t)j * 1024);
+    vx_dma4(rec, (uint32_t)X_GC + (uint32_t)lane * 4, lds + X3_TILES * 1024);
+}
+
+// bf16 hi, lo of 4 floats, as two packed uint2
+__device__ __forceinline__ void split4(const floatx4_t v, uint2 &h, uint2 &l) {
+    h = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+    const uint16_t *hs = (const uint16_t *)&h;
+    l = make_uint2(pack2(v[0] - vx_bf16_to_f32(hs[0]), v[1] - vx_bf16_to_f32(hs[1])),
+                   pack2(v[2] - vx_bf16_to_f32(hs[2]), v[3] - vx_bf16_to_f32(hs[3])));
+}
+
+#define MFMA3(acc, ah, al, bh, bl)                                              \
+    do {                                                                        \
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);    \
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);    \
+        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);    \
+    } while (0)
+
+__global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int b = blockIdx.y, bid = blockIdx.x;
+    int vh, slice;
+    if (p.xcd_map) {
+        const int xcd = bid & 7, idx = bid >> 3;
+        slice = idx % NSLICE;
+        vh = (idx / NSLICE) * 8 + xcd;
+    } else {
+        vh = bid / NSLICE;
+        slice = bid % NSLICE;
+    }
+    const int col = slice * 16 + n;
+
+    __shared__ __align__(16) char ops_l[4 * X3_WAVE];
+    __shared__ uint16_t S_h[16][HD + 8], S_lo[16][HD + 8];   // S slice hi/lo, [column][key dim]
+    __shared__ uint16_t U_h[16][CH + 8], U_lo[16][CH + 8];   // U slice hi/lo, [column][token]
+
+    const char *rec0 = vx_uniform_ptr(p.rec + ((size_t)b * p.nv + vh) * p.NC * XREC);
+    const uint32_t ops_w = vx_lds_addr(ops_l) + (uint32_t)wave * X3_WAVE;
+    x3_fetch(rec0, ops_w, wave, slice, lane);
+
+    float *Sg = p.S + ((size_t)b * p.nv + vh) * HD * HD;
+    floatx4_t S[2];
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) S[r][i] = Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + col];
+    __asm__ volatile("" ::"v"(S[0]), "v"(S[1]));
+
+    floatx4_t Oprev = {0.f, 0.f, 0.f, 0.f};
+    const uint4 *t = (const uint4 *)&ops_l[wave * X3_WAVE] + lane;
+    for (int c = 0; c < p.NC; c++) {
+        // chunk c's operands have landed (and the previous step's stores are done)
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        if (c > 0) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int tt = (c - 1) * CH + wave * 16 + 4 * g + i;
+                if (tt < p.T) p.out[(((size_t)b * p.T + tt) * p.nv + vh) * HD + col] = Oprev[i];
+            }
+        }
+        uint4 op[X3_TILES];
+#pragma unroll
+        for (int j = 0; j < X3_TILES; j++) op[j] = t[j * 64];
+        const float gc = *(const float *)&ops_l[wave * X3_WAVE + X3_TILES * 1024];
+        // S -> bf16 hi/lo, [column][key dim]
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            const int d = (2 * wave + r) * 16 + 4 * g;
+            uint2 h, l;
+            split4(S[r], h, l);
+            *(uint2 *)&S_h[n][d] = h;
+            *(uint2 *)&S_lo[n][d] = l;
+        }
+        // the slot is read out: the next chunk's loads go into it now
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
+        if (c + 1 < p.NC) x3_fetch(rec0 + (size_t)(c + 1) * XREC, ops_w, wave, slice, lane);
+        vx_lds_barrier();   // S hi/lo complete
+        bf16x8_t sbh[4], sbl[4];
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            sbh[ks] = as_bf16x8(*(const uint4 *)&S_h[n][32 * ks + 8 * g]);
+            sbl[ks] = as_bf16x8(*(const uint4 *)&S_lo[n][32 * ks + 8 * g]);
+        }
+        // U = Ut - W S and the e^gam Q S part of O, in independent chains
+        const uint4 utu = op[28];
+        floatx4_t U0 = (floatx4_t){__uint_as_float(utu.x), __uint_as_float(utu.y), __uint_as_float(utu.z), __uint_as_float(utu.w)};
+        floatx4_t U1 = {0.f, 0.f, 0.f, 0.f}, U2 = {0.f, 0.f, 0.f, 0.f}, U3 = {0.f, 0.f, 0.f, 0.f};
+        floatx4_t O0 = {0.f, 0.f, 0.f, 0.f}, O1 = {0.f, 0.f, 0.f, 0.f};
+        MFMA3(U0, as_bf16x8(op[0]), as_bf16x8(op[4]), sbh[0], sbl[0]);
+        MFMA3(U1, as_bf16x8(op[1]), as_bf16x8(op[5]), sbh[1], sbl[1]);
+        MFMA3(U2, as_bf16x8(op[2]), as_bf16x8(op[6]), sbh[2], sbl[2]);
+        MFMA3(U3, as_bf16x8(op[3]), as_bf16x8(op[7]), sbh[3], sbl[3]);
+        const floatx4_t U = (U0 + U1) + (U2 + U3);
+        {
+            uint2 h, l;
+            split4(U, h, l);
+            *(uint2 *)&U_h[n][wave * 16 + 4 * g] = h;
+            *(uint2 *)&U_lo[n][wave * 16 + 4 * g] = l;
+        }
+        MFMA3(O0, as_bf16x8(op[8]), as_bf16x8(op[12]), sbh[0], sbl[0]);
+        MFMA3(O1, as_bf16x8(op[9]), as_bf16x8(op[13]), sbh[1], sbl[1]);
+        MFMA3(O0, as_bf16x8(op[10]), as_bf16x8(op[14]), sbh[2], sbl[2]);
+        MFMA3(O1, as_bf16x8(op[11]), as_bf16x8(op[15]), sbh[3], sbl[3]);
+        vx_lds_barrier();   // U hi/lo complete
+        bf16x8_t ubh[2], ubl[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            ubh[ks] = as_bf16x8(*(const uint4 *)&U_h[n][32 * ks + 8 * g]);
+            ubl[ks] = as_bf16x8(*(const uint4 *)&U_lo[n][32 * ks + 8 * g]);
+        }
+        // S = e^gam_C S + Kt^T U, per row block two chains
+#pragma unroll
+        for (int r = 0; r < 2; r++) {
+            floatx4_t Sa = S[r] * gc, Sb = {0.f, 0.f, 0.f, 0.f};
+            MFMA3(Sa, as_bf16x8(op[16 + 2 * r]), as_bf16x8(op[20 + 2 * r]), ubh[0], ubl[0]);
+            MFMA3(Sb, as_bf16x8(op[17 + 2 * r]), as_bf16x8(op[21 + 2 * r]), ubh[1], ubl[1]);
+            S[r] = Sa + Sb;
+        }
+        // O += P U
+        MFMA3(O0, as_bf16x8(op[24]), as_bf16x8(op[26]), ubh[0], ubl[0]);
+        MFMA3(O1, as_bf16x8(op[25]), as_bf16x8(op[27]), ubh[1], ubl[1]);
+        Oprev = O0 + O1;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int tt = (p.NC - 1) * CH + wave * 16 + 4 * g + i;
+        if (tt < p.T) p.out[(((size_t)b * p.T + tt) * p.nv + vh) * HD + col] = Oprev[i];
+    }
+#pragma unroll
+    for (int r = 0; r < 2; r++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + col] = S[r][i];
+}
+
+// ---- the glue of vx27_qlayer_batch around the chunked core --------------
+// dnp_glue_in: one workgroup (4 waves) per token row (b, t): for every
+// 128-channel head of the q|k|v row (wave w takes heads w, w+4, ...; a lane
+// two channels), the causal conv + SiLU from the prompt's x and the carried
+// conv state (VX27_DN_CONV; else the bf16 q/k/v widened), then on q and k
+// heads the pre-norms the flags ask for -- rmsn(x)(1+w) (vx27_qfwd.c:32-39,
+// 123) and l2norm with q/sqrt(128) (:124-130), sums in double -- and the
+// result rounded to bf16 for the chunked products (whose prep applies
+// step_exact's own l2norm and scale once more, as the reference does).
+struct GlueInArgs {
+    int B, T, nqk, nv, C;
+    unsigned flags;
+    int w_bf16;
+    const float *x;            // [B][T][C] (VX27_DN_CONV)
+    const float *conv_state;   // [B][C][3], the state before token 0
+    const void *conv_w;
+    const uint16_t *q, *k, *v; // bf16 inputs without VX27_DN_CONV
+    const float *norm_w;       // [128]
+    uint16_t *qo, *ko, *vo;    // bf16 [B][T][nqk|nqk|nv][128]
+    uint16_t *qol, *kol, *vol; // their lo parts (x - bf16(x)), or NULL
+};
+__global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
+    const int t = blockIdx.x, b = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int nh = 2 * a.nqk + a.nv;
+    const size_t row = (size_t)b * a.T + t;
+    const float qs = 1.0f / sqrtf((float)HD);
+    const bool conv = (a.flags & VX27_DN_CONV) != 0;
+    for (int hh = wave; hh < nh; hh += 4) {
+        const bool is_q = hh < a.nqk, is_k = !is_q && hh < 2 * a.nqk;
+        float v2[2];
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const int i = lane + 64 * e;
+            const size_t ch = (size_t)hh * HD + i;
+            if (conv) {
+                float w[4], c[3];
+                load_conv_w(a.conv_w, a.w_bf16, ch, w);
+#pragma unroll
+                for (int j = 0; j < 3; j++) {   // token t - 3 + j, or the carried state
+                    const int s = t - 3 + j;
+                    c[j] = s >= 0 ? a.x[((size_t)b * a.T + s) * a.C + ch]
+                                  : a.conv_state[((size_t)b * a.C + ch) * 3 + (3 + s)];
+                }
+                v2[e] = conv_step(c, w, a.x[row * a.C + ch]);
+            } else {
+                const uint16_t *src = is_q ? a.q + (row * a.nqk + hh) * HD
+                                    : is_k ? a.k + (row * a.nqk + (hh - a.nqk)) * HD
+                                           : a.v + (row * a.nv + (hh - 2 * a.nqk)) * HD;
+                v2[e] = vx_bf16_to_f32(src[i]);
+            }
+        }
+        if ((is_q || is_k) && (a.flags & (VX27_DN_PRE_RMS | VX27_DN_PRE_L2))) {
+            if (a.flags & VX27_DN_PRE_RMS) {
+                const double ss = vx_wave_sum_f64_dpp((double)v2[0] * (double)v2[0] + (double)v2[1] * (double)v2[1]);
+                const float is = 1.0f / sqrtf((float)(ss / HD) + 1e-6f);
+#pragma unroll
+                for (int e = 0; e < 2; e++) v2[e] = (v2[e] * is) * (a.norm_w[lane + 64 * e] + 1.0f);
+            }
+            if (a.flags & VX27_DN_PRE_L2) {
+                const double ss = vx_wave_sum_f64_dpp((double)v2[0] * (double)v2[0] + (double)v2[1] * (double)v2[1]);
+                const float il = 1.0f / sqrtf((float)ss + 1e-6f);
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    v2[e] = v2[e] * il;
+                    if (is_q) v2[e] = v2[e] * qs;
+                }
+            }
+        }
+        uint16_t *dst = is_q ? a.qo + (row * a.nqk + hh) * HD
+                      : is_k ? a.ko + (row * a.nqk + (hh - a.nqk)) * HD
+                             : a.vo + (row * a.nv + (hh - 2 * a.nqk)) * HD;
+        const uint16_t h0 = vx_f32_to_bf16(v2[0]), h1 = vx_f32_to_bf16(v2[1]);
+        dst[lane] = h0;
+        dst[lane + 64] = h1;
+        if (a.qol) {
+            uint16_t *dl = is_q ? a.qol + (row * a.nqk + hh) * HD
+                         : is_k ? a.kol + (row * a.nqk + (hh - a.nqk)) * HD
+                                : a.vol + (row * a.nv + (hh - 2 * a.nqk)) * HD;
+            dl[lane] = vx_f32_to_bf16(v2[0] - vx_bf16_to_f32(h0));
+            dl[lane + 64] = vx_f32_to_bf16(v2[1] - vx_bf16_to_f32(h1));
+        }
+    }
+}
+
+// The conv state after the prompt: the last three inputs of each channel
+// (older ones from the state itself when T < 3).  One thread per (b, c); it
+// runs after dnp_glue_in, which read the state before token 0.
+__global__ __launch_bounds__(256) void dnp_conv_state(int B, int T, int C, const float *x, float *state) {
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= (size_t)B * C) return;
+    const int b = (int)(id / C), c = (int)(id % C);
+    float *sp = state + id * 3;
+    float n[3];
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+        const int s = T - 3 + j;
+        n[j] = s >= 0 ? x[((size_t)b * T + s) * C + c] : sp[3 + s];   // (T < 3: the old state shifted)
+    }
+    sp[0] = n[0]; sp[1] = n[1]; sp[2] = n[2];
+}
+
+// Gated output norm in place (vx27_qfwd.c:145-151): one wave per (token,
+// value head) row: out = rmsn_std(o) * norm_w * silu(z), sum in double.
+__global__ __launch_bounds__(256) void dnp_out_gate(int rows, const float *z, const float *norm_w, float *out) {
+    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (r >= rows) return;
+    float *o = out + (size_t)r * HD;
+    const float *zr = z + (size_t)r * HD;
+    float f0 = o[lane], f1 = o[lane + 64];
+    const double so = vx_wave_sum_f64_dpp((double)f0 * (double)f0 + (double)f1 * (double)f1);
+    const float is = 1.0f / sqrtf((float)(so / HD) + 1e-6f);
+    f0 = ((f0 * is) * norm_w[lane]) * silu_f(zr[lane]);
+    f1 = ((f1 * is) * norm_w[lane + 64]) * silu_f(zr[lane + 64]);
+    o[lane] = f0;
+    o[lane + 64] = f1;
+}
+
+// Widen bf16 q|k|v rows into one fp32 row per token (the exact path's input
+// without the conv): act [B][T][C].
+__global__ __launch_bounds__(256) void dnp_widen(int rows, int nqk, int nv, const uint16_t *q, const uint16_t *k,
+                                                 const uint16_t *v, float *act) {
+    const int qd = nqk * HD, vd = nv * HD, C = 2 * qd + vd;
+    const size_t id = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (id >= (size_t)rows * C) return;
+    const size_t r = id / C;
+    const int c = (int)(id % C);
+    const uint16_t h = c < qd ? q[r * qd + c] : c < 2 * qd ? k[r * qd + (c - qd)] : v[r * vd + (c - 2 * qd)];
+    act[id] = vx_bf16_to_f32(h);
+}
+
+// vx27_hip_dn_commit: checkpoint m[b] of sequence b into the live state.
+// grid (chunks of 256 elements, B), block 256.
+__global__ __launch_bounds__(256) void dn_commit_kernel(int T, size_t s_elems, size_t c_elems, const int *m,
+                                                        const float *S_ckpt, const float *conv_ckpt, float *S,
+                                                        float *conv, int *err_flag) {
+    const int b = blockIdx.y;
+    const int mb = m[b];
+    if (mb < 0) return;
+    if (mb >= T) {
+        if (blockIdx.x == 0 && threadIdx.x == 0) *err_flag = 1;
+        return;
+    }
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (S_ckpt && i < s_elems) S[(size_t)b * s_elems + i] = S_ckpt[((size_t)b * T + mb) * s_elems + i];
+    if (conv_ckpt && i < c_elems) conv[(size_t)b * c_elems + i] = conv_ckpt[((size_t)b * T + mb) * c_elems + i];
+}
+
 }  // namespace
+
+// The exact path: the decode kernels token by token (prefill layout).
+static int dn_prefill_exact(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d) {
+    const int qd = d->nqk * HD, vd = d->nv * HD, C = 2 * qd + vd;
+    const bool conv = (d->flags & VX27_DN_CONV) != 0;
+    const size_t rows = (size_t)d->B * d->T;
+    const size_t gate_bytes = (rows * d->nv * sizeof(double2) + 255) & ~(size_t)255;
+    const size_t opre_bytes = ((size_t)d->B * vd * sizeof(float) + 255) & ~(size_t)255;
+    void *scr;
+    if (vx_ctx_scratch(ctx, gate_bytes + opre_bytes + rows * C * sizeof(float), &scr)) return -1;
+    double2 *gates = (double2 *)scr;
+    float *act = (float *)((char *)scr + gate_bytes + opre_bytes);
+    const size_t n_gate = rows * d->nv;
+    if (vx_dn_gates(ctx, n_gate, d->nv, d->a, d->b, d->A_log, d->dt_bias, gates)) return -1;
+    if (conv) {
+        ConvArgs ca = {d->B, C, d->T, d->conv_w_dtype == VX27_BF16, d->conv_state, d->conv_w, d->x, act, 1, d->T,
+                       d->conv_ckpt};
+        if (vx_dn_conv(ctx, ca)) return -1;
+    } else {
+        const size_t n = rows * C;
+        VX_LAUNCH(ctx, dnp_widen, dim3((unsigned)((n + 255) / 256)), dim3(256), (int)rows, d->nqk, d->nv, d->q, d->k,
+                  d->v, act);
+    }
+    DnArgs a = {};
+    a.B = d->B; a.nqk = d->nqk; a.nv = d->nv; a.flags = d->flags & (VX27_DN_PRE_RMS | VX27_DN_PRE_L2 | VX27_DN_OUT_GATE);
+    a.t_step = 1; a.b_step = d->T;
+    a.S = d->S; a.norm_w = d->norm_w; a.z = d->z; a.z_tok = (size_t)vd;
+    a.q_tok = a.k_tok = a.v_tok = (size_t)C;
+    a.out_tok = (size_t)vd;
+    a.o_pre = (float *)((char *)scr + gate_bytes);
+    if (!d->S_ckpt) {   // one launch, the state resident in registers
+        a.steps = d->T;
+        a.q = act; a.k = act + qd; a.v = act + 2 * qd;
+        a.gates = gates; a.out = d->out;
+        return vx_dn_recurrence(ctx, a);
+    }
+    // token by token, the state written out after each (single-step kernel)
+    const size_t s_bytes = (size_t)d->nv * HD * HD * sizeof(float);
+    for (int t = 0; t < d->T; t++) {
+        DnArgs at = a;
+        at.steps = 1;
+        at.q = act + (size_t)t * C; at.k = at.q + qd; at.v = at.q + 2 * qd;
+        at.gates = gates + (size_t)t * d->nv;
+        at.z = d->z ? d->z + (size_t)t * vd : nullptr;
+        at.out = d->out + (size_t)t * vd;
+        if (vx_dn_recurrence(ctx, at)) return -1;
+        VX_HIP(hipMemcpy2DAsync((char *)d->S_ckpt + (size_t)t * s_bytes, (size_t)d->T * s_bytes, d->S, s_bytes, s_bytes,
+                                (size_t)d->B, hipMemcpyDeviceToDevice, ctx->stream));
+    }
+    return 0;
+}
 
 extern "C" int vx27_hip_dn_prefill(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d) {
     if (vx_ctx_enter(ctx)) return -1;
@@ -567,19 +1278,81 @@ extern "C" int vx27_hip_dn_prefill(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc
     VX_REQUIRE(d->hd == HD, "vx27_hip_dn_prefill: head_dim must be 128 (got %d)", d->hd);
     VX_REQUIRE(d->B >= 1 && d->T >= 1 && d->nqk >= 1 && d->nv >= d->nqk && d->nv % d->nqk == 0 && d->nv <= 4096,
                "vx27_hip_dn_prefill: bad sizes B=%d T=%d nqk=%d nv=%d", d->B, d->T, d->nqk, d->nv);
-    VX_REQUIRE(d->flags == 0, "vx27_hip_dn_prefill: flags must be 0");
-    VX_REQUIRE(d->S && d->q && d->k && d->v && d->a && d->b && d->A_log && d->dt_bias && d->out,
-               "vx27_hip_dn_prefill: null pointer");
+    VX_REQUIRE((d->flags & ~63u) == 0, "vx27_hip_dn_prefill: unknown flags %#x", d->flags);
+    VX_REQUIRE(d->S && d->a && d->b && d->A_log && d->dt_bias && d->out, "vx27_hip_dn_prefill: null pointer");
+    const bool conv = (d->flags & VX27_DN_CONV) != 0;
+    if (conv) {
+        VX_REQUIRE(d->x && d->conv_state && d->conv_w, "vx27_hip_dn_prefill: VX27_DN_CONV needs x, conv_state, conv_w");
+        VX_REQUIRE(d->conv_w_dtype == VX27_F32 || d->conv_w_dtype == VX27_BF16,
+                   "vx27_hip_dn_prefill: conv_w_dtype must be VX27_F32 or VX27_BF16");
+    } else {
+        VX_REQUIRE(d->q && d->k && d->v, "vx27_hip_dn_prefill: q, k, v are required without VX27_DN_CONV");
+        VX_REQUIRE(!d->conv_ckpt, "vx27_hip_dn_prefill: conv_ckpt needs VX27_DN_CONV");
+    }
+    if (d->flags & (VX27_DN_PRE_RMS | VX27_DN_OUT_GATE))
+        VX_REQUIRE(d->norm_w != nullptr, "vx27_hip_dn_prefill: norm_w required by PRE_RMS/OUT_GATE");
+    if (d->flags & VX27_DN_OUT_GATE) VX_REQUIRE(d->z != nullptr, "vx27_hip_dn_prefill: z required by OUT_GATE");
+    if ((d->flags & VX27_DN_EXACT) || d->S_ckpt || d->conv_ckpt) return dn_prefill_exact(ctx, d);
+
     const int NC = (d->T + CH - 1) / CH;
+    const bool x3 = !(d->flags & VX27_DN_BF16);   // split (bf16x3) products unless asked for bf16
+    const size_t rec_bytes = x3 ? XREC : REC;
     const size_t n_rec = (size_t)d->B * d->nv * NC;
-    const size_t gc_off = (n_rec * REC + 255) & ~(size_t)255;
+    const size_t gc_off = (n_rec * rec_bytes + 255) & ~(size_t)255;
+    const bool glue = conv || (d->flags & (VX27_DN_PRE_RMS | VX27_DN_PRE_L2));
+    const int qd = d->nqk * HD, vd = d->nv * HD, C = 2 * qd + vd;
+    const size_t glue_off = (gc_off + n_rec * sizeof(float) + 255) & ~(size_t)255;
+    const size_t rows = (size_t)d->B * d->T;
+    const size_t glue_bytes = glue ? rows * C * sizeof(uint16_t) * (x3 ? 2 : 1) : 0;
     void *scr;
-    if (vx_ctx_scratch(ctx, gc_off + n_rec * sizeof(float), &scr)) return -1;
-    PrepArgs pa{d->T, d->nqk, d->nv, NC, d->q, d->k, d->v, d->a, d->b, d->A_log, d->dt_bias,
-                (char *)scr, (float *)((char *)scr + gc_off)};
-    VX_LAUNCH(ctx, dnp_prep, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B), dim3(256), pa);
+    if (vx_ctx_scratch(ctx, glue_off + glue_bytes, &scr)) return -1;
+    const uint16_t *q = d->q, *k = d->k, *v = d->v;
+    const uint16_t *ql = nullptr, *kl = nullptr, *vl = nullptr;
+    if (glue) {   // conv and pre-norms in fp32, then q, k, v as bf16 (hi, and lo for the split form)
+        uint16_t *qo = (uint16_t *)((char *)scr + glue_off), *ko = qo + rows * qd, *vo = ko + rows * qd;
+        uint16_t *qol = x3 ? vo + rows * vd : nullptr;
+        uint16_t *kol = x3 ? qol + rows * qd : nullptr, *vol = x3 ? kol + rows * qd : nullptr;
+        GlueInArgs ga{d->B, d->T, d->nqk, d->nv, C, d->flags, d->conv_w_dtype == VX27_BF16, d->x, d->conv_state,
+                      d->conv_w, d->q, d->k, d->v, d->norm_w, qo, ko, vo, qol, kol, vol};
+        VX_LAUNCH(ctx, dnp_glue_in, dim3((unsigned)d->T, (unsigned)d->B), dim3(256), ga);
+        if (conv) {
+            const size_t nthr = (size_t)d->B * C;
+            VX_LAUNCH(ctx, dnp_conv_state, dim3((unsigned)((nthr + 255) / 256)), dim3(256), d->B, d->T, C, d->x,
+                      d->conv_state);
+        }
+        q = qo; k = ko; v = vo;
+        ql = qol; kl = kol; vl = vol;
+    }
     ScanArgs sa{d->T, d->nv, NC, (d->nv % 8) == 0, (const char *)scr, (const float *)((char *)scr + gc_off),
                 d->S, d->out};
-    VX_LAUNCH(ctx, dnp_scan, dim3((unsigned)(d->nv * NSLICE), (unsigned)d->B), dim3(256), sa);
+    if (x3) {
+        Prep3Args pa{d->T, d->nqk, d->nv, NC, q, k, v, ql, kl, vl, d->a, d->b, d->A_log, d->dt_bias, (char *)scr};
+        VX_LAUNCH(ctx, dnp_prep3, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B), dim3(256), pa);
+        VX_LAUNCH_NAMED(ctx, "dnp_scan3", dnp_scan3, dim3((unsigned)(d->nv * NSLICE), (unsigned)d->B), dim3(256), sa);
+    } else {
+        PrepArgs pa{d->T, d->nqk, d->nv, NC, q, k, v, d->a, d->b, d->A_log, d->dt_bias,
+                    (char *)scr, (float *)((char *)scr + gc_off)};
+        VX_LAUNCH(ctx, dnp_prep, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B), dim3(256), pa);
+        VX_LAUNCH(ctx, dnp_scan, dim3((unsigned)(d->nv * NSLICE), (unsigned)d->B), dim3(256), sa);
+    }
+    if (d->flags & VX27_DN_OUT_GATE) {
+        const int nrow = (int)(rows * d->nv);
+        VX_LAUNCH(ctx, dnp_out_gate, dim3((unsigned)((nrow + 3) / 4)), dim3(256), nrow, d->z, d->norm_w, d->out);
+    }
+    return 0;
+}
+
+extern "C" int vx27_hip_dn_commit(vx27_hip_ctx *ctx, int B, int T, int nv, int hd, int C, const int *m,
+                                  const float *S_ckpt, const float *conv_ckpt, float *S, float *conv_state) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(hd == HD && B >= 1 && T >= 1 && nv >= 1 && C >= 0 && m,
+               "vx27_hip_dn_commit: bad arguments (B=%d T=%d nv=%d hd=%d C=%d)", B, T, nv, hd, C);
+    VX_REQUIRE(!S_ckpt || S, "vx27_hip_dn_commit: S_ckpt without S");
+    VX_REQUIRE(!conv_ckpt || conv_state, "vx27_hip_dn_commit: conv_ckpt without conv_state");
+    const size_t s_elems = (size_t)nv * HD * HD, c_elems = (size_t)C * 3;
+    const size_t n = std::max(S_ckpt ? s_elems : 0, conv_ckpt ? c_elems : 0);
+    if (n == 0) return 0;
+    VX_LAUNCH(ctx, dn_commit_kernel, dim3((unsigned)((n + 255) / 256), (unsigned)B), dim3(256), T, s_elems, c_elems, m,
+              S_ckpt, conv_ckpt, S, conv_state, ctx->err_flag);
     return 0;
 }

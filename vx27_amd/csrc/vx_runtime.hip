@@ -181,8 +181,9 @@ extern "C" int vx27_hip_sync(vx27_hip_ctx *ctx) {
     VX_HIP(hipMemcpy(&flag, ctx->err_flag, sizeof flag, hipMemcpyDeviceToHost));
     if (flag) {
         VX_HIP(hipMemset(ctx->err_flag, 0, sizeof flag));
-        VX_REQUIRE(false, "vx27_hip_sync: a decode call since the last sync had a position outside its KV cache "
-                          "(pos < 0 or pos >= L); its outputs are undefined");
+        VX_REQUIRE(false, "vx27_hip_sync: a call since the last sync had an index outside its range (a decode "
+                          "position outside its KV cache, or a commit index past its checkpoints); that call's "
+                          "outputs are undefined");
     }
     return 0;
 }

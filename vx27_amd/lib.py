@@ -15,7 +15,7 @@ LIB_PATH = os.path.join(PKG, "libvx27_hip.so")
 
 VP = C.c_void_p
 F32, BF16 = 0, 1
-DN_CONV, DN_PRE_RMS, DN_PRE_L2, DN_OUT_GATE = 1, 2, 4, 8
+DN_CONV, DN_PRE_RMS, DN_PRE_L2, DN_OUT_GATE, DN_EXACT, DN_BF16 = 1, 2, 4, 8, 16, 32
 GQA_NORM_W = 1
 GQA_NO_GATE = 2
 ERR_ABORT, ERR_POISON = 0, 1
@@ -32,7 +32,9 @@ class DnDesc(C.Structure):
 class DnPrefillDesc(C.Structure):
     _fields_ = [("B", C.c_int), ("T", C.c_int), ("nqk", C.c_int), ("nv", C.c_int), ("hd", C.c_int),
                 ("flags", C.c_uint), ("S", VP), ("q", VP), ("k", VP), ("v", VP), ("a", VP), ("b", VP),
-                ("A_log", VP), ("dt_bias", VP), ("out", VP)]
+                ("A_log", VP), ("dt_bias", VP), ("out", VP),
+                ("x", VP), ("conv_state", VP), ("conv_w", VP), ("conv_w_dtype", C.c_int),
+                ("norm_w", VP), ("z", VP), ("S_ckpt", VP), ("conv_ckpt", VP)]
 
 
 class GqaPrefillDesc(C.Structure):
@@ -95,6 +97,7 @@ _SIGS = {
     "vx27_hip_memset": (C.c_int, [VP, VP, C.c_int, C.c_size_t]),
     "vx27_hip_dn_decode": (C.c_int, [VP, C.POINTER(DnDesc)]),
     "vx27_hip_dn_prefill": (C.c_int, [VP, C.POINTER(DnPrefillDesc)]),
+    "vx27_hip_dn_commit": (C.c_int, [VP] + [C.c_int] * 5 + [VP] * 5),
     "vx27_hip_gqa_prefill": (C.c_int, [VP, C.POINTER(GqaPrefillDesc)]),
     "vx27_hip_gqa_decode": (C.c_int, [VP, C.POINTER(GqaDesc)]),
     "vx27_hip_gqa_decode_noalloc": (C.c_int, [VP, C.POINTER(GqaDesc)]),

@@ -9,6 +9,8 @@ the CPU baseline / parity checks.  Streams are numpy PCG64 seeded with
                  specifies)
   dn_conv        batched DeltaNet decode with the fused causal conv
   gqa_decode     gated GQA single-query decode over a bf16 KV cache
+  dn_prefill_glue  a prompt through the whole DeltaNet branch of
+                 vx27_qlayer_batch: projection outputs x, gates, z
 """
 from __future__ import annotations
 
@@ -109,6 +111,28 @@ def dn_prefill(B=1, T=4096, nqk=16, nv=16, hd=128, config=4, S0_std=0.0):
     d["b"] = normal(r, (B, T, nv))
     d["S0"] = (normal(r, (B, nv, hd, hd), S0_std) if S0_std > 0
                else np.zeros((B, nv, hd, hd), np.float32))
+    return d
+
+
+def dn_prefill_glue(B=1, T=4096, nqk=16, nv=48, hd=128, config=6, S0_std=0.02):
+    """A prompt through the DeltaNet branch of vx27_qlayer_batch: the
+    projection outputs x [B][T][C] (q|k|v channels, C = 2*nqk*hd + nv*hd),
+    a, b [B][T][nv], z [B][T][nv][hd], all ~N(0,1); conv weights bf16
+    ~N(0,0.2), conv state ~N(0,0.5), state ~N(0,0.02), norm weight
+    1+N(0,0.1); A_log ~U(-2,1), dt_bias ~N(0,0.1)."""
+    r = rng(config, "dn_prefill_glue")
+    C = 2 * nqk * hd + nv * hd
+    A_log, dt_bias = dn_heads(r, nv)
+    d = dict(A_log=A_log, dt_bias=dt_bias)
+    d["conv_w_bf16"] = bf16_bits(normal(r, (C, 4), 0.2))
+    d["conv_w"] = bf16_to_f32(d["conv_w_bf16"])
+    d["conv0"] = normal(r, (B, C, 3), 0.5)
+    d["S0"] = normal(r, (B, nv, hd, hd), S0_std)
+    d["norm_w"] = normal(r, hd, 0.1, 1.0)
+    d["x"] = normal(r, (B, T, C))
+    d["a"] = normal(r, (B, T, nv))
+    d["b"] = normal(r, (B, T, nv))
+    d["z"] = normal(r, (B, T, nv, hd))
     return d
 
 
