@@ -1073,14 +1073,17 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
 }
 
 // ---- the glue of vx27_qlayer_batch around the chunked core --------------
-// dnp_glue_in: one workgroup (4 waves) per token row (b, t): for every
-// 128-channel head of the q|k|v row (wave w takes heads w, w+4, ...; a lane
-// two channels), the causal conv + SiLU from the prompt's x and the carried
-// conv state (VX27_DN_CONV; else the bf16 q/k/v widened), then on q and k
-// heads the pre-norms the flags ask for -- rmsn(x)(1+w) (vx27_qfwd.c:32-39,
-// 123) and l2norm with q/sqrt(128) (:124-130), sums in double -- and the
-// result rounded to bf16 for the chunked products (whose prep applies
-// step_exact's own l2norm and scale once more, as the reference does).
+// dnp_glue_in: one wave per (128-channel head of the q|k|v row, block of
+// GT tokens): the head's conv weights and the prompt's x rows t0-3 .. t0+GT-1
+// are loaded once (a lane holds two channels), then for each token the
+// causal conv + SiLU from the prompt's x and the carried conv state
+// (VX27_DN_CONV; else the bf16 q/k/v widened), on q and k heads the
+// pre-norms the flags ask for -- rmsn(x)(1+w) (vx27_qfwd.c:32-39, 123) and
+// l2norm with q/sqrt(128) (:124-130), sums in double -- and the result as
+// bf16 hi (and lo) for the chunked products (whose prep applies step_exact's
+// own l2norm and scale once more, as the reference does).
+// grid (ceil(T/GT), ceil(heads/4), B), block 256.
+constexpr int GT = 8;
 struct GlueInArgs {
     int B, T, nqk, nv, C;
     unsigned flags;
@@ -1094,33 +1097,44 @@ struct GlueInArgs {
     uint16_t *qol, *kol, *vol; // their lo parts (x - bf16(x)), or NULL
 };
 __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
-    const int t = blockIdx.x, b = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
+    const int hh = blockIdx.y * 4 + wave, b = blockIdx.z, t0 = blockIdx.x * GT;
     const int nh = 2 * a.nqk + a.nv;
-    const size_t row = (size_t)b * a.T + t;
-    const float qs = 1.0f / sqrtf((float)HD);
+    if (hh >= nh) return;
+    const bool is_q = hh < a.nqk, is_k = !is_q && hh < 2 * a.nqk;
     const bool conv = (a.flags & VX27_DN_CONV) != 0;
-    for (int hh = wave; hh < nh; hh += 4) {
-        const bool is_q = hh < a.nqk, is_k = !is_q && hh < 2 * a.nqk;
+    const float qs = 1.0f / sqrtf((float)HD);
+    const int nt = min(GT, a.T - t0);
+    // x window of the two channels: tokens t0-3 .. t0+GT-1 (older ones from the state)
+    float xw[2][GT + 3], w[2][4];
+    float nw[2] = {1.0f, 1.0f};
+#pragma unroll
+    for (int e = 0; e < 2; e++) {
+        const size_t ch = (size_t)hh * HD + lane + 64 * e;
+        if (conv) {
+            load_conv_w(a.conv_w, a.w_bf16, ch, w[e]);
+#pragma unroll
+            for (int j = 0; j < GT + 3; j++) {
+                const int s = t0 - 3 + j;
+                xw[e][j] = s < 0 ? a.conv_state[((size_t)b * a.C + ch) * 3 + (3 + s)]
+                         : s < a.T ? a.x[((size_t)b * a.T + s) * a.C + ch] : 0.0f;
+            }
+        }
+        if (a.norm_w && (is_q || is_k)) nw[e] = a.norm_w[lane + 64 * e];
+    }
+    for (int j = 0; j < nt; j++) {
+        const size_t row = (size_t)b * a.T + t0 + j;
         float v2[2];
 #pragma unroll
         for (int e = 0; e < 2; e++) {
-            const int i = lane + 64 * e;
-            const size_t ch = (size_t)hh * HD + i;
             if (conv) {
-                float w[4], c[3];
-                load_conv_w(a.conv_w, a.w_bf16, ch, w);
-#pragma unroll
-                for (int j = 0; j < 3; j++) {   // token t - 3 + j, or the carried state
-                    const int s = t - 3 + j;
-                    c[j] = s >= 0 ? a.x[((size_t)b * a.T + s) * a.C + ch]
-                                  : a.conv_state[((size_t)b * a.C + ch) * 3 + (3 + s)];
-                }
-                v2[e] = conv_step(c, w, a.x[row * a.C + ch]);
+                float c[3] = {xw[e][j], xw[e][j + 1], xw[e][j + 2]};
+                v2[e] = conv_step(c, w[e], xw[e][j + 3]);
             } else {
                 const uint16_t *src = is_q ? a.q + (row * a.nqk + hh) * HD
                                     : is_k ? a.k + (row * a.nqk + (hh - a.nqk)) * HD
                                            : a.v + (row * a.nv + (hh - 2 * a.nqk)) * HD;
-                v2[e] = vx_bf16_to_f32(src[i]);
+                v2[e] = vx_bf16_to_f32(src[lane + 64 * e]);
             }
         }
         if ((is_q || is_k) && (a.flags & (VX27_DN_PRE_RMS | VX27_DN_PRE_L2))) {
@@ -1128,7 +1142,7 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
                 const double ss = vx_wave_sum_f64_dpp((double)v2[0] * (double)v2[0] + (double)v2[1] * (double)v2[1]);
                 const float is = 1.0f / sqrtf((float)(ss / HD) + 1e-6f);
 #pragma unroll
-                for (int e = 0; e < 2; e++) v2[e] = (v2[e] * is) * (a.norm_w[lane + 64 * e] + 1.0f);
+                for (int e = 0; e < 2; e++) v2[e] = (v2[e] * is) * (nw[e] + 1.0f);
             }
             if (a.flags & VX27_DN_PRE_L2) {
                 const double ss = vx_wave_sum_f64_dpp((double)v2[0] * (double)v2[0] + (double)v2[1] * (double)v2[1]);
@@ -1314,7 +1328,9 @@ extern "C" int vx27_hip_dn_prefill(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc
         uint16_t *kol = x3 ? qol + rows * qd : nullptr, *vol = x3 ? kol + rows * qd : nullptr;
         GlueInArgs ga{d->B, d->T, d->nqk, d->nv, C, d->flags, d->conv_w_dtype == VX27_BF16, d->x, d->conv_state,
                       d->conv_w, d->q, d->k, d->v, d->norm_w, qo, ko, vo, qol, kol, vol};
-        VX_LAUNCH(ctx, dnp_glue_in, dim3((unsigned)d->T, (unsigned)d->B), dim3(256), ga);
+        const int nh = 2 * d->nqk + d->nv;
+        VX_LAUNCH(ctx, dnp_glue_in, dim3((unsigned)((d->T + GT - 1) / GT), (unsigned)((nh + 3) / 4), (unsigned)d->B),
+                  dim3(256), ga);
         if (conv) {
             const size_t nthr = (size_t)d->B * C;
             VX_LAUNCH(ctx, dnp_conv_state, dim3((unsigned)((nthr + 255) / 256)), dim3(256), d->B, d->T, C, d->x,
