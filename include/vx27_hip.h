@@ -303,7 +303,7 @@ int vx27_hip_rope_table(vx27_hip_ctx *ctx, const int *pos, int n, int rope_dim,
                         float theta, float yarn, float *cosv, float *sinv);
 
 /* ------------------------------------------------ projections and layers */
-/* y[b*y_stride + n] = sum_k W[n][k] * x[b*x_stride + k] for B <= 5 vectors:
+/* y[b*y_stride + n] = sum_k W[n][k] * x[b*x_stride + k] for B >= 1 vectors:
  * W bf16 row-major [N][K] (N % 16 == 0, K % 32 == 0), x and y fp32.  The
  * F32 matvec of the reference (vx27_pmat.c:98-101, 119-125) on bf16 weights;
  * x enters the MFMA exactly (split into three bf16 parts), fp32 accumulation. */
@@ -320,8 +320,9 @@ int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const
  * weight format (src/vx_forge.c). */
 int vx27_hip_pack_weights_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, uint16_t *W_tiled);
 
-/* The mixer of one Gated DeltaNet layer for one decode token of B <= 5
- * sequences, from the layer input xn to the out_proj output (the DeltaNet
+/* The mixer of one Gated DeltaNet layer for one decode token of B
+ * sequences (any B; the projections stream their weights once per 15
+ * sequences), from the layer input xn to the out_proj output (the DeltaNet
  * branch of vx27_qlayer, vx27_qfwd.c:102-153):
  *   [qkv | z | a | b] = W_in xn      (in_proj_qkv, in_proj_z, in_proj_a, in_proj_b
  *                                      stacked row-wise: C + nv*hd + 2*nv rows)
@@ -344,7 +345,8 @@ typedef struct {
 } vx27_dn_layer_desc;
 int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_desc *d);
 
-/* The mixer of one gated GQA layer for one decode token of B <= 5 sequences
+/* The mixer of one gated GQA layer for one decode token of B sequences
+ * (any B; weights streamed once per 15 sequences)
  * (the attention branch of vx27_qlayer, vx27_qfwd.c:162-213):
  *   [q|gate interleaved per head | k | v] = W_qkv xn  (q_proj, k_proj, v_proj
  *                                      stacked: n_q*2*hd + 2*n_kv*hd rows),
@@ -366,8 +368,8 @@ typedef struct {
 int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer_desc *d);
 
 /* Pack x [B][K] once for several layers that read the same input
- * (x_packed of the layer descriptors); packed holds vx27_hip_pack_bytes(K). */
-size_t vx27_hip_pack_bytes(int K);
+ * (x_packed of the layer descriptors); packed holds vx27_hip_pack_bytes(K, B). */
+size_t vx27_hip_pack_bytes(int K, int B);
 int vx27_hip_pack_x(vx27_hip_ctx *ctx, const float *x, int B, int K, uint16_t *packed);
 
 /* pos[b] += 1 for b < B (advances decode positions inside a captured graph) */

@@ -58,7 +58,7 @@ int main(void) {
     printf("kv_for_q_23 %d\n", vx27_gqa_kv_for_q(23));
     printf("gate %.17g %.17g\n", beta, g_log);
     printf("rope_c0_131072 %.9g\n", (double)c[0]);
-    printf("pack_bytes_5120 %zu\n", vx27_hip_pack_bytes(5120));
+    printf("pack_bytes_5120 %zu\n", vx27_hip_pack_bytes(5120, 4));
     printf("version %s\n", vx27_hip_version());
     print_layout();
     return 0;

@@ -34,7 +34,8 @@ def bf16w(r, shape, std):
 def test_gemv_bf16_vs_reference_matvec(ctx):
     from vx27_amd import lib as L, workloads as W
     r = W.rng(7, "gemv")
-    for N, K, B in ((16432, 5120, 4), (5120, 6144, 4), (1024, 5120, 1), (64, 96, 5)):
+    for N, K, B in ((16432, 5120, 4), (5120, 6144, 4), (1024, 5120, 1), (64, 96, 5), (1024, 5120, 8),
+                    (512, 2048, 32), (256, 5120, 64)):
         Wb = bf16w(r, (N, K), 0.02)
         x = W.normal(r, (B, K))
         y = np.empty((B, N), np.float32)
@@ -64,11 +65,14 @@ def dn_layer_inputs(r, B, nqk=16, nv=48, hd=128):
     return w, S, conv
 
 
-def test_dn_layer_decode(ctx):
-    """The real layer shape (nqk 16, nv 48, hidden 5120), batch 4, 3 tokens."""
+@pytest.mark.parametrize("B", [4, 8, 20])
+def test_dn_layer_decode(ctx, B):
+    """The real layer shape (nqk 16, nv 48, hidden 5120), 3 tokens, batch 4,
+    the reference's batch limit 8 (two activation groups), and 20 (two
+    passes over the weights)."""
     from vx27_amd import lib as L, workloads as W
-    B, nqk, nv = 4, 16, 48
-    r = W.rng(8, "dn_layer")
+    nqk, nv = 16, 48
+    r = W.rng(8, f"dn_layer_{B}")
     w, S, conv = dn_layer_inputs(r, B, nqk, nv)
     dev = {k: ctx.put(w[k]) for k in ("conv_w_bf16", "A_log", "dt_bias", "norm_w")}
     dev["w_in"], dev["w_out"] = ctx.put_tiled(w["w_in"]), ctx.put_tiled(w["w_out"])
@@ -105,18 +109,19 @@ def gqa_layer_inputs(r, B, Lcap, n_ctx):
     return w, kc, vc
 
 
-def test_gqa_layer_decode(ctx):
-    """Real layer shape (24Q/4KV hd 256, hidden 5120), batch 4 at ragged
-    positions, 2 tokens."""
+@pytest.mark.parametrize("B", [4, 8, 17])
+def test_gqa_layer_decode(ctx, B):
+    """Real layer shape (24Q/4KV hd 256, hidden 5120) at ragged positions,
+    2 tokens, batch 4, 8 and 17 (two passes over the weights)."""
     from vx27_amd import lib as L, mixers as M, workloads as W
-    B, Lcap, n_ctx = 4, 768, 700
-    r = W.rng(9, "gqa_layer")
+    Lcap, n_ctx = 768, 700
+    r = W.rng(9, f"gqa_layer_{B}")
     w, kc, vc = gqa_layer_inputs(r, B, Lcap, n_ctx)
     lay = M.GatedGQALayer(ctx, B, Lcap, w["q_norm_w"], w["k_norm_w"])
     for b in range(B):
         lay.write_kv(b, 0, W.bf16_to_f32(kc[b, :n_ctx]), W.bf16_to_f32(vc[b, :n_ctx]))
     wq, wo = ctx.put_tiled(w["w_qkv"]), ctx.put_tiled(w["w_o"])
-    pos = np.array([650, 0, 31, 699], np.int32)
+    pos = np.array([650, 0, 31, 699] * (B // 4) + [333] * (B % 4), np.int32)[:B]
     pb = ctx.put(pos)
     xb, ob = ctx.buf(B * H * 4), ctx.buf(B * H * 4)
     d = L.GqaLayerDesc(B, 24, 4, 256, H, 64, 1e7, 1.0, Lcap, xb.ptr, None, wq.ptr, wo.ptr,

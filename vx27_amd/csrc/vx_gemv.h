@@ -9,10 +9,17 @@
 int vx_gemv_plan(int N, int K, int *n_seg, int *ks_per);
 int vx_gemv_pseg(int n_seg);
 size_t vx_gemv_part_bytes(int N, int n_seg);
-size_t vx_pack_bytes(int K);
+// Packed activations: vectors go in groups of VX_PACK_GV, each group one
+// 16-column MFMA B operand (the three parts of its <= 5 vectors): layout
+// [K/32 k-steps][groups][64 lanes][8] bf16.
+constexpr int VX_PACK_GV = 5;
+__host__ __device__ __forceinline__ int vx_pack_groups(int B) { return (B + VX_PACK_GV - 1) / VX_PACK_GV; }
+size_t vx_pack_bytes(int K, int B);
 // x [B][K] (row stride x_stride) -> packed MFMA B operand (three bf16 parts).
 int vx_pack(vx27_hip_ctx *ctx, const float *x, size_t x_stride, int B, int K, uint16_t *packed);
 // y[b*y_stride + n] = sum over k of W[n][k] x_b[k] for tiled W and a packed x
+// of B vectors (any B: passes of up to three groups, 15 vectors, each
+// streaming W once)
 int vx_gemv_store(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const uint16_t *packed, int B, float *y,
                   size_t y_stride);
 
@@ -28,16 +35,20 @@ __device__ __forceinline__ uint16_t vx_bf16_part(float x, int p) {
     return h;
 }
 
-// Element k of vector b (of B) as the three parts of the packed operand.
+// Element k of vector b (of B) as the three parts of the packed operand:
+// group j = b / 5 holds its Bj <= 5 vectors' part p of vector b' at column
+// p*Bj + b'.
 __device__ __forceinline__ void vx_pack_store(uint16_t *packed, int B, int b, int k, float x) {
-    const size_t base = ((size_t)(k >> 5) * 64 + ((k >> 3) & 3) * 16) * 8 + (k & 7);
+    const int G = vx_pack_groups(B), j = b / VX_PACK_GV, bl = b - VX_PACK_GV * j;
+    const int Bj = min(VX_PACK_GV, B - VX_PACK_GV * j);
+    const size_t base = (((size_t)(k >> 5) * G + j) * 64 + ((k >> 3) & 3) * 16) * 8 + (k & 7);
     uint16_t h = vx_f32_to_bf16(x);
-    packed[base + (size_t)b * 8] = h;
+    packed[base + (size_t)bl * 8] = h;
     x = x - vx_bf16_to_f32(h);
     h = vx_f32_to_bf16(x);
-    packed[base + (size_t)(B + b) * 8] = h;
+    packed[base + (size_t)(Bj + bl) * 8] = h;
     x = x - vx_bf16_to_f32(h);
-    packed[base + (size_t)(2 * B + b) * 8] = vx_f32_to_bf16(x);
+    packed[base + (size_t)(2 * Bj + bl) * 8] = vx_f32_to_bf16(x);
 }
 
 // Sums of the partials of row n for each vector b < B (three parts):

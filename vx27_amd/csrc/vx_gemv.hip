@@ -1,21 +1,24 @@
 // Skinny bf16 GEMM (the mixer projections) on gfx950 MFMA.
 //
-// y[b][n] = sum_k W[n][k] * x[b][k] for B <= 5 activation vectors (decode:
-// one token per sequence), W bf16 [N][K] (the reference's weight tensors,
+// y[b][n] = sum_k W[n][k] * x[b][k] for B activation vectors (decode: one
+// token per sequence), W bf16 [N][K] (the reference's weight tensors,
 // vx27_pmat.h:6-8), x and y fp32.
 //
 // The fp32 activations enter the MFMA exactly: each x is split into three
 // bf16 parts hi + mid + lo (8 mantissa bits each, 24 in all), and the parts
-// of the B vectors are the columns of the MFMA's B operand (3*B <= 15 of the
-// 16 columns).  One v_mfma_f32_16x16x32_bf16 therefore multiplies 16 weight
-// rows by every part of every vector; the products are exact in fp32 and the
-// only rounding is the fp32 accumulation, as in a plain fp32 dot product.
+// of up to 5 vectors are the columns of one MFMA B operand (3*5 <= 15 of the
+// 16 columns): one v_mfma_f32_16x16x32_bf16 multiplies 16 weight rows by
+// every part of 5 vectors; the products are exact in fp32 and the only
+// rounding is the fp32 accumulation, as in a plain fp32 dot product.  More
+// vectors go in more such groups: a weight tile loaded once feeds one MFMA
+// per group, up to 3 groups (15 vectors) per pass over the weights.
 // Output column n of an MFMA depends only on operand column n, so operand
 // columns >= 3*B may hold anything: they feed output columns nobody reads.
 //
 // Layouts:
-//   packed activations  [K/32 k-steps][64 lanes][8] bf16: lane (g,n) of k-step
-//                       s holds part n/B of vector n%B at k = 32s + 8g + 0..7
+//   packed activations  [K/32 k-steps][groups][64 lanes][8] bf16: lane (g,n)
+//                       of group j (its Bj <= 5 vectors 5j..) at k-step s
+//                       holds part n/Bj of vector 5j + n%Bj at k = 32s + 8g + 0..7
 //   tiled weights       [K/(32 KG) k-groups][N/16 row blocks][KG][64 lanes][8]
 //                       bf16 (KG = 1 by default): lane (g,m) of tile (s, rb)
 //                       holds W[16*rb + m][32s + 8g + 0..7].  A wave's A
@@ -28,6 +31,8 @@
 // vx27_hip_gemv_bf16 call): gemv_part_rm, 4-wave workgroups of 64 rows over
 // K segments, partial sums [pseg][N][16] reduced by gemv_reduce_store in a
 // fixed order.
+#include <algorithm>
+
 #include "vx_gemv_body.h"
 
 namespace {
@@ -40,11 +45,13 @@ constexpr int RB = 4;   // row blocks per workgroup of the row-major path
 #define VX_GEMV_MINKS 8      // at least this many 32-wide k-steps per wave
 #endif
 
-// pack activations: grid (K/32), block 64; lane (g,n) writes its 8 elements
+// pack activations: grid (K/32, groups), block 64; lane (g,n) of group j
+// writes its 8 elements
 __global__ __launch_bounds__(64) void pack_x(const float *x, size_t x_stride, int B, uint16_t *out) {
-    const int s = blockIdx.x, lane = threadIdx.x, g = lane >> 4, n = lane & 15;
-    if (n >= 3 * B) return;   // padding columns feed unread output columns
-    const int p = n / B, b = n % B;
+    const int s = blockIdx.x, j = blockIdx.y, lane = threadIdx.x, g = lane >> 4, n = lane & 15;
+    const int Bj = min(VX_PACK_GV, B - VX_PACK_GV * j);
+    if (n >= 3 * Bj) return;   // padding columns feed unread output columns
+    const int p = n / Bj, b = VX_PACK_GV * j + n % Bj;
     const float *xr = x + (size_t)b * x_stride + 32 * s + 8 * g;
     uint16_t v[8];
 #pragma unroll
@@ -55,7 +62,7 @@ __global__ __launch_bounds__(64) void pack_x(const float *x, size_t x_stride, in
     w.y = v[2] | ((uint32_t)v[3] << 16);
     w.z = v[4] | ((uint32_t)v[5] << 16);
     w.w = v[6] | ((uint32_t)v[7] << 16);
-    *(uint4 *)(out + ((size_t)s * 64 + lane) * 8) = w;
+    *(uint4 *)(out + (((size_t)s * gridDim.y + j) * 64 + lane) * 8) = w;
 }
 
 // row-major W [N][K] -> tiled; grid (N/16, K/32), block 64
@@ -65,10 +72,10 @@ __global__ __launch_bounds__(64) void pack_w(const uint16_t *W, int K, uint16_t 
     *(uint4 *)(Wt + vx_tile_off(s, rb, gridDim.x, vx_gemv_kg(K)) + lane * 8) = v;
 }
 
-template <int RBW, bool NT>
-__global__ __launch_bounds__(1024) void gemv_wk_store(const uint16_t *W, int N, int K, const uint16_t *xp, int B,
-                                                      WkStore epi) {
-    vx_gemv_wk_body<RBW, NT>(W, N, K, xp, B, epi);
+template <int RBW, bool NT, int G>
+__global__ __launch_bounds__(1024) void gemv_wk_store(const uint16_t *W, int N, int K, const uint16_t *xp, int Gt,
+                                                      int g0, int B, WkStore epi) {
+    vx_gemv_wk_body<RBW, NT, G>(W, N, K, xp, Gt, g0, B, epi);
 }
 
 // Row-major W: grid (ceil(N/64), ceil(n_seg/4)), block 256; wave w takes K
@@ -131,11 +138,13 @@ __global__ __launch_bounds__(256) void gemv_reduce_store(const float *part, int 
 #ifndef VX_GEMV_NT_MIB
 #define VX_GEMV_NT_MIB 32   // matrices of at least this many MiB are read with streaming loads
 #endif
-WkPlan vx_gemv_wk_plan(int N, int K, int n_cu) {
+WkPlan vx_gemv_wk_plan(int N, int K, int n_cu, int G) {
     const int nb = N / 16;
+    const int max_rb = VX_WK_MAX_RB / G;   // RB x G accumulator tiles (LDS reduction space)
     WkPlan p;
-    p.rb = VX_WK_MAX_RB;
-    for (int rb = 1; rb <= VX_WK_MAX_RB; rb++)
+    p.g = G;
+    p.rb = max_rb;
+    for (int rb = 1; rb <= max_rb; rb++)
         if ((nb + rb - 1) / rb <= n_cu) {
             p.rb = rb;
             break;
@@ -149,10 +158,15 @@ WkPlan vx_gemv_wk_plan(int N, int K, int n_cu) {
 
 int vx_gemv_store(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const uint16_t *packed, int B, float *y,
                   size_t y_stride) {
-    VX_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 32 == 0 && B >= 1 && B <= 5,
-               "gemv: N must be a multiple of 16, K of 32, B in 1..5 (N=%d K=%d B=%d)", N, K, B);
-    const WkPlan p = vx_gemv_wk_plan(N, K, ctx->n_cu);
-    VX_WK_DISPATCH(ctx, gemv_wk_store, p, W, N, K, packed, B, (WkStore{y, y_stride}));
+    VX_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 32 == 0 && B >= 1,
+               "gemv: N must be a multiple of 16, K of 32, B >= 1 (N=%d K=%d B=%d)", N, K, B);
+    const int Gt = vx_pack_groups(B);
+    for (int g0 = 0; g0 < Gt; g0 += 3) {   // passes of up to three groups (15 vectors)
+        const int G = std::min(3, Gt - g0), b0 = g0 * VX_PACK_GV;
+        const int Bp = std::min(B - b0, G * VX_PACK_GV);
+        const WkPlan p = vx_gemv_wk_plan(N, K, ctx->n_cu, G);
+        VX_WK_DISPATCH(ctx, gemv_wk_store, p, W, N, K, packed, Gt, g0, Bp, (WkStore{y, y_stride, b0}));
+    }
     return 0;
 }
 
@@ -173,11 +187,13 @@ int vx_gemv_plan(int N, int K, int *n_seg, int *ks_per) {
 
 int vx_gemv_pseg(int n_seg) { return (n_seg + 3) / 4; }
 size_t vx_gemv_part_bytes(int N, int n_seg) { return (size_t)vx_gemv_pseg(n_seg) * N * 16 * sizeof(float); }
-size_t vx_pack_bytes(int K) { return (size_t)(K / 32) * 64 * 8 * sizeof(uint16_t); }
+size_t vx_pack_bytes(int K, int B) {
+    return (size_t)(K / 32) * vx_pack_groups(B) * 64 * 8 * sizeof(uint16_t);
+}
 
 int vx_pack(vx27_hip_ctx *ctx, const float *x, size_t x_stride, int B, int K, uint16_t *packed) {
-    VX_REQUIRE(B >= 1 && B <= 5 && K % 32 == 0, "pack: need B <= 5, K %% 32 == 0");
-    VX_LAUNCH(ctx, pack_x, dim3(K / 32), dim3(64), x, x_stride, B, packed);
+    VX_REQUIRE(B >= 1 && K % 32 == 0, "pack: need B >= 1, K %% 32 == 0");
+    VX_LAUNCH(ctx, pack_x, dim3(K / 32, vx_pack_groups(B)), dim3(64), x, x_stride, B, packed);
     return 0;
 }
 
@@ -194,18 +210,22 @@ extern "C" int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, i
                                   size_t x_stride, int B, float *y, size_t y_stride) {
     if (vx_ctx_enter(ctx)) return -1;
     VX_REQUIRE(W && x && y, "vx27_hip_gemv_bf16: null pointer");
-    VX_REQUIRE(B >= 1 && B <= 5, "vx27_hip_gemv_bf16: B must be 1..5 (got %d)", B);
+    VX_REQUIRE(B >= 1, "vx27_hip_gemv_bf16: B must be >= 1 (got %d)", B);
     int n_seg, ks_per;
     if (vx_gemv_plan(N, K, &n_seg, &ks_per)) return -1;
-    const size_t pk = (vx_pack_bytes(K) + 255) & ~(size_t)255;
+    const size_t pk = (vx_pack_bytes(K, VX_PACK_GV) + 255) & ~(size_t)255;
     void *scr;
     if (vx_ctx_scratch(ctx, pk + vx_gemv_part_bytes(N, n_seg), &scr)) return -1;
     uint16_t *packed = (uint16_t *)scr;
     float *part = (float *)((char *)scr + pk);
-    if (vx_pack(ctx, x, x_stride, B, K, packed)) return -1;
-    const dim3 grid((N + 16 * RB - 1) / (16 * RB), vx_gemv_pseg(n_seg));
-    VX_LAUNCH(ctx, gemv_part_rm, grid, dim3(256), W, N, K, packed, ks_per, n_seg, part);
-    VX_LAUNCH(ctx, gemv_reduce_store, dim3((N + 255) / 256), dim3(256), part, N, B, vx_gemv_pseg(n_seg), y,
-              y_stride);
+    // passes of up to 5 vectors (one packed group each)
+    for (int b0 = 0; b0 < B; b0 += VX_PACK_GV) {
+        const int Bp = std::min(VX_PACK_GV, B - b0);
+        if (vx_pack(ctx, x + (size_t)b0 * x_stride, x_stride, Bp, K, packed)) return -1;
+        const dim3 grid((N + 16 * RB - 1) / (16 * RB), vx_gemv_pseg(n_seg));
+        VX_LAUNCH(ctx, gemv_part_rm, grid, dim3(256), W, N, K, packed, ks_per, n_seg, part);
+        VX_LAUNCH(ctx, gemv_reduce_store, dim3((N + 255) / 256), dim3(256), part, N, Bp, vx_gemv_pseg(n_seg),
+                  y + (size_t)b0 * y_stride, y_stride);
+    }
     return 0;
 }

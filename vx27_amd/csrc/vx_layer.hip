@@ -35,23 +35,25 @@ struct DnInArgs {
     const float *A_log, *dt_bias;
     float *act, *z;
     double2 *gates;
+    int b0;   // first vector of this pass (the pass's B vectors are b0 .. b0+B-1)
 };
 
 // Epilogue of the stacked DeltaNet input projection [qkv | z | a | b]
-// (vx27_qfwd.c:102-117), one thread per row, all sequences:
+// (vx27_qfwd.c:102-117), one thread per row, all vectors of the pass:
 //   q|k|v rows: causal conv + SiLU (conv state in place) -> act; the q/k
 //               normalisation chain runs in the recurrence kernel, which
 //               has whole heads
 //   z rows:     copied out; a rows: decay = exp(g_log); b rows: beta
 // The conv weights (raw bits, converted after the loop so that nothing
-// waits on them) and the conv state of a q|k|v row are loaded before the
-// projection's K loop.
-constexpr int DN_MAXB = 5;
+// waits on them) and the conv state of a q|k|v row (first DN_PREB vectors
+// of the pass) are loaded before the projection's K loop.
+constexpr int DN_MAXB = 15;   // vectors per GEMV pass (three groups of 5)
+constexpr int DN_PREB = 5;
 struct DnInEpi {
     DnInArgs a;
     struct Pre {
         uint32_t w[4];   // bf16: 4 values in w[0..1]; f32: 4 values
-        float st[DN_MAXB][3];
+        float st[DN_PREB][3];
     };
     __device__ __forceinline__ Pre prefetch(int row0, int rows, int tid) const {
         Pre p;
@@ -69,9 +71,9 @@ struct DnInEpi {
                 p.w[3] = u.w;
             }
 #pragma unroll
-            for (int b = 0; b < DN_MAXB; b++)
+            for (int b = 0; b < DN_PREB; b++)
                 if (b < a.B) {
-                    const float *sp = a.conv_state + ((size_t)b * a.C + n) * 3;
+                    const float *sp = a.conv_state + ((size_t)(a.b0 + b) * a.C + n) * 3;
                     p.st[b][0] = sp[0];
                     p.st[b][1] = sp[1];
                     p.st[b][2] = sp[2];
@@ -79,8 +81,9 @@ struct DnInEpi {
         }
         return p;
     }
-    template <int RB>
-    __device__ __forceinline__ void operator()(int row0, int rows, const WkRows<RB> &c, int tid, const Pre &p) const {
+    template <int RB, int G>
+    __device__ __forceinline__ void operator()(int row0, int rows, const WkRows<RB, G> &c, int tid,
+                                               const Pre &p) const {
         if (tid >= rows) return;
         const int n = row0 + tid;
         float v[DN_MAXB];
@@ -101,34 +104,39 @@ struct DnInEpi {
 #pragma unroll
             for (int b = 0; b < DN_MAXB; b++)
                 if (b < a.B) {
-                    float *sp = a.conv_state + ((size_t)b * a.C + n) * 3;
-                    float st[3] = {p.st[b][0], p.st[b][1], p.st[b][2]};
-                    a.act[(size_t)b * a.C + n] = conv_step(st, w, v[b]);
+                    float *sp = a.conv_state + ((size_t)(a.b0 + b) * a.C + n) * 3;
+                    float st[3];
+                    if (b < DN_PREB) {
+                        st[0] = p.st[b][0]; st[1] = p.st[b][1]; st[2] = p.st[b][2];
+                    } else {
+                        st[0] = sp[0]; st[1] = sp[1]; st[2] = sp[2];
+                    }
+                    a.act[(size_t)(a.b0 + b) * a.C + n] = conv_step(st, w, v[b]);
                     sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
                 }
         } else if (n < a.C + a.vd) {         // z
 #pragma unroll
             for (int b = 0; b < DN_MAXB; b++)
-                if (b < a.B) a.z[(size_t)b * a.vd + (n - a.C)] = v[b];
+                if (b < a.B) a.z[(size_t)(a.b0 + b) * a.vd + (n - a.C)] = v[b];
         } else if (n < a.C + a.vd + a.nv) {  // a -> decay = exp(g_log), vx27_deltanet.c:68,82
             const int vh = n - a.C - a.vd;
             const double eA = exp((double)a.A_log[vh]), dtb = (double)a.dt_bias[vh];
 #pragma unroll
             for (int b = 0; b < DN_MAXB; b++)
-                if (b < a.B) a.gates[(size_t)b * a.nv + vh].y = exp(-eA * softplus_d((double)v[b] + dtb));
+                if (b < a.B) a.gates[(size_t)(a.b0 + b) * a.nv + vh].y = exp(-eA * softplus_d((double)v[b] + dtb));
         } else {                             // b -> beta = sigmoid(b), vx27_deltanet.c:67
             const int vh = n - a.C - a.vd - a.nv;
 #pragma unroll
             for (int b = 0; b < DN_MAXB; b++)
-                if (b < a.B) a.gates[(size_t)b * a.nv + vh].x = 1.0 / (1.0 + exp(-(double)v[b]));
+                if (b < a.B) a.gates[(size_t)(a.b0 + b) * a.nv + vh].x = 1.0 / (1.0 + exp(-(double)v[b]));
         }
     }
 };
 
-template <int RBW, bool NT>
-__global__ __launch_bounds__(1024) void gemv_dn_in(const uint16_t *W, int N, int K, const uint16_t *xp, int B,
-                                                   DnInEpi epi) {
-    vx_gemv_wk_body<RBW, NT>(W, N, K, xp, B, epi);
+template <int RBW, bool NT, int G>
+__global__ __launch_bounds__(1024) void gemv_dn_in(const uint16_t *W, int N, int K, const uint16_t *xp, int Gt,
+                                                   int g0, int B, DnInEpi epi) {
+    vx_gemv_wk_body<RBW, NT, G>(W, N, K, xp, Gt, g0, B, epi);
 }
 
 __global__ void advance_pos_kernel(int *pos, int B) {
@@ -160,11 +168,11 @@ __global__ void fill_bf16_kernel(uint16_t *p, size_t n, uint64_t seed, float mea
 
 }  // namespace
 
-extern "C" size_t vx27_hip_pack_bytes(int K) { return vx_pack_bytes(K); }
+extern "C" size_t vx27_hip_pack_bytes(int K, int B) { return vx_pack_bytes(K, B); }
 
 extern "C" int vx27_hip_pack_x(vx27_hip_ctx *ctx, const float *x, int B, int K, uint16_t *packed) {
     if (vx_ctx_enter(ctx)) return -1;
-    VX_REQUIRE(x && packed && B >= 1 && B <= 5, "vx27_hip_pack_x: bad arguments");
+    VX_REQUIRE(x && packed && B >= 1, "vx27_hip_pack_x: bad arguments");
     return vx_pack(ctx, x, (size_t)K, B, K, packed);
 }
 
@@ -172,7 +180,7 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     if (vx_ctx_enter(ctx)) return -1;
     VX_REQUIRE(d != nullptr, "vx27_hip_dn_layer_decode: null descriptor");
     VX_REQUIRE(d->hd == HD, "vx27_hip_dn_layer_decode: hd must be 128");
-    VX_REQUIRE(d->B >= 1 && d->B <= 5, "vx27_hip_dn_layer_decode: B must be 1..5 (got %d)", d->B);
+    VX_REQUIRE(d->B >= 1, "vx27_hip_dn_layer_decode: B must be >= 1 (got %d)", d->B);
     VX_REQUIRE(d->nqk >= 1 && d->nv % d->nqk == 0 && d->nv % 8 == 0,
                "vx27_hip_dn_layer_decode: nv must be a multiple of nqk and of 8 (nqk=%d nv=%d)", d->nqk, d->nv);
     VX_REQUIRE(d->hidden > 0 && d->hidden % 32 == 0, "vx27_hip_dn_layer_decode: hidden must be a multiple of 32");
@@ -184,10 +192,10 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     VX_REQUIRE(((uintptr_t)d->conv_w & 15) == 0, "vx27_hip_dn_layer_decode: conv_w must be 16-byte aligned");
     const int B = d->B, nv = d->nv, qd = d->nqk * HD, vd = nv * HD, C = 2 * qd + vd, H = d->hidden;
     const int Nin = C + vd + 2 * nv;
-    const size_t pk_x = d->x_packed ? 0 : align256(vx_pack_bytes(H));
+    const size_t pk_x = d->x_packed ? 0 : align256(vx_pack_bytes(H, B));
     const size_t act_b = align256((size_t)B * C * 4), z_b = align256((size_t)B * vd * 4);
     const size_t g_b = align256((size_t)B * nv * sizeof(double2));
-    const size_t pk_o = align256(vx_pack_bytes(vd));
+    const size_t pk_o = align256(vx_pack_bytes(vd, B));
     void *scr;
     if (vx_ctx_scratch(ctx, pk_x + act_b + z_b + g_b + pk_o, &scr)) return -1;
     char *p = (char *)scr;
@@ -199,11 +207,14 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     uint16_t *op = (uint16_t *)p;
 
     if (!d->x_packed && vx_pack(ctx, d->x, (size_t)H, B, H, xp)) return -1;
-    {
-        const DnInArgs ea = {B, C, vd, nv, d->conv_state, d->conv_w, d->conv_w_dtype == VX27_BF16,
-                             d->A_log, d->dt_bias, act, z, gates};
-        const WkPlan wp = vx_gemv_wk_plan(Nin, H, ctx->n_cu);
-        VX_WK_DISPATCH(ctx, gemv_dn_in, wp, d->w_in, Nin, H, xp, B, (DnInEpi{ea}));
+    const int Gt = vx_pack_groups(B);
+    for (int g0 = 0; g0 < Gt; g0 += 3) {   // passes of up to three groups (15 vectors) over W_in
+        const int G = g0 + 3 <= Gt ? 3 : Gt - g0, b0 = g0 * VX_PACK_GV;
+        const int Bp = B - b0 < G * VX_PACK_GV ? B - b0 : G * VX_PACK_GV;
+        const DnInArgs ea = {Bp, C, vd, nv, d->conv_state, d->conv_w, d->conv_w_dtype == VX27_BF16,
+                             d->A_log, d->dt_bias, act, z, gates, b0};
+        const WkPlan wp = vx_gemv_wk_plan(Nin, H, ctx->n_cu, G);
+        VX_WK_DISPATCH(ctx, gemv_dn_in, wp, d->w_in, Nin, H, xp, Gt, g0, Bp, (DnInEpi{ea}));
     }
 
     DnArgs ra = {};
@@ -222,7 +233,7 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
 extern "C" int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer_desc *d) {
     if (vx_ctx_enter(ctx)) return -1;
     VX_REQUIRE(d != nullptr, "vx27_hip_gqa_layer_decode: null descriptor");
-    VX_REQUIRE(d->B >= 1 && d->B <= 5, "vx27_hip_gqa_layer_decode: B must be 1..5 (got %d)", d->B);
+    VX_REQUIRE(d->B >= 1, "vx27_hip_gqa_layer_decode: B must be >= 1 (got %d)", d->B);
     VX_REQUIRE(d->hidden > 0 && d->hidden % 32 == 0 && d->hd == 256,
                "vx27_hip_gqa_layer_decode: hidden must be a multiple of 32 and hd 256");
     VX_REQUIRE(d->x && d->w_qkv && d->w_o && d->out, "vx27_hip_gqa_layer_decode: null pointer in descriptor");
@@ -238,9 +249,9 @@ extern "C" int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer
     g.q_norm_w = d->q_norm_w; g.k_norm_w = d->k_norm_w;
     g.k_cache = d->k_cache; g.v_cache = d->v_cache; g.n_split = d->n_split;
 
-    const size_t pk_x = d->x_packed ? 0 : align256(vx_pack_bytes(H));
+    const size_t pk_x = d->x_packed ? 0 : align256(vx_pack_bytes(H, B));
     const size_t y_b = align256((size_t)B * Nqkv * 4);
-    const size_t pk_a = align256(vx_pack_bytes(Ka));
+    const size_t pk_a = align256(vx_pack_bytes(Ka, B));
     // placeholders so the scratch size of the attention step can be planned
     g.q = g.gate = g.k_new = g.v_new = (const float *)1;
     const size_t gq_b = align256(vx_gqa_scratch_bytes(&g));

@@ -107,7 +107,7 @@ _SIGS = {
     "vx27_hip_gemv_bf16": (C.c_int, [VP, VP, C.c_int, C.c_int, VP, C.c_size_t, C.c_int, VP, C.c_size_t]),
     "vx27_hip_dn_layer_decode": (C.c_int, [VP, C.POINTER(DnLayerDesc)]),
     "vx27_hip_gqa_layer_decode": (C.c_int, [VP, C.POINTER(GqaLayerDesc)]),
-    "vx27_hip_pack_bytes": (C.c_size_t, [C.c_int]),
+    "vx27_hip_pack_bytes": (C.c_size_t, [C.c_int, C.c_int]),
     "vx27_hip_pack_weights_bf16": (C.c_int, [VP, VP, C.c_int, C.c_int, VP]),
     "vx27_hip_pack_x": (C.c_int, [VP, VP, C.c_int, C.c_int, VP]),
     "vx27_hip_advance_pos": (C.c_int, [VP, VP, C.c_int]),

@@ -40,7 +40,7 @@ class MixerStack:
         s = 5000
         fill = ctx.fill_normal
         self.x = ctx.buf(B * H * 4)
-        self.xp = ctx.buf(L.lib().vx27_hip_pack_bytes(H))
+        self.xp = ctx.buf(L.lib().vx27_hip_pack_bytes(H, B))
         self.out = ctx.buf(n_layers * B * H * 4)
         self.pos = ctx.put(p0)
         self.layers = []
