@@ -367,6 +367,50 @@ typedef struct {
 } vx27_gqa_layer_desc;
 int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer_desc *d);
 
+/* The DeltaNet layer for T tokens of each of B sequences, in order: the
+ * device form of vx27_qlayer_batch's DeltaNet branch (vx27_qfwd.c:249-313)
+ * as vx27_engine_batch_step runs it per layer (vx27_run.c:187-238):
+ * [qkv|z|a|b] = W_in x for every token, then vx27_hip_dn_prefill with every
+ * glue stage (and the checkpoints, when given), then out = W_out o.  The
+ * projections stream their weights once per 15 tokens, so this is for short
+ * windows such as an MTP verify batch (the reference's batch is at most 8
+ * tokens); a long prompt's projections belong in a GEMM.  x and out are
+ * [B][T][hidden]; the other fields as vx27_dn_layer_desc; flags
+ * VX27_DN_EXACT / VX27_DN_BF16 choose the prefill algorithm (checkpoints
+ * imply the exact one, bit-identical to T vx27_hip_dn_layer_decode calls). */
+typedef struct {
+    int B, T, nqk, nv, hd, hidden;
+    unsigned flags;
+    const float *x;
+    const uint16_t *w_in, *w_out;   /* tiled */
+    const void *conv_w;
+    int conv_w_dtype;
+    const float *A_log, *dt_bias, *norm_w;
+    float *S, *conv_state;
+    float *out;
+    float *S_ckpt, *conv_ckpt;      /* optional: [B][T][nv][hd][hd], [B][T][C][3] */
+} vx27_dn_layer_prefill_desc;
+int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_prefill_desc *d);
+
+/* The gated GQA layer for T tokens of each of B sequences at positions
+ * pos0 .. pos0+T-1 (vx27_qlayer_batch's attention branch,
+ * vx27_qfwd.c:314-376): [q|gate|k|v] = W_qkv x for every token, rounded to
+ * bf16, vx27_hip_gqa_prefill (cache rows written, causal attention, gate),
+ * out = W_o att.  Same window note as vx27_hip_dn_layer_prefill; flags as
+ * vx27_gqa_prefill_desc. */
+typedef struct {
+    int B, T, n_q, n_kv, hd, hidden, rope_dim;
+    float rope_theta, rope_yarn;
+    int L, pos0;
+    unsigned flags;
+    const float *x;                 /* [B][T][hidden] */
+    const uint16_t *w_qkv, *w_o;    /* tiled */
+    const float *q_norm_w, *k_norm_w;
+    uint16_t *k_cache, *v_cache;
+    float *out;                     /* [B][T][hidden] */
+} vx27_gqa_layer_prefill_desc;
+int vx27_hip_gqa_layer_prefill(vx27_hip_ctx *ctx, const vx27_gqa_layer_prefill_desc *d);
+
 /* Pack x [B][K] once for several layers that read the same input
  * (x_packed of the layer descriptors); packed holds vx27_hip_pack_bytes(K, B). */
 size_t vx27_hip_pack_bytes(int K, int B);

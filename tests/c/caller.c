@@ -37,6 +37,7 @@ int main(void) {
         REF(vx27_hip_dn_decode), REF(vx27_hip_dn_prefill), REF(vx27_hip_dn_commit), REF(vx27_hip_gqa_decode), REF(vx27_hip_gqa_decode_noalloc), REF(vx27_hip_gqa_prefill),
         REF(vx27_hip_kv_write), REF(vx27_hip_kv_read), REF(vx27_hip_rope_table), REF(vx27_hip_gemv_bf16),
         REF(vx27_hip_pack_weights_bf16), REF(vx27_hip_dn_layer_decode), REF(vx27_hip_gqa_layer_decode),
+        REF(vx27_hip_dn_layer_prefill), REF(vx27_hip_gqa_layer_prefill),
         REF(vx27_hip_pack_bytes), REF(vx27_hip_pack_x), REF(vx27_hip_advance_pos), REF(vx27_hip_graph_begin),
         REF(vx27_hip_graph_end), REF(vx27_hip_graph_launch), REF(vx27_hip_graph_destroy),
         REF(vx27_hip_fill_normal_f32), REF(vx27_hip_fill_normal_bf16), REF(vx27_hip_step_exact),

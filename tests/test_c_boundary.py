@@ -18,6 +18,8 @@ STRUCTS = {   # C typedef -> ctypes mirror
     "vx27_gqa_prefill_desc": "GqaPrefillDesc",
     "vx27_dn_layer_desc": "DnLayerDesc",
     "vx27_gqa_layer_desc": "GqaLayerDesc",
+    "vx27_dn_layer_prefill_desc": "DnLayerPrefillDesc",
+    "vx27_gqa_layer_prefill_desc": "GqaLayerPrefillDesc",
 }
 
 

@@ -124,3 +124,8 @@ int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a);
 // Whether vx_dn_recurrence runs a call as one single-step kernel (which can
 // also map the gates itself, with gates == NULL).
 bool vx_dn_single_step(const DnArgs &a);
+
+// The DeltaNet prefill on caller-provided scratch (vx_dn_prefill.hip), for
+// entry points that hold other scratch of their own at the same time.
+size_t vx_dn_prefill_scratch(const vx27_dn_prefill_desc *d);
+int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *scr);

@@ -1235,15 +1235,31 @@ __global__ __launch_bounds__(256) void dn_commit_kernel(int T, size_t s_elems, s
 
 }  // namespace
 
+// Scratch layout of one prefill call (sizes in bytes, 256-aligned pieces).
+static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
+static bool dn_prefill_is_exact(const vx27_dn_prefill_desc *d) {
+    return (d->flags & VX27_DN_EXACT) || d->S_ckpt || d->conv_ckpt;
+}
+size_t vx_dn_prefill_scratch(const vx27_dn_prefill_desc *d) {
+    const int qd = d->nqk * HD, vd = d->nv * HD, C = 2 * qd + vd;
+    const size_t rows = (size_t)d->B * d->T;
+    if (dn_prefill_is_exact(d))
+        return al256(rows * d->nv * sizeof(double2)) + al256((size_t)d->B * vd * sizeof(float)) + rows * C * sizeof(float);
+    const int NC = (d->T + CH - 1) / CH;
+    const bool x3 = !(d->flags & VX27_DN_BF16);
+    const size_t n_rec = (size_t)d->B * d->nv * NC;
+    const bool glue = (d->flags & (VX27_DN_CONV | VX27_DN_PRE_RMS | VX27_DN_PRE_L2)) != 0;
+    return al256(n_rec * (x3 ? XREC : REC)) + al256(n_rec * sizeof(float)) +
+           (glue ? rows * C * sizeof(uint16_t) * (x3 ? 2 : 1) : 0);
+}
+
 // The exact path: the decode kernels token by token (prefill layout).
-static int dn_prefill_exact(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d) {
+static int dn_prefill_exact(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *scr) {
     const int qd = d->nqk * HD, vd = d->nv * HD, C = 2 * qd + vd;
     const bool conv = (d->flags & VX27_DN_CONV) != 0;
     const size_t rows = (size_t)d->B * d->T;
-    const size_t gate_bytes = (rows * d->nv * sizeof(double2) + 255) & ~(size_t)255;
-    const size_t opre_bytes = ((size_t)d->B * vd * sizeof(float) + 255) & ~(size_t)255;
-    void *scr;
-    if (vx_ctx_scratch(ctx, gate_bytes + opre_bytes + rows * C * sizeof(float), &scr)) return -1;
+    const size_t gate_bytes = al256(rows * d->nv * sizeof(double2));
+    const size_t opre_bytes = al256((size_t)d->B * vd * sizeof(float));
     double2 *gates = (double2 *)scr;
     float *act = (float *)((char *)scr + gate_bytes + opre_bytes);
     const size_t n_gate = rows * d->nv;
@@ -1286,8 +1302,7 @@ static int dn_prefill_exact(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d) {
     return 0;
 }
 
-extern "C" int vx27_hip_dn_prefill(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d) {
-    if (vx_ctx_enter(ctx)) return -1;
+static int dn_prefill_check(const vx27_dn_prefill_desc *d) {
     VX_REQUIRE(d, "vx27_hip_dn_prefill: null descriptor");
     VX_REQUIRE(d->hd == HD, "vx27_hip_dn_prefill: head_dim must be 128 (got %d)", d->hd);
     VX_REQUIRE(d->B >= 1 && d->T >= 1 && d->nqk >= 1 && d->nv >= d->nqk && d->nv % d->nqk == 0 && d->nv <= 4096,
@@ -1306,20 +1321,22 @@ extern "C" int vx27_hip_dn_prefill(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc
     if (d->flags & (VX27_DN_PRE_RMS | VX27_DN_OUT_GATE))
         VX_REQUIRE(d->norm_w != nullptr, "vx27_hip_dn_prefill: norm_w required by PRE_RMS/OUT_GATE");
     if (d->flags & VX27_DN_OUT_GATE) VX_REQUIRE(d->z != nullptr, "vx27_hip_dn_prefill: z required by OUT_GATE");
-    if ((d->flags & VX27_DN_EXACT) || d->S_ckpt || d->conv_ckpt) return dn_prefill_exact(ctx, d);
+    return 0;
+}
 
+// The prefill on caller-provided scratch of vx_dn_prefill_scratch(d) bytes.
+int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *scr) {
+    if (dn_prefill_check(d)) return -1;
+    if (dn_prefill_is_exact(d)) return dn_prefill_exact(ctx, d, scr);
+    const bool conv = (d->flags & VX27_DN_CONV) != 0;
     const int NC = (d->T + CH - 1) / CH;
     const bool x3 = !(d->flags & VX27_DN_BF16);   // split (bf16x3) products unless asked for bf16
-    const size_t rec_bytes = x3 ? XREC : REC;
     const size_t n_rec = (size_t)d->B * d->nv * NC;
-    const size_t gc_off = (n_rec * rec_bytes + 255) & ~(size_t)255;
+    const size_t gc_off = al256(n_rec * (x3 ? XREC : REC));
     const bool glue = conv || (d->flags & (VX27_DN_PRE_RMS | VX27_DN_PRE_L2));
     const int qd = d->nqk * HD, vd = d->nv * HD, C = 2 * qd + vd;
-    const size_t glue_off = (gc_off + n_rec * sizeof(float) + 255) & ~(size_t)255;
+    const size_t glue_off = gc_off + al256(n_rec * sizeof(float));
     const size_t rows = (size_t)d->B * d->T;
-    const size_t glue_bytes = glue ? rows * C * sizeof(uint16_t) * (x3 ? 2 : 1) : 0;
-    void *scr;
-    if (vx_ctx_scratch(ctx, glue_off + glue_bytes, &scr)) return -1;
     const uint16_t *q = d->q, *k = d->k, *v = d->v;
     const uint16_t *ql = nullptr, *kl = nullptr, *vl = nullptr;
     if (glue) {   // conv and pre-norms in fp32, then q, k, v as bf16 (hi, and lo for the split form)
@@ -1356,6 +1373,14 @@ extern "C" int vx27_hip_dn_prefill(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc
         VX_LAUNCH(ctx, dnp_out_gate, dim3((unsigned)((nrow + 3) / 4)), dim3(256), nrow, d->z, d->norm_w, d->out);
     }
     return 0;
+}
+
+extern "C" int vx27_hip_dn_prefill(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d) {
+    if (vx_ctx_enter(ctx)) return -1;
+    if (dn_prefill_check(d)) return -1;
+    void *scr;
+    if (vx_ctx_scratch(ctx, vx_dn_prefill_scratch(d), &scr)) return -1;
+    return vx_dn_prefill_into(ctx, d, scr);
 }
 
 extern "C" int vx27_hip_dn_commit(vx27_hip_ctx *ctx, int B, int T, int nv, int hd, int C, const int *m,

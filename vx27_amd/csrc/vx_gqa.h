@@ -42,3 +42,6 @@ int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uin
 // Looks up the per-device address of the no-allocation decode scratch
 // (vx_gqa_decode.hip); called by vx27_hip_open with the device current.
 int vx_noalloc_init(int device);
+// The prefill on caller-provided scratch (vx_gqa_prefill.hip).
+size_t vx_gqa_prefill_scratch(const vx27_gqa_prefill_desc *d);
+int vx_gqa_prefill_into(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d, void *scr);

@@ -1026,8 +1026,7 @@ void vx_gqp_sched_free(vx27_hip_ctx *ctx) {
     ctx->gqp_scheds.clear();
 }
 
-extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d) {
-    if (vx_ctx_enter(ctx)) return -1;
+static int gqa_prefill_check(const vx27_gqa_prefill_desc *d) {
     VX_REQUIRE(d, "vx27_hip_gqa_prefill: null descriptor");
     VX_REQUIRE(d->hd == HDG, "vx27_hip_gqa_prefill: hd must be 256 (got %d)", d->hd);
     VX_REQUIRE(d->B >= 1 && d->T >= 1 && d->n_kv >= 1 && d->n_q >= d->n_kv && d->n_q % d->n_kv == 0,
@@ -1053,14 +1052,23 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     VX_REQUIRE(d->q && (d->gate || !gated) && d->k_new && d->v_new && d->q_norm_w && d->k_norm_w && d->k_cache &&
                    d->v_cache && d->out,
                "vx27_hip_gqa_prefill: null pointer in descriptor");
+    return 0;
+}
+
+size_t vx_gqa_prefill_scratch(const vx27_gqa_prefill_desc *d) {
+    return (size_t)d->T * (d->rope_dim / 2 + 1) * sizeof(float2);
+}
+
+// The prefill on caller-provided scratch of vx_gqa_prefill_scratch(d) bytes.
+int vx_gqa_prefill_into(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d, void *scr) {
+    if (gqa_prefill_check(d)) return -1;
+    const bool gated = !(d->flags & VX27_GQA_NO_GATE);
     KvArgs ka = {};
     if (d->rope_dim > 0 && vx_rope_fill(ka.rope, d->rope_dim, d->rope_theta)) return -1;
     ka.T = d->T; ka.n_kv = d->n_kv; ka.rope_dim = d->rope_dim; ka.L = d->L; ka.pos0 = d->pos0;
     ka.flags = d->flags; ka.yarn = d->rope_yarn < 1.0f ? 1.0f : d->rope_yarn;
     ka.k = d->k_new; ka.v = d->v_new; ka.kv_ts = (size_t)d->n_kv * HDG;
     ka.k_norm_w = d->k_norm_w; ka.k_cache = d->k_cache; ka.v_cache = d->v_cache;
-    void *scr;
-    if (vx_ctx_scratch(ctx, (size_t)d->T * (d->rope_dim / 2 + 1) * sizeof(float2), &scr)) return -1;
     ka.cs_tab = (float2 *)scr;
     {
         const int nblk = (d->pos0 + d->T - 1) / VX_GQA_VBLK - d->pos0 / VX_GQA_VBLK + 1;
@@ -1095,3 +1103,12 @@ extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_de
     }
     return 0;
 }
+
+extern "C" int vx27_hip_gqa_prefill(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d) {
+    if (vx_ctx_enter(ctx)) return -1;
+    if (gqa_prefill_check(d)) return -1;
+    void *scr;
+    if (vx_ctx_scratch(ctx, vx_gqa_prefill_scratch(d), &scr)) return -1;
+    return vx_gqa_prefill_into(ctx, d, scr);
+}
+

@@ -166,6 +166,20 @@ __global__ void fill_bf16_kernel(uint16_t *p, size_t n, uint64_t seed, float mea
         p[i] = vx_f32_to_bf16(mean + std * normal_at(seed, i));
 }
 
+// q|gate|k|v projection rows [R][Nq + 2 kvd] fp32 -> bf16 operands of the
+// GQA prefill: qg [R][Nq] (q_proj's interleaved layout kept), k, v [R][kvd].
+// grid (R, ceil((Nq + 2 kvd) / 256)), block 256.
+__global__ __launch_bounds__(256) void qkv_to_bf16(const float *y, int Nq, int kvd, uint16_t *qg, uint16_t *k,
+                                                   uint16_t *v) {
+    const size_t r = blockIdx.x;
+    const int j = blockIdx.y * 256 + threadIdx.x, N = Nq + 2 * kvd;
+    if (j >= N) return;
+    const uint16_t h = vx_f32_to_bf16(y[r * N + j]);
+    if (j < Nq) qg[r * Nq + j] = h;
+    else if (j < Nq + kvd) k[r * kvd + (j - Nq)] = h;
+    else v[r * kvd + (j - Nq - kvd)] = h;
+}
+
 }  // namespace
 
 extern "C" size_t vx27_hip_pack_bytes(int K, int B) { return vx_pack_bytes(K, B); }
@@ -295,4 +309,97 @@ extern "C" int vx27_hip_fill_normal_bf16(vx27_hip_ctx *ctx, uint16_t *p, size_t 
     VX_REQUIRE(p != nullptr, "vx27_hip_fill_normal_bf16: null pointer");
     VX_LAUNCH(ctx, fill_bf16_kernel, dim3(8192), dim3(256), p, n, seed, mean, std);
     return 0;
+}
+
+extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_prefill_desc *d) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(d != nullptr, "vx27_hip_dn_layer_prefill: null descriptor");
+    VX_REQUIRE(d->hd == HD && d->B >= 1 && d->T >= 1 && d->nqk >= 1 && d->nv % d->nqk == 0 && d->hidden > 0 &&
+                   d->hidden % 32 == 0,
+               "vx27_hip_dn_layer_prefill: bad sizes (B=%d T=%d nqk=%d nv=%d hd=%d hidden=%d)", d->B, d->T, d->nqk,
+               d->nv, d->hd, d->hidden);
+    VX_REQUIRE((d->flags & ~(VX27_DN_EXACT | VX27_DN_BF16)) == 0,
+               "vx27_hip_dn_layer_prefill: flags may only be VX27_DN_EXACT, VX27_DN_BF16");
+    VX_REQUIRE(d->x && d->w_in && d->w_out && d->conv_w && d->A_log && d->dt_bias && d->norm_w && d->S &&
+                   d->conv_state && d->out,
+               "vx27_hip_dn_layer_prefill: null pointer in descriptor");
+    const int R = d->B * d->T, nv = d->nv, qd = d->nqk * HD, vd = nv * HD, C = 2 * qd + vd, H = d->hidden;
+    const int Nin = C + vd + 2 * nv;
+    vx27_dn_prefill_desc pd = {};
+    pd.B = d->B; pd.T = d->T; pd.nqk = d->nqk; pd.nv = nv; pd.hd = HD;
+    pd.flags = VX27_DN_CONV | VX27_DN_PRE_RMS | VX27_DN_PRE_L2 | VX27_DN_OUT_GATE | d->flags;
+    pd.S = d->S; pd.A_log = d->A_log; pd.dt_bias = d->dt_bias;
+    pd.conv_state = d->conv_state; pd.conv_w = d->conv_w; pd.conv_w_dtype = d->conv_w_dtype;
+    pd.norm_w = d->norm_w; pd.S_ckpt = d->S_ckpt; pd.conv_ckpt = d->conv_ckpt;
+    const size_t pk_x = align256(vx_pack_bytes(H, R)), y_b = align256((size_t)R * Nin * 4);
+    const size_t x_b = align256((size_t)R * C * 4), z_b = align256((size_t)R * vd * 4);
+    const size_t g_b = align256((size_t)R * nv * 4), o_b = align256((size_t)R * vd * 4);
+    const size_t pk_o = align256(vx_pack_bytes(vd, R));
+    const size_t inner = vx_dn_prefill_scratch(&pd);
+    void *scr;
+    if (vx_ctx_scratch(ctx, pk_x + y_b + x_b + z_b + 2 * g_b + o_b + pk_o + inner, &scr)) return -1;
+    char *p = (char *)scr;
+    uint16_t *xp = (uint16_t *)p; p += pk_x;
+    float *y = (float *)p; p += y_b;
+    float *xq = (float *)p; p += x_b;
+    float *z = (float *)p; p += z_b;
+    float *ga = (float *)p; p += g_b;
+    float *gb = (float *)p; p += g_b;
+    float *o = (float *)p; p += o_b;
+    uint16_t *op = (uint16_t *)p; p += pk_o;
+    // [qkv | z | a | b] = W_in x for all B*T tokens (one pass over W_in per 15 tokens)
+    if (vx_pack(ctx, d->x, (size_t)H, R, H, xp)) return -1;
+    if (vx_gemv_store(ctx, d->w_in, Nin, H, xp, R, y, (size_t)Nin)) return -1;
+    const size_t ys = (size_t)Nin * 4;
+    VX_HIP(hipMemcpy2DAsync(xq, (size_t)C * 4, y, ys, (size_t)C * 4, (size_t)R, hipMemcpyDeviceToDevice, ctx->stream));
+    VX_HIP(hipMemcpy2DAsync(z, (size_t)vd * 4, y + C, ys, (size_t)vd * 4, (size_t)R, hipMemcpyDeviceToDevice,
+                            ctx->stream));
+    VX_HIP(hipMemcpy2DAsync(ga, (size_t)nv * 4, y + C + vd, ys, (size_t)nv * 4, (size_t)R, hipMemcpyDeviceToDevice,
+                            ctx->stream));
+    VX_HIP(hipMemcpy2DAsync(gb, (size_t)nv * 4, y + C + vd + nv, ys, (size_t)nv * 4, (size_t)R,
+                            hipMemcpyDeviceToDevice, ctx->stream));
+    pd.x = xq; pd.z = z; pd.a = ga; pd.b = gb; pd.out = o;
+    if (vx_dn_prefill_into(ctx, &pd, p)) return -1;
+    if (vx_pack(ctx, o, (size_t)vd, R, vd, op)) return -1;
+    return vx_gemv_store(ctx, d->w_out, H, vd, op, R, d->out, (size_t)H);
+}
+
+extern "C" int vx27_hip_gqa_layer_prefill(vx27_hip_ctx *ctx, const vx27_gqa_layer_prefill_desc *d) {
+    if (vx_ctx_enter(ctx)) return -1;
+    VX_REQUIRE(d != nullptr, "vx27_hip_gqa_layer_prefill: null descriptor");
+    VX_REQUIRE(d->B >= 1 && d->T >= 1 && d->hd == 256 && d->hidden > 0 && d->hidden % 32 == 0 && d->n_kv >= 1 &&
+                   d->n_q % d->n_kv == 0,
+               "vx27_hip_gqa_layer_prefill: bad sizes (B=%d T=%d n_q=%d n_kv=%d hd=%d hidden=%d)", d->B, d->T,
+               d->n_q, d->n_kv, d->hd, d->hidden);
+    VX_REQUIRE(d->x && d->w_qkv && d->w_o && d->q_norm_w && d->k_norm_w && d->k_cache && d->v_cache && d->out,
+               "vx27_hip_gqa_layer_prefill: null pointer in descriptor");
+    const int R = d->B * d->T, H = d->hidden, hd = d->hd, kvd = d->n_kv * hd;
+    const int Nq = d->n_q * 2 * hd, Nqkv = Nq + 2 * kvd, Ka = d->n_q * hd;
+    vx27_gqa_prefill_desc gp = {};
+    gp.B = d->B; gp.T = d->T; gp.n_q = d->n_q; gp.n_kv = d->n_kv; gp.hd = hd; gp.rope_dim = d->rope_dim;
+    gp.rope_theta = d->rope_theta; gp.rope_yarn = d->rope_yarn; gp.L = d->L; gp.pos0 = d->pos0; gp.flags = d->flags;
+    gp.q_tok_stride = (size_t)Nq; gp.q_head_stride = (size_t)2 * hd;
+    gp.gate_tok_stride = (size_t)Nq; gp.gate_head_stride = (size_t)2 * hd;
+    gp.q_norm_w = d->q_norm_w; gp.k_norm_w = d->k_norm_w; gp.k_cache = d->k_cache; gp.v_cache = d->v_cache;
+    const size_t pk_x = align256(vx_pack_bytes(H, R)), y_b = align256((size_t)R * Nqkv * 4);
+    const size_t qg_b = align256((size_t)R * Nq * 2), kv_b = align256((size_t)R * kvd * 2);
+    const size_t at_b = align256((size_t)R * Ka * 4), pk_a = align256(vx_pack_bytes(Ka, R));
+    const size_t inner = vx_gqa_prefill_scratch(&gp);
+    void *scr;
+    if (vx_ctx_scratch(ctx, pk_x + y_b + qg_b + 2 * kv_b + at_b + pk_a + inner, &scr)) return -1;
+    char *p = (char *)scr;
+    uint16_t *xp = (uint16_t *)p; p += pk_x;
+    float *y = (float *)p; p += y_b;
+    uint16_t *qg = (uint16_t *)p; p += qg_b;
+    uint16_t *kb = (uint16_t *)p; p += kv_b;
+    uint16_t *vb = (uint16_t *)p; p += kv_b;
+    float *att = (float *)p; p += at_b;
+    uint16_t *ap = (uint16_t *)p; p += pk_a;
+    if (vx_pack(ctx, d->x, (size_t)H, R, H, xp)) return -1;
+    if (vx_gemv_store(ctx, d->w_qkv, Nqkv, H, xp, R, y, (size_t)Nqkv)) return -1;
+    VX_LAUNCH(ctx, qkv_to_bf16, dim3((unsigned)R, (unsigned)((Nqkv + 255) / 256)), dim3(256), y, Nq, kvd, qg, kb, vb);
+    gp.q = qg; gp.gate = qg + hd; gp.k_new = kb; gp.v_new = vb; gp.out = att;
+    if (vx_gqa_prefill_into(ctx, &gp, p)) return -1;
+    if (vx_pack(ctx, att, (size_t)Ka, R, Ka, ap)) return -1;
+    return vx_gemv_store(ctx, d->w_o, H, Ka, ap, R, d->out, (size_t)H);
 }

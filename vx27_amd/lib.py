@@ -72,6 +72,20 @@ class GqaLayerDesc(C.Structure):
                 ("pos", VP), ("k_cache", VP), ("v_cache", VP), ("out", VP), ("n_split", C.c_int)]
 
 
+class DnLayerPrefillDesc(C.Structure):
+    _fields_ = [("B", C.c_int), ("T", C.c_int), ("nqk", C.c_int), ("nv", C.c_int), ("hd", C.c_int),
+                ("hidden", C.c_int), ("flags", C.c_uint), ("x", VP), ("w_in", VP), ("w_out", VP), ("conv_w", VP),
+                ("conv_w_dtype", C.c_int), ("A_log", VP), ("dt_bias", VP), ("norm_w", VP), ("S", VP),
+                ("conv_state", VP), ("out", VP), ("S_ckpt", VP), ("conv_ckpt", VP)]
+
+
+class GqaLayerPrefillDesc(C.Structure):
+    _fields_ = [("B", C.c_int), ("T", C.c_int), ("n_q", C.c_int), ("n_kv", C.c_int), ("hd", C.c_int),
+                ("hidden", C.c_int), ("rope_dim", C.c_int), ("rope_theta", C.c_float), ("rope_yarn", C.c_float),
+                ("L", C.c_int), ("pos0", C.c_int), ("flags", C.c_uint), ("x", VP), ("w_qkv", VP), ("w_o", VP),
+                ("q_norm_w", VP), ("k_norm_w", VP), ("k_cache", VP), ("v_cache", VP), ("out", VP)]
+
+
 _SIGS = {
     "vx27_hip_open": (C.c_int, [C.POINTER(VP), C.c_int, C.c_char_p, C.c_size_t]),
     "vx27_hip_close": (None, [VP]),
@@ -107,6 +121,8 @@ _SIGS = {
     "vx27_hip_gemv_bf16": (C.c_int, [VP, VP, C.c_int, C.c_int, VP, C.c_size_t, C.c_int, VP, C.c_size_t]),
     "vx27_hip_dn_layer_decode": (C.c_int, [VP, C.POINTER(DnLayerDesc)]),
     "vx27_hip_gqa_layer_decode": (C.c_int, [VP, C.POINTER(GqaLayerDesc)]),
+    "vx27_hip_dn_layer_prefill": (C.c_int, [VP, C.POINTER(DnLayerPrefillDesc)]),
+    "vx27_hip_gqa_layer_prefill": (C.c_int, [VP, C.POINTER(GqaLayerPrefillDesc)]),
     "vx27_hip_pack_bytes": (C.c_size_t, [C.c_int, C.c_int]),
     "vx27_hip_pack_weights_bf16": (C.c_int, [VP, VP, C.c_int, C.c_int, VP]),
     "vx27_hip_pack_x": (C.c_int, [VP, VP, C.c_int, C.c_int, VP]),
