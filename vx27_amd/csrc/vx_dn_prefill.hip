@@ -611,6 +611,28 @@ constexpr int X3_SC = X3_GAM + CH * 8;
 constexpr int X3_TOTAL = X3_SC + 5 * CH * 4;
 static_assert(CH * RP * 2 <= HD * TP * 2, "k rows fit the V^T region");
 
+// Transpose a row-major [64 tokens][RP] bf16 tile (128 dims) into
+// [128 dims][TP] (64 tokens) with all 256 threads: thread (wave w, half h,
+// pair q) takes tokens 2q, 2q+1 and dims 32w + 2i + h (i < 16), and packs the
+// two tokens of a dim into one 32-bit LDS store (the halves of a wave write
+// neighbouring dims, whose rows start 36 banks apart).
+__device__ __forceinline__ void tr_rows(const uint16_t *src, uint16_t *dst, int tid) {
+    const int w = tid >> 6, h = (tid >> 5) & 1, q = tid & 31;
+    uint32_t r0[16], r1[16];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint4 a0 = *(const uint4 *)&src[(2 * q) * RP + 32 * w + 8 * k];
+        const uint4 a1 = *(const uint4 *)&src[(2 * q + 1) * RP + 32 * w + 8 * k];
+        r0[4 * k] = a0.x; r0[4 * k + 1] = a0.y; r0[4 * k + 2] = a0.z; r0[4 * k + 3] = a0.w;
+        r1[4 * k] = a1.x; r1[4 * k + 1] = a1.y; r1[4 * k + 2] = a1.z; r1[4 * k + 3] = a1.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const uint32_t x = h ? r0[i] >> 16 : r0[i] & 0xffffu, y = h ? r1[i] >> 16 : r1[i] & 0xffffu;
+        *(uint32_t *)&dst[(32 * w + 2 * i + h) * TP + 2 * q] = x | (y << 16);
+    }
+}
+
 __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
     const int c = blockIdx.x, vh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, m = lane & 15;
@@ -688,24 +710,12 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
             *(uint4 *)&rows[lane * RP + 8 * j] = raw[j];
             *(uint4 *)&rowl[lane * RP + 8 * j] = rawl[j];
         }
-        if (wave == 1) {
-            ik_s[lane] = inv;
-#pragma unroll
-            for (int j = 0; j < 16; j++) {
-                const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
-                const uint32_t l4[4] = {rawl[j].x, rawl[j].y, rawl[j].z, rawl[j].w};
-#pragma unroll
-                for (int e = 0; e < 4; e++) {
-                    K_h[(8 * j + 2 * e) * TP + lane] = (uint16_t)w4[e];
-                    K_h[(8 * j + 2 * e + 1) * TP + lane] = (uint16_t)(w4[e] >> 16);
-                    K_l[(8 * j + 2 * e) * TP + lane] = (uint16_t)l4[e];
-                    K_l[(8 * j + 2 * e + 1) * TP + lane] = (uint16_t)(l4[e] >> 16);
-                }
-            }
-        } else {
-            iq_s[lane] = inv;
-        }
+        if (wave == 1) ik_s[lane] = inv;
+        else iq_s[lane] = inv;
     }
+    __syncthreads();
+    tr_rows(k_rows, K_h, tid);   // K^T (hi, lo) by all waves
+    tr_rows(k_lo, K_l, tid);
     __syncthreads();
 
     char *rec = p.rec + (((size_t)b * p.nv + vh) * p.NC + c) * XREC;
@@ -769,32 +779,35 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
     }
     __syncthreads();   // q and k rows are no longer read
 
-    // ---- phase 3: A (fp32), P hi/lo staging, V^T hi/lo
+    // ---- phase 3: A (fp32), P hi/lo staging.  The per-token scalars of
+    // this lane's rows s and columns r come first, in one batch of LDS
+    // reads; the 16 elements then need no branch (the masked ones are
+    // selected away), so no LDS round trip waits inside the loop.
+    double gs[4], gr[4];
+    float bs[4], iks[4], iqs[4], ikr[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        const int s = wave * 16 + 4 * g + i, r = i * 16 + m;
+        gs[i] = gam_s[s];
+        bs[i] = beta_s[s];
+        iks[i] = ik_s[s];
+        iqs[i] = iq_s[s] * qscale;
+        gr[i] = gam_s[r];
+        ikr[i] = ik_s[r];
+    }
 #pragma unroll
     for (int nb = 0; nb < 4; nb++) {
 #pragma unroll
         for (int i = 0; i < 4; i++) {
             const int s = wave * 16 + 4 * g + i, r = nb * 16 + m;
-            const float ed = r <= s ? expf((float)(gam_s[s] - gam_s[r])) : 0.0f;
-            A_s[s * AP + r] = r < s ? beta_s[s] * ed * ((ik_s[s] * ik_s[r]) * acck[nb][i]) : 0.0f;
-            const float pv = ed * (((iq_s[s] * qscale) * ik_s[r]) * accq[nb][i]);
+            const float e = expf((float)(gs[i] - gr[nb]));   // masked when r > s (may be inf there)
+            const float ed = r <= s ? e : 0.0f;
+            const float av = bs[i] * ed * ((iks[i] * ikr[nb]) * acck[nb][i]);
+            A_s[s * AP + r] = r < s ? av : 0.0f;
+            const float pv = ed * ((iqs[i] * ikr[nb]) * accq[nb][i]);
             const uint16_t ph = vx_f32_to_bf16(pv);
             P_h[s * TP + r] = ph;
             P_l[s * TP + r] = vx_f32_to_bf16(pv - vx_bf16_to_f32(ph));
-        }
-    }
-    if (wave == 3) {
-#pragma unroll
-        for (int j = 0; j < 16; j++) {
-            const uint32_t w4[4] = {raw[j].x, raw[j].y, raw[j].z, raw[j].w};
-            const uint32_t l4[4] = {rawl[j].x, rawl[j].y, rawl[j].z, rawl[j].w};
-#pragma unroll
-            for (int e = 0; e < 4; e++) {
-                V_h[(8 * j + 2 * e) * TP + lane] = (uint16_t)w4[e];
-                V_h[(8 * j + 2 * e + 1) * TP + lane] = (uint16_t)(w4[e] >> 16);
-                V_l[(8 * j + 2 * e) * TP + lane] = (uint16_t)l4[e];
-                V_l[(8 * j + 2 * e + 1) * TP + lane] = (uint16_t)(l4[e] >> 16);
-            }
         }
     }
     __syncthreads();
@@ -804,7 +817,18 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
         *(uint4 *)(rec + X_P + o) = *(const uint4 *)&P_h[rowA * TP + 32 * ks + 8 * g];
         *(uint4 *)(rec + X_P + 8192 + o) = *(const uint4 *)&P_l[rowA * TP + 32 * ks + 8 * g];
     }
-    __syncthreads();   // P staging is read out; the q region takes T
+    __syncthreads();   // P staging is read out: the q region takes the v rows, then T
+    if (wave == 3) {
+#pragma unroll
+        for (int j = 0; j < 16; j++) {
+            *(uint4 *)&q_rows[lane * RP + 8 * j] = raw[j];
+            *(uint4 *)&q_lo[lane * RP + 8 * j] = rawl[j];
+        }
+    }
+    __syncthreads();
+    tr_rows(q_rows, V_h, tid);   // V^T (hi, lo) by all waves
+    tr_rows(q_lo, V_l, tid);
+    __syncthreads();
 
     // ---- phase 4: T = (I + A)^-1 (as dnp_prep)
     if (tid < 64) {
@@ -855,14 +879,24 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
     bf16x8_t tv[2][2], tk[2][2];   // [k-step][hi, lo]
 #pragma unroll
     for (int ks = 0; ks < 2; ks++) {
+        // row s of T and the scalars of tokens r0..r0+7 as vector LDS reads
+        // (the upper blocks of T hold stale bytes: selected away, never used)
         const int s = wave * 16 + m, r0 = 32 * ks + 8 * g;
+        float tr[8], bt[8], ev[8], kv[8];
+        *(float4 *)&tr[0] = *(const float4 *)&T_s[s * 64 + r0];
+        *(float4 *)&tr[4] = *(const float4 *)&T_s[s * 64 + r0 + 4];
+        *(float4 *)&bt[0] = *(const float4 *)&beta_s[r0];
+        *(float4 *)&bt[4] = *(const float4 *)&beta_s[r0 + 4];
+        *(float4 *)&ev[0] = *(const float4 *)&eg_s[r0];
+        *(float4 *)&ev[4] = *(const float4 *)&eg_s[r0 + 4];
+        *(float4 *)&kv[0] = *(const float4 *)&ik_s[r0];
+        *(float4 *)&kv[4] = *(const float4 *)&ik_s[r0 + 4];
         float fv[8], fk[8];
 #pragma unroll
         for (int e = 0; e < 8; e++) {
-            const int r = r0 + e;
-            const float tsr = r <= s ? T_s[s * 64 + r] : 0.0f;
-            fv[e] = tsr * beta_s[r];
-            fk[e] = tsr * ((beta_s[r] * eg_s[r]) * ik_s[r]);
+            const float tsr = r0 + e <= s ? tr[e] : 0.0f;
+            fv[e] = tsr * bt[e];
+            fk[e] = tsr * ((bt[e] * ev[e]) * kv[e]);
         }
         uint4 hv, lv, hk, lk;
         split8(fv, hv, lv);
@@ -933,11 +967,30 @@ __device__ __forceinline__ uint32_t x3_src(int j, int wave, int slice) {
            : j < 28 ? (uint32_t)(X_P + ((j - 24) >> 1) * 8192 + (wave * 2 + (j & 1)) * 1024)
                     : (uint32_t)(X_UT + (wave * 8 + slice) * 1024);
 }
+// tiles j0 .. j1-1 of a wave's slot (j1 == X3_TILES also brings e^gam_C)
+template <int J0, int J1>
 __device__ __forceinline__ void x3_fetch(const char *rec, uint32_t lds, int wave, int slice, int lane) {
 #pragma unroll
-    for (int j = 0; j < X3_TILES; j++)
+    for (int j = J0; j < J1; j++)
         vx_dma16(rec, x3_src(j, wave, slice) + (uint32_t)lane * 16, lds + (uint32_t)j * 1024);
-    vx_dma4(rec, (uint32_t)X_GC + (uint32_t)lane * 4, lds + X3_TILES * 1024);
+    if (J1 == X3_TILES) vx_dma4(rec, (uint32_t)X_GC + (uint32_t)lane * 4, lds + X3_TILES * 1024);
+}
+// Warm the L2 with a chunk record one step before its x3_fetch: the eight
+// slices of a head (on one XCD) each pull an eighth of the 112 tiles they
+// all read, and each wave its own U tile and the e^gam_C word, so the next
+// step's fetch finds every line in L2 instead of waiting on HBM.  The bytes
+// land in a junk LDS area.  Always X3_PF instructions per wave, so the wait
+// for the older fetch is a fixed count.
+constexpr int X3_PF = 6;
+__device__ __forceinline__ void x3_prefetch(const char *rec, uint32_t junk, int wave, int slice, int lane) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        int j = slice * 4 + wave + 32 * i;   // shared tiles 0..111: NW, QE, KT, P
+        if (j >= 112) j = slice * 4 + wave;
+        vx_dma16(rec, (uint32_t)j * 1024 + (uint32_t)lane * 16, junk);
+    }
+    vx_dma16(rec, (uint32_t)(X_UT + (wave * 8 + slice) * 1024) + (uint32_t)lane * 16, junk);
+    vx_dma4(rec, (uint32_t)X_GC + (uint32_t)lane * 4, junk);
 }
 
 // bf16 hi, lo of 4 floats, as two packed uint2
@@ -971,12 +1024,15 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
     const int col = slice * 16 + n;
 
     __shared__ __align__(16) char ops_l[4 * X3_WAVE];
+    __shared__ __align__(16) char junk_l[4][1024];
     __shared__ uint16_t S_h[16][HD + 8], S_lo[16][HD + 8];   // S slice hi/lo, [column][key dim]
     __shared__ uint16_t U_h[16][CH + 8], U_lo[16][CH + 8];   // U slice hi/lo, [column][token]
 
     const char *rec0 = vx_uniform_ptr(p.rec + ((size_t)b * p.nv + vh) * p.NC * XREC);
     const uint32_t ops_w = vx_lds_addr(ops_l) + (uint32_t)wave * X3_WAVE;
-    x3_fetch(rec0, ops_w, wave, slice, lane);
+    const uint32_t junk = vx_lds_addr(junk_l[wave]);
+    x3_fetch<0, X3_TILES>(rec0, ops_w, wave, slice, lane);
+    if (p.NC > 1) x3_prefetch(rec0 + XREC, junk, wave, slice, lane);
 
     float *Sg = p.S + ((size_t)b * p.nv + vh) * HD * HD;
     floatx4_t S[2];
@@ -989,8 +1045,12 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
     floatx4_t Oprev = {0.f, 0.f, 0.f, 0.f};
     const uint4 *t = (const uint4 *)&ops_l[wave * X3_WAVE] + lane;
     for (int c = 0; c < p.NC; c++) {
-        // chunk c's operands have landed (and the previous step's stores are done)
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // chunk c's operands have landed (and the previous step's stores are
+        // done); the prefetch of chunk c+1, issued after them, may still fly
+        if (c + 1 < p.NC)
+            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(X3_PF) : "memory");
+        else
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
         if (c > 0) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -1011,9 +1071,15 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
             *(uint2 *)&S_h[n][d] = h;
             *(uint2 *)&S_lo[n][d] = l;
         }
-        // the slot is read out: the next chunk's loads go into it now
+        // The slot is read out: the next chunk's loads go into it now, in
+        // four groups between the MFMA runs below (a CU's memory pipe takes
+        // about 16 cycles per 1 KiB load, so a burst of all 30 would stall
+        // the wave for most of a chunk step instead of running beside its
+        // MFMAs).
         __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        if (c + 1 < p.NC) x3_fetch(rec0 + (size_t)(c + 1) * XREC, ops_w, wave, slice, lane);
+        const bool more = c + 1 < p.NC;
+        const char *rec1 = rec0 + (size_t)(c + 1) * XREC;
+        if (more) x3_fetch<0, 8>(rec1, ops_w, wave, slice, lane);
         vx_lds_barrier();   // S hi/lo complete
         bf16x8_t sbh[4], sbl[4];
 #pragma unroll
@@ -1030,6 +1096,9 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
         MFMA3(U1, as_bf16x8(op[1]), as_bf16x8(op[5]), sbh[1], sbl[1]);
         MFMA3(U2, as_bf16x8(op[2]), as_bf16x8(op[6]), sbh[2], sbl[2]);
         MFMA3(U3, as_bf16x8(op[3]), as_bf16x8(op[7]), sbh[3], sbl[3]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) x3_fetch<8, 16>(rec1, ops_w, wave, slice, lane);
+        __builtin_amdgcn_sched_barrier(0);
         const floatx4_t U = (U0 + U1) + (U2 + U3);
         {
             uint2 h, l;
@@ -1041,6 +1110,9 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
         MFMA3(O1, as_bf16x8(op[9]), as_bf16x8(op[13]), sbh[1], sbl[1]);
         MFMA3(O0, as_bf16x8(op[10]), as_bf16x8(op[14]), sbh[2], sbl[2]);
         MFMA3(O1, as_bf16x8(op[11]), as_bf16x8(op[15]), sbh[3], sbl[3]);
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) x3_fetch<16, 22>(rec1, ops_w, wave, slice, lane);
+        __builtin_amdgcn_sched_barrier(0);
         vx_lds_barrier();   // U hi/lo complete
         bf16x8_t ubh[2], ubl[2];
 #pragma unroll
@@ -1056,6 +1128,10 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
             MFMA3(Sb, as_bf16x8(op[17 + 2 * r]), as_bf16x8(op[21 + 2 * r]), ubh[1], ubl[1]);
             S[r] = Sa + Sb;
         }
+        __builtin_amdgcn_sched_barrier(0);
+        if (more) x3_fetch<22, X3_TILES>(rec1, ops_w, wave, slice, lane);
+        if (c + 2 < p.NC) x3_prefetch(rec0 + (size_t)(c + 2) * XREC, junk, wave, slice, lane);
+        __builtin_amdgcn_sched_barrier(0);
         // O += P U
         MFMA3(O0, as_bf16x8(op[24]), as_bf16x8(op[26]), ubh[0], ubl[0]);
         MFMA3(O1, as_bf16x8(op[25]), as_bf16x8(op[27]), ubh[1], ubl[1]);
