@@ -610,6 +610,19 @@ constexpr int X3_GAM = X3_MT + 3 * 256 * 4;
 constexpr int X3_SC = X3_GAM + CH * 8;
 constexpr int X3_TOTAL = X3_SC + 5 * CH * 4;
 static_assert(CH * RP * 2 <= HD * TP * 2, "k rows fit the V^T region");
+// Without lo parts (bf16 inputs) four regions suffice, 76.5 KiB, so two
+// workgroups share a CU:
+constexpr int XN_QH = 0;                        // q rows -> P hi staging -> v rows -> T fp32
+constexpr int XN_KH = XN_QH + CH * RP * 2;      // k rows -> P lo staging -> V^T -> -W hi staging
+constexpr int XN_TH = XN_KH + HD * TP * 2;      // K^T -> -W lo staging
+constexpr int XN_AS = XN_TH + HD * TP * 2;      // A fp32
+constexpr int XN_MT = XN_AS + CH * AP * 4;
+constexpr int XN_GAM = XN_MT + 3 * 256 * 4;
+constexpr int XN_SC = XN_GAM + CH * 8;
+constexpr int XN_TOTAL = XN_SC + 5 * CH * 4;
+static_assert(CH * 64 * 4 <= CH * RP * 2 && CH * TP * 2 <= HD * TP * 2 && CH * RP * 2 <= HD * TP * 2,
+              "T, P and -W staging fit their regions");
+static_assert(2 * XN_TOTAL <= 160 * 1024, "two workgroups per CU");
 
 // Transpose a row-major [64 tokens][RP] bf16 tile (128 dims) into
 // [128 dims][TP] (64 tokens) with all 256 threads: thread (wave w, half h,
@@ -633,6 +646,9 @@ __device__ __forceinline__ void tr_rows(const uint16_t *src, uint16_t *dst, int 
     }
 }
 
+// LO: the inputs come with lo parts (the glue's fp32 values as bf16 pairs);
+// without them every lo array is zero and is neither stored nor read.
+template <bool LO>
 __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
     const int c = blockIdx.x, vh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, m = lane & 15;
@@ -640,20 +656,25 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
     const int qh = vh * p.nqk / p.nv;
     const int t0 = c * CH;
     const int nvalid = min(CH, p.T - t0);
-    const bool has_lo = p.ql != nullptr;
+    constexpr bool has_lo = LO;
 
-    __shared__ __attribute__((aligned(16))) char smem[X3_TOTAL];
-    uint16_t *q_rows = (uint16_t *)(smem + X3_QH), *q_lo = (uint16_t *)(smem + X3_QL);
-    uint16_t *P_h = (uint16_t *)(smem + X3_QH), *P_l = (uint16_t *)(smem + X3_QL);   // [64][TP]
-    float *T_s = (float *)(smem + X3_QH);                                              // [64][64]
-    uint16_t *k_rows = (uint16_t *)(smem + X3_KH), *k_lo = (uint16_t *)(smem + X3_KL);
-    uint16_t *V_h = (uint16_t *)(smem + X3_KH), *V_l = (uint16_t *)(smem + X3_KL);   // [128][TP]
-    uint16_t *W_h = (uint16_t *)(smem + X3_KH), *W_l = (uint16_t *)(smem + X3_KL);   // [64][RP]
-    uint16_t *K_h = (uint16_t *)(smem + X3_TH), *K_l = (uint16_t *)(smem + X3_TL);   // [128][TP]
-    float *A_s = (float *)(smem + X3_AS);
-    float *M_t = (float *)(smem + X3_MT);
-    double *gam_s = (double *)(smem + X3_GAM);
-    float *beta_s = (float *)(smem + X3_SC), *eg_s = beta_s + CH, *egc_s = eg_s + CH;
+    __shared__ __attribute__((aligned(16))) char smem[LO ? X3_TOTAL : XN_TOTAL];
+    constexpr int QH = LO ? X3_QH : XN_QH, KH = LO ? X3_KH : XN_KH, TH = LO ? X3_TH : XN_TH;
+    constexpr int QL = LO ? X3_QL : XN_QH, KL = LO ? X3_KL : XN_KH, TL = LO ? X3_TL : XN_TH;
+    constexpr int PL = LO ? X3_QL : XN_KH, WL = LO ? X3_KL : XN_TH;
+    constexpr int AS = LO ? X3_AS : XN_AS, MT = LO ? X3_MT : XN_MT, GAM = LO ? X3_GAM : XN_GAM;
+    constexpr int SCL = LO ? X3_SC : XN_SC;
+    uint16_t *q_rows = (uint16_t *)(smem + QH), *q_lo = (uint16_t *)(smem + QL);
+    uint16_t *P_h = (uint16_t *)(smem + QH), *P_l = (uint16_t *)(smem + PL);          // [64][TP]
+    float *T_s = (float *)(smem + QH);                                                // [64][64]
+    uint16_t *k_rows = (uint16_t *)(smem + KH), *k_lo = (uint16_t *)(smem + KL);
+    uint16_t *V_h = (uint16_t *)(smem + KH), *V_l = (uint16_t *)(smem + KL);          // [128][TP]
+    uint16_t *W_h = (uint16_t *)(smem + KH), *W_l = (uint16_t *)(smem + WL);          // [64][RP]
+    uint16_t *K_h = (uint16_t *)(smem + TH), *K_l = (uint16_t *)(smem + TL);          // [128][TP]
+    float *A_s = (float *)(smem + AS);
+    float *M_t = (float *)(smem + MT);
+    double *gam_s = (double *)(smem + GAM);
+    float *beta_s = (float *)(smem + SCL), *eg_s = beta_s + CH, *egc_s = eg_s + CH;
     float *iq_s = egc_s + CH, *ik_s = iq_s + CH;
 
     // ---- phase 1: gates (wave 0); k, q, v rows (waves 1, 2, 3), hi and lo
@@ -708,14 +729,14 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             *(uint4 *)&rows[lane * RP + 8 * j] = raw[j];
-            *(uint4 *)&rowl[lane * RP + 8 * j] = rawl[j];
+            if (LO) *(uint4 *)&rowl[lane * RP + 8 * j] = rawl[j];
         }
         if (wave == 1) ik_s[lane] = inv;
         else iq_s[lane] = inv;
     }
     __syncthreads();
     tr_rows(k_rows, K_h, tid);   // K^T (hi, lo) by all waves
-    tr_rows(k_lo, K_l, tid);
+    if (LO) tr_rows(k_lo, K_l, tid);
     __syncthreads();
 
     char *rec = p.rec + (((size_t)b * p.nv + vh) * p.NC + c) * XREC;
@@ -735,8 +756,9 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
         const int d0 = 32 * ks + 8 * g;
-        const uint4 qa = *(const uint4 *)&q_rows[rowA * RP + d0], qal = *(const uint4 *)&q_lo[rowA * RP + d0];
-        const uint4 ka = *(const uint4 *)&k_rows[rowA * RP + d0], kal = *(const uint4 *)&k_lo[rowA * RP + d0];
+        const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+        const uint4 qa = *(const uint4 *)&q_rows[rowA * RP + d0], qal = LO ? *(const uint4 *)&q_lo[rowA * RP + d0] : z4;
+        const uint4 ka = *(const uint4 *)&k_rows[rowA * RP + d0], kal = LO ? *(const uint4 *)&k_lo[rowA * RP + d0] : z4;
         {   // e^gam qn tile (row block wave, k-step ks), hi and lo
             const uint16_t *qs = (const uint16_t *)&qa, *qsl = (const uint16_t *)&qal;
             float f[8];
@@ -766,7 +788,8 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
     for (int j = 0; j < 4; j++) {
         const int tile = wave * 4 + j, rb = tile >> 1, ks = tile & 1;
         const int i = rb * 16 + m, tb = 32 * ks + 8 * g;
-        const uint4 kr = *(const uint4 *)&K_h[i * TP + tb], krl = *(const uint4 *)&K_l[i * TP + tb];
+        const uint4 kr = *(const uint4 *)&K_h[i * TP + tb];
+        const uint4 krl = LO ? *(const uint4 *)&K_l[i * TP + tb] : make_uint4(0u, 0u, 0u, 0u);
         const uint16_t *kv = (const uint16_t *)&kr, *kvl = (const uint16_t *)&krl;
         float f[8];
 #pragma unroll
@@ -822,12 +845,12 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             *(uint4 *)&q_rows[lane * RP + 8 * j] = raw[j];
-            *(uint4 *)&q_lo[lane * RP + 8 * j] = rawl[j];
+            if (LO) *(uint4 *)&q_lo[lane * RP + 8 * j] = rawl[j];
         }
     }
     __syncthreads();
     tr_rows(q_rows, V_h, tid);   // V^T (hi, lo) by all waves
-    tr_rows(q_lo, V_l, tid);
+    if (LO) tr_rows(q_lo, V_l, tid);
     __syncthreads();
 
     // ---- phase 4: T = (I + A)^-1 (as dnp_prep)
@@ -1436,7 +1459,12 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
                 d->S, d->out};
     if (x3) {
         Prep3Args pa{d->T, d->nqk, d->nv, NC, q, k, v, ql, kl, vl, d->a, d->b, d->A_log, d->dt_bias, (char *)scr};
-        VX_LAUNCH(ctx, dnp_prep3, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B), dim3(256), pa);
+        if (pa.ql)
+            VX_LAUNCH_NAMED(ctx, "dnp_prep3", dnp_prep3<true>, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B),
+                            dim3(256), pa);
+        else
+            VX_LAUNCH_NAMED(ctx, "dnp_prep3", dnp_prep3<false>, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B),
+                            dim3(256), pa);
         VX_LAUNCH_NAMED(ctx, "dnp_scan3", dnp_scan3, dim3((unsigned)(d->nv * NSLICE), (unsigned)d->B), dim3(256), sa);
     } else {
         PrepArgs pa{d->T, d->nqk, d->nv, NC, q, k, v, d->a, d->b, d->A_log, d->dt_bias,
