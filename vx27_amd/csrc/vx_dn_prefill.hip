@@ -973,16 +973,19 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
 }
 
 // dnp_scan3: the chunk walk of dnp_scan with every operand as a hi/lo pair.
-// A wave's operands of one chunk (29 tiles of 1 KiB + the record's last 256
-// bytes) are staged in one LDS slot per wave: at the top of a chunk step the
-// wave reads the whole slot into registers and at once starts the next
-// chunk's direct-to-LDS loads into it, so they have a whole step to land.
+// A wave's operands of one chunk are 29 tiles of 1 KiB plus e^gam_C; they
+// come straight from the record into registers (no LDS staging: a CU's
+// memory pipe, about 64 B per cycle, is what bounds a chunk step, and an LDS
+// slot would add its write and read).  The operand groups are consumed in
+// order -- -W and Ut by U = Ut - W S, e^gam Q by O, Kt^T and e^gam_C by the
+// state update, P by O += P U -- and each group's registers take the next
+// chunk's loads as soon as its MFMAs have read them, so every load has about
+// a whole chunk step to land and only one chunk's operands are live.
 // The output rows of a chunk are stored at the top of the next step.
 constexpr int X3_TILES = 29;
-constexpr uint32_t X3_WAVE = X3_TILES * 1024 + 256;
 
 __device__ __forceinline__ uint32_t x3_src(int j, int wave, int slice) {
-    // slot order: NW hi 0-3, NW lo 4-7, QE hi 8-11, QE lo 12-15, KT hi 16-19,
+    // operand order: NW hi 0-3, NW lo 4-7, QE hi 8-11, QE lo 12-15, KT hi 16-19,
     // KT lo 20-23, P hi 24-25, P lo 26-27, Ut 28
     return j < 8    ? (uint32_t)(X_NW + (j >> 2) * 16384 + (wave * 4 + (j & 3)) * 1024)
            : j < 16 ? (uint32_t)(X_QE + ((j - 8) >> 2) * 16384 + (wave * 4 + (j & 3)) * 1024)
@@ -990,30 +993,19 @@ __device__ __forceinline__ uint32_t x3_src(int j, int wave, int slice) {
            : j < 28 ? (uint32_t)(X_P + ((j - 24) >> 1) * 8192 + (wave * 2 + (j & 1)) * 1024)
                     : (uint32_t)(X_UT + (wave * 8 + slice) * 1024);
 }
-// tiles j0 .. j1-1 of a wave's slot (j1 == X3_TILES also brings e^gam_C)
+// tiles J0 .. J1-1 of a wave's operands of one chunk record into op[J0 ..]
+// (global address space: a generic pointer would make these flat loads,
+// which count on the LDS counter too, so every LDS wait would drain them)
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4_t g_u32x4;
+typedef const __attribute__((address_space(1))) float g_float;
 template <int J0, int J1>
-__device__ __forceinline__ void x3_fetch(const char *rec, uint32_t lds, int wave, int slice, int lane) {
+__device__ __forceinline__ void x3_load(const char *rec, int wave, int slice, int lane, uint4 *op) {
 #pragma unroll
-    for (int j = J0; j < J1; j++)
-        vx_dma16(rec, x3_src(j, wave, slice) + (uint32_t)lane * 16, lds + (uint32_t)j * 1024);
-    if (J1 == X3_TILES) vx_dma4(rec, (uint32_t)X_GC + (uint32_t)lane * 4, lds + X3_TILES * 1024);
-}
-// Warm the L2 with a chunk record one step before its x3_fetch: the eight
-// slices of a head (on one XCD) each pull an eighth of the 112 tiles they
-// all read, and each wave its own U tile and the e^gam_C word, so the next
-// step's fetch finds every line in L2 instead of waiting on HBM.  The bytes
-// land in a junk LDS area.  Always X3_PF instructions per wave, so the wait
-// for the older fetch is a fixed count.
-constexpr int X3_PF = 6;
-__device__ __forceinline__ void x3_prefetch(const char *rec, uint32_t junk, int wave, int slice, int lane) {
-#pragma unroll
-    for (int i = 0; i < 4; i++) {
-        int j = slice * 4 + wave + 32 * i;   // shared tiles 0..111: NW, QE, KT, P
-        if (j >= 112) j = slice * 4 + wave;
-        vx_dma16(rec, (uint32_t)j * 1024 + (uint32_t)lane * 16, junk);
+    for (int j = J0; j < J1; j++) {
+        const u32x4_t v = *(g_u32x4 *)(rec + x3_src(j, wave, slice) + (uint32_t)lane * 16);
+        op[j] = make_uint4(v.x, v.y, v.z, v.w);
     }
-    vx_dma16(rec, (uint32_t)(X_UT + (wave * 8 + slice) * 1024) + (uint32_t)lane * 16, junk);
-    vx_dma4(rec, (uint32_t)X_GC + (uint32_t)lane * 4, junk);
 }
 
 // bf16 hi, lo of 4 floats, as two packed uint2
@@ -1046,16 +1038,13 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
     }
     const int col = slice * 16 + n;
 
-    __shared__ __align__(16) char ops_l[4 * X3_WAVE];
-    __shared__ __align__(16) char junk_l[4][1024];
     __shared__ uint16_t S_h[16][HD + 8], S_lo[16][HD + 8];   // S slice hi/lo, [column][key dim]
     __shared__ uint16_t U_h[16][CH + 8], U_lo[16][CH + 8];   // U slice hi/lo, [column][token]
 
     const char *rec0 = vx_uniform_ptr(p.rec + ((size_t)b * p.nv + vh) * p.NC * XREC);
-    const uint32_t ops_w = vx_lds_addr(ops_l) + (uint32_t)wave * X3_WAVE;
-    const uint32_t junk = vx_lds_addr(junk_l[wave]);
-    x3_fetch<0, X3_TILES>(rec0, ops_w, wave, slice, lane);
-    if (p.NC > 1) x3_prefetch(rec0 + XREC, junk, wave, slice, lane);
+    uint4 op[X3_TILES];
+    x3_load<0, X3_TILES>(rec0, wave, slice, lane, op);
+    float gc = *(g_float *)(rec0 + X_GC);
 
     float *Sg = p.S + ((size_t)b * p.nv + vh) * HD * HD;
     floatx4_t S[2];
@@ -1063,17 +1052,12 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
     for (int r = 0; r < 2; r++)
 #pragma unroll
         for (int i = 0; i < 4; i++) S[r][i] = Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + col];
-    __asm__ volatile("" ::"v"(S[0]), "v"(S[1]));
 
     floatx4_t Oprev = {0.f, 0.f, 0.f, 0.f};
-    const uint4 *t = (const uint4 *)&ops_l[wave * X3_WAVE] + lane;
     for (int c = 0; c < p.NC; c++) {
-        // chunk c's operands have landed (and the previous step's stores are
-        // done); the prefetch of chunk c+1, issued after them, may still fly
-        if (c + 1 < p.NC)
-            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(X3_PF) : "memory");
-        else
-            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // the next chunk's record (the last one again after the end: those
+        // loads are never used)
+        const char *rec1 = rec0 + (size_t)min(c + 1, p.NC - 1) * XREC;
         if (c > 0) {
 #pragma unroll
             for (int i = 0; i < 4; i++) {
@@ -1081,10 +1065,6 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
                 if (tt < p.T) p.out[(((size_t)b * p.T + tt) * p.nv + vh) * HD + col] = Oprev[i];
             }
         }
-        uint4 op[X3_TILES];
-#pragma unroll
-        for (int j = 0; j < X3_TILES; j++) op[j] = t[j * 64];
-        const float gc = *(const float *)&ops_l[wave * X3_WAVE + X3_TILES * 1024];
         // S -> bf16 hi/lo, [column][key dim]
 #pragma unroll
         for (int r = 0; r < 2; r++) {
@@ -1094,33 +1074,24 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
             *(uint2 *)&S_h[n][d] = h;
             *(uint2 *)&S_lo[n][d] = l;
         }
-        // The slot is read out: the next chunk's loads go into it now, in
-        // four groups between the MFMA runs below (a CU's memory pipe takes
-        // about 16 cycles per 1 KiB load, so a burst of all 30 would stall
-        // the wave for most of a chunk step instead of running beside its
-        // MFMAs).
-        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");
-        const bool more = c + 1 < p.NC;
-        const char *rec1 = rec0 + (size_t)(c + 1) * XREC;
-        if (more) x3_fetch<0, 8>(rec1, ops_w, wave, slice, lane);
-        vx_lds_barrier();   // S hi/lo complete
+        __syncthreads();   // S hi/lo complete
         bf16x8_t sbh[4], sbl[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             sbh[ks] = as_bf16x8(*(const uint4 *)&S_h[n][32 * ks + 8 * g]);
             sbl[ks] = as_bf16x8(*(const uint4 *)&S_lo[n][32 * ks + 8 * g]);
         }
-        // U = Ut - W S and the e^gam Q S part of O, in independent chains
+        // U = Ut - W S, in independent chains; then -W and Ut take chunk c+1
         const uint4 utu = op[28];
         floatx4_t U0 = (floatx4_t){__uint_as_float(utu.x), __uint_as_float(utu.y), __uint_as_float(utu.z), __uint_as_float(utu.w)};
         floatx4_t U1 = {0.f, 0.f, 0.f, 0.f}, U2 = {0.f, 0.f, 0.f, 0.f}, U3 = {0.f, 0.f, 0.f, 0.f};
-        floatx4_t O0 = {0.f, 0.f, 0.f, 0.f}, O1 = {0.f, 0.f, 0.f, 0.f};
         MFMA3(U0, as_bf16x8(op[0]), as_bf16x8(op[4]), sbh[0], sbl[0]);
         MFMA3(U1, as_bf16x8(op[1]), as_bf16x8(op[5]), sbh[1], sbl[1]);
         MFMA3(U2, as_bf16x8(op[2]), as_bf16x8(op[6]), sbh[2], sbl[2]);
         MFMA3(U3, as_bf16x8(op[3]), as_bf16x8(op[7]), sbh[3], sbl[3]);
         __builtin_amdgcn_sched_barrier(0);
-        if (more) x3_fetch<8, 16>(rec1, ops_w, wave, slice, lane);
+        x3_load<0, 8>(rec1, wave, slice, lane, op);
+        x3_load<28, 29>(rec1, wave, slice, lane, op);
         __builtin_amdgcn_sched_barrier(0);
         const floatx4_t U = (U0 + U1) + (U2 + U3);
         {
@@ -1129,21 +1100,24 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
             *(uint2 *)&U_h[n][wave * 16 + 4 * g] = h;
             *(uint2 *)&U_lo[n][wave * 16 + 4 * g] = l;
         }
+        // the e^gam Q S part of O; then e^gam Q takes chunk c+1
+        floatx4_t O0 = {0.f, 0.f, 0.f, 0.f}, O1 = {0.f, 0.f, 0.f, 0.f};
         MFMA3(O0, as_bf16x8(op[8]), as_bf16x8(op[12]), sbh[0], sbl[0]);
         MFMA3(O1, as_bf16x8(op[9]), as_bf16x8(op[13]), sbh[1], sbl[1]);
         MFMA3(O0, as_bf16x8(op[10]), as_bf16x8(op[14]), sbh[2], sbl[2]);
         MFMA3(O1, as_bf16x8(op[11]), as_bf16x8(op[15]), sbh[3], sbl[3]);
         __builtin_amdgcn_sched_barrier(0);
-        if (more) x3_fetch<16, 22>(rec1, ops_w, wave, slice, lane);
+        x3_load<8, 16>(rec1, wave, slice, lane, op);
         __builtin_amdgcn_sched_barrier(0);
-        vx_lds_barrier();   // U hi/lo complete
+        __syncthreads();   // U hi/lo complete
         bf16x8_t ubh[2], ubl[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
             ubh[ks] = as_bf16x8(*(const uint4 *)&U_h[n][32 * ks + 8 * g]);
             ubl[ks] = as_bf16x8(*(const uint4 *)&U_lo[n][32 * ks + 8 * g]);
         }
-        // S = e^gam_C S + Kt^T U, per row block two chains
+        // S = e^gam_C S + Kt^T U, per row block two chains; then Kt^T and
+        // e^gam_C take chunk c+1
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             floatx4_t Sa = S[r] * gc, Sb = {0.f, 0.f, 0.f, 0.f};
@@ -1152,12 +1126,15 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
             S[r] = Sa + Sb;
         }
         __builtin_amdgcn_sched_barrier(0);
-        if (more) x3_fetch<22, X3_TILES>(rec1, ops_w, wave, slice, lane);
-        if (c + 2 < p.NC) x3_prefetch(rec0 + (size_t)(c + 2) * XREC, junk, wave, slice, lane);
+        x3_load<16, 24>(rec1, wave, slice, lane, op);
+        gc = *(g_float *)(rec1 + X_GC);
         __builtin_amdgcn_sched_barrier(0);
-        // O += P U
+        // O += P U; then P takes chunk c+1
         MFMA3(O0, as_bf16x8(op[24]), as_bf16x8(op[26]), ubh[0], ubl[0]);
         MFMA3(O1, as_bf16x8(op[25]), as_bf16x8(op[27]), ubh[1], ubl[1]);
+        __builtin_amdgcn_sched_barrier(0);
+        x3_load<24, 28>(rec1, wave, slice, lane, op);
+        __builtin_amdgcn_sched_barrier(0);
         Oprev = O0 + O1;
     }
 #pragma unroll
