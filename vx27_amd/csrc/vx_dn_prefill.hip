@@ -22,10 +22,9 @@
 //           chunks in order; a workgroup owns 16 value columns of one head's
 //           state (columns are independent in all three products), keeps
 //           them in MFMA accumulators and runs 14 MFMAs per wave per chunk.
-//           Each wave streams its own operand tiles of the chunk two ahead
-//           straight into LDS (two slots, explicit vmcnt waits, no barrier
-//           for the hand-off).  The 8 slices of a head are placed on one XCD so the records they
-//           share are read from HBM once.
+//           Each wave loads its own operand tiles straight into registers,
+//           a chunk ahead.  The 8 slices of a head are placed on one XCD so
+//           the records they share are read from HBM once.
 //
 // Operand tiles ([rows/16][k/32][64 lanes][8] bf16) follow the MFMA operand
 // layout of v_mfma_f32_16x16x32_bf16: lane (g = l/16, m = l%16) of an A tile
@@ -398,15 +397,13 @@ struct ScanArgs {
     float *out;      // [B][T][nv][128]
 };
 
-// A wave's operands of one chunk: 15 tiles of 1 KiB in its record, staged in
-// LDS in this order: -W (rows 16w..16w+15, 4 k-steps), e^gam Q (same rows),
-// Kt^T (row blocks 2w, 2w+1, 2 k-steps each), P (rows 16w.., 2 k-steps) and
-// the wave's Ut block of the slice; then the record's last 256 bytes, whose
-// first float is e^gam_C.
+// A wave's operands of one chunk: 15 tiles of 1 KiB in its record -- -W
+// (rows 16w..16w+15, 4 k-steps), e^gam Q (same rows), Kt^T (row blocks 2w,
+// 2w+1, 2 k-steps each), P (rows 16w.., 2 k-steps) and the wave's Ut block
+// of the slice -- and e^gam_C.  They come straight from the record into
+// registers, and each group takes the next chunk's loads as soon as its
+// MFMAs have read it (as in dnp_scan3, below).
 constexpr int OPS_TILES = 15;
-constexpr int OPS_LOADS = OPS_TILES + 1;   // load instructions per wave and chunk
-constexpr uint32_t OPS_WAVE = OPS_TILES * 1024 + 256;
-constexpr uint32_t OPS_BUF = 4 * OPS_WAVE;
 
 __device__ __forceinline__ uint32_t ops_src(int j, int wave, int slice) {
     return j < 4    ? (uint32_t)(R_NW + (wave * 4 + j) * 1024)
@@ -415,23 +412,18 @@ __device__ __forceinline__ uint32_t ops_src(int j, int wave, int slice) {
            : j < 14 ? (uint32_t)(R_P + (wave * 2 + j - 12) * 1024)
                     : (uint32_t)(R_UT + (wave * 8 + slice) * 1024);
 }
-
-// Starts group q (0..3) of the wave's 16 direct-to-LDS loads of record
-// `rec` into its slot at LDS address `lds` (tiles 4q .. 4q+3, the last
-// group ending with the record's final 256 bytes).  Each wave reads back only
-// what it loaded itself, so the hand-off needs this wave's vmcnt wait and no
-// barrier.  The groups are issued at spread-out points of a chunk step: the
-// load path drains 60 KiB per chunk per CU, and issuing all of it at once
-// stalls the wave.
-__device__ __forceinline__ void fetch_ops(const char *rec, uint32_t lds, int wave, int slice, int lane, int q) {
+// (global address space: a generic pointer would make these flat loads,
+// which count on the LDS counter too, so every LDS wait would drain them)
+typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
+typedef const __attribute__((address_space(1))) u32x4_t g_u32x4;
+typedef const __attribute__((address_space(1))) float g_float;
+template <int J0, int J1>
+__device__ __forceinline__ void ops_load(const char *rec, int wave, int slice, int lane, uint4 *op) {
 #pragma unroll
-    for (int j = 4 * q; j < 4 * q + 4 && j < OPS_TILES; j++)
-        vx_dma16(rec, ops_src(j, wave, slice) + (uint32_t)lane * 16, lds + (uint32_t)j * 1024);
-    if (q == 3) vx_dma4(rec, (uint32_t)R_GC + (uint32_t)lane * 4, lds + OPS_TILES * 1024);
-}
-__device__ __forceinline__ void fetch_ops(const char *rec, uint32_t lds, int wave, int slice, int lane) {
-#pragma unroll
-    for (int q = 0; q < 4; q++) fetch_ops(rec, lds, wave, slice, lane, q);
+    for (int j = J0; j < J1; j++) {
+        const u32x4_t v = *(g_u32x4 *)(rec + ops_src(j, wave, slice) + (uint32_t)lane * 16);
+        op[j] = make_uint4(v.x, v.y, v.z, v.w);
+    }
 }
 
 __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
@@ -449,14 +441,13 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
     }
     const int col = slice * 16 + n;
 
-    __shared__ __align__(16) char ops_l[2][OPS_BUF];   // chunk operands, two chunks in flight
     __shared__ uint16_t S_l[16][HD + 8];   // S slice, bf16, [column][key dim]
     __shared__ uint16_t U_l[16][CH + 8];   // U slice, bf16, [column][token]
 
     const char *rec0 = vx_uniform_ptr(p.rec + ((size_t)b * p.nv + vh) * p.NC * REC);
-    const uint32_t ops_w = vx_lds_addr(ops_l) + (uint32_t)wave * OPS_WAVE;
-    fetch_ops(rec0, ops_w, wave, slice, lane);
-    if (p.NC > 1) fetch_ops(rec0 + REC, ops_w + OPS_BUF, wave, slice, lane);
+    uint4 op[OPS_TILES];
+    ops_load<0, OPS_TILES>(rec0, wave, slice, lane, op);
+    float gc = *(g_float *)(rec0 + R_GC);
 
     // state rows 32w .. 32w+31 (row blocks 2w, 2w+1) of the slice, C layout
     float *Sg = p.S + ((size_t)b * p.nv + vh) * HD * HD;
@@ -465,89 +456,58 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
     for (int r = 0; r < 2; r++)
 #pragma unroll
         for (int i = 0; i < 4; i++) S[r][i] = Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + col];
-    // take the state loads' wait here, once, rather than inside the loop
-    __asm__ volatile("" ::"v"(S[0]), "v"(S[1]));
 
     for (int c = 0; c < p.NC; c++) {
-        // The chunk's dependent chain S -> U -> S' starts at once; the operand
-        // reads go into its shadow (before the barrier whose far side needs
-        // them), and chunk c+2's loads start once this slot is read out.
+        const char *rec1 = rec0 + (size_t)min(c + 1, p.NC - 1) * REC;   // the last one again after the end
         // S (bf16) -> LDS as [column][key dim]
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             const int d = (2 * wave + r) * 16 + 4 * g;
             *(uint2 *)&S_l[n][d] = make_uint2(pack2(S[r][0], S[r][1]), pack2(S[r][2], S[r][3]));
         }
-        // chunk c's loads have landed once at most the loads issued after its
-        // last group are still outstanding: groups 0 and 1 of chunk c+1 (8
-        // loads; loads complete in issue order)
-        if (c + 1 < p.NC)
-            __asm__ volatile("s_waitcnt vmcnt(8)" ::: "memory");
-        else
-            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
-        // groups 2 and 3 of chunk c+1 go out in this step's first half
-        const bool fill1 = c >= 1 && c + 1 < p.NC;   // (chunks 0 and 1 are loaded whole up front)
-        const char *rec1 = rec0 + (size_t)(c + 1) * REC;
-        const uint32_t slot1 = ops_w + (uint32_t)((c + 1) & 1) * OPS_BUF;
-        if (fill1) fetch_ops(rec1, slot1, wave, slice, lane, 2);
-        const char *slot = &ops_l[c & 1][wave * OPS_WAVE];
-        const uint4 *t = (const uint4 *)slot + lane;
-        uint4 nw[4], qe[4];
-#pragma unroll
-        for (int ks = 0; ks < 4; ks++) {
-            nw[ks] = t[ks * 64];
-            qe[ks] = t[(4 + ks) * 64];
-        }
-        const uint4 utu = t[14 * 64];
-        const float gc = *(const float *)(slot + OPS_TILES * 1024);
-        vx_lds_barrier();   // S_l complete (and this wave's operand reads returned)
-        if (fill1) fetch_ops(rec1, slot1, wave, slice, lane, 3);
+        __syncthreads();   // S_l complete
         bf16x8_t sb[4];
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) sb[ks] = as_bf16x8(*(const uint4 *)&S_l[n][32 * ks + 8 * g]);
         // U = Ut - W S for tokens 16w .. 16w+15, and the e^gam Q S part of O,
-        // as independent two-MFMA chains (the dependent-MFMA latency, not the
-        // issue rate, bounds this loop)
+        // as independent two-MFMA chains; then -W, e^gam Q and Ut take chunk c+1
+        const uint4 utu = op[14];
         floatx4_t U0 = (floatx4_t){__uint_as_float(utu.x), __uint_as_float(utu.y), __uint_as_float(utu.z), __uint_as_float(utu.w)};
         floatx4_t U1 = {0.f, 0.f, 0.f, 0.f};
         floatx4_t O0 = {0.f, 0.f, 0.f, 0.f}, O1 = {0.f, 0.f, 0.f, 0.f};
-        U0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(nw[0]), sb[0], U0, 0, 0, 0);
-        U1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(nw[1]), sb[1], U1, 0, 0, 0);
-        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qe[0]), sb[0], O0, 0, 0, 0);
-        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qe[1]), sb[1], O1, 0, 0, 0);
-        U0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(nw[2]), sb[2], U0, 0, 0, 0);
-        U1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(nw[3]), sb[3], U1, 0, 0, 0);
-        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qe[2]), sb[2], O0, 0, 0, 0);
-        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qe[3]), sb[3], O1, 0, 0, 0);
+        U0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[0]), sb[0], U0, 0, 0, 0);
+        U1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[1]), sb[1], U1, 0, 0, 0);
+        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[4]), sb[0], O0, 0, 0, 0);
+        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[5]), sb[1], O1, 0, 0, 0);
+        U0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[2]), sb[2], U0, 0, 0, 0);
+        U1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[3]), sb[3], U1, 0, 0, 0);
+        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[6]), sb[2], O0, 0, 0, 0);
+        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[7]), sb[3], O1, 0, 0, 0);
+        __builtin_amdgcn_sched_barrier(0);
+        ops_load<0, 8>(rec1, wave, slice, lane, op);
+        ops_load<14, 15>(rec1, wave, slice, lane, op);
+        __builtin_amdgcn_sched_barrier(0);
         const floatx4_t U = U0 + U1;
         *(uint2 *)&U_l[n][wave * 16 + 4 * g] = make_uint2(pack2(U[0], U[1]), pack2(U[2], U[3]));
-        uint4 kt[4], pp[2];
-#pragma unroll
-        for (int j = 0; j < 4; j++) kt[j] = t[(8 + j) * 64];
-        pp[0] = t[12 * 64];
-        pp[1] = t[13 * 64];
-        vx_lds_barrier();   // U_l complete; every read of this slot has returned
-        // the slot is free: refill it with chunk c+2, groups 0 and 1 in this
-        // step, 2 and 3 in the next
-        const bool refill = c + 2 < p.NC;
-        const char *rec2 = rec0 + (size_t)(c + 2) * REC;
-        const uint32_t slot2 = ops_w + (uint32_t)(c & 1) * OPS_BUF;
-        if (refill) fetch_ops(rec2, slot2, wave, slice, lane, 0);
+        __syncthreads();   // U_l complete
         bf16x8_t ub[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) ub[ks] = as_bf16x8(*(const uint4 *)&U_l[n][32 * ks + 8 * g]);
-        // O += P U (two more independent MFMAs), then the two chains merge
-        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pp[0]), ub[0], O0, 0, 0, 0);
-        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(pp[1]), ub[1], O1, 0, 0, 0);
-        if (refill) fetch_ops(rec2, slot2, wave, slice, lane, 1);
-        // S = e^gam_C S + Kt^T U: per row block, two independent MFMAs
+        // O += P U (two more independent MFMAs); S = e^gam_C S + Kt^T U (per
+        // row block, two independent MFMAs); then P, Kt^T, e^gam_C take chunk c+1
+        O0 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[12]), ub[0], O0, 0, 0, 0);
+        O1 = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[13]), ub[1], O1, 0, 0, 0);
 #pragma unroll
         for (int r = 0; r < 2; r++) {
             floatx4_t Sa = S[r] * gc, Sb = {0.f, 0.f, 0.f, 0.f};
-            Sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kt[2 * r]), ub[0], Sa, 0, 0, 0);
-            Sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kt[2 * r + 1]), ub[1], Sb, 0, 0, 0);
+            Sa = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[8 + 2 * r]), ub[0], Sa, 0, 0, 0);
+            Sb = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(op[9 + 2 * r]), ub[1], Sb, 0, 0, 0);
             S[r] = Sa + Sb;
         }
+        __builtin_amdgcn_sched_barrier(0);
+        ops_load<8, 14>(rec1, wave, slice, lane, op);
+        gc = *(g_float *)(rec1 + R_GC);
+        __builtin_amdgcn_sched_barrier(0);
         const floatx4_t O = O0 + O1;
 #pragma unroll
         for (int i = 0; i < 4; i++) {
@@ -994,11 +954,6 @@ __device__ __forceinline__ uint32_t x3_src(int j, int wave, int slice) {
                     : (uint32_t)(X_UT + (wave * 8 + slice) * 1024);
 }
 // tiles J0 .. J1-1 of a wave's operands of one chunk record into op[J0 ..]
-// (global address space: a generic pointer would make these flat loads,
-// which count on the LDS counter too, so every LDS wait would drain them)
-typedef unsigned int u32x4_t __attribute__((ext_vector_type(4)));
-typedef const __attribute__((address_space(1))) u32x4_t g_u32x4;
-typedef const __attribute__((address_space(1))) float g_float;
 template <int J0, int J1>
 __device__ __forceinline__ void x3_load(const char *rec, int wave, int slice, int lane, uint4 *op) {
 #pragma unroll
