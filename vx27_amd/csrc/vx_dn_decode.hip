@@ -120,24 +120,49 @@ __global__ __launch_bounds__(HD / CS * R) void dn_decode_kernel(DnArgs a) {
     const float nwc = a.norm_w ? a.norm_w[col] : 1.0f;                // output column weight
     const float qs = 1.0f / sqrtf((float)HD);
 
-    for (int t = 0; t < a.steps; t++) {
+    // The inputs of step t+1 (gates, and x or q/k/v) are loaded while step t
+    // runs: nothing in them depends on the state, so their memory latency
+    // leaves the step's dependent chain.
+    auto fetch = [&](int t, float &xq, float &xk, float &xv, double2 &gg) {
         const size_t sb = (size_t)t * a.t_step + (size_t)b * a.b_step;
-        const double2 gt = a.gates[sb * a.nv + vh];   // uniform address: scalar load
-        // ---- activations of this token
-        float qa = 0.0f, ka = 0.0f, va = 0.0f;
+        gg = a.gates[sb * a.nv + vh];   // uniform address: scalar load
         if (conv) {
             const float *x = a.x + sb * C;
             if (qk_lane) {
-                qa = conv_step(cq, wq, x[chq]);
-                ka = conv_step(ck, wk, x[chk]);
+                xq = x[chq];
+                xk = x[chk];
             }
-            if (v_lane) va = conv_step(cv, wv, x[chv]);
+            if (v_lane) xv = x[chv];
         } else {
             if (qk_lane) {
-                qa = a.q[sb * a.q_tok + (size_t)g * HD + j];
-                ka = a.k[sb * a.k_tok + (size_t)g * HD + j];
+                xq = a.q[sb * a.q_tok + (size_t)g * HD + j];
+                xk = a.k[sb * a.k_tok + (size_t)g * HD + j];
             }
-            if (v_lane) va = a.v[sb * a.v_tok + (size_t)vh * HD + col];
+            if (v_lane) xv = a.v[sb * a.v_tok + (size_t)vh * HD + col];
+        }
+    };
+    float nq = 0.0f, nk = 0.0f, nvx = 0.0f;
+    double2 ng;
+    fetch(0, nq, nk, nvx, ng);
+    for (int t = 0; t < a.steps; t++) {
+        const size_t sb = (size_t)t * a.t_step + (size_t)b * a.b_step;
+        const double2 gt = ng;
+        const float xq = nq, xk = nk, xv = nvx;
+        if (t + 1 < a.steps) fetch(t + 1, nq, nk, nvx, ng);
+        // ---- activations of this token
+        float qa = 0.0f, ka = 0.0f, va = 0.0f;
+        if (conv) {
+            if (qk_lane) {
+                qa = conv_step(cq, wq, xq);
+                ka = conv_step(ck, wk, xk);
+            }
+            if (v_lane) va = conv_step(cv, wv, xv);
+        } else {
+            if (qk_lane) {
+                qa = xq;
+                ka = xk;
+            }
+            if (v_lane) va = xv;
         }
         if (R > 1) va = __shfl(va, (tid & 63) - part, 64);   // from the column's part-0 lane
         // ---- q/k normalisation chain (skipped when q, k arrive final)
