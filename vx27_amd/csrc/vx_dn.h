@@ -46,7 +46,7 @@ __device__ __forceinline__ void load_conv_w(const void *w, int bf16, size_t ch, 
 template <int NW>
 __device__ __forceinline__ void block_sum2(double &u, double &v, double (*slot)[2]) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const double su = vx_wave_sum_f64(u), sv = vx_wave_sum_f64(v);
+    const double su = vx_wave_sum_f64_dpp(u), sv = vx_wave_sum_f64_dpp(v);
     if (lane == 0) {
         slot[wave][0] = su;
         slot[wave][1] = sv;
