@@ -101,7 +101,13 @@ struct DnArgs {
     // call with VX27_DN_OUT_GATE split each head's columns over workgroups
     // (the output norm then runs in a separate finish kernel)
     float *o_pre;
+    // optional scratch of vx_dn_qk_bytes(a) bytes: a multi-step call (no fused
+    // conv) then normalises every token's q and k up front, in parallel, and
+    // the recurrence's per-token chain skips the q/k normalisation
+    float *qk_buf;
 };
+// bytes of DnArgs::qk_buf: q and k of every (token, sequence), [steps*B][nqk][128] each
+inline size_t vx_dn_qk_bytes(int steps, int B, int nqk) { return (size_t)2 * steps * B * nqk * HD * sizeof(float); }
 
 // Channel-parallel causal conv over `steps` tokens (dn_conv_kernel): one
 // thread per (b, c), the state carried in registers; act receives silu(conv).

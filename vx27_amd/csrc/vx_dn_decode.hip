@@ -565,6 +565,43 @@ __global__ __launch_bounds__(256) void dn_conv_kernel(ConvArgs a) {
 
 }  // namespace
 
+// The q/k normalisation chain of dn_decode_kernel for every token up front:
+// grid (rows, nqk), block 128 (lane j = element j), row r = t * t_step +
+// b * b_step as in the recurrence.  The same operations and the same
+// two-wave sums (block_sum2), so the values equal those the recurrence would
+// form in its own chain; written as final (q scaled by 1/sqrt(128)).
+__global__ __launch_bounds__(HD) void dn_qk_norm_kernel(DnArgs a, float *qo, float *ko) {
+    const size_t r = blockIdx.x;
+    const int g = blockIdx.y, j = threadIdx.x;
+    __shared__ double s_red[3][2][2];
+    float qa = a.q[r * a.q_tok + (size_t)g * HD + j];
+    float ka = a.k[r * a.k_tok + (size_t)g * HD + j];
+    const float qs = 1.0f / sqrtf((float)HD);
+    if (a.flags & VX27_DN_PRE_RMS) {       // rmsn(x)*(1+w), vx27_qfwd.c:32-39,123
+        const float nwj = a.norm_w[j];
+        double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+        block_sum2<2>(sq, sk, s_red[0]);
+        const float iq = 1.0f / sqrtf((float)(sq / HD) + 1e-6f);
+        const float ik = 1.0f / sqrtf((float)(sk / HD) + 1e-6f);
+        qa = (qa * iq) * (nwj + 1.0f);
+        ka = (ka * ik) * (nwj + 1.0f);
+    }
+    if (a.flags & VX27_DN_PRE_L2) {        // l2norm + q/sqrt(hd), vx27_qfwd.c:124-130
+        double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+        block_sum2<2>(sq, sk, s_red[1]);
+        qa = qa * (1.0f / sqrtf((float)sq + 1e-6f));
+        ka = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+        qa = qa * qs;
+    }
+    {                                       // inside step_exact, vx27_deltanet.c:77-80
+        double sq = (double)qa * (double)qa, sk = (double)ka * (double)ka;
+        block_sum2<2>(sq, sk, s_red[2]);
+        const float qn = qa * (1.0f / sqrtf((float)sq + 1e-6f));
+        qo[(r * a.nqk + g) * HD + j] = qn * qs;
+        ko[(r * a.nqk + g) * HD + j] = ka * (1.0f / sqrtf((float)sk + 1e-6f));
+    }
+}
+
 bool vx_dn_single_step(const DnArgs &a) {
 #ifndef VX_DN_STEP
 #define VX_DN_STEP 1
@@ -590,6 +627,15 @@ int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a_in) {
         return 0;
     }
     VX_REQUIRE(a.gates != nullptr, "internal: the multi-step recurrence needs mapped gates");
+    if (a.qk_buf && !a.fused_conv && !(a.flags & VX_DN_QK_READY)) {
+        const size_t rows = (size_t)a.steps * a.B;
+        float *qo = a.qk_buf, *ko = a.qk_buf + rows * a.nqk * HD;
+        VX_LAUNCH(ctx, dn_qk_norm_kernel, dim3((unsigned)rows, (unsigned)a.nqk), dim3(HD), a, qo, ko);
+        a.q = qo;
+        a.k = ko;
+        a.q_tok = a.k_tok = (size_t)a.nqk * HD;
+        a.flags |= VX_DN_QK_READY;
+    }
     // (With the output gate, one workgroup per head keeps the norm in the
     // kernel; splitting would need the dn_out_gate launch, which costs more
     // than the split gains.)
@@ -669,9 +715,11 @@ extern "C" int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d) {
     const size_t n_gate = (size_t)d->steps * d->B * d->nv;
     const size_t gate_bytes = (n_gate * sizeof(double2) + 255) & ~(size_t)255;
     const size_t opre_bytes = ((size_t)d->B * vd * sizeof(float) + 255) & ~(size_t)255;
-    const size_t act_elems = sep_conv ? (size_t)d->steps * d->B * C : 0;
+    const size_t act_bytes = ((sep_conv ? (size_t)d->steps * d->B * C : 0) * sizeof(float) + 255) & ~(size_t)255;
+    const size_t qk_bytes = d->steps > 1 ? vx_dn_qk_bytes(d->steps, d->B, d->nqk) : 0;
     void *scr;
-    if (vx_ctx_scratch(ctx, gate_bytes + opre_bytes + act_elems * sizeof(float), &scr)) return -1;
+    if (vx_ctx_scratch(ctx, gate_bytes + opre_bytes + act_bytes + qk_bytes, &scr)) return -1;
+    if (qk_bytes) a.qk_buf = (float *)((char *)scr + gate_bytes + opre_bytes + act_bytes);
     double2 *gates = (double2 *)scr;
     a.o_pre = (float *)((char *)scr + gate_bytes);
     a.ga = d->a; a.gb = d->b; a.A_log = d->A_log; a.dt_bias = d->dt_bias;
