@@ -49,18 +49,20 @@ __global__ __launch_bounds__(256) void dn_gate_kernel(int n, int nv, const float
 
 
 
-// Sum over the R (<= 8) adjacent lanes of a column, a butterfly on the
+// Sum over the R (<= 16) adjacent lanes of a column, a butterfly on the
 // VALU's DPP paths (no LDS crossbar): lane l ^ 1 and l ^ 2 by quad
 // permutes, then, the quads being uniform, the other quad of the 8-lane
-// half-row by row_half_mirror.  Each step adds two values that every lane of
-// the pair sees in the same two roles, so all R lanes end with the same bits
-// (the association of x + shfl_xor(x, 1), 2, 4).
+// half-row by row_half_mirror, and, the half-rows being uniform, the other
+// half of the 16-lane row by row_mirror.  Each step adds two values that
+// every lane of the pair sees in the same two roles, so all R lanes end with
+// the same bits (the association of x + shfl_xor(x, 1), 2, 4, 8).
 template <int R>
 __device__ __forceinline__ double part_sum(double x) {
-    static_assert(R == 1 || R == 2 || R == 4 || R == 8, "part_sum: R lanes per column");
+    static_assert(R == 1 || R == 2 || R == 4 || R == 8 || R == 16, "part_sum: R lanes per column");
     if (R >= 2) x = x + vx_dpp_f64<0xB1, 0xF>(x);    // quad_perm [1,0,3,2]
     if (R >= 4) x = x + vx_dpp_f64<0x4E, 0xF>(x);    // quad_perm [2,3,0,1]
     if (R >= 8) x = x + vx_dpp_f64<0x141, 0xF>(x);   // row_half_mirror
+    if (R >= 16) x = x + vx_dpp_f64<0x140, 0xF>(x);  // row_mirror
     return x;
 }
 
@@ -656,7 +658,7 @@ int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a_in) {
                 VX_LAUNCH_NAMED(ctx, "dn_decode_kernel", (dn_decode_kernel<4, 1>), grid, dim3(HD * 4), a);
             break;
 #ifndef VX_DN_RS
-#define VX_DN_RS 1   // lanes per column = CS * VX_DN_RS
+#define VX_DN_RS 2   // lanes per column = CS * VX_DN_RS
 #endif
         case 2:
             VX_LAUNCH_NAMED(ctx, "dn_decode_kernel", (dn_decode_kernel<2 * VX_DN_RS, 2>), grid, dim3(HD * VX_DN_RS), a);
