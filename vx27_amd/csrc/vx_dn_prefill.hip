@@ -1275,7 +1275,8 @@ size_t vx_dn_prefill_scratch(const vx27_dn_prefill_desc *d) {
     const int qd = d->nqk * HD, vd = d->nv * HD, C = 2 * qd + vd;
     const size_t rows = (size_t)d->B * d->T;
     if (dn_prefill_is_exact(d))
-        return al256(rows * d->nv * sizeof(double2)) + al256((size_t)d->B * vd * sizeof(float)) + rows * C * sizeof(float);
+        return al256(rows * d->nv * sizeof(double2)) + al256((size_t)d->B * vd * sizeof(float)) +
+               al256(rows * C * sizeof(float)) + (d->S_ckpt ? 0 : vx_dn_qk_bytes(d->T, d->B, d->nqk));
     const int NC = (d->T + CH - 1) / CH;
     const bool x3 = !(d->flags & VX27_DN_BF16);
     const size_t n_rec = (size_t)d->B * d->nv * NC;
@@ -1315,6 +1316,7 @@ static int dn_prefill_exact(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, vo
         a.steps = d->T;
         a.q = act; a.k = act + qd; a.v = act + 2 * qd;
         a.gates = gates; a.out = d->out;
+        a.qk_buf = (float *)((char *)act + al256(rows * C * sizeof(float)));
         return vx_dn_recurrence(ctx, a);
     }
     // token by token, the state written out after each (single-step kernel)
