@@ -159,15 +159,23 @@ __global__ __launch_bounds__(64) __attribute__((amdgpu_waves_per_eu(VX_SPLIT_WPE
     // Q^T operand: lane (g,n) holds dims 32s + 8g + 0..7 of query head n
     bf16x8_t qB[8];
     {
+        // every lane loads (lanes past the group's heads re-read head 0 and
+        // zero it), as 16-byte loads all in flight at once: a load under the
+        // lane condition would be a branch with its own wait per element
         const bool live = n < qg;
-        const float *qp = a.q_rot + ((size_t)b * a.n_q + (size_t)kvh * qg + (live ? n : 0)) * HDG;
+        const float4 *qp = (const float4 *)(a.q_rot + ((size_t)b * a.n_q + (size_t)kvh * qg + (live ? n : 0)) * HDG);
+        float4 qv[16];
 #pragma unroll
         for (int s = 0; s < 8; s++) {
+            qv[2 * s] = qp[(32 * s + 8 * g) / 4];
+            qv[2 * s + 1] = qp[(32 * s + 8 * g) / 4 + 1];
+        }
 #pragma unroll
-            for (int e = 0; e < 8; e++) {
-                const float v = live ? qp[32 * s + 8 * g + e] : 0.0f;
-                qB[s][e] = (__bf16)v;
-            }
+        for (int s = 0; s < 8; s++) {
+            const float f[8] = {qv[2 * s].x, qv[2 * s].y, qv[2 * s].z, qv[2 * s].w,
+                                qv[2 * s + 1].x, qv[2 * s + 1].y, qv[2 * s + 1].z, qv[2 * s + 1].w};
+#pragma unroll
+            for (int e = 0; e < 8; e++) qB[s][e] = (__bf16)(live ? f[e] : 0.0f);
         }
     }
     floatx4_t acc[16];
