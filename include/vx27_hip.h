@@ -117,7 +117,7 @@ typedef struct {
     unsigned flags; /* VX27_DN_* */
     float *S;       /* [B][nv][hd][hd] fp32 state, row = key dim, column = value dim; in/out */
     float *conv_state;  /* [B][C][3] fp32, oldest first (VX27_DN_CONV); in/out */
-    const void *conv_w; /* [C][4] weights, tap 3 = newest (VX27_DN_CONV) */
+    const void *conv_w; /* [C][4] weights, tap 3 = newest, 16-byte aligned (VX27_DN_CONV) */
     int conv_w_dtype;   /* VX27_F32 or VX27_BF16 */
     /* Per-token inputs, fp32, token t of sequence b at [t][b]:
      *   VX27_DN_CONV:  x [steps][B][C], C = 2*nqk*hd + nv*hd, channels q|k|v

@@ -40,6 +40,20 @@ __device__ __forceinline__ void load_conv_w(const void *w, int bf16, size_t ch, 
         for (int t = 0; t < 4; t++) out[t] = p[t];
     }
 }
+// Conv weights held as raw words (bf16: the 4 values in r[0..1]; f32:
+// r[0..3]), converted after the load so that the load's wait falls at the
+// first use of the values.
+__device__ __forceinline__ void conv_w_decode(int bf16, const uint32_t r[4], float out[4]) {
+    if (bf16) {
+        out[0] = __uint_as_float(r[0] << 16);
+        out[1] = __uint_as_float(r[0] & 0xffff0000u);
+        out[2] = __uint_as_float(r[1] << 16);
+        out[3] = __uint_as_float(r[1] & 0xffff0000u);
+    } else {
+#pragma unroll
+        for (int t = 0; t < 4; t++) out[t] = __uint_as_float(r[t]);
+    }
+}
 // Sum of two per-lane doubles over all NW waves of the block (wave partials
 // added in wave order); every thread must call it (barrier inside).  slot is
 // private to one call site.

@@ -302,8 +302,10 @@ __global__ __launch_bounds__(HD / CS * R) void dn_decode_kernel(DnArgs a) {
 #ifndef DN_STATE_NT_ST
 #define DN_STATE_NT_ST 1    // streaming stores of the state
 #endif
+template <bool FC>   // FC: the fused conv (a.fused_conv)
 __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
-    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // uniform: wave 0's work is a scalar branch
     const int part = tid >> 5, c4 = tid & 31;
     const int head = blockIdx.x, b = head / a.nv, vh = head % a.nv;
     const int g = vh * a.nqk / a.nv;           // QK head (vx27_qfwd.c:137)
@@ -312,36 +314,45 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
     __shared__ double s_red[8][HD];           // per-wave partial kv, then o
     __shared__ double s_dl[HD];
 
-    // wave 0 owns the head's q, k and v: elements lane and lane + 64
+    // the state rows are loaded first, ahead of every other load and of any
+    // wait (the conv's inputs and the gates' scalar loads would otherwise hold
+    // them back by a round trip); wave 0's q/k chain waits for its own rows
+    float *Sg = a.S + ((size_t)b * a.nv + vh) * HD * HD + (size_t)(8 * part) * HD + 4 * c4;
+    float4 S4[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        const f4v *sp = (const f4v *)(Sg + (size_t)r * HD);
+        const f4v v = DN_STATE_NT_LD ? __builtin_nontemporal_load(sp) : *sp;
+        S4[r] = make_float4(v.x, v.y, v.z, v.w);
+    }
+    // wave 0 owns the head's q, k and v: elements lane and lane + 64.  With
+    // the fused conv (nv == nqk: g == vh) it loads the conv's inputs for this
+    // head's q, k and v channels, branch-free (each channel's weights as two
+    // 8-byte words: the second one repeats the first for bf16), and runs the
+    // conv below.
     float qa[2] = {0.f, 0.f}, ka[2] = {0.f, 0.f}, va[2] = {0.f, 0.f};
+    const int qd = a.nqk * HD, Cc = 2 * qd + a.nv * HD;
+    uint2 cw[2][3][2];
+    float cs[2][3][3], cx[2][3];
     if (wave == 0) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int i = lane + 64 * h;
-            if (a.fused_conv) {   // causal conv + SiLU of this head's q, k, v channels (nv == nqk: g == vh)
-                const int qd = a.nqk * HD, C = 2 * qd + a.nv * HD;
-                const size_t chq = (size_t)g * HD + i, chk = (size_t)qd + g * HD + i,
-                             chv = (size_t)2 * qd + (size_t)vh * HD + i;
-                const float *x = a.x + (size_t)b * a.b_step * C;
-                float *cst = a.conv_state + (size_t)b * C * 3;
-                float wq[4], wk[4], wv[4], cq[3], ck[3], cv[3];
-                load_conv_w(a.conv_w, a.conv_bf16, chq, wq);
-                load_conv_w(a.conv_w, a.conv_bf16, chk, wk);
-                load_conv_w(a.conv_w, a.conv_bf16, chv, wv);
+            if (FC) {
+                const size_t ch[3] = {(size_t)g * HD + i, (size_t)qd + g * HD + i,
+                                      (size_t)2 * qd + (size_t)vh * HD + i};
+                const float *x = a.x + (size_t)b * a.b_step * Cc;
+                const float *cst = a.conv_state + (size_t)b * Cc * 3;
+                const uint2 *wb = (const uint2 *)a.conv_w;
 #pragma unroll
-                for (int t = 0; t < 3; t++) {
-                    cq[t] = cst[chq * 3 + t];
-                    ck[t] = cst[chk * 3 + t];
-                    cv[t] = cst[chv * 3 + t];
-                }
-                qa[h] = conv_step(cq, wq, x[chq]);
-                ka[h] = conv_step(ck, wk, x[chk]);
-                va[h] = conv_step(cv, wv, x[chv]);
+                for (int j = 0; j < 3; j++) {
+                    const size_t w0 = a.conv_bf16 ? ch[j] : 2 * ch[j];
+                    cw[h][j][0] = wb[w0];
+                    cw[h][j][1] = wb[a.conv_bf16 ? w0 : w0 + 1];
 #pragma unroll
-                for (int t = 0; t < 3; t++) {
-                    cst[chq * 3 + t] = cq[t];
-                    cst[chk * 3 + t] = ck[t];
-                    cst[chv * 3 + t] = cv[t];
+                    for (int t = 0; t < 3; t++) cs[h][j][t] = cst[ch[j] * 3 + t];
+                    cx[h][j] = x[ch[j]];
                 }
             } else {
                 const size_t bs = (size_t)b * a.b_step;
@@ -363,26 +374,47 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
             w1 = a.norm_w[lane + 64];
         }
     }
+    // gate inputs (uniform addresses: scalar loads)
+    const size_t ge = (size_t)b * a.b_step * a.nv + vh;
+    double2 gt = {0.0, 0.0};
+    float gbv = 0.f, gav = 0.f, alog = 0.f, dtb = 0.f;
+    if (a.gates) {
+        gt = a.gates[ge];
+    } else {
+        gbv = a.gb[ge];
+        gav = a.ga[ge];
+        alog = a.A_log[vh];
+        dtb = a.dt_bias[vh];
+    }
     double beta, decay;
     if (a.gates) {
-        const double2 gt = a.gates[(size_t)b * a.b_step * a.nv + vh];   // uniform address: scalar load
         beta = gt.x;
         decay = gt.y;
     } else {   // vx27_deltanet_gate_params (vx27_deltanet.c:65-69), decay = exp(g_log)
-        const size_t e = (size_t)b * a.b_step * a.nv + vh;
-        beta = 1.0 / (1.0 + exp(-(double)a.gb[e]));
-        decay = exp(-exp((double)a.A_log[vh]) * softplus_d((double)a.ga[e] + (double)a.dt_bias[vh]));
+        beta = 1.0 / (1.0 + exp(-(double)gbv));
+        decay = exp(-exp((double)alog) * softplus_d((double)gav + (double)dtb));
     }
-    // state loads after the small ones: those return first (loads complete in
-    // order), so the q/k chain below overlaps the state's arrival
-    float *Sg = a.S + ((size_t)b * a.nv + vh) * HD * HD + (size_t)(8 * part) * HD + 4 * c4;
-    float4 S4[8];
+    if (FC && wave == 0) {   // causal conv + SiLU, conv state written back
+        float *cst = a.conv_state + (size_t)b * Cc * 3;
 #pragma unroll
-    for (int r = 0; r < 8; r++) {
-        typedef float f4v __attribute__((ext_vector_type(4)));
-        const f4v *sp = (const f4v *)(Sg + (size_t)r * HD);
-        const f4v v = DN_STATE_NT_LD ? __builtin_nontemporal_load(sp) : *sp;
-        S4[r] = make_float4(v.x, v.y, v.z, v.w);
+        for (int h = 0; h < 2; h++) {
+            const int i = lane + 64 * h;
+            const size_t ch[3] = {(size_t)g * HD + i, (size_t)qd + g * HD + i,
+                                  (size_t)2 * qd + (size_t)vh * HD + i};
+            float w[3][4];
+#pragma unroll
+            for (int j = 0; j < 3; j++) {
+                const uint32_t r[4] = {cw[h][j][0].x, cw[h][j][0].y, cw[h][j][1].x, cw[h][j][1].y};
+                conv_w_decode(a.conv_bf16, r, w[j]);
+            }
+            qa[h] = conv_step(cs[h][0], w[0], cx[h][0]);
+            ka[h] = conv_step(cs[h][1], w[1], cx[h][1]);
+            va[h] = conv_step(cs[h][2], w[2], cx[h][2]);
+#pragma unroll
+            for (int j = 0; j < 3; j++)
+#pragma unroll
+                for (int t = 0; t < 3; t++) cst[ch[j] * 3 + t] = cs[h][j][t];
+        }
     }
     if (wave == 0 && !(a.flags & VX_DN_QK_READY)) {
         // q/k normalisation chain (vx27_qfwd.c:119-130 per flags, then
@@ -625,7 +657,10 @@ int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a_in) {
     const int heads = a.B * a.nv;
     const bool gate = (a.flags & VX27_DN_OUT_GATE) != 0;
     if (vx_dn_single_step(a)) {
-        VX_LAUNCH(ctx, dn_step_kernel, dim3((unsigned)heads), dim3(512), a);
+        if (a.fused_conv)
+            VX_LAUNCH_NAMED(ctx, "dn_step_kernel", dn_step_kernel<true>, dim3((unsigned)heads), dim3(512), a);
+        else
+            VX_LAUNCH_NAMED(ctx, "dn_step_kernel", dn_step_kernel<false>, dim3((unsigned)heads), dim3(512), a);
         return 0;
     }
     VX_REQUIRE(a.gates != nullptr, "internal: the multi-step recurrence needs mapped gates");
@@ -691,6 +726,7 @@ extern "C" int vx27_hip_dn_decode(vx27_hip_ctx *ctx, const vx27_dn_desc *d) {
         VX_REQUIRE(d->x && d->conv_state && d->conv_w, "vx27_hip_dn_decode: conv needs x, conv_state, conv_w");
         VX_REQUIRE(d->conv_w_dtype == VX27_F32 || d->conv_w_dtype == VX27_BF16,
                    "vx27_hip_dn_decode: conv_w_dtype must be VX27_F32 or VX27_BF16");
+        VX_REQUIRE(((uintptr_t)d->conv_w & 15) == 0, "vx27_hip_dn_decode: conv_w must be 16-byte aligned");
     } else {
         VX_REQUIRE(d->q && d->k && d->v, "vx27_hip_dn_decode: q, k, v are required without conv");
     }
