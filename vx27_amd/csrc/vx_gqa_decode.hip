@@ -30,6 +30,7 @@
 //                                           dim-major V block.
 #include <math.h>
 
+#include <algorithm>
 #include <mutex>
 
 #include "vx_gemv.h"
@@ -54,11 +55,11 @@ __device__ __forceinline__ size_t v_index(int n_kv, int L, int b, int h, int p, 
     return vx_v_index(n_kv, L, b, h, p, i);
 }
 
-// Block-wide double sum over 256 threads (4 waves); contains barriers.
+// Block-wide double sum over 256 threads (4 waves, wave sums on the DPP
+// paths, then in wave order); contains barriers.
 __device__ __forceinline__ double block_sum256(double v, double *red) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    v = vx_wave_sum_f64(v);
-    __syncthreads();
+    v = vx_wave_sum_f64_dpp(v);
     if (lane == 0) red[wave] = v;
     __syncthreads();
     return ((red[0] + red[1]) + red[2]) + red[3];
@@ -85,6 +86,17 @@ __global__ __launch_bounds__(256) void gqa_prep(PrepArgs a) {
     __shared__ double red[4];
     __shared__ float row[HDG];
     __shared__ float cs[MAXR], sn[MAXR];
+    // the row's loads first (one load each, from an address chosen per head
+    // kind): they do not need the position, whose load and angles follow
+    const bool is_q = h < a.n_q;
+    const int hk = h - a.n_q;
+    const float *xp = is_q ? a.q + (size_t)b * a.q_ss + (size_t)h * a.q_hs + i
+                           : a.k_new + (size_t)b * a.kv_ss + (size_t)hk * HDG + i;
+    const float *vp = is_q ? xp : a.v_new + (size_t)b * a.kv_ss + (size_t)hk * HDG + i;
+    const float x = *xp;
+    const float w = (is_q ? a.q_norm_w : a.k_norm_w)[i];
+    const float vv = *vp;   // the new value row (k heads; q heads re-read x)
+    const float fr = a.rope.freq[min(i, MAXR - 1)];
     // positions outside the cache are clamped so no access leaves the
     // buffers, and flagged for vx27_hip_sync to report (the host contract is
     // 0 <= pos < L)
@@ -93,15 +105,10 @@ __global__ __launch_bounds__(256) void gqa_prep(PrepArgs a) {
     if (pos != pos_in && h == 0 && i == 0) *a.err_flag = 1;
     const int half = a.rope_dim / 2;
     if (i < half) {
-        const float2 c = vx_rope_cs(a.rope, pos, a.yarn, i);
+        const float2 c = vx_rope_cs_f(fr, pos, a.yarn);
         cs[i] = c.x;
         sn[i] = c.y;
     }
-    const bool is_q = h < a.n_q;
-    const int hk = h - a.n_q;
-    const float x = is_q ? a.q[(size_t)b * a.q_ss + (size_t)h * a.q_hs + i]
-                         : a.k_new[(size_t)b * a.kv_ss + (size_t)hk * HDG + i];
-    const float w = is_q ? a.q_norm_w[i] : a.k_norm_w[i];
     const double ss = block_sum256((double)x * (double)x, red);
     const float s = 1.0f / sqrtf((float)(ss / HDG) + 1e-6f);
     const float y = (a.flags & VX27_GQA_NORM_W) ? (x * s) * w : (x * s) * (w + 1.0f);
@@ -117,7 +124,6 @@ __global__ __launch_bounds__(256) void gqa_prep(PrepArgs a) {
         a.q_out[((size_t)b * a.n_q + h) * HDG + i] = r;
     } else {
         a.k_cache[k_index(a.B, a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(r);
-        const float vv = a.v_new[(size_t)b * a.kv_ss + (size_t)hk * HDG + i];
         a.v_cache[v_index(a.n_kv, a.L, b, hk, pos, i)] = vx_f32_to_bf16(vv);
     }
 }
@@ -279,42 +285,81 @@ struct CombArgs {
     uint16_t *out_packed;        // optional packed GEMV operand of out (K = n_q*256)
 };
 
-// grid (n_q, B, 4 dim chunks), block 256: wave w merges splits w, w+4, ...
-// for 64 dims, then the four waves are merged in LDS in wave order.
-__global__ __launch_bounds__(256) void gqa_combine(CombArgs a) {
-    const int h = blockIdx.x, b = blockIdx.y, wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int i = blockIdx.z * 64 + lane;
+// grid (n_q, B), block 64 nw (nw <= 16 waves, enough for 12 splits a wave):
+// wave w merges splits w, w + nw, ... over all 256 dims (four per lane, one
+// 16-byte load per split), against its own running maximum, with the loads
+// of 12 splits in flight at once; the nw wave results are then merged in LDS
+// in wave order.  One pass over the partials.
+constexpr int CB_W = 16, CB_N = 12;
+__global__ __launch_bounds__(1024) void gqa_combine(CombArgs a) {
+    const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), nw = blockDim.x >> 6;
     const int qg = a.n_q / a.n_kv, kvh = h / qg, n = h % qg;
     const size_t base = ((size_t)b * a.n_kv + kvh) * a.n_split;
-    __shared__ float s_o[4][64], s_l[4];
-    // global max of the split maxima (every wave computes it)
-    float M = -INFINITY;
-    for (int s = lane; s < a.n_split; s += 64) M = fmaxf(M, a.part_ml[((base + s) * qg + n) * 2]);
+    __shared__ float4 s_o[CB_W][64];
+    __shared__ float s_m[CB_W], s_l[CB_W];
+    float gl = 0.0f;   // the gate of dim tid, loaded first
+    if (a.gate && tid < HDG) gl = a.gate[(size_t)b * a.g_ss + (size_t)h * a.g_hs + tid];
+    float M = -INFINITY, L = 0.0f;
+    float4 O = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (int s0 = wave; s0 < a.n_split; s0 += nw * CB_N) {
+        // (m, l) of split s0 + nw j by lane j (lanes repeat j mod 16), then
+        // the CB_N partial rows; past n_split the last split is re-read,
+        // weighed 0
+        const float2 ml = ((const float2 *)a.part_ml)[(base + min(s0 + nw * (lane & 15), a.n_split - 1)) * qg + n];
+        float4 o[CB_N];
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1) M = fmaxf(M, __shfl_xor(M, off, 64));
-    float L = 0.0f, O = 0.0f;
-#pragma unroll 8
-    for (int s = wave; s < a.n_split; s += 4) {
-        const float m = a.part_ml[((base + s) * qg + n) * 2];
-        const float l = a.part_ml[((base + s) * qg + n) * 2 + 1];
-        const float o = a.part_o[((base + s) * qg + n) * HDG + i];
-        const float w = (m == -INFINITY) ? 0.0f : exp2f(m - M);
-        L += l * w;
-        O += o * w;
+        for (int j = 0; j < CB_N; j++) {
+            const size_t pi = (base + min(s0 + nw * j, a.n_split - 1)) * qg + n;
+            o[j] = ((const float4 *)(a.part_o + pi * HDG))[lane];
+        }
+        __builtin_amdgcn_sched_barrier(0);   // every load issued before the first wait
+        float m[CB_N], l[CB_N];
+        float mb = M;
+#pragma unroll
+        for (int j = 0; j < CB_N; j++) {
+            m[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml.x), j));
+            l[j] = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(ml.y), j));
+            if (s0 + nw * j >= a.n_split) m[j] = -INFINITY;
+            mb = fmaxf(mb, m[j]);
+        }
+        // no branch here (the partial rows' loads would sink into it): with
+        // every maximum still -inf the sums stay 0
+        const bool none = mb == -INFINITY;
+        const float sc = none ? 1.0f : exp2f(M - mb);   // 0 while M is -inf
+        L *= sc;
+        O.x *= sc; O.y *= sc; O.z *= sc; O.w *= sc;
+#pragma unroll
+        for (int j = 0; j < CB_N; j++) {
+            const float w = none ? 0.0f : exp2f(m[j] - mb);
+            L += l[j] * w;
+            O.x += o[j].x * w; O.y += o[j].y * w; O.z += o[j].z * w; O.w += o[j].w * w;
+        }
+        M = mb;
     }
     s_o[wave][lane] = O;
-    if (lane == 0) s_l[wave] = L;
-    __syncthreads();
-    if (wave != 0) return;
-    const float Lt = ((s_l[0] + s_l[1]) + s_l[2]) + s_l[3];
-    const float Ot = ((s_o[0][lane] + s_o[1][lane]) + s_o[2][lane]) + s_o[3][lane];
-    float r = Ot / Lt;
-    if (a.gate) {
-        const float gl = a.gate[(size_t)b * a.g_ss + (size_t)h * a.g_hs + i];
-        r = r * (1.0f / (1.0f + expf(-gl)));
+    if (lane == 0) {
+        s_m[wave] = M;
+        s_l[wave] = L;
     }
-    if (a.out) a.out[((size_t)b * a.n_q + h) * HDG + i] = r;
-    if (a.out_packed) vx_pack_store(a.out_packed, a.B, b, h * HDG + i, r);
+    __syncthreads();
+    for (int d = tid; d < HDG; d += blockDim.x) {
+        float Mt = s_m[0];
+        for (int w = 1; w < nw; w++) Mt = fmaxf(Mt, s_m[w]);
+        float Lt = 0.0f, Ot = 0.0f;
+        for (int w = 0; w < nw; w++) {
+            const float sc = (s_m[w] == -INFINITY) ? 0.0f : exp2f(s_m[w] - Mt);
+            Lt += s_l[w] * sc;
+            Ot += ((const float *)s_o[w])[d] * sc;
+        }
+        float r = Ot / Lt;
+        if (a.gate) {
+            if (d != tid) gl = a.gate[(size_t)b * a.g_ss + (size_t)h * a.g_hs + d];
+            r = r * (1.0f / (1.0f + expf(-gl)));
+        }
+        if (a.out) a.out[((size_t)b * a.n_q + h) * HDG + d] = r;
+        if (a.out_packed) vx_pack_store(a.out_packed, a.B, b, h * HDG + d, r);
+    }
 }
 
 struct KvMoveArgs {
@@ -435,7 +480,8 @@ int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uin
     ca.part_o = part_o; ca.part_ml = part_ml; ca.gate = (d->flags & VX27_GQA_NO_GATE) ? nullptr : d->gate;
     ca.g_ss = d->gate_seq_stride; ca.g_hs = d->gate_head_stride; ca.out = d->out;
     ca.out_packed = out_packed;
-    VX_LAUNCH(ctx, gqa_combine, dim3(d->n_q, d->B, HDG / 64), dim3(256), ca);
+    const int cb_waves = std::min(CB_W, (n_split + CB_N - 1) / CB_N);
+    VX_LAUNCH(ctx, gqa_combine, dim3(d->n_q, d->B), dim3(64 * cb_waves), ca);
     return 0;
 }
 
