@@ -542,7 +542,9 @@ constexpr size_t XREC = X_GC + 256;
 struct Prep3Args {
     int T, nqk, nv, NC;
     const uint16_t *q, *k, *v;          // hi parts [B][T][nqk|nqk|nv][128] bf16
-    const uint16_t *ql, *kl, *vl;       // lo parts, or NULL
+    const uint16_t *ql, *kl;            // lo parts of q, k as rows, or NULL
+    const uint16_t *klT, *vlT;          // lo parts of k, v transposed, [B][nqk|nv][128][Tp]
+    int Tp;
     const float *a, *b;
     const float *A_log, *dt_bias;
     char *rec;                          // [B][nv][NC] records of XREC bytes
@@ -558,21 +560,10 @@ __device__ __forceinline__ void split8(const float *f, uint4 &hi, uint4 &lo) {
     lo = pack8(r);
 }
 
-// LDS of dnp_prep3 (phases as dnp_prep's; every bf16 array has a lo twin)
-constexpr int X3_QH = 0;                                  // q rows hi -> P hi staging -> T fp32
-constexpr int X3_QL = X3_QH + CH * RP * 2;                // q rows lo -> P lo staging
-constexpr int X3_KH = X3_QL + CH * RP * 2;                // k rows hi -> V^T hi -> -W hi staging
-constexpr int X3_KL = X3_KH + HD * TP * 2;                // k rows lo -> V^T lo -> -W lo staging
-constexpr int X3_TH = X3_KL + HD * TP * 2;                // K^T hi
-constexpr int X3_TL = X3_TH + HD * TP * 2;                // K^T lo
-constexpr int X3_AS = X3_TL + HD * TP * 2;                // A fp32
-constexpr int X3_MT = X3_AS + CH * AP * 4;
-constexpr int X3_GAM = X3_MT + 3 * 256 * 4;
-constexpr int X3_SC = X3_GAM + CH * 8;
-constexpr int X3_TOTAL = X3_SC + 5 * CH * 4;
-static_assert(CH * RP * 2 <= HD * TP * 2, "k rows fit the V^T region");
-// Without lo parts (bf16 inputs) four regions suffice, 76.5 KiB, so two
-// workgroups share a CU:
+// LDS of dnp_prep3 (phases as dnp_prep's), 76.5 KiB, so two workgroups
+// share a CU: four regions whose contents change with the phase.  The lo
+// parts of split inputs never enter it: each is read from global memory in
+// the layout its use needs (rows, or transposed).
 constexpr int XN_QH = 0;                        // q rows -> P hi staging -> v rows -> T fp32
 constexpr int XN_KH = XN_QH + CH * RP * 2;      // k rows -> P lo staging -> V^T -> -W hi staging
 constexpr int XN_TH = XN_KH + HD * TP * 2;      // K^T -> -W lo staging
@@ -607,8 +598,9 @@ __device__ __forceinline__ void tr_rows(const uint16_t *src, uint16_t *dst, int 
     }
 }
 
-// LO: the inputs come with lo parts (the glue's fp32 values as bf16 pairs);
-// without them every lo array is zero and is neither stored nor read.
+// LO: the inputs come with lo parts (the glue's fp32 values as bf16 pairs),
+// read from global memory where a product or an operand tile takes them;
+// without them they are zero and never read.
 template <bool LO>
 __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
     const int c = blockIdx.x, vh = blockIdx.y, b = blockIdx.z;
@@ -619,24 +611,38 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
     const int nvalid = min(CH, p.T - t0);
     constexpr bool has_lo = LO;
 
-    __shared__ __attribute__((aligned(16))) char smem[LO ? X3_TOTAL : XN_TOTAL];
-    constexpr int QH = LO ? X3_QH : XN_QH, KH = LO ? X3_KH : XN_KH, TH = LO ? X3_TH : XN_TH;
-    constexpr int QL = LO ? X3_QL : XN_QH, KL = LO ? X3_KL : XN_KH, TL = LO ? X3_TL : XN_TH;
-    constexpr int PL = LO ? X3_QL : XN_KH, WL = LO ? X3_KL : XN_TH;
-    constexpr int AS = LO ? X3_AS : XN_AS, MT = LO ? X3_MT : XN_MT, GAM = LO ? X3_GAM : XN_GAM;
-    constexpr int SCL = LO ? X3_SC : XN_SC;
-    uint16_t *q_rows = (uint16_t *)(smem + QH), *q_lo = (uint16_t *)(smem + QL);
-    uint16_t *P_h = (uint16_t *)(smem + QH), *P_l = (uint16_t *)(smem + PL);          // [64][TP]
-    float *T_s = (float *)(smem + QH);                                                // [64][64]
-    uint16_t *k_rows = (uint16_t *)(smem + KH), *k_lo = (uint16_t *)(smem + KL);
-    uint16_t *V_h = (uint16_t *)(smem + KH), *V_l = (uint16_t *)(smem + KL);          // [128][TP]
-    uint16_t *W_h = (uint16_t *)(smem + KH), *W_l = (uint16_t *)(smem + WL);          // [64][RP]
-    uint16_t *K_h = (uint16_t *)(smem + TH), *K_l = (uint16_t *)(smem + TL);          // [128][TP]
-    float *A_s = (float *)(smem + AS);
-    float *M_t = (float *)(smem + MT);
-    double *gam_s = (double *)(smem + GAM);
-    float *beta_s = (float *)(smem + SCL), *eg_s = beta_s + CH, *egc_s = eg_s + CH;
+    __shared__ __attribute__((aligned(16))) char smem[XN_TOTAL];
+    uint16_t *q_rows = (uint16_t *)(smem + XN_QH);
+    uint16_t *P_h = (uint16_t *)(smem + XN_QH), *P_l = (uint16_t *)(smem + XN_KH);    // [64][TP]
+    float *T_s = (float *)(smem + XN_QH);                                             // [64][64]
+    uint16_t *k_rows = (uint16_t *)(smem + XN_KH);
+    uint16_t *V_h = (uint16_t *)(smem + XN_KH);                                       // [128][TP]
+    uint16_t *W_h = (uint16_t *)(smem + XN_KH), *W_l = (uint16_t *)(smem + XN_TH);    // [64][RP]
+    uint16_t *K_h = (uint16_t *)(smem + XN_TH);                                       // [128][TP]
+    float *A_s = (float *)(smem + XN_AS);
+    float *M_t = (float *)(smem + XN_MT);
+    double *gam_s = (double *)(smem + XN_GAM);
+    float *beta_s = (float *)(smem + XN_SC), *eg_s = beta_s + CH, *egc_s = eg_s + CH;
     float *iq_s = egc_s + CH, *ik_s = iq_s + CH;
+    // lo parts from global memory: 8 dims d0.. of row r of the chunk (q or
+    // k; rows past the prompt read row 0 and give zeros), and 8 tokens t..
+    // of dim d of the transposed k or v (zero past the prompt)
+    const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+    auto lo_row = [&](const uint16_t *base, int r, int d0) -> uint4 {
+        const size_t row = ((size_t)b * p.T + t0 + (r < nvalid ? r : 0)) * p.nqk + qh;
+        const u32x4_t v = *(g_u32x4 *)(base + row * HD + d0);
+        // masked by AND with an opaque mask: a select would let the compiler
+        // move the load under a branch, with a wait at its end
+        uint32_t mk = r < nvalid ? 0xffffffffu : 0u;
+        __asm__("" : "+v"(mk));
+        return make_uint4(v.x & mk, v.y & mk, v.z & mk, v.w & mk);
+    };
+    const uint16_t *klT = LO ? p.klT + ((size_t)b * p.nqk + qh) * HD * p.Tp + t0 : nullptr;
+    const uint16_t *vlT = LO ? p.vlT + ((size_t)b * p.nv + vh) * HD * p.Tp + t0 : nullptr;
+    auto lo_tr = [&](const uint16_t *base, int d, int t) -> uint4 {
+        const u32x4_t v = *(g_u32x4 *)(base + (size_t)d * p.Tp + t);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    };
 
     // ---- phase 1: gates (wave 0); k, q, v rows (waves 1, 2, 3), hi and lo
     if (wave == 0) {
@@ -663,11 +669,12 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
         const size_t row = wave == 3 ? (((size_t)b * p.T + t0 + lane) * p.nv + vh) * HD
                                      : (((size_t)b * p.T + t0 + lane) * p.nqk + qh) * HD;
         const uint16_t *src = wave == 1 ? p.k : wave == 2 ? p.q : p.v;
-        const uint16_t *srl = wave == 1 ? p.kl : wave == 2 ? p.ql : p.vl;
+        const uint16_t *srl = wave == 1 ? p.kl : p.ql;   // (v's lo part is read transposed, in phase 5)
 #pragma unroll
         for (int j = 0; j < 16; j++) {
             raw[j] = lane < nvalid ? *(const uint4 *)(src + row + 8 * j) : make_uint4(0u, 0u, 0u, 0u);
-            rawl[j] = (has_lo && lane < nvalid) ? *(const uint4 *)(srl + row + 8 * j) : make_uint4(0u, 0u, 0u, 0u);
+            rawl[j] = (has_lo && wave < 3 && lane < nvalid) ? *(const uint4 *)(srl + row + 8 * j)
+                                                            : make_uint4(0u, 0u, 0u, 0u);
         }
     }
     if (wave == 1 || wave == 2) {
@@ -686,18 +693,34 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
             }
         }
         const float inv = 1.0f / sqrtf((float)ss + 1e-6f);   // l2norm, vx27_deltanet.c:51-56
-        uint16_t *rows = wave == 1 ? k_rows : q_rows, *rowl = wave == 1 ? k_lo : q_lo;
+        uint16_t *rows = wave == 1 ? k_rows : q_rows;
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            *(uint4 *)&rows[lane * RP + 8 * j] = raw[j];
-            if (LO) *(uint4 *)&rowl[lane * RP + 8 * j] = rawl[j];
-        }
+        for (int j = 0; j < 16; j++) *(uint4 *)&rows[lane * RP + 8 * j] = raw[j];
         if (wave == 1) ik_s[lane] = inv;
         else iq_s[lane] = inv;
     }
     __syncthreads();
-    tr_rows(k_rows, K_h, tid);   // K^T (hi, lo) by all waves
-    if (LO) tr_rows(k_lo, K_l, tid);
+    // the lo operands of phase 2 (split inputs), all issued now so that they
+    // arrive during the transposition: this wave's q and k rows (A) and the
+    // chunk's k rows (B) for every k-step, and its Kt^T tiles' lo parts
+    const int rowA = wave * 16 + m;
+    uint4 qal[4], kal[4], bkl[4][4], krl[4];
+    if (LO) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            qal[ks] = lo_row(p.ql, rowA, 32 * ks + 8 * g);
+            kal[ks] = lo_row(p.kl, rowA, 32 * ks + 8 * g);
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++) bkl[nb][ks] = lo_row(p.kl, nb * 16 + m, 32 * ks + 8 * g);
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int tile = wave * 4 + j;
+            krl[j] = lo_tr(klT, (tile >> 1) * 16 + m, 32 * (tile & 1) + 8 * g);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    tr_rows(k_rows, K_h, tid);   // K^T by all waves
     __syncthreads();
 
     char *rec = p.rec + (((size_t)b * p.nv + vh) * p.NC + c) * XREC;
@@ -712,16 +735,14 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
         acck[nb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
         accq[nb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
     }
-    const int rowA = wave * 16 + m;
     const float qeA = eg_s[rowA] * (iq_s[rowA] * qscale);
 #pragma unroll
     for (int ks = 0; ks < 4; ks++) {
         const int d0 = 32 * ks + 8 * g;
-        const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
-        const uint4 qa = *(const uint4 *)&q_rows[rowA * RP + d0], qal = LO ? *(const uint4 *)&q_lo[rowA * RP + d0] : z4;
-        const uint4 ka = *(const uint4 *)&k_rows[rowA * RP + d0], kal = LO ? *(const uint4 *)&k_lo[rowA * RP + d0] : z4;
+        const uint4 qa = *(const uint4 *)&q_rows[rowA * RP + d0], qlo = LO ? qal[ks] : z4;
+        const uint4 ka = *(const uint4 *)&k_rows[rowA * RP + d0], klo = LO ? kal[ks] : z4;
         {   // e^gam qn tile (row block wave, k-step ks), hi and lo
-            const uint16_t *qs = (const uint16_t *)&qa, *qsl = (const uint16_t *)&qal;
+            const uint16_t *qs = (const uint16_t *)&qa, *qsl = (const uint16_t *)&qlo;
             float f[8];
 #pragma unroll
             for (int e = 0; e < 8; e++) f[e] = qeA * (vx_bf16_to_f32(qs[e]) + vx_bf16_to_f32(qsl[e]));
@@ -736,11 +757,11 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
             acck[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka), bk, acck[nb], 0, 0, 0);
             accq[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa), bk, accq[nb], 0, 0, 0);
             if (has_lo) {
-                const bf16x8_t bkl = as_bf16x8(*(const uint4 *)&k_lo[(nb * 16 + m) * RP + d0]);
-                acck[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(kal), bk, acck[nb], 0, 0, 0);
-                acck[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka), bkl, acck[nb], 0, 0, 0);
-                accq[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qal), bk, accq[nb], 0, 0, 0);
-                accq[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa), bkl, accq[nb], 0, 0, 0);
+                const bf16x8_t bklo = as_bf16x8(bkl[nb][ks]);
+                acck[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(klo), bk, acck[nb], 0, 0, 0);
+                acck[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(ka), bklo, acck[nb], 0, 0, 0);
+                accq[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qlo), bk, accq[nb], 0, 0, 0);
+                accq[nb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(as_bf16x8(qa), bklo, accq[nb], 0, 0, 0);
             }
         }
     }
@@ -750,8 +771,8 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
         const int tile = wave * 4 + j, rb = tile >> 1, ks = tile & 1;
         const int i = rb * 16 + m, tb = 32 * ks + 8 * g;
         const uint4 kr = *(const uint4 *)&K_h[i * TP + tb];
-        const uint4 krl = LO ? *(const uint4 *)&K_l[i * TP + tb] : make_uint4(0u, 0u, 0u, 0u);
-        const uint16_t *kv = (const uint16_t *)&kr, *kvl = (const uint16_t *)&krl;
+        const uint4 krlo = LO ? krl[j] : z4;
+        const uint16_t *kv = (const uint16_t *)&kr, *kvl = (const uint16_t *)&krlo;
         float f[8];
 #pragma unroll
         for (int e = 0; e < 8; e++)
@@ -804,15 +825,22 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
     __syncthreads();   // P staging is read out: the q region takes the v rows, then T
     if (wave == 3) {
 #pragma unroll
-        for (int j = 0; j < 16; j++) {
-            *(uint4 *)&q_rows[lane * RP + 8 * j] = raw[j];
-            if (LO) *(uint4 *)&q_lo[lane * RP + 8 * j] = rawl[j];
-        }
+        for (int j = 0; j < 16; j++) *(uint4 *)&q_rows[lane * RP + 8 * j] = raw[j];
     }
     __syncthreads();
-    tr_rows(q_rows, V_h, tid);   // V^T (hi, lo) by all waves
-    if (LO) tr_rows(q_lo, V_l, tid);
+    tr_rows(q_rows, V_h, tid);   // V^T by all waves
     __syncthreads();
+
+    // the lo parts of phase 5's B operands (split inputs): V^T's now, to
+    // arrive during the inversion; K^T's at the start of phase 5
+    uint4 vlo[8][2], klo5[8][2];
+    if (LO) {
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++)
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) vlo[cb][ks] = lo_tr(vlT, cb * 16 + m, 32 * ks + 8 * g);
+    }
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- phase 4: T = (I + A)^-1 (as dnp_prep)
     if (tid < 64) {
@@ -890,12 +918,19 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
         tk[ks][0] = as_bf16x8(hk);
         tk[ks][1] = as_bf16x8(lk);
     }
+    if (LO) {
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++)
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) klo5[cb][ks] = lo_tr(klT, cb * 16 + m, 32 * ks + 8 * g);
+    }
+    __builtin_amdgcn_sched_barrier(0);
     floatx4_t wacc[8];
     float *ut = (float *)(rec + X_UT);
 #pragma unroll
     for (int cb = 0; cb < 16; cb++) {
         const bool isv = cb < 8;
-        const uint16_t *src = isv ? V_h : K_h, *srl = isv ? V_l : K_l;
+        const uint16_t *src = isv ? V_h : K_h;
         const int col = (cb & 7) * 16 + m;
         floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -904,7 +939,7 @@ __global__ __launch_bounds__(256) void dnp_prep3(Prep3Args p) {
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(isv ? tv[ks][0] : tk[ks][0], bop, acc, 0, 0, 0);
             acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(isv ? tv[ks][1] : tk[ks][1], bop, acc, 0, 0, 0);
             if (has_lo) {
-                const bf16x8_t bol = as_bf16x8(*(const uint4 *)&srl[col * TP + 32 * ks + 8 * g]);
+                const bf16x8_t bol = as_bf16x8(isv ? vlo[cb & 7][ks] : klo5[cb & 7][ks]);
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(isv ? tv[ks][0] : tk[ks][0], bol, acc, 0, 0, 0);
             }
         }
@@ -1151,7 +1186,12 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
 // l2norm with q/sqrt(128) (:124-130), sums in double -- and the result as
 // bf16 hi (and lo) for the chunked products (whose prep applies step_exact's
 // own l2norm and scale once more, as the reference does).
-// grid (ceil(T/GT), ceil(heads/4), B), block 256.
+// The lo parts (split form) go to the layouts the chunk prep reads them in:
+// q and k lo as rows, k and v lo also transposed, [B][head][128 dims][Tp
+// tokens] with Tp the prompt padded to whole chunks (8 tokens of a dim are
+// one 16-byte store; the blocks past T write the padding's zeros).
+// grid (ceil(Tp/GT) with lo parts, else ceil(T/GT), ceil(heads/4), B),
+// block 256.
 constexpr int GT = 8;
 struct GlueInArgs {
     int B, T, nqk, nv, C;
@@ -1163,7 +1203,9 @@ struct GlueInArgs {
     const uint16_t *q, *k, *v; // bf16 inputs without VX27_DN_CONV
     const float *norm_w;       // [128]
     uint16_t *qo, *ko, *vo;    // bf16 [B][T][nqk|nqk|nv][128]
-    uint16_t *qol, *kol, *vol; // their lo parts (x - bf16(x)), or NULL
+    uint16_t *qol, *kol;       // lo parts (x - bf16(x)) of q, k as rows, or NULL
+    uint16_t *klT, *vlT;       // lo parts of k, v transposed, [B][nqk|nv][128][Tp]
+    int Tp;
 };
 __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
@@ -1171,6 +1213,18 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
     const int nh = 2 * a.nqk + a.nv;
     if (hh >= nh) return;
     const bool is_q = hh < a.nqk, is_k = !is_q && hh < 2 * a.nqk;
+    // transposed lo rows of this head's two dims (k and v heads)
+    uint16_t *tl = nullptr;
+    if (a.qol && !is_q)
+        tl = is_k ? a.klT + ((size_t)b * a.nqk + (hh - a.nqk)) * HD * a.Tp
+                  : a.vlT + ((size_t)b * a.nv + (hh - 2 * a.nqk)) * HD * a.Tp;
+    if (t0 >= a.T) {   // padding past the prompt: zeros in the transposed lo rows
+        if (tl) {
+#pragma unroll
+            for (int e = 0; e < 2; e++) *(uint4 *)&tl[(size_t)(lane + 64 * e) * a.Tp + t0] = make_uint4(0u, 0u, 0u, 0u);
+        }
+        return;
+    }
     const bool conv = (a.flags & VX27_DN_CONV) != 0;
     const float qs = 1.0f / sqrtf((float)HD);
     const int nt = min(GT, a.T - t0);
@@ -1191,6 +1245,7 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
         }
         if (a.norm_w && (is_q || is_k)) nw[e] = a.norm_w[lane + 64 * e];
     }
+    uint64_t lt[2][2] = {{0, 0}, {0, 0}};   // the block's transposed lo values, four tokens a word
     for (int j = 0; j < nt; j++) {
         const size_t row = (size_t)b * a.T + t0 + j;
         float v2[2];
@@ -1230,12 +1285,28 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
         dst[lane] = h0;
         dst[lane + 64] = h1;
         if (a.qol) {
-            uint16_t *dl = is_q ? a.qol + (row * a.nqk + hh) * HD
-                         : is_k ? a.kol + (row * a.nqk + (hh - a.nqk)) * HD
-                                : a.vol + (row * a.nv + (hh - 2 * a.nqk)) * HD;
-            dl[lane] = vx_f32_to_bf16(v2[0] - vx_bf16_to_f32(h0));
-            dl[lane + 64] = vx_f32_to_bf16(v2[1] - vx_bf16_to_f32(h1));
+            const uint16_t l0 = vx_f32_to_bf16(v2[0] - vx_bf16_to_f32(h0));
+            const uint16_t l1 = vx_f32_to_bf16(v2[1] - vx_bf16_to_f32(h1));
+            if (is_q || is_k) {
+                uint16_t *dl = is_q ? a.qol + (row * a.nqk + hh) * HD : a.kol + (row * a.nqk + (hh - a.nqk)) * HD;
+                dl[lane] = l0;
+                dl[lane + 64] = l1;
+            }
+            const int sh = 16 * (j & 3);
+            if (j < 4) {
+                lt[0][0] |= (uint64_t)l0 << sh;
+                lt[1][0] |= (uint64_t)l1 << sh;
+            } else {
+                lt[0][1] |= (uint64_t)l0 << sh;
+                lt[1][1] |= (uint64_t)l1 << sh;
+            }
         }
+    }
+    if (tl) {   // tokens past nt stay zero
+#pragma unroll
+        for (int e = 0; e < 2; e++)
+            *(uint4 *)&tl[(size_t)(lane + 64 * e) * a.Tp + t0] =
+                make_uint4((uint32_t)lt[e][0], (uint32_t)(lt[e][0] >> 32), (uint32_t)lt[e][1], (uint32_t)(lt[e][1] >> 32));
     }
 }
 
@@ -1309,6 +1380,16 @@ static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 static bool dn_prefill_is_exact(const vx27_dn_prefill_desc *d) {
     return (d->flags & VX27_DN_EXACT) || d->S_ckpt || d->conv_ckpt;
 }
+// The glue's outputs: q, k, v hi rows; with the split form q and k lo rows
+// and the transposed k and v lo parts over the prompt padded to chunks.
+static size_t vx_dn_glue_bytes(int B, int T, int nqk, int nv, bool x3) {
+    const size_t rows = (size_t)B * T, Tp = (size_t)(T + CH - 1) / CH * CH;
+    const size_t qd = (size_t)nqk * HD, vd = (size_t)nv * HD;
+    size_t n = rows * (2 * qd + vd);                                // hi
+    if (x3) n += rows * 2 * qd + (size_t)B * (qd + vd) * Tp;        // lo rows, lo transposed
+    return n * sizeof(uint16_t);
+}
+
 size_t vx_dn_prefill_scratch(const vx27_dn_prefill_desc *d) {
     const int qd = d->nqk * HD, vd = d->nv * HD, C = 2 * qd + vd;
     const size_t rows = (size_t)d->B * d->T;
@@ -1320,7 +1401,7 @@ size_t vx_dn_prefill_scratch(const vx27_dn_prefill_desc *d) {
     const size_t n_rec = (size_t)d->B * d->nv * NC;
     const bool glue = (d->flags & (VX27_DN_CONV | VX27_DN_PRE_RMS | VX27_DN_PRE_L2)) != 0;
     return al256(n_rec * (x3 ? XREC : REC)) + al256(n_rec * sizeof(float)) +
-           (glue ? rows * C * sizeof(uint16_t) * (x3 ? 2 : 1) : 0);
+           (glue ? vx_dn_glue_bytes(d->B, d->T, d->nqk, d->nv, x3) : 0);
 }
 
 // The exact path: the decode kernels token by token (prefill layout).
@@ -1409,28 +1490,30 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
     const size_t glue_off = gc_off + al256(n_rec * sizeof(float));
     const size_t rows = (size_t)d->B * d->T;
     const uint16_t *q = d->q, *k = d->k, *v = d->v;
-    const uint16_t *ql = nullptr, *kl = nullptr, *vl = nullptr;
+    const uint16_t *ql = nullptr, *kl = nullptr, *klT = nullptr, *vlT = nullptr;
+    const int Tp = NC * CH;
     if (glue) {   // conv and pre-norms in fp32, then q, k, v as bf16 (hi, and lo for the split form)
         uint16_t *qo = (uint16_t *)((char *)scr + glue_off), *ko = qo + rows * qd, *vo = ko + rows * qd;
-        uint16_t *qol = x3 ? vo + rows * vd : nullptr;
-        uint16_t *kol = x3 ? qol + rows * qd : nullptr, *vol = x3 ? kol + rows * qd : nullptr;
+        uint16_t *qol = x3 ? vo + rows * vd : nullptr, *kol = x3 ? qol + rows * qd : nullptr;
+        uint16_t *kT = x3 ? kol + rows * qd : nullptr, *vT = x3 ? kT + (size_t)d->B * qd * Tp : nullptr;
         GlueInArgs ga{d->B, d->T, d->nqk, d->nv, C, d->flags, d->conv_w_dtype == VX27_BF16, d->x, d->conv_state,
-                      d->conv_w, d->q, d->k, d->v, d->norm_w, qo, ko, vo, qol, kol, vol};
+                      d->conv_w, d->q, d->k, d->v, d->norm_w, qo, ko, vo, qol, kol, kT, vT, Tp};
         const int nh = 2 * d->nqk + d->nv;
-        VX_LAUNCH(ctx, dnp_glue_in, dim3((unsigned)((d->T + GT - 1) / GT), (unsigned)((nh + 3) / 4), (unsigned)d->B),
-                  dim3(256), ga);
+        const int tblk = ((x3 ? Tp : d->T) + GT - 1) / GT;   // the split form also zeroes the padding
+        VX_LAUNCH(ctx, dnp_glue_in, dim3((unsigned)tblk, (unsigned)((nh + 3) / 4), (unsigned)d->B), dim3(256), ga);
         if (conv) {
             const size_t nthr = (size_t)d->B * C;
             VX_LAUNCH(ctx, dnp_conv_state, dim3((unsigned)((nthr + 255) / 256)), dim3(256), d->B, d->T, C, d->x,
                       d->conv_state);
         }
         q = qo; k = ko; v = vo;
-        ql = qol; kl = kol; vl = vol;
+        ql = qol; kl = kol; klT = kT; vlT = vT;
     }
     ScanArgs sa{d->T, d->nv, NC, (d->nv % 8) == 0, (const char *)scr, (const float *)((char *)scr + gc_off),
                 d->S, d->out};
     if (x3) {
-        Prep3Args pa{d->T, d->nqk, d->nv, NC, q, k, v, ql, kl, vl, d->a, d->b, d->A_log, d->dt_bias, (char *)scr};
+        Prep3Args pa{d->T, d->nqk, d->nv, NC, q, k, v, ql, kl, klT, vlT, Tp, d->a, d->b, d->A_log, d->dt_bias,
+                     (char *)scr};
         if (pa.ql)
             VX_LAUNCH_NAMED(ctx, "dnp_prep3", dnp_prep3<true>, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B),
                             dim3(256), pa);
