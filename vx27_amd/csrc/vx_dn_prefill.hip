@@ -1190,8 +1190,9 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
 // q and k lo as rows, k and v lo also transposed, [B][head][128 dims][Tp
 // tokens] with Tp the prompt padded to whole chunks (8 tokens of a dim are
 // one 16-byte store; the blocks past T write the padding's zeros).
-// grid (ceil(Tp/GT) with lo parts, else ceil(T/GT), ceil(heads/4), B),
-// block 256.
+// The four waves of a workgroup take four consecutive token blocks of one
+// head, so a dim's transposed lo run of 32 tokens is written by one CU.
+// grid (ceil(Tp/GT/4) with lo parts, else ceil(T/GT/4), heads, B), block 256.
 constexpr int GT = 8;
 struct GlueInArgs {
     int B, T, nqk, nv, C;
@@ -1209,9 +1210,8 @@ struct GlueInArgs {
 };
 __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
-    const int hh = blockIdx.y * 4 + wave, b = blockIdx.z, t0 = blockIdx.x * GT;
-    const int nh = 2 * a.nqk + a.nv;
-    if (hh >= nh) return;
+    const int hh = blockIdx.y, b = blockIdx.z, t0 = (blockIdx.x * 4 + wave) * GT;
+    if (t0 >= (a.qol ? a.Tp : a.T)) return;
     const bool is_q = hh < a.nqk, is_k = !is_q && hh < 2 * a.nqk;
     // transposed lo rows of this head's two dims (k and v heads)
     uint16_t *tl = nullptr;
@@ -1500,7 +1500,7 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
                       d->conv_w, d->q, d->k, d->v, d->norm_w, qo, ko, vo, qol, kol, kT, vT, Tp};
         const int nh = 2 * d->nqk + d->nv;
         const int tblk = ((x3 ? Tp : d->T) + GT - 1) / GT;   // the split form also zeroes the padding
-        VX_LAUNCH(ctx, dnp_glue_in, dim3((unsigned)tblk, (unsigned)((nh + 3) / 4), (unsigned)d->B), dim3(256), ga);
+        VX_LAUNCH(ctx, dnp_glue_in, dim3((unsigned)((tblk + 3) / 4), (unsigned)nh, (unsigned)d->B), dim3(256), ga);
         if (conv) {
             const size_t nthr = (size_t)d->B * C;
             VX_LAUNCH(ctx, dnp_conv_state, dim3((unsigned)((nthr + 255) / 256)), dim3(256), d->B, d->T, C, d->x,
