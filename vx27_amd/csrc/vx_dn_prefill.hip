@@ -1228,22 +1228,59 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
     const bool conv = (a.flags & VX27_DN_CONV) != 0;
     const float qs = 1.0f / sqrtf((float)HD);
     const int nt = min(GT, a.T - t0);
-    // x window of the two channels: tokens t0-3 .. t0+GT-1 (older ones from the state)
+    // Every input of the block is loaded first, unconditionally, from
+    // addresses clamped into the buffers, and the cases are selected after:
+    // a load under a condition would wait for its data inside its branch.
+    // With the conv: the x window of the two channels, tokens t0-3 ..
+    // t0+GT-1 (older ones from the state, none past the prompt), and the
+    // conv weights as raw words (two 8-byte words, the second one repeating
+    // the first for bf16); without it, the block's q, k or v values.
     float xw[2][GT + 3], w[2][4];
     float nw[2] = {1.0f, 1.0f};
+    uint2 wr[2][2];
+    float cst[2][3];
+    const uint16_t *src = is_q ? a.q + hh * HD : is_k ? a.k + (hh - a.nqk) * HD : a.v + (hh - 2 * a.nqk) * HD;
+    const int hstride = (is_q || is_k) ? a.nqk * HD : a.nv * HD;
+    if (conv) {   // (one branch around both channels' loads: they all stay in flight together)
 #pragma unroll
-    for (int e = 0; e < 2; e++) {
-        const size_t ch = (size_t)hh * HD + lane + 64 * e;
-        if (conv) {
-            load_conv_w(a.conv_w, a.w_bf16, ch, w[e]);
+        for (int e = 0; e < 2; e++) {
+            const size_t ch = (size_t)hh * HD + lane + 64 * e;
+            const uint2 *wb = (const uint2 *)a.conv_w;
+            const size_t w0 = a.w_bf16 ? ch : 2 * ch;
+            wr[e][0] = wb[w0];
+            wr[e][1] = wb[a.w_bf16 ? w0 : w0 + 1];
+#pragma unroll
+            for (int t = 0; t < 3; t++) cst[e][t] = a.conv_state[((size_t)b * a.C + ch) * 3 + t];
 #pragma unroll
             for (int j = 0; j < GT + 3; j++) {
-                const int s = t0 - 3 + j;
-                xw[e][j] = s < 0 ? a.conv_state[((size_t)b * a.C + ch) * 3 + (3 + s)]
-                         : s < a.T ? a.x[((size_t)b * a.T + s) * a.C + ch] : 0.0f;
+                const int sc = min(max(t0 - 3 + j, 0), a.T - 1);
+                xw[e][j] = a.x[((size_t)b * a.T + sc) * a.C + ch];
             }
         }
-        if (a.norm_w && (is_q || is_k)) nw[e] = a.norm_w[lane + 64 * e];
+    } else {
+#pragma unroll
+        for (int e = 0; e < 2; e++)
+#pragma unroll
+            for (int j = 0; j < GT; j++) {
+                const size_t row = (size_t)b * a.T + min(t0 + j, a.T - 1);
+                xw[e][j] = vx_bf16_to_f32(src[row * hstride + lane + 64 * e]);
+            }
+    }
+    if (a.norm_w && (is_q || is_k)) {
+        nw[0] = a.norm_w[lane];
+        nw[1] = a.norm_w[lane + 64];
+    }
+    if (conv) {
+#pragma unroll
+        for (int e = 0; e < 2; e++) {
+            const uint32_t r[4] = {wr[e][0].x, wr[e][0].y, wr[e][1].x, wr[e][1].y};
+            conv_w_decode(a.w_bf16, r, w[e]);
+#pragma unroll
+            for (int j = 0; j < GT + 3; j++) {
+                const int s = t0 - 3 + j;   // s < 0 only for j < 3 (t0 = 0): state slot j
+                xw[e][j] = s < 0 ? cst[e][j < 3 ? j : 0] : s < a.T ? xw[e][j] : 0.0f;
+            }
+        }
     }
     uint64_t lt[2][2] = {{0, 0}, {0, 0}};   // the block's transposed lo values, four tokens a word
     for (int j = 0; j < nt; j++) {
@@ -1255,10 +1292,7 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
                 float c[3] = {xw[e][j], xw[e][j + 1], xw[e][j + 2]};
                 v2[e] = conv_step(c, w[e], xw[e][j + 3]);
             } else {
-                const uint16_t *src = is_q ? a.q + (row * a.nqk + hh) * HD
-                                    : is_k ? a.k + (row * a.nqk + (hh - a.nqk)) * HD
-                                           : a.v + (row * a.nv + (hh - 2 * a.nqk)) * HD;
-                v2[e] = vx_bf16_to_f32(src[lane + 64 * e]);
+                v2[e] = xw[e][j];
             }
         }
         if ((is_q || is_k) && (a.flags & (VX27_DN_PRE_RMS | VX27_DN_PRE_L2))) {
@@ -1466,6 +1500,7 @@ static int dn_prefill_check(const vx27_dn_prefill_desc *d) {
         VX_REQUIRE(d->x && d->conv_state && d->conv_w, "vx27_hip_dn_prefill: VX27_DN_CONV needs x, conv_state, conv_w");
         VX_REQUIRE(d->conv_w_dtype == VX27_F32 || d->conv_w_dtype == VX27_BF16,
                    "vx27_hip_dn_prefill: conv_w_dtype must be VX27_F32 or VX27_BF16");
+        VX_REQUIRE(((uintptr_t)d->conv_w & 15) == 0, "vx27_hip_dn_prefill: conv_w must be 16-byte aligned");
     } else {
         VX_REQUIRE(d->q && d->k && d->v, "vx27_hip_dn_prefill: q, k, v are required without VX27_DN_CONV");
         VX_REQUIRE(!d->conv_ckpt, "vx27_hip_dn_prefill: conv_ckpt needs VX27_DN_CONV");
