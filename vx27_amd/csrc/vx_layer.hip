@@ -4,10 +4,11 @@
 // DeltaNet layer (vx27_qfwd.c:102-153), one decode token of B sequences:
 //   gemv_dn_in               [qkv | z | a | b] projection with its epilogue
 //                            (DnInEpi): causal conv/SiLU on qkv (state in
-//                            place), z, decay from a, beta from b
-//   dn_step_kernel           q/k normalisation chain, exact step, gated
-//                            output norm, output written as the packed
-//                            operand of W_out
+//                            place), z, a and b copied out
+//   dn_step_kernel           gates (decay from a, beta from b), q/k
+//                            normalisation chain, exact step, gated output
+//                            norm, output written as the packed operand of
+//                            W_out
 //   gemv_wk_store(W_out)     -> out
 // Gated GQA layer (vx27_qfwd.c:162-213):
 //   gemv_wk_store(W_qkv)     -> [q|gate interleaved | k | v]
@@ -32,9 +33,8 @@ struct DnInArgs {
     float *conv_state;
     const void *conv_w;
     int conv_bf16;
-    const float *A_log, *dt_bias;
     float *act, *z;
-    double2 *gates;
+    float *ga, *gb;   // the a and b rows, [B][nv] each (the step kernel maps them to the gates)
     int b0;   // first vector of this pass (the pass's B vectors are b0 .. b0+B-1)
 };
 
@@ -43,7 +43,9 @@ struct DnInArgs {
 //   q|k|v rows: causal conv + SiLU (conv state in place) -> act; the q/k
 //               normalisation chain runs in the recurrence kernel, which
 //               has whole heads
-//   z rows:     copied out; a rows: decay = exp(g_log); b rows: beta
+//   z, a, b rows: copied out (the step kernel maps a and b to decay and
+//               beta, after its state loads are issued: no WG of this
+//               kernel waits on transcendental code)
 // The conv weights (raw bits, converted after the loop so that nothing
 // waits on them) and the conv state of a q|k|v row (first DN_PREB vectors
 // of the pass) are loaded before the projection's K loop.
@@ -118,17 +120,16 @@ struct DnInEpi {
 #pragma unroll
             for (int b = 0; b < DN_MAXB; b++)
                 if (b < a.B) a.z[(size_t)(a.b0 + b) * a.vd + (n - a.C)] = v[b];
-        } else if (n < a.C + a.vd + a.nv) {  // a -> decay = exp(g_log), vx27_deltanet.c:68,82
+        } else if (n < a.C + a.vd + a.nv) {  // a
             const int vh = n - a.C - a.vd;
-            const double eA = exp((double)a.A_log[vh]), dtb = (double)a.dt_bias[vh];
 #pragma unroll
             for (int b = 0; b < DN_MAXB; b++)
-                if (b < a.B) a.gates[(size_t)(a.b0 + b) * a.nv + vh].y = exp(-eA * softplus_d((double)v[b] + dtb));
-        } else {                             // b -> beta = sigmoid(b), vx27_deltanet.c:67
+                if (b < a.B) a.ga[(size_t)(a.b0 + b) * a.nv + vh] = v[b];
+        } else {                             // b
             const int vh = n - a.C - a.vd - a.nv;
 #pragma unroll
             for (int b = 0; b < DN_MAXB; b++)
-                if (b < a.B) a.gates[(size_t)(a.b0 + b) * a.nv + vh].x = 1.0 / (1.0 + exp(-(double)v[b]));
+                if (b < a.B) a.gb[(size_t)(a.b0 + b) * a.nv + vh] = v[b];
         }
     }
 };
@@ -208,16 +209,19 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     const int Nin = C + vd + 2 * nv;
     const size_t pk_x = d->x_packed ? 0 : align256(vx_pack_bytes(H, B));
     const size_t act_b = align256((size_t)B * C * 4), z_b = align256((size_t)B * vd * 4);
-    const size_t g_b = align256((size_t)B * nv * sizeof(double2));
+    const size_t g_b = align256((size_t)B * nv * sizeof(float));
+    const size_t gm_b = align256((size_t)B * nv * sizeof(double2));
     const size_t pk_o = align256(vx_pack_bytes(vd, B));
     void *scr;
-    if (vx_ctx_scratch(ctx, pk_x + act_b + z_b + g_b + pk_o, &scr)) return -1;
+    if (vx_ctx_scratch(ctx, pk_x + act_b + z_b + 2 * g_b + gm_b + pk_o, &scr)) return -1;
     char *p = (char *)scr;
     uint16_t *xp = d->x_packed ? (uint16_t *)d->x_packed : (uint16_t *)p;
     p += pk_x;
     float *act = (float *)p; p += act_b;
     float *z = (float *)p; p += z_b;
-    double2 *gates = (double2 *)p; p += g_b;
+    float *ga = (float *)p; p += g_b;
+    float *gb = (float *)p; p += g_b;
+    double2 *gates = (double2 *)p; p += gm_b;
     uint16_t *op = (uint16_t *)p;
 
     if (!d->x_packed && vx_pack(ctx, d->x, (size_t)H, B, H, xp)) return -1;
@@ -225,8 +229,8 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     for (int g0 = 0; g0 < Gt; g0 += 3) {   // passes of up to three groups (15 vectors) over W_in
         const int G = g0 + 3 <= Gt ? 3 : Gt - g0, b0 = g0 * VX_PACK_GV;
         const int Bp = B - b0 < G * VX_PACK_GV ? B - b0 : G * VX_PACK_GV;
-        const DnInArgs ea = {Bp, C, vd, nv, d->conv_state, d->conv_w, d->conv_w_dtype == VX27_BF16,
-                             d->A_log, d->dt_bias, act, z, gates, b0};
+        const DnInArgs ea = {Bp, C, vd, nv, d->conv_state, d->conv_w, d->conv_w_dtype == VX27_BF16, act, z, ga, gb,
+                             b0};
         const WkPlan wp = vx_gemv_wk_plan(Nin, H, ctx->n_cu, G);
         VX_WK_DISPATCH(ctx, gemv_dn_in, wp, d->w_in, Nin, H, xp, Gt, g0, Bp, (DnInEpi{ea}));
     }
@@ -237,8 +241,13 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     ra.S = d->S;
     ra.q = act; ra.k = act + qd; ra.v = act + 2 * qd;
     ra.q_tok = ra.k_tok = ra.v_tok = (size_t)C;
-    ra.gates = gates; ra.norm_w = d->norm_w; ra.z = z; ra.z_tok = (size_t)vd;
+    ra.ga = ga; ra.gb = gb; ra.A_log = d->A_log; ra.dt_bias = d->dt_bias;   // mapped by the step kernel
+    ra.norm_w = d->norm_w; ra.z = z; ra.z_tok = (size_t)vd;
     ra.out = nullptr; ra.out_tok = (size_t)vd; ra.out_packed = op;
+    if (!vx_dn_single_step(ra)) {   // (the multi-step kernel takes mapped gates)
+        if (vx_dn_gates(ctx, (size_t)B * nv, nv, ga, gb, d->A_log, d->dt_bias, gates)) return -1;
+        ra.gates = gates;
+    }
     if (vx_dn_recurrence(ctx, ra)) return -1;
 
     return vx_gemv_store(ctx, d->w_out, H, vd, op, B, d->out, (size_t)H);
