@@ -28,9 +28,14 @@ int vx_rope_fill(vx_rope_tab &t, int rope_dim, float theta);
 // freq_i in float, then the device's float cosf/sinf (vx27_rope.c:11-14).
 // Every kernel that rotates (decode prep, prefill k/v and query prologues
 // through the prefill's table, vx27_hip_rope_table) evaluates it here.
-__device__ __forceinline__ float2 vx_rope_cs_f(float freq, int pos, float yarn) {
-    const float ang = ((float)pos / yarn) * freq;
+__device__ __forceinline__ float vx_rope_angle(float freq, int pos, float yarn) {
+    return ((float)pos / yarn) * freq;
+}
+__device__ __forceinline__ float2 vx_rope_cs_angle(float ang) {
     return make_float2(cosf(ang), sinf(ang));
+}
+__device__ __forceinline__ float2 vx_rope_cs_f(float freq, int pos, float yarn) {
+    return vx_rope_cs_angle(vx_rope_angle(freq, pos, yarn));
 }
 __device__ __forceinline__ float2 vx_rope_cs(const vx_rope_tab &t, int pos, float yarn, int i) {
     return vx_rope_cs_f(t.freq[i], pos, yarn);

@@ -92,36 +92,59 @@ __global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
     __shared__ float2 csn[VB][VX_ROPE_MAXH / 2];                          // rope_dim <= 128 here
     __shared__ __attribute__((aligned(16))) uint16_t vt[VB][HDG];         // the block's v rows
 
-    uint4 vr[KV_VLD];
+    // Every load is unconditional, from a position clamped into [lo, hi):
+    // a load under the position test would be a branch with its own wait.
+    // The frequency of this thread's (position, frequency) pairs goes first,
+    // so that the angles wait for it alone (half is 32 or 64, so every pair
+    // of thread tid has frequency tid % half).
+    constexpr int NCS = VB * (VX_ROPE_MAXH / 2) / 256;
+    const int hm = max(half, 1);
+    const float fr = a.rope.freq[tid % hm];
+    __builtin_amdgcn_sched_barrier(0);
+    u32x4_t vr[KV_VLD];
 #pragma unroll
     for (int r = 0; r < KV_VLD; r++) {
-        const int e = tid + 256 * r, j = e / (HDG / 8), c = e % (HDG / 8), pos = p0 + j;
-        if (pos >= lo && pos < hi)
-            vr[r] = *(const uint4 *)(a.v + ((size_t)b * a.T + (pos - a.pos0)) * a.kv_ts + (size_t)hk * HDG + c * 8);
+        const int e = tid + 256 * r, j = e / (HDG / 8), c = e % (HDG / 8), pos = min(max(p0 + j, lo), hi - 1);
+        vr[r] = *(const u32x4_t *)(a.v + ((size_t)b * a.T + (pos - a.pos0)) * a.kv_ts + (size_t)hk * HDG + c * 8);
     }
     uint2 kr[VB / 4];
 #pragma unroll
     for (int jj = 0; jj < VB / 4; jj++) {
-        const int pos = p0 + wave + 4 * jj;
-        if (pos >= lo && pos < hi)
-            kr[jj] = *(const uint2 *)(a.k + ((size_t)b * a.T + (pos - a.pos0)) * a.kv_ts + (size_t)hk * HDG + 4 * lane);
+        const int pos = min(max(p0 + wave + 4 * jj, lo), hi - 1);
+        kr[jj] = *(const uint2 *)(a.k + ((size_t)b * a.T + (pos - a.pos0)) * a.kv_ts + (size_t)hk * HDG + 4 * lane);
     }
     float w[4];
 #pragma unroll
     for (int e = 0; e < 4; e++) w[e] = a.k_norm_w[4 * lane + e];
+    // the angles of this thread's pairs, for clamped positions: computed
+    // unconditionally, so the frequency load is not moved under the tests
+    // below (with a wait of its own)
+    __builtin_amdgcn_sched_barrier(0);
+    float ang[NCS];
+#pragma unroll
+    for (int it = 0; it < NCS; it++) ang[it] = vx_rope_angle(fr, min(max(p0 + (tid + 256 * it) / hm, lo), hi - 1), a.yarn);
 
-    // cos/sin of every (position, frequency) of the block
-    for (int e = tid; e < VB * half; e += 256) {
-        const int j = e / half, i = e % half, pos = p0 + j;
-        if (pos < lo || pos >= hi) continue;
-        const float2 v = vx_rope_cs(a.rope, pos, a.yarn, i);
-        csn[j][i] = v;
-        if (b == 0 && hk == 0) a.cs_tab[(size_t)(pos - a.pos0) * half + i] = v;
-    }
+    // the v rows into LDS (rows outside [lo, hi) hold a clamped row, never
+    // stored), before the cos/sin code, whose temporaries would push them
+    // out of registers
 #pragma unroll
     for (int r = 0; r < KV_VLD; r++) {
-        const int e = tid + 256 * r, j = e / (HDG / 8), c = e % (HDG / 8), pos = p0 + j;
-        if (pos >= lo && pos < hi) *(uint4 *)&vt[j][c * 8] = vr[r];
+        const int e = tid + 256 * r, j = e / (HDG / 8), c = e % (HDG / 8);
+        *(u32x4_t *)&vt[j][c * 8] = vr[r];
+    }
+
+    // cos/sin of every (position, frequency) of the block
+#pragma unroll
+    for (int it = 0; it < NCS; it++) {
+        const int e = tid + 256 * it;
+        if (e < VB * half) {
+            const int j = e / half, i = e % half, pos = p0 + j;
+            if (pos >= lo && pos < hi) {
+                const float2 v = vx_rope_cs_angle(ang[it]);
+                csn[j][i] = v;
+                if (b == 0 && hk == 0) a.cs_tab[(size_t)(pos - a.pos0) * half + i] = v;
+            }
+        }
     }
 
     // k: rmsn (sum of squares in double) of the wave's 8 tokens
