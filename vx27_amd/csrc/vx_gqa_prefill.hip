@@ -278,19 +278,9 @@ __device__ __forceinline__ int kswz(int r) { return (r & 3) | ((r >> 1) & 12); }
 // The squares of the bf16 inputs are exact in fp32; the sum of squares is
 // fp32 per lane and double across the row's 4 lanes.  Every global load
 // (rows, norm weights, cos/sin) is issued before any of them is used: one
-// round trip.  The raw rows come in as u (q_rows loads them from global
-// memory; the pipelined kernel may have staged them in LDS instead).
+// round trip.  The raw rows come in as u (the attention kernel stages them
+// in LDS).
 constexpr int HQ_MAX = VX_ROPE_MAXH / 64;   // k-steps holding the first half of the pairs, at most
-template <int NB>
-__device__ __forceinline__ void q_rows(const AttnArgs &a, int b, int h, const int (&t)[NB], int g,
-                                       uint4 (&u)[NB][8]) {
-#pragma unroll
-    for (int blk = 0; blk < NB; blk++) {
-        const uint16_t *src = a.q + ((size_t)b * a.T + t[blk]) * a.q_ts + (size_t)h * a.q_hs + 8 * g;
-#pragma unroll
-        for (int ks = 0; ks < 8; ks++) u[blk][ks] = *(const uint4 *)(src + 32 * ks);
-    }
-}
 template <int NB>
 __device__ __forceinline__ void q_prep_rows(const AttnArgs &a, const int (&t)[NB], int g, const uint4 (&u)[NB][8],
                                             bf16x8_t (&qv)[NB][8]) {
@@ -370,13 +360,6 @@ __device__ __forceinline__ void q_prep_rows(const AttnArgs &a, const int (&t)[NB
                                                pack2(x[ks][4], x[ks][5]), pack2(x[ks][6], x[ks][7])));
     }
 }
-template <int NB>
-__device__ __forceinline__ void q_prep(const AttnArgs &a, int b, int h, const int (&t)[NB], int g,
-                                       bf16x8_t (&qv)[NB][8]) {
-    uint4 u[NB][8];
-    q_rows<NB>(a, b, h, t, g, u);
-    q_prep_rows<NB>(a, t, g, u, qv);
-}
 
 // Software-pipelined attention: 4 waves of 32 queries (two 16-query blocks,
 // so every K and V operand read from LDS feeds two MFMAs).  The stretch
@@ -395,26 +378,18 @@ __device__ __forceinline__ void q_prep(const AttnArgs &a, int b, int h, const in
 // finite, and the wave redoes its queries with the online (rescaling)
 // softmax, reading K and V straight from the cache.  grid (ceil(T/128) *
 // n_q, B), block 256.
-#ifndef GQP_PP_NW
-#define GQP_PP_NW 4         // waves per pipelined-attention workgroup: 4 x 32 queries or 8 x 16
-#endif
-#ifndef GQP_PP_RB
-#define GQP_PP_RB (8 / GQP_PP_NW)   // 16-query blocks per wave
-#endif
-constexpr int PP_NW = GQP_PP_NW, PP_RB = GQP_PP_RB, PP_QT = PP_NW * PP_RB * 16, PP_PER = 32 / PP_NW;
-#ifndef GQP_QSTAGE
-#define GQP_QSTAGE 1        // the epilogue stages the next item's query rows in LDS
-#endif
-// (a wave's 16 RB query rows fill its two V-buffer slots exactly, and the
-// epilogue's transposition, 16 KiB per wave, stays in the K buffers: 4 x 32
-// queries; with 8 waves it covers the V buffers too)
-constexpr bool QSTAGE = GQP_QSTAGE && PP_RB * 8 == 2 * PP_PER && PP_NW * 16 * HDG * 4 <= 2 * (int)KBUF;
+// 4 waves x 2 blocks of 16 queries (measured: 8 waves x 16 queries 3% slower,
+// 4 x 48 spills and runs 25% slower)
+constexpr int PP_NW = 4, PP_RB = 2, PP_QT = PP_NW * PP_RB * 16, PP_PER = 32 / PP_NW;
+// The epilogue stages the next item's query rows in LDS (about 4% off the
+// kernel against loading them in the prologue): a wave's 16 RB query rows
+// fill its two V-buffer slots exactly, and the epilogue's transposition,
+// 16 KiB per wave, stays in the K buffers.
+static_assert(PP_RB * 8 == 2 * PP_PER && PP_NW * 16 * HDG * 4 <= 2 * (int)KBUF, "query staging layout");
 #ifndef GQP_OUT_NT
 #define GQP_OUT_NT 1        // streaming (nontemporal) stores of the attention output
 #endif
 constexpr bool OUT_NT = GQP_OUT_NT;
-static_assert((PP_NW == 4 && (PP_RB == 2 || PP_RB == 3)) || (PP_NW == 8 && PP_RB == 1),
-              "4 waves of 32 or 48 queries, or 8 of 16");
 
 __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
     constexpr int RB = PP_RB, QT = PP_QT, PER = PP_PER;
@@ -469,7 +444,7 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
             vx_dma16(qb, off, vb + ((2 * j) / (RB * 8)) * KBUF + ((2 * j) % (RB * 8)) * 512);
         }
     };
-    if (QSTAGE) {
+    {
         int qt0, h0, b0;
         if (item_of(0, qt0, h0, b0)) stage_q(qt0, h0, b0);
     }
@@ -521,35 +496,25 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) tq[rb] = min(r0 + 16 * rb + n, a.T - 1);
         uint4 u[RB][8];
-        if (QSTAGE) {
 #pragma unroll
-            for (int j = 0; j < PER; j++) dma_k(0, 0, j);
+        for (int j = 0; j < PER; j++) dma_k(0, 0, j);
 #pragma unroll
-            for (int j = 0; j < PER; j++) dma_k(min(1, n_tiles - 1), 1, j);
-            // the staging loads and everything issued before K(0) have landed
-            __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PER) : "memory");
-            int ln = lane;   // (opaque, as in stage_q)
-            __asm__ volatile("" : "+v"(ln));
-            const int gg = ln >> 4, nn = ln & 15;
+        for (int j = 0; j < PER; j++) dma_k(min(1, n_tiles - 1), 1, j);
+        // the staging loads and everything issued before K(0) have landed
+        __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(2 * PER) : "memory");
+        int ln = lane;   // (opaque, as in stage_q)
+        __asm__ volatile("" : "+v"(ln));
+        const int gg = ln >> 4, nn = ln & 15;
 #pragma unroll
-            for (int rb = 0; rb < RB; rb++) {
-                const int q = 16 * rb + nn;
-                const char *rp = smem + (2 + q / (RB * 8)) * KBUF + wave * PER * 1024 + (q % (RB * 8)) * 512;
+        for (int rb = 0; rb < RB; rb++) {
+            const int q = 16 * rb + nn;
+            const char *rp = smem + (2 + q / (RB * 8)) * KBUF + wave * PER * 1024 + (q % (RB * 8)) * 512;
 #pragma unroll
-                for (int ks = 0; ks < 8; ks++) u[rb][ks] = *(const uint4 *)(rp + (((4 * ks + gg) ^ (q & 15)) << 4));
-            }
-            __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read out before V(0) lands there
-#pragma unroll
-            for (int j = 0; j < PER; j++) dma_v(0, 0, j);
-        } else {
-#pragma unroll
-            for (int j = 0; j < PER; j++) dma_k(0, 0, j);
-#pragma unroll
-            for (int j = 0; j < PER; j++) dma_v(0, 0, j);
-#pragma unroll
-            for (int j = 0; j < PER; j++) dma_k(min(1, n_tiles - 1), 1, j);
-            q_rows<RB>(a, b, h, tq, g, u);
+            for (int ks = 0; ks < 8; ks++) u[rb][ks] = *(const uint4 *)(rp + (((4 * ks + gg) ^ (q & 15)) << 4));
         }
+        __asm__ volatile("s_waitcnt lgkmcnt(0)" ::: "memory");   // read out before V(0) lands there
+#pragma unroll
+        for (int j = 0; j < PER; j++) dma_v(0, 0, j);
         q_prep_rows<RB>(a, tq, g, u, qv);
     }
 
@@ -874,7 +839,7 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
     vx_lds_barrier();   // every wave is done with the tile buffers
     // the next item's query rows go into this wave's V-buffer slots while
     // this epilogue runs (the transposition below uses only the K buffers)
-    if (QSTAGE && item + 1 < n_items) {
+    if (item + 1 < n_items) {
         int nqt, nh, nb;
         if (item_of(item + 1, nqt, nh, nb)) stage_q(nqt, nh, nb);
     }
