@@ -12,7 +12,11 @@ carries:
                 library's stream during one profiled step, against 8 TB/s;
                 `traffic` is the HBM bytes per launch that rocprofv3's
                 FETCH_SIZE and WRITE_SIZE counters read for that kernel at the
-                default workload (scaled by a copy-kernel calibration)
+                default workload (scaled by a copy-kernel calibration);
+                `measured_read_GBs` / `measured_copy_GBs` are what a plain
+                streaming read and a plain copy kernel reach over 4 GiB on
+                the same GPU (vx27_hip_bw_probe), and `frac_of_measured_read`
+                is the kernel's rate against the read
   cpu_baseline  the oracle (CPU restatement of the reference path) timed on
                 this host on a bounded sample of the same workload
   extra         the other decode configurations, measured the same way
@@ -696,6 +700,9 @@ def main():
         from oracle import oracle as O
         extra["host"] = dict(O.host_info(), cpu_baseline_threads=O.default_threads())
     ach = kbytes / (kus / 1e6)
+    rbw, cbw = C.c_double(), C.c_double()
+    L.check(L.lib().vx27_hip_bw_probe(ctx.h, 4 << 30, 5, C.byref(rbw), C.byref(cbw)), "bw_probe")
+    log(f"  bandwidth probe (4 GiB): read {rbw.value:.0f} GB/s, copy {cbw.value:.0f} GB/s")
     line = {
         "metric": METRIC,
         "value": round(value, 4),
@@ -708,7 +715,9 @@ def main():
         "roofline": {"bound": "hbm", "achieved": round(ach / 1e9, 1), "peak": HBM_PEAK / 1e9,
                      "unit": "GB/s", "frac": round(ach / HBM_PEAK, 4), "traffic": traffic,
                      "kernel": res["kernel"], "kernel_us": round(kus, 2),
-                     "alg_bytes_per_launch": kbytes},
+                     "alg_bytes_per_launch": kbytes,
+                     "measured_read_GBs": round(rbw.value, 1), "measured_copy_GBs": round(cbw.value, 1),
+                     "frac_of_measured_read": round(ach / (rbw.value * 1e9), 4) if rbw.value > 0 else None},
         "cpu_baseline": res.get("cpu"),
         "extra": extra,
     }

@@ -88,6 +88,15 @@ int vx27_hip_h2d(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
 int vx27_hip_d2h(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
 int vx27_hip_d2d(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
 int vx27_hip_memset(vx27_hip_ctx *ctx, void *dst, int byte, size_t bytes);
+/* HBM bandwidth probe, a measurement utility with no counterpart in the
+ * reference: allocates `bytes` of device memory (at least 1 MiB; use far
+ * more than the 256 MiB Infinity Cache), then `iters` times (after one
+ * warm-up) streams it with a plain read kernel and copies its first half
+ * into its second with a plain copy kernel, timed with events on the
+ * context stream, and frees it.  Returns the best rates in GB/s, counting
+ * `bytes` moved per kernel (the copy: bytes/2 read + bytes/2 written).  Not
+ * allowed inside a graph capture. */
+int vx27_hip_bw_probe(vx27_hip_ctx *ctx, size_t bytes, int iters, double *read_GBs, double *copy_GBs);
 
 /* dtype codes */
 #define VX27_F32 0

@@ -109,6 +109,7 @@ _SIGS = {
     "vx27_hip_d2h": (C.c_int, [VP, VP, VP, C.c_size_t]),
     "vx27_hip_d2d": (C.c_int, [VP, VP, VP, C.c_size_t]),
     "vx27_hip_memset": (C.c_int, [VP, VP, C.c_int, C.c_size_t]),
+    "vx27_hip_bw_probe": (C.c_int, [VP, C.c_size_t, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "vx27_hip_dn_decode": (C.c_int, [VP, C.POINTER(DnDesc)]),
     "vx27_hip_dn_prefill": (C.c_int, [VP, C.POINTER(DnPrefillDesc)]),
     "vx27_hip_dn_commit": (C.c_int, [VP] + [C.c_int] * 5 + [VP] * 5),
