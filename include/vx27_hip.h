@@ -189,7 +189,7 @@ typedef struct {
     const void *conv_w;
     int conv_w_dtype;
     const float *norm_w;         /* [hd] (PRE_RMS uses 1+w, OUT_GATE uses w) */
-    const float *z;              /* [B][T][nv][hd] (OUT_GATE) */
+    const float *z;              /* [B][T][nv][hd] (OUT_GATE; then z, norm_w and out 16-byte aligned) */
     /* optional checkpoints (either selects the exact algorithm):
      * S_ckpt [B][T][nv][hd][hd] the state after each token,
      * conv_ckpt [B][T][C][3] the conv state after each token (VX27_DN_CONV) */
@@ -392,9 +392,9 @@ typedef struct {
     unsigned flags;
     const float *x;
     const uint16_t *w_in, *w_out;   /* tiled */
-    const void *conv_w;
+    const void *conv_w;             /* 16-byte aligned */
     int conv_w_dtype;
-    const float *A_log, *dt_bias, *norm_w;
+    const float *A_log, *dt_bias, *norm_w;  /* norm_w 16-byte aligned */
     float *S, *conv_state;
     float *out;
     float *S_ckpt, *conv_ckpt;      /* optional: [B][T][nv][hd][hd], [B][T][C][3] */

@@ -1361,20 +1361,42 @@ __global__ __launch_bounds__(256) void dnp_conv_state(int B, int T, int C, const
     sp[0] = n[0]; sp[1] = n[1]; sp[2] = n[2];
 }
 
-// Gated output norm in place (vx27_qfwd.c:145-151): one wave per (token,
-// value head) row: out = rmsn_std(o) * norm_w * silu(z), sum in double.
+// dnp_out_gate: the gated RMS norm rmsn_std(o) * norm_w * silu(z) of every
+// (token, head) row of 128 (vx27_qfwd.c:145-151), in place.  One wave per 8
+// rows, a half-wave per row (lane: 4 consecutive floats), every load of the
+// 8 rows (o and z) issued before any is used; the sum of squares in double
+// over the half-wave.  out, z and norm_w 16-byte aligned.
+// grid ceil(rows / 32), block 256.
 __global__ __launch_bounds__(256) void dnp_out_gate(int rows, const float *z, const float *norm_w, float *out) {
-    const int r = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
-    if (r >= rows) return;
-    float *o = out + (size_t)r * HD;
-    const float *zr = z + (size_t)r * HD;
-    float f0 = o[lane], f1 = o[lane + 64];
-    const double so = vx_wave_sum_f64_dpp((double)f0 * (double)f0 + (double)f1 * (double)f1);
-    const float is = 1.0f / sqrtf((float)(so / HD) + 1e-6f);
-    f0 = ((f0 * is) * norm_w[lane]) * silu_f(zr[lane]);
-    f1 = ((f1 * is) * norm_w[lane + 64]) * silu_f(zr[lane + 64]);
-    o[lane] = f0;
-    o[lane + 64] = f1;
+    const int lane = threadIdx.x & 63, hl = lane & 31, hr = lane >> 5;
+    const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 8;
+    if (r0 >= rows) return;   // (wave-uniform)
+    float4 o[4], zz[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) {   // rows past the end re-read the last row
+        const size_t r = (size_t)min(r0 + 2 * i + hr, rows - 1);
+        o[i] = *(const float4 *)(out + r * HD + 4 * hl);
+        zz[i] = *(const float4 *)(z + r * HD + 4 * hl);
+    }
+    const float4 w = *(const float4 *)(norm_w + 4 * hl);
+    __builtin_amdgcn_sched_barrier(0);   // every load issued before the first wait
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+        double ss = (((double)o[i].x * (double)o[i].x + (double)o[i].y * (double)o[i].y) +
+                     (double)o[i].z * (double)o[i].z) + (double)o[i].w * (double)o[i].w;
+#pragma unroll
+        for (int off = 1; off < 32; off <<= 1) ss += __shfl_xor(ss, off, 64);
+        const float is = 1.0f / sqrtf((float)(ss / HD) + 1e-6f);
+        float4 y;
+        y.x = ((o[i].x * is) * w.x) * silu_f(zz[i].x);
+        y.y = ((o[i].y * is) * w.y) * silu_f(zz[i].y);
+        y.z = ((o[i].z * is) * w.z) * silu_f(zz[i].z);
+        y.w = ((o[i].w * is) * w.w) * silu_f(zz[i].w);
+        // (unconditional: rows past the end store the last row's own result
+        // again; a store under the row test would take the loads into its
+        // branch, with a wait for all of them)
+        *(float4 *)(out + (size_t)min(r0 + 2 * i + hr, rows - 1) * HD + 4 * hl) = y;
+    }
 }
 
 // Widen bf16 q|k|v rows into one fp32 row per token (the exact path's input
@@ -1507,7 +1529,11 @@ static int dn_prefill_check(const vx27_dn_prefill_desc *d) {
     }
     if (d->flags & (VX27_DN_PRE_RMS | VX27_DN_OUT_GATE))
         VX_REQUIRE(d->norm_w != nullptr, "vx27_hip_dn_prefill: norm_w required by PRE_RMS/OUT_GATE");
-    if (d->flags & VX27_DN_OUT_GATE) VX_REQUIRE(d->z != nullptr, "vx27_hip_dn_prefill: z required by OUT_GATE");
+    if (d->flags & VX27_DN_OUT_GATE) {
+        VX_REQUIRE(d->z != nullptr, "vx27_hip_dn_prefill: z required by OUT_GATE");
+        VX_REQUIRE((((uintptr_t)d->z | (uintptr_t)d->norm_w | (uintptr_t)d->out) & 15) == 0,
+                   "vx27_hip_dn_prefill: OUT_GATE needs z, norm_w and out 16-byte aligned");
+    }
     return 0;
 }
 
@@ -1572,7 +1598,7 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
     }
     if (d->flags & VX27_DN_OUT_GATE) {
         const int nrow = (int)(rows * d->nv);
-        VX_LAUNCH(ctx, dnp_out_gate, dim3((unsigned)((nrow + 3) / 4)), dim3(256), nrow, d->z, d->norm_w, d->out);
+        VX_LAUNCH(ctx, dnp_out_gate, dim3((unsigned)((nrow + 31) / 32)), dim3(256), nrow, d->z, d->norm_w, d->out);
     }
     return 0;
 }
