@@ -418,7 +418,7 @@ def bench_gqa(ctx, B, Lctx=8192, iters=20, cpu=False):
     kern_s = sum(ms for _, ms in kern.values()) / iters / 1e3
     res = {"workload": f"gqa_decode B={B} L={Lctx}", "us_per_step": wall * 1e6,
            "us_per_token": wall / B * 1e6,
-           "kernels_us": {k: v[1] / v[0] * 1e3 for k, v in kern.items()},
+           "kernels_us": {k: v[1] / v[0] * 1e3 for k, v in kern.items() if v[0]},
            "kernel": "gqa_split", "kernel_us": split_s * 1e6,
            "alg_bytes_per_step": alg, "kernel_alg_bytes": kv, "achieved_GBs": kv / split_s / 1e9,
            "hbm_frac_kernel": kv / split_s / HBM_PEAK, "hbm_frac_kernels": alg / kern_s / HBM_PEAK,

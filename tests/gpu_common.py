@@ -44,7 +44,7 @@ def bitexact_frac(a, b):
     return float(np.mean(np.asarray(a) == np.asarray(b)))
 
 
-def oracle_gqa_decode(d, Lcap, threads=None, no_gate=False):
+def oracle_gqa_decode(d, Lcap, threads=None, no_gate=False, rope_dim=64):
     """Oracle for one gated-GQA decode step of every sequence of workload d
     (gqa_decode): bf16 cache [B][Lcap][n_kv][hd] holding the prefix, append at
     pos, attend 0..pos (double dot), gate.  Returns (out [B][n_q][hd],
@@ -65,8 +65,8 @@ def oracle_gqa_decode(d, Lcap, threads=None, no_gate=False):
         nk = d["K"].shape[1]
         kc[:nk] = d["K"][b]
         vc[:nk] = d["V"][b]
-        cs, sn = O.rope_cos_sin(pos)
-        cfg = O.GqaCfg(n_q, n_kv, hd, 64, 1, qn.ctypes.data, kn.ctypes.data, kc.ctypes.data,
+        cs, sn = O.rope_cos_sin(pos, max(rope_dim, 2))
+        cfg = O.GqaCfg(n_q, n_kv, hd, rope_dim, 1, qn.ctypes.data, kn.ctypes.data, kc.ctypes.data,
                        vc.ctypes.data, n_kv * hd, hd, n_kv * hd, hd, int(no_gate))
         out = np.empty((n_q, hd), np.float32)
         k1 = np.ascontiguousarray(d["k_new"][b], np.float32)

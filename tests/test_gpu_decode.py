@@ -180,6 +180,31 @@ def test_gqa_edges_and_splits(ctx):
     assert np.abs(outs[-1][0] - want).max() < 1e-5
 
 
+@pytest.mark.parametrize("rope_dim", [0, 32, 128, 256])
+def test_gqa_decode_rope_dims(ctx, rope_dim):
+    """Other rotary widths (0: no rotation; 256: every dim rotated), ragged
+    positions; the appended k, v rows are checked too."""
+    from vx27_amd import mixers as M, workloads as W
+    d = W.gqa_decode(B=3, L=700, config=25)
+    d["pos"] = np.array([700, 31, 415], np.int32)
+    Lcap = 768
+    say(f"gqa_decode: rope_dim={rope_dim} B=3 pos={d['pos'].tolist()}")
+    lay = M.GatedGQALayer(ctx, 3, Lcap, d["q_norm_w"], d["k_norm_w"], rope_dim=rope_dim)
+    for b in range(3):
+        lay.write_kv(b, 0, W.bf16_to_f32(d["K"][b]), W.bf16_to_f32(d["V"][b]))
+    out = lay.decode(d["pos"], d["qg"], d["k_new"], d["v_new"])
+    ref, kr, vr = oracle_gqa_decode(d, Lcap, rope_dim=rope_dim)
+    _check_gqa(out, ref, f"rope_dim={rope_dim}")
+    for b in range(3):
+        k, v = lay.read_kv(b, int(d["pos"][b]), 1)
+        assert np.array_equal(W.bf16_bits(v[0]), vr[b])
+        kd = np.abs(k[0] - W.bf16_to_f32(kr[b]))
+        assert np.all(kd <= np.abs(W.bf16_to_f32(kr[b])) * 2 ** -7 + 1e-30)
+    if rope_dim:   # the width changes the answer
+        other, _, _ = oracle_gqa_decode(d, Lcap, rope_dim=rope_dim // 2)
+        assert np.abs(other - ref).max() > 1e-3
+
+
 def test_gqa_decode_norm_w(ctx):
     """VX27_GQA_NORM_W on the decode (q/k norm as x*s*w, vx27_gqa.c:10-15).
     Oracle: the (1+w) form with w - 1, exact for w in [0.5, 2] (Sterbenz)."""
