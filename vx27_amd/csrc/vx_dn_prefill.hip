@@ -1282,36 +1282,58 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
             }
         }
     }
-    uint64_t lt[2][2] = {{0, 0}, {0, 0}};   // the block's transposed lo values, four tokens a word
-    for (int j = 0; j < nt; j++) {
-        const size_t row = (size_t)b * a.T + t0 + j;
-        float v2[2];
+    // Every token of the block first (tokens past nt come from clamped or
+    // zero inputs and are never stored), then the pre-norms of all GT tokens
+    // side by side: their wave sums are independent chains that the
+    // scheduler interleaves, where one token at a time they ran back to back.
+    // Each token's operations and their order are unchanged.
+    float v2s[GT][2];
+#pragma unroll
+    for (int j = 0; j < GT; j++)
 #pragma unroll
         for (int e = 0; e < 2; e++) {
             if (conv) {
                 float c[3] = {xw[e][j], xw[e][j + 1], xw[e][j + 2]};
-                v2[e] = conv_step(c, w[e], xw[e][j + 3]);
+                v2s[j][e] = conv_step(c, w[e], xw[e][j + 3]);
             } else {
-                v2[e] = xw[e][j];
+                v2s[j][e] = xw[e][j];
             }
         }
-        if ((is_q || is_k) && (a.flags & (VX27_DN_PRE_RMS | VX27_DN_PRE_L2))) {
-            if (a.flags & VX27_DN_PRE_RMS) {
-                const double ss = vx_wave_sum_f64_dpp((double)v2[0] * (double)v2[0] + (double)v2[1] * (double)v2[1]);
-                const float is = 1.0f / sqrtf((float)(ss / HD) + 1e-6f);
+    if ((is_q || is_k) && (a.flags & (VX27_DN_PRE_RMS | VX27_DN_PRE_L2))) {
+        if (a.flags & VX27_DN_PRE_RMS) {
+            double ss[GT];
 #pragma unroll
-                for (int e = 0; e < 2; e++) v2[e] = (v2[e] * is) * (nw[e] + 1.0f);
+            for (int j = 0; j < GT; j++)
+                ss[j] = vx_wave_sum_f64_dpp((double)v2s[j][0] * (double)v2s[j][0] + (double)v2s[j][1] * (double)v2s[j][1]);
+#pragma unroll
+            for (int j = 0; j < GT; j++) {
+                const float is = 1.0f / sqrtf((float)(ss[j] / HD) + 1e-6f);
+#pragma unroll
+                for (int e = 0; e < 2; e++) v2s[j][e] = (v2s[j][e] * is) * (nw[e] + 1.0f);
             }
-            if (a.flags & VX27_DN_PRE_L2) {
-                const double ss = vx_wave_sum_f64_dpp((double)v2[0] * (double)v2[0] + (double)v2[1] * (double)v2[1]);
-                const float il = 1.0f / sqrtf((float)ss + 1e-6f);
+        }
+        if (a.flags & VX27_DN_PRE_L2) {
+            double ss[GT];
+#pragma unroll
+            for (int j = 0; j < GT; j++)
+                ss[j] = vx_wave_sum_f64_dpp((double)v2s[j][0] * (double)v2s[j][0] + (double)v2s[j][1] * (double)v2s[j][1]);
+#pragma unroll
+            for (int j = 0; j < GT; j++) {
+                const float il = 1.0f / sqrtf((float)ss[j] + 1e-6f);
 #pragma unroll
                 for (int e = 0; e < 2; e++) {
-                    v2[e] = v2[e] * il;
-                    if (is_q) v2[e] = v2[e] * qs;
+                    v2s[j][e] = v2s[j][e] * il;
+                    if (is_q) v2s[j][e] = v2s[j][e] * qs;
                 }
             }
         }
+    }
+    uint64_t lt[2][2] = {{0, 0}, {0, 0}};   // the block's transposed lo values, four tokens a word
+#pragma unroll
+    for (int j = 0; j < GT; j++) {
+        if (j >= nt) break;
+        const size_t row = (size_t)b * a.T + t0 + j;
+        const float v2[2] = {v2s[j][0], v2s[j][1]};
         uint16_t *dst = is_q ? a.qo + (row * a.nqk + hh) * HD
                       : is_k ? a.ko + (row * a.nqk + (hh - a.nqk)) * HD
                              : a.vo + (row * a.nv + (hh - 2 * a.nqk)) * HD;
