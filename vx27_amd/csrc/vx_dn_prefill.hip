@@ -1218,151 +1218,161 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
     if (a.qol && !is_q)
         tl = is_k ? a.klT + ((size_t)b * a.nqk + (hh - a.nqk)) * HD * a.Tp
                   : a.vlT + ((size_t)b * a.nv + (hh - 2 * a.nqk)) * HD * a.Tp;
-    if (t0 >= a.T) {   // padding past the prompt: zeros in the transposed lo rows
-        if (tl) {
+    // Waves past the prompt (padding up to Tp) only take part in the
+    // transposed store at the end, with zeros: with lo parts every wave of a
+    // workgroup passes the test above (Tp is a multiple of 64 and a
+    // workgroup spans 4 GT = 32 tokens), so all four reach its barrier.
+    uint64_t lt[2][2] = {{0, 0}, {0, 0}};   // the block's transposed lo values, four tokens a word
+    if (t0 < a.T) {
+        const bool conv = (a.flags & VX27_DN_CONV) != 0;
+        const float qs = 1.0f / sqrtf((float)HD);
+        const int nt = min(GT, a.T - t0);
+        // Every input of the block is loaded first, unconditionally, from
+        // addresses clamped into the buffers, and the cases are selected after:
+        // a load under a condition would wait for its data inside its branch.
+        // With the conv: the x window of the two channels, tokens t0-3 ..
+        // t0+GT-1 (older ones from the state, none past the prompt), and the
+        // conv weights as raw words (two 8-byte words, the second one repeating
+        // the first for bf16); without it, the block's q, k or v values.
+        float xw[2][GT + 3], w[2][4];
+        float nw[2] = {1.0f, 1.0f};
+        uint2 wr[2][2];
+        float cst[2][3];
+        const uint16_t *src = is_q ? a.q + hh * HD : is_k ? a.k + (hh - a.nqk) * HD : a.v + (hh - 2 * a.nqk) * HD;
+        const int hstride = (is_q || is_k) ? a.nqk * HD : a.nv * HD;
+        if (conv) {   // (one branch around both channels' loads: they all stay in flight together)
 #pragma unroll
-            for (int e = 0; e < 2; e++) *(uint4 *)&tl[(size_t)(lane + 64 * e) * a.Tp + t0] = make_uint4(0u, 0u, 0u, 0u);
+            for (int e = 0; e < 2; e++) {
+                const size_t ch = (size_t)hh * HD + lane + 64 * e;
+                const uint2 *wb = (const uint2 *)a.conv_w;
+                const size_t w0 = a.w_bf16 ? ch : 2 * ch;
+                wr[e][0] = wb[w0];
+                wr[e][1] = wb[a.w_bf16 ? w0 : w0 + 1];
+#pragma unroll
+                for (int t = 0; t < 3; t++) cst[e][t] = a.conv_state[((size_t)b * a.C + ch) * 3 + t];
+#pragma unroll
+                for (int j = 0; j < GT + 3; j++) {
+                    const int sc = min(max(t0 - 3 + j, 0), a.T - 1);
+                    xw[e][j] = a.x[((size_t)b * a.T + sc) * a.C + ch];
+                }
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 2; e++)
+#pragma unroll
+                for (int j = 0; j < GT; j++) {
+                    const size_t row = (size_t)b * a.T + min(t0 + j, a.T - 1);
+                    xw[e][j] = vx_bf16_to_f32(src[row * hstride + lane + 64 * e]);
+                }
         }
-        return;
-    }
-    const bool conv = (a.flags & VX27_DN_CONV) != 0;
-    const float qs = 1.0f / sqrtf((float)HD);
-    const int nt = min(GT, a.T - t0);
-    // Every input of the block is loaded first, unconditionally, from
-    // addresses clamped into the buffers, and the cases are selected after:
-    // a load under a condition would wait for its data inside its branch.
-    // With the conv: the x window of the two channels, tokens t0-3 ..
-    // t0+GT-1 (older ones from the state, none past the prompt), and the
-    // conv weights as raw words (two 8-byte words, the second one repeating
-    // the first for bf16); without it, the block's q, k or v values.
-    float xw[2][GT + 3], w[2][4];
-    float nw[2] = {1.0f, 1.0f};
-    uint2 wr[2][2];
-    float cst[2][3];
-    const uint16_t *src = is_q ? a.q + hh * HD : is_k ? a.k + (hh - a.nqk) * HD : a.v + (hh - 2 * a.nqk) * HD;
-    const int hstride = (is_q || is_k) ? a.nqk * HD : a.nv * HD;
-    if (conv) {   // (one branch around both channels' loads: they all stay in flight together)
+        if (a.norm_w && (is_q || is_k)) {
+            nw[0] = a.norm_w[lane];
+            nw[1] = a.norm_w[lane + 64];
+        }
+        if (conv) {
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const size_t ch = (size_t)hh * HD + lane + 64 * e;
-            const uint2 *wb = (const uint2 *)a.conv_w;
-            const size_t w0 = a.w_bf16 ? ch : 2 * ch;
-            wr[e][0] = wb[w0];
-            wr[e][1] = wb[a.w_bf16 ? w0 : w0 + 1];
+            for (int e = 0; e < 2; e++) {
+                const uint32_t r[4] = {wr[e][0].x, wr[e][0].y, wr[e][1].x, wr[e][1].y};
+                conv_w_decode(a.w_bf16, r, w[e]);
 #pragma unroll
-            for (int t = 0; t < 3; t++) cst[e][t] = a.conv_state[((size_t)b * a.C + ch) * 3 + t];
-#pragma unroll
-            for (int j = 0; j < GT + 3; j++) {
-                const int sc = min(max(t0 - 3 + j, 0), a.T - 1);
-                xw[e][j] = a.x[((size_t)b * a.T + sc) * a.C + ch];
+                for (int j = 0; j < GT + 3; j++) {
+                    const int s = t0 - 3 + j;   // s < 0 only for j < 3 (t0 = 0): state slot j
+                    xw[e][j] = s < 0 ? cst[e][j < 3 ? j : 0] : s < a.T ? xw[e][j] : 0.0f;
+                }
             }
         }
-    } else {
+        // Every token of the block first (tokens past nt come from clamped or
+        // zero inputs and are never stored), then the pre-norms of all GT tokens
+        // side by side: their wave sums are independent chains that the
+        // scheduler interleaves, where one token at a time they ran back to back.
+        // Each token's operations and their order are unchanged.
+        float v2s[GT][2];
 #pragma unroll
-        for (int e = 0; e < 2; e++)
+        for (int j = 0; j < GT; j++)
 #pragma unroll
-            for (int j = 0; j < GT; j++) {
-                const size_t row = (size_t)b * a.T + min(t0 + j, a.T - 1);
-                xw[e][j] = vx_bf16_to_f32(src[row * hstride + lane + 64 * e]);
+            for (int e = 0; e < 2; e++) {
+                if (conv) {
+                    float c[3] = {xw[e][j], xw[e][j + 1], xw[e][j + 2]};
+                    v2s[j][e] = conv_step(c, w[e], xw[e][j + 3]);
+                } else {
+                    v2s[j][e] = xw[e][j];
+                }
             }
-    }
-    if (a.norm_w && (is_q || is_k)) {
-        nw[0] = a.norm_w[lane];
-        nw[1] = a.norm_w[lane + 64];
-    }
-    if (conv) {
+        if ((is_q || is_k) && (a.flags & (VX27_DN_PRE_RMS | VX27_DN_PRE_L2))) {
+            if (a.flags & VX27_DN_PRE_RMS) {
+                double ss[GT];
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-            const uint32_t r[4] = {wr[e][0].x, wr[e][0].y, wr[e][1].x, wr[e][1].y};
-            conv_w_decode(a.w_bf16, r, w[e]);
+                for (int j = 0; j < GT; j++)
+                    ss[j] = vx_wave_sum_f64_dpp((double)v2s[j][0] * (double)v2s[j][0] + (double)v2s[j][1] * (double)v2s[j][1]);
 #pragma unroll
-            for (int j = 0; j < GT + 3; j++) {
-                const int s = t0 - 3 + j;   // s < 0 only for j < 3 (t0 = 0): state slot j
-                xw[e][j] = s < 0 ? cst[e][j < 3 ? j : 0] : s < a.T ? xw[e][j] : 0.0f;
+                for (int j = 0; j < GT; j++) {
+                    const float is = 1.0f / sqrtf((float)(ss[j] / HD) + 1e-6f);
+#pragma unroll
+                    for (int e = 0; e < 2; e++) v2s[j][e] = (v2s[j][e] * is) * (nw[e] + 1.0f);
+                }
             }
-        }
-    }
-    // Every token of the block first (tokens past nt come from clamped or
-    // zero inputs and are never stored), then the pre-norms of all GT tokens
-    // side by side: their wave sums are independent chains that the
-    // scheduler interleaves, where one token at a time they ran back to back.
-    // Each token's operations and their order are unchanged.
-    float v2s[GT][2];
+            if (a.flags & VX27_DN_PRE_L2) {
+                double ss[GT];
 #pragma unroll
-    for (int j = 0; j < GT; j++)
+                for (int j = 0; j < GT; j++)
+                    ss[j] = vx_wave_sum_f64_dpp((double)v2s[j][0] * (double)v2s[j][0] + (double)v2s[j][1] * (double)v2s[j][1]);
 #pragma unroll
-        for (int e = 0; e < 2; e++) {
-            if (conv) {
-                float c[3] = {xw[e][j], xw[e][j + 1], xw[e][j + 2]};
-                v2s[j][e] = conv_step(c, w[e], xw[e][j + 3]);
-            } else {
-                v2s[j][e] = xw[e][j];
-            }
-        }
-    if ((is_q || is_k) && (a.flags & (VX27_DN_PRE_RMS | VX27_DN_PRE_L2))) {
-        if (a.flags & VX27_DN_PRE_RMS) {
-            double ss[GT];
+                for (int j = 0; j < GT; j++) {
+                    const float il = 1.0f / sqrtf((float)ss[j] + 1e-6f);
 #pragma unroll
-            for (int j = 0; j < GT; j++)
-                ss[j] = vx_wave_sum_f64_dpp((double)v2s[j][0] * (double)v2s[j][0] + (double)v2s[j][1] * (double)v2s[j][1]);
-#pragma unroll
-            for (int j = 0; j < GT; j++) {
-                const float is = 1.0f / sqrtf((float)(ss[j] / HD) + 1e-6f);
-#pragma unroll
-                for (int e = 0; e < 2; e++) v2s[j][e] = (v2s[j][e] * is) * (nw[e] + 1.0f);
+                    for (int e = 0; e < 2; e++) {
+                        v2s[j][e] = v2s[j][e] * il;
+                        if (is_q) v2s[j][e] = v2s[j][e] * qs;
+                    }
+                }
             }
         }
-        if (a.flags & VX27_DN_PRE_L2) {
-            double ss[GT];
 #pragma unroll
-            for (int j = 0; j < GT; j++)
-                ss[j] = vx_wave_sum_f64_dpp((double)v2s[j][0] * (double)v2s[j][0] + (double)v2s[j][1] * (double)v2s[j][1]);
-#pragma unroll
-            for (int j = 0; j < GT; j++) {
-                const float il = 1.0f / sqrtf((float)ss[j] + 1e-6f);
-#pragma unroll
-                for (int e = 0; e < 2; e++) {
-                    v2s[j][e] = v2s[j][e] * il;
-                    if (is_q) v2s[j][e] = v2s[j][e] * qs;
+        for (int j = 0; j < GT; j++) {
+            if (j >= nt) break;
+            const size_t row = (size_t)b * a.T + t0 + j;
+            const float v2[2] = {v2s[j][0], v2s[j][1]};
+            uint16_t *dst = is_q ? a.qo + (row * a.nqk + hh) * HD
+                          : is_k ? a.ko + (row * a.nqk + (hh - a.nqk)) * HD
+                                 : a.vo + (row * a.nv + (hh - 2 * a.nqk)) * HD;
+            const uint16_t h0 = vx_f32_to_bf16(v2[0]), h1 = vx_f32_to_bf16(v2[1]);
+            dst[lane] = h0;
+            dst[lane + 64] = h1;
+            if (a.qol) {
+                const uint16_t l0 = vx_f32_to_bf16(v2[0] - vx_bf16_to_f32(h0));
+                const uint16_t l1 = vx_f32_to_bf16(v2[1] - vx_bf16_to_f32(h1));
+                if (is_q || is_k) {
+                    uint16_t *dl = is_q ? a.qol + (row * a.nqk + hh) * HD : a.kol + (row * a.nqk + (hh - a.nqk)) * HD;
+                    dl[lane] = l0;
+                    dl[lane + 64] = l1;
+                }
+                const int sh = 16 * (j & 3);
+                if (j < 4) {
+                    lt[0][0] |= (uint64_t)l0 << sh;
+                    lt[1][0] |= (uint64_t)l1 << sh;
+                } else {
+                    lt[0][1] |= (uint64_t)l0 << sh;
+                    lt[1][1] |= (uint64_t)l1 << sh;
                 }
             }
         }
     }
-    uint64_t lt[2][2] = {{0, 0}, {0, 0}};   // the block's transposed lo values, four tokens a word
-#pragma unroll
-    for (int j = 0; j < GT; j++) {
-        if (j >= nt) break;
-        const size_t row = (size_t)b * a.T + t0 + j;
-        const float v2[2] = {v2s[j][0], v2s[j][1]};
-        uint16_t *dst = is_q ? a.qo + (row * a.nqk + hh) * HD
-                      : is_k ? a.ko + (row * a.nqk + (hh - a.nqk)) * HD
-                             : a.vo + (row * a.nv + (hh - 2 * a.nqk)) * HD;
-        const uint16_t h0 = vx_f32_to_bf16(v2[0]), h1 = vx_f32_to_bf16(v2[1]);
-        dst[lane] = h0;
-        dst[lane + 64] = h1;
-        if (a.qol) {
-            const uint16_t l0 = vx_f32_to_bf16(v2[0] - vx_bf16_to_f32(h0));
-            const uint16_t l1 = vx_f32_to_bf16(v2[1] - vx_bf16_to_f32(h1));
-            if (is_q || is_k) {
-                uint16_t *dl = is_q ? a.qol + (row * a.nqk + hh) * HD : a.kol + (row * a.nqk + (hh - a.nqk)) * HD;
-                dl[lane] = l0;
-                dl[lane + 64] = l1;
-            }
-            const int sh = 16 * (j & 3);
-            if (j < 4) {
-                lt[0][0] |= (uint64_t)l0 << sh;
-                lt[1][0] |= (uint64_t)l1 << sh;
-            } else {
-                lt[0][1] |= (uint64_t)l0 << sh;
-                lt[1][1] |= (uint64_t)l1 << sh;
-            }
-        }
-    }
-    if (tl) {   // tokens past nt stay zero
+    if (tl) {   // (uniform in the workgroup) tokens past nt stay zero
+        // the four waves' 8 tokens of each channel side by side in LDS, then
+        // stored as 64-byte runs (four lanes a channel) instead of 16-byte
+        // pieces one row apart
+        __shared__ uint4 s_lt[2][64][4];   // [e][lane][wave]
 #pragma unroll
         for (int e = 0; e < 2; e++)
-            *(uint4 *)&tl[(size_t)(lane + 64 * e) * a.Tp + t0] =
-                make_uint4((uint32_t)lt[e][0], (uint32_t)(lt[e][0] >> 32), (uint32_t)lt[e][1], (uint32_t)(lt[e][1] >> 32));
+            s_lt[e][lane][wave] = make_uint4((uint32_t)lt[e][0], (uint32_t)(lt[e][0] >> 32), (uint32_t)lt[e][1],
+                                             (uint32_t)(lt[e][1] >> 32));
+        __syncthreads();
+        const int tw = blockIdx.x * 4 * GT;   // the workgroup's first token
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int pc = threadIdx.x + 256 * i, c = pc >> 2, q = pc & 3;   // channel c (0..127), wave slot q
+            *(uint4 *)&tl[(size_t)c * a.Tp + tw + GT * q] = s_lt[c >> 6][c & 63][q];
+        }
     }
 }
 
