@@ -1223,6 +1223,7 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
     // workgroup passes the test above (Tp is a multiple of 64 and a
     // workgroup spans 4 GT = 32 tokens), so all four reach its barrier.
     uint64_t lt[2][2] = {{0, 0}, {0, 0}};   // the block's transposed lo values, four tokens a word
+    __shared__ __attribute__((aligned(16))) uint16_t s_rows[4][2][GT][HD];   // [wave][hi, lo][token][channel]
     if (t0 < a.T) {
         const bool conv = (a.flags & VX27_DN_CONV) != 0;
         const float qs = 1.0f / sqrtf((float)HD);
@@ -1330,22 +1331,15 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
 #pragma unroll
         for (int j = 0; j < GT; j++) {
             if (j >= nt) break;
-            const size_t row = (size_t)b * a.T + t0 + j;
             const float v2[2] = {v2s[j][0], v2s[j][1]};
-            uint16_t *dst = is_q ? a.qo + (row * a.nqk + hh) * HD
-                          : is_k ? a.ko + (row * a.nqk + (hh - a.nqk)) * HD
-                                 : a.vo + (row * a.nv + (hh - 2 * a.nqk)) * HD;
             const uint16_t h0 = vx_f32_to_bf16(v2[0]), h1 = vx_f32_to_bf16(v2[1]);
-            dst[lane] = h0;
-            dst[lane + 64] = h1;
+            s_rows[wave][0][j][lane] = h0;
+            s_rows[wave][0][j][lane + 64] = h1;
             if (a.qol) {
                 const uint16_t l0 = vx_f32_to_bf16(v2[0] - vx_bf16_to_f32(h0));
                 const uint16_t l1 = vx_f32_to_bf16(v2[1] - vx_bf16_to_f32(h1));
-                if (is_q || is_k) {
-                    uint16_t *dl = is_q ? a.qol + (row * a.nqk + hh) * HD : a.kol + (row * a.nqk + (hh - a.nqk)) * HD;
-                    dl[lane] = l0;
-                    dl[lane + 64] = l1;
-                }
+                s_rows[wave][1][j][lane] = l0;
+                s_rows[wave][1][j][lane + 64] = l1;
                 const int sh = 16 * (j & 3);
                 if (j < 4) {
                     lt[0][0] |= (uint64_t)l0 << sh;
@@ -1353,6 +1347,27 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
                 } else {
                     lt[0][1] |= (uint64_t)l0 << sh;
                     lt[1][1] |= (uint64_t)l1 << sh;
+                }
+            }
+        }
+        // the block's rows out of the wave's own LDS slots, 16 bytes a lane
+        // (lane: row (lane >> 4) + 4 i, channels 8 (lane & 15) ..): two stores
+        // of hi rows (and of lo rows for q, k) instead of one 2-byte store per
+        // row and channel half
+        const int cg = lane & 15;
+        __builtin_amdgcn_wave_barrier();   // (the slots are this wave's own: LDS runs its ops in order)
+#pragma unroll
+        for (int i = 0; i < 2; i++) {
+            const int jr = (lane >> 4) + 4 * i;
+            if (jr < nt) {
+                const size_t row = (size_t)b * a.T + t0 + jr;
+                uint16_t *dst = is_q ? a.qo + (row * a.nqk + hh) * HD
+                              : is_k ? a.ko + (row * a.nqk + (hh - a.nqk)) * HD
+                                     : a.vo + (row * a.nv + (hh - 2 * a.nqk)) * HD;
+                *(uint4 *)(dst + 8 * cg) = *(const uint4 *)&s_rows[wave][0][jr][8 * cg];
+                if (a.qol && (is_q || is_k)) {
+                    uint16_t *dl = is_q ? a.qol + (row * a.nqk + hh) * HD : a.kol + (row * a.nqk + (hh - a.nqk)) * HD;
+                    *(uint4 *)(dl + 8 * cg) = *(const uint4 *)&s_rows[wave][1][jr][8 * cg];
                 }
             }
         }
