@@ -87,7 +87,15 @@ int vx27_hip_free(vx27_hip_ctx *ctx, void *dptr);
 int vx27_hip_h2d(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
 int vx27_hip_d2h(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
 int vx27_hip_d2d(vx27_hip_ctx *ctx, void *dst, const void *src, size_t bytes);
+/* Fills `bytes` bytes at dst with `byte`, by a kernel on the context stream
+ * (never hipMemsetAsync), so it may be captured into a graph. */
 int vx27_hip_memset(vx27_hip_ctx *ctx, void *dst, int byte, size_t bytes);
+/* Diagnostics with no counterpart in the reference: the context's scratch
+ * size, how many device buffers it keeps retired for live graphs, how many
+ * prefill attention schedules it caches and how many graphs captured on it
+ * are alive.  Any output pointer may be NULL. */
+int vx27_hip_mem_info(vx27_hip_ctx *ctx, size_t *scratch_bytes, int *retired_buffers, int *cached_schedules,
+                      int *live_graphs);
 /* HBM bandwidth probe, a measurement utility with no counterpart in the
  * reference: allocates `bytes` of device memory (at least 1 MiB; use far
  * more than the 256 MiB Infinity Cache), then `iters` times (after one

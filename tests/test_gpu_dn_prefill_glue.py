@@ -7,10 +7,12 @@ vx27_engine_commit_ckpt (vx27_run.c:250-255).
 Oracle: orc_dn_run with the same flags (the restated vx27_qlayer glue,
 pinned bit-exact to the compiled reference's vx27_qlayer), fed the same fp32
 inputs in token order.
-Bars: the exact path (fp32 recurrence token by token) 1e-5; the chunked path
-(q, k, v enter bf16 MFMA products) the bf16 bar 2e-2 + 1e-2|ref| and max|d|
-<= 2% of max|ref|; conv states bit-exact (they are copies of inputs); the
-checkpointed path bit-exact against vx27_hip_dn_decode called token by
+Bars: the exact path (fp32 recurrence token by token) 1e-5; the chunked
+default (every operand of the chunk products a bf16 hi + lo pair) max|d| <=
+1e-4 of max|ref| on outputs and final state, on top of the bf16 bar; the
+VX27_DN_BF16 form (single bf16 operands) the bf16 bar 2e-2 + 1e-2|ref| and
+max|d| <= 2% of max|ref|; conv states bit-exact (they are copies of inputs);
+the checkpointed path bit-exact against vx27_hip_dn_decode called token by
 token."""
 import ctypes as C
 
@@ -95,18 +97,45 @@ def check_bf16(got, ref, tag):
     assert np.all(err <= lim) and err.max() <= 0.02 * big, tag
 
 
+X3_REL = 1e-4   # split-precision bar: max|d| <= 1e-4 of max|ref| (single bf16 products reach ~4e-3)
+
+
+def check_split(got, ref, tag):
+    """The chunked default's bar: the bf16 bar, and max|d| <= X3_REL max|ref|."""
+    check_bf16(got, ref, tag)
+    rel = maxabs(got, ref) / np.abs(ref).max()
+    say(f"  {tag}: max|d|/max|ref| = {rel:.3e} (bar {X3_REL:g})")
+    assert rel <= X3_REL, tag
+
+
 def test_dn_prefill_glue_chunked_4096(ctx):
     """The real layer's shape (nqk 16, nv 48), one 4096-token prompt, every
-    glue stage, chunked algorithm."""
+    glue stage, chunked algorithm (split-precision products)."""
     from vx27_amd import workloads as W
     d = W.dn_prefill_glue(B=1, T=4096, nqk=16, nv=48)
     say("dn prefill glue: B=1 T=4096 nqk=16 nv=48 all stages, chunked")
     g = run_prefill(ctx, d, 16, ALL)
     ref, S, conv = oracle(d, 16, ALL)
-    check_bf16(g["out"], ref, "out")
-    eS = maxabs(g["S"], S)
-    say(f"  final state max|d|={eS:.3e} (max|S|={np.abs(S).max():.3f})")
-    check_bf16(g["S"], S, "final state")
+    check_split(g["out"], ref, "out")
+    check_split(g["S"], S, "final state")
+    assert np.array_equal(g["conv"], conv)
+
+
+def test_dn_prefill_glue_chunked_bf16(ctx):
+    """VX27_DN_BF16 with every glue stage (single bf16 operands).  The gated
+    output norm makes these outputs large (|o| up to ~19) and the bf16
+    products' error scales with them, so the bar is the scale one: max|d| <=
+    2% of max|ref|, outputs and final state (a dropped or mis-decayed chunk
+    term exceeds it)."""
+    from vx27_amd import lib as L, workloads as W
+    d = W.dn_prefill_glue(B=2, T=333, nqk=16, nv=48, config=10)
+    say("dn prefill glue: B=2 T=333 nqk=16 nv=48 all stages, chunked, bf16 products")
+    g = run_prefill(ctx, d, 16, ALL | L.DN_BF16)
+    ref, S, conv = oracle(d, 16, ALL)
+    for got, want, tag in ((g["out"], ref, "out"), (g["S"], S, "final state")):
+        rel = maxabs(got, want) / np.abs(want).max()
+        say(f"  {tag}: max|d|/max|ref| = {rel:.3e} (bar 0.02)")
+        assert np.all(np.isfinite(got)) and rel <= 0.02, tag
     assert np.array_equal(g["conv"], conv)
 
 
@@ -137,8 +166,8 @@ def test_dn_prefill_glue_chunked_flags(ctx, flags):
     else:
         ref, S, conv = oracle(d, 16, flags)
         assert np.array_equal(g["conv"], conv)
-    check_bf16(g["out"], ref, f"flags={flags}")
-    check_bf16(g["S"], S, f"flags={flags} final state")
+    check_split(g["out"], ref, f"flags={flags}")
+    check_split(g["S"], S, f"flags={flags} final state")
 
 
 def test_dn_prefill_exact_path(ctx):

@@ -51,11 +51,12 @@ def test_graph_survives_scratch_growth():
         pd = L.DnPrefillDesc(1, 2048, 16, 16, 128, 0, bufs["S0"].ptr, bufs["q"].ptr, bufs["k"].ptr, bufs["v"].ptr,
                              bufs["a"].ptr, bufs["b"].ptr, bufs["A_log"].ptr, bufs["dt_bias"].ptr, po.ptr)
         L.check(lib.vx27_hip_dn_prefill(ctx.h, C.byref(pd)), "dn_prefill")
-        gp = W.gqa_prefill(B=1, T=200, config=43)
+        # (1300 tokens: 11 query tiles x 24 heads, more items than CUs, so a schedule is built)
+        gp = W.gqa_prefill(B=1, T=1300, config=43)
         gb = {k: ctx.put(gp[k]) for k in ("q", "gate", "k", "v", "q_norm_w", "k_norm_w")}
-        kc, vc, go = ctx.buf(4 * 256 * 256 * 2), ctx.buf(4 * 256 * 256 * 2), ctx.buf(200 * 24 * 256 * 4)
-        gd = L.GqaPrefillDesc(1, 200, 24, 4, 256, 64, 1e7, 1.0, 256, 0, 0, gb["q"].ptr, 0, 0, gb["gate"].ptr, 0, 0,
-                              gb["k"].ptr, gb["v"].ptr, gb["q_norm_w"].ptr, gb["k_norm_w"].ptr, kc.ptr, vc.ptr,
+        kc, vc, go = ctx.buf(4 * 1344 * 256 * 2), ctx.buf(4 * 1344 * 256 * 2), ctx.buf(1300 * 24 * 256 * 4)
+        gd = L.GqaPrefillDesc(1, 1300, 24, 4, 256, 64, 1e7, 1.0, 1344, 0, 0, gb["q"].ptr, 0, 0, gb["gate"].ptr, 0,
+                              0, gb["k"].ptr, gb["v"].ptr, gb["q_norm_w"].ptr, gb["k_norm_w"].ptr, kc.ptr, vc.ptr,
                               go.ptr)
         L.check(lib.vx27_hip_gqa_prefill(ctx.h, C.byref(gd)), "gqa_prefill")
         ctx.sync()
@@ -165,5 +166,96 @@ def test_dn_prefill_graph_replay():
                 assert np.array_equal(o_g, o_e) and np.array_equal(S_g, S_e), rep
                 reset(); run(); ctx.sync()     # eager between replays, same answer
                 assert np.array_equal(po.download((T, 16, 128), np.float32), o_e)
+        finally:
+            L.check(lib.vx27_hip_graph_destroy(g), "graph_destroy")
+
+
+def _gqa_prefill_setup(ctx, T, Lc, config):
+    from vx27_amd import lib as L, workloads as W
+    d = W.gqa_prefill(B=1, T=T, config=config)
+    bufs = {k: ctx.put(d[k]) for k in ("q", "gate", "k", "v", "q_norm_w", "k_norm_w")}
+    kc, vc, ob = ctx.buf(4 * Lc * 256 * 2), ctx.buf(4 * Lc * 256 * 2), ctx.buf(T * 24 * 256 * 4)
+    desc = L.GqaPrefillDesc(1, T, 24, 4, 256, 64, 1e7, 1.0, Lc, 0, 0, bufs["q"].ptr, 0, 0, bufs["gate"].ptr, 0, 0,
+                            bufs["k"].ptr, bufs["v"].ptr, bufs["q_norm_w"].ptr, bufs["k_norm_w"].ptr, kc.ptr, vc.ptr,
+                            ob.ptr)
+    return desc, ob
+
+
+def test_schedule_cache_bounded_with_live_graph():
+    """Prefills at many distinct start positions while a captured graph is
+    alive (a serving loop that keeps a decode graph): the schedule cache
+    flushes at 64 shapes and frees the schedules no capture launched, so the
+    context keeps only the one schedule the graph uses; that one is released
+    when the graph is destroyed.  A short window (one query tile per head)
+    builds no schedule at all."""
+    from vx27_amd import lib as L
+    lib = L.lib()
+    with L.Ctx(0) as ctx:
+        T, Lc = 1300, 1408
+        desc, ob = _gqa_prefill_setup(ctx, T, Lc, 61)
+        L.check(lib.vx27_hip_gqa_prefill(ctx.h, C.byref(desc)), "gqa_prefill")   # sizes scratch, caches pos0 = 0
+        ctx.sync()
+        eager = ob.download((1, T, 24, 256), np.float32)
+        ctx.graph_begin()
+        L.check(lib.vx27_hip_gqa_prefill(ctx.h, C.byref(desc)), "gqa_prefill (capture)")
+        g = ctx.graph_end()
+        info0 = ctx.mem_info()
+        say(f"  after capture: {info0}")
+        try:
+            for p0 in range(1, 100):
+                desc.pos0 = p0
+                L.check(lib.vx27_hip_gqa_prefill(ctx.h, C.byref(desc)), "gqa_prefill")
+            ctx.sync()
+            info = ctx.mem_info()
+            say(f"  after 99 more start positions: {info}")
+            assert info["schedules"] <= 64
+            assert info["retired"] <= info0["retired"] + 1     # only the captured schedule is kept
+            desc.pos0 = 0
+            ob.zero()
+            ctx.graph_launch(g)
+            ctx.sync()
+            assert np.array_equal(ob.download((1, T, 24, 256), np.float32), eager)
+        finally:
+            L.check(lib.vx27_hip_graph_destroy(g), "graph_destroy")
+        assert ctx.mem_info()["retired"] == 0 and ctx.mem_info()["live_graphs"] == 0
+        # a verify window of 8 tokens at a moving position caches nothing
+        n0 = ctx.mem_info()["schedules"]
+        small, _ = _gqa_prefill_setup(ctx, 8, 256, 62)
+        for p0 in range(0, 80, 8):
+            small.pos0 = p0
+            L.check(lib.vx27_hip_gqa_prefill(ctx.h, C.byref(small)), "gqa_prefill (window)")
+        ctx.sync()
+        assert ctx.mem_info()["schedules"] == n0
+
+
+def test_memset_kernel_and_capture():
+    """vx27_hip_memset fills any byte range (unaligned head and tail) by a
+    kernel, so it may be captured: a captured fill replays correctly with
+    other writes between the replays."""
+    from vx27_amd import lib as L
+    lib = L.lib()
+    with L.Ctx(0) as ctx:
+        n = 10007
+        buf = ctx.buf(n)
+        for off, cnt, byte in ((0, n, 0xAB), (3, 5000, 0x00), (17, 1, 0x7F), (5, 16, 0x11), (1, 40, 0xFE)):
+            L.check(lib.vx27_hip_memset(ctx.h, buf.ptr, 0x5A, n), "memset")
+            L.check(lib.vx27_hip_memset(ctx.h, buf.ptr + off, byte, cnt), "memset")
+            ctx.sync()
+            got = buf.download((n,), np.uint8)
+            want = np.full(n, 0x5A, np.uint8)
+            want[off:off + cnt] = byte
+            assert np.array_equal(got, want), (off, cnt, byte)
+        ctx.graph_begin()
+        L.check(lib.vx27_hip_memset(ctx.h, buf.ptr + 9, 0x33, 9000), "memset (capture)")
+        g = ctx.graph_end()
+        try:
+            for rep in range(3):
+                L.check(lib.vx27_hip_memset(ctx.h, buf.ptr, 0xC3, n), "memset")
+                ctx.sync()
+                ctx.graph_launch(g)
+                ctx.sync()
+                want = np.full(n, 0xC3, np.uint8)
+                want[9:9009] = 0x33
+                assert np.array_equal(buf.download((n,), np.uint8), want), rep
         finally:
             L.check(lib.vx27_hip_graph_destroy(g), "graph_destroy")

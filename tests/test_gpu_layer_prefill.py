@@ -89,9 +89,10 @@ def test_dn_layer_prefill_verify_window(ctx):
 
 
 def test_dn_layer_prefill_chunked(ctx):
-    """The chunked default on a 40-token prompt of one sequence."""
+    """The chunked default on a 130-token prompt of one sequence (three
+    chunks, the last one ragged, so the state crosses chunk boundaries)."""
     from vx27_amd import workloads as W
-    B, T, nqk, nv = 1, 40, 16, 48
+    B, T, nqk, nv = 1, 130, 16, 48
     r = W.rng(13, "dn_layer_prefill_chunked")
     w, S, conv = dn_layer_inputs(r, B, nqk, nv)
     x = W.normal(r, (B, T, H))
@@ -102,8 +103,9 @@ def test_dn_layer_prefill_chunked(ctx):
     err = np.abs(g["out"].astype(np.float64) - ref)
     big = np.abs(ref).max()
     say(f"  chunked: max|d out|={err.max():.3e} (max|ref|={big:.3f}) max|d S|={maxabs(g['S'], Sr):.3e}")
-    assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)) and err.max() <= 1e-3 * big
-    assert maxabs(g["S"], Sr) <= 1e-3 * np.abs(Sr).max()
+    # split-precision products: within 1e-4 of max|ref| (single bf16 products reach ~4e-3)
+    assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)) and err.max() <= 1e-4 * big
+    assert maxabs(g["S"], Sr) <= 1e-4 * np.abs(Sr).max()
     # the conv state holds projection outputs: fp32 MFMA sums vs the oracle's double sums
     assert maxabs(g["conv"], cr) <= 1e-5
 

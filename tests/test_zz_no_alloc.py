@@ -49,10 +49,45 @@ def test_noalloc_matches_gqa_decode():
             orc, _, _ = oracle_gqa_decode(d, Lcap)
             err = np.abs(got.astype(np.float64) - orc)
             assert np.all(err <= 2e-2 + 1e-2 * np.abs(orc)) and err.max() <= 0.02 * np.abs(orc).max()
-        # beyond the static scratch: 1024 splits x 64 sequences of partials
+        # beyond the static scratch: 2 sequences x 4096 splits x 24 query heads of
+        # partials (258 floats each) need about 50 MB, over the 16 MiB array
         desc.B = 2
         desc.n_split = 4096
         rc = lib.vx27_hip_gqa_decode_noalloc(ctx.h, C.byref(desc))
         msg = lib.vx27_hip_last_error().decode()
         say(f"  oversize: rc={rc} {msg}")
         assert rc == -1 and "static buffer" in msg
+
+
+def test_noalloc_captured_on_fresh_context():
+    """The no-allocation entry point captured into a graph as the first call
+    on a fresh context (no earlier call sized anything): two replays, with
+    eager work between them, equal the eager vx27_hip_gqa_decode bit for bit."""
+    from vx27_amd import lib as L
+    lib = L.lib()
+    with L.Ctx(0) as ctx:
+        B, nk, Lcap = 2, 3000, 3072
+        say(f"noalloc capture on a fresh context: B={B} keys={nk + 1}")
+        d, lay, desc, ob = _setup(ctx, B, nk, Lcap, 73)
+        ctx.graph_begin()
+        L.check(lib.vx27_hip_gqa_decode_noalloc(ctx.h, C.byref(desc)), "gqa_decode_noalloc (capture)")
+        g = ctx.graph_end()
+        try:
+            replays = []
+            for _ in range(2):
+                ob.zero()
+                ctx.sync()
+                ctx.graph_launch(g)
+                ctx.sync()
+                replays.append(ob.download((B, 24, 256), np.float32))
+                L.check(lib.vx27_hip_gqa_decode_noalloc(ctx.h, C.byref(desc)), "gqa_decode_noalloc")   # eager between
+                ctx.sync()
+        finally:
+            L.check(lib.vx27_hip_graph_destroy(g), "graph_destroy")
+        ob.zero()
+        L.check(lib.vx27_hip_gqa_decode(ctx.h, C.byref(desc)), "gqa_decode")
+        ctx.sync()
+        ref = ob.download((B, 24, 256), np.float32)
+        for i, r in enumerate(replays):
+            say(f"  replay {i}: equal to vx27_hip_gqa_decode {np.array_equal(r, ref)}")
+            assert np.array_equal(r, ref), i

@@ -36,8 +36,9 @@ struct vx27_hip_ctx {
     int live_graphs;
     std::vector<void *> retired;
     // device flag set by a decode kernel that saw a position outside its KV
-    // cache; read back and cleared by vx27_hip_sync
+    // cache; read back (into err_host, pinned) and cleared by vx27_hip_sync
     int *err_flag;
+    int *err_host;
     // kernel profiler (vx27_hip_prof_*): off unless enabled
     int prof_on;
     vx_prof_rec *prof;

@@ -896,6 +896,7 @@ struct GqpSched {
     int key[7];
     int *dev;
     int len, n_wg;
+    bool captured;   // launched inside a stream capture: a graph may hold dev
 };
 typedef std::pair<int, int> CostItem;   // (cost, item code)
 
@@ -942,22 +943,34 @@ void gqp_pack(std::vector<CostItem> items, int nb, std::vector<std::vector<CostI
         std::sort(bn.begin(), bn.end(), [](const CostItem &x, const CostItem &y) { return x.first > y.first; });
 }
 
-// The schedule for this call's shape (built and uploaded once per shape and
-// kept until the context closes: a captured graph holds its address);
-// nullptr when it would have to be uploaded inside a stream capture.
+// The schedule for this call's shape, built and uploaded once per shape and
+// cached; nullptr when the items fit the CUs (one workgroup per item needs no
+// list) or when it would have to be uploaded inside a stream capture.  After
+// 64 shapes the cache starts afresh: a schedule that a capture launched is
+// retired (kept while a captured graph may hold its address), the others are
+// freed at once.  A verify window that moves pos0 every step has at most one
+// 128-query tile per head, so it never builds a schedule.
 const GqpSched *gqp_schedule(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d, int xcd_map) {
     const int n_qt = (d->T + PP_QT - 1) / PP_QT;
+    if ((long long)d->B * d->n_q * n_qt <= ctx->n_cu) return nullptr;
+    const bool capturing = vx_ctx_capturing(ctx);
     const int key[7] = {d->T, d->pos0, d->n_q, d->n_kv, d->B, ctx->n_cu, xcd_map};
     for (void *p : ctx->gqp_scheds) {
-        const GqpSched *c = (const GqpSched *)p;
-        if (std::equal(key, key + 7, c->key)) return c;
+        GqpSched *c = (GqpSched *)p;
+        if (std::equal(key, key + 7, c->key)) {
+            if (capturing) c->captured = true;
+            return c;
+        }
     }
-    if (vx_ctx_capturing(ctx)) return nullptr;
-    if (ctx->gqp_scheds.size() >= 64) {   // many shapes seen: start the cache afresh
+    if (capturing) return nullptr;
+    if (ctx->gqp_scheds.size() >= 64) {
         if (hipStreamSynchronize(ctx->stream) != hipSuccess) return nullptr;
         for (void *p : ctx->gqp_scheds) {
             GqpSched *old = (GqpSched *)p;
-            vx_ctx_release(ctx, old->dev);   // kept while a captured graph may use it
+            if (old->captured)
+                vx_ctx_release(ctx, old->dev);
+            else
+                (void)hipFree(old->dev);
             free(old);
         }
         ctx->gqp_scheds.clear();
@@ -1086,7 +1099,7 @@ int vx_gqa_prefill_into(vx27_hip_ctx *ctx, const vx27_gqa_prefill_desc *d, void 
         aa.sched = sc->dev;
         aa.sched_len = sc->len;
         VX_LAUNCH_NAMED(ctx, "gqp_attn", gqp_attn_pp, dim3((unsigned)sc->n_wg), dim3(PP_NW * 64), aa);
-    } else {    // (inside a stream capture, first call of a shape) one workgroup per item
+    } else {    // few items, or a capture's first call of a shape: one workgroup per item
         VX_LAUNCH_NAMED(ctx, "gqp_attn", gqp_attn_pp, dim3((unsigned)(n_qt * d->n_q), (unsigned)d->B), dim3(PP_NW * 64), aa);
     }
     return 0;

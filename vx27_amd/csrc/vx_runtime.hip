@@ -72,13 +72,17 @@ extern "C" int vx27_hip_open(vx27_hip_ctx **out, int device, char *err, size_t e
         delete c;
         return fail();
     }
-    if (hipMalloc((void **)&c->err_flag, 256) != hipSuccess || hipMemset(c->err_flag, 0, 256) != hipSuccess) {
+    if (hipMalloc((void **)&c->err_flag, 256) != hipSuccess || hipMemset(c->err_flag, 0, 256) != hipSuccess ||
+        hipHostMalloc((void **)&c->err_host, 256, hipHostMallocDefault) != hipSuccess) {
         vx_set_error("vx27_hip_open: cannot allocate the error flag on device %d", device);
+        if (c->err_flag) (void)hipFree(c->err_flag);
         (void)hipStreamDestroy(c->own_stream);
         delete c;
         return fail();
     }
+    *c->err_host = 0;
     if (vx_noalloc_init(device) != 0) {
+        (void)hipHostFree(c->err_host);
         (void)hipFree(c->err_flag);
         (void)hipStreamDestroy(c->own_stream);
         delete c;
@@ -170,17 +174,21 @@ extern "C" void vx27_hip_close(vx27_hip_ctx *ctx) {
     if (ctx->scratch) (void)hipFree(ctx->scratch);
     if (ctx->stage) (void)hipFree(ctx->stage);
     if (ctx->err_flag) (void)hipFree(ctx->err_flag);
+    if (ctx->err_host) (void)hipHostFree(ctx->err_host);
     (void)hipStreamDestroy(ctx->own_stream);
     delete ctx;
 }
 
 extern "C" int vx27_hip_sync(vx27_hip_ctx *ctx) {
     if (vx_ctx_enter(ctx)) return -1;
+    // the flag's copy rides on the stream, so one wait covers both
+    VX_HIP(hipMemcpyAsync(ctx->err_host, ctx->err_flag, sizeof(int), hipMemcpyDeviceToHost, ctx->stream));
     VX_HIP(hipStreamSynchronize(ctx->stream));
-    int flag = 0;
-    VX_HIP(hipMemcpy(&flag, ctx->err_flag, sizeof flag, hipMemcpyDeviceToHost));
+    const int flag = *(volatile int *)ctx->err_host;
     if (flag) {
-        VX_HIP(hipMemset(ctx->err_flag, 0, sizeof flag));
+        *ctx->err_host = 0;
+        VX_HIP(hipMemcpyAsync(ctx->err_flag, ctx->err_host, sizeof(int), hipMemcpyHostToDevice, ctx->stream));
+        VX_HIP(hipStreamSynchronize(ctx->stream));
         VX_REQUIRE(false, "vx27_hip_sync: a call since the last sync had an index outside its range (a decode "
                           "position outside its KV cache, or a commit index past its checkpoints); that call's "
                           "outputs are undefined");
@@ -349,9 +357,42 @@ extern "C" int vx27_hip_d2d(vx27_hip_ctx *ctx, void *dst, const void *src, size_
     VX_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, ctx->stream));
     return 0;
 }
+// A byte fill as a kernel, not hipMemsetAsync, so that a caller may capture
+// it into a graph: the bytes before the first 16-byte boundary and after the
+// last one are stored singly, the rest as 16-byte vector stores.
+__global__ __launch_bounds__(256) void vx_fill_kernel(unsigned char *dst, size_t head, size_t n16, size_t tail,
+                                                      uint32_t word) {
+    const size_t i = (size_t)blockIdx.x * blockDim.x + threadIdx.x, stride = (size_t)gridDim.x * blockDim.x;
+    const uint4 w4 = make_uint4(word, word, word, word);
+    uint4 *body = (uint4 *)(dst + head);
+    for (size_t j = i; j < n16; j += stride) body[j] = w4;
+    if (i < head) dst[i] = (unsigned char)word;
+    if (i < tail) dst[head + n16 * 16 + i] = (unsigned char)word;
+}
+
 extern "C" int vx27_hip_memset(vx27_hip_ctx *ctx, void *dst, int byte, size_t bytes) {
     if (vx_ctx_enter(ctx)) return -1;
-    VX_HIP(hipMemsetAsync(dst, byte, bytes, ctx->stream));
+    if (bytes == 0) return 0;
+    VX_REQUIRE(dst != nullptr, "vx27_hip_memset: null pointer");
+    const uintptr_t a = (uintptr_t)dst;
+    size_t head = (16 - (a & 15)) & 15;
+    if (head > bytes) head = bytes;
+    const size_t n16 = (bytes - head) / 16, tail = bytes - head - n16 * 16;
+    const uint32_t word = 0x01010101u * (uint32_t)(unsigned char)byte;
+    const size_t want = (n16 + 255) / 256;
+    const unsigned grid = (unsigned)(want < 1 ? 1 : want > 4096 ? 4096 : want);
+    VX_LAUNCH(ctx, vx_fill_kernel, dim3(grid), dim3(256), (unsigned char *)dst, head, n16, tail, word);
+    return 0;
+}
+
+extern "C" int vx27_hip_mem_info(vx27_hip_ctx *ctx, size_t *scratch_bytes, int *retired_buffers,
+                                 int *cached_schedules, int *live_graphs) {
+    VX_REQUIRE(ctx != nullptr, "null context");
+    std::lock_guard<std::mutex> lk(g_graph_mu);
+    if (scratch_bytes) *scratch_bytes = ctx->scratch_bytes;
+    if (retired_buffers) *retired_buffers = (int)ctx->retired.size();
+    if (cached_schedules) *cached_schedules = (int)ctx->gqp_scheds.size();
+    if (live_graphs) *live_graphs = ctx->live_graphs;
     return 0;
 }
 

@@ -109,6 +109,8 @@ _SIGS = {
     "vx27_hip_d2h": (C.c_int, [VP, VP, VP, C.c_size_t]),
     "vx27_hip_d2d": (C.c_int, [VP, VP, VP, C.c_size_t]),
     "vx27_hip_memset": (C.c_int, [VP, VP, C.c_int, C.c_size_t]),
+    "vx27_hip_mem_info": (C.c_int, [VP, C.POINTER(C.c_size_t), C.POINTER(C.c_int), C.POINTER(C.c_int),
+                                    C.POINTER(C.c_int)]),
     "vx27_hip_bw_probe": (C.c_int, [VP, C.c_size_t, C.c_int, C.POINTER(C.c_double), C.POINTER(C.c_double)]),
     "vx27_hip_dn_decode": (C.c_int, [VP, C.POINTER(DnDesc)]),
     "vx27_hip_dn_prefill": (C.c_int, [VP, C.POINTER(DnPrefillDesc)]),
@@ -261,6 +263,12 @@ class Ctx:
 
     def sync(self):
         check(lib().vx27_hip_sync(self.h), "sync")
+
+    def mem_info(self):
+        """dict(scratch_bytes, retired, schedules, live_graphs) of the context."""
+        sb, r, sc, lg = C.c_size_t(), C.c_int(), C.c_int(), C.c_int()
+        check(lib().vx27_hip_mem_info(self.h, C.byref(sb), C.byref(r), C.byref(sc), C.byref(lg)), "mem_info")
+        return {"scratch_bytes": sb.value, "retired": r.value, "schedules": sc.value, "live_graphs": lg.value}
 
     def prof_enable(self, on=True):
         check(lib().vx27_hip_prof_enable(self.h, int(on)), "prof_enable")
