@@ -471,7 +471,8 @@ def _time_calls(ctx, fn, kernels, iters):
     return wall * 1e6, per
 
 
-DNP_KERNELS = ("dnp_glue_in", "dnp_conv_state", "dnp_prep3", "dnp_scan3", "dnp_prep", "dnp_scan", "dnp_out_gate")
+DNP_KERNELS = ("dnp_glue_in", "dnp_conv_state", "dnp_prept", "dnp_scant", "dnp_prep3", "dnp_scan3", "dnp_prep", "dnp_scan",
+               "dnp_out_gate")
 
 
 def dn_prefill_flops(T, H, hd=128, C_=64):

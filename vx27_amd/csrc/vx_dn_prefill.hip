@@ -403,7 +403,7 @@ struct ScanArgs {
 // 2w+1, 2 k-steps each), P (rows 16w.., 2 k-steps) and the wave's Ut block
 // of the slice -- and e^gam_C.  They come straight from the record into
 // registers, and each group takes the next chunk's loads as soon as its
-// MFMAs have read it (as in dnp_scan3, below).
+// MFMAs have read it (as in dnp_scant, below).
 constexpr int OPS_TILES = 15;
 
 __device__ __forceinline__ uint32_t ops_src(int j, int wave, int slice) {
@@ -522,7 +522,762 @@ __global__ __launch_bounds__(256) void dnp_scan(ScanArgs p) {
         for (int i = 0; i < 4; i++) Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + col] = S[r][i];
 }
 
-// ---- split precision (bf16x3) ----------------------------------------------
+// ---- split precision, T records (the default chunked form) ----------------
+// Every product of the chunk form enters the MFMAs as bf16 pairs, hi =
+// bf16(x) and lo = bf16(x - hi), summed as hi*hi + lo*hi + hi*lo (the lo*lo
+// term, ~2^-16 of the product, is dropped): about 16 significand bits per
+// operand, so the result stays within ~1e-5 of the fp32 recurrence instead
+// of bf16's ~1e-2.  Inputs that are exact in bf16 (no lo part) take two.
+//
+// With K, Q the raw k, q rows of a chunk and kn = diag(1/|k|) K,
+//   T' = (I + A)^-1 diag(beta),  Ut = T' V,  T'' = T' diag(sk),
+//   sk_t = e^gam_t / |k_t|,  skc_t = e^(gam_C - gam_t) / |k_t|,
+//   sq_t = e^gam_t / (|q_t| sqrt(128)),
+// the chunk step is
+//   U = Ut - T'' (K S0),
+//   O = diag(sq) Q S0 + P U,
+//   S = e^gam_C S0 + K^T diag(skc) U,
+// so the chunk record (dnp_prept) holds -T'' and P as hi/lo operand tiles,
+// Ut and the scales skc, sq, e^gam_C (65 KiB), and the raw K, Q and K^T
+// operand tiles are kept once per QK head.  This is the form of the glue's
+// inputs (q, k split into hi/lo pairs, v in fp32, nv = 3 nqk at the real
+// layer): its records are less than half the full form's and the QK head's
+// Gram products are shared by its value heads.  Masked tokens past the prompt have
+// beta = 0 and g = 0: their columns of T' (and rows, since their row of A is
+// zero) vanish, so whatever finite values their K, Q rows hold never reach
+// U, S or a stored output.
+constexpr size_t T_TH = 0;                 // -T'' hi: [4 rb][2 ks][64][8] bf16
+constexpr size_t T_TL = 8192;              // -T'' lo
+constexpr size_t T_PH = 16384;             // P hi
+constexpr size_t T_PL = 24576;             // P lo
+constexpr size_t T_UT = 32768;             // Ut fp32, C layout [4 rb][8 column blocks][64][4]
+constexpr size_t T_SC = 65536;             // float skc[64], sq[64], e^gam_C
+constexpr size_t TREC = T_SC + 1024;
+// K record of (sequence, QK head, chunk): the raw k, q rows as MFMA operand
+// tiles, 16 KiB each, hi parts then (with lo parts) lo parts:
+constexpr size_t K_KT = 0;                 // K^T [8 rb (key dims)][2 ks (tokens)][64][8] bf16
+constexpr size_t K_KA = 16384;             // K [4 rb (tokens)][4 dim blocks of 32][64][8]
+constexpr size_t K_QA = 32768;             // Q, as K
+constexpr size_t K_LO = 49152;             // offset of the lo parts
+
+struct PrepTArgs {
+    int T, nqk, nv, NC;
+    const uint16_t *q, *k;          // hi parts [B][T][nqk][128] bf16
+    const uint16_t *ql, *kl;        // lo parts as rows
+    const float *v;                 // [B][T][nv][128] fp32
+    const float *a, *b;             // [B][T][nv]
+    const float *A_log, *dt_bias;   // [nv]
+    char *rec;                      // [B][nv][NC] records of TREC bytes
+    char *krec;                     // [B][nqk][NC] K records of krec_bytes
+    int krec_bytes;
+};
+
+// bf16 hi and lo of 8 floats
+__device__ __forceinline__ void split8(const float *f, uint4 &hi, uint4 &lo) {
+    hi = pack8(f);
+    const uint16_t *h = (const uint16_t *)&hi;
+    float r[8];
+#pragma unroll
+    for (int e = 0; e < 8; e++) r[e] = f[e] - vx_bf16_to_f32(h[e]);
+    lo = pack8(r);
+}
+// bf16 hi, lo of 4 floats, as two packed uint2
+__device__ __forceinline__ void split4(const floatx4_t v, uint2 &h, uint2 &l) {
+    h = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
+    const uint16_t *hs = (const uint16_t *)&h;
+    l = make_uint2(pack2(v[0] - vx_bf16_to_f32(hs[0]), v[1] - vx_bf16_to_f32(hs[1])),
+                   pack2(v[2] - vx_bf16_to_f32(hs[2]), v[3] - vx_bf16_to_f32(hs[3])));
+}
+
+#define MFMA1(acc, a, b) acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, acc, 0, 0, 0)
+#define MFMA3(acc, ah, al, bh, bl) \
+    do {                           \
+        MFMA1(acc, ah, bh);        \
+        MFMA1(acc, al, bh);        \
+        MFMA1(acc, ah, bl);        \
+    } while (0)
+
+// Transpose a row-major [64 tokens][RP] bf16 tile (128 dims) into
+// [128 dims][TP] (64 tokens) with all 256 threads: thread (wave w, half h,
+// pair q) takes tokens 2q, 2q+1 and dims 32w + 2i + h (i < 16), and packs the
+// two tokens of a dim into one 32-bit LDS store (the halves of a wave write
+// neighbouring dims, whose rows start 36 banks apart).
+__device__ __forceinline__ void tr_rows(const uint16_t *src, uint16_t *dst, int tid) {
+    const int w = tid >> 6, h = (tid >> 5) & 1, q = tid & 31;
+    uint32_t r0[16], r1[16];
+#pragma unroll
+    for (int k = 0; k < 4; k++) {
+        const uint4 a0 = *(const uint4 *)&src[(2 * q) * RP + 32 * w + 8 * k];
+        const uint4 a1 = *(const uint4 *)&src[(2 * q + 1) * RP + 32 * w + 8 * k];
+        r0[4 * k] = a0.x; r0[4 * k + 1] = a0.y; r0[4 * k + 2] = a0.z; r0[4 * k + 3] = a0.w;
+        r1[4 * k] = a1.x; r1[4 * k + 1] = a1.y; r1[4 * k + 2] = a1.z; r1[4 * k + 3] = a1.w;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {
+        const uint32_t x = h ? r0[i] >> 16 : r0[i] & 0xffffu, y = h ? r1[i] >> 16 : r1[i] & 0xffffu;
+        *(uint32_t *)&dst[(32 * w + 2 * i + h) * TP + 2 * q] = x | (y << 16);
+    }
+}
+
+// Sum of a double over the 16 lanes of each 16-lane row (a fixed butterfly).
+__device__ __forceinline__ double row16_sum(double v) {
+#pragma unroll
+    for (int off = 1; off < 16; off <<= 1) v += __shfl_xor(v, off, 64);
+    return v;
+}
+
+// LDS of dnp_prept, 77 KiB (two workgroups a CU), four regions whose
+// contents change with the phase:
+//   R0: q rows [64][RP] bf16 -> K^T lo [128][TP] -> A [64][AP] fp32 -> V hi rows
+//   R1: k rows [64][RP] bf16 -> k lo rows -> T [64][64] fp32 -> V lo rows
+//   R2: K^T hi [128][TP] -> P hi, lo staging 2 x [64][TP] -> V^T hi [128][TP]
+//   R3: V^T lo [128][TP]
+constexpr int TN_REG = HD * TP * 2;
+constexpr int TN_R0 = 0;
+constexpr int TN_R1 = TN_R0 + TN_REG;
+constexpr int TN_R2 = TN_R1 + TN_REG;
+constexpr int TN_R3 = TN_R2 + TN_REG;
+constexpr int TN_MT = TN_R3 + TN_REG;              // level products [3][16][16] fp32
+constexpr int TN_GAM = TN_MT + 3 * 256 * 4;        // double gam[64]
+constexpr int TN_SC = TN_GAM + CH * 8;             // float beta, e^gam, e^(gamC-gam), 1/|q|, 1/|k| [64]
+constexpr int TN_TOTAL = TN_SC + 5 * CH * 4;
+static_assert(CH * RP * 2 <= TN_REG && CH * AP * 4 <= TN_REG && CH * 64 * 4 <= TN_REG && 2 * CH * TP * 2 <= TN_REG,
+              "regions hold rows, A, T and the P staging");
+static_assert(2 * TN_TOTAL <= 160 * 1024, "two workgroups per CU");
+
+// One workgroup per (chunk of 64 tokens, QK head, sequence); the value
+// heads that share the QK head (nv / nqk of them) reuse its Gram products:
+//   phase 1  q, k rows (hi to LDS; the lo parts from global memory where a
+//            product needs them), four rows per instruction (thread: row
+//            t/16 + 16 j, 8 dims), and 1/|q|, 1/|k| (double sums)
+//   phase 2  K K^T and Q K^T on MFMA (raw rows, norms applied after); the
+//            K^T operand tiles (hi, lo) into the K record
+//   then per value head:
+//   phase 3  gates and the cumulative log-decay (wave 0); the scales skc,
+//            sq; A = beta e^(gam_s - gam_r) kn_s.kn_r (r < s) in LDS;
+//            P = e^(gam_t - gam_s) qn_t.kn_s (s <= t) as hi/lo tiles
+//   phase 4  T = (I + A)^-1, blocked: the four 16x16 diagonal blocks by
+//            forward substitution, then T_ij = -T_ii sum_k A_ik T_kj level
+//            by level (fp32 MFMA)
+//   phase 5  T' = T diag(beta) (hi/lo in registers); -T'' = -T' diag(sk)
+//            as hi/lo tiles; V through LDS transposed, Ut = T' V on MFMA
+__global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
+    constexpr bool LO = true;   // (the glue's q, k, v always come with lo parts)
+    const int c = blockIdx.x, qh = blockIdx.y, b = blockIdx.z;
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, m = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool w2 = wave >= 2;
+    const int nr = p.nv / p.nqk;
+    const int t0 = c * CH;
+    const int nvalid = min(CH, p.T - t0);
+
+    __shared__ __attribute__((aligned(16))) char smem[TN_TOTAL];
+    uint16_t *q_rows = (uint16_t *)(smem + TN_R0), *kT_l = (uint16_t *)(smem + TN_R0);
+    float *A_s = (float *)(smem + TN_R0);
+    uint16_t *vh_rows = (uint16_t *)(smem + TN_R0);
+    uint16_t *k_rows = (uint16_t *)(smem + TN_R1), *vl_rows = (uint16_t *)(smem + TN_R1);
+    float *T_s = (float *)(smem + TN_R1);
+    uint16_t *kT_h = (uint16_t *)(smem + TN_R2);
+    uint16_t *P_h = (uint16_t *)(smem + TN_R2), *P_l = P_h + CH * TP;
+    uint16_t *vT_h = (uint16_t *)(smem + TN_R2), *vT_l = (uint16_t *)(smem + TN_R3);
+    float *M_t = (float *)(smem + TN_MT);
+    double *gam_s = (double *)(smem + TN_GAM);
+    float *beta_s = (float *)(smem + TN_SC), *eg_s = beta_s + CH, *egc_s = eg_s + CH;
+    float *iq_s = egc_s + CH, *ik_s = iq_s + CH;
+    const uint4 z4 = make_uint4(0u, 0u, 0u, 0u);
+    const int seg = tid & 15;   // 8-dim segment of a row (phase 1, V rows)
+
+    // ---- phase 1: k and q rows, thread (row tid/16 + 16 j, dims 8 seg ..)
+    uint4 kh[4], kl[4], qhv[4], qlv[4];
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int r = (tid >> 4) + 16 * j;
+        const size_t off = (((size_t)b * p.T + t0 + r) * p.nqk + qh) * HD + 8 * seg;
+        const bool ok = r < nvalid;
+        kh[j] = ok ? *(const uint4 *)(p.k + off) : z4;
+        qhv[j] = ok ? *(const uint4 *)(p.q + off) : z4;
+        kl[j] = (LO && ok) ? *(const uint4 *)(p.kl + off) : z4;
+        qlv[j] = (LO && ok) ? *(const uint4 *)(p.ql + off) : z4;
+    }
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int r = (tid >> 4) + 16 * j;
+        *(uint4 *)&k_rows[r * RP + 8 * seg] = kh[j];
+        *(uint4 *)&q_rows[r * RP + 8 * seg] = qhv[j];
+        double sk = 0.0, sq = 0.0;   // of the values hi + lo (exact in double)
+        const uint32_t kw[4] = {kh[j].x, kh[j].y, kh[j].z, kh[j].w}, klw[4] = {kl[j].x, kl[j].y, kl[j].z, kl[j].w};
+        const uint32_t qw[4] = {qhv[j].x, qhv[j].y, qhv[j].z, qhv[j].w},
+                       qlw[4] = {qlv[j].x, qlv[j].y, qlv[j].z, qlv[j].w};
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            const double k0 = (double)vx_bf16_to_f32((uint16_t)kw[e]) + (double)vx_bf16_to_f32((uint16_t)klw[e]);
+            const double k1 = (double)vx_bf16_to_f32((uint16_t)(kw[e] >> 16)) +
+                              (double)vx_bf16_to_f32((uint16_t)(klw[e] >> 16));
+            const double q0 = (double)vx_bf16_to_f32((uint16_t)qw[e]) + (double)vx_bf16_to_f32((uint16_t)qlw[e]);
+            const double q1 = (double)vx_bf16_to_f32((uint16_t)(qw[e] >> 16)) +
+                              (double)vx_bf16_to_f32((uint16_t)(qlw[e] >> 16));
+            sk = sk + k0 * k0;
+            sk = sk + k1 * k1;
+            sq = sq + q0 * q0;
+            sq = sq + q1 * q1;
+        }
+        sk = row16_sum(sk);
+        sq = row16_sum(sq);
+        if (seg == 0) {   // l2norm, vx27_deltanet.c:51-56
+            ik_s[r] = 1.0f / sqrtf((float)sk + 1e-6f);
+            iq_s[r] = 1.0f / sqrtf((float)sq + 1e-6f);
+        }
+    }
+    __syncthreads();
+    // the lo operands of the Gram products (global memory, issued now so that
+    // they arrive during the transposition): this wave's q and k rows (A) and
+    // the chunk's k rows (B) for every k-step; rows past the prompt give zeros
+    const int rowA = wave * 16 + m;
+    auto lo_row = [&](const uint16_t *base, int r, int d0) -> uint4 {
+        const size_t row = ((size_t)b * p.T + t0 + (r < nvalid ? r : 0)) * p.nqk + qh;
+        const u32x4_t v = *(g_u32x4 *)(base + row * HD + d0);
+        // masked by AND with an opaque mask: a select would let the compiler
+        // move the load under a branch, with a wait at its end
+        uint32_t mk = r < nvalid ? 0xffffffffu : 0u;
+        __asm__("" : "+v"(mk));
+        return make_uint4(v.x & mk, v.y & mk, v.z & mk, v.w & mk);
+    };
+    uint4 qal[4], kal[4], bkl[4][4];
+    if (LO) {
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            qal[ks] = lo_row(p.ql, rowA, 32 * ks + 8 * g);
+            kal[ks] = lo_row(p.kl, rowA, 32 * ks + 8 * g);
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++) bkl[nb][ks] = lo_row(p.kl, nb * 16 + m, 32 * ks + 8 * g);
+        }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    tr_rows(k_rows, kT_h, tid);   // K^T hi by all waves
+    __syncthreads();
+
+    // ---- phase 2: K K^T and Q K^T (hi*hi + lo*hi + hi*lo)
+    floatx4_t acck[4], accq[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; nb++) {
+        acck[nb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+        accq[nb] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ks++) {
+        const int d0 = 32 * ks + 8 * g;
+        const bf16x8_t qa = as_bf16x8(*(const uint4 *)&q_rows[rowA * RP + d0]);
+        const bf16x8_t ka = as_bf16x8(*(const uint4 *)&k_rows[rowA * RP + d0]);
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) {
+            const bf16x8_t bk = as_bf16x8(*(const uint4 *)&k_rows[(nb * 16 + m) * RP + d0]);
+            MFMA1(acck[nb], ka, bk);
+            MFMA1(accq[nb], qa, bk);
+            if (LO) {
+                const bf16x8_t bklo = as_bf16x8(bkl[nb][ks]);
+                MFMA1(acck[nb], as_bf16x8(kal[ks]), bk);
+                MFMA1(acck[nb], ka, bklo);
+                MFMA1(accq[nb], as_bf16x8(qal[ks]), bk);
+                MFMA1(accq[nb], qa, bklo);
+            }
+        }
+    }
+    // the K record: K^T operand tiles (rows = key dims in 8 blocks, k =
+    // tokens in 2 steps) and the K and Q operand tiles (rows = tokens, k =
+    // one 32-dim block), four of each a wave
+    char *kr = p.krec + (((size_t)b * p.nqk + qh) * p.NC + c) * p.krec_bytes;
+#pragma unroll
+    for (int j = 0; j < 4; j++) {
+        const int tile = wave * 4 + j, rb = tile >> 1, ks = tile & 1;
+        const int tr = tile >> 2, db = tile & 3;
+        const size_t o = ((size_t)tile * 64 + lane) * 16;
+        *(uint4 *)(kr + K_KT + o) = *(const uint4 *)&kT_h[(rb * 16 + m) * TP + 32 * ks + 8 * g];
+        *(uint4 *)(kr + K_KA + o) = *(const uint4 *)&k_rows[(tr * 16 + m) * RP + 32 * db + 8 * g];
+        *(uint4 *)(kr + K_QA + o) = *(const uint4 *)&q_rows[(tr * 16 + m) * RP + 32 * db + 8 * g];
+    }
+    __syncthreads();   // the rows and K^T hi are read out
+    if (LO) {          // the lo parts: k lo rows through R1 (K^T lo transposed into R0), then q lo rows
+#pragma unroll
+        for (int j = 0; j < 4; j++) *(uint4 *)&k_rows[((tid >> 4) + 16 * j) * RP + 8 * seg] = kl[j];
+        __syncthreads();
+        tr_rows(k_rows, kT_l, tid);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int tile = wave * 4 + j, tr = tile >> 2, db = tile & 3;
+            *(uint4 *)(kr + K_LO + K_KA + ((size_t)tile * 64 + lane) * 16) =
+                *(const uint4 *)&k_rows[(tr * 16 + m) * RP + 32 * db + 8 * g];
+        }
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int tile = wave * 4 + j, rb = tile >> 1, ks = tile & 1;
+            *(uint4 *)(kr + K_LO + K_KT + ((size_t)tile * 64 + lane) * 16) =
+                *(const uint4 *)&kT_l[(rb * 16 + m) * TP + 32 * ks + 8 * g];
+        }
+#pragma unroll
+        for (int j = 0; j < 4; j++) *(uint4 *)&k_rows[((tid >> 4) + 16 * j) * RP + 8 * seg] = qlv[j];
+        __syncthreads();
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int tile = wave * 4 + j, tr = tile >> 2, db = tile & 3;
+            *(uint4 *)(kr + K_LO + K_QA + ((size_t)tile * 64 + lane) * 16) =
+                *(const uint4 *)&k_rows[(tr * 16 + m) * RP + 32 * db + 8 * g];
+        }
+        __syncthreads();   // R0 and R1 are free
+    }
+
+    const float qscale = 1.0f / sqrtf((float)HD);
+    for (int jv = 0; jv < nr; jv++) {
+        const int vh = qh * nr + jv;
+        // ---- phase 3: gates and the cumulative log-decay (wave 0, lane =
+        // token); masked tokens get beta = 0 and g = 0
+        if (wave == 0) {
+            double beta = 0.0, glog = 0.0;
+            if (lane < nvalid) {
+                const size_t e = ((size_t)b * p.T + t0 + lane) * p.nv + vh;
+                beta = 1.0 / (1.0 + exp(-(double)p.b[e]));
+                glog = -exp((double)p.A_log[vh]) * softplus_d((double)p.a[e] + (double)p.dt_bias[vh]);
+            }
+            double sc = glog;
+#pragma unroll
+            for (int off = 1; off < 64; off <<= 1) {
+                const double o = __shfl_up(sc, off, 64);
+                if (lane >= off) sc += o;
+            }
+            const double sC = __shfl(sc, 63, 64);
+            gam_s[lane] = sc;
+            beta_s[lane] = (float)beta;
+            eg_s[lane] = (float)exp(sc);
+            egc_s[lane] = (float)exp(sC - sc);
+        }
+        __syncthreads();
+        char *rec = p.rec + (((size_t)b * p.nv + vh) * p.NC + c) * TREC;
+        if (wave == 1) {   // the walk's per-token scales
+            float *sc = (float *)(rec + T_SC);
+            sc[lane] = egc_s[lane] * ik_s[lane];
+            sc[64 + lane] = eg_s[lane] * (iq_s[lane] * qscale);
+            if (lane == 0) sc[128] = (float)exp(gam_s[CH - 1]);
+        }
+        // A (fp32) and P hi/lo staging: the per-token scalars of this lane's
+        // rows s and columns r in one batch of LDS reads, then 16 elements
+        // with no branch (the masked ones selected away)
+        double gs[4], gr[4];
+        float bs[4], iks[4], iqs[4], ikr[4];
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+            const int s = wave * 16 + 4 * g + i, r = i * 16 + m;
+            gs[i] = gam_s[s];
+            bs[i] = beta_s[s];
+            iks[i] = ik_s[s];
+            iqs[i] = iq_s[s] * qscale;
+            gr[i] = gam_s[r];
+            ikr[i] = ik_s[r];
+        }
+#pragma unroll
+        for (int nb = 0; nb < 4; nb++) {
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const int s = wave * 16 + 4 * g + i, r = nb * 16 + m;
+                const float e = expf((float)(gs[i] - gr[nb]));   // masked when r > s (may be inf there)
+                const float ed = r <= s ? e : 0.0f;
+                const float av = bs[i] * ed * ((iks[i] * ikr[nb]) * acck[nb][i]);
+                A_s[s * AP + r] = r < s ? av : 0.0f;
+                const float pv = ed * ((iqs[i] * ikr[nb]) * accq[nb][i]);
+                const uint16_t ph = vx_f32_to_bf16(pv);
+                P_h[s * TP + r] = ph;
+                P_l[s * TP + r] = vx_f32_to_bf16(pv - vx_bf16_to_f32(ph));
+            }
+        }
+        __syncthreads();
+        // P operand tiles (row block wave, 2 k-steps) out of the staging
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const size_t o = ((size_t)(wave * 2 + ks) * 64 + lane) * 16;
+            *(uint4 *)(rec + T_PH + o) = *(const uint4 *)&P_h[rowA * TP + 32 * ks + 8 * g];
+            *(uint4 *)(rec + T_PL + o) = *(const uint4 *)&P_l[rowA * TP + 32 * ks + 8 * g];
+        }
+        // ---- phase 4: T = (I + A)^-1; the diagonal blocks, one lane per column
+        if (tid < 64) {
+            const int bi = tid >> 4, cc = tid & 15, o = 16 * bi;
+            float t[16];
+#pragma unroll
+            for (int r = 0; r < 16; r++) {
+                float acc = r == cc ? 1.0f : 0.0f;
+#pragma unroll
+                for (int k = 0; k < r; k++) acc -= A_s[(o + r) * AP + o + k] * t[k];
+                t[r] = acc;
+            }
+#pragma unroll
+            for (int r = 0; r < 16; r++) T_s[(o + r) * 64 + o + cc] = t[r];
+        }
+        __syncthreads();
+        float *Mw = M_t + (wave < 3 ? wave : 0) * 256;
+#pragma unroll
+        for (int lev = 1; lev < 4; lev++) {
+            if (wave < 4 - lev) {
+                const int j = wave, i = j + lev;
+                floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
+                for (int kb = j; kb < i; kb++) {
+#pragma unroll
+                    for (int k0 = 0; k0 < 16; k0 += 4) {
+                        const float av = A_s[(16 * i + m) * AP + 16 * kb + k0 + g];
+                        const float bv = T_s[(16 * kb + k0 + g) * 64 + 16 * j + m];
+                        acc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, acc, 0, 0, 0);
+                    }
+                }
+#pragma unroll
+                for (int ii = 0; ii < 4; ii++) Mw[(4 * g + ii) * 16 + m] = acc[ii];
+                asm volatile("" ::: "memory");
+                floatx4_t tacc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int k0 = 0; k0 < 16; k0 += 4) {
+                    const float av = T_s[(16 * i + m) * 64 + 16 * i + k0 + g];
+                    const float bv = Mw[(k0 + g) * 16 + m];
+                    tacc = __builtin_amdgcn_mfma_f32_16x16x4f32(av, bv, tacc, 0, 0, 0);
+                }
+#pragma unroll
+                for (int ii = 0; ii < 4; ii++) T_s[(16 * i + 4 * g + ii) * 64 + 16 * j + m] = -tacc[ii];
+            }
+            __syncthreads();
+        }
+        // ---- phase 5: T' = T diag(beta), row block wave, in registers (the
+        // upper blocks of T hold stale bytes: selected away); -T'' tiles
+        bf16x8_t tph[2], tpl[2];
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++) {
+            const int s = wave * 16 + m, r0 = 32 * ks + 8 * g;
+            float tr[8], bt[8], eg[8], ik[8];
+            *(float4 *)&tr[0] = *(const float4 *)&T_s[s * 64 + r0];
+            *(float4 *)&tr[4] = *(const float4 *)&T_s[s * 64 + r0 + 4];
+            *(float4 *)&bt[0] = *(const float4 *)&beta_s[r0];
+            *(float4 *)&bt[4] = *(const float4 *)&beta_s[r0 + 4];
+            *(float4 *)&eg[0] = *(const float4 *)&eg_s[r0];
+            *(float4 *)&eg[4] = *(const float4 *)&eg_s[r0 + 4];
+            *(float4 *)&ik[0] = *(const float4 *)&ik_s[r0];
+            *(float4 *)&ik[4] = *(const float4 *)&ik_s[r0 + 4];
+            float f[8], f2[8];
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                f[e] = (r0 + e <= s ? tr[e] : 0.0f) * bt[e];
+                f2[e] = -(f[e] * (eg[e] * ik[e]));
+            }
+            uint4 h, l;
+            split8(f, h, l);
+            tph[ks] = as_bf16x8(h);
+            tpl[ks] = as_bf16x8(l);
+            split8(f2, h, l);
+            const size_t o = ((size_t)(wave * 2 + ks) * 64 + lane) * 16;
+            *(uint4 *)(rec + T_TH + o) = h;
+            *(uint4 *)(rec + T_TL + o) = l;
+        }
+        __syncthreads();   // A, T and the P staging are read out
+        // V rows (hi to R0, with LO the lo parts of the fp32 values to R1),
+        // thread (row tid/16 + 16 j, 8 columns), then transposed
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = (tid >> 4) + 16 * j;
+            const bool ok = r < nvalid;
+            const size_t off = (((size_t)b * p.T + t0 + r) * p.nv + vh) * HD + 8 * seg;
+            const float *vf = p.v + off;
+            const float4 a0 = ok ? *(const float4 *)vf : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float4 a1 = ok ? *(const float4 *)(vf + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+            const float f[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+            uint4 h, l;
+            split8(f, h, l);
+            *(uint4 *)&vh_rows[r * RP + 8 * seg] = h;
+            *(uint4 *)&vl_rows[r * RP + 8 * seg] = l;
+        }
+        __syncthreads();
+        tr_rows(vh_rows, vT_h, tid);
+        tr_rows(vl_rows, vT_l, tid);
+        __syncthreads();
+        // Ut = T' V, row block wave, as C-layout tiles per 16-column block
+#pragma unroll
+        for (int cb = 0; cb < 8; cb++) {
+            floatx4_t u0 = {0.f, 0.f, 0.f, 0.f}, u1 = {0.f, 0.f, 0.f, 0.f};
+            const int col = cb * 16 + m;
+            {
+                const bf16x8_t vb = as_bf16x8(*(const uint4 *)&vT_h[col * TP + 8 * g]);
+                MFMA1(u0, tph[0], vb);
+                MFMA1(u0, tpl[0], vb);
+                if (LO) MFMA1(u0, tph[0], as_bf16x8(*(const uint4 *)&vT_l[col * TP + 8 * g]));
+            }
+            if (w2) {
+                const bf16x8_t vb = as_bf16x8(*(const uint4 *)&vT_h[col * TP + 32 + 8 * g]);
+                MFMA1(u1, tph[1], vb);
+                MFMA1(u1, tpl[1], vb);
+                if (LO) MFMA1(u1, tph[1], as_bf16x8(*(const uint4 *)&vT_l[col * TP + 32 + 8 * g]));
+            }
+            *(floatx4_t *)(rec + T_UT + ((size_t)(wave * 8 + cb) * 64 + lane) * 16) = u0 + u1;
+        }
+        __syncthreads();   // before the next value head rewrites the LDS
+    }
+}
+
+struct ScanTArgs {
+    int T, nqk, nv, NC, xcd_map;
+    const uint16_t *q, *k;          // hi parts [B][T][nqk][128] bf16
+    const uint16_t *ql, *kl;        // lo parts as rows (LO)
+    const char *rec, *krec;
+    int krec_bytes;
+    float *S;                       // [B][nv][128][128]
+    float *out;                     // [B][T][nv][128]
+};
+
+// dnp_scant: the walk over the chunks of one value head.  A workgroup owns
+// NCB blocks of 16 state columns (columns are independent in every
+// product), wave w the state rows 32w .. 32w+31 of each block.  Per chunk:
+//   the wave's S rows become the MFMA operand of its 32 key dims by two
+//   lane swaps (no LDS); partial K S and (Q S)^T over those dims for all 64
+//   tokens go to LDS;
+//   [barrier] U = Ut - T'' sum(K S) for the wave's tokens 16w .. 16w+15,
+//   and skc U, to LDS (hi/lo); the wave's rows of sum (Q S)^T are read now;
+//   [barrier] S = e^gam_C S + K^T (skc U) for the wave's rows, and
+//   O^T = sq (Q S)^T + U^T P^T for its tokens, stored 16 bytes a lane.
+// Each wave loads its operands straight into registers (K and Q from the
+// inputs, the rest from the records); each group takes the next chunk's
+// loads as soon as its last MFMA has read it.  T'' and P vanish above the
+// diagonal, so waves 0 and 1 skip their second k-step of both.
+typedef const __attribute__((address_space(1))) floatx4_t g_floatx4;
+template <int NCB>
+__global__ __launch_bounds__(256) void dnp_scant(ScanTArgs p) {
+    constexpr bool LO = true;
+    constexpr int NSL = NSLICE / NCB;
+    constexpr int KR = CH + 4, QR = 20;   // padded rows of the partial sums (floats)
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const bool w2 = wave >= 2;
+    const int b = blockIdx.y, bid = blockIdx.x;
+    const int nr = p.nv / p.nqk;
+    int vh, slice;
+    if (p.xcd_map) {   // the value heads of a QK head, all their slices, on one XCD
+        const int xcd = bid & 7, idx = bid >> 3, per = nr * NSL;
+        const int qh = (idx / per) * 8 + xcd, rem = idx % per;
+        vh = qh * nr + rem / NSL;
+        slice = rem % NSL;
+    } else {
+        vh = bid / NSL;
+        slice = bid % NSL;
+    }
+    const int qh = vh / nr;
+    const int cb0 = slice * NCB;
+
+    __shared__ __attribute__((aligned(16))) float KSp[4][NCB][16][KR];   // partial K S [wave][block][column][token]
+    __shared__ __attribute__((aligned(16))) float QSp[4][NCB][CH][QR];   // partial (Q S)^T [wave][block][token][column]
+    __shared__ __attribute__((aligned(16))) uint16_t U_h[NCB][16][CH + 8], U_l[NCB][16][CH + 8];
+    __shared__ __attribute__((aligned(16))) uint16_t W_h[NCB][16][CH + 8], W_l[NCB][16][CH + 8];
+
+    const char *rec0 = vx_uniform_ptr(p.rec + ((size_t)b * p.nv + vh) * p.NC * TREC);
+    const char *krec0 = vx_uniform_ptr(p.krec + ((size_t)b * p.nqk + qh) * p.NC * p.krec_bytes);
+
+    // operand registers of one chunk
+    uint4 kA[4], qA[4], kAl[4], qAl[4];     // K, Q tiles: rows 16 rb + n, dims 32w + 8g .. (4 row blocks)
+    uint4 tp[2][2], pp[2][2];               // -T'', P row block w [k-step][hi, lo]
+    uint4 kt[2][2], ktl[2][2];              // K^T row blocks 2w, 2w+1 [rb][k-step], hi and lo
+    floatx4_t ut[NCB], skc4;
+    float sqv, gc;
+    auto rec_of = [&](int cc) { return rec0 + (size_t)cc * TREC; };
+    auto ld_tile = [&](const char *base, size_t off) -> uint4 {
+        const u32x4_t v = *(g_u32x4 *)(base + off + (size_t)lane * 16);
+        return make_uint4(v.x, v.y, v.z, v.w);
+    };
+    auto ld_kq = [&](int cc) {
+        const char *kr = krec0 + (size_t)cc * p.krec_bytes;
+#pragma unroll
+        for (int rb = 0; rb < 4; rb++) {
+            const size_t o = (size_t)(rb * 4 + wave) * 1024;
+            kA[rb] = ld_tile(kr, K_KA + o);
+            qA[rb] = ld_tile(kr, K_QA + o);
+            if (LO) {
+                kAl[rb] = ld_tile(kr, K_LO + K_KA + o);
+                qAl[rb] = ld_tile(kr, K_LO + K_QA + o);
+            }
+        }
+    };
+    auto ld_u = [&](int cc) {
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+            if (ks == 0 || w2) {
+                tp[ks][0] = ld_tile(rec_of(cc), T_TH + (size_t)(wave * 2 + ks) * 1024);
+                tp[ks][1] = ld_tile(rec_of(cc), T_TL + (size_t)(wave * 2 + ks) * 1024);
+            }
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++)
+            ut[cb] = *(g_floatx4 *)(rec_of(cc) + T_UT + ((size_t)(wave * 8 + cb0 + cb) * 64 + lane) * 16);
+        skc4 = *(g_floatx4 *)(rec_of(cc) + T_SC + (16 * wave + 4 * g) * 4);
+    };
+    auto ld_s = [&](int cc) {
+        const char *kr = krec0 + (size_t)cc * p.krec_bytes;
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                kt[r][ks] = ld_tile(kr, K_KT + (size_t)((2 * wave + r) * 2 + ks) * 1024);
+                if (LO) ktl[r][ks] = ld_tile(kr, K_LO + K_KT + (size_t)((2 * wave + r) * 2 + ks) * 1024);
+            }
+#pragma unroll
+        for (int ks = 0; ks < 2; ks++)
+            if (ks == 0 || w2) {
+                pp[ks][0] = ld_tile(rec_of(cc), T_PH + (size_t)(wave * 2 + ks) * 1024);
+                pp[ks][1] = ld_tile(rec_of(cc), T_PL + (size_t)(wave * 2 + ks) * 1024);
+            }
+        sqv = *(g_float *)(rec_of(cc) + T_SC + 256 + (16 * wave + n) * 4);
+        gc = *(g_float *)(rec_of(cc) + T_SC + 512);
+    };
+    // The state first, waited for here: the loop head joins this path and the
+    // loop's back edge, and a load still pending on either path would make
+    // every iteration wait there for the loads of the step before.
+    float *Sg = p.S + ((size_t)b * p.nv + vh) * HD * HD;
+    floatx4_t S[NCB][2];
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                S[cb][r][i] = Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + (cb0 + cb) * 16 + n];
+    __builtin_amdgcn_s_waitcnt(0x0F70);   // vmcnt(0)
+    ld_kq(0);
+    ld_u(0);
+    ld_s(0);
+
+    const floatx4_t z = {0.f, 0.f, 0.f, 0.f};
+    for (int c = 0; c < p.NC; c++) {
+        const int nx = min(c + 1, p.NC - 1);   // (the last chunk again after the end: never used)
+        // the wave's S rows as the B operand of its 32 dims: lane (g, n)
+        // takes dims 8g .. 8g+7 of column n from the two C tiles (rows 4g'+i
+        // of lane group g') by a 32-lane and a 16-lane swap
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++) {
+            float e[8];
+#pragma unroll
+            for (int i = 0; i < 4; i++) {
+                const auto r1 = __builtin_amdgcn_permlane32_swap(__float_as_uint(S[cb][0][i]),
+                                                                 __float_as_uint(S[cb][1][i]), false, false);
+                const auto r2 = __builtin_amdgcn_permlane16_swap(r1[0], r1[1], false, false);
+                e[i] = __uint_as_float(r2[0]);
+                e[4 + i] = __uint_as_float(r2[1]);
+            }
+            uint4 h, l;
+            split8(e, h, l);
+            const bf16x8_t sh = as_bf16x8(h), sl = as_bf16x8(l);
+#pragma unroll
+            for (int rb = 0; rb < 4; rb++) {
+                floatx4_t ks = z, qs = z;
+                MFMA1(ks, as_bf16x8(kA[rb]), sh);
+                MFMA1(qs, sh, as_bf16x8(qA[rb]));
+                MFMA1(ks, as_bf16x8(kA[rb]), sl);
+                MFMA1(qs, sl, as_bf16x8(qA[rb]));
+                if (LO) {
+                    MFMA1(ks, as_bf16x8(kAl[rb]), sh);
+                    MFMA1(qs, sh, as_bf16x8(qAl[rb]));
+                }
+                *(floatx4_t *)&KSp[wave][cb][n][16 * rb + 4 * g] = ks;
+                *(floatx4_t *)&QSp[wave][cb][16 * rb + n][4 * g] = qs;
+            }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        ld_kq(nx);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        // U = Ut - T'' K S of the wave's tokens; skc U; the wave's (Q S)^T
+        floatx4_t qsum[NCB];
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++) {
+            bf16x8_t xh[2], xl[2];
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++)
+                if (ks == 0 || w2) {
+                    float f[8];
+                    floatx4_t a0 = *(const floatx4_t *)&KSp[0][cb][n][32 * ks + 8 * g];
+                    floatx4_t a1 = *(const floatx4_t *)&KSp[0][cb][n][32 * ks + 8 * g + 4];
+#pragma unroll
+                    for (int w = 1; w < 4; w++) {
+                        a0 += *(const floatx4_t *)&KSp[w][cb][n][32 * ks + 8 * g];
+                        a1 += *(const floatx4_t *)&KSp[w][cb][n][32 * ks + 8 * g + 4];
+                    }
+#pragma unroll
+                    for (int i = 0; i < 4; i++) {
+                        f[i] = a0[i];
+                        f[4 + i] = a1[i];
+                    }
+                    uint4 h, l;
+                    split8(f, h, l);
+                    xh[ks] = as_bf16x8(h);
+                    xl[ks] = as_bf16x8(l);
+                }
+            floatx4_t u0 = ut[cb], u1 = z;
+            MFMA3(u0, as_bf16x8(tp[0][0]), as_bf16x8(tp[0][1]), xh[0], xl[0]);
+            if (w2) MFMA3(u1, as_bf16x8(tp[1][0]), as_bf16x8(tp[1][1]), xh[1], xl[1]);
+            const floatx4_t U = u0 + u1;
+            uint2 h, l;
+            split4(U, h, l);
+            *(uint2 *)&U_h[cb][n][16 * wave + 4 * g] = h;
+            *(uint2 *)&U_l[cb][n][16 * wave + 4 * g] = l;
+            split4(U * skc4, h, l);
+            *(uint2 *)&W_h[cb][n][16 * wave + 4 * g] = h;
+            *(uint2 *)&W_l[cb][n][16 * wave + 4 * g] = l;
+            floatx4_t qq = *(const floatx4_t *)&QSp[0][cb][16 * wave + n][4 * g];
+#pragma unroll
+            for (int w = 1; w < 4; w++) qq += *(const floatx4_t *)&QSp[w][cb][16 * wave + n][4 * g];
+            qsum[cb] = qq;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        ld_u(nx);
+        __builtin_amdgcn_sched_barrier(0);
+        __syncthreads();
+        // S = e^gam_C S + K^T (skc U);  O^T = sq (Q S)^T + U^T P^T
+#pragma unroll
+        for (int cb = 0; cb < NCB; cb++) {
+            bf16x8_t uh[2], ul[2], wh[2], wl[2];
+#pragma unroll
+            for (int ks = 0; ks < 2; ks++) {
+                uh[ks] = as_bf16x8(*(const uint4 *)&U_h[cb][n][32 * ks + 8 * g]);
+                ul[ks] = as_bf16x8(*(const uint4 *)&U_l[cb][n][32 * ks + 8 * g]);
+                wh[ks] = as_bf16x8(*(const uint4 *)&W_h[cb][n][32 * ks + 8 * g]);
+                wl[ks] = as_bf16x8(*(const uint4 *)&W_l[cb][n][32 * ks + 8 * g]);
+            }
+#pragma unroll
+            for (int r = 0; r < 2; r++) {
+                floatx4_t sa = S[cb][r] * gc, sb = z;
+                MFMA1(sa, as_bf16x8(kt[r][0]), wh[0]);
+                MFMA1(sb, as_bf16x8(kt[r][1]), wh[1]);
+                MFMA1(sa, as_bf16x8(kt[r][0]), wl[0]);
+                MFMA1(sb, as_bf16x8(kt[r][1]), wl[1]);
+                if (LO) {
+                    MFMA1(sa, as_bf16x8(ktl[r][0]), wh[0]);
+                    MFMA1(sb, as_bf16x8(ktl[r][1]), wh[1]);
+                }
+                S[cb][r] = sa + sb;
+            }
+            floatx4_t o0 = qsum[cb] * sqv, o1 = z;
+            MFMA3(o0, uh[0], ul[0], as_bf16x8(pp[0][0]), as_bf16x8(pp[0][1]));
+            if (w2) MFMA3(o1, uh[1], ul[1], as_bf16x8(pp[1][0]), as_bf16x8(pp[1][1]));
+            const int tt = c * CH + 16 * wave + n;
+            if (tt < p.T)
+                *(floatx4_t *)(p.out + (((size_t)b * p.T + tt) * p.nv + vh) * HD + (cb0 + cb) * 16 + 4 * g) = o0 + o1;
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        ld_s(nx);
+        __builtin_amdgcn_sched_barrier(0);
+    }
+#pragma unroll
+    for (int cb = 0; cb < NCB; cb++)
+#pragma unroll
+        for (int r = 0; r < 2; r++)
+#pragma unroll
+            for (int i = 0; i < 4; i++)
+                Sg[(size_t)((2 * wave + r) * 16 + 4 * g + i) * HD + (cb0 + cb) * 16 + n] = S[cb][r][i];
+}
+
+// ---- split precision, full records (bf16 inputs without the glue) --------
+// The form for inputs that are exact in bf16: the preparation writes every
+// operand of the walk (-W, e^gam Q, Kt^T, P as hi/lo tiles, Ut), 144 KiB per
+// (chunk, value head), and the walk has two LDS hand-offs per chunk (S, U).
+// With q, k, v exact in bf16 these records stay in L2 across the head's
+// column slices, and the walk's lighter LDS traffic makes it the faster one;
+// the T-record form above wins once the glue's lo parts and 48 value heads
+// make the records large.
 // The default chunked form: every operand of the chunk products enters the
 // MFMAs as a pair of bf16 values, hi = bf16(x) and lo = bf16(x - hi), and
 // each product is hi*hi + lo*hi + hi*lo (the lo*lo term, ~2^-16 of the
@@ -550,15 +1305,6 @@ struct Prep3Args {
     char *rec;                          // [B][nv][NC] records of XREC bytes
 };
 
-// bf16 hi and lo of 8 floats
-__device__ __forceinline__ void split8(const float *f, uint4 &hi, uint4 &lo) {
-    hi = pack8(f);
-    const uint16_t *h = (const uint16_t *)&hi;
-    float r[8];
-#pragma unroll
-    for (int e = 0; e < 8; e++) r[e] = f[e] - vx_bf16_to_f32(h[e]);
-    lo = pack8(r);
-}
 
 // LDS of dnp_prep3 (phases as dnp_prep's), 76.5 KiB, so two workgroups
 // share a CU: four regions whose contents change with the phase.  The lo
@@ -576,27 +1322,6 @@ static_assert(CH * 64 * 4 <= CH * RP * 2 && CH * TP * 2 <= HD * TP * 2 && CH * R
               "T, P and -W staging fit their regions");
 static_assert(2 * XN_TOTAL <= 160 * 1024, "two workgroups per CU");
 
-// Transpose a row-major [64 tokens][RP] bf16 tile (128 dims) into
-// [128 dims][TP] (64 tokens) with all 256 threads: thread (wave w, half h,
-// pair q) takes tokens 2q, 2q+1 and dims 32w + 2i + h (i < 16), and packs the
-// two tokens of a dim into one 32-bit LDS store (the halves of a wave write
-// neighbouring dims, whose rows start 36 banks apart).
-__device__ __forceinline__ void tr_rows(const uint16_t *src, uint16_t *dst, int tid) {
-    const int w = tid >> 6, h = (tid >> 5) & 1, q = tid & 31;
-    uint32_t r0[16], r1[16];
-#pragma unroll
-    for (int k = 0; k < 4; k++) {
-        const uint4 a0 = *(const uint4 *)&src[(2 * q) * RP + 32 * w + 8 * k];
-        const uint4 a1 = *(const uint4 *)&src[(2 * q + 1) * RP + 32 * w + 8 * k];
-        r0[4 * k] = a0.x; r0[4 * k + 1] = a0.y; r0[4 * k + 2] = a0.z; r0[4 * k + 3] = a0.w;
-        r1[4 * k] = a1.x; r1[4 * k + 1] = a1.y; r1[4 * k + 2] = a1.z; r1[4 * k + 3] = a1.w;
-    }
-#pragma unroll
-    for (int i = 0; i < 16; i++) {
-        const uint32_t x = h ? r0[i] >> 16 : r0[i] & 0xffffu, y = h ? r1[i] >> 16 : r1[i] & 0xffffu;
-        *(uint32_t *)&dst[(32 * w + 2 * i + h) * TP + 2 * q] = x | (y << 16);
-    }
-}
 
 // LO: the inputs come with lo parts (the glue's fp32 values as bf16 pairs),
 // read from global memory where a product or an operand tile takes them;
@@ -998,20 +1723,7 @@ __device__ __forceinline__ void x3_load(const char *rec, int wave, int slice, in
     }
 }
 
-// bf16 hi, lo of 4 floats, as two packed uint2
-__device__ __forceinline__ void split4(const floatx4_t v, uint2 &h, uint2 &l) {
-    h = make_uint2(pack2(v[0], v[1]), pack2(v[2], v[3]));
-    const uint16_t *hs = (const uint16_t *)&h;
-    l = make_uint2(pack2(v[0] - vx_bf16_to_f32(hs[0]), v[1] - vx_bf16_to_f32(hs[1])),
-                   pack2(v[2] - vx_bf16_to_f32(hs[2]), v[3] - vx_bf16_to_f32(hs[3])));
-}
 
-#define MFMA3(acc, ah, al, bh, bl)                                              \
-    do {                                                                        \
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bh, acc, 0, 0, 0);    \
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(al, bh, acc, 0, 0, 0);    \
-        acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(ah, bl, acc, 0, 0, 0);    \
-    } while (0)
 
 // NCB column blocks of 16 per workgroup (NSLICE / NCB workgroups per head):
 // the A operands (-W, e^gam Q, Kt^T, P) a wave loads serve all NCB blocks,
@@ -1185,14 +1897,10 @@ __global__ __launch_bounds__(256) void dnp_scan3(ScanArgs p) {
 // pre-norms the flags ask for -- rmsn(x)(1+w) (vx27_qfwd.c:32-39, 123) and
 // l2norm with q/sqrt(128) (:124-130), sums in double -- and the result as
 // bf16 hi (and lo) for the chunked products (whose prep applies step_exact's
-// own l2norm and scale once more, as the reference does).
-// The lo parts (split form) go to the layouts the chunk prep reads them in:
-// q and k lo as rows, k and v lo also transposed, [B][head][128 dims][Tp
-// tokens] with Tp the prompt padded to whole chunks (8 tokens of a dim are
-// one 16-byte store; the blocks past T write the padding's zeros).
-// The four waves of a workgroup take four consecutive token blocks of one
-// head, so a dim's transposed lo run of 32 tokens is written by one CU.
-// grid (ceil(Tp/GT/4) with lo parts, else ceil(T/GT/4), heads, B), block 256.
+// own l2norm and scale once more, as the reference does).  In the split
+// form q and k also get their lo parts as rows, and v is kept in fp32 (the
+// walk subtracts from it in fp32 and never multiplies it on MFMA).
+// grid (ceil(T/GT/4), heads, B), block 256.
 constexpr int GT = 8;
 struct GlueInArgs {
     int B, T, nqk, nv, C;
@@ -1203,28 +1911,17 @@ struct GlueInArgs {
     const void *conv_w;
     const uint16_t *q, *k, *v; // bf16 inputs without VX27_DN_CONV
     const float *norm_w;       // [128]
-    uint16_t *qo, *ko, *vo;    // bf16 [B][T][nqk|nqk|nv][128]
+    uint16_t *qo, *ko, *vo;    // bf16 [B][T][nqk|nqk|nv][128] (vo: without vo32)
     uint16_t *qol, *kol;       // lo parts (x - bf16(x)) of q, k as rows, or NULL
-    uint16_t *klT, *vlT;       // lo parts of k, v transposed, [B][nqk|nv][128][Tp]
-    int Tp;
+    float *vo32;               // v as fp32 rows [B][T][nv][128], or NULL
 };
 __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
     const int wave = threadIdx.x >> 6, lane = threadIdx.x & 63;
     const int hh = blockIdx.y, b = blockIdx.z, t0 = (blockIdx.x * 4 + wave) * GT;
-    if (t0 >= (a.qol ? a.Tp : a.T)) return;
+    if (t0 >= a.T) return;
     const bool is_q = hh < a.nqk, is_k = !is_q && hh < 2 * a.nqk;
-    // transposed lo rows of this head's two dims (k and v heads)
-    uint16_t *tl = nullptr;
-    if (a.qol && !is_q)
-        tl = is_k ? a.klT + ((size_t)b * a.nqk + (hh - a.nqk)) * HD * a.Tp
-                  : a.vlT + ((size_t)b * a.nv + (hh - 2 * a.nqk)) * HD * a.Tp;
-    // Waves past the prompt (padding up to Tp) only take part in the
-    // transposed store at the end, with zeros: with lo parts every wave of a
-    // workgroup passes the test above (Tp is a multiple of 64 and a
-    // workgroup spans 4 GT = 32 tokens), so all four reach its barrier.
-    uint64_t lt[2][2] = {{0, 0}, {0, 0}};   // the block's transposed lo values, four tokens a word
     __shared__ __attribute__((aligned(16))) uint16_t s_rows[4][2][GT][HD];   // [wave][hi, lo][token][channel]
-    if (t0 < a.T) {
+    {
         const bool conv = (a.flags & VX27_DN_CONV) != 0;
         const float qs = 1.0f / sqrtf((float)HD);
         const int nt = min(GT, a.T - t0);
@@ -1328,6 +2025,16 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
                 }
             }
         }
+        if (a.vo32 && !is_q && !is_k) {   // v in fp32: 256 contiguous bytes per channel half
+#pragma unroll
+            for (int j = 0; j < GT; j++) {
+                if (j >= nt) break;
+                float *dst = a.vo32 + (((size_t)b * a.T + t0 + j) * a.nv + (hh - 2 * a.nqk)) * HD;
+                dst[lane] = v2s[j][0];
+                dst[lane + 64] = v2s[j][1];
+            }
+            return;
+        }
 #pragma unroll
         for (int j = 0; j < GT; j++) {
             if (j >= nt) break;
@@ -1336,18 +2043,8 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
             s_rows[wave][0][j][lane] = h0;
             s_rows[wave][0][j][lane + 64] = h1;
             if (a.qol) {
-                const uint16_t l0 = vx_f32_to_bf16(v2[0] - vx_bf16_to_f32(h0));
-                const uint16_t l1 = vx_f32_to_bf16(v2[1] - vx_bf16_to_f32(h1));
-                s_rows[wave][1][j][lane] = l0;
-                s_rows[wave][1][j][lane + 64] = l1;
-                const int sh = 16 * (j & 3);
-                if (j < 4) {
-                    lt[0][0] |= (uint64_t)l0 << sh;
-                    lt[1][0] |= (uint64_t)l1 << sh;
-                } else {
-                    lt[0][1] |= (uint64_t)l0 << sh;
-                    lt[1][1] |= (uint64_t)l1 << sh;
-                }
+                s_rows[wave][1][j][lane] = vx_f32_to_bf16(v2[0] - vx_bf16_to_f32(h0));
+                s_rows[wave][1][j][lane + 64] = vx_f32_to_bf16(v2[1] - vx_bf16_to_f32(h1));
             }
         }
         // the block's rows out of the wave's own LDS slots, 16 bytes a lane
@@ -1370,23 +2067,6 @@ __global__ __launch_bounds__(256) void dnp_glue_in(GlueInArgs a) {
                     *(uint4 *)(dl + 8 * cg) = *(const uint4 *)&s_rows[wave][1][jr][8 * cg];
                 }
             }
-        }
-    }
-    if (tl) {   // (uniform in the workgroup) tokens past nt stay zero
-        // the four waves' 8 tokens of each channel side by side in LDS, then
-        // stored as 64-byte runs (four lanes a channel) instead of 16-byte
-        // pieces one row apart
-        __shared__ uint4 s_lt[2][64][4];   // [e][lane][wave]
-#pragma unroll
-        for (int e = 0; e < 2; e++)
-            s_lt[e][lane][wave] = make_uint4((uint32_t)lt[e][0], (uint32_t)(lt[e][0] >> 32), (uint32_t)lt[e][1],
-                                             (uint32_t)(lt[e][1] >> 32));
-        __syncthreads();
-        const int tw = blockIdx.x * 4 * GT;   // the workgroup's first token
-#pragma unroll
-        for (int i = 0; i < 2; i++) {
-            const int pc = threadIdx.x + 256 * i, c = pc >> 2, q = pc & 3;   // channel c (0..127), wave slot q
-            *(uint4 *)&tl[(size_t)c * a.Tp + tw + GT * q] = s_lt[c >> 6][c & 63][q];
         }
     }
 }
@@ -1483,15 +2163,16 @@ static size_t al256(size_t x) { return (x + 255) & ~(size_t)255; }
 static bool dn_prefill_is_exact(const vx27_dn_prefill_desc *d) {
     return (d->flags & VX27_DN_EXACT) || d->S_ckpt || d->conv_ckpt;
 }
-// The glue's outputs: q, k, v hi rows; with the split form q and k lo rows
-// and the transposed k and v lo parts over the prompt padded to chunks.
+// The glue's outputs: q, k hi rows and v as bf16 rows; the split form adds
+// the q and k lo rows and keeps v in fp32 instead.
 static size_t vx_dn_glue_bytes(int B, int T, int nqk, int nv, bool x3) {
-    const size_t rows = (size_t)B * T, Tp = (size_t)(T + CH - 1) / CH * CH;
+    const size_t rows = (size_t)B * T;
     const size_t qd = (size_t)nqk * HD, vd = (size_t)nv * HD;
-    size_t n = rows * (2 * qd + vd);                                // hi
-    if (x3) n += rows * 2 * qd + (size_t)B * (qd + vd) * Tp;        // lo rows, lo transposed
-    return n * sizeof(uint16_t);
+    return x3 ? al256(rows * 4 * qd * sizeof(uint16_t)) + rows * vd * sizeof(float)
+              : rows * (2 * qd + vd) * sizeof(uint16_t);
 }
+// Bytes of one K record (K^T operand tiles, hi and, with lo parts, lo).
+static size_t vx_dn_krec_bytes(bool lo) { return lo ? 2 * K_LO : K_LO; }
 
 size_t vx_dn_prefill_scratch(const vx27_dn_prefill_desc *d) {
     const int qd = d->nqk * HD, vd = d->nv * HD, C = 2 * qd + vd;
@@ -1503,8 +2184,10 @@ size_t vx_dn_prefill_scratch(const vx27_dn_prefill_desc *d) {
     const bool x3 = !(d->flags & VX27_DN_BF16);
     const size_t n_rec = (size_t)d->B * d->nv * NC;
     const bool glue = (d->flags & (VX27_DN_CONV | VX27_DN_PRE_RMS | VX27_DN_PRE_L2)) != 0;
-    return al256(n_rec * (x3 ? XREC : REC)) + al256(n_rec * sizeof(float)) +
-           (glue ? vx_dn_glue_bytes(d->B, d->T, d->nqk, d->nv, x3) : 0);
+    const size_t glue_bytes = glue ? vx_dn_glue_bytes(d->B, d->T, d->nqk, d->nv, x3) : 0;
+    if (x3 && glue)
+        return al256(n_rec * TREC) + al256((size_t)d->B * d->nqk * NC * vx_dn_krec_bytes(true)) + glue_bytes;
+    return al256(n_rec * (x3 ? XREC : REC)) + al256(n_rec * sizeof(float)) + glue_bytes;
 }
 
 // The exact path: the decode kernels token by token (prefill layout).
@@ -1572,8 +2255,11 @@ static int dn_prefill_check(const vx27_dn_prefill_desc *d) {
         VX_REQUIRE(((uintptr_t)d->conv_w & 15) == 0, "vx27_hip_dn_prefill: conv_w must be 16-byte aligned");
     } else {
         VX_REQUIRE(d->q && d->k && d->v, "vx27_hip_dn_prefill: q, k, v are required without VX27_DN_CONV");
+        VX_REQUIRE((((uintptr_t)d->q | (uintptr_t)d->k | (uintptr_t)d->v) & 15) == 0,
+                   "vx27_hip_dn_prefill: q, k and v must be 16-byte aligned");
         VX_REQUIRE(!d->conv_ckpt, "vx27_hip_dn_prefill: conv_ckpt needs VX27_DN_CONV");
     }
+    VX_REQUIRE(((uintptr_t)d->out & 15) == 0, "vx27_hip_dn_prefill: out must be 16-byte aligned");
     if (d->flags & (VX27_DN_PRE_RMS | VX27_DN_OUT_GATE))
         VX_REQUIRE(d->norm_w != nullptr, "vx27_hip_dn_prefill: norm_w required by PRE_RMS/OUT_GATE");
     if (d->flags & VX27_DN_OUT_GATE) {
@@ -1592,22 +2278,28 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
     const int NC = (d->T + CH - 1) / CH;
     const bool x3 = !(d->flags & VX27_DN_BF16);   // split (bf16x3) products unless asked for bf16
     const size_t n_rec = (size_t)d->B * d->nv * NC;
-    const size_t gc_off = al256(n_rec * (x3 ? XREC : REC));
     const bool glue = conv || (d->flags & (VX27_DN_PRE_RMS | VX27_DN_PRE_L2));
     const int qd = d->nqk * HD, vd = d->nv * HD, C = 2 * qd + vd;
-    const size_t glue_off = gc_off + al256(n_rec * sizeof(float));
     const size_t rows = (size_t)d->B * d->T;
+    // the T-record form for the glue's split inputs, the full records for
+    // inputs exact in bf16 (and for the bf16 products)
+    const bool trec = x3 && glue;
+    const size_t rec_bytes = trec ? al256(n_rec * TREC) : al256(n_rec * (x3 ? XREC : REC)) + al256(n_rec * sizeof(float));
+    const size_t krec_one = vx_dn_krec_bytes(true);
+    const size_t krec_bytes = trec ? al256((size_t)d->B * d->nqk * NC * krec_one) : 0;
+    char *glue_buf = (char *)scr + rec_bytes + krec_bytes;
     const uint16_t *q = d->q, *k = d->k, *v = d->v;
-    const uint16_t *ql = nullptr, *kl = nullptr, *klT = nullptr, *vlT = nullptr;
-    const int Tp = NC * CH;
-    if (glue) {   // conv and pre-norms in fp32, then q, k, v as bf16 (hi, and lo for the split form)
-        uint16_t *qo = (uint16_t *)((char *)scr + glue_off), *ko = qo + rows * qd, *vo = ko + rows * qd;
-        uint16_t *qol = x3 ? vo + rows * vd : nullptr, *kol = x3 ? qol + rows * qd : nullptr;
-        uint16_t *kT = x3 ? kol + rows * qd : nullptr, *vT = x3 ? kT + (size_t)d->B * qd * Tp : nullptr;
+    const uint16_t *ql = nullptr, *kl = nullptr;
+    const float *v32 = nullptr;
+    if (glue) {   // conv and pre-norms in fp32, then q, k as bf16 (hi, and lo for the split form), v
+        uint16_t *qo = (uint16_t *)glue_buf, *ko = qo + rows * qd;
+        uint16_t *qol = x3 ? ko + rows * qd : nullptr, *kol = x3 ? qol + rows * qd : nullptr;
+        uint16_t *vo = x3 ? nullptr : ko + rows * qd;
+        float *vo32 = x3 ? (float *)(glue_buf + al256(rows * 4 * qd * sizeof(uint16_t))) : nullptr;
         GlueInArgs ga{d->B, d->T, d->nqk, d->nv, C, d->flags, d->conv_w_dtype == VX27_BF16, d->x, d->conv_state,
-                      d->conv_w, d->q, d->k, d->v, d->norm_w, qo, ko, vo, qol, kol, kT, vT, Tp};
+                      d->conv_w, d->q, d->k, d->v, d->norm_w, qo, ko, vo, qol, kol, vo32};
         const int nh = 2 * d->nqk + d->nv;
-        const int tblk = ((x3 ? Tp : d->T) + GT - 1) / GT;   // the split form also zeroes the padding
+        const int tblk = (d->T + GT - 1) / GT;
         VX_LAUNCH(ctx, dnp_glue_in, dim3((unsigned)((tblk + 3) / 4), (unsigned)nh, (unsigned)d->B), dim3(256), ga);
         if (conv) {
             const size_t nthr = (size_t)d->B * C;
@@ -1615,31 +2307,37 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
                       d->conv_state);
         }
         q = qo; k = ko; v = vo;
-        ql = qol; kl = kol; klT = kT; vlT = vT;
+        ql = qol; kl = kol; v32 = vo32;
     }
-    ScanArgs sa{d->T, d->nv, NC, (d->nv % 8) == 0, (const char *)scr, (const float *)((char *)scr + gc_off),
-                d->S, d->out};
-    if (x3) {
-        Prep3Args pa{d->T, d->nqk, d->nv, NC, q, k, v, ql, kl, klT, vlT, Tp, d->a, d->b, d->A_log, d->dt_bias,
-                     (char *)scr};
-        if (pa.ql)
-            VX_LAUNCH_NAMED(ctx, "dnp_prep3", dnp_prep3<true>, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B),
-                            dim3(256), pa);
-        else
-            VX_LAUNCH_NAMED(ctx, "dnp_prep3", dnp_prep3<false>, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B),
-                            dim3(256), pa);
-        // two column blocks per workgroup once one each would exceed the CUs
-        // (measured at 48 heads: 222 us against 285 us for two workgroups of
-        // one block sharing a CU; at 16 heads one block a workgroup is faster)
-        if (d->nv * NSLICE * d->B > ctx->n_cu)
+    // two column blocks per walk workgroup once one each would exceed the CUs
+    const bool two = d->nv * NSLICE * d->B > ctx->n_cu;
+    if (trec) {
+        char *rec = (char *)scr, *krec = (char *)scr + rec_bytes;
+        PrepTArgs pa{d->T, d->nqk, d->nv, NC, q, k, ql, kl, v32, d->a, d->b, d->A_log, d->dt_bias, rec, krec,
+                     (int)krec_one};
+        VX_LAUNCH(ctx, dnp_prept, dim3((unsigned)NC, (unsigned)d->nqk, (unsigned)d->B), dim3(256), pa);
+        ScanTArgs sa{d->T, d->nqk, d->nv, NC, (d->nqk % 8) == 0, q, k, ql, kl, rec, krec, (int)krec_one, d->S, d->out};
+        const dim3 sg((unsigned)(d->nv * NSLICE / (two ? 2 : 1)), (unsigned)d->B);
+        if (two) VX_LAUNCH_NAMED(ctx, "dnp_scant", dnp_scant<2>, sg, dim3(256), sa);
+        else VX_LAUNCH_NAMED(ctx, "dnp_scant", dnp_scant<1>, sg, dim3(256), sa);
+    } else if (x3) {
+        ScanArgs sa{d->T, d->nv, NC, (d->nv % 8) == 0, (const char *)scr,
+                    (const float *)((char *)scr + al256(n_rec * XREC)), d->S, d->out};
+        Prep3Args pa{d->T, d->nqk, d->nv, NC, q, k, v, nullptr, nullptr, nullptr, nullptr, NC * CH, d->a, d->b,
+                     d->A_log, d->dt_bias, (char *)scr};
+        VX_LAUNCH_NAMED(ctx, "dnp_prep3", dnp_prep3<false>, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B),
+                        dim3(256), pa);
+        if (two)
             VX_LAUNCH_NAMED(ctx, "dnp_scan3", dnp_scan3<2>, dim3((unsigned)(d->nv * NSLICE / 2), (unsigned)d->B),
                             dim3(256), sa);
         else
             VX_LAUNCH_NAMED(ctx, "dnp_scan3", dnp_scan3<1>, dim3((unsigned)(d->nv * NSLICE), (unsigned)d->B),
                             dim3(256), sa);
     } else {
+        ScanArgs sa{d->T, d->nv, NC, (d->nv % 8) == 0, (const char *)scr, (const float *)((char *)scr + al256(n_rec * REC)),
+                    d->S, d->out};
         PrepArgs pa{d->T, d->nqk, d->nv, NC, q, k, v, d->a, d->b, d->A_log, d->dt_bias,
-                    (char *)scr, (float *)((char *)scr + gc_off)};
+                    (char *)scr, (float *)((char *)scr + al256(n_rec * REC))};
         VX_LAUNCH(ctx, dnp_prep, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B), dim3(256), pa);
         VX_LAUNCH(ctx, dnp_scan, dim3((unsigned)(d->nv * NSLICE), (unsigned)d->B), dim3(256), sa);
     }
