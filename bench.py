@@ -221,11 +221,11 @@ def bench_dn_conv(ctx, steps, warmup, B=64, H=16, cpu=True):
     for t in range(warmup, total):
         L.check(fn(ctx.h, C.byref(descs[t])), "dn_decode")
     ctx.sync()
-    kname = "dn_step_kernel"   # one step per call: the single-step kernel (conv and gates fused)
-    n, ms = ctx.prof_read(kname)
-    if n == 0:
-        kname = "dn_decode_kernel"
+    # one step per call: the single-step kernel (conv and gates fused), column-split for few heads
+    for kname in ("dn_step_kernel", "dn_step_split", "dn_decode_kernel"):
         n, ms = ctx.prof_read(kname)
+        if n:
+            break
     ctx.prof_enable(False)
     alg = dn_conv_alg_bytes(B, H, hd)
     avg_s = ms / n / 1e3
@@ -304,12 +304,27 @@ def bench_dn_recurrent(ctx, steps=2000, cpu=True):
     for t in range(200):
         L.check(fn(ctx.h, C.byref(per[t])), "dn_decode")
     ctx.sync()
-    kern = {k: ctx.prof_read(k) for k in ("dn_step_kernel", "dn_decode_kernel", "dn_gate_kernel")}
+    kern = {k: ctx.prof_read(k) for k in ("dn_step_kernel", "dn_step_split", "dn_decode_kernel", "dn_gate_kernel")}
     ctx.prof_enable(False)
+    # the same per-step calls captured as one graph of 200 launches: the
+    # device-side time per step without the host's per-call cost
+    ctx.graph_begin()
+    for t in range(200):
+        L.check(fn(ctx.h, C.byref(per[t])), "dn_decode")
+    g = ctx.graph_end()
+    ctx.graph_launch(g)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        ctx.graph_launch(g)
+    ctx.sync()
+    graph_step = (time.perf_counter() - t0) / (5 * 200)
+    L.check(L.lib().vx27_hip_graph_destroy(g), "graph_destroy")
     k_us = sum(ms for _, ms in kern.values()) / 200 * 1e3
     res = {"workload": f"dn_recurrent B=1 heads=16 {steps} steps",
            "us_per_step_resident": multi / steps * 1e6,
            "us_per_step_streamed": single / steps * 1e6,
+           "us_per_step_streamed_graph": graph_step * 1e6,
            "kernel_us_streamed": k_us,
            "kernels_streamed": {k: v[0] / 200 for k, v in kern.items() if v[0]},
            "alg_bytes_per_step_streamed": C1_BYTES_PER_STEP,

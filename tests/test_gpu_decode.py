@@ -78,6 +78,49 @@ def test_dn_conv_batched_full(ctx):
     assert np.array_equal(lay.conv(), conv)
 
 
+@pytest.mark.parametrize("B,flags,conv", [(1, 0, False), (2, 0, False), (4, 4, False), (8, 2 | 4, False),
+                                           (1, 1 | 4, True), (4, 1 | 4, True)])
+def test_dn_single_step_calls(ctx, B, flags, conv):
+    """One step per call with few heads (B x 16).  Without the conv this is
+    the column-split step kernel (8, 4 or 2 workgroups per head for 16, 64
+    and 128 heads), with it the one-block-per-head kernel.  24 calls in a
+    row against the oracle: outputs and state within 1e-5, conv state
+    bit-exact; and the same calls again from the same start give the same
+    bits."""
+    from vx27_amd import workloads as W
+    H, steps = 16, 24
+    if conv:
+        d = W.dn_conv(B=B, H=H, steps=steps, config=11)
+    else:
+        d = W.dn_recurrent(B=B, H=H, steps=steps, S0_std=0.05, config=11)
+    nw = None
+    if flags & 2:   # rmsn(1+w) pre-norm
+        nw = d["norm_w"] = W.normal(W.rng(11, "split_norm_w"), 128, 0.1, 1.0)
+    say(f"dn single-step calls: B={B} flags={flags} conv={conv}")
+
+    def run():
+        lay = _dn_layer(ctx, d, B, H, H, conv=conv, norm_w=nw)
+        outs = []
+        for t in range(steps):
+            sl = slice(t, t + 1)
+            if conv:
+                outs.append(lay.decode(1, flags, d["a"][sl], d["b"][sl], x=d["x"][sl]))
+            else:
+                outs.append(lay.decode(1, flags, d["a"][sl], d["b"][sl], q=d["q"][sl], k=d["k"][sl], v=d["v"][sl]))
+        return np.concatenate(outs), lay.state(), (lay.conv() if conv else None)
+    out, S, cv = run()
+    ref, Sr, cr, _ = oracle_dn(d, flags, B, H, H, steps)
+    e_o, e_s = maxabs(out, ref), maxabs(S, Sr)
+    say(f"  max|d out|={e_o:.3e} max|d S|={e_s:.3e} bit-exact out={bitexact_frac(out, ref):.4f}")
+    assert e_o <= DN_TOL and e_s <= DN_TOL
+    if conv:
+        assert np.array_equal(cv, cr)
+    out2, S2, cv2 = run()
+    assert np.array_equal(out2, out) and np.array_equal(S2, S)
+    if conv:
+        assert np.array_equal(cv2, cv)
+
+
 @pytest.mark.parametrize("nv", [16, 32, 48])
 def test_dn_qlayer_glue(ctx, nv):
     """All stages of the vx27_qlayer DeltaNet branch: conv, rmsn(1+w), l2norm,

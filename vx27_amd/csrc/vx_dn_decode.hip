@@ -558,6 +558,183 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
     }
 }
 
+// One step with a head's columns split over CS workgroups of 128 lanes, for
+// few heads (B * nv * CS workgroups spread the state over more of the chip
+// than one block per head).  Workgroup (head, slice) owns columns
+// slice*128/CS ..; lane (c4, pw) = (lane / PW, lane % PW) of wave w holds
+// rows RPL*(w*PW + pw) .. of columns 4 c4 .. 4 c4 + 3 of the slice, so the
+// PW lanes sharing columns are adjacent and their kv and o partial sums add
+// on the DPP paths (part_sum), then the two waves in LDS.  Wave 0 forms the
+// whole head's q, k and v as dn_step_kernel does (each slice recomputes
+// them).  Not with the output gate (its norm spans all 128 columns) nor the
+// fused conv (the slices would share the q/k channels' conv state, which one
+// of them must advance only after all have read it).
+template <int CS>
+__global__ __launch_bounds__(128) void dn_step_split(DnArgs a) {
+    constexpr int NCOL = HD / CS, CG = NCOL / 4, PW = 64 / CG, RPL = HD / (2 * PW);
+    const int tid = threadIdx.x, lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int c4 = lane / PW, pw = lane % PW, part = wave * PW + pw;
+    const int head = blockIdx.x / CS, slice = blockIdx.x % CS;
+    const int b = head / a.nv, vh = head % a.nv;
+    const int g = vh * a.nqk / a.nv;           // QK head (vx27_qfwd.c:137)
+
+    __shared__ float s_qn[HD], s_kn[HD], s_v[HD];
+    __shared__ double s_red[2][NCOL];
+    __shared__ double s_dl[NCOL];
+
+    float *Sg = a.S + ((size_t)b * a.nv + vh) * HD * HD + (size_t)(RPL * part) * HD + slice * NCOL + 4 * c4;
+    float4 S4[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        const f4v *sp = (const f4v *)(Sg + (size_t)r * HD);
+        const f4v v = DN_STATE_NT_LD ? __builtin_nontemporal_load(sp) : *sp;
+        S4[r] = make_float4(v.x, v.y, v.z, v.w);
+    }
+    float qa[2] = {0.f, 0.f}, ka[2] = {0.f, 0.f}, va[2] = {0.f, 0.f};
+    if (wave == 0) {
+        const size_t bs = (size_t)b * a.b_step;
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            const int i = lane + 64 * h;
+            qa[h] = a.q[bs * a.q_tok + (size_t)g * HD + i];
+            ka[h] = a.k[bs * a.k_tok + (size_t)g * HD + i];
+            va[h] = a.v[bs * a.v_tok + (size_t)vh * HD + i];
+        }
+    }
+    float w0 = 1.f, w1 = 1.f;
+    if (wave == 0 && !(a.flags & VX_DN_QK_READY) && a.norm_w) {
+        w0 = a.norm_w[lane];
+        w1 = a.norm_w[lane + 64];
+    }
+    const size_t ge = (size_t)b * a.b_step * a.nv + vh;
+    double beta, decay;
+    if (a.gates) {
+        const double2 gt = a.gates[ge];
+        beta = gt.x;
+        decay = gt.y;
+    } else {   // vx27_deltanet_gate_params (vx27_deltanet.c:65-69), decay = exp(g_log)
+        const float gbv = a.gb[ge], gav = a.ga[ge], alog = a.A_log[vh], dtb = a.dt_bias[vh];
+        beta = 1.0 / (1.0 + exp(-(double)gbv));
+        decay = exp(-exp((double)alog) * softplus_d((double)gav + (double)dtb));
+    }
+    if (wave == 0 && !(a.flags & VX_DN_QK_READY)) {
+        // q/k normalisation chain (vx27_qfwd.c:119-130 per flags, then
+        // step_exact's own l2norm, vx27_deltanet.c:77-80), as dn_step_kernel
+        const float qs = 1.0f / sqrtf((float)HD);
+        const float nw[2] = {w0, w1};
+        auto sums = [&](double &sq, double &sk) {
+            sq = vx_wave_sum_f64_dpp((double)qa[0] * (double)qa[0] + (double)qa[1] * (double)qa[1]);
+            sk = vx_wave_sum_f64_dpp((double)ka[0] * (double)ka[0] + (double)ka[1] * (double)ka[1]);
+        };
+        double sq, sk;
+        if (a.flags & VX27_DN_PRE_RMS) {       // rmsn(x)*(1+w), vx27_qfwd.c:32-39,123
+            sums(sq, sk);
+            const float iq = 1.0f / sqrtf((float)(sq / HD) + 1e-6f);
+            const float ik = 1.0f / sqrtf((float)(sk / HD) + 1e-6f);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                qa[h] = (qa[h] * iq) * (nw[h] + 1.0f);
+                ka[h] = (ka[h] * ik) * (nw[h] + 1.0f);
+            }
+        }
+        if (a.flags & VX27_DN_PRE_L2) {        // l2norm + q/sqrt(hd), vx27_qfwd.c:124-130
+            sums(sq, sk);
+            const float iq = 1.0f / sqrtf((float)sq + 1e-6f), ik = 1.0f / sqrtf((float)sk + 1e-6f);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                qa[h] = qa[h] * iq;
+                ka[h] = ka[h] * ik;
+                qa[h] = qa[h] * qs;
+            }
+        }
+        {                                       // inside step_exact, vx27_deltanet.c:77-80
+            sums(sq, sk);
+            const float iq = 1.0f / sqrtf((float)sq + 1e-6f), ik = 1.0f / sqrtf((float)sk + 1e-6f);
+#pragma unroll
+            for (int h = 0; h < 2; h++) {
+                qa[h] = (qa[h] * iq) * qs;
+                ka[h] = ka[h] * ik;
+            }
+        }
+    }
+    if (wave == 0) {
+#pragma unroll
+        for (int h = 0; h < 2; h++) {
+            s_qn[lane + 64 * h] = qa[h];
+            s_kn[lane + 64 * h] = ka[h];
+            s_v[lane + 64 * h] = va[h];
+        }
+    }
+    __syncthreads();
+
+    float kn[RPL], qn[RPL];
+#pragma unroll
+    for (int r = 0; r < RPL; r += 4) {
+        const float4 k4 = *(const float4 *)&s_kn[RPL * part + r], q4 = *(const float4 *)&s_qn[RPL * part + r];
+        kn[r] = k4.x; kn[r + 1] = k4.y; kn[r + 2] = k4.z; kn[r + 3] = k4.w;
+        qn[r] = q4.x; qn[r + 1] = q4.y; qn[r + 2] = q4.z; qn[r + 3] = q4.w;
+    }
+    // ---- S *= decay ; kv = S^T kn
+    double kv[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+        float *e = (float *)&S4[r];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float sd = (float)((double)e[c] * decay);
+            e[c] = sd;
+            kv[c] = __builtin_fma((double)sd, (double)kn[r], kv[c]);
+        }
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) kv[c] = part_sum<PW>(kv[c]);
+    if (pw == 0) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) s_red[wave][4 * c4 + c] = kv[c];
+    }
+    __syncthreads();
+    if (tid < NCOL) s_dl[tid] = ((double)s_v[slice * NCOL + tid] - (s_red[0][tid] + s_red[1][tid])) * beta;
+    __syncthreads();
+    // ---- S += kn (x) dl ; o = S^T qn
+    double dl[4];
+#pragma unroll
+    for (int c = 0; c < 4; c++) dl[c] = s_dl[4 * c4 + c];
+    double o[4] = {0.0, 0.0, 0.0, 0.0};
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+        float *e = (float *)&S4[r];
+#pragma unroll
+        for (int c = 0; c < 4; c++) {
+            const float su = (float)((double)e[c] + (double)kn[r] * dl[c]);
+            e[c] = su;
+            o[c] = __builtin_fma((double)su, (double)qn[r], o[c]);
+        }
+    }
+#pragma unroll
+    for (int r = 0; r < RPL; r++) {
+        typedef float f4v __attribute__((ext_vector_type(4)));
+        f4v *sp = (f4v *)(Sg + (size_t)r * HD);
+        const f4v v = {S4[r].x, S4[r].y, S4[r].z, S4[r].w};
+        if (DN_STATE_NT_ST) __builtin_nontemporal_store(v, sp); else *sp = v;
+    }
+#pragma unroll
+    for (int c = 0; c < 4; c++) o[c] = part_sum<PW>(o[c]);
+    __syncthreads();   // (s_red's kv values are read out)
+    if (pw == 0) {
+#pragma unroll
+        for (int c = 0; c < 4; c++) s_red[wave][4 * c4 + c] = o[c];
+    }
+    __syncthreads();
+    if (tid < NCOL) {
+        const float f = (float)(s_red[0][tid] + s_red[1][tid]);
+        const int j = slice * NCOL + tid;
+        if (a.out) a.out[(size_t)b * a.b_step * a.out_tok + (size_t)vh * HD + j] = f;
+        if (a.out_packed) vx_pack_store(a.out_packed, a.B, b, vh * HD + j, f);
+    }
+}
+
 // Gated output norm of one step for column-split heads: one block of 128
 // lanes per (sequence, value head); out = rmsn_std(o)*norm_w * silu(z)
 // (vx27_qfwd.c:147-151) from the pre-norm outputs in o_pre.
@@ -657,6 +834,15 @@ int vx_dn_recurrence(vx27_hip_ctx *ctx, const DnArgs &a_in) {
     const int heads = a.B * a.nv;
     const bool gate = (a.flags & VX27_DN_OUT_GATE) != 0;
     if (vx_dn_single_step(a)) {
+        // few heads, no fused conv and no output gate: columns split over CS workgroups
+        const int CS = (gate || a.fused_conv || heads > 128) ? 1 : heads <= 32 ? 8 : heads <= 64 ? 4 : 2;
+        if (CS > 1) {
+            const dim3 grid((unsigned)(heads * CS));
+            if (CS == 8) VX_LAUNCH_NAMED(ctx, "dn_step_split", dn_step_split<8>, grid, dim3(128), a);
+            else if (CS == 4) VX_LAUNCH_NAMED(ctx, "dn_step_split", dn_step_split<4>, grid, dim3(128), a);
+            else VX_LAUNCH_NAMED(ctx, "dn_step_split", dn_step_split<2>, grid, dim3(128), a);
+            return 0;
+        }
         if (a.fused_conv)
             VX_LAUNCH_NAMED(ctx, "dn_step_kernel", dn_step_kernel<true>, dim3((unsigned)heads), dim3(512), a);
         else

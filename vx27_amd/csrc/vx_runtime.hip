@@ -76,6 +76,7 @@ extern "C" int vx27_hip_open(vx27_hip_ctx **out, int device, char *err, size_t e
         hipHostMalloc((void **)&c->err_host, 256, hipHostMallocDefault) != hipSuccess) {
         vx_set_error("vx27_hip_open: cannot allocate the error flag on device %d", device);
         if (c->err_flag) (void)hipFree(c->err_flag);
+        if (c->err_host) (void)hipHostFree(c->err_host);
         (void)hipStreamDestroy(c->own_stream);
         delete c;
         return fail();
