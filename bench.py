@@ -43,6 +43,9 @@ and roofline fraction, and the oracle timed on this host where noted:
                     (33,640,448 B per sequence); CPU at B=1 and 32
   c3_dn_conv_B{1,4,16,64}  batched DeltaNet decode with the fused conv;
                     CPU at B=64 (16 threads and 1 thread)
+  layer_decode_B{16,64}  one DeltaNet and one gated-GQA mixer layer with
+                    their projections (GQA at 4096 cached positions), per
+                    layer and per projection kernel against 8 TB/s
   c4a/c4b           the two prefills of a 4096-token prompt (chunked
                     DeltaNet, 16 heads; causal gated GQA, 24Q/4KV hd 256)
                     against the bf16 MFMA peak
@@ -467,6 +470,71 @@ def cpu_gqa(d, B, nk):
                       "median of 3"}
 
 
+# ------------------------------------------------------- whole mixer layers
+def bench_layer_decode(ctx, B, Lctx=4096, iters=10):
+    """One decode token of B sequences through a Gated DeltaNet mixer layer
+    (16 QK / 48 V heads of 128, hidden 5120) and a gated-GQA mixer layer
+    (24 Q / 4 KV heads of 256, Lctx cached positions), bf16 weights, each
+    with its input and output projection (one pass over each weight matrix
+    for up to 65 sequences).  The stack holds 9 DeltaNet and 3 GQA layers
+    and each timing runs all layers of one kind in turn (HIP graph, 'iters'
+    replays), so that every layer streams its weights from HBM as in a full
+    decode step (one layer's weights alone would stay in the 256 MiB
+    last-level cache between replays).  Per-kernel times from a profiled
+    eager pass.  Algorithmic bytes: weights, DeltaNet state and conv state
+    r+w (or the K/V rows attended and written), x and out."""
+    from vx27_amd import lib as L
+    from vx27_amd.stack import GQ, HD, H, MixerStack
+    st = MixerStack(ctx, B=B, Lctx=Lctx, extra_pos=8, n_layers=12)
+    lib = L.lib()
+    ctx.fill_normal(st.x, B * H, 91, 1.0)
+    L.check(lib.vx27_hip_pack_x(ctx.h, st.x.ptr, B, H, st.xp.ptr), "pack_x")
+    nv = st.nv
+    vd, C_ = nv * HD, st.C
+    res = {"workload": f"DeltaNet and gated-GQA mixer layer decode, B={B}, GQA context {Lctx}"}
+    for kind in ("dn", "gqa"):
+        lays = [lay for lay in st.layers if lay["kind"] == kind]
+        fn = lib.vx27_hip_dn_layer_decode if kind == "dn" else lib.vx27_hip_gqa_layer_decode
+
+        def call():
+            for lay in lays:
+                L.check(fn(ctx.h, C.byref(lay["desc"])), kind)
+        call()
+        ctx.sync()
+        ctx.graph_begin()
+        call()
+        g = ctx.graph_end()
+        ctx.graph_launch(g)
+        ctx.sync()
+        t0 = time.perf_counter()
+        for _ in range(iters):
+            ctx.graph_launch(g)
+        ctx.sync()
+        wall = (time.perf_counter() - t0) / iters / len(lays)
+        lib.vx27_hip_graph_destroy(g)
+        kernels = (("gemv_dn_in", "gemv_wk_store", "dn_step_kernel", "dn_step_split", "dn_decode_kernel")
+                   if kind == "dn" else ("gemv_wk_store", "gqa_prep", "gqa_split", "gqa_combine"))
+        _, per = _time_calls(ctx, call, kernels, iters)
+        per = {k: v / len(lays) for k, v in per.items()}
+        io = 2 * B * H * 4
+        if kind == "dn":
+            w_in, w_out = (C_ + vd + 2 * nv) * H * 2, H * vd * 2
+            alg = w_in + w_out + 2 * B * nv * HD * HD * 4 + 2 * B * C_ * 3 * 4 + C_ * 4 * 2 + io
+            proj = {"gemv_dn_in": (w_in, per["gemv_dn_in"]), "gemv_wk_store": (w_out, per["gemv_wk_store"])}
+        else:
+            w_qkv, w_o = (24 * 2 * GQ + 2 * 4 * GQ) * H * 2, H * 24 * GQ * 2
+            alg = w_qkv + w_o + B * 4 * (Lctx + 1) * GQ * 2 * 2 + B * 4 * GQ * 2 * 2 + io
+            proj = {"gemv_wk_store": (w_qkv + w_o, per["gemv_wk_store"])}
+        res[kind] = {
+            "layers_timed": len(lays),
+            "us_per_layer": round(wall * 1e6, 2), "us_per_token": round(wall / B * 1e6, 3),
+            "alg_bytes": alg, "hbm_frac": round(alg / wall / HBM_PEAK, 4),
+            "kernels_us": {k: round(v, 2) for k, v in per.items() if v > 0},
+            "projection_hbm_frac": {k: round(b / (us / 1e6) / HBM_PEAK, 4) for k, (b, us) in proj.items() if us > 0},
+        }
+    return res
+
+
 # ---------------------------------------------------------------- prefill
 MFMA_BF16_PEAK = 2.5e15     # flop/s, MI355X dense bf16
 
@@ -626,7 +694,7 @@ def main():
     ap.add_argument("--context", type=int, default=131072)
     ap.add_argument("--no-extra", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
-    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4"],
+    ap.add_argument("--only", choices=["c1", "c2", "c3", "c4", "layers"],
                     help="run one extra configuration alone and print its figures (for profiling)")
     args = ap.parse_args()
     if args.gpus != 1:
@@ -643,6 +711,7 @@ def main():
                 "c2": lambda: {f"c2_gqa8k_B{B}": bench_gqa(ctx, B, cpu=cpu) for B in (1, 4, 32)},
                 "c3": lambda: {f"c3_dn_conv_B{B}": bench_dn_conv(ctx, 256, 8, B=B, cpu=cpu and B == 64)
                                for B in (1, 4, 16, 64)},
+                "layers": lambda: {f"layer_decode_B{B}": bench_layer_decode(ctx, B) for B in (4, 16, 64)},
                 "c4": lambda: {"c4a_dn_prefill_T4096": bench_dn_prefill(ctx, cpu=cpu),
                                "c4a_dn_prefill_layer_T4096": bench_dn_prefill_glue(ctx),
                                "c4b_gqa_prefill_T4096": bench_gqa_prefill(ctx, cpu=cpu)}}
@@ -690,6 +759,13 @@ def main():
             log(f"  gqa B={B}: {r['us_per_step']:.1f} us/step, split kernel {r['kernel_us']:.1f} us, "
                 f"{r['achieved_GBs']:.0f} GB/s ({100 * r['hbm_frac_kernel']:.1f}% HBM), "
                 f"step {100 * r['hbm_frac_step']:.1f}% HBM")
+        for B in (16, 64):
+            r = bench_layer_decode(ctx, B)
+            extra[f"layer_decode_B{B}"] = r
+            for kind in ("dn", "gqa"):
+                q = r[kind]
+                log(f"  {kind} layer decode B={B}: {q['us_per_layer']:.1f} us/layer, "
+                    f"{100 * q['hbm_frac']:.1f}% HBM; projections {q['projection_hbm_frac']}")
         r = bench_dn_prefill(ctx, cpu=cpu)
         extra["c4a_dn_prefill_T4096"] = r
         log(f"  dn_prefill: {r['kernel_us']:.1f} us ({r['tokens_per_s']:.3g} tok/s), "

@@ -323,7 +323,8 @@ int vx27_hip_rope_table(vx27_hip_ctx *ctx, const int *pos, int n, int rope_dim,
 /* y[b*y_stride + n] = sum_k W[n][k] * x[b*x_stride + k] for B >= 1 vectors:
  * W bf16 row-major [N][K] (N % 16 == 0, K % 32 == 0), x and y fp32.  The
  * F32 matvec of the reference (vx27_pmat.c:98-101, 119-125) on bf16 weights;
- * x enters the MFMA exactly (split into three bf16 parts), fp32 accumulation. */
+ * x enters the MFMA exactly (split into three bf16 parts), fp32 accumulation.
+ * W is read once per 65 vectors. */
 int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x,
                        size_t x_stride, int B, float *y, size_t y_stride);
 
@@ -338,7 +339,7 @@ int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const
 int vx27_hip_pack_weights_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, uint16_t *W_tiled);
 
 /* The mixer of one Gated DeltaNet layer for one decode token of B
- * sequences (any B; the projections stream their weights once per 15
+ * sequences (any B; the projections stream their weights once per 65
  * sequences), from the layer input xn to the out_proj output (the DeltaNet
  * branch of vx27_qlayer, vx27_qfwd.c:102-153):
  *   [qkv | z | a | b] = W_in xn      (in_proj_qkv, in_proj_z, in_proj_a, in_proj_b
@@ -363,7 +364,7 @@ typedef struct {
 int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_desc *d);
 
 /* The mixer of one gated GQA layer for one decode token of B sequences
- * (any B; weights streamed once per 15 sequences)
+ * (any B; weights streamed once per 65 sequences)
  * (the attention branch of vx27_qlayer, vx27_qfwd.c:162-213):
  *   [q|gate interleaved per head | k | v] = W_qkv xn  (q_proj, k_proj, v_proj
  *                                      stacked: n_q*2*hd + 2*n_kv*hd rows),
@@ -389,7 +390,7 @@ int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer_desc *d);
  * as vx27_engine_batch_step runs it per layer (vx27_run.c:187-238):
  * [qkv|z|a|b] = W_in x for every token, then vx27_hip_dn_prefill with every
  * glue stage (and the checkpoints, when given), then out = W_out o.  The
- * projections stream their weights once per 15 tokens, so this is for short
+ * projections stream their weights once per 65 tokens, so this is for short
  * windows such as an MTP verify batch (the reference's batch is at most 8
  * tokens); a long prompt's projections belong in a GEMM.  x and out are
  * [B][T][hidden]; the other fields as vx27_dn_layer_desc; flags

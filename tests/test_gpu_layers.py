@@ -34,8 +34,11 @@ def bf16w(r, shape, std):
 def test_gemv_bf16_vs_reference_matvec(ctx):
     from vx27_amd import lib as L, workloads as W
     r = W.rng(7, "gemv")
+    # one pass over W for up to 65 vectors (13 groups; 4, 7 and 10 groups
+    # pad to the next instance), passes of 13 groups beyond
     for N, K, B in ((16432, 5120, 4), (5120, 6144, 4), (1024, 5120, 1), (64, 96, 5), (1024, 5120, 8),
-                    (512, 2048, 32), (256, 5120, 64)):
+                    (512, 2048, 32), (256, 5120, 64), (5120, 6144, 16), (16480, 5120, 64), (2048, 5120, 33),
+                    (1024, 512, 70), (512, 1024, 130), (512, 1024, 21)):
         Wb = bf16w(r, (N, K), 0.02)
         x = W.normal(r, (B, K))
         y = np.empty((B, N), np.float32)
@@ -65,11 +68,11 @@ def dn_layer_inputs(r, B, nqk=16, nv=48, hd=128):
     return w, S, conv
 
 
-@pytest.mark.parametrize("B", [4, 8, 20])
+@pytest.mark.parametrize("B", [4, 8, 16, 20, 32, 64])
 def test_dn_layer_decode(ctx, B):
     """The real layer shape (nqk 16, nv 48, hidden 5120), 3 tokens, batch 4,
-    the reference's batch limit 8 (two activation groups), and 20 (two
-    passes over the weights)."""
+    the reference's batch limit 8 (two activation groups), and 16 to 64
+    (4 to 13 groups, one pass over the weights)."""
     from vx27_amd import lib as L, workloads as W
     nqk, nv = 16, 48
     r = W.rng(8, f"dn_layer_{B}")
@@ -109,10 +112,10 @@ def gqa_layer_inputs(r, B, Lcap, n_ctx):
     return w, kc, vc
 
 
-@pytest.mark.parametrize("B", [4, 8, 17])
+@pytest.mark.parametrize("B", [4, 8, 17, 64])
 def test_gqa_layer_decode(ctx, B):
     """Real layer shape (24Q/4KV hd 256, hidden 5120) at ragged positions,
-    2 tokens, batch 4, 8 and 17 (two passes over the weights)."""
+    2 tokens, batch 4, 8, 17 and 64 (one pass over the weights each)."""
     from vx27_amd import lib as L, mixers as M, workloads as W
     Lcap, n_ctx = 768, 700
     r = W.rng(9, f"gqa_layer_{B}")

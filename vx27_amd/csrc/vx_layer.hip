@@ -39,17 +39,17 @@ struct DnInArgs {
 };
 
 // Epilogue of the stacked DeltaNet input projection [qkv | z | a | b]
-// (vx27_qfwd.c:102-117), one thread per row, all vectors of the pass:
+// (vx27_qfwd.c:102-117): one thread per row for all vectors of a pass of up
+// to DN_PREB vectors, one thread per (row, vector) for larger passes:
 //   q|k|v rows: causal conv + SiLU (conv state in place) -> act; the q/k
 //               normalisation chain runs in the recurrence kernel, which
 //               has whole heads
 //   z, a, b rows: copied out (the step kernel maps a and b to decay and
 //               beta, after its state loads are issued: no WG of this
 //               kernel waits on transcendental code)
-// The conv weights (raw bits, converted after the loop so that nothing
-// waits on them) and the conv state of a q|k|v row (first DN_PREB vectors
-// of the pass) are loaded before the projection's K loop.
-constexpr int DN_MAXB = 15;   // vectors per GEMV pass (three groups of 5)
+// For passes of up to DN_PREB vectors the conv weights (raw bits, converted
+// after the loop so that nothing waits on them) and the conv state of a
+// q|k|v row are loaded before the projection's K loop.
 constexpr int DN_PREB = 5;
 struct DnInEpi {
     DnInArgs a;
@@ -60,7 +60,7 @@ struct DnInEpi {
     __device__ __forceinline__ Pre prefetch(int row0, int rows, int tid) const {
         Pre p;
         const int n = row0 + tid;
-        if (tid < rows && n < a.C) {
+        if (a.B <= DN_PREB && tid < rows && n < a.C) {
             if (a.conv_bf16) {
                 const uint2 u = *((const uint2 *)a.conv_w + n);
                 p.w[0] = u.x;
@@ -83,61 +83,89 @@ struct DnInEpi {
         }
         return p;
     }
+    // conv taps of channel n from their raw words (bf16 pairs or fp32)
+    __device__ __forceinline__ void taps(const uint32_t u[4], float w[4]) const {
+        if (a.conv_bf16) {
+            w[0] = __uint_as_float(u[0] << 16);
+            w[1] = __uint_as_float(u[0] & 0xffff0000u);
+            w[2] = __uint_as_float(u[1] << 16);
+            w[3] = __uint_as_float(u[1] & 0xffff0000u);
+        } else {
+#pragma unroll
+            for (int t = 0; t < 4; t++) w[t] = __uint_as_float(u[t]);
+        }
+    }
+    // one (row n, vector b) result y
+    __device__ __forceinline__ void item(int n, int b, float y) const {
+        if (n < a.C) {
+            uint32_t u[4] = {0u, 0u, 0u, 0u};
+            if (a.conv_bf16) {
+                const uint2 v = *((const uint2 *)a.conv_w + n);
+                u[0] = v.x;
+                u[1] = v.y;
+            } else {
+                const uint4 v = *((const uint4 *)a.conv_w + n);
+                u[0] = v.x;
+                u[1] = v.y;
+                u[2] = v.z;
+                u[3] = v.w;
+            }
+            float w[4];
+            taps(u, w);
+            float *sp = a.conv_state + ((size_t)(a.b0 + b) * a.C + n) * 3;
+            float st[3] = {sp[0], sp[1], sp[2]};
+            a.act[(size_t)(a.b0 + b) * a.C + n] = conv_step(st, w, y);
+            sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
+        } else if (n < a.C + a.vd) {
+            a.z[(size_t)(a.b0 + b) * a.vd + (n - a.C)] = y;
+        } else if (n < a.C + a.vd + a.nv) {
+            a.ga[(size_t)(a.b0 + b) * a.nv + (n - a.C - a.vd)] = y;
+        } else {
+            a.gb[(size_t)(a.b0 + b) * a.nv + (n - a.C - a.vd - a.nv)] = y;
+        }
+    }
     template <int RB, int G>
     __device__ __forceinline__ void operator()(int row0, int rows, const WkRows<RB, G> &c, int tid,
                                                const Pre &p) const {
-        if (tid >= rows) return;
+        if (a.B > DN_PREB) {   // more vectors: one thread per (row, vector)
+            for (int t = tid; t < rows * a.B; t += blockDim.x) {
+                const int r = t % rows, b = t / rows;
+                item(row0 + r, b, c.y(r, b));
+            }
+            return;
+        }
+        if (tid >= rows) return;   // up to DN_PREB vectors: one thread per row, prefetched state
         const int n = row0 + tid;
-        float v[DN_MAXB];
-#pragma unroll
-        for (int b = 0; b < DN_MAXB; b++)
-            if (b < a.B) v[b] = c.y(tid, b);
         if (n < a.C) {                       // q, k or v channel: causal conv + SiLU
             float w[4];
-            if (a.conv_bf16) {
-                w[0] = __uint_as_float(p.w[0] << 16);
-                w[1] = __uint_as_float(p.w[0] & 0xffff0000u);
-                w[2] = __uint_as_float(p.w[1] << 16);
-                w[3] = __uint_as_float(p.w[1] & 0xffff0000u);
-            } else {
+            taps(p.w, w);
+            auto step = [&](int b, float st[3]) {
+                float *sp = a.conv_state + ((size_t)(a.b0 + b) * a.C + n) * 3;
+                a.act[(size_t)(a.b0 + b) * a.C + n] = conv_step(st, w, c.y(tid, b));
+                sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
+            };
 #pragma unroll
-                for (int t = 0; t < 4; t++) w[t] = __uint_as_float(p.w[t]);
-            }
-#pragma unroll
-            for (int b = 0; b < DN_MAXB; b++)
+            for (int b = 0; b < DN_PREB; b++)   // the prefetched states
                 if (b < a.B) {
-                    float *sp = a.conv_state + ((size_t)(a.b0 + b) * a.C + n) * 3;
-                    float st[3];
-                    if (b < DN_PREB) {
-                        st[0] = p.st[b][0]; st[1] = p.st[b][1]; st[2] = p.st[b][2];
-                    } else {
-                        st[0] = sp[0]; st[1] = sp[1]; st[2] = sp[2];
-                    }
-                    a.act[(size_t)(a.b0 + b) * a.C + n] = conv_step(st, w, v[b]);
-                    sp[0] = st[0]; sp[1] = st[1]; sp[2] = st[2];
+                    float st[3] = {p.st[b][0], p.st[b][1], p.st[b][2]};
+                    step(b, st);
                 }
         } else if (n < a.C + a.vd) {         // z
-#pragma unroll
-            for (int b = 0; b < DN_MAXB; b++)
-                if (b < a.B) a.z[(size_t)(a.b0 + b) * a.vd + (n - a.C)] = v[b];
+            for (int b = 0; b < a.B; b++) a.z[(size_t)(a.b0 + b) * a.vd + (n - a.C)] = c.y(tid, b);
         } else if (n < a.C + a.vd + a.nv) {  // a
             const int vh = n - a.C - a.vd;
-#pragma unroll
-            for (int b = 0; b < DN_MAXB; b++)
-                if (b < a.B) a.ga[(size_t)(a.b0 + b) * a.nv + vh] = v[b];
+            for (int b = 0; b < a.B; b++) a.ga[(size_t)(a.b0 + b) * a.nv + vh] = c.y(tid, b);
         } else {                             // b
             const int vh = n - a.C - a.vd - a.nv;
-#pragma unroll
-            for (int b = 0; b < DN_MAXB; b++)
-                if (b < a.B) a.gb[(size_t)(a.b0 + b) * a.nv + vh] = v[b];
+            for (int b = 0; b < a.B; b++) a.gb[(size_t)(a.b0 + b) * a.nv + vh] = c.y(tid, b);
         }
     }
 };
 
-template <int RBW, bool NT, int G>
-__global__ __launch_bounds__(1024) void gemv_dn_in(const uint16_t *W, int N, int K, const uint16_t *xp, int Gt,
-                                                   int g0, int B, DnInEpi epi) {
-    vx_gemv_wk_body<RBW, NT, G>(W, N, K, xp, Gt, g0, B, epi);
+template <int RB, int G>
+__global__ __launch_bounds__(VX_WK_NW * 64) void gemv_dn_in(WkWeights wt, int N, int K, const uint16_t *xp, int Gt,
+                                                           int g0, int B, DnInEpi epi) {
+    vx_gemv_wk_body<RB, G>(wt, N, K, xp, Gt, g0, B, epi);
 }
 
 __global__ void advance_pos_kernel(int *pos, int B) {
@@ -226,13 +254,13 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
 
     if (!d->x_packed && vx_pack(ctx, d->x, (size_t)H, B, H, xp)) return -1;
     const int Gt = vx_pack_groups(B);
-    for (int g0 = 0; g0 < Gt; g0 += 3) {   // passes of up to three groups (15 vectors) over W_in
-        const int G = g0 + 3 <= Gt ? 3 : Gt - g0, b0 = g0 * VX_PACK_GV;
+    for (int g0 = 0; g0 < Gt; g0 += VX_PASS_G) {   // one pass over W_in up to 13 groups (65 vectors)
+        const int b0 = g0 * VX_PACK_GV, G = vx_pass_groups(B, b0);
         const int Bp = B - b0 < G * VX_PACK_GV ? B - b0 : G * VX_PACK_GV;
         const DnInArgs ea = {Bp, C, vd, nv, d->conv_state, d->conv_w, d->conv_w_dtype == VX27_BF16, act, z, ga, gb,
                              b0};
         const WkPlan wp = vx_gemv_wk_plan(Nin, H, ctx->n_cu, G);
-        VX_WK_DISPATCH(ctx, gemv_dn_in, wp, d->w_in, Nin, H, xp, Gt, g0, Bp, (DnInEpi{ea}));
+        VX_WK_DISPATCH(ctx, gemv_dn_in, wp, (WkWeights{d->w_in, 0}), Nin, H, xp, Gt, g0, Bp, (DnInEpi{ea}));
     }
 
     DnArgs ra = {};
@@ -356,7 +384,8 @@ extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_
     float *gb = (float *)p; p += g_b;
     float *o = (float *)p; p += o_b;
     uint16_t *op = (uint16_t *)p; p += pk_o;
-    // [qkv | z | a | b] = W_in x for all B*T tokens (one pass over W_in per 15 tokens)
+    // [qkv | z | a | b] = W_in x for all B*T tokens (one pass over W_in per 65
+    // tokens; each row summed in the same order as in a decode step)
     if (vx_pack(ctx, d->x, (size_t)H, R, H, xp)) return -1;
     if (vx_gemv_store(ctx, d->w_in, Nin, H, xp, R, y, (size_t)Nin)) return -1;
     const size_t ys = (size_t)Nin * 4;
