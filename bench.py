@@ -66,10 +66,22 @@ ROOT = os.path.dirname(os.path.abspath(__file__))
 sys.path.insert(0, ROOT)
 
 HBM_PEAK = 8.0e12           # bytes/s, MI355X
-# HBM bytes per gqa_split launch at batch 4, context 131072: FETCH_SIZE (x2, the
-# factor a plain copy kernel of known size gives) + WRITE_SIZE, rocprofv3 --pmc
-# runs of this script, summarised in profiles/c5_decode_step_pmc.txt
-GQA_SPLIT_TRAFFIC_B4_L131072 = 2.1851e9
+# rocprofv3 --pmc summary of this script's default workload (FETCH_SIZE and
+# WRITE_SIZE per dispatch, scaled by a copy-kernel calibration); its line
+# "gqa_split (the dominant kernel): traffic = T B per launch" gives the
+# roofline's `traffic`
+PMC_SUMMARY = os.path.join(ROOT, "profiles", "c5_decode_step_pmc.txt")
+
+
+def measured_traffic(kernel="gqa_split"):
+    """HBM bytes per launch of `kernel` from the committed PMC summary, or None."""
+    import re
+    try:
+        txt = open(PMC_SUMMARY).read()
+    except OSError:
+        return None
+    m = re.search(re.escape(kernel) + r" \(the dominant kernel\): traffic = ([0-9.eE+]+) B per launch", txt)
+    return float(m.group(1)) if m else None
 METRIC = "mixer µs/token decode (B=1..64) + % HBM roofline; prefill tok/s + MFMA util"
 
 
@@ -730,7 +742,7 @@ def main():
                   "deltanet_layers": 48, "gqa_layers": 16, "deltanet_v_heads": 48, "weights": "bf16",
                   "kv_cache": "bf16", "state": "fp32"}
         kbytes, kus = res["kernel_alg_bytes"], res["kernel_us"]
-        traffic = GQA_SPLIT_TRAFFIC_B4_L131072 if args.context == 131072 else None
+        traffic = measured_traffic() if args.context == 131072 else None
         step_frac = res["step_GBs"] * 1e9 / HBM_PEAK
         extra["c5_step"] = {k: v for k, v in res.items() if k != "cpu"}
         extra["c5_step"]["step_roofline_frac"] = round(step_frac, 4)
