@@ -31,9 +31,11 @@ size_t vx_pack_bytes(int K, int B);
 int vx_pack(vx27_hip_ctx *ctx, const float *x, size_t x_stride, int B, int K, uint16_t *packed);
 // y[b*y_stride + n] = sum over k of W[n][k] x_b[k] for tiled W and a packed x
 // of B vectors (one pass over W for up to 65 vectors; passes of 13 groups
-// beyond).  Each row's sum order is the same for any B.
+// beyond).  Each row's sum order is the same for any B.  y_zeroed: y holds
+// zeros (written by an earlier kernel on the stream), so the rows may be
+// added in two halves.
 int vx_gemv_store(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const uint16_t *packed, int B, float *y,
-                  size_t y_stride);
+                  size_t y_stride, bool y_zeroed = false);
 
 // Part p (0 = hi, 1 = mid, 2 = lo) of the exact three-way bf16 split of x:
 // hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid); each difference

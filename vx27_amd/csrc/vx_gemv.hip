@@ -66,43 +66,45 @@ __global__ __launch_bounds__(64) void pack_w(const uint16_t *W, int K, uint16_t 
 
 template <int RB, int G>
 __global__ __launch_bounds__(VX_WK_NW * 64) void gemv_wk_store(WkWeights wt, int N, int K, const uint16_t *xp,
-                                                              int Gt, int g0, int B, WkStore epi) {
-    vx_gemv_wk_body<RB, G>(wt, N, K, xp, Gt, g0, B, epi);
+                                                              int Gt, int g0, int B, int halves, WkStore epi) {
+    vx_gemv_wk_body<RB, G>(wt, N, K, xp, Gt, g0, B, halves, epi);
 }
 
 }  // namespace
 
-WkPlan vx_gemv_wk_plan(int N, int K, int n_cu, int G) {
+WkPlan vx_gemv_wk_plan(int N, int K, int n_cu, int G, bool allow_halves) {
     (void)K;
     const int nb = N / 16;
-    WkPlan best = {0, G, 0};
+    WkPlan best = {0, G, 0, 1};
     double best_t = 0.0;
     for (int single = 1; single >= 0 && best.rb == 0; single--)
-        for (int rb = 1; rb <= vx_wk_max_rb(G); rb++) {
-            const int wgs = (nb + rb - 1) / rb;
-            if (single && wgs > n_cu) continue;
-            // CU time ~ rounds x (rb weight tiles + G operand tiles per
-            // k-step, an operand tile from L2 costing about a quarter of a
-            // weight tile from HBM); ties keep the smaller rb
-            const double t = (double)((wgs + n_cu - 1) / n_cu) * (rb + 0.25 * G);
-            if (best.rb == 0 || t < best_t - 1e-9) {
-                best_t = t;
-                best = {rb, G, wgs};
+        for (int halves = 1; halves <= (allow_halves ? 2 : 1); halves++)
+            for (int rb = 1; rb <= vx_wk_max_rb(G); rb++) {
+                const int wgs = halves * ((nb + rb - 1) / rb);
+                if (single && wgs > n_cu) continue;
+                // CU time ~ rounds x (rb weight tiles + G operand tiles per
+                // k-step, an operand tile from L2 costing about a quarter of
+                // a weight tile from HBM) x the share of the k-steps; ties
+                // keep whole workgroups, then the smaller rb
+                const double t = (double)((wgs + n_cu - 1) / n_cu) * (rb + 0.25 * G) / halves;
+                if (best.rb == 0 || t < best_t - 1e-9) {
+                    best_t = t;
+                    best = {rb, G, wgs, halves};
+                }
             }
-        }
     return best;
 }
 
 int vx_gemv_store(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const uint16_t *packed, int B, float *y,
-                  size_t y_stride) {
+                  size_t y_stride, bool y_zeroed) {
     VX_REQUIRE(N > 0 && N % 16 == 0 && K > 0 && K % 32 == 0 && B >= 1,
                "gemv: N must be a multiple of 16, K of 32, B >= 1 (N=%d K=%d B=%d)", N, K, B);
     const int Gt = vx_pack_groups(B);
     for (int g0 = 0; g0 < Gt; g0 += VX_PASS_G) {   // one pass up to 13 groups (65 vectors)
         const int b0 = g0 * VX_PACK_GV, G = vx_pass_groups(B, b0);
         const int Bp = std::min(B - b0, G * VX_PACK_GV);
-        const WkPlan p = vx_gemv_wk_plan(N, K, ctx->n_cu, G);
-        VX_WK_DISPATCH(ctx, gemv_wk_store, p, (WkWeights{W, 0}), N, K, packed, Gt, g0, Bp,
+        const WkPlan p = vx_gemv_wk_plan(N, K, ctx->n_cu, G, y_zeroed);
+        VX_WK_DISPATCH(ctx, gemv_wk_store, p, (WkWeights{W, 0}), N, K, packed, Gt, g0, Bp, p.halves,
                        (WkStore{y, y_stride, b0}));
     }
     return 0;
@@ -143,7 +145,7 @@ extern "C" int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, i
         const int Bp = std::min(B - b0, VX_PASS_G * VX_PACK_GV), G = vx_pack_groups(Bp);
         if (vx_pack(ctx, x + (size_t)b0 * x_stride, x_stride, Bp, K, packed)) return -1;
         const WkPlan p = vx_gemv_wk_plan(N, K, ctx->n_cu, G);
-        VX_WK_DISPATCH(ctx, gemv_wk_store, p, (WkWeights{W, 1}), N, K, packed, G, 0, Bp,
+        VX_WK_DISPATCH(ctx, gemv_wk_store, p, (WkWeights{W, 1}), N, K, packed, G, 0, Bp, p.halves,
                        (WkStore{y, y_stride, b0}));
     }
     return 0;

@@ -9,11 +9,15 @@
 // (one pass over the weights for up to 65 vectors).  Each wave keeps a ring
 // of D operand sets: the loads of its next D - 1 k-steps are in flight
 // while the MFMAs of the current one run, so that a workgroup keeps about
-// 8 D (RB + G) KiB of loads outstanding.  The 8 wave partials are summed in
-// LDS in wave order, then the three bf16 parts of each vector (hi + mid +
-// lo), and the epilogue gets whole rows: no split-K partials in memory and
-// no second kernel.  A row's sum order is fixed by the 8-wave split alone,
-// so it is the same whatever RB, D or the number of vectors in the pass.
+// 8 D (RB + G) KiB of loads outstanding.  A row's value is fixed as
+//   y = y0 + y1,   yh = (hi_h + mid_h) + lo_h,
+// where hi_h, mid_h, lo_h are the column sums of waves 4h .. 4h+3 in wave
+// order: the 8 partials are summed in LDS as two halves.  A plain-store
+// epilogue may instead run the two halves as two workgroups of 4 waves
+// that add y0 and y1 into a zeroed output with fp32 atomics: two addends
+// commute, so the bits are the same, and the finer grid fills the CUs
+// where whole rows would leave some idle.  The sum order is the same
+// whatever RB, D, the halves or the number of vectors in the pass.
 // (A split of K over workgroups, whose last arrival sums the slices, was
 // measured slower on every projection shape of the model, with or without
 // device-scope fences.)
@@ -72,15 +76,20 @@ struct WkWeights {
 };
 
 // Summed rows handed to an epilogue: y(r, b) for local row r < rows and
-// vector b < B of the pass (its groups g0 .. g0+G-1 of the packed operand).
+// vector b < B of the pass (its groups g0 .. g0+G-1 of the packed operand):
+// the nh halves' values added in order (nh = 1 in a half workgroup).
 template <int RB, int G>
 struct WkRows {
-    const float (*c)[16 * G + 1];   // [16 RB][16 G + 1]: the MFMA output columns of the G groups
-    int B;                          // vectors in this pass (<= 5 G)
+    const float (*c)[16 * RB][16 * G + 1];   // [2][16 RB][16 G + 1]: each half's MFMA output columns
+    int B;                                   // vectors in this pass (<= 5 G)
+    int nh;                                  // halves summed here (2, or 1 in a half workgroup)
     __device__ __forceinline__ float y(int r, int b) const {
         const int j = b / VX_PACK_GV, bl = b - VX_PACK_GV * j, Bj = min(VX_PACK_GV, B - VX_PACK_GV * j);
-        const float *cr = c[r] + 16 * j;
-        return (cr[bl] + cr[Bj + bl]) + cr[2 * Bj + bl];
+        const float *c0 = c[0][r] + 16 * j;
+        const float y0 = (c0[bl] + c0[Bj + bl]) + c0[2 * Bj + bl];
+        if (nh == 1) return y0;
+        const float *c1 = c[1][r] + 16 * j;
+        return y0 + ((c1[bl] + c1[Bj + bl]) + c1[2 * Bj + bl]);
     }
 };
 
@@ -91,14 +100,19 @@ struct WkRows {
 //       then hides under the loop instead of trailing it)
 //   void operator()(int row0, int rows, const WkRows<RB, G> &, int tid, const Pre &) const
 // One pass covers the B vectors of groups g0 .. g0+G-1 of a packed operand
-// with Gt groups in all; grid ceil(N / 16 RB), block 512.
+// with Gt groups in all.  halves = 1: grid ceil(N / 16 RB), block 512;
+// halves = 2: grid 2 ceil(N / 16 RB), block 256, workgroup 2i + h running
+// waves 4h .. 4h+3 of row group i (the epilogue then gets only its half).
 template <int RB, int G, class Epi>
 __device__ __forceinline__ void vx_gemv_wk_body(const WkWeights &wt, int N, int K, const uint16_t *xp, int Gt,
-                                                int g0, int B, const Epi &epi) {
+                                                int g0, int B, int halves, const Epi &epi) {
     constexpr int NW = VX_WK_NW, D = vx_wk_depth(RB, G);
     const int tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-    const int rb0 = blockIdx.x * RB, nb = N / 16;
+    const int h = halves == 2 ? (int)(blockIdx.x & 1) : 0;
+    const int nwp = halves == 2 ? NW / 2 : NW;   // waves in this workgroup
+    const int vw = h * (NW / 2) + wave;          // the wave's place in the 8-wave split
+    const int rb0 = (halves == 2 ? (int)(blockIdx.x >> 1) : (int)blockIdx.x) * RB, nb = N / 16;
     const int nks = K / 32, kg = vx_gemv_kg(K);
     const int k0 = 0, k1 = nks;
     const int row0 = rb0 * 16;
@@ -139,8 +153,8 @@ __device__ __forceinline__ void vx_gemv_wk_body(const WkWeights &wt, int N, int 
     // are uniform: s is a wave constant)
     vx_bf16x8_t a[D][RB], b[D][G];
 #pragma unroll
-    for (int d = 0; d < D; d++) load(k0 + wave + d * NW, a[d], b[d]);
-    for (int s = k0 + wave; s < k1; s += D * NW) {   // whole rounds of D k-steps
+    for (int d = 0; d < D; d++) load(k0 + vw + d * NW, a[d], b[d]);
+    for (int s = k0 + vw; s < k1; s += D * NW) {   // whole rounds of D k-steps
 #pragma unroll
         for (int d = 0; d < D; d++) {
             mma(a[d], b[d]);
@@ -150,7 +164,8 @@ __device__ __forceinline__ void vx_gemv_wk_body(const WkWeights &wt, int N, int 
     constexpr int NTL = RB * G;                         // accumulator tiles
     constexpr int RC = NTL < 64 / NW ? NTL : 64 / NW;   // tiles reduced per round (64 KiB of LDS)
     __shared__ vx_floatx4_t red[NW][RC][64];
-    __shared__ float ct[16 * RB][16 * G + 1];
+    __shared__ float ct[2][16 * RB][16 * G + 1];
+    const int nh = nwp / 4;   // halves summed in this workgroup
 #pragma unroll
     for (int t0 = 0; t0 < NTL; t0 += RC) {
         if (t0) __syncthreads();   // the previous round's partials are read out
@@ -158,24 +173,26 @@ __device__ __forceinline__ void vx_gemv_wk_body(const WkWeights &wt, int N, int 
         for (int q = 0; q < RC; q++)
             if (t0 + q < NTL) red[wave][q][lane] = acc[(t0 + q) / G][(t0 + q) % G];
         __syncthreads();
-        for (int t = tid; t < RC * 64; t += NW * 64) {   // (tile t0 + q, lane l): wave partials in order
+        for (int t = tid; t < RC * 64; t += nwp * 64) {   // (tile t0 + q, lane l): each half's 4 partials in order
             const int q = t >> 6, l = t & 63, g = l >> 4, m = l & 15;
             const int rj = t0 + q;
             if (rj >= NTL) continue;
             const int r = rj / G, j = rj % G;
-            vx_floatx4_t v = red[0][q][l];
+            for (int hh = 0; hh < nh; hh++) {
+                const vx_floatx4_t v = ((red[4 * hh][q][l] + red[4 * hh + 1][q][l]) + red[4 * hh + 2][q][l]) +
+                                       red[4 * hh + 3][q][l];
+                // lane (g,m) holds C[4g+i][m]: row 16r + 4g + i, column 16j + m
 #pragma unroll
-            for (int w = 1; w < NW; w++) v += red[w][q][l];
-            // lane (g,m) holds C[4g+i][m]: row 16r + 4g + i, column 16j + m
-#pragma unroll
-            for (int i = 0; i < 4; i++) ct[16 * r + 4 * g + i][16 * j + m] = v[i];
+                for (int i = 0; i < 4; i++) ct[hh][16 * r + 4 * g + i][16 * j + m] = v[i];
+            }
         }
     }
     __syncthreads();
-    epi(row0, rows, WkRows<RB, G>{ct, B}, tid, pre);
+    epi(row0, rows, WkRows<RB, G>{ct, B, nh}, tid, pre);
 }
 
-// Epilogue: y[(b0 + b)*y_stride + n] for every row n of the workgroup.
+// Epilogue: y[(b0 + b)*y_stride + n] for every row n of the workgroup
+// (added with an atomic in a half workgroup: y must then start at zero).
 struct WkStore {
     float *y;
     size_t y_stride;
@@ -184,21 +201,25 @@ struct WkStore {
     __device__ __forceinline__ Pre prefetch(int, int, int) const { return {}; }
     template <int RB, int G>
     __device__ __forceinline__ void operator()(int row0, int rows, const WkRows<RB, G> &c, int tid, const Pre &) const {
-        for (int t = tid; t < rows * c.B; t += VX_WK_NW * 64) {
+        for (int t = tid; t < rows * c.B; t += c.nh * 4 * 64) {
             const int r = t % rows, b = t / rows;
-            y[(size_t)(b0 + b) * y_stride + row0 + r] = c.y(r, b);
+            float *yp = y + (size_t)(b0 + b) * y_stride + row0 + r;
+            if (c.nh == 1) atomicAdd(yp, c.y(r, b));
+            else *yp = c.y(r, b);
         }
     }
 };
 
 // Launch plan for an N x K matrix and a pass of G groups: RB row blocks per
-// workgroup, grid ceil(N / 16 RB).  The plan takes the RB that best
-// balances the CUs in one round of workgroups (several rounds only when no
-// single-round plan exists).
+// workgroup, whole (halves = 1, grid ceil(N / 16 RB)) or split in two half
+// workgroups (halves = 2, twice the grid, only when allow_halves: an
+// epilogue that adds into a zeroed output).  The plan takes the shape that
+// best balances the CUs in one round of workgroups (several rounds only
+// when no single-round plan exists).
 struct WkPlan {
-    int rb, g, grid;
+    int rb, g, grid, halves;
 };
-WkPlan vx_gemv_wk_plan(int N, int K, int n_cu, int G);
+WkPlan vx_gemv_wk_plan(int N, int K, int n_cu, int G, bool allow_halves = false);
 
 // every (RB, G) instance: RB = 1 .. vx_wk_max_rb(G)
 #define VX_WK_RB_G1(X, ...)                                                                                      \
@@ -223,10 +244,12 @@ WkPlan vx_gemv_wk_plan(int N, int K, int n_cu, int G);
 #define VX_WK_ALL(X, ...)                                                                                        \
     VX_WK_RB_G1(X, __VA_ARGS__) VX_WK_RB_G2(X, __VA_ARGS__) VX_WK_RB_G3(X, __VA_ARGS__) VX_WK_RB_BIG(X, __VA_ARGS__)
 
-// Launch KERNEL<rb, g>(args...) for a plan (grid plan.grid, block 512).
-#define VX_WK_CASE(R, GG, ctx, KERNEL, p, ...)                                                                  \
-    case GG * 64 + R:                                                                                           \
-        VX_LAUNCH_NAMED(ctx, #KERNEL, (KERNEL<R, GG>), dim3((unsigned)p.grid), dim3(VX_WK_NW * 64), __VA_ARGS__); \
+// Launch KERNEL<rb, g>(args...) for a plan (grid plan.grid, block 512 or
+// 256 for half workgroups).
+#define VX_WK_CASE(R, GG, ctx, KERNEL, p, ...)                                                                 \
+    case GG * 64 + R:                                                                                          \
+        VX_LAUNCH_NAMED(ctx, #KERNEL, (KERNEL<R, GG>), dim3((unsigned)p.grid),                                 \
+                        dim3(VX_WK_NW * 64 / p.halves), __VA_ARGS__);                                          \
         break;
 #define VX_WK_DISPATCH(ctx, KERNEL, p, ...)                                                   \
     do {                                                                                      \

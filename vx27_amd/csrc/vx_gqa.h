@@ -45,7 +45,8 @@ size_t vx_gqa_scratch_bytes(const vx27_gqa_desc *d);
 // The decode step with caller-provided scratch of vx_gqa_scratch_bytes(d);
 // out_packed (optional) receives the gated attention as the packed operand of
 // the output projection.
-int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uint16_t *out_packed);
+int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uint16_t *out_packed,
+                       float *zero = nullptr, size_t zero_n = 0);
 
 // Looks up the per-device address of the no-allocation decode scratch
 // (vx_gqa_decode.hip); called by vx27_hip_open with the device current.

@@ -283,6 +283,8 @@ struct CombArgs {
     size_t g_ss, g_hs;
     float *out;                  // [B][n_q][256] or NULL
     uint16_t *out_packed;        // optional packed GEMV operand of out (K = n_q*256)
+    float *zero;                 // optional: zero_n floats cleared (the next projection's output)
+    size_t zero_n;
 };
 
 // grid (n_q, B), block 64 nw (nw <= 16 waves, enough for 12 splits a wave):
@@ -294,6 +296,11 @@ constexpr int CB_W = 16, CB_N = 12;
 __global__ __launch_bounds__(1024) void gqa_combine(CombArgs a) {
     const int h = blockIdx.x, b = blockIdx.y, tid = threadIdx.x, lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), nw = blockDim.x >> 6;
+    if (a.zero) {   // this workgroup's share of the range
+        const size_t nwg = (size_t)gridDim.x * gridDim.y, wg = (size_t)b * gridDim.x + h;
+        const size_t lo = a.zero_n * wg / nwg, hi = a.zero_n * (wg + 1) / nwg;
+        for (size_t i = lo + tid; i < hi; i += blockDim.x) a.zero[i] = 0.0f;
+    }
     const int qg = a.n_q / a.n_kv, kvh = h / qg, n = h % qg;
     const size_t base = ((size_t)b * a.n_kv + kvh) * a.n_split;
     __shared__ float4 s_o[CB_W][64];
@@ -446,8 +453,10 @@ size_t vx_gqa_scratch_bytes(const vx27_gqa_desc *d) {
 }
 
 // The decode step with caller-provided scratch of vx_gqa_scratch_bytes(d);
-// out_packed (optional) receives the output as the packed GEMV operand.
-int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uint16_t *out_packed) {
+// out_packed (optional) receives the output as the packed GEMV operand;
+// zero (optional) is cleared by the combine kernel.
+int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uint16_t *out_packed, float *zero,
+                       size_t zero_n) {
     if (gqa_check(d)) return -1;
     RopeTab rt = {};
     if (d->rope_dim > 0 && vx_rope_fill(rt, d->rope_dim, d->rope_theta)) return -1;
@@ -480,6 +489,7 @@ int vx_gqa_decode_into(vx27_hip_ctx *ctx, const vx27_gqa_desc *d, void *scr, uin
     ca.part_o = part_o; ca.part_ml = part_ml; ca.gate = (d->flags & VX27_GQA_NO_GATE) ? nullptr : d->gate;
     ca.g_ss = d->gate_seq_stride; ca.g_hs = d->gate_head_stride; ca.out = d->out;
     ca.out_packed = out_packed;
+    ca.zero = zero; ca.zero_n = zero_n;
     const int cb_waves = std::min(CB_W, (n_split + CB_N - 1) / CB_N);
     VX_LAUNCH(ctx, gqa_combine, dim3(d->n_q, d->B), dim3(64 * cb_waves), ca);
     return 0;

@@ -36,6 +36,8 @@ struct DnInArgs {
     float *act, *z;
     float *ga, *gb;   // the a and b rows, [B][nv] each (the step kernel maps them to the gates)
     int b0;   // first vector of this pass (the pass's B vectors are b0 .. b0+B-1)
+    float *zero;    // optional: zero_n floats cleared (the output out_proj adds its halves into)
+    size_t zero_n;
 };
 
 // Epilogue of the stacked DeltaNet input projection [qkv | z | a | b]
@@ -127,6 +129,11 @@ struct DnInEpi {
     template <int RB, int G>
     __device__ __forceinline__ void operator()(int row0, int rows, const WkRows<RB, G> &c, int tid,
                                                const Pre &p) const {
+        if (a.zero) {   // this workgroup's share of the range to clear
+            const size_t nwg = gridDim.x, wg = blockIdx.x;
+            const size_t lo = a.zero_n * wg / nwg, hi = a.zero_n * (wg + 1) / nwg;
+            for (size_t i = lo + tid; i < hi; i += blockDim.x) a.zero[i] = 0.0f;
+        }
         if (a.B > DN_PREB) {   // more vectors: one thread per (row, vector)
             for (int t = tid; t < rows * a.B; t += blockDim.x) {
                 const int r = t % rows, b = t / rows;
@@ -165,7 +172,7 @@ struct DnInEpi {
 template <int RB, int G>
 __global__ __launch_bounds__(VX_WK_NW * 64) void gemv_dn_in(WkWeights wt, int N, int K, const uint16_t *xp, int Gt,
                                                            int g0, int B, DnInEpi epi) {
-    vx_gemv_wk_body<RB, G>(wt, N, K, xp, Gt, g0, B, epi);
+    vx_gemv_wk_body<RB, G>(wt, N, K, xp, Gt, g0, B, 1, epi);   // whole rows (the conv needs them)
 }
 
 __global__ void advance_pos_kernel(int *pos, int B) {
@@ -257,8 +264,10 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     for (int g0 = 0; g0 < Gt; g0 += VX_PASS_G) {   // one pass over W_in up to 13 groups (65 vectors)
         const int b0 = g0 * VX_PACK_GV, G = vx_pass_groups(B, b0);
         const int Bp = B - b0 < G * VX_PACK_GV ? B - b0 : G * VX_PACK_GV;
+        // the first pass clears out, so that out_proj may add its two halves
+        // into it (the same bits as whole rows)
         const DnInArgs ea = {Bp, C, vd, nv, d->conv_state, d->conv_w, d->conv_w_dtype == VX27_BF16, act, z, ga, gb,
-                             b0};
+                             b0, g0 == 0 ? d->out : nullptr, (size_t)B * H};
         const WkPlan wp = vx_gemv_wk_plan(Nin, H, ctx->n_cu, G);
         VX_WK_DISPATCH(ctx, gemv_dn_in, wp, (WkWeights{d->w_in, 0}), Nin, H, xp, Gt, g0, Bp, (DnInEpi{ea}));
     }
@@ -278,7 +287,7 @@ extern "C" int vx27_hip_dn_layer_decode(vx27_hip_ctx *ctx, const vx27_dn_layer_d
     }
     if (vx_dn_recurrence(ctx, ra)) return -1;
 
-    return vx_gemv_store(ctx, d->w_out, H, vd, op, B, d->out, (size_t)H);
+    return vx_gemv_store(ctx, d->w_out, H, vd, op, B, d->out, (size_t)H, true);
 }
 
 extern "C" int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer_desc *d) {
@@ -319,8 +328,9 @@ extern "C" int vx27_hip_gqa_layer_decode(vx27_hip_ctx *ctx, const vx27_gqa_layer
     if (vx_gemv_store(ctx, d->w_qkv, Nqkv, H, xp, B, y, (size_t)Nqkv)) return -1;
     g.q = y; g.gate = y + hd; g.k_new = y + Nq; g.v_new = y + Nq + (size_t)d->n_kv * hd;
     g.out = nullptr;
-    if (vx_gqa_decode_into(ctx, &g, gscr, ap)) return -1;
-    return vx_gemv_store(ctx, d->w_o, H, Ka, ap, B, d->out, (size_t)H);
+    // the combine kernel clears out for o_proj's two halves
+    if (vx_gqa_decode_into(ctx, &g, gscr, ap, d->out, (size_t)B * H)) return -1;
+    return vx_gemv_store(ctx, d->w_o, H, Ka, ap, B, d->out, (size_t)H, true);
 }
 
 extern "C" int vx27_hip_advance_pos(vx27_hip_ctx *ctx, int *pos, int B) {
