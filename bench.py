@@ -335,11 +335,38 @@ def bench_dn_recurrent(ctx, steps=2000, cpu=True):
     ctx.sync()
     graph_step = (time.perf_counter() - t0) / (5 * 200)
     L.check(L.lib().vx27_hip_graph_destroy(g), "graph_destroy")
+    # the floor of a one-step call: the same 200 launches of the smallest
+    # kernel of the library (a one-workgroup 64-byte fill), eager and graphed
+    tiny = ctx.buf(64)
+    fill = L.lib().vx27_hip_memset
+    for _ in range(20):
+        L.check(fill(ctx.h, tiny.ptr, 0, 64), "memset")
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(200):
+        L.check(fill(ctx.h, tiny.ptr, 0, 64), "memset")
+    ctx.sync()
+    floor_eager = (time.perf_counter() - t0) / 200
+    ctx.graph_begin()
+    for _ in range(200):
+        L.check(fill(ctx.h, tiny.ptr, 0, 64), "memset")
+    g = ctx.graph_end()
+    ctx.graph_launch(g)
+    ctx.sync()
+    t0 = time.perf_counter()
+    for _ in range(5):
+        ctx.graph_launch(g)
+    ctx.sync()
+    floor_graph = (time.perf_counter() - t0) / (5 * 200)
+    L.check(L.lib().vx27_hip_graph_destroy(g), "graph_destroy")
+    tiny.free()
     k_us = sum(ms for _, ms in kern.values()) / 200 * 1e3
     res = {"workload": f"dn_recurrent B=1 heads=16 {steps} steps",
            "us_per_step_resident": multi / steps * 1e6,
            "us_per_step_streamed": single / steps * 1e6,
            "us_per_step_streamed_graph": graph_step * 1e6,
+           "launch_floor_us": {"eager": floor_eager * 1e6, "graph": floor_graph * 1e6,
+                               "kernel": "vx_fill_kernel, 1 workgroup, 64 bytes"},
            "kernel_us_streamed": k_us,
            "kernels_streamed": {k: v[0] / 200 for k, v in kern.items() if v[0]},
            "alg_bytes_per_step_streamed": C1_BYTES_PER_STEP,
@@ -796,7 +823,8 @@ def main():
         extra["c1_dn_recurrent"] = r
         log(f"  dn_recurrent: {r['us_per_step_resident']:.2f} us/step (state resident, one call), "
             f"{r['us_per_step_streamed']:.2f} us/step (per-step calls; kernel {r['kernel_us_streamed']:.2f} us, "
-            f"{100 * r['hbm_frac_streamed_kernel']:.1f}% HBM)")
+            f"{100 * r['hbm_frac_streamed_kernel']:.1f}% HBM; a one-workgroup fill launch takes "
+            f"{r['launch_floor_us']['eager']:.2f} us eager, {r['launch_floor_us']['graph']:.2f} graphed)")
         if cpu:
             log(f"  dn_recurrent cpu: exact {r['cpu_exact']['value']:.1f} us/step, avx2 "
                 f"{r['cpu_avx2']['value']:.1f} us/step ({r['cpu_avx2']['kind']})")
