@@ -564,12 +564,17 @@ struct PrepTArgs {
     int T, nqk, nv, NC;
     const uint16_t *q, *k;          // hi parts [B][T][nqk][128] bf16
     const uint16_t *ql, *kl;        // lo parts as rows
-    const float *v;                 // [B][T][nv][128] fp32
+    const float *v;                 // [B][T][nv][128] fp32 (unless VCONV)
     const float *a, *b;             // [B][T][nv]
     const float *A_log, *dt_bias;   // [nv]
     char *rec;                      // [B][nv][NC] records of TREC bytes
     char *krec;                     // [B][nqk][NC] K records of krec_bytes
     int krec_bytes;
+    // VCONV: v = silu(causal conv) of the v channels of x [B][T][C], formed
+    // here (state before token 0 in conv_state [B][C][3], taps conv_w [C][4])
+    int C, w_bf16;
+    const float *x, *conv_state;
+    const void *conv_w;
 };
 
 // bf16 hi and lo of 8 floats
@@ -661,6 +666,9 @@ static_assert(2 * TN_TOTAL <= 160 * 1024, "two workgroups per CU");
 //            by level (fp32 MFMA)
 //   phase 5  T' = T diag(beta) (hi/lo in registers); -T'' = -T' diag(sk)
 //            as hi/lo tiles; V through LDS transposed, Ut = T' V on MFMA
+//            (with VCONV the V rows are the causal conv + SiLU of x, formed
+//            here: the glue writes no v rows)
+template <bool VCONV>
 __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
     constexpr bool LO = true;   // (the glue's q, k, v always come with lo parts)
     const int c = blockIdx.x, qh = blockIdx.y, b = blockIdx.z;
@@ -941,7 +949,14 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
             __syncthreads();
         }
         // ---- phase 5: T' = T diag(beta), row block wave, in registers (the
-        // upper blocks of T hold stale bytes: selected away); -T'' tiles
+        // upper blocks of T hold stale bytes: selected away); -T'' tiles.
+        // With VCONV the v channels' conv taps go to the level products'
+        // LDS (free after phase 4) for the V rows below.
+        if (VCONV && tid < HD) {
+            float w4[4];
+            load_conv_w(p.conv_w, p.w_bf16, (size_t)2 * p.nqk * HD + (size_t)vh * HD + tid, w4);
+            *(float4 *)&M_t[tid * 4] = make_float4(w4[0], w4[1], w4[2], w4[3]);
+        }
         bf16x8_t tph[2], tpl[2];
 #pragma unroll
         for (int ks = 0; ks < 2; ks++) {
@@ -973,19 +988,68 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
         __syncthreads();   // A, T and the P staging are read out
         // V rows (hi to R0, with LO the lo parts of the fp32 values to R1),
         // thread (row tid/16 + 16 j, 8 columns), then transposed
+        if (VCONV) {
+            // thread (rows 4 (tid/16) .. +3, 8 v channels), 2 channels at a
+            // time: the window of tokens t-3 .. t+3 (earlier than token 0: the
+            // conv state; past the end: clamped, and the rows zeroed) as
+            // 8-byte loads, the taps from LDS, conv + SiLU per token
+            // (vx27_qfwd.c:118-131)
+            const size_t ch0 = (size_t)2 * p.nqk * HD + (size_t)vh * HD + 8 * seg;
+            const int r0 = 4 * (tid >> 4);
+            int t = t0 + r0;
+            asm volatile("" : "+v"(t));   // the window's addresses stay inside the value-head loop
+#pragma unroll 1
+            for (int qt = 0; qt < 4; qt++) {
+                float xw[7][2];
+                const float *xr = p.x + (size_t)b * p.T * p.C + ch0 + 2 * qt;
 #pragma unroll
-        for (int j = 0; j < 4; j++) {
-            const int r = (tid >> 4) + 16 * j;
-            const bool ok = r < nvalid;
-            const size_t off = (((size_t)b * p.T + t0 + r) * p.nv + vh) * HD + 8 * seg;
-            const float *vf = p.v + off;
-            const float4 a0 = ok ? *(const float4 *)vf : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float4 a1 = ok ? *(const float4 *)(vf + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-            const float f[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-            uint4 h, l;
-            split8(f, h, l);
-            *(uint4 *)&vh_rows[r * RP + 8 * seg] = h;
-            *(uint4 *)&vl_rows[r * RP + 8 * seg] = l;
+                for (int i = 0; i < 7; i++) {
+                    const float2 v = *(const float2 *)(xr + (size_t)min(max(t - 3 + i, 0), p.T - 1) * p.C);
+                    xw[i][0] = v.x; xw[i][1] = v.y;
+                }
+                if (t < 3) {   // tokens before 0: state slots t-3+i+3 (oldest first)
+                    const float *sp = p.conv_state + ((size_t)b * p.C + ch0 + 2 * qt) * 3;
+#pragma unroll
+                    for (int i = 0; i < 3; i++)
+                        if (t - 3 + i < 0) { xw[i][0] = sp[t + i]; xw[i][1] = sp[3 + t + i]; }
+                }
+                float w[2][4];
+#pragma unroll
+                for (int e = 0; e < 2; e++) {
+                    const float4 wv = *(const float4 *)&M_t[(8 * seg + 2 * qt + e) * 4];
+                    w[e][0] = wv.x; w[e][1] = wv.y; w[e][2] = wv.z; w[e][3] = wv.w;
+                }
+#pragma unroll
+                for (int j = 0; j < 4; j++) {
+                    const bool ok = r0 + j < nvalid;
+                    float f[2];
+#pragma unroll
+                    for (int e = 0; e < 2; e++) {
+                        float cs[3] = {xw[j][e], xw[j + 1][e], xw[j + 2][e]};
+                        f[e] = ok ? conv_step(cs, w[e], xw[j + 3][e]) : 0.0f;
+                    }
+                    const uint32_t h = pack2(f[0], f[1]);
+                    const uint16_t *hs = (const uint16_t *)&h;
+                    const uint32_t l = pack2(f[0] - vx_bf16_to_f32(hs[0]), f[1] - vx_bf16_to_f32(hs[1]));
+                    *(uint32_t *)&vh_rows[(r0 + j) * RP + 8 * seg + 2 * qt] = h;
+                    *(uint32_t *)&vl_rows[(r0 + j) * RP + 8 * seg + 2 * qt] = l;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int r = (tid >> 4) + 16 * j;
+                const bool ok = r < nvalid;
+                const size_t off = (((size_t)b * p.T + t0 + r) * p.nv + vh) * HD + 8 * seg;
+                const float *vf = p.v + off;
+                const float4 a0 = ok ? *(const float4 *)vf : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float4 a1 = ok ? *(const float4 *)(vf + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float f[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                uint4 h, l;
+                split8(f, h, l);
+                *(uint4 *)&vh_rows[r * RP + 8 * seg] = h;
+                *(uint4 *)&vl_rows[r * RP + 8 * seg] = l;
+            }
         }
         __syncthreads();
         tr_rows(vh_rows, vT_h, tid);
@@ -2165,11 +2229,16 @@ static bool dn_prefill_is_exact(const vx27_dn_prefill_desc *d) {
 }
 // The glue's outputs: q, k hi rows and v as bf16 rows; the split form adds
 // the q and k lo rows and keeps v in fp32 instead.
-static size_t vx_dn_glue_bytes(int B, int T, int nqk, int nv, bool x3) {
+static size_t vx_dn_glue_bytes(int B, int T, int nqk, int nv, bool x3, bool vconv) {
     const size_t rows = (size_t)B * T;
     const size_t qd = (size_t)nqk * HD, vd = (size_t)nv * HD;
-    return x3 ? al256(rows * 4 * qd * sizeof(uint16_t)) + rows * vd * sizeof(float)
+    return x3 ? al256(rows * 4 * qd * sizeof(uint16_t)) + (vconv ? 0 : rows * vd * sizeof(float))
               : rows * (2 * qd + vd) * sizeof(uint16_t);
+}
+// The T-record form with the conv forms v from x itself (prept), so the glue
+// writes no v rows: split products, the conv, and 16-byte aligned x rows.
+static bool dn_prefill_vconv(const vx27_dn_prefill_desc *d) {
+    return !(d->flags & VX27_DN_BF16) && (d->flags & VX27_DN_CONV) && ((uintptr_t)d->x & 15) == 0;
 }
 // Bytes of one K record (K^T operand tiles, hi and, with lo parts, lo).
 static size_t vx_dn_krec_bytes(bool lo) { return lo ? 2 * K_LO : K_LO; }
@@ -2184,7 +2253,7 @@ size_t vx_dn_prefill_scratch(const vx27_dn_prefill_desc *d) {
     const bool x3 = !(d->flags & VX27_DN_BF16);
     const size_t n_rec = (size_t)d->B * d->nv * NC;
     const bool glue = (d->flags & (VX27_DN_CONV | VX27_DN_PRE_RMS | VX27_DN_PRE_L2)) != 0;
-    const size_t glue_bytes = glue ? vx_dn_glue_bytes(d->B, d->T, d->nqk, d->nv, x3) : 0;
+    const size_t glue_bytes = glue ? vx_dn_glue_bytes(d->B, d->T, d->nqk, d->nv, x3, dn_prefill_vconv(d)) : 0;
     if (x3 && glue)
         return al256(n_rec * TREC) + al256((size_t)d->B * d->nqk * NC * vx_dn_krec_bytes(true)) + glue_bytes;
     return al256(n_rec * (x3 ? XREC : REC)) + al256(n_rec * sizeof(float)) + glue_bytes;
@@ -2291,21 +2360,25 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
     const uint16_t *q = d->q, *k = d->k, *v = d->v;
     const uint16_t *ql = nullptr, *kl = nullptr;
     const float *v32 = nullptr;
+    // the T form with the conv forms v itself from x (16-byte rows needed)
+    const bool vconv = trec && dn_prefill_vconv(d);
+    auto conv_state_update = [&]() -> int {   // after every reader of the old state
+        const size_t nthr = (size_t)d->B * C;
+        VX_LAUNCH(ctx, dnp_conv_state, dim3((unsigned)((nthr + 255) / 256)), dim3(256), d->B, d->T, C, d->x,
+                  d->conv_state);
+        return 0;
+    };
     if (glue) {   // conv and pre-norms in fp32, then q, k as bf16 (hi, and lo for the split form), v
         uint16_t *qo = (uint16_t *)glue_buf, *ko = qo + rows * qd;
         uint16_t *qol = x3 ? ko + rows * qd : nullptr, *kol = x3 ? qol + rows * qd : nullptr;
         uint16_t *vo = x3 ? nullptr : ko + rows * qd;
-        float *vo32 = x3 ? (float *)(glue_buf + al256(rows * 4 * qd * sizeof(uint16_t))) : nullptr;
+        float *vo32 = x3 && !vconv ? (float *)(glue_buf + al256(rows * 4 * qd * sizeof(uint16_t))) : nullptr;
         GlueInArgs ga{d->B, d->T, d->nqk, d->nv, C, d->flags, d->conv_w_dtype == VX27_BF16, d->x, d->conv_state,
                       d->conv_w, d->q, d->k, d->v, d->norm_w, qo, ko, vo, qol, kol, vo32};
-        const int nh = 2 * d->nqk + d->nv;
+        const int nh = 2 * d->nqk + (vconv ? 0 : d->nv);   // (q, k heads first: with vconv the v heads are skipped)
         const int tblk = (d->T + GT - 1) / GT;
         VX_LAUNCH(ctx, dnp_glue_in, dim3((unsigned)((tblk + 3) / 4), (unsigned)nh, (unsigned)d->B), dim3(256), ga);
-        if (conv) {
-            const size_t nthr = (size_t)d->B * C;
-            VX_LAUNCH(ctx, dnp_conv_state, dim3((unsigned)((nthr + 255) / 256)), dim3(256), d->B, d->T, C, d->x,
-                      d->conv_state);
-        }
+        if (conv && !vconv && conv_state_update()) return -1;
         q = qo; k = ko; v = vo;
         ql = qol; kl = kol; v32 = vo32;
     }
@@ -2314,8 +2387,11 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
     if (trec) {
         char *rec = (char *)scr, *krec = (char *)scr + rec_bytes;
         PrepTArgs pa{d->T, d->nqk, d->nv, NC, q, k, ql, kl, v32, d->a, d->b, d->A_log, d->dt_bias, rec, krec,
-                     (int)krec_one};
-        VX_LAUNCH(ctx, dnp_prept, dim3((unsigned)NC, (unsigned)d->nqk, (unsigned)d->B), dim3(256), pa);
+                     (int)krec_one, C, d->conv_w_dtype == VX27_BF16, d->x, d->conv_state, d->conv_w};
+        const dim3 pg((unsigned)NC, (unsigned)d->nqk, (unsigned)d->B);
+        if (vconv) VX_LAUNCH_NAMED(ctx, "dnp_prept", dnp_prept<true>, pg, dim3(256), pa);
+        else VX_LAUNCH_NAMED(ctx, "dnp_prept", dnp_prept<false>, pg, dim3(256), pa);
+        if (vconv && conv_state_update()) return -1;   // prept read the state before token 0
         ScanTArgs sa{d->T, d->nqk, d->nv, NC, (d->nqk % 8) == 0, q, k, ql, kl, rec, krec, (int)krec_one, d->S, d->out};
         const dim3 sg((unsigned)(d->nv * NSLICE / (two ? 2 : 1)), (unsigned)d->B);
         if (two) VX_LAUNCH_NAMED(ctx, "dnp_scant", dnp_scant<2>, sg, dim3(256), sa);
