@@ -1140,21 +1140,30 @@ __global__ __launch_bounds__(256) void dnp_scant(ScanTArgs p) {
     uint4 kt[2][2], ktl[2][2];              // K^T row blocks 2w, 2w+1 [rb][k-step], hi and lo
     floatx4_t ut[NCB], skc4;
     float sqv, gc;
-    auto rec_of = [&](int cc) { return rec0 + (size_t)cc * TREC; };
-    auto ld_tile = [&](const char *base, size_t off) -> uint4 {
-        const u32x4_t v = *(g_u32x4 *)(base + off + (size_t)lane * 16);
+    // Buffer loads: the head's records as one resource each, the chunk and
+    // tile offsets in scalar registers, the lane's offset one VGPR, so an
+    // operand load costs no vector instruction (the sizes are checked on
+    // the host: below 2^31 bytes)
+    const __amdgpu_buffer_rsrc_t Rr = __builtin_amdgcn_make_buffer_rsrc((void *)rec0, 0, (int)(p.NC * TREC), 0x00020000);
+    const __amdgpu_buffer_rsrc_t Rk = __builtin_amdgcn_make_buffer_rsrc((void *)krec0, 0, p.NC * p.krec_bytes, 0x00020000);
+    const int lo16 = lane * 16;
+    auto ld_r = [&](int cc, int off) -> uint4 {   // a T-record tile
+        const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(Rr, lo16, cc * (int)TREC + off, 0));
+        return make_uint4(v.x, v.y, v.z, v.w);
+    };
+    auto ld_k = [&](int cc, int off) -> uint4 {   // a K-record tile
+        const u32x4_t v = __builtin_bit_cast(u32x4_t, __builtin_amdgcn_raw_buffer_load_b128(Rk, lo16, cc * p.krec_bytes + off, 0));
         return make_uint4(v.x, v.y, v.z, v.w);
     };
     auto ld_kq = [&](int cc) {
-        const char *kr = krec0 + (size_t)cc * p.krec_bytes;
 #pragma unroll
         for (int rb = 0; rb < 4; rb++) {
-            const size_t o = (size_t)(rb * 4 + wave) * 1024;
-            kA[rb] = ld_tile(kr, K_KA + o);
-            qA[rb] = ld_tile(kr, K_QA + o);
+            const int o = (rb * 4 + wave) * 1024;
+            kA[rb] = ld_k(cc, (int)K_KA + o);
+            qA[rb] = ld_k(cc, (int)K_QA + o);
             if (LO) {
-                kAl[rb] = ld_tile(kr, K_LO + K_KA + o);
-                qAl[rb] = ld_tile(kr, K_LO + K_QA + o);
+                kAl[rb] = ld_k(cc, (int)(K_LO + K_KA) + o);
+                qAl[rb] = ld_k(cc, (int)(K_LO + K_QA) + o);
             }
         }
     };
@@ -1162,31 +1171,30 @@ __global__ __launch_bounds__(256) void dnp_scant(ScanTArgs p) {
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)
             if (ks == 0 || w2) {
-                tp[ks][0] = ld_tile(rec_of(cc), T_TH + (size_t)(wave * 2 + ks) * 1024);
-                tp[ks][1] = ld_tile(rec_of(cc), T_TL + (size_t)(wave * 2 + ks) * 1024);
+                tp[ks][0] = ld_r(cc, (int)T_TH + (wave * 2 + ks) * 1024);
+                tp[ks][1] = ld_r(cc, (int)T_TL + (wave * 2 + ks) * 1024);
             }
 #pragma unroll
         for (int cb = 0; cb < NCB; cb++)
-            ut[cb] = *(g_floatx4 *)(rec_of(cc) + T_UT + ((size_t)(wave * 8 + cb0 + cb) * 64 + lane) * 16);
-        skc4 = *(g_floatx4 *)(rec_of(cc) + T_SC + (16 * wave + 4 * g) * 4);
+            ut[cb] = __builtin_bit_cast(floatx4_t, ld_r(cc, (int)T_UT + (wave * 8 + cb0 + cb) * 1024));
+        skc4 = __builtin_bit_cast(floatx4_t, __builtin_amdgcn_raw_buffer_load_b128(Rr, (16 * wave + 4 * g) * 4, cc * (int)TREC + (int)T_SC, 0));
     };
     auto ld_s = [&](int cc) {
-        const char *kr = krec0 + (size_t)cc * p.krec_bytes;
 #pragma unroll
         for (int r = 0; r < 2; r++)
 #pragma unroll
             for (int ks = 0; ks < 2; ks++) {
-                kt[r][ks] = ld_tile(kr, K_KT + (size_t)((2 * wave + r) * 2 + ks) * 1024);
-                if (LO) ktl[r][ks] = ld_tile(kr, K_LO + K_KT + (size_t)((2 * wave + r) * 2 + ks) * 1024);
+                kt[r][ks] = ld_k(cc, (int)K_KT + ((2 * wave + r) * 2 + ks) * 1024);
+                if (LO) ktl[r][ks] = ld_k(cc, (int)(K_LO + K_KT) + ((2 * wave + r) * 2 + ks) * 1024);
             }
 #pragma unroll
         for (int ks = 0; ks < 2; ks++)
             if (ks == 0 || w2) {
-                pp[ks][0] = ld_tile(rec_of(cc), T_PH + (size_t)(wave * 2 + ks) * 1024);
-                pp[ks][1] = ld_tile(rec_of(cc), T_PL + (size_t)(wave * 2 + ks) * 1024);
+                pp[ks][0] = ld_r(cc, (int)T_PH + (wave * 2 + ks) * 1024);
+                pp[ks][1] = ld_r(cc, (int)T_PL + (wave * 2 + ks) * 1024);
             }
-        sqv = *(g_float *)(rec_of(cc) + T_SC + 256 + (16 * wave + n) * 4);
-        gc = *(g_float *)(rec_of(cc) + T_SC + 512);
+        sqv = __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(Rr, (16 * wave + n) * 4, cc * (int)TREC + (int)T_SC + 256, 0));
+        gc = *(g_float *)(rec0 + (size_t)cc * TREC + T_SC + 512);
     };
     // The state first, waited for here: the loop head joins this path and the
     // loop's back edge, and a load still pending on either path would make
@@ -2356,6 +2364,9 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
     const size_t rec_bytes = trec ? al256(n_rec * TREC) : al256(n_rec * (x3 ? XREC : REC)) + al256(n_rec * sizeof(float));
     const size_t krec_one = vx_dn_krec_bytes(true);
     const size_t krec_bytes = trec ? al256((size_t)d->B * d->nqk * NC * krec_one) : 0;
+    // (the walk addresses one head's records with 32-bit offsets)
+    VX_REQUIRE(!trec || (size_t)NC * krec_one < ((size_t)1 << 31),
+               "vx27_hip_dn_prefill: T = %d exceeds the 1398080-token limit of one call", d->T);
     char *glue_buf = (char *)scr + rec_bytes + krec_bytes;
     const uint16_t *q = d->q, *k = d->k, *v = d->v;
     const uint16_t *ql = nullptr, *kl = nullptr;
