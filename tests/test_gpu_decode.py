@@ -79,7 +79,7 @@ def test_dn_conv_batched_full(ctx):
 
 
 @pytest.mark.parametrize("B,flags,conv", [(1, 0, False), (2, 0, False), (4, 4, False), (8, 2 | 4, False),
-                                           (1, 1 | 4, True), (4, 1 | 4, True)])
+                                           (1, 1 | 4, True), (4, 1 | 4, True), (8, 1 | 4, True)])
 def test_dn_single_step_calls(ctx, B, flags, conv):
     """One step per call with few heads (B x 16).  Without the conv this is
     the column-split step kernel (8, 4 or 2 workgroups per head for 16, 64

@@ -259,3 +259,66 @@ def test_memset_kernel_and_capture():
                 assert np.array_equal(buf.download((n,), np.uint8), want), rep
         finally:
             L.check(lib.vx27_hip_graph_destroy(g), "graph_destroy")
+
+
+def test_dn_conv_step_graph_replay():
+    """One fused-conv decode step at batch 1 (16 heads, the conv state
+    advanced in place by the step kernel) captured as a graph.  Replayed
+    once per token with the token's inputs copied into the captured
+    buffers, eager calls and synchronisations between replays: every
+    output, the state and the conv state equal eager calls bit for bit."""
+    from vx27_amd import lib as L, mixers as M, workloads as W
+    lib = L.lib()
+    with L.Ctx(0) as ctx:
+        B, H, steps = 1, 16, 6
+        d = W.dn_conv(B=B, H=H, steps=steps, config=12)
+        flags = L.DN_CONV | L.DN_PRE_L2
+        lay = M.DeltaNetLayer(ctx, B, H, H, d["A_log"], d["dt_bias"], conv_w=d["conv_w_bf16"],
+                              conv_w_dtype=L.BF16, S0=d["S0"], conv0=d["conv0"])
+        S0 = ctx.put(np.ascontiguousarray(d["S0"], np.float32))
+        c0 = ctx.put(np.ascontiguousarray(d["conv0"], np.float32))
+        xs, as_, bs = (ctx.put(np.ascontiguousarray(d[k], np.float32)) for k in ("x", "a", "b"))
+        xb, ab, bb = ctx.buf(xs.nbytes // steps), ctx.buf(as_.nbytes // steps), ctx.buf(bs.nbytes // steps)
+        ob = ctx.buf(B * H * 128 * 4)
+        desc = lay.desc(1, flags, ob.ptr, ab.ptr, bb.ptr, x=xb.ptr)
+
+        def reset():
+            L.check(lib.vx27_hip_d2d(ctx.h, lay.S.ptr, S0.ptr, S0.nbytes), "d2d")
+            L.check(lib.vx27_hip_d2d(ctx.h, lay.conv_state.ptr, c0.ptr, c0.nbytes), "d2d")
+
+        def feed(t):
+            for src, dst in ((xs, xb), (as_, ab), (bs, bb)):
+                L.check(lib.vx27_hip_d2d(ctx.h, dst.ptr, src.ptr + t * dst.nbytes, dst.nbytes), "d2d")
+
+        def eager_all():
+            outs = []
+            for t in range(steps):
+                feed(t)
+                L.check(lib.vx27_hip_dn_decode(ctx.h, C.byref(desc)), "dn_decode")
+                outs.append(ob.download((B, H, 128), np.float32))
+            return outs, lay.state(), lay.conv()
+
+        reset()
+        o_e, S_e, c_e = eager_all()
+        reset()
+        feed(0)
+        ctx.graph_begin()
+        L.check(lib.vx27_hip_dn_decode(ctx.h, C.byref(desc)), "dn_decode (capture)")
+        g = ctx.graph_end()
+        try:
+            reset()
+            for t in range(steps):
+                feed(t)
+                ctx.graph_launch(g)
+                ctx.sync()
+                o_g = ob.download((B, H, 128), np.float32)
+                say(f"  replay {t}: output equal {np.array_equal(o_g, o_e[t])}")
+                assert np.array_equal(o_g, o_e[t]), t
+            S_g, c_g = lay.state(), lay.conv()
+            assert np.array_equal(S_g, S_e) and np.array_equal(c_g, c_e)
+            reset()
+            o_2, S_2, c_2 = eager_all()       # eager again after the replays, same bits
+            assert all(np.array_equal(a, b) for a, b in zip(o_2, o_e))
+            assert np.array_equal(S_2, S_e) and np.array_equal(c_2, c_e)
+        finally:
+            L.check(lib.vx27_hip_graph_destroy(g), "graph_destroy")
