@@ -634,9 +634,11 @@ __device__ __forceinline__ double row16_sum(double v) {
 // LDS of dnp_prept, 77 KiB (two workgroups a CU), four regions whose
 // contents change with the phase:
 //   R0: q rows [64][RP] bf16 -> K^T lo [128][TP] -> A [64][AP] fp32 -> V hi rows
-//   R1: k rows [64][RP] bf16 -> k lo rows -> T [64][64] fp32 -> V lo rows
+//       (VCONV: V^T hi [128][TP])
+//   R1: k rows [64][RP] bf16 -> k lo rows -> T [64][64] fp32 -> V^T lo [128][TP]
 //   R2: K^T hi [128][TP] -> P hi, lo staging 2 x [64][TP] -> V^T hi [128][TP]
-//   R3: V^T lo [128][TP]
+//       (VCONV: the x window of v channels 64-127, [68 tokens][64] fp32)
+//   R3: V lo rows [64][RP] (VCONV: the x window of v channels 0-63)
 constexpr int TN_REG = HD * TP * 2;
 constexpr int TN_R0 = 0;
 constexpr int TN_R1 = TN_R0 + TN_REG;
@@ -683,11 +685,11 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
     uint16_t *q_rows = (uint16_t *)(smem + TN_R0), *kT_l = (uint16_t *)(smem + TN_R0);
     float *A_s = (float *)(smem + TN_R0);
     uint16_t *vh_rows = (uint16_t *)(smem + TN_R0);
-    uint16_t *k_rows = (uint16_t *)(smem + TN_R1), *vl_rows = (uint16_t *)(smem + TN_R1);
+    uint16_t *k_rows = (uint16_t *)(smem + TN_R1), *vl_rows = (uint16_t *)(smem + TN_R3);
     float *T_s = (float *)(smem + TN_R1);
     uint16_t *kT_h = (uint16_t *)(smem + TN_R2);
     uint16_t *P_h = (uint16_t *)(smem + TN_R2), *P_l = P_h + CH * TP;
-    uint16_t *vT_h = (uint16_t *)(smem + TN_R2), *vT_l = (uint16_t *)(smem + TN_R3);
+    uint16_t *vT_h = (uint16_t *)(smem + TN_R2), *vT_l = (uint16_t *)(smem + TN_R1);
     float *M_t = (float *)(smem + TN_MT);
     double *gam_s = (double *)(smem + TN_GAM);
     float *beta_s = (float *)(smem + TN_SC), *eg_s = beta_s + CH, *egc_s = eg_s + CH;
@@ -835,8 +837,22 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
     }
 
     const float qscale = 1.0f / sqrtf((float)HD);
+    // VCONV: the x window of one value head's v channels (tokens t0-3 ..
+    // t0+64, clamped to the prompt; 64 channels, 256-byte rows) streamed
+    // into LDS region `lds` by direct loads, 4 rows a wave instruction, while
+    // the phases before phase 5 run (waited for before phase 5's conv)
+    auto x_window = [&](int vh, int half, uint32_t lds) {
+        const float *xb = p.x + (size_t)b * p.T * p.C + (size_t)2 * p.nqk * HD + (size_t)vh * HD + 64 * half;
+        for (int i = wave; i < 17; i += 4) {
+            const int row0 = min(max(t0 - 3 + 4 * i, 0), p.T - 1);
+            const int row = min(max(t0 - 3 + 4 * i + (lane >> 4), 0), p.T - 1);
+            const float *base = vx_uniform_ptr(xb + (size_t)row0 * p.C);
+            vx_dma16(base, (uint32_t)(((row - row0) * p.C + 4 * (lane & 15)) * 4), lds + 1024 * i);
+        }
+    };
     for (int jv = 0; jv < nr; jv++) {
         const int vh = qh * nr + jv;
+        if (VCONV) x_window(vh, 0, vx_lds_addr(smem + TN_R3));
         // ---- phase 3: gates and the cumulative log-decay (wave 0, lane =
         // token); masked tokens get beta = 0 and g = 0
         if (wave == 0) {
@@ -905,6 +921,11 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
             *(uint4 *)(rec + T_PL + o) = *(const uint4 *)&P_l[rowA * TP + 32 * ks + 8 * g];
         }
         // ---- phase 4: T = (I + A)^-1; the diagonal blocks, one lane per column
+        // (with VCONV waves 1 and 2, idle here, load the conv taps of the
+        // head's 128 v channels, stored in the last level below)
+        float w4[4];
+        if (VCONV && (wave == 1 || wave == 2))
+            load_conv_w(p.conv_w, p.w_bf16, (size_t)2 * p.nqk * HD + (size_t)vh * HD + (tid - 64), w4);
         if (tid < 64) {
             const int bi = tid >> 4, cc = tid & 15, o = 16 * bi;
             float t[16];
@@ -918,10 +939,13 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
 #pragma unroll
             for (int r = 0; r < 16; r++) T_s[(o + r) * 64 + o + cc] = t[r];
         }
-        __syncthreads();
+        __syncthreads();   // (and the P staging in R2 is read out)
+        if (VCONV) x_window(vh, 1, vx_lds_addr(smem + TN_R2));
         float *Mw = M_t + (wave < 3 ? wave : 0) * 256;
 #pragma unroll
         for (int lev = 1; lev < 4; lev++) {
+            if (VCONV && lev == 3 && (wave == 1 || wave == 2))   // (wave 0 alone uses its scratch, M_t[0, 256))
+                *(float4 *)&M_t[256 + (tid - 64) * 4] = make_float4(w4[0], w4[1], w4[2], w4[3]);
             if (wave < 4 - lev) {
                 const int j = wave, i = j + lev;
                 floatx4_t acc = {0.f, 0.f, 0.f, 0.f};
@@ -948,14 +972,28 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
             }
             __syncthreads();
         }
-        // ---- phase 5: T' = T diag(beta), row block wave, in registers (the
-        // upper blocks of T hold stale bytes: selected away); -T'' tiles.
-        // With VCONV the v channels' conv taps go to the level products'
-        // LDS (free after phase 4) for the V rows below.
-        if (VCONV && tid < HD) {
-            float w4[4];
-            load_conv_w(p.conv_w, p.w_bf16, (size_t)2 * p.nqk * HD + (size_t)vh * HD + tid, w4);
-            *(float4 *)&M_t[tid * 4] = make_float4(w4[0], w4[1], w4[2], w4[3]);
+        // ---- phase 5: T' = T diag(beta) of row block wave in registers (the
+        // upper blocks of T hold stale bytes: selected away) and the -T''
+        // tiles; V^T hi/lo: without VCONV from the fp32 v rows (hi to R0, lo
+        // to R3, thread (row tid/16 + 16 j, 8 columns)) transposed into R2
+        // and R1; with VCONV the causal conv + SiLU of the x window in LDS,
+        // thread (tokens 16 wave .. +15, channels lane and lane + 64), written
+        // transposed straight into R0 and R1 (vx27_qfwd.c:118-131)
+        if (!VCONV) {
+#pragma unroll
+            for (int j = 0; j < 4; j++) {
+                const int r = (tid >> 4) + 16 * j;
+                const bool ok = r < nvalid;
+                const size_t off = (((size_t)b * p.T + t0 + r) * p.nv + vh) * HD + 8 * seg;
+                const float *vf = p.v + off;
+                const float4 a0 = ok ? *(const float4 *)vf : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float4 a1 = ok ? *(const float4 *)(vf + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
+                const float f[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+                uint4 h, l;
+                split8(f, h, l);
+                *(uint4 *)&vh_rows[r * RP + 8 * seg] = h;
+                *(uint4 *)&vl_rows[r * RP + 8 * seg] = l;
+            }
         }
         bf16x8_t tph[2], tpl[2];
 #pragma unroll
@@ -985,89 +1023,57 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
             *(uint4 *)(rec + T_TH + o) = h;
             *(uint4 *)(rec + T_TL + o) = l;
         }
-        __syncthreads();   // A, T and the P staging are read out
-        // V rows (hi to R0, with LO the lo parts of the fp32 values to R1),
-        // thread (row tid/16 + 16 j, 8 columns), then transposed
+        uint16_t *vTh = VCONV ? (uint16_t *)(smem + TN_R0) : vT_h;
         if (VCONV) {
-            // thread (rows 4 (tid/16) .. +3, 8 v channels), 2 channels at a
-            // time: the window of tokens t-3 .. t+3 (earlier than token 0: the
-            // conv state; past the end: clamped, and the rows zeroed) as
-            // 8-byte loads, the taps from LDS, conv + SiLU per token
-            // (vx27_qfwd.c:118-131)
-            const size_t ch0 = (size_t)2 * p.nqk * HD + (size_t)vh * HD + 8 * seg;
-            const int r0 = 4 * (tid >> 4);
-            int t = t0 + r0;
-            asm volatile("" : "+v"(t));   // the window's addresses stay inside the value-head loop
-#pragma unroll 1
-            for (int qt = 0; qt < 4; qt++) {
-                float xw[7][2];
-                const float *xr = p.x + (size_t)b * p.T * p.C + ch0 + 2 * qt;
+            __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's window loads
+            __syncthreads();   // every wave's window is in LDS, and T is read out
+            const float *win[2] = {(const float *)(smem + TN_R3), (const float *)(smem + TN_R2)};
 #pragma unroll
-                for (int i = 0; i < 7; i++) {
-                    const float2 v = *(const float2 *)(xr + (size_t)min(max(t - 3 + i, 0), p.T - 1) * p.C);
-                    xw[i][0] = v.x; xw[i][1] = v.y;
+            for (int hc = 0; hc < 2; hc++) {
+                const int ch = lane + 64 * hc;
+                const float4 wv = *(const float4 *)&M_t[256 + ch * 4];
+                const float w[4] = {wv.x, wv.y, wv.z, wv.w};
+                const float *xw = win[hc] + lane;   // row r: token t0 - 3 + r
+                float cs[3] = {xw[(16 * wave) * 64], xw[(16 * wave + 1) * 64], xw[(16 * wave + 2) * 64]};
+                if (t0 == 0 && wave == 0) {   // tokens -3 .. -1: the conv state (oldest first)
+                    const float *sp = p.conv_state + ((size_t)b * p.C + (size_t)2 * p.nqk * HD + (size_t)vh * HD + ch) * 3;
+                    cs[0] = sp[0]; cs[1] = sp[1]; cs[2] = sp[2];
                 }
-                if (t < 3) {   // tokens before 0: state slots t-3+i+3 (oldest first)
-                    const float *sp = p.conv_state + ((size_t)b * p.C + ch0 + 2 * qt) * 3;
+                float f[16];
 #pragma unroll
-                    for (int i = 0; i < 3; i++)
-                        if (t - 3 + i < 0) { xw[i][0] = sp[t + i]; xw[i][1] = sp[3 + t + i]; }
+                for (int k = 0; k < 16; k++) {
+                    const float xv = xw[(16 * wave + 3 + k) * 64];
+                    const float y = conv_step(cs, w, xv);
+                    f[k] = 16 * wave + k < nvalid ? y : 0.0f;
                 }
-                float w[2][4];
-#pragma unroll
-                for (int e = 0; e < 2; e++) {
-                    const float4 wv = *(const float4 *)&M_t[(8 * seg + 2 * qt + e) * 4];
-                    w[e][0] = wv.x; w[e][1] = wv.y; w[e][2] = wv.z; w[e][3] = wv.w;
-                }
-#pragma unroll
-                for (int j = 0; j < 4; j++) {
-                    const bool ok = r0 + j < nvalid;
-                    float f[2];
-#pragma unroll
-                    for (int e = 0; e < 2; e++) {
-                        float cs[3] = {xw[j][e], xw[j + 1][e], xw[j + 2][e]};
-                        f[e] = ok ? conv_step(cs, w[e], xw[j + 3][e]) : 0.0f;
-                    }
-                    const uint32_t h = pack2(f[0], f[1]);
-                    const uint16_t *hs = (const uint16_t *)&h;
-                    const uint32_t l = pack2(f[0] - vx_bf16_to_f32(hs[0]), f[1] - vx_bf16_to_f32(hs[1]));
-                    *(uint32_t *)&vh_rows[(r0 + j) * RP + 8 * seg + 2 * qt] = h;
-                    *(uint32_t *)&vl_rows[(r0 + j) * RP + 8 * seg + 2 * qt] = l;
-                }
+                uint4 h0, l0, h1, l1;
+                split8(f, h0, l0);
+                split8(f + 8, h1, l1);
+                *(uint4 *)&vTh[ch * TP + 16 * wave] = h0;
+                *(uint4 *)&vTh[ch * TP + 16 * wave + 8] = h1;
+                *(uint4 *)&vT_l[ch * TP + 16 * wave] = l0;
+                *(uint4 *)&vT_l[ch * TP + 16 * wave + 8] = l1;
             }
+            __syncthreads();
         } else {
-#pragma unroll
-            for (int j = 0; j < 4; j++) {
-                const int r = (tid >> 4) + 16 * j;
-                const bool ok = r < nvalid;
-                const size_t off = (((size_t)b * p.T + t0 + r) * p.nv + vh) * HD + 8 * seg;
-                const float *vf = p.v + off;
-                const float4 a0 = ok ? *(const float4 *)vf : make_float4(0.f, 0.f, 0.f, 0.f);
-                const float4 a1 = ok ? *(const float4 *)(vf + 4) : make_float4(0.f, 0.f, 0.f, 0.f);
-                const float f[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
-                uint4 h, l;
-                split8(f, h, l);
-                *(uint4 *)&vh_rows[r * RP + 8 * seg] = h;
-                *(uint4 *)&vl_rows[r * RP + 8 * seg] = l;
-            }
+            __syncthreads();   // the V rows are complete and T is read out
+            tr_rows(vh_rows, vT_h, tid);
+            tr_rows(vl_rows, vT_l, tid);
+            __syncthreads();
         }
-        __syncthreads();
-        tr_rows(vh_rows, vT_h, tid);
-        tr_rows(vl_rows, vT_l, tid);
-        __syncthreads();
         // Ut = T' V, row block wave, as C-layout tiles per 16-column block
 #pragma unroll
         for (int cb = 0; cb < 8; cb++) {
             floatx4_t u0 = {0.f, 0.f, 0.f, 0.f}, u1 = {0.f, 0.f, 0.f, 0.f};
             const int col = cb * 16 + m;
             {
-                const bf16x8_t vb = as_bf16x8(*(const uint4 *)&vT_h[col * TP + 8 * g]);
+                const bf16x8_t vb = as_bf16x8(*(const uint4 *)&vTh[col * TP + 8 * g]);
                 MFMA1(u0, tph[0], vb);
                 MFMA1(u0, tpl[0], vb);
                 if (LO) MFMA1(u0, tph[0], as_bf16x8(*(const uint4 *)&vT_l[col * TP + 8 * g]));
             }
             if (w2) {
-                const bf16x8_t vb = as_bf16x8(*(const uint4 *)&vT_h[col * TP + 32 + 8 * g]);
+                const bf16x8_t vb = as_bf16x8(*(const uint4 *)&vTh[col * TP + 32 + 8 * g]);
                 MFMA1(u1, tph[1], vb);
                 MFMA1(u1, tpl[1], vb);
                 if (LO) MFMA1(u1, tph[1], as_bf16x8(*(const uint4 *)&vT_l[col * TP + 32 + 8 * g]));
