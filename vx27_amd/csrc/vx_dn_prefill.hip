@@ -709,6 +709,31 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
         kl[j] = (LO && ok) ? *(const uint4 *)(p.kl + off) : z4;
         qlv[j] = (LO && ok) ? *(const uint4 *)(p.ql + off) : z4;
     }
+    // the gates of value head jv < 4 by wave jv, while the rows arrive (lane =
+    // token; masked tokens get beta = 0 and g = 0): beta, the cumulative
+    // log-decay gam and e^gam, e^(gam_C - gam), written to LDS in its phase 3
+    double g_gam = 0.0;
+    float g_beta = 0.f, g_eg = 0.f, g_egc = 0.f;
+    auto gates = [&](int vh, double &gam, float &bt, float &eg, float &egc) {
+        double beta = 0.0, glog = 0.0;
+        if (lane < nvalid) {
+            const size_t e = ((size_t)b * p.T + t0 + lane) * p.nv + vh;
+            beta = 1.0 / (1.0 + exp(-(double)p.b[e]));
+            glog = -exp((double)p.A_log[vh]) * softplus_d((double)p.a[e] + (double)p.dt_bias[vh]);
+        }
+        double sc = glog;
+#pragma unroll
+        for (int off = 1; off < 64; off <<= 1) {
+            const double o = __shfl_up(sc, off, 64);
+            if (lane >= off) sc += o;
+        }
+        const double sC = __shfl(sc, 63, 64);
+        gam = sc;
+        bt = (float)beta;
+        eg = (float)exp(sc);
+        egc = (float)exp(sC - sc);
+    };
+    if (wave < nr) gates(qh * nr + wave, g_gam, g_beta, g_eg, g_egc);
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int r = (tid >> 4) + 16 * j;
@@ -853,26 +878,14 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
     for (int jv = 0; jv < nr; jv++) {
         const int vh = qh * nr + jv;
         if (VCONV) x_window(vh, 0, vx_lds_addr(smem + TN_R3));
-        // ---- phase 3: gates and the cumulative log-decay (wave 0, lane =
-        // token); masked tokens get beta = 0 and g = 0
-        if (wave == 0) {
-            double beta = 0.0, glog = 0.0;
-            if (lane < nvalid) {
-                const size_t e = ((size_t)b * p.T + t0 + lane) * p.nv + vh;
-                beta = 1.0 / (1.0 + exp(-(double)p.b[e]));
-                glog = -exp((double)p.A_log[vh]) * softplus_d((double)p.a[e] + (double)p.dt_bias[vh]);
-            }
-            double sc = glog;
-#pragma unroll
-            for (int off = 1; off < 64; off <<= 1) {
-                const double o = __shfl_up(sc, off, 64);
-                if (lane >= off) sc += o;
-            }
-            const double sC = __shfl(sc, 63, 64);
-            gam_s[lane] = sc;
-            beta_s[lane] = (float)beta;
-            eg_s[lane] = (float)exp(sc);
-            egc_s[lane] = (float)exp(sC - sc);
+        // ---- phase 3: the gates to LDS (computed in phase 1 by wave jv for
+        // jv < 4, else here by wave 0)
+        if (jv < 4 ? wave == jv : wave == 0) {
+            if (jv >= 4) gates(vh, g_gam, g_beta, g_eg, g_egc);
+            gam_s[lane] = g_gam;
+            beta_s[lane] = g_beta;
+            eg_s[lane] = g_eg;
+            egc_s[lane] = g_egc;
         }
         __syncthreads();
         char *rec = p.rec + (((size_t)b * p.nv + vh) * p.NC + c) * TREC;
@@ -1042,8 +1055,18 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
                 float f[16];
 #pragma unroll
                 for (int k = 0; k < 16; k++) {
+                    // the conv's sum as conv_step's; SiLU as v / (1 + e^-v) with
+                    // the hardware exp2 and reciprocal (a few ulp from the
+                    // correctly rounded quotient)
                     const float xv = xw[(16 * wave + 3 + k) * 64];
-                    const float y = conv_step(cs, w, xv);
+                    float acc = w[0] * cs[0];
+                    acc = acc + w[1] * cs[1];
+                    acc = acc + w[2] * cs[2];
+                    acc = acc + w[3] * xv;
+                    cs[0] = cs[1];
+                    cs[1] = cs[2];
+                    cs[2] = xv;
+                    const float y = acc * __builtin_amdgcn_rcpf(1.0f + __builtin_amdgcn_exp2f(acc * -1.4426950408889634f));
                     f[k] = 16 * wave + k < nvalid ? y : 0.0f;
                 }
                 uint4 h0, l0, h1, l1;
