@@ -564,17 +564,20 @@ struct PrepTArgs {
     int T, nqk, nv, NC;
     const uint16_t *q, *k;          // hi parts [B][T][nqk][128] bf16
     const uint16_t *ql, *kl;        // lo parts as rows
-    const float *v;                 // [B][T][nv][128] fp32 (unless VCONV)
+    const float *v;                 // [B][T][nv][128] fp32 (unless XIN)
     const float *a, *b;             // [B][T][nv]
     const float *A_log, *dt_bias;   // [nv]
     char *rec;                      // [B][nv][NC] records of TREC bytes
     char *krec;                     // [B][nqk][NC] K records of krec_bytes
     int krec_bytes;
-    // VCONV: v = silu(causal conv) of the v channels of x [B][T][C], formed
-    // here (state before token 0 in conv_state [B][C][3], taps conv_w [C][4])
+    // XIN: q, k and v formed here from x [B][T][C]: the causal conv + SiLU
+    // (state before token 0 in conv_state [B][C][3], taps conv_w [C][4]),
+    // then for q and k the pre-norms of `flags` (norm_w [128])
     int C, w_bf16;
     const float *x, *conv_state;
     const void *conv_w;
+    unsigned flags;
+    const float *norm_w;
 };
 
 // bf16 hi and lo of 8 floats
@@ -647,13 +650,16 @@ __device__ __forceinline__ double row16_sum(double v) {
 }
 
 // LDS of dnp_prept, 77 KiB (two workgroups a CU), four regions whose
-// contents change with the phase:
+// contents change with the phase (XIN, phase 1 first: the x windows of the
+// QK head's q channels in R0-R1 and k channels in R2-R3, [68 tokens][128]
+// fp32; then q and k after the conv as fp32 rows [64][128] in R0-R1 and
+// R2-R3; then the lo rows of q in R2 and k in R3 beside the hi rows):
 //   R0: q rows [64][RP] bf16 -> K^T lo [128][TP] -> A [64][AP] fp32 -> V hi rows
-//       (VCONV: V^T hi [128][TP])
+//       (XIN: V^T hi [128][TP])
 //   R1: k rows [64][RP] bf16 -> k lo rows -> T [64][64] fp32 -> V^T lo [128][TP]
 //   R2: K^T hi [128][TP] -> P hi, lo staging 2 x [64][TP] -> V^T hi [128][TP]
-//       (VCONV: the x window of v channels 64-127, [68 tokens][64] fp32)
-//   R3: V lo rows [64][RP] (VCONV: the x window of v channels 0-63)
+//       (XIN: the x window of v channels 64-127, [68 tokens][64] fp32)
+//   R3: V lo rows [64][RP] (XIN: the x window of v channels 0-63)
 constexpr int TN_REG = HD * TP * 2;
 constexpr int TN_R0 = 0;
 constexpr int TN_R1 = TN_R0 + TN_REG;
@@ -683,10 +689,11 @@ static_assert(2 * TN_TOTAL <= 160 * 1024, "two workgroups per CU");
 //            by level (fp32 MFMA)
 //   phase 5  T' = T diag(beta) (hi/lo in registers); -T'' = -T' diag(sk)
 //            as hi/lo tiles; V through LDS transposed, Ut = T' V on MFMA
-//            (with VCONV the V rows are the causal conv + SiLU of x, formed
-//            here: the glue writes no v rows)
-template <bool VCONV>
-__global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
+//            (with XIN q, k and v are formed here from x: phase 1 runs the
+//            q/k conv and pre-norms, phase 5 the v conv; there is no glue
+//            kernel)
+template <bool XIN>
+__global__ __launch_bounds__(256, 2) void dnp_prept(PrepTArgs p) {   // (two workgroups a CU: 256 registers)
     constexpr bool LO = true;   // (the glue's q, k, v always come with lo parts)
     const int c = blockIdx.x, qh = blockIdx.y, b = blockIdx.z;
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, m = lane & 15;
@@ -714,15 +721,37 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
 
     // ---- phase 1: k and q rows, thread (row tid/16 + 16 j, dims 8 seg ..)
     uint4 kh[4], kl[4], qhv[4], qlv[4];
+    float xq[2][4], xk[2][4];   // (XIN) conv taps
+    if (XIN) {
+        // the x windows of the QK head's q and k channels (tokens t0-3 ..
+        // t0+64, clamped to the prompt; 512-byte rows) into R0-R1 and R2-R3
+        // by direct loads, 2 rows a wave instruction; the taps of channels
+        // lane and lane + 64 of q and of k
+        const float *xb = p.x + (size_t)b * p.T * p.C + (size_t)qh * HD;
+        for (int i = wave; i < 34; i += 4) {
+            const int row0 = min(max(t0 - 3 + 2 * i, 0), p.T - 1);
+            const int row = min(max(t0 - 3 + 2 * i + (lane >> 5), 0), p.T - 1);
+            const uint32_t off = (uint32_t)(((row - row0) * p.C + 4 * (lane & 31)) * 4);
+            vx_dma16(vx_uniform_ptr(xb + (size_t)row0 * p.C), off, vx_lds_addr(smem + TN_R0) + 1024 * i);
+            vx_dma16(vx_uniform_ptr(xb + (size_t)p.nqk * HD + (size_t)row0 * p.C), off, vx_lds_addr(smem + TN_R2) + 1024 * i);
+        }
 #pragma unroll
-    for (int j = 0; j < 4; j++) {
-        const int r = (tid >> 4) + 16 * j;
-        const size_t off = (((size_t)b * p.T + t0 + r) * p.nqk + qh) * HD + 8 * seg;
-        const bool ok = r < nvalid;
-        kh[j] = ok ? *(const uint4 *)(p.k + off) : z4;
-        qhv[j] = ok ? *(const uint4 *)(p.q + off) : z4;
-        kl[j] = (LO && ok) ? *(const uint4 *)(p.kl + off) : z4;
-        qlv[j] = (LO && ok) ? *(const uint4 *)(p.ql + off) : z4;
+        for (int hc = 0; hc < 2; hc++) {
+            const size_t chq = (size_t)qh * HD + lane + 64 * hc, chk = chq + (size_t)p.nqk * HD;
+            load_conv_w(p.conv_w, p.w_bf16, chq, xq[hc]);
+            load_conv_w(p.conv_w, p.w_bf16, chk, xk[hc]);
+        }
+    } else {
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = (tid >> 4) + 16 * j;
+            const size_t off = (((size_t)b * p.T + t0 + r) * p.nqk + qh) * HD + 8 * seg;
+            const bool ok = r < nvalid;
+            kh[j] = ok ? *(const uint4 *)(p.k + off) : z4;
+            qhv[j] = ok ? *(const uint4 *)(p.q + off) : z4;
+            kl[j] = (LO && ok) ? *(const uint4 *)(p.kl + off) : z4;
+            qlv[j] = (LO && ok) ? *(const uint4 *)(p.ql + off) : z4;
+        }
     }
     // the gates of value head jv < 4 by wave jv, while the rows arrive (lane =
     // token; masked tokens get beta = 0 and g = 0): beta, the cumulative
@@ -749,9 +778,114 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
         egc = (float)exp(sC - sc);
     };
     if (wave < nr) gates(qh * nr + wave, g_gam, g_beta, g_eg, g_egc);
+    if (XIN) {
+        // q and k from x as the glue's operations (vx27_qfwd.c:118-131): the
+        // conv + SiLU, thread (tokens 16 wave .. +15, channels lane and
+        // lane + 64) out of the LDS windows (row r: token t0 - 3 + r) ...
+        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's window loads
+        __syncthreads();
+        float yq[2][16], yk[2][16];
+        const float *wq = (const float *)(smem + TN_R0), *wk = (const float *)(smem + TN_R2);
+#pragma unroll
+        for (int hc = 0; hc < 2; hc++) {
+            const int ch = lane + 64 * hc;
+            float cq[3], ck[3];
+#pragma unroll
+            for (int t = 0; t < 3; t++) {
+                cq[t] = wq[(16 * wave + t) * HD + ch];
+                ck[t] = wk[(16 * wave + t) * HD + ch];
+            }
+            if (t0 == 0 && wave == 0) {   // tokens -3 .. -1: the conv state (oldest first)
+                const size_t chq = (size_t)qh * HD + ch, chk = chq + (size_t)p.nqk * HD;
+#pragma unroll
+                for (int t = 0; t < 3; t++) {
+                    cq[t] = p.conv_state[((size_t)b * p.C + chq) * 3 + t];
+                    ck[t] = p.conv_state[((size_t)b * p.C + chk) * 3 + t];
+                }
+            }
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                yq[hc][k] = conv_step_fast(cq, xq[hc], wq[(16 * wave + 3 + k) * HD + ch]);
+                yk[hc][k] = conv_step_fast(ck, xk[hc], wk[(16 * wave + 3 + k) * HD + ch]);
+            }
+        }
+        __syncthreads();   // the windows are read out: the fp32 rows take R0-R1 and R2-R3
+        float *fq = (float *)(smem + TN_R0), *fk = (float *)(smem + TN_R2);
+#pragma unroll
+        for (int hc = 0; hc < 2; hc++)
+#pragma unroll
+            for (int k = 0; k < 16; k++) {
+                fq[(16 * wave + k) * HD + lane + 64 * hc] = yq[hc][k];
+                fk[(16 * wave + k) * HD + lane + 64 * hc] = yk[hc][k];
+            }
+        __syncthreads();
+        // ... then per row (thread: rows tid/16 + 16 j, dims 8 seg) the
+        // (1+w) RMS pre-norm and l2norm with q/sqrt(128) (double sums over
+        // the row's 16 lanes), rows past the prompt zero, and the bf16 hi/lo
+        // split of the values
+        float nw[8];
+#pragma unroll
+        for (int e = 0; e < 8; e++) nw[e] = p.norm_w ? p.norm_w[8 * seg + e] : 1.0f;
+        const float qs = 1.0f / sqrtf((float)HD);
+#pragma unroll
+        for (int j = 0; j < 4; j++) {
+            const int r = (tid >> 4) + 16 * j;
+            float vq[8], vk[8];
+            *(float4 *)&vq[0] = *(const float4 *)&fq[r * HD + 8 * seg];
+            *(float4 *)&vq[4] = *(const float4 *)&fq[r * HD + 8 * seg + 4];
+            *(float4 *)&vk[0] = *(const float4 *)&fk[r * HD + 8 * seg];
+            *(float4 *)&vk[4] = *(const float4 *)&fk[r * HD + 8 * seg + 4];
+            if (p.flags & VX27_DN_PRE_RMS) {   // rmsn(x)*(1+w), vx27_qfwd.c:32-39,123
+                double ssq = 0.0, ssk = 0.0;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    ssq = ssq + (double)vq[e] * (double)vq[e];
+                    ssk = ssk + (double)vk[e] * (double)vk[e];
+                }
+                ssq = row16_sum(ssq);
+                ssk = row16_sum(ssk);
+                const float iq = 1.0f / sqrtf((float)(ssq / HD) + 1e-6f), ik = 1.0f / sqrtf((float)(ssk / HD) + 1e-6f);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    vq[e] = (vq[e] * iq) * (nw[e] + 1.0f);
+                    vk[e] = (vk[e] * ik) * (nw[e] + 1.0f);
+                }
+            }
+            if (p.flags & VX27_DN_PRE_L2) {    // l2norm + q/sqrt(hd), vx27_qfwd.c:124-130
+                double ssq = 0.0, ssk = 0.0;
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    ssq = ssq + (double)vq[e] * (double)vq[e];
+                    ssk = ssk + (double)vk[e] * (double)vk[e];
+                }
+                ssq = row16_sum(ssq);
+                ssk = row16_sum(ssk);
+                const float iq = 1.0f / sqrtf((float)ssq + 1e-6f), ik = 1.0f / sqrtf((float)ssk + 1e-6f);
+#pragma unroll
+                for (int e = 0; e < 8; e++) {
+                    vq[e] = vq[e] * iq;
+                    vk[e] = vk[e] * ik;
+                    vq[e] = vq[e] * qs;
+                }
+            }
+            const bool ok = r < nvalid;
+#pragma unroll
+            for (int e = 0; e < 8; e++) {
+                vq[e] = ok ? vq[e] : 0.0f;
+                vk[e] = ok ? vk[e] : 0.0f;
+            }
+            split8(vq, qhv[j], qlv[j]);
+            split8(vk, kh[j], kl[j]);
+        }
+        __syncthreads();   // the fp32 rows are read out
+    }
 #pragma unroll
     for (int j = 0; j < 4; j++) {
         const int r = (tid >> 4) + 16 * j;
+        if (XIN) {   // lo rows beside the hi rows: q in R2, k in R3 (phase 2's lo operands)
+            *(uint4 *)&((uint16_t *)(smem + TN_R2))[r * RP + 8 * seg] = qlv[j];
+            *(uint4 *)&((uint16_t *)(smem + TN_R3))[r * RP + 8 * seg] = kl[j];
+        }
         *(uint4 *)&k_rows[r * RP + 8 * seg] = kh[j];
         *(uint4 *)&q_rows[r * RP + 8 * seg] = qhv[j];
         double sk = 0.0, sq = 0.0;   // of the values hi + lo (exact in double)
@@ -793,7 +927,17 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
         return make_uint4(v.x & mk, v.y & mk, v.z & mk, v.w & mk);
     };
     uint4 qal[4], kal[4], bkl[4][4];
-    if (LO) {
+    if (XIN) {   // from the lo rows in LDS (rows past the prompt are zero there)
+        const uint16_t *qlr = (const uint16_t *)(smem + TN_R2), *klr = (const uint16_t *)(smem + TN_R3);
+#pragma unroll
+        for (int ks = 0; ks < 4; ks++) {
+            qal[ks] = *(const uint4 *)&qlr[rowA * RP + 32 * ks + 8 * g];
+            kal[ks] = *(const uint4 *)&klr[rowA * RP + 32 * ks + 8 * g];
+#pragma unroll
+            for (int nb = 0; nb < 4; nb++) bkl[nb][ks] = *(const uint4 *)&klr[(nb * 16 + m) * RP + 32 * ks + 8 * g];
+        }
+        __syncthreads();   // the lo rows are read out: R2 takes K^T hi
+    } else if (LO) {
 #pragma unroll
         for (int ks = 0; ks < 4; ks++) {
             qal[ks] = lo_row(p.ql, rowA, 32 * ks + 8 * g);
@@ -877,7 +1021,7 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
     }
 
     const float qscale = 1.0f / sqrtf((float)HD);
-    // VCONV: the x window of one value head's v channels (tokens t0-3 ..
+    // XIN: the x window of one value head's v channels (tokens t0-3 ..
     // t0+64, clamped to the prompt; 64 channels, 256-byte rows) streamed
     // into LDS region `lds` by direct loads, 4 rows a wave instruction, while
     // the phases before phase 5 run (waited for before phase 5's conv)
@@ -892,7 +1036,7 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
     };
     for (int jv = 0; jv < nr; jv++) {
         const int vh = qh * nr + jv;
-        if (VCONV) x_window(vh, 0, vx_lds_addr(smem + TN_R3));
+        if (XIN) x_window(vh, 0, vx_lds_addr(smem + TN_R3));
         // ---- phase 3: the gates to LDS (computed in phase 1 by wave jv for
         // jv < 4, else here by wave 0)
         if (jv < 4 ? wave == jv : wave == 0) {
@@ -949,10 +1093,10 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
             *(uint4 *)(rec + T_PL + o) = *(const uint4 *)&P_l[rowA * TP + 32 * ks + 8 * g];
         }
         // ---- phase 4: T = (I + A)^-1; the diagonal blocks, one lane per column
-        // (with VCONV waves 1 and 2, idle here, load the conv taps of the
+        // (with XIN waves 1 and 2, idle here, load the conv taps of the
         // head's 128 v channels, stored in the last level below)
         float w4[4];
-        if (VCONV && (wave == 1 || wave == 2))
+        if (XIN && (wave == 1 || wave == 2))
             load_conv_w(p.conv_w, p.w_bf16, (size_t)2 * p.nqk * HD + (size_t)vh * HD + (tid - 64), w4);
         if (tid < 64) {
             const int bi = tid >> 4, cc = tid & 15, o = 16 * bi;
@@ -968,11 +1112,11 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
             for (int r = 0; r < 16; r++) T_s[(o + r) * 64 + o + cc] = t[r];
         }
         __syncthreads();   // (and the P staging in R2 is read out)
-        if (VCONV) x_window(vh, 1, vx_lds_addr(smem + TN_R2));
+        if (XIN) x_window(vh, 1, vx_lds_addr(smem + TN_R2));
         float *Mw = M_t + (wave < 3 ? wave : 0) * 256;
 #pragma unroll
         for (int lev = 1; lev < 4; lev++) {
-            if (VCONV && lev == 3 && (wave == 1 || wave == 2))   // (wave 0 alone uses its scratch, M_t[0, 256))
+            if (XIN && lev == 3 && (wave == 1 || wave == 2))   // (wave 0 alone uses its scratch, M_t[0, 256))
                 *(float4 *)&M_t[256 + (tid - 64) * 4] = make_float4(w4[0], w4[1], w4[2], w4[3]);
             if (wave < 4 - lev) {
                 const int j = wave, i = j + lev;
@@ -1002,12 +1146,12 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
         }
         // ---- phase 5: T' = T diag(beta) of row block wave in registers (the
         // upper blocks of T hold stale bytes: selected away) and the -T''
-        // tiles; V^T hi/lo: without VCONV from the fp32 v rows (hi to R0, lo
+        // tiles; V^T hi/lo: without XIN from the fp32 v rows (hi to R0, lo
         // to R3, thread (row tid/16 + 16 j, 8 columns)) transposed into R2
-        // and R1; with VCONV the causal conv + SiLU of the x window in LDS,
+        // and R1; with XIN the causal conv + SiLU of the x window in LDS,
         // thread (tokens 16 wave .. +15, channels lane and lane + 64), written
         // transposed straight into R0 and R1 (vx27_qfwd.c:118-131)
-        if (!VCONV) {
+        if (!XIN) {
 #pragma unroll
             for (int j = 0; j < 4; j++) {
                 const int r = (tid >> 4) + 16 * j;
@@ -1051,8 +1195,8 @@ __global__ __launch_bounds__(256) void dnp_prept(PrepTArgs p) {
             *(uint4 *)(rec + T_TH + o) = h;
             *(uint4 *)(rec + T_TL + o) = l;
         }
-        uint16_t *vTh = VCONV ? (uint16_t *)(smem + TN_R0) : vT_h;
-        if (VCONV) {
+        uint16_t *vTh = XIN ? (uint16_t *)(smem + TN_R0) : vT_h;
+        if (XIN) {
             __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");   // this wave's window loads
             __syncthreads();   // every wave's window is in LDS, and T is read out
             const float *win[2] = {(const float *)(smem + TN_R3), (const float *)(smem + TN_R2)};
@@ -2270,15 +2414,16 @@ static bool dn_prefill_is_exact(const vx27_dn_prefill_desc *d) {
 }
 // The glue's outputs: q, k hi rows and v as bf16 rows; the split form adds
 // the q and k lo rows and keeps v in fp32 instead.
-static size_t vx_dn_glue_bytes(int B, int T, int nqk, int nv, bool x3, bool vconv) {
+static size_t vx_dn_glue_bytes(int B, int T, int nqk, int nv, bool x3, bool xin) {
     const size_t rows = (size_t)B * T;
     const size_t qd = (size_t)nqk * HD, vd = (size_t)nv * HD;
-    return x3 ? al256(rows * 4 * qd * sizeof(uint16_t)) + (vconv ? 0 : rows * vd * sizeof(float))
+    if (xin) return 0;   // prept forms q, k and v from x: no glue kernel
+    return x3 ? al256(rows * 4 * qd * sizeof(uint16_t)) + rows * vd * sizeof(float)
               : rows * (2 * qd + vd) * sizeof(uint16_t);
 }
-// The T-record form with the conv forms v from x itself (prept), so the glue
-// writes no v rows: split products, the conv, and 16-byte aligned x rows.
-static bool dn_prefill_vconv(const vx27_dn_prefill_desc *d) {
+// The T-record form with the conv forms q, k and v from x itself (prept),
+// with no glue kernel: split products, the conv, and 16-byte aligned x rows.
+static bool dn_prefill_xin(const vx27_dn_prefill_desc *d) {
     return !(d->flags & VX27_DN_BF16) && (d->flags & VX27_DN_CONV) && ((uintptr_t)d->x & 15) == 0;
 }
 // Bytes of one K record (K^T operand tiles, hi and, with lo parts, lo).
@@ -2294,7 +2439,7 @@ size_t vx_dn_prefill_scratch(const vx27_dn_prefill_desc *d) {
     const bool x3 = !(d->flags & VX27_DN_BF16);
     const size_t n_rec = (size_t)d->B * d->nv * NC;
     const bool glue = (d->flags & (VX27_DN_CONV | VX27_DN_PRE_RMS | VX27_DN_PRE_L2)) != 0;
-    const size_t glue_bytes = glue ? vx_dn_glue_bytes(d->B, d->T, d->nqk, d->nv, x3, dn_prefill_vconv(d)) : 0;
+    const size_t glue_bytes = glue ? vx_dn_glue_bytes(d->B, d->T, d->nqk, d->nv, x3, dn_prefill_xin(d)) : 0;
     if (x3 && glue)
         return al256(n_rec * TREC) + al256((size_t)d->B * d->nqk * NC * vx_dn_krec_bytes(true)) + glue_bytes;
     return al256(n_rec * (x3 ? XREC : REC)) + al256(n_rec * sizeof(float)) + glue_bytes;
@@ -2404,25 +2549,25 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
     const uint16_t *q = d->q, *k = d->k, *v = d->v;
     const uint16_t *ql = nullptr, *kl = nullptr;
     const float *v32 = nullptr;
-    // the T form with the conv forms v itself from x (16-byte rows needed)
-    const bool vconv = trec && dn_prefill_vconv(d);
+    // the T form with the conv forms q, k and v itself from x (16-byte rows needed)
+    const bool xin = trec && dn_prefill_xin(d);
     auto conv_state_update = [&]() -> int {   // after every reader of the old state
         const size_t nthr = (size_t)d->B * C;
         VX_LAUNCH(ctx, dnp_conv_state, dim3((unsigned)((nthr + 255) / 256)), dim3(256), d->B, d->T, C, d->x,
                   d->conv_state);
         return 0;
     };
-    if (glue) {   // conv and pre-norms in fp32, then q, k as bf16 (hi, and lo for the split form), v
+    if (glue && !xin) {   // conv and pre-norms in fp32, then q, k as bf16 (hi, and lo for the split form), v
         uint16_t *qo = (uint16_t *)glue_buf, *ko = qo + rows * qd;
         uint16_t *qol = x3 ? ko + rows * qd : nullptr, *kol = x3 ? qol + rows * qd : nullptr;
         uint16_t *vo = x3 ? nullptr : ko + rows * qd;
-        float *vo32 = x3 && !vconv ? (float *)(glue_buf + al256(rows * 4 * qd * sizeof(uint16_t))) : nullptr;
+        float *vo32 = x3 ? (float *)(glue_buf + al256(rows * 4 * qd * sizeof(uint16_t))) : nullptr;
         GlueInArgs ga{d->B, d->T, d->nqk, d->nv, C, d->flags, d->conv_w_dtype == VX27_BF16, d->x, d->conv_state,
                       d->conv_w, d->q, d->k, d->v, d->norm_w, qo, ko, vo, qol, kol, vo32};
-        const int nh = 2 * d->nqk + (vconv ? 0 : d->nv);   // (q, k heads first: with vconv the v heads are skipped)
+        const int nh = 2 * d->nqk + d->nv;   // (q, k heads first)
         const int tblk = (d->T + GT - 1) / GT;
         VX_LAUNCH(ctx, dnp_glue_in, dim3((unsigned)((tblk + 3) / 4), (unsigned)nh, (unsigned)d->B), dim3(256), ga);
-        if (conv && !vconv && conv_state_update()) return -1;
+        if (conv && conv_state_update()) return -1;
         q = qo; k = ko; v = vo;
         ql = qol; kl = kol; v32 = vo32;
     }
@@ -2431,11 +2576,11 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
     if (trec) {
         char *rec = (char *)scr, *krec = (char *)scr + rec_bytes;
         PrepTArgs pa{d->T, d->nqk, d->nv, NC, q, k, ql, kl, v32, d->a, d->b, d->A_log, d->dt_bias, rec, krec,
-                     (int)krec_one, C, d->conv_w_dtype == VX27_BF16, d->x, d->conv_state, d->conv_w};
+                     (int)krec_one, C, d->conv_w_dtype == VX27_BF16, d->x, d->conv_state, d->conv_w, d->flags, d->norm_w};
         const dim3 pg((unsigned)NC, (unsigned)d->nqk, (unsigned)d->B);
-        if (vconv) VX_LAUNCH_NAMED(ctx, "dnp_prept", dnp_prept<true>, pg, dim3(256), pa);
+        if (xin) VX_LAUNCH_NAMED(ctx, "dnp_prept", dnp_prept<true>, pg, dim3(256), pa);
         else VX_LAUNCH_NAMED(ctx, "dnp_prept", dnp_prept<false>, pg, dim3(256), pa);
-        if (vconv && conv_state_update()) return -1;   // prept read the state before token 0
+        if (xin && conv_state_update()) return -1;   // prept read the state before token 0
         ScanTArgs sa{d->T, d->nqk, d->nv, NC, (d->nqk % 8) == 0, q, k, ql, kl, rec, krec, (int)krec_one, d->S, d->out};
         const dim3 sg((unsigned)(d->nv * NSLICE / (two ? 2 : 1)), (unsigned)d->B);
         if (two) VX_LAUNCH_NAMED(ctx, "dnp_scant", dnp_scant<2>, sg, dim3(256), sa);
