@@ -648,6 +648,16 @@ __device__ __forceinline__ double row16_sum(double v) {
     for (int off = 1; off < 16; off <<= 1) v += __shfl_xor(v, off, 64);
     return v;
 }
+// The same sum on the DPP paths (no LDS round trips): quad exchanges 1 and 2,
+// row rotations by 4 and 8 (a fixed tree), then lane 0's total broadcast to
+// its row, so that every lane of a row holds the same bits.
+__device__ __forceinline__ double row16_sum_dpp(double v) {
+    v = v + vx_dpp_f64<0xB1, 0xF>(v);    // quad_perm [1,0,3,2]
+    v = v + vx_dpp_f64<0x4E, 0xF>(v);    // quad_perm [2,3,0,1]
+    v = v + vx_dpp_f64<0x124, 0xF>(v);   // row_ror:4
+    v = v + vx_dpp_f64<0x128, 0xF>(v);   // row_ror:8
+    return vx_dpp_f64<0x150, 0xF>(v);    // row_newbcast:0
+}
 
 // LDS of dnp_prept, 77 KiB (two workgroups a CU), four regions whose
 // contents change with the phase (XIN, phase 1 first: the x windows of the
@@ -741,6 +751,7 @@ __global__ __launch_bounds__(256, 2) void dnp_prept(PrepTArgs p) {   // (two wor
             load_conv_w(p.conv_w, p.w_bf16, chq, xq[hc]);
             load_conv_w(p.conv_w, p.w_bf16, chk, xk[hc]);
         }
+        if (tid < HD) M_t[tid] = p.norm_w ? p.norm_w[tid] : 1.0f;   // (M_t is free until phase 4)
     } else {
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -824,8 +835,8 @@ __global__ __launch_bounds__(256, 2) void dnp_prept(PrepTArgs p) {   // (two wor
         // the row's 16 lanes), rows past the prompt zero, and the bf16 hi/lo
         // split of the values
         float nw[8];
-#pragma unroll
-        for (int e = 0; e < 8; e++) nw[e] = p.norm_w ? p.norm_w[8 * seg + e] : 1.0f;
+        *(float4 *)&nw[0] = *(const float4 *)&M_t[8 * seg];
+        *(float4 *)&nw[4] = *(const float4 *)&M_t[8 * seg + 4];
         const float qs = 1.0f / sqrtf((float)HD);
 #pragma unroll
         for (int j = 0; j < 4; j++) {
@@ -842,8 +853,8 @@ __global__ __launch_bounds__(256, 2) void dnp_prept(PrepTArgs p) {   // (two wor
                     ssq = ssq + (double)vq[e] * (double)vq[e];
                     ssk = ssk + (double)vk[e] * (double)vk[e];
                 }
-                ssq = row16_sum(ssq);
-                ssk = row16_sum(ssk);
+                ssq = row16_sum_dpp(ssq);
+                ssk = row16_sum_dpp(ssk);
                 const float iq = 1.0f / sqrtf((float)(ssq / HD) + 1e-6f), ik = 1.0f / sqrtf((float)(ssk / HD) + 1e-6f);
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
@@ -858,8 +869,8 @@ __global__ __launch_bounds__(256, 2) void dnp_prept(PrepTArgs p) {   // (two wor
                     ssq = ssq + (double)vq[e] * (double)vq[e];
                     ssk = ssk + (double)vk[e] * (double)vk[e];
                 }
-                ssq = row16_sum(ssq);
-                ssk = row16_sum(ssk);
+                ssq = row16_sum_dpp(ssq);
+                ssk = row16_sum_dpp(ssk);
                 const float iq = 1.0f / sqrtf((float)ssq + 1e-6f), ik = 1.0f / sqrtf((float)ssk + 1e-6f);
 #pragma unroll
                 for (int e = 0; e < 8; e++) {
@@ -905,8 +916,8 @@ __global__ __launch_bounds__(256, 2) void dnp_prept(PrepTArgs p) {   // (two wor
             sq = sq + q0 * q0;
             sq = sq + q1 * q1;
         }
-        sk = row16_sum(sk);
-        sq = row16_sum(sq);
+        sk = row16_sum_dpp(sk);
+        sq = row16_sum_dpp(sq);
         if (seg == 0) {   // l2norm, vx27_deltanet.c:51-56
             ik_s[r] = 1.0f / sqrtf((float)sk + 1e-6f);
             iq_s[r] = 1.0f / sqrtf((float)sq + 1e-6f);
