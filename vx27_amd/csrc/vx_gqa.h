@@ -32,7 +32,9 @@ __device__ __forceinline__ float vx_rope_angle(float freq, int pos, float yarn) 
     return ((float)pos / yarn) * freq;
 }
 __device__ __forceinline__ float2 vx_rope_cs_angle(float ang) {
-    return make_float2(cosf(ang), sinf(ang));
+    float sn, cs;
+    sincosf(ang, &sn, &cs);   // (one argument reduction for both)
+    return make_float2(cs, sn);
 }
 __device__ __forceinline__ float2 vx_rope_cs_f(float freq, int pos, float yarn) {
     return vx_rope_cs_angle(vx_rope_angle(freq, pos, yarn));

@@ -162,10 +162,9 @@ __global__ __launch_bounds__(256) void gqp_kv(KvArgs a) {
             ss[jj] += (double)x[jj][e] * (double)x[jj][e];
         }
     }
+    // (wave sums on the DPP paths: no LDS round trips)
 #pragma unroll
-    for (int off = 32; off >= 1; off >>= 1)
-#pragma unroll
-        for (int jj = 0; jj < VB / 4; jj++) ss[jj] += __shfl_xor(ss[jj], off, 64);
+    for (int jj = 0; jj < VB / 4; jj++) ss[jj] = vx_wave_sum_f64_dpp(ss[jj]);
     __syncthreads();   // csn and vt complete
 
     // V block [256 dims][32 positions]: thread -> (dim, 8 positions)
