@@ -326,46 +326,45 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
         const f4v v = DN_STATE_NT_LD ? __builtin_nontemporal_load(sp) : *sp;
         S4[r] = make_float4(v.x, v.y, v.z, v.w);
     }
-    // wave 0 owns the head's q, k and v: elements lane and lane + 64.  With
-    // the fused conv (nv == nqk: g == vh) it loads the conv's inputs for this
-    // head's q, k and v channels, branch-free (each channel's weights as two
-    // 8-byte words: the second one repeats the first for bf16), and runs the
-    // conv below.
-    float qa[2] = {0.f, 0.f}, ka[2] = {0.f, 0.f}, va[2] = {0.f, 0.f};
+    // waves 0, 1 and 2 own the head's q, k and v (elements lane and
+    // lane + 64 each), so the three chains run side by side; wave 3 maps the
+    // gates.  With the fused conv (nv == nqk: g == vh) a wave loads the
+    // conv's inputs for its 128 channels, branch-free (each channel's weights
+    // as two 8-byte words: the second one repeats the first for bf16), and
+    // runs the conv below.
     const int qd = a.nqk * HD, Cc = 2 * qd + a.nv * HD;
-    uint2 cw[2][3][2];
-    float cs[2][3][3], cx[2][3];
-    if (wave == 0) {
+    const int own = wave < 3 ? wave : -1;   // 0: q, 1: k, 2: v
+    float xa[2] = {0.f, 0.f};
+    uint2 cw[2][2];
+    float cs[2][3], cx[2];
+    if (own >= 0) {
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int i = lane + 64 * h;
+            const size_t ch = own == 0 ? (size_t)g * HD + i : own == 1 ? (size_t)qd + g * HD + i
+                                                                       : (size_t)2 * qd + (size_t)vh * HD + i;
             if (FC) {
-                const size_t ch[3] = {(size_t)g * HD + i, (size_t)qd + g * HD + i,
-                                      (size_t)2 * qd + (size_t)vh * HD + i};
                 const float *x = a.x + (size_t)b * a.b_step * Cc;
                 const float *cst = a.conv_state + (size_t)b * Cc * 3;
                 const uint2 *wb = (const uint2 *)a.conv_w;
+                const size_t w0 = a.conv_bf16 ? ch : 2 * ch;
+                cw[h][0] = wb[w0];
+                cw[h][1] = wb[a.conv_bf16 ? w0 : w0 + 1];
 #pragma unroll
-                for (int j = 0; j < 3; j++) {
-                    const size_t w0 = a.conv_bf16 ? ch[j] : 2 * ch[j];
-                    cw[h][j][0] = wb[w0];
-                    cw[h][j][1] = wb[a.conv_bf16 ? w0 : w0 + 1];
-#pragma unroll
-                    for (int t = 0; t < 3; t++) cs[h][j][t] = cst[ch[j] * 3 + t];
-                    cx[h][j] = x[ch[j]];
-                }
+                for (int t = 0; t < 3; t++) cs[h][t] = cst[ch * 3 + t];
+                cx[h] = x[ch];
             } else {
                 const size_t bs = (size_t)b * a.b_step;
-                qa[h] = a.q[bs * a.q_tok + (size_t)g * HD + i];
-                ka[h] = a.k[bs * a.k_tok + (size_t)g * HD + i];
-                va[h] = a.v[bs * a.v_tok + (size_t)vh * HD + i];
+                xa[h] = own == 0 ? a.q[bs * a.q_tok + (size_t)g * HD + i]
+                      : own == 1 ? a.k[bs * a.k_tok + (size_t)g * HD + i]
+                                 : a.v[bs * a.v_tok + (size_t)vh * HD + i];
             }
         }
     }
     const bool gate = (a.flags & VX27_DN_OUT_GATE) != 0;
     float z0 = 0.f, z1 = 0.f, w0 = 1.f, w1 = 1.f;
-    if (wave == 0 && (gate || !(a.flags & VX_DN_QK_READY))) {
-        if (gate) {
+    if ((wave == 0 && gate) || (own >= 0 && own < 2 && !(a.flags & VX_DN_QK_READY))) {
+        if (wave == 0 && gate) {
             z0 = a.z[(size_t)b * a.b_step * a.z_tok + (size_t)vh * HD + lane];
             z1 = a.z[(size_t)b * a.b_step * a.z_tok + (size_t)vh * HD + lane + 64];
         }
@@ -374,99 +373,80 @@ __global__ __launch_bounds__(512) void dn_step_kernel(DnArgs a) {
             w1 = a.norm_w[lane + 64];
         }
     }
-    // gate inputs (uniform addresses: scalar loads)
+    // gates: given (double2), or mapped by wave 3 (vx27_deltanet_gate_params,
+    // vx27_deltanet.c:65-69, decay = exp(g_log)) and passed on in LDS
+    __shared__ double s_gt[2];
     const size_t ge = (size_t)b * a.b_step * a.nv + vh;
-    double2 gt = {0.0, 0.0};
-    float gbv = 0.f, gav = 0.f, alog = 0.f, dtb = 0.f;
+    double beta = 0.0, decay = 0.0;
     if (a.gates) {
-        gt = a.gates[ge];
-    } else {
-        gbv = a.gb[ge];
-        gav = a.ga[ge];
-        alog = a.A_log[vh];
-        dtb = a.dt_bias[vh];
-    }
-    double beta, decay;
-    if (a.gates) {
+        const double2 gt = a.gates[ge];
         beta = gt.x;
         decay = gt.y;
-    } else {   // vx27_deltanet_gate_params (vx27_deltanet.c:65-69), decay = exp(g_log)
-        beta = 1.0 / (1.0 + exp(-(double)gbv));
-        decay = exp(-exp((double)alog) * softplus_d((double)gav + (double)dtb));
+    } else if (wave == 3) {
+        const float gbv = a.gb[ge], gav = a.ga[ge], alog = a.A_log[vh], dtb = a.dt_bias[vh];
+        const double bt = 1.0 / (1.0 + exp(-(double)gbv));
+        const double dc = exp(-exp((double)alog) * softplus_d((double)gav + (double)dtb));
+        if (lane == 0) {
+            s_gt[0] = bt;
+            s_gt[1] = dc;
+        }
     }
-    if (FC && wave == 0) {   // causal conv + SiLU, conv state written back
+    if (FC && own >= 0) {   // causal conv + SiLU, the wave's conv state written back
         float *cst = a.conv_state + (size_t)b * Cc * 3;
 #pragma unroll
         for (int h = 0; h < 2; h++) {
             const int i = lane + 64 * h;
-            const size_t ch[3] = {(size_t)g * HD + i, (size_t)qd + g * HD + i,
-                                  (size_t)2 * qd + (size_t)vh * HD + i};
-            float w[3][4];
+            const size_t ch = own == 0 ? (size_t)g * HD + i : own == 1 ? (size_t)qd + g * HD + i
+                                                                       : (size_t)2 * qd + (size_t)vh * HD + i;
+            float w[4];
+            const uint32_t r[4] = {cw[h][0].x, cw[h][0].y, cw[h][1].x, cw[h][1].y};
+            conv_w_decode(a.conv_bf16, r, w);
+            xa[h] = conv_step(cs[h], w, cx[h]);
 #pragma unroll
-            for (int j = 0; j < 3; j++) {
-                const uint32_t r[4] = {cw[h][j][0].x, cw[h][j][0].y, cw[h][j][1].x, cw[h][j][1].y};
-                conv_w_decode(a.conv_bf16, r, w[j]);
-            }
-            qa[h] = conv_step(cs[h][0], w[0], cx[h][0]);
-            ka[h] = conv_step(cs[h][1], w[1], cx[h][1]);
-            va[h] = conv_step(cs[h][2], w[2], cx[h][2]);
-#pragma unroll
-            for (int j = 0; j < 3; j++)
-#pragma unroll
-                for (int t = 0; t < 3; t++) cst[ch[j] * 3 + t] = cs[h][j][t];
+            for (int t = 0; t < 3; t++) cst[ch * 3 + t] = cs[h][t];
         }
     }
-    if (wave == 0 && !(a.flags & VX_DN_QK_READY)) {
-        // q/k normalisation chain (vx27_qfwd.c:119-130 per flags, then
-        // step_exact's own l2norm, vx27_deltanet.c:77-80), all in wave 0:
+    if (own >= 0 && own < 2 && !(a.flags & VX_DN_QK_READY)) {
+        // the q (wave 0) or k (wave 1) normalisation chain (vx27_qfwd.c:119-130
+        // per flags, then step_exact's own l2norm, vx27_deltanet.c:77-80):
         // sums of squares in double, each lane's two elements, then the
         // wave's DPP tree; no barriers, and the state loads stay in flight.
         const float qs = 1.0f / sqrtf((float)HD);
         const float nw[2] = {w0, w1};
-        auto sums = [&](double &sq, double &sk) {
-            sq = vx_wave_sum_f64_dpp((double)qa[0] * (double)qa[0] + (double)qa[1] * (double)qa[1]);
-            sk = vx_wave_sum_f64_dpp((double)ka[0] * (double)ka[0] + (double)ka[1] * (double)ka[1]);
-        };
-        double sq, sk;
+        const bool isq = own == 0;
+        auto sum = [&]() { return vx_wave_sum_f64_dpp((double)xa[0] * (double)xa[0] + (double)xa[1] * (double)xa[1]); };
         if (a.flags & VX27_DN_PRE_RMS) {       // rmsn(x)*(1+w), vx27_qfwd.c:32-39,123
-            sums(sq, sk);
-            const float iq = 1.0f / sqrtf((float)(sq / HD) + 1e-6f);
-            const float ik = 1.0f / sqrtf((float)(sk / HD) + 1e-6f);
+            const double ss = sum();
+            const float is = 1.0f / sqrtf((float)(ss / HD) + 1e-6f);
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                qa[h] = (qa[h] * iq) * (nw[h] + 1.0f);
-                ka[h] = (ka[h] * ik) * (nw[h] + 1.0f);
-            }
+            for (int h = 0; h < 2; h++) xa[h] = (xa[h] * is) * (nw[h] + 1.0f);
         }
         if (a.flags & VX27_DN_PRE_L2) {        // l2norm + q/sqrt(hd), vx27_qfwd.c:124-130
-            sums(sq, sk);
-            const float iq = 1.0f / sqrtf((float)sq + 1e-6f), ik = 1.0f / sqrtf((float)sk + 1e-6f);
+            const double ss = sum();
+            const float il = 1.0f / sqrtf((float)ss + 1e-6f);
 #pragma unroll
             for (int h = 0; h < 2; h++) {
-                qa[h] = qa[h] * iq;
-                ka[h] = ka[h] * ik;
-                qa[h] = qa[h] * qs;
+                xa[h] = xa[h] * il;
+                if (isq) xa[h] = xa[h] * qs;
             }
         }
         {                                       // inside step_exact, vx27_deltanet.c:77-80
-            sums(sq, sk);
-            const float iq = 1.0f / sqrtf((float)sq + 1e-6f), ik = 1.0f / sqrtf((float)sk + 1e-6f);
+            const double ss = sum();
+            const float il = 1.0f / sqrtf((float)ss + 1e-6f);
 #pragma unroll
-            for (int h = 0; h < 2; h++) {
-                qa[h] = (qa[h] * iq) * qs;
-                ka[h] = ka[h] * ik;
-            }
+            for (int h = 0; h < 2; h++) xa[h] = isq ? (xa[h] * il) * qs : xa[h] * il;
         }
     }
-    if (wave == 0) {   // v goes through LDS too, so its use waits on nothing late
+    if (own >= 0) {   // v goes through LDS too, so its use waits on nothing late
+        float *dst = own == 0 ? s_qn : own == 1 ? s_kn : s_v;
 #pragma unroll
-        for (int h = 0; h < 2; h++) {
-            s_qn[lane + 64 * h] = qa[h];
-            s_kn[lane + 64 * h] = ka[h];
-            s_v[lane + 64 * h] = va[h];
-        }
+        for (int h = 0; h < 2; h++) dst[lane + 64 * h] = xa[h];
     }
     __syncthreads();
+    if (!a.gates) {
+        beta = s_gt[0];
+        decay = s_gt[1];
+    }
 
     float kn[8], qn[8];
     {
