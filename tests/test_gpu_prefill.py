@@ -129,10 +129,10 @@ def test_dn_prefill_split_prompt(ctx):
 
 
 # ------------------------------------------------------------------ GQA
-def run_gqa_prefill(ctx, d, L, prior=None, interleave=False, flags=0, rope_dim=64):
+def run_gqa_prefill(ctx, d, L, prior=None, interleave=False, flags=0, rope_dim=64, stale=0xFF):
     """Prefill the workload's T tokens at positions pos0.. into a fresh cache of
-    capacity L (rows < pos0 from `prior` = (k, v) fp32 [B][pos0][n_kv][256]);
-    returns out [B][T][n_q][256]."""
+    capacity L (rows < pos0 from `prior` = (k, v) fp32 [B][pos0][n_kv][256],
+    every other row filled with the byte `stale`); returns out [B][T][n_q][256]."""
     from vx27_amd import lib as L_
     lib = L_.lib()
     B, T, n_q, hd = d["q"].shape
@@ -140,8 +140,8 @@ def run_gqa_prefill(ctx, d, L, prior=None, interleave=False, flags=0, rope_dim=6
     pos0 = d["pos0"]
     kc = ctx.buf(B * n_kv * L * hd * 2)
     vc = ctx.buf(B * n_kv * L * hd * 2)
-    lib.vx27_hip_memset(ctx.h, kc.ptr, 0xFF, kc.nbytes)       # stale rows hold NaN bit patterns
-    lib.vx27_hip_memset(ctx.h, vc.ptr, 0xFF, vc.nbytes)
+    lib.vx27_hip_memset(ctx.h, kc.ptr, stale, kc.nbytes)       # 0xFF: stale rows hold NaN bit patterns
+    lib.vx27_hip_memset(ctx.h, vc.ptr, stale, vc.nbytes)
     keep = []
     if prior is not None:
         for b in range(B):
@@ -216,6 +216,26 @@ def test_gqa_prefill_shapes(ctx, B, T, pos0, L, inter):
     out = run_gqa_prefill(ctx, d, L, prior, inter)
     ref, _ = oracle_gqa_prefill(d, L, prior)
     check_bf16(out, ref, "out")
+
+
+@pytest.mark.parametrize("B,T,pos0,L", [(1, 1300, 0, 1408), (2, 200, 100, 320), (1, 40, 0, 64), (1, 97, 20, 128)])
+def test_gqa_prefill_stale_rows_inert(ctx, B, T, pos0, L):
+    """Cache rows past pos0 + T take no part in any output bit: the same
+    prefill over caches whose stale rows hold zeros, huge finite values
+    (bf16 0x7F7F) and NaNs gives identical outputs.  The shapes leave the
+    last query block partly (or, for whole waves, entirely) past T, the rows
+    whose positions run into the stale keys."""
+    from vx27_amd import workloads as W
+    d = W.gqa_prefill(B=B, T=T, pos0=pos0, config=55)
+    say(f"gqa_prefill stale rows: B={B} T={T} pos0={pos0} L={L}")
+    prior = None
+    if pos0:
+        r = W.rng(56, "gqa_prefill_prior")
+        prior = tuple(W.bf16_to_f32(W.bf16_bits(W.normal(r, (B, pos0, 4, 256)))) for _ in range(2))
+    outs = [run_gqa_prefill(ctx, d, L, prior, stale=f) for f in (0x00, 0x7F, 0xFF)]
+    assert np.isfinite(outs[0]).all()
+    for o, f in zip(outs[1:], ("0x7F", "0xFF")):
+        assert np.array_equal(o, outs[0]), f"stale rows filled with {f} change the output"
 
 
 @pytest.mark.parametrize("rope_dim", [0, 128])

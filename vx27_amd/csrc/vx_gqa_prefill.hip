@@ -462,7 +462,11 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
     const int wg_last = a.pos0 + min(qt * QT + QT, a.T) - 1;
     const int n_tiles = wg_last / KT + 1;
     const int wave_tiles = (a.pos0 + min(r0 + RB * 16 - 1, a.T - 1)) / KT + 1;   // tiles with a key this wave sees
-    const int n_main = min((a.pos0 + r0 + 1) / KT, n_tiles);   // tiles with no key past any query of this wave
+    // tiles with no key past any query of this wave (a wave wholly past the T
+    // new tokens counts as the last one: its main tiles then end before the
+    // partial last tile, which every wave takes as a tail interval, with the
+    // barrier of its V zeroing)
+    const int n_main = min((a.pos0 + min(r0, a.T - 1) + 1) / KT, n_tiles);
     const char *Kc = (const char *)(a.k_cache + vx_k_index(a.n_kv, a.L, b, kvh, 0, 0));
     const char *Vc = (const char *)(a.v_cache + vx_v_index(a.n_kv, a.L, b, kvh, 0, 0));
 
@@ -556,10 +560,14 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
                     x[kb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(kf[ks & 1][kb], qv[rb][ks], x[kb][rb], 0, 0, 0);
         }
     };
-    auto mask = [&](int k0, floatx4_t (&x)[4][RB]) {   // causal: keys past the query's position
+    // causal: keys past the query's position.  Rows past the T new tokens
+    // (the last query block's padding, never stored) are masked as the last
+    // token: keys past the cache's valid ones hold stale data, and an
+    // overflow there would send the wave's valid rows down the fallback.
+    auto mask = [&](int k0, floatx4_t (&x)[4][RB]) {
 #pragma unroll
         for (int rb = 0; rb < RB; rb++) {
-            const int qpos = a.pos0 + r0 + rb * 16 + n;
+            const int qpos = min(a.pos0 + r0 + rb * 16 + n, n_keys - 1);
 #pragma unroll
             for (int kb = 0; kb < 4; kb++)
 #pragma unroll
@@ -727,7 +735,7 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
     floatx4_t sS[4][RB];
     zero_s(sS);
     s_tile(Kl[0], sS);
-    if (KT - 1 > a.pos0 + r0) mask(0, sS);
+    if (KT - 1 > min(a.pos0 + r0, n_keys - 1)) mask(0, sS);
 #pragma unroll
     for (int rb = 0; rb < RB; rb++) {
         m0[rb] = row_max(sS, rb);
