@@ -679,6 +679,70 @@ def bench_dn_prefill_glue(ctx, T=4096, iters=10):
     return res
 
 
+def bench_layer_prefill(ctx, T=4096, iters=5):
+    """Both mixer layers on one T-token prompt with their projections
+    (vx27_hip_dn_layer_prefill, vx27_hip_gqa_layer_prefill at the real layer
+    shapes, hidden 5120): from 256 tokens on the projections run in the
+    long-prompt GEMM (weights read once per 256 tokens, x as two bf16 parts).
+    Synthetic weights filled on the device straight into the tiled layout."""
+    from vx27_amd import lib as L, workloads as W
+    H, nqk, nv, hd = 5120, 16, 48, 128
+    qd, vd = nqk * hd, nv * hd
+    C_ = 2 * qd + vd
+    Nin = C_ + vd + 2 * nv
+    Nqkv, Ka = 24 * 2 * 256 + 2 * 4 * 256, 24 * 256
+    x = ctx.buf(T * H * 4)
+    ctx.fill_normal(x, T * H, 31)
+    out = ctx.buf(T * H * 4)
+    res = {}
+    # DeltaNet layer
+    d = W.dn_prefill_glue(B=1, T=1, nqk=nqk, nv=nv)
+    w_in, w_out = ctx.buf(Nin * H * 2), ctx.buf(H * vd * 2)
+    ctx.fill_normal(w_in, Nin * H, 32, 0.02, bf16=True)
+    ctx.fill_normal(w_out, H * vd, 33, 0.02, bf16=True)
+    bufs = {k: ctx.put(d[k]) for k in ("A_log", "dt_bias", "S0", "conv0", "conv_w_bf16", "norm_w")}
+    desc = L.DnLayerPrefillDesc(1, T, nqk, nv, hd, H, 0, x.ptr, w_in.ptr, w_out.ptr, bufs["conv_w_bf16"].ptr,
+                                L.BF16, bufs["A_log"].ptr, bufs["dt_bias"].ptr, bufs["norm_w"].ptr,
+                                bufs["S0"].ptr, bufs["conv0"].ptr, out.ptr)
+
+    def run_dn():
+        L.check(L.lib().vx27_hip_dn_layer_prefill(ctx.h, C.byref(desc)), "dn_layer_prefill")
+    run_dn()
+    kern = ("gemm_wx", "pack_x", "gemv_wk_store") + DNP_KERNELS
+    wall_us, per = _time_calls(ctx, run_dn, kern, iters)
+    per = {k: round(v, 1) for k, v in per.items() if v > 0}
+    proj_flops = 2.0 * T * (Nin * H + H * vd)
+    res["dn"] = {"workload": f"DeltaNet layer prefill B=1 T={T} nqk=16 nv=48 hidden=5120 (projections + "
+                             f"chunked core)", "us_per_call": wall_us, "kernel_us": sum(per.values()),
+                 "kernels_us": per, "tokens_per_s": T / (sum(per.values()) / 1e6),
+                 "projection_tflops": proj_flops / (per.get("gemm_wx", 0) * 1e-6) / 1e12 if per.get("gemm_wx") else None}
+    for b in list(bufs.values()) + [w_in, w_out]:
+        b.free()
+    # gated GQA layer, positions 0 .. T-1 of a T-row cache
+    w_qkv, w_o = ctx.buf(Nqkv * H * 2), ctx.buf(H * Ka * 2)
+    ctx.fill_normal(w_qkv, Nqkv * H, 34, 0.02, bf16=True)
+    ctx.fill_normal(w_o, H * Ka, 35, 0.02, bf16=True)
+    qn, kn = ctx.put(W.normal(W.rng(36, "lp_qn"), 256, 0.1)), ctx.put(W.normal(W.rng(37, "lp_kn"), 256, 0.1))
+    kc, vc = ctx.buf(T * 4 * 256 * 2), ctx.buf(T * 4 * 256 * 2)
+    g = L.GqaLayerPrefillDesc(1, T, 24, 4, 256, H, 64, 1e7, 1.0, T, 0, 0, x.ptr, w_qkv.ptr, w_o.ptr, qn.ptr, kn.ptr,
+                              kc.ptr, vc.ptr, out.ptr)
+
+    def run_gqa():
+        L.check(L.lib().vx27_hip_gqa_layer_prefill(ctx.h, C.byref(g)), "gqa_layer_prefill")
+    run_gqa()
+    kern = ("gemm_wx", "pack_x", "gemv_wk_store", "qkv_to_bf16", "gqp_kv", "gqp_attn")
+    wall_us, per = _time_calls(ctx, run_gqa, kern, iters)
+    per = {k: round(v, 1) for k, v in per.items() if v > 0}
+    proj_flops = 2.0 * T * (Nqkv * H + H * Ka)
+    res["gqa"] = {"workload": f"gated GQA layer prefill B=1 T={T} 24Q/4KV hd 256 hidden=5120 (projections + "
+                              f"causal attention)", "us_per_call": wall_us, "kernel_us": sum(per.values()),
+                  "kernels_us": per, "tokens_per_s": T / (sum(per.values()) / 1e6),
+                  "projection_tflops": proj_flops / (per.get("gemm_wx", 0) * 1e-6) / 1e12 if per.get("gemm_wx") else None}
+    for b in (w_qkv, w_o, qn, kn, kc, vc, x, out):
+        b.free()
+    return res
+
+
 def bench_gqa_prefill(ctx, T=4096, iters=10, cpu=True):
     """Causal gated GQA prefill: one T-token prompt, 24Q/4KV hd 256."""
     from vx27_amd import lib as L, workloads as W
@@ -750,7 +814,8 @@ def main():
                 "c2": lambda: {f"c2_gqa8k_B{B}": bench_gqa(ctx, B, cpu=cpu) for B in (1, 4, 32)},
                 "c3": lambda: {f"c3_dn_conv_B{B}": bench_dn_conv(ctx, 256, 8, B=B, cpu=cpu and B == 64)
                                for B in (1, 4, 16, 64)},
-                "layers": lambda: {f"layer_decode_B{B}": bench_layer_decode(ctx, B) for B in (4, 16, 64)},
+                "layers": lambda: dict({f"layer_decode_B{B}": bench_layer_decode(ctx, B) for B in (4, 16, 64)},
+                                       layer_prefill_T4096=bench_layer_prefill(ctx)),
                 "c4": lambda: {"c4a_dn_prefill_T4096": bench_dn_prefill(ctx, cpu=cpu),
                                "c4a_dn_prefill_layer_T4096": bench_dn_prefill_glue(ctx),
                                "c4b_gqa_prefill_T4096": bench_gqa_prefill(ctx, cpu=cpu)}}
@@ -819,6 +884,12 @@ def main():
         log(f"  gqa_prefill: {r['kernel_us']:.1f} us ({r['tokens_per_s']:.3g} tok/s), "
             f"MFMA {100 * r['mfma_frac']:.1f}% (attention kernel {100 * r['attn_mfma_frac']:.1f}%)  "
             f"{r['kernels_us']}")
+        r = bench_layer_prefill(ctx)
+        extra["layer_prefill_T4096"] = r
+        for kind in ("dn", "gqa"):
+            q = r[kind]
+            log(f"  {kind} layer prefill T=4096 with projections: {q['kernel_us']:.0f} us "
+                f"({q['tokens_per_s']:.3g} tok/s), projections {q['projection_tflops']:.0f} TFLOP/s  {q['kernels_us']}")
         r = bench_dn_recurrent(ctx, cpu=cpu)
         extra["c1_dn_recurrent"] = r
         log(f"  dn_recurrent: {r['us_per_step_resident']:.2f} us/step (state resident, one call), "

@@ -8,7 +8,9 @@ calls of vx27_hip_dn_layer_decode, states and checkpoints included, and
 within 1e-5 of the oracle's layer glue applied token by token; the chunked
 default (split-precision products) on the oracle's outputs within 1e-3 of
 max|ref| and the bf16 bar.  GQA: the attention bar and 2% of max|ref| against
-the oracle's per-token layer (q/k/v enter the prefill attention as bf16)."""
+the oracle's per-token layer (q/k/v enter the prefill attention as bf16).
+From 256 tokens on, the projections run in the long-prompt GEMM: 4096-token
+prompts of both layers, checked on a 256-token prefix."""
 import ctypes as C
 
 import numpy as np
@@ -132,4 +134,54 @@ def test_gqa_layer_prefill(ctx):
     big = np.abs(ref).max()
     say(f"  gqa layer prefill: max|d|={err.max():.3e} (max|ref|={big:.3f})")
     assert np.all(np.isfinite(out))
+    assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)) and err.max() <= 0.02 * big
+
+
+def test_dn_layer_prefill_long_prompt(ctx):
+    """A 4096-token prompt through the DeltaNet layer (nqk 16, nv 48, hidden
+    5120): the projections run in the long-prompt GEMM (x as two bf16 parts)
+    and the core in the chunked form.  Its first 256 outputs depend on the
+    first 256 tokens only, so they are checked against the oracle's per-token
+    layer on that prefix, to the chunked form's bar (1e-4 of max|ref|)."""
+    import time
+    from vx27_amd import workloads as W
+    B, T, P, nqk, nv = 1, 4096, 256, 16, 48
+    r = W.rng(15, "dn_layer_prefill_long")
+    w, S, conv = dn_layer_inputs(r, B, nqk, nv)
+    x = W.normal(r, (B, T, H))
+    dev = dn_device(ctx, w)
+    g = run_dn_layer_prefill(ctx, dev, x, S, conv)
+    assert np.all(np.isfinite(g["out"])) and np.all(np.isfinite(g["S"]))
+    t0 = time.perf_counter()
+    Sr, cr = S.copy(), conv.copy()
+    ref = np.stack([oracle_dn_layer(w, np.ascontiguousarray(x[:, t]), Sr, cr, nqk, nv) for t in range(P)], axis=1)
+    err = np.abs(g["out"][:, :P].astype(np.float64) - ref)
+    big = np.abs(ref).max()
+    say(f"  4096-token layer, first {P} tokens: max|d out|={err.max():.3e} (max|ref|={big:.3f}); "
+        f"oracle {time.perf_counter() - t0:.1f}s")
+    assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)) and err.max() <= 1e-4 * big
+
+
+def test_gqa_layer_prefill_long_prompt(ctx):
+    """A 4096-token prompt through the gated GQA layer from position 0: the
+    projections run in the long-prompt GEMM; the first 256 outputs against the
+    oracle's per-token layer (the attention bar)."""
+    from vx27_amd import lib as L, mixers as M, workloads as W
+    B, T, P, Lcap = 1, 4096, 256, 4096
+    r = W.rng(16, "gqa_layer_prefill_long")
+    w, kc, vc = gqa_layer_inputs(r, B, Lcap, 0)
+    x = W.normal(r, (B, T, H))
+    lay = M.GatedGQALayer(ctx, B, Lcap, w["q_norm_w"], w["k_norm_w"])
+    wq, wo = ctx.put_tiled(w["w_qkv"]), ctx.put_tiled(w["w_o"])
+    xb, ob = ctx.put(x), ctx.buf(B * T * H * 4)
+    d = L.GqaLayerPrefillDesc(B, T, 24, 4, 256, H, 64, 1e7, 1.0, Lcap, 0, 0, xb.ptr, wq.ptr, wo.ptr,
+                              lay.q_norm_w.ptr, lay.k_norm_w.ptr, lay.k_cache.ptr, lay.v_cache.ptr, ob.ptr)
+    L.check(L.lib().vx27_hip_gqa_layer_prefill(ctx.h, C.byref(d)), "gqa_layer_prefill")
+    out = ob.download((B, T, H), np.float32)
+    assert np.all(np.isfinite(out))
+    ref = np.stack([oracle_gqa_layer(w, np.ascontiguousarray(x[:, t]), kc, vc, np.full(B, t, np.int32))
+                    for t in range(P)], axis=1)
+    err = np.abs(out[:, :P].astype(np.float64) - ref)
+    big = np.abs(ref).max()
+    say(f"  4096-token gqa layer, first {P} tokens: max|d|={err.max():.3e} (max|ref|={big:.3f})")
     assert np.all(err <= 2e-2 + 1e-2 * np.abs(ref)) and err.max() <= 0.02 * big

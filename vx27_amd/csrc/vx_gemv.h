@@ -37,6 +37,31 @@ int vx_pack(vx27_hip_ctx *ctx, const float *x, size_t x_stride, int B, int K, ui
 int vx_gemv_store(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const uint16_t *packed, int B, float *y,
                   size_t y_stride, bool y_zeroed = false);
 
+// The projection of R tokens at once (vx_gemm.hip): y[r][n] = sum over k of
+// W[n][k] x_r[k] for tiled W, fp32 x rows (x as two bf16 parts; K % 64 == 0,
+// 16-byte aligned rows, R x_stride 4 < 2^31).
+int vx_gemm_store(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x, size_t x_stride, int R,
+                  float *y, size_t y_stride);
+// whether vx_gemm_store takes this shape (else the GEMV passes)
+bool vx_gemm_fits(int N, int K, int R, const float *x, size_t x_stride, const float *y, size_t y_stride);
+// Output in segments: rows n >= 16 rb0 of segment s (up to the next
+// segment's) go to p[r * stride + n - 16 rb0], as fp32 or as bf16 (round to
+// nearest even, vx_f32_to_bf16).  Segment 0 starts at rb0 = 0.
+struct GemmSeg {
+    int rb0, bf16;
+    size_t stride;
+    void *p;
+};
+constexpr int VX_GEMM_SEGS = 4;
+struct GemmOut {
+    int n;
+    GemmSeg s[VX_GEMM_SEGS];
+};
+int vx_gemm_store_seg(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x, size_t x_stride, int R,
+                      const GemmOut &out);
+bool vx_gemm_fits_seg(int N, int K, int R, const float *x, size_t x_stride, const GemmOut &out);
+constexpr int VX_GEMM_MIN_ROWS = 256;   // layer prefills use the GEMM from this many tokens (one token tile)
+
 // Part p (0 = hi, 1 = mid, 2 = lo) of the exact three-way bf16 split of x:
 // hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid); each difference
 // is exact in fp32.

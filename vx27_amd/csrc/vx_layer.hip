@@ -394,20 +394,42 @@ extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_
     float *gb = (float *)p; p += g_b;
     float *o = (float *)p; p += o_b;
     uint16_t *op = (uint16_t *)p; p += pk_o;
-    // [qkv | z | a | b] = W_in x for all B*T tokens (one pass over W_in per 65
-    // tokens; each row summed in the same order as in a decode step)
-    if (vx_pack(ctx, d->x, (size_t)H, R, H, xp)) return -1;
-    if (vx_gemv_store(ctx, d->w_in, Nin, H, xp, R, y, (size_t)Nin)) return -1;
-    const size_t ys = (size_t)Nin * 4;
-    VX_HIP(hipMemcpy2DAsync(xq, (size_t)C * 4, y, ys, (size_t)C * 4, (size_t)R, hipMemcpyDeviceToDevice, ctx->stream));
-    VX_HIP(hipMemcpy2DAsync(z, (size_t)vd * 4, y + C, ys, (size_t)vd * 4, (size_t)R, hipMemcpyDeviceToDevice,
-                            ctx->stream));
-    VX_HIP(hipMemcpy2DAsync(ga, (size_t)nv * 4, y + C + vd, ys, (size_t)nv * 4, (size_t)R, hipMemcpyDeviceToDevice,
-                            ctx->stream));
-    VX_HIP(hipMemcpy2DAsync(gb, (size_t)nv * 4, y + C + vd + nv, ys, (size_t)nv * 4, (size_t)R,
-                            hipMemcpyDeviceToDevice, ctx->stream));
+    // [qkv | z | a | b] = W_in x for all B*T tokens: a long prompt of the
+    // chunked form in the GEMM (W_in read once per 256 tokens, x as two bf16
+    // parts, as precise as the chunked products); otherwise one pass over W_in
+    // per 65 tokens with each row summed in the same order as in a decode step
+    // (the exact form is bit-identical to T decode calls)
+    const bool exact = (d->flags & VX27_DN_EXACT) || d->S_ckpt || d->conv_ckpt;
+    const bool gemm = !exact && R >= VX_GEMM_MIN_ROWS;
+    GemmOut seg = {};   // (the GEMM writes qkv, z, a and b straight into their buffers)
+    seg.n = 4;
+    seg.s[0] = GemmSeg{0, 0, (size_t)C, xq};
+    seg.s[1] = GemmSeg{C / 16, 0, (size_t)vd, z};
+    seg.s[2] = GemmSeg{(C + vd) / 16, 0, (size_t)nv, ga};
+    seg.s[3] = GemmSeg{(C + vd + nv) / 16, 0, (size_t)nv, gb};
+    if (gemm && nv % 16 == 0 && vx_gemm_fits_seg(Nin, H, R, d->x, (size_t)H, seg)) {
+        if (vx_gemm_store_seg(ctx, d->w_in, Nin, H, d->x, (size_t)H, R, seg)) return -1;
+    } else {
+        if (gemm && vx_gemm_fits(Nin, H, R, d->x, (size_t)H, y, (size_t)Nin)) {
+            if (vx_gemm_store(ctx, d->w_in, Nin, H, d->x, (size_t)H, R, y, (size_t)Nin)) return -1;
+        } else {
+            if (vx_pack(ctx, d->x, (size_t)H, R, H, xp)) return -1;
+            if (vx_gemv_store(ctx, d->w_in, Nin, H, xp, R, y, (size_t)Nin)) return -1;
+        }
+        const size_t ys = (size_t)Nin * 4;
+        VX_HIP(hipMemcpy2DAsync(xq, (size_t)C * 4, y, ys, (size_t)C * 4, (size_t)R, hipMemcpyDeviceToDevice,
+                                ctx->stream));
+        VX_HIP(hipMemcpy2DAsync(z, (size_t)vd * 4, y + C, ys, (size_t)vd * 4, (size_t)R, hipMemcpyDeviceToDevice,
+                                ctx->stream));
+        VX_HIP(hipMemcpy2DAsync(ga, (size_t)nv * 4, y + C + vd, ys, (size_t)nv * 4, (size_t)R,
+                                hipMemcpyDeviceToDevice, ctx->stream));
+        VX_HIP(hipMemcpy2DAsync(gb, (size_t)nv * 4, y + C + vd + nv, ys, (size_t)nv * 4, (size_t)R,
+                                hipMemcpyDeviceToDevice, ctx->stream));
+    }
     pd.x = xq; pd.z = z; pd.a = ga; pd.b = gb; pd.out = o;
     if (vx_dn_prefill_into(ctx, &pd, p)) return -1;
+    if (gemm && vx_gemm_fits(H, vd, R, o, (size_t)vd, d->out, (size_t)H))
+        return vx_gemm_store(ctx, d->w_out, H, vd, o, (size_t)vd, R, d->out, (size_t)H);
     if (vx_pack(ctx, o, (size_t)vd, R, vd, op)) return -1;
     return vx_gemv_store(ctx, d->w_out, H, vd, op, R, d->out, (size_t)H);
 }
@@ -443,11 +465,26 @@ extern "C" int vx27_hip_gqa_layer_prefill(vx27_hip_ctx *ctx, const vx27_gqa_laye
     uint16_t *vb = (uint16_t *)p; p += kv_b;
     float *att = (float *)p; p += at_b;
     uint16_t *ap = (uint16_t *)p; p += pk_a;
-    if (vx_pack(ctx, d->x, (size_t)H, R, H, xp)) return -1;
-    if (vx_gemv_store(ctx, d->w_qkv, Nqkv, H, xp, R, y, (size_t)Nqkv)) return -1;
-    VX_LAUNCH(ctx, qkv_to_bf16, dim3((unsigned)R, (unsigned)((Nqkv + 255) / 256)), dim3(256), y, Nq, kvd, qg, kb, vb);
+    // a long prompt's projections in the GEMM (weights once per 256 tokens),
+    // rounded to bf16 straight into q|gate, k and v
+    const bool gemm = R >= VX_GEMM_MIN_ROWS;
+    GemmOut seg = {};
+    seg.n = 3;
+    seg.s[0] = GemmSeg{0, 1, (size_t)Nq, qg};
+    seg.s[1] = GemmSeg{Nq / 16, 1, (size_t)kvd, kb};
+    seg.s[2] = GemmSeg{(Nq + kvd) / 16, 1, (size_t)kvd, vb};
+    if (gemm && vx_gemm_fits_seg(Nqkv, H, R, d->x, (size_t)H, seg)) {
+        if (vx_gemm_store_seg(ctx, d->w_qkv, Nqkv, H, d->x, (size_t)H, R, seg)) return -1;
+    } else {
+        if (vx_pack(ctx, d->x, (size_t)H, R, H, xp)) return -1;
+        if (vx_gemv_store(ctx, d->w_qkv, Nqkv, H, xp, R, y, (size_t)Nqkv)) return -1;
+        VX_LAUNCH(ctx, qkv_to_bf16, dim3((unsigned)R, (unsigned)((Nqkv + 255) / 256)), dim3(256), y, Nq, kvd, qg, kb,
+                  vb);
+    }
     gp.q = qg; gp.gate = qg + hd; gp.k_new = kb; gp.v_new = vb; gp.out = att;
     if (vx_gqa_prefill_into(ctx, &gp, p)) return -1;
+    if (gemm && vx_gemm_fits(H, Ka, R, att, (size_t)Ka, d->out, (size_t)H))
+        return vx_gemm_store(ctx, d->w_o, H, Ka, att, (size_t)Ka, R, d->out, (size_t)H);
     if (vx_pack(ctx, att, (size_t)Ka, R, Ka, ap)) return -1;
     return vx_gemv_store(ctx, d->w_o, H, Ka, ap, R, d->out, (size_t)H);
 }

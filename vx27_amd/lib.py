@@ -128,6 +128,7 @@ _SIGS = {
     "vx27_hip_gqa_layer_prefill": (C.c_int, [VP, C.POINTER(GqaLayerPrefillDesc)]),
     "vx27_hip_pack_bytes": (C.c_size_t, [C.c_int, C.c_int]),
     "vx27_hip_pack_weights_bf16": (C.c_int, [VP, VP, C.c_int, C.c_int, VP]),
+    "vx27_hip_gemm_bf16": (C.c_int, [VP, VP, C.c_int, C.c_int, VP, C.c_size_t, C.c_int, VP, C.c_size_t]),
     "vx27_hip_pack_x": (C.c_int, [VP, VP, C.c_int, C.c_int, VP]),
     "vx27_hip_advance_pos": (C.c_int, [VP, VP, C.c_int]),
     "vx27_hip_graph_begin": (C.c_int, [VP]),
