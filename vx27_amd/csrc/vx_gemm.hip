@@ -33,6 +33,8 @@
 // contiguous range of tile indices, numbered in groups of 4 token tiles x
 // all row tiles (token tile fastest), so the tiles an XCD runs together
 // share 4 token slabs and about 8 weight slabs in its L2.
+#include <algorithm>
+
 #include "vx_gemv.h"
 #include "vx_gemv_body.h"
 #include "vx_lds.h"
@@ -68,22 +70,61 @@ struct GemmArgs {
     const float *x;       // [R] rows of K, row stride x_stride (16-byte aligned rows)
     size_t x_stride;
     GemmOut out;          // where the rows of the product go (fp32 or bf16 segments)
-    int n_tm, n_tn, per_xcd;
+    int n_tm, n_tn;
+    // this launch: tiles tile0 .. tile0 + n_t - 1 of the tile order; P = 1:
+    // whole tiles, XCD-grouped (per_xcd a XCD); P > 1: each tile's k-steps in
+    // P parts (workgroup w: tile w % n_t, part w / n_t), the partial sums
+    // into ws, for gemm_reduce
+    int tile0, n_t, per_xcd, P;
+    floatx4_t *ws;        // [P][n_t][32 accumulators (j, i)][512 lanes], float4s
 };
+
+// (tm, tn) of tile t: groups of G_GM token tiles x all row tiles, token tile fastest
+__device__ __forceinline__ void gemm_tile(const GemmArgs &a, int t, int &tm, int &tn) {
+    const int gsize = G_GM * a.n_tn, grp = t / gsize, first_m = grp * G_GM;
+    const int msz = min(G_GM, a.n_tm - first_m), rr = t - grp * gsize;
+    tm = first_m + rr % msz;
+    tn = rr / msz;
+}
+
+// Accumulator (j, i) of lane (g, n) of wave (wm, wn): token 16 i + n of the
+// wave's 64, rows 16 j + 4 g .. +3 of its 128, into the segment that holds
+// the row block (wave-uniform).
+__device__ __forceinline__ void gemm_store1(const GemmArgs &a, int tm, int tn, int wm, int wn, int g, int n, int j,
+                                            int i, floatx4_t v) {
+    const int rb = tn * GRB + wn * 8 + j, tk = tm * GT + wm * 64 + 16 * i + n;
+    if (rb >= a.N / 16 || tk >= a.R) return;
+    int si = 0;
+#pragma unroll
+    for (int q = 1; q < VX_GEMM_SEGS; q++)
+        if (q < a.out.n && rb >= a.out.s[q].rb0) si = q;
+    const GemmSeg sg = a.out.s[si];
+    const size_t o = (size_t)tk * sg.stride + (size_t)(rb - sg.rb0) * 16 + 4 * g;
+    if (sg.bf16)
+        *(uint2 *)((uint16_t *)sg.p + o) = make_uint2(vx_f32_to_bf16(v[0]) | ((uint32_t)vx_f32_to_bf16(v[1]) << 16),
+                                                      vx_f32_to_bf16(v[2]) | ((uint32_t)vx_f32_to_bf16(v[3]) << 16));
+    else
+        *(floatx4_t *)((float *)sg.p + o) = v;
+}
 
 __global__ __launch_bounds__(512, 1) void gemm_wx(GemmArgs a) {
     __shared__ __attribute__((aligned(16))) char smem[2 * G_STAGE];
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave & 3, wn = wave >> 2;
 
-    // tile of this workgroup
-    const int xcd = blockIdx.x & 7;
-    const int t = xcd * a.per_xcd + (int)(blockIdx.x >> 3);
-    if (t >= a.n_tm * a.n_tn) return;
-    const int gsize = G_GM * a.n_tn, grp = t / gsize, first_m = grp * G_GM;
-    const int msz = min(G_GM, a.n_tm - first_m), rr = t - grp * gsize;
-    const int tm = first_m + rr % msz, tn = rr / msz;
-    const int nb = a.N / 16, KS = a.K / 32;
+    // tile (and k-steps ks0 .. ks1 - 1) of this workgroup
+    int tl, part = 0;
+    if (a.P == 1) {
+        tl = (blockIdx.x & 7) * a.per_xcd + (int)(blockIdx.x >> 3);
+        if (tl >= a.n_t) return;
+    } else {
+        tl = (int)blockIdx.x % a.n_t;
+        part = (int)blockIdx.x / a.n_t;
+    }
+    int tm, tn;
+    gemm_tile(a, a.tile0 + tl, tm, tn);
+    const int nb = a.N / 16, KSall = a.K / 32;
+    const int ks0 = part * KSall / a.P, KS = (part + 1) * KSall / a.P;   // (KS: the end)
     const int rb0 = tn * GRB, tok0 = tm * GT;
 
     // this wave's DMA of W tiles 2 wave, 2 wave + 1 (row blocks clamped:
@@ -116,9 +157,12 @@ __global__ __launch_bounds__(512, 1) void gemm_wx(GemmArgs a) {
         }
     };
     // Token tile layout: lane (g, n)'s 16 bytes (token n, k 8g..8g+7) sit at
-    // 16-byte unit g * 16 + (n ^ 8 (g & 1)): the hi/lo writes below (8 columns
-    // x 4 values of g a store) then meet each bank at most twice, and the
-    // operand reads (16 lanes of one g) stay a permutation of 16 units.
+    // 16-byte unit g * 16 + (n ^ 2g).  The LDS serves 128 bytes (32 banks) a
+    // cycle: a store below writes 8 bytes a lane, 16 lanes a cycle (2 columns
+    // x 4 values of g x 2 halves), whose units n ^ 2g then cover all 8
+    // 16-byte bank groups once (without the XOR all 16 lanes fell on the
+    // same 128 bytes: four ways, the LDS's largest cost here); the operand
+    // reads (8 lanes a cycle, one g) stay one aligned 128-byte block each.
     // Token t' = 32 wave + 8 i + lane / 8 is column t' % 16 of token block
     // t' / 16; its floats 4c..4c+3 (c = lane % 8) are elements 4 (c % 2) ..
     // of lane (c / 2, t' % 16).
@@ -131,12 +175,12 @@ __global__ __launch_bounds__(512, 1) void gemm_wx(GemmArgs a) {
             const uint2 h = make_uint2(pack2(xr[i][0], xr[i][1]), pack2(xr[i][2], xr[i][3]));
             const uint2 l = make_uint2(pack2(xr[i][0] - __uint_as_float(h.x << 16), xr[i][1] - __uint_as_float(h.x & 0xffff0000u)),
                                        pack2(xr[i][2] - __uint_as_float(h.y << 16), xr[i][3] - __uint_as_float(h.y & 0xffff0000u)));
-            const int off = (gw * 16 + (col ^ ((gw & 1) << 3))) * 16 + (c & 1) * 8;
+            const int off = (gw * 16 + (col ^ (gw << 1))) * 16 + (c & 1) * 8;
             *(uint2 *)(xb + (tb * 2 + 0) * 1024 + off) = h;
             *(uint2 *)(xb + (tb * 2 + 1) * 1024 + off) = l;
         }
     };
-    const uint32_t xrd = (uint32_t)(g * 16 + (n ^ ((g & 1) << 3))) * 16;   // this lane's operand unit
+    const uint32_t xrd = (uint32_t)(g * 16 + (n ^ (g << 1))) * 16;   // this lane's operand unit
 
     floatx4_t acc[8][4];
 #pragma unroll
@@ -176,42 +220,42 @@ __global__ __launch_bounds__(512, 1) void gemm_wx(GemmArgs a) {
         vx_lds_barrier();
     };
 
-    dma_w(0, 0);
-    load_x(0, xr);
-    store_x(0, xr);
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");   // (the W DMA of stage 0)
+    dma_w(ks0, ks0 & 1);
+    load_x(ks0, xr);
+    store_x(ks0 & 1, xr);
+    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");   // (the W DMA of the first stage)
     vx_lds_barrier();
-    for (int s = 0; s < KS; s++) step(s);
+    for (int s = ks0; s < KS; s++) step(s);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");   // (the last, unused loads)
 
-    // lane (g, n) of accumulator (j, i): token 16 i + n of the wave's 64,
-    // rows 16 j + 4 g .. +3 of its 128, into the segment that holds the row
-    // block (wave-uniform)
+    if (a.P == 1) {
 #pragma unroll
-    for (int j = 0; j < 8; j++) {
-        const int rb = rb0 + wn * 8 + j;
-        if (rb >= nb) continue;
-        int si = 0;
+        for (int j = 0; j < 8; j++)
 #pragma unroll
-        for (int q = 1; q < VX_GEMM_SEGS; q++)
-            if (q < a.out.n && rb >= a.out.s[q].rb0) si = q;
-        const GemmSeg sg = a.out.s[si];
-        const size_t col = (size_t)(rb - sg.rb0) * 16 + 4 * g;
+            for (int i = 0; i < 4; i++) gemm_store1(a, tm, tn, wm, wn, g, n, j, i, acc[j][i]);
+    } else {   // this part's sums for gemm_reduce (1 KiB runs per wave and accumulator)
+        floatx4_t *w = a.ws + ((size_t)part * a.n_t + tl) * 32 * 512 + tid;
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int tk = tok0 + wm * 64 + 16 * i + n;
-            if (tk >= a.R) continue;
-            const size_t o = (size_t)tk * sg.stride + col;
-            if (sg.bf16) {
-                const floatx4_t v = acc[j][i];
-                *(uint2 *)((uint16_t *)sg.p + o) =
-                    make_uint2(vx_f32_to_bf16(v[0]) | ((uint32_t)vx_f32_to_bf16(v[1]) << 16),
-                               vx_f32_to_bf16(v[2]) | ((uint32_t)vx_f32_to_bf16(v[3]) << 16));
-            } else {
-                *(floatx4_t *)((float *)sg.p + o) = acc[j][i];
-            }
-        }
+        for (int j = 0; j < 8; j++)
+#pragma unroll
+            for (int i = 0; i < 4; i++) w[(j * 4 + i) * 512] = acc[j][i];
     }
+}
+
+// The tiles of a split launch: the P partial sums of each value added in
+// part order (the same bits every run), then stored as the whole-tile
+// launch stores them.  grid (n_t, 32 accumulators), block 512.
+__global__ __launch_bounds__(512) void gemm_reduce(GemmArgs a) {
+    const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave & 3, wn = wave >> 2;
+    const int tl = blockIdx.x, q = blockIdx.y;
+    int tm, tn;
+    gemm_tile(a, a.tile0 + tl, tm, tn);
+    const floatx4_t *w = a.ws + ((size_t)tl * 32 + q) * 512 + tid;
+    const size_t pstride = (size_t)a.n_t * 32 * 512;   // float4s between parts
+    floatx4_t v = w[0];
+    for (int p = 1; p < a.P; p++) v += w[p * pstride];
+    gemm_store1(a, tm, tn, wm, wn, g, n, q >> 2, q & 3, v);
 }
 
 }  // namespace
@@ -236,8 +280,33 @@ bool vx_gemm_fits(int N, int K, int R, const float *x, size_t x_stride, const fl
     return vx_gemm_fits_seg(N, K, R, x, x_stride, o);
 }
 
+namespace {
+// Whole rounds of tiles (one per CU) as whole tiles; a last partial round of
+// rem tiles, when it fills at most half of the CUs, in P parts along k (at
+// least 8 k-steps each), so that it takes about one round of parts instead of
+// one round of whole tiles.
+struct GemmPlan {
+    int n_main, rem, P;
+    size_t ws_bytes;
+};
+GemmPlan gemm_plan(int N, int K, int R, int n_cu) {
+    const int n_tiles = ((R + GT - 1) / GT) * ((N / 16 + GRB - 1) / GRB);
+    GemmPlan pl = {n_tiles, 0, 1, 0};
+    const int rem = n_tiles % n_cu;
+    if (rem > 0 && 2 * rem <= n_cu) {
+        const int P = std::min(n_cu / rem, K / 32 / 8);
+        if (P >= 2) pl = {n_tiles - rem, rem, P, (size_t)rem * P * 512 * 32 * sizeof(floatx4_t)};
+    }
+    return pl;
+}
+}  // namespace
+
+size_t vx_gemm_ws_bytes(int N, int K, int R, int n_cu) {
+    return gemm_plan(N, K, R, n_cu).ws_bytes;
+}
+
 int vx_gemm_store_seg(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x, size_t x_stride, int R,
-                      const GemmOut &out) {
+                      const GemmOut &out, void *ws) {
     VX_REQUIRE(vx_gemm_fits_seg(N, K, R, x, x_stride, out),
                "gemm: need N %% 16 == 0, K %% 64 == 0, 16-byte aligned x rows within 2^31 bytes and aligned "
                "output segments (N=%d K=%d R=%d)", N, K, R);
@@ -246,23 +315,35 @@ int vx_gemm_store_seg(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const 
     a.x = x; a.x_stride = x_stride; a.out = out;
     a.n_tm = (R + GT - 1) / GT;
     a.n_tn = (N / 16 + GRB - 1) / GRB;
-    const int n_tiles = a.n_tm * a.n_tn;
-    a.per_xcd = (n_tiles + 7) / 8;
-    VX_LAUNCH(ctx, gemm_wx, dim3((unsigned)(8 * a.per_xcd)), dim3(512), a);
+    GemmPlan pl = gemm_plan(N, K, R, ctx->n_cu);
+    if (!ws) pl = {a.n_tm * a.n_tn, 0, 1, 0};
+    if (pl.n_main > 0) {
+        a.tile0 = 0; a.n_t = pl.n_main; a.P = 1; a.ws = nullptr;
+        a.per_xcd = (pl.n_main + 7) / 8;
+        VX_LAUNCH(ctx, gemm_wx, dim3((unsigned)(8 * a.per_xcd)), dim3(512), a);
+    }
+    if (pl.rem > 0) {
+        a.tile0 = pl.n_main; a.n_t = pl.rem; a.P = pl.P; a.ws = (floatx4_t *)ws; a.per_xcd = 0;
+        VX_LAUNCH(ctx, gemm_wx, dim3((unsigned)(pl.rem * pl.P)), dim3(512), a);
+        VX_LAUNCH(ctx, gemm_reduce, dim3((unsigned)pl.rem, 32), dim3(512), a);
+    }
     return 0;
 }
 
 int vx_gemm_store(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x, size_t x_stride, int R,
-                  float *y, size_t y_stride) {
+                  float *y, size_t y_stride, void *ws) {
     GemmOut o = {};
     o.n = 1;
     o.s[0] = GemmSeg{0, 0, y_stride, (void *)y};
-    return vx_gemm_store_seg(ctx, W, N, K, x, x_stride, R, o);
+    return vx_gemm_store_seg(ctx, W, N, K, x, x_stride, R, o, ws);
 }
 
 extern "C" int vx27_hip_gemm_bf16(vx27_hip_ctx *ctx, const uint16_t *W_tiled, int N, int K, const float *x,
                                   size_t x_stride, int R, float *y, size_t y_stride) {
     if (vx_ctx_enter(ctx)) return -1;
     VX_REQUIRE(W_tiled && x && y, "vx27_hip_gemm_bf16: null pointer");
-    return vx_gemm_store(ctx, W_tiled, N, K, x, x_stride, R, y, y_stride);
+    void *ws = nullptr;
+    const size_t wsb = vx_gemm_ws_bytes(N, K, R, ctx->n_cu);
+    if (wsb && vx_ctx_scratch(ctx, wsb, &ws)) return -1;
+    return vx_gemm_store(ctx, W_tiled, N, K, x, x_stride, R, y, y_stride, ws);
 }

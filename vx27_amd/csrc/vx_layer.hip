@@ -19,6 +19,8 @@
 // vx_gemv_body.h)
 #include <math.h>
 
+#include <algorithm>
+
 #include "vx_dn.h"
 #include "vx_gemv_body.h"
 #include "vx_gqa.h"
@@ -383,8 +385,10 @@ extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_
     const size_t g_b = align256((size_t)R * nv * 4), o_b = align256((size_t)R * vd * 4);
     const size_t pk_o = align256(vx_pack_bytes(vd, R));
     const size_t inner = vx_dn_prefill_scratch(&pd);
+    // (the long-prompt GEMMs' workspace, one region for both)
+    const size_t ws_b = align256(std::max(vx_gemm_ws_bytes(Nin, H, R, ctx->n_cu), vx_gemm_ws_bytes(H, vd, R, ctx->n_cu)));
     void *scr;
-    if (vx_ctx_scratch(ctx, pk_x + y_b + x_b + z_b + 2 * g_b + o_b + pk_o + inner, &scr)) return -1;
+    if (vx_ctx_scratch(ctx, pk_x + y_b + x_b + z_b + 2 * g_b + o_b + pk_o + ws_b + inner, &scr)) return -1;
     char *p = (char *)scr;
     uint16_t *xp = (uint16_t *)p; p += pk_x;
     float *y = (float *)p; p += y_b;
@@ -394,6 +398,7 @@ extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_
     float *gb = (float *)p; p += g_b;
     float *o = (float *)p; p += o_b;
     uint16_t *op = (uint16_t *)p; p += pk_o;
+    void *gws = p; p += ws_b;
     // [qkv | z | a | b] = W_in x for all B*T tokens: a long prompt of the
     // chunked form in the GEMM (W_in read once per 256 tokens, x as two bf16
     // parts, as precise as the chunked products); otherwise one pass over W_in
@@ -408,10 +413,10 @@ extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_
     seg.s[2] = GemmSeg{(C + vd) / 16, 0, (size_t)nv, ga};
     seg.s[3] = GemmSeg{(C + vd + nv) / 16, 0, (size_t)nv, gb};
     if (gemm && nv % 16 == 0 && vx_gemm_fits_seg(Nin, H, R, d->x, (size_t)H, seg)) {
-        if (vx_gemm_store_seg(ctx, d->w_in, Nin, H, d->x, (size_t)H, R, seg)) return -1;
+        if (vx_gemm_store_seg(ctx, d->w_in, Nin, H, d->x, (size_t)H, R, seg, gws)) return -1;
     } else {
         if (gemm && vx_gemm_fits(Nin, H, R, d->x, (size_t)H, y, (size_t)Nin)) {
-            if (vx_gemm_store(ctx, d->w_in, Nin, H, d->x, (size_t)H, R, y, (size_t)Nin)) return -1;
+            if (vx_gemm_store(ctx, d->w_in, Nin, H, d->x, (size_t)H, R, y, (size_t)Nin, gws)) return -1;
         } else {
             if (vx_pack(ctx, d->x, (size_t)H, R, H, xp)) return -1;
             if (vx_gemv_store(ctx, d->w_in, Nin, H, xp, R, y, (size_t)Nin)) return -1;
@@ -429,7 +434,7 @@ extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_
     pd.x = xq; pd.z = z; pd.a = ga; pd.b = gb; pd.out = o;
     if (vx_dn_prefill_into(ctx, &pd, p)) return -1;
     if (gemm && vx_gemm_fits(H, vd, R, o, (size_t)vd, d->out, (size_t)H))
-        return vx_gemm_store(ctx, d->w_out, H, vd, o, (size_t)vd, R, d->out, (size_t)H);
+        return vx_gemm_store(ctx, d->w_out, H, vd, o, (size_t)vd, R, d->out, (size_t)H, gws);
     if (vx_pack(ctx, o, (size_t)vd, R, vd, op)) return -1;
     return vx_gemv_store(ctx, d->w_out, H, vd, op, R, d->out, (size_t)H);
 }
@@ -455,8 +460,9 @@ extern "C" int vx27_hip_gqa_layer_prefill(vx27_hip_ctx *ctx, const vx27_gqa_laye
     const size_t qg_b = align256((size_t)R * Nq * 2), kv_b = align256((size_t)R * kvd * 2);
     const size_t at_b = align256((size_t)R * Ka * 4), pk_a = align256(vx_pack_bytes(Ka, R));
     const size_t inner = vx_gqa_prefill_scratch(&gp);
+    const size_t ws_b = align256(std::max(vx_gemm_ws_bytes(Nqkv, H, R, ctx->n_cu), vx_gemm_ws_bytes(H, Ka, R, ctx->n_cu)));
     void *scr;
-    if (vx_ctx_scratch(ctx, pk_x + y_b + qg_b + 2 * kv_b + at_b + pk_a + inner, &scr)) return -1;
+    if (vx_ctx_scratch(ctx, pk_x + y_b + qg_b + 2 * kv_b + at_b + pk_a + ws_b + inner, &scr)) return -1;
     char *p = (char *)scr;
     uint16_t *xp = (uint16_t *)p; p += pk_x;
     float *y = (float *)p; p += y_b;
@@ -465,6 +471,7 @@ extern "C" int vx27_hip_gqa_layer_prefill(vx27_hip_ctx *ctx, const vx27_gqa_laye
     uint16_t *vb = (uint16_t *)p; p += kv_b;
     float *att = (float *)p; p += at_b;
     uint16_t *ap = (uint16_t *)p; p += pk_a;
+    void *gws = p; p += ws_b;
     // a long prompt's projections in the GEMM (weights once per 256 tokens),
     // rounded to bf16 straight into q|gate, k and v
     const bool gemm = R >= VX_GEMM_MIN_ROWS;
@@ -474,7 +481,7 @@ extern "C" int vx27_hip_gqa_layer_prefill(vx27_hip_ctx *ctx, const vx27_gqa_laye
     seg.s[1] = GemmSeg{Nq / 16, 1, (size_t)kvd, kb};
     seg.s[2] = GemmSeg{(Nq + kvd) / 16, 1, (size_t)kvd, vb};
     if (gemm && vx_gemm_fits_seg(Nqkv, H, R, d->x, (size_t)H, seg)) {
-        if (vx_gemm_store_seg(ctx, d->w_qkv, Nqkv, H, d->x, (size_t)H, R, seg)) return -1;
+        if (vx_gemm_store_seg(ctx, d->w_qkv, Nqkv, H, d->x, (size_t)H, R, seg, gws)) return -1;
     } else {
         if (vx_pack(ctx, d->x, (size_t)H, R, H, xp)) return -1;
         if (vx_gemv_store(ctx, d->w_qkv, Nqkv, H, xp, R, y, (size_t)Nqkv)) return -1;
@@ -484,7 +491,7 @@ extern "C" int vx27_hip_gqa_layer_prefill(vx27_hip_ctx *ctx, const vx27_gqa_laye
     gp.q = qg; gp.gate = qg + hd; gp.k_new = kb; gp.v_new = vb; gp.out = att;
     if (vx_gqa_prefill_into(ctx, &gp, p)) return -1;
     if (gemm && vx_gemm_fits(H, Ka, R, att, (size_t)Ka, d->out, (size_t)H))
-        return vx_gemm_store(ctx, d->w_o, H, Ka, att, (size_t)Ka, R, d->out, (size_t)H);
+        return vx_gemm_store(ctx, d->w_o, H, Ka, att, (size_t)Ka, R, d->out, (size_t)H, gws);
     if (vx_pack(ctx, att, (size_t)Ka, R, Ka, ap)) return -1;
     return vx_gemv_store(ctx, d->w_o, H, Ka, ap, R, d->out, (size_t)H);
 }
