@@ -753,15 +753,21 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
     // Overflow past the fixed reference: redo this wave's queries with the
     // online softmax (running max per query, O and l rescaled when it moves
     // by more than 16), K and V operands read from the cache.
-    bool bad = false;
+    // (x * 0 is 0 for a finite x and NaN for an infinite or NaN one, so a sum
+    // of such products is NaN exactly when some O or l is not finite: four
+    // independent chains of fma(x, 0, acc), two VALU operations a value,
+    // where a per-value class test ran as one serial chain through the
+    // scalar unit)
+    float zc[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int rb = 0; rb < RB; rb++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-            bad = bad || !__builtin_isfinite(Ol[rb][i]);
+            zc[i] = __builtin_fmaf(Ol[rb][i], 0.f, zc[i]);
 #pragma unroll
-            for (int db = 0; db < 16; db++) bad = bad || !__builtin_isfinite(O[rb][db][i]);
+            for (int db = 0; db < 16; db++) zc[i] = __builtin_fmaf(O[rb][db][i], 0.f, zc[i]);
         }
+    const bool bad = !((zc[0] + zc[1]) + (zc[2] + zc[3]) == 0.f);
     if (__any(bad)) {
         float mrow[RB];
 #pragma unroll
@@ -844,12 +850,6 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
                       : make_uint2(0u, 0u);
     }
     vx_lds_barrier();   // every wave is done with the tile buffers
-    // the next item's query rows go into this wave's V-buffer slots while
-    // this epilogue runs (the transposition below uses only the K buffers)
-    if (item + 1 < n_items) {
-        int nqt, nh, nb;
-        if (item_of(item + 1, nqt, nh, nb)) stage_q(nqt, nh, nb);
-    }
     float *Ow = (float *)smem + wave * (16 * HDG);   // 16 rows at a time
     constexpr float L2E = 1.4426950408889634f;
 #pragma unroll
@@ -861,10 +861,18 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
             for (int db = 0; db < 16; db++) Ow[(4 * g + i) * HDG + ((db ^ g) * 16) + n] = O[rb][db][i] * il;
         }
         __builtin_amdgcn_wave_barrier();   // (one wave's LDS operations complete in order)
+        // each row's LDS read is issued one row ahead, so that it lands while
+        // the previous row's gate factors are computed
+        auto orow = [&](int qq) {
+            const int sw = (qq >> 2) & 3;
+            return *(const float4 *)&Ow[qq * HDG + (((lane >> 2) ^ sw) * 16) + 4 * (lane & 3)];
+        };
+        float4 on = orow(0);
 #pragma unroll
         for (int qq = 0; qq < 16; qq++) {
-            const int q = rb * 16 + qq, t = r0 + q, sw = (qq >> 2) & 3;
-            const float4 o = *(const float4 *)&Ow[qq * HDG + (((lane >> 2) ^ sw) * 16) + 4 * (lane & 3)];
+            const int q = rb * 16 + qq, t = r0 + q;
+            const float4 o = on;
+            if (qq + 1 < 16) on = orow(qq + 1);
             const float g0 = __uint_as_float(gv[q].x << 16), g1 = __uint_as_float(gv[q].x & 0xffff0000u);
             const float g2 = __uint_as_float(gv[q].y << 16), g3 = __uint_as_float(gv[q].y & 0xffff0000u);
             float4 r = o;
@@ -881,6 +889,14 @@ __global__ __launch_bounds__(PP_NW * 64) void gqp_attn_pp(AttnArgs a) {
             }
         }
         __builtin_amdgcn_wave_barrier();   // this pass's reads before the next pass's writes
+        // the next item's query rows go into this wave's V-buffer slots while
+        // the second pass runs (the transposition uses only the K buffers).
+        // Not before the first pass: its first gate value would then wait
+        // for these loads too, vmcnt counting in issue order.
+        if (rb == 0 && item + 1 < n_items) {
+            int nqt, nh, nb;
+            if (item_of(item + 1, nqt, nh, nb)) stage_q(nqt, nh, nb);
+        }
     }
     }   // items
 }
