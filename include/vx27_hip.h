@@ -330,12 +330,13 @@ int vx27_hip_gemv_bf16(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const
 
 /* The same product for many tokens at once (a prompt's projections): y[r*y_stride + n] =
  * sum_k W[n][k] * x[r*x_stride + k] for R >= 1 rows, W tiled (vx27_hip_pack_weights_bf16,
- * N % 16 == 0, K % 64 == 0), x and y fp32 with 16-byte aligned rows (strides % 4 == 0) and
- * R*x_stride*4 < 2^31.  A bf16 MFMA GEMM (tiles of 256 tokens x 256 rows, W read once per
- * 256 tokens); each x enters as two bf16 parts hi + lo (16 significand bits: relative error
- * about 2^-17 per product), fp32 accumulation.  No counterpart in the reference, whose
- * batched matvec (vx27_pmat.c:212-227) serves at most 8 tokens; the layer prefill entry
- * points use it from 128 tokens on. */
+ * N % 16 == 0, K % 64 == 0), x and y fp32 with 16-byte aligned rows (strides % 4 == 0).
+ * A bf16 MFMA GEMM (tiles of 256 tokens x 256 rows, W read once per 256 tokens); each x
+ * enters as two bf16 parts hi + lo (16 significand bits: relative error about 2^-17 per
+ * product), fp32 accumulation.  Context scratch holds x packed for the MFMAs (R*K*4 bytes,
+ * R rounded up to 256).  No counterpart in the reference, whose batched matvec
+ * (vx27_pmat.c:212-227) serves at most 8 tokens; the layer prefill entry points use it from
+ * 256 tokens on. */
 int vx27_hip_gemm_bf16(vx27_hip_ctx *ctx, const uint16_t *W_tiled, int N, int K, const float *x,
                        size_t x_stride, int R, float *y, size_t y_stride);
 

@@ -18,16 +18,19 @@
 // copied a loop-carried share of them through VGPRs every k-step; 64 x 128
 // rather than 128 x 64 since the token operand comes twice, hi and lo, so
 // this shape reads the least from LDS), the W tile as operand A (lane
-// (g, m): row m,
-// k 8g..8g+7: exactly the tiled layout) and the token tile as operand B
-// (lane (g, n): token n, k 8g..8g+7), so a lane's four outputs are four
-// consecutive rows of one token (one 16-byte store).  Per 32-wide k-step a
-// stage in LDS holds the 16 W tiles (16 KiB, direct-to-LDS loads of their
-// 1 KiB runs) and the 16 token tiles as hi and lo parts (32 KiB, split from
-// the fp32 rows on the way in); two stages alternate, one barrier per
-// k-step.  Per k-step and wave: 16 operand reads of 1 KiB from LDS, 64
-// MFMAs (two waves a SIMD: about 2048 cycles of the SIMD's matrix core), 4
-// row loads of 16 bytes a lane and 2 tile DMAs, all for the next k-step.
+// (g, m): row m, k 8g..8g+7: exactly the tiled layout) and the token tile
+// as operand B (lane (g, n): token n, k 8g..8g+7), so a lane's four outputs
+// are four consecutive rows of one token (one 16-byte store).  Per 32-wide
+// k-step a stage in LDS holds the 16 W tiles (16 KiB) and the 16 token
+// tiles as hi and lo parts (32 KiB), both brought in by direct-to-LDS loads
+// of 1 KiB runs; three stages rotate (the loads run two k-steps ahead), one
+// barrier per k-step.  The token tiles come as their LDS image, written
+// once per call by gemm_pack: the fp32 rows read and split into hi and lo
+// once, where splitting them on the way into LDS cost every row tile of a
+// token tile the loads, conversions and LDS stores again (9-10% of the
+// kernel).  Per k-step and wave: 16 operand reads of 1 KiB from LDS, 64
+// MFMAs (two waves a SIMD: about 2048 cycles of the SIMD's matrix core) and
+// 6 DMAs of 1 KiB (2 W tiles, 4 KiB of the token image).
 //
 // Tiles are ordered per XCD (workgroup i runs on XCD i % 8): XCD x takes a
 // contiguous range of tile indices, numbered in groups of 4 token tiles x
@@ -50,6 +53,12 @@ constexpr int G_W = 0;                   // stage: W tiles [16][1 KiB]
 constexpr int G_X = GRB * 1024;          // stage: token tiles [16 token blocks][hi, lo][1 KiB]
 constexpr int G_STAGE = G_X + 32 * 1024; // 48 KiB
 constexpr int G_GM = 4;                  // token tiles per group of the tile order
+constexpr int G_XIMG = 32 * 1024;        // packed token tile image per k-step
+#ifndef GEMM_NST
+#define GEMM_NST 3                       // LDS stages (the loads run GEMM_NST - 1 k-steps ahead)
+#endif
+constexpr int G_NST = GEMM_NST;
+constexpr int G_DMA = 6;                 // DMAs per wave and k-step (2 W tiles, 4 KiB of tokens)
 
 // two floats as packed bf16, round to nearest even (v_cvt_pk_bf16_f32)
 __device__ __forceinline__ uint32_t pack2(float x, float y) {
@@ -67,8 +76,7 @@ __device__ __forceinline__ bf16x8_t as_bf16x8(uint4 v) {
 struct GemmArgs {
     const uint16_t *W;    // tiled [K/(32 kg)][N/16][kg][64][8]
     int N, K, R, kg;
-    const float *x;       // [R] rows of K, row stride x_stride (16-byte aligned rows)
-    size_t x_stride;
+    const char *xp;       // packed token tiles [n_tm][K/32][32 KiB] (gemm_pack)
     GemmOut out;          // where the rows of the product go (fp32 or bf16 segments)
     int n_tm, n_tn;
     // this launch: tiles tile0 .. tile0 + n_t - 1 of the tile order; P = 1:
@@ -107,8 +115,42 @@ __device__ __forceinline__ void gemm_store1(const GemmArgs &a, int tm, int tn, i
         *(floatx4_t *)((float *)sg.p + o) = v;
 }
 
+// Token tile layout in LDS, per k-step: 16 token blocks x (hi, lo) x 1 KiB;
+// lane (g, n)'s 16 bytes (token n of the block, k 8g..8g+7 of the step) sit
+// at 16-byte unit g * 16 + (n ^ 2g).  The operand reads (8 lanes a cycle,
+// one g) stay one aligned 128-byte block each, and the XOR spreads the
+// units that one token column touches over the LDS's 32 banks.
+// gemm_pack writes this image for every (token tile, k-step) of x (tokens
+// past R as zeros), so that gemm_wx copies it into LDS verbatim by
+// direct-to-LDS loads.  grid (K/32, token tiles), block 256.
+__global__ __launch_bounds__(256) void gemm_pack(const float *x, size_t x_stride, int R, char *xp) {
+    const int s = blockIdx.x, tm = blockIdx.y;
+    char *img = xp + ((size_t)tm * gridDim.x + s) * G_XIMG;
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+        const int u = threadIdx.x + 256 * q, tb = u >> 6, g = (u >> 4) & 3, n = u & 15;
+        const int t = tm * GT + tb * 16 + n;
+        float v[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+        if (t < R) {
+            const float4 *p = (const float4 *)(x + (size_t)t * x_stride + 32 * s + 8 * g);
+            const float4 v0 = p[0], v1 = p[1];
+            v[0] = v0.x; v[1] = v0.y; v[2] = v0.z; v[3] = v0.w;
+            v[4] = v1.x; v[5] = v1.y; v[6] = v1.z; v[7] = v1.w;
+        }
+        uint32_t h[4], l[4];
+#pragma unroll
+        for (int e = 0; e < 4; e++) {
+            h[e] = pack2(v[2 * e], v[2 * e + 1]);   // hi = bf16(x), then lo = bf16(x - hi)
+            l[e] = pack2(v[2 * e] - __uint_as_float(h[e] << 16), v[2 * e + 1] - __uint_as_float(h[e] & 0xffff0000u));
+        }
+        const int off = (g * 16 + (n ^ (g << 1))) * 16;
+        *(uint4 *)(img + (tb * 2 + 0) * 1024 + off) = make_uint4(h[0], h[1], h[2], h[3]);
+        *(uint4 *)(img + (tb * 2 + 1) * 1024 + off) = make_uint4(l[0], l[1], l[2], l[3]);
+    }
+}
+
 __global__ __launch_bounds__(512, 1) void gemm_wx(GemmArgs a) {
-    __shared__ __attribute__((aligned(16))) char smem[2 * G_STAGE];
+    __shared__ __attribute__((aligned(16))) char smem[G_NST * G_STAGE];
     const int tid = threadIdx.x, lane = tid & 63, g = lane >> 4, n = lane & 15;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6), wm = wave & 3, wn = wave >> 2;
 
@@ -138,47 +180,12 @@ __global__ __launch_bounds__(512, 1) void gemm_wx(GemmArgs a) {
             vx_dma16(Wb + vx_tile_off(s, rb, nb, a.kg) * 2, (uint32_t)lane * 16, base + jj * 1024);
         }
     };
-    // token rows: load i of this wave covers tokens 32 wave + 8 i + lane / 8,
-    // floats 4 (lane % 8) .. +3 of the k-step, through a buffer resource: the
-    // lane's byte offset plus a scalar one per k-step (tokens past R read row
-    // R - 1; the host keeps x within 2^31 bytes)
-    const __amdgpu_buffer_rsrc_t xres = __builtin_amdgcn_make_buffer_rsrc(
-        (void *)a.x, (short)0, (int)((size_t)a.R * a.x_stride * 4), 0x00020000);
-    const int tok_l = tok0 + wave * 32 + (lane >> 3);
-    uint32_t xoff[4];
+    // this wave's 4 KiB of the packed token image of k-step s
+    const char *xpt = a.xp + (size_t)tm * KSall * G_XIMG + wave * 4096;
+    auto dma_x = [&](int s, int st) {
+        const uint32_t base = vx_lds_addr(smem) + st * G_STAGE + G_X + wave * 4096;
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-        xoff[i] = (uint32_t)((size_t)min(tok_l + i * 8, a.R - 1) * a.x_stride * 4) + 16u * (uint32_t)(lane & 7);
-    auto load_x = [&](int s, floatx4_t (&xr)[4]) {
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const uint4 v = __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(xres, (int)xoff[i], 128 * s, 0));
-            xr[i] = (floatx4_t){__uint_as_float(v.x), __uint_as_float(v.y), __uint_as_float(v.z), __uint_as_float(v.w)};
-        }
-    };
-    // Token tile layout: lane (g, n)'s 16 bytes (token n, k 8g..8g+7) sit at
-    // 16-byte unit g * 16 + (n ^ 2g).  The LDS serves 128 bytes (32 banks) a
-    // cycle: a store below writes 8 bytes a lane, 16 lanes a cycle (2 columns
-    // x 4 values of g x 2 halves), whose units n ^ 2g then cover all 8
-    // 16-byte bank groups once (without the XOR all 16 lanes fell on the
-    // same 128 bytes: four ways, the LDS's largest cost here); the operand
-    // reads (8 lanes a cycle, one g) stay one aligned 128-byte block each.
-    // Token t' = 32 wave + 8 i + lane / 8 is column t' % 16 of token block
-    // t' / 16; its floats 4c..4c+3 (c = lane % 8) are elements 4 (c % 2) ..
-    // of lane (c / 2, t' % 16).
-    auto store_x = [&](int st, const floatx4_t (&xr)[4]) {
-        char *xb = smem + st * G_STAGE + G_X;
-        const int c = lane & 7, gw = c >> 1;
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-            const int tt = wave * 32 + i * 8 + (lane >> 3), tb = tt >> 4, col = tt & 15;
-            const uint2 h = make_uint2(pack2(xr[i][0], xr[i][1]), pack2(xr[i][2], xr[i][3]));
-            const uint2 l = make_uint2(pack2(xr[i][0] - __uint_as_float(h.x << 16), xr[i][1] - __uint_as_float(h.x & 0xffff0000u)),
-                                       pack2(xr[i][2] - __uint_as_float(h.y << 16), xr[i][3] - __uint_as_float(h.y & 0xffff0000u)));
-            const int off = (gw * 16 + (col ^ (gw << 1))) * 16 + (c & 1) * 8;
-            *(uint2 *)(xb + (tb * 2 + 0) * 1024 + off) = h;
-            *(uint2 *)(xb + (tb * 2 + 1) * 1024 + off) = l;
-        }
+        for (int q = 0; q < 4; q++) vx_dma16(xpt + (size_t)s * G_XIMG + q * 1024, (uint32_t)lane * 16, base + q * 1024);
     };
     const uint32_t xrd = (uint32_t)(g * 16 + (n ^ (g << 1))) * 16;   // this lane's operand unit
 
@@ -188,15 +195,15 @@ __global__ __launch_bounds__(512, 1) void gemm_wx(GemmArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; i++) acc[j][i] = (floatx4_t){0.f, 0.f, 0.f, 0.f};
 
-    // k-step s: the W tiles and the rows of s + 1 are requested first
+    // k-step s (in stage s % G_NST): the W tiles and token image of
+    // s + G_NST - 1 are requested first into the stage that step s - 1 read
     // (clamped at the end: the extra loads land in a stage nobody reads
-    // again), then the MFMAs on stage s, then the rows split into the other
-    // stage.  No branch in the step, so the waits count only what they need.
-    floatx4_t xr[4];
-    auto step = [&](int s) {
-        const int cur = s & 1;
-        dma_w(min(s + 1, KS - 1), cur ^ 1);
-        load_x(min(s + 1, KS - 1), xr);
+    // again), then the MFMAs on stage s.  No branch in the step, so the
+    // waits count only what they need.
+    auto step = [&](int s, int cur) {
+        const int ld = cur == 0 ? G_NST - 1 : cur - 1;
+        dma_w(min(s + G_NST - 1, KS - 1), ld);
+        dma_x(min(s + G_NST - 1, KS - 1), ld);
         __builtin_amdgcn_sched_barrier(0);
         const char *sb = smem + cur * G_STAGE;
         bf16x8_t aw[8];
@@ -214,18 +221,20 @@ __global__ __launch_bounds__(512, 1) void gemm_wx(GemmArgs a) {
             }
         }
         __builtin_amdgcn_sched_barrier(0);
-        store_x(cur ^ 1, xr);
-        // this wave's W DMA has landed, then every wave's stage is complete
-        __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");
+        // this wave's DMAs of step s + 1 have landed (only the ones just
+        // issued may be in flight), then every wave's stage is complete
+        __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(G_DMA * (G_NST - 2)) : "memory");
         vx_lds_barrier();
     };
 
-    dma_w(ks0, ks0 & 1);
-    load_x(ks0, xr);
-    store_x(ks0 & 1, xr);
-    __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");   // (the W DMA of the first stage)
+#pragma unroll
+    for (int q = 0; q < G_NST - 1; q++) {
+        dma_w(min(ks0 + q, KS - 1), (ks0 + q) % G_NST);
+        dma_x(min(ks0 + q, KS - 1), (ks0 + q) % G_NST);
+    }
+    __asm__ volatile("s_waitcnt vmcnt(%0)" ::"n"(G_DMA * (G_NST - 2)) : "memory");   // (the first stage)
     vx_lds_barrier();
-    for (int s = ks0; s < KS; s++) step(s);
+    for (int s = ks0; s < KS; s++) step(s, s % G_NST);
     __asm__ volatile("s_waitcnt vmcnt(0)" ::: "memory");   // (the last, unused loads)
 
     if (a.P == 1) {
@@ -261,8 +270,7 @@ __global__ __launch_bounds__(512) void gemm_reduce(GemmArgs a) {
 }  // namespace
 
 bool vx_gemm_fits_seg(int N, int K, int R, const float *x, size_t x_stride, const GemmOut &out) {
-    if (!(N > 0 && N % 16 == 0 && K > 0 && K % 64 == 0 && R >= 1 && x_stride % 4 == 0 && ((uintptr_t)x & 15) == 0 &&
-          (size_t)R * x_stride * 4 < ((size_t)1 << 31)))
+    if (!(N > 0 && N % 16 == 0 && K > 0 && K % 64 == 0 && R >= 1 && x_stride % 4 == 0 && ((uintptr_t)x & 15) == 0))
         return false;
     if (out.n < 1 || out.n > VX_GEMM_SEGS || out.s[0].rb0 != 0) return false;
     for (int q = 0; q < out.n; q++) {
@@ -287,7 +295,7 @@ namespace {
 // one round of whole tiles.
 struct GemmPlan {
     int n_main, rem, P;
-    size_t ws_bytes;
+    size_t ws_bytes;   // the split's partial sums (a multiple of 256 bytes), then the packed tokens
 };
 GemmPlan gemm_plan(int N, int K, int R, int n_cu) {
     const int n_tiles = ((R + GT - 1) / GT) * ((N / 16 + GRB - 1) / GRB);
@@ -299,24 +307,30 @@ GemmPlan gemm_plan(int N, int K, int R, int n_cu) {
     }
     return pl;
 }
+size_t gemm_pack_bytes(int K, int R) {
+    return (size_t)((R + GT - 1) / GT) * (K / 32) * G_XIMG;
+}
 }  // namespace
 
 size_t vx_gemm_ws_bytes(int N, int K, int R, int n_cu) {
-    return gemm_plan(N, K, R, n_cu).ws_bytes;
+    return gemm_plan(N, K, R, n_cu).ws_bytes + gemm_pack_bytes(K, R);
 }
 
 int vx_gemm_store_seg(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x, size_t x_stride, int R,
                       const GemmOut &out, void *ws) {
     VX_REQUIRE(vx_gemm_fits_seg(N, K, R, x, x_stride, out),
-               "gemm: need N %% 16 == 0, K %% 64 == 0, 16-byte aligned x rows within 2^31 bytes and aligned "
-               "output segments (N=%d K=%d R=%d)", N, K, R);
+               "gemm: need N %% 16 == 0, K %% 64 == 0, 16-byte aligned x rows and aligned output segments "
+               "(N=%d K=%d R=%d)", N, K, R);
+    VX_REQUIRE(ws != nullptr, "gemm: needs its workspace (vx_gemm_ws_bytes)");
     GemmArgs a;
     a.W = W; a.N = N; a.K = K; a.R = R; a.kg = vx_gemv_kg(K);
-    a.x = x; a.x_stride = x_stride; a.out = out;
+    a.out = out;
     a.n_tm = (R + GT - 1) / GT;
     a.n_tn = (N / 16 + GRB - 1) / GRB;
-    GemmPlan pl = gemm_plan(N, K, R, ctx->n_cu);
-    if (!ws) pl = {a.n_tm * a.n_tn, 0, 1, 0};
+    const GemmPlan pl = gemm_plan(N, K, R, ctx->n_cu);
+    char *xp = (char *)ws + pl.ws_bytes;
+    a.xp = xp;
+    VX_LAUNCH(ctx, gemm_pack, dim3((unsigned)(K / 32), (unsigned)a.n_tm), dim3(256), x, x_stride, R, xp);
     if (pl.n_main > 0) {
         a.tile0 = 0; a.n_t = pl.n_main; a.P = 1; a.ws = nullptr;
         a.per_xcd = (pl.n_main + 7) / 8;

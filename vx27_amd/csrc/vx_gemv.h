@@ -39,11 +39,11 @@ int vx_gemv_store(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const uint
 
 // The projection of R tokens at once (vx_gemm.hip): y[r][n] = sum over k of
 // W[n][k] x_r[k] for tiled W, fp32 x rows (x as two bf16 parts; K % 64 == 0,
-// 16-byte aligned rows, R x_stride 4 < 2^31).
-// ws: vx_gemm_ws_bytes of device scratch for the split of the last round of
-// tiles along k (NULL: whole tiles only)
+// 16-byte aligned rows).
+// ws: vx_gemm_ws_bytes of device scratch (the tokens packed for the MFMAs,
+// and the partial sums of a last round of tiles split along k)
 int vx_gemm_store(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x, size_t x_stride, int R,
-                  float *y, size_t y_stride, void *ws = nullptr);
+                  float *y, size_t y_stride, void *ws);
 size_t vx_gemm_ws_bytes(int N, int K, int R, int n_cu);
 // whether vx_gemm_store takes this shape (else the GEMV passes)
 bool vx_gemm_fits(int N, int K, int R, const float *x, size_t x_stride, const float *y, size_t y_stride);
@@ -61,7 +61,7 @@ struct GemmOut {
     GemmSeg s[VX_GEMM_SEGS];
 };
 int vx_gemm_store_seg(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x, size_t x_stride, int R,
-                      const GemmOut &out, void *ws = nullptr);
+                      const GemmOut &out, void *ws);
 bool vx_gemm_fits_seg(int N, int K, int R, const float *x, size_t x_stride, const GemmOut &out);
 constexpr int VX_GEMM_MIN_ROWS = 256;   // layer prefills use the GEMM from this many tokens (one token tile)
 

@@ -385,8 +385,16 @@ extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_
     const size_t g_b = align256((size_t)R * nv * 4), o_b = align256((size_t)R * vd * 4);
     const size_t pk_o = align256(vx_pack_bytes(vd, R));
     const size_t inner = vx_dn_prefill_scratch(&pd);
+    // [qkv | z | a | b] = W_in x for all B*T tokens: a long prompt of the
+    // chunked form in the GEMM (W_in read once per 256 tokens, x as two bf16
+    // parts, as precise as the chunked products); otherwise one pass over W_in
+    // per 65 tokens with each row summed in the same order as in a decode step
+    // (the exact form is bit-identical to T decode calls)
+    const bool exact = (d->flags & VX27_DN_EXACT) || d->S_ckpt || d->conv_ckpt;
+    const bool gemm = !exact && R >= VX_GEMM_MIN_ROWS;
     // (the long-prompt GEMMs' workspace, one region for both)
-    const size_t ws_b = align256(std::max(vx_gemm_ws_bytes(Nin, H, R, ctx->n_cu), vx_gemm_ws_bytes(H, vd, R, ctx->n_cu)));
+    const size_t ws_b =
+        gemm ? align256(std::max(vx_gemm_ws_bytes(Nin, H, R, ctx->n_cu), vx_gemm_ws_bytes(H, vd, R, ctx->n_cu))) : 0;
     void *scr;
     if (vx_ctx_scratch(ctx, pk_x + y_b + x_b + z_b + 2 * g_b + o_b + pk_o + ws_b + inner, &scr)) return -1;
     char *p = (char *)scr;
@@ -399,13 +407,6 @@ extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_
     float *o = (float *)p; p += o_b;
     uint16_t *op = (uint16_t *)p; p += pk_o;
     void *gws = p; p += ws_b;
-    // [qkv | z | a | b] = W_in x for all B*T tokens: a long prompt of the
-    // chunked form in the GEMM (W_in read once per 256 tokens, x as two bf16
-    // parts, as precise as the chunked products); otherwise one pass over W_in
-    // per 65 tokens with each row summed in the same order as in a decode step
-    // (the exact form is bit-identical to T decode calls)
-    const bool exact = (d->flags & VX27_DN_EXACT) || d->S_ckpt || d->conv_ckpt;
-    const bool gemm = !exact && R >= VX_GEMM_MIN_ROWS;
     GemmOut seg = {};   // (the GEMM writes qkv, z, a and b straight into their buffers)
     seg.n = 4;
     seg.s[0] = GemmSeg{0, 0, (size_t)C, xq};
@@ -460,7 +461,11 @@ extern "C" int vx27_hip_gqa_layer_prefill(vx27_hip_ctx *ctx, const vx27_gqa_laye
     const size_t qg_b = align256((size_t)R * Nq * 2), kv_b = align256((size_t)R * kvd * 2);
     const size_t at_b = align256((size_t)R * Ka * 4), pk_a = align256(vx_pack_bytes(Ka, R));
     const size_t inner = vx_gqa_prefill_scratch(&gp);
-    const size_t ws_b = align256(std::max(vx_gemm_ws_bytes(Nqkv, H, R, ctx->n_cu), vx_gemm_ws_bytes(H, Ka, R, ctx->n_cu)));
+    // a long prompt's projections in the GEMM (weights once per 256 tokens),
+    // rounded to bf16 straight into q|gate, k and v
+    const bool gemm = R >= VX_GEMM_MIN_ROWS;
+    const size_t ws_b =
+        gemm ? align256(std::max(vx_gemm_ws_bytes(Nqkv, H, R, ctx->n_cu), vx_gemm_ws_bytes(H, Ka, R, ctx->n_cu))) : 0;
     void *scr;
     if (vx_ctx_scratch(ctx, pk_x + y_b + qg_b + 2 * kv_b + at_b + pk_a + ws_b + inner, &scr)) return -1;
     char *p = (char *)scr;
@@ -472,9 +477,6 @@ extern "C" int vx27_hip_gqa_layer_prefill(vx27_hip_ctx *ctx, const vx27_gqa_laye
     float *att = (float *)p; p += at_b;
     uint16_t *ap = (uint16_t *)p; p += pk_a;
     void *gws = p; p += ws_b;
-    // a long prompt's projections in the GEMM (weights once per 256 tokens),
-    // rounded to bf16 straight into q|gate, k and v
-    const bool gemm = R >= VX_GEMM_MIN_ROWS;
     GemmOut seg = {};
     seg.n = 3;
     seg.s[0] = GemmSeg{0, 1, (size_t)Nq, qg};
