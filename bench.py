@@ -708,14 +708,14 @@ def bench_layer_prefill(ctx, T=4096, iters=5):
     def run_dn():
         L.check(L.lib().vx27_hip_dn_layer_prefill(ctx.h, C.byref(desc)), "dn_layer_prefill")
     run_dn()
-    kern = ("gemm_wx", "gemm_reduce", "pack_x", "gemv_wk_store") + DNP_KERNELS
+    kern = ("gemm_pack", "gemm_wx", "gemm_reduce", "pack_x", "gemv_wk_store") + DNP_KERNELS
     wall_us, per = _time_calls(ctx, run_dn, kern, iters)
     per = {k: round(v, 1) for k, v in per.items() if v > 0}
     proj_flops = 2.0 * T * (Nin * H + H * vd)
     res["dn"] = {"workload": f"DeltaNet layer prefill B=1 T={T} nqk=16 nv=48 hidden=5120 (projections + "
                              f"chunked core)", "us_per_call": wall_us, "kernel_us": sum(per.values()),
                  "kernels_us": per, "tokens_per_s": T / (sum(per.values()) / 1e6),
-                 "projection_tflops": proj_flops / ((per.get("gemm_wx", 0) + per.get("gemm_reduce", 0)) * 1e-6) / 1e12
+                 "projection_tflops": proj_flops / ((per.get("gemm_pack", 0) + per.get("gemm_wx", 0) + per.get("gemm_reduce", 0)) * 1e-6) / 1e12
                  if per.get("gemm_wx") else None}
     for b in list(bufs.values()) + [w_in, w_out]:
         b.free()
@@ -731,14 +731,14 @@ def bench_layer_prefill(ctx, T=4096, iters=5):
     def run_gqa():
         L.check(L.lib().vx27_hip_gqa_layer_prefill(ctx.h, C.byref(g)), "gqa_layer_prefill")
     run_gqa()
-    kern = ("gemm_wx", "gemm_reduce", "pack_x", "gemv_wk_store", "qkv_to_bf16", "gqp_kv", "gqp_attn")
+    kern = ("gemm_pack", "gemm_wx", "gemm_reduce", "pack_x", "gemv_wk_store", "qkv_to_bf16", "gqp_kv", "gqp_attn")
     wall_us, per = _time_calls(ctx, run_gqa, kern, iters)
     per = {k: round(v, 1) for k, v in per.items() if v > 0}
     proj_flops = 2.0 * T * (Nqkv * H + H * Ka)
     res["gqa"] = {"workload": f"gated GQA layer prefill B=1 T={T} 24Q/4KV hd 256 hidden=5120 (projections + "
                               f"causal attention)", "us_per_call": wall_us, "kernel_us": sum(per.values()),
                   "kernels_us": per, "tokens_per_s": T / (sum(per.values()) / 1e6),
-                  "projection_tflops": proj_flops / ((per.get("gemm_wx", 0) + per.get("gemm_reduce", 0)) * 1e-6) / 1e12
+                  "projection_tflops": proj_flops / ((per.get("gemm_pack", 0) + per.get("gemm_wx", 0) + per.get("gemm_reduce", 0)) * 1e-6) / 1e12
                   if per.get("gemm_wx") else None}
     for b in (w_qkv, w_o, qn, kn, kc, vc, x, out):
         b.free()
