@@ -594,6 +594,7 @@ def _time_calls(ctx, fn, kernels, iters):
 
 
 DNP_KERNELS = ("dnp_glue_in", "dnp_conv_state", "dnp_prept", "dnp_scant", "dnp_prep3", "dnp_scan3", "dnp_prep", "dnp_scan",
+               "dnp_out_gate_packed",
                "dnp_out_gate")
 
 

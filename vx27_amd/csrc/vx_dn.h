@@ -148,4 +148,8 @@ bool vx_dn_single_step(const DnArgs &a);
 // The DeltaNet prefill on caller-provided scratch (vx_dn_prefill.hip), for
 // entry points that hold other scratch of their own at the same time.
 size_t vx_dn_prefill_scratch(const vx27_dn_prefill_desc *d);
-int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *scr);
+// out_packed: the gated output written instead as the long-prompt GEMM's
+// packed tokens (vx_gemm_pack_unit, K = nv 128) for a projection that takes
+// it next; the chunked form with VX27_DN_OUT_GATE only (d->out then holds
+// the ungated output).
+int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *scr, char *out_packed = nullptr);

@@ -32,6 +32,7 @@
 #include <algorithm>
 
 #include "vx_dn.h"
+#include "vx_gemv.h"
 #include "vx_lds.h"
 
 namespace {
@@ -2354,6 +2355,22 @@ __global__ __launch_bounds__(256) void dnp_conv_state(int B, int T, int C, const
 // 8 rows (o and z) issued before any is used; the sum of squares in double
 // over the half-wave.  out, z and norm_w 16-byte aligned.
 // grid ceil(rows / 32), block 256.
+// One row's gated norm: rmsn_std(o) * norm_w * silu(z) for the 4 values a
+// lane holds (the row's 128 values on the 32 lanes of a wave half).
+__device__ __forceinline__ float4 out_gate_row(float4 o, float4 zz, float4 w) {
+    double ss = (((double)o.x * (double)o.x + (double)o.y * (double)o.y) + (double)o.z * (double)o.z) +
+                (double)o.w * (double)o.w;
+#pragma unroll
+    for (int off = 1; off < 32; off <<= 1) ss += __shfl_xor(ss, off, 64);
+    const float is = 1.0f / sqrtf((float)(ss / HD) + 1e-6f);
+    float4 y;
+    y.x = ((o.x * is) * w.x) * silu_f(zz.x);
+    y.y = ((o.y * is) * w.y) * silu_f(zz.y);
+    y.z = ((o.z * is) * w.z) * silu_f(zz.z);
+    y.w = ((o.w * is) * w.w) * silu_f(zz.w);
+    return y;
+}
+
 __global__ __launch_bounds__(256) void dnp_out_gate(int rows, const float *z, const float *norm_w, float *out) {
     const int lane = threadIdx.x & 63, hl = lane & 31, hr = lane >> 5;
     const int r0 = (blockIdx.x * 4 + (threadIdx.x >> 6)) * 8;
@@ -2369,20 +2386,59 @@ __global__ __launch_bounds__(256) void dnp_out_gate(int rows, const float *z, co
     __builtin_amdgcn_sched_barrier(0);   // every load issued before the first wait
 #pragma unroll
     for (int i = 0; i < 4; i++) {
-        double ss = (((double)o[i].x * (double)o[i].x + (double)o[i].y * (double)o[i].y) +
-                     (double)o[i].z * (double)o[i].z) + (double)o[i].w * (double)o[i].w;
-#pragma unroll
-        for (int off = 1; off < 32; off <<= 1) ss += __shfl_xor(ss, off, 64);
-        const float is = 1.0f / sqrtf((float)(ss / HD) + 1e-6f);
-        float4 y;
-        y.x = ((o[i].x * is) * w.x) * silu_f(zz[i].x);
-        y.y = ((o[i].y * is) * w.y) * silu_f(zz[i].y);
-        y.z = ((o[i].z * is) * w.z) * silu_f(zz[i].z);
-        y.w = ((o[i].w * is) * w.w) * silu_f(zz[i].w);
+        const float4 y = out_gate_row(o[i], zz[i], w);
         // (unconditional: rows past the end store the last row's own result
         // again; a store under the row test would take the loads into its
         // branch, with a wait for all of them)
         *(float4 *)(out + (size_t)min(r0 + 2 * i + hr, rows - 1) * HD + 4 * hl) = y;
+    }
+}
+
+// The same gated norm written as the packed tokens of the long-prompt GEMM
+// that takes it next (out_proj: K = nv 128, vx_gemm_pack_unit): hi =
+// bf16(y), lo = bf16(y - hi), the split gemm_pack would make of the fp32
+// rows, without writing and reading them back.  grid (token blocks of 16,
+// nv), block 256: wave w takes tokens 4w .. 4w+3 of the block, for value
+// head blockIdx.y.  The workgroup's share of the images (4 k-steps x hi,
+// lo x one 1 KiB block) is assembled in LDS and stored as whole blocks, 16
+// bytes a lane.  R: tokens (B T); rows t nv + h of o and z.
+__global__ __launch_bounds__(256) void dnp_out_gate_packed(int R, int nv, const float *o, const float *z,
+                                                           const float *norm_w, char *xp) {
+    __shared__ __attribute__((aligned(16))) char img[8 * 1024];   // [k-step s of the head][hi, lo][1 KiB]
+    const int tid = threadIdx.x, lane = tid & 63, hl = lane & 31, hr = lane >> 5;
+    const int h = blockIdx.y, tb0 = blockIdx.x * 16, t0 = tb0 + (tid >> 6) * 4;
+    float4 ov[2], zv[2];
+#pragma unroll
+    for (int i = 0; i < 2; i++) {   // tokens past the end re-do the last token
+        const size_t r = (size_t)min(t0 + 2 * i + hr, R - 1) * nv + h;
+        ov[i] = *(const float4 *)(o + r * HD + 4 * hl);
+        zv[i] = *(const float4 *)(z + r * HD + 4 * hl);
+    }
+    const float4 w = *(const float4 *)(norm_w + 4 * hl);
+    __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+    for (int i = 0; i < 2; i++) {
+        const float4 y = out_gate_row(ov[i], zv[i], w);
+        const uint32_t h0 = pack2(y.x, y.y), h1 = pack2(y.z, y.w);
+        const uint32_t l0 = pack2(y.x - __uint_as_float(h0 << 16), y.y - __uint_as_float(h0 & 0xffff0000u));
+        const uint32_t l1 = pack2(y.z - __uint_as_float(h1 << 16), y.w - __uint_as_float(h1 & 0xffff0000u));
+        // dims 4 hl .. of token n: k-step hl / 8 of the head, unit g = (hl / 2) % 4,
+        // half hl % 2 (lanes hl, hl ^ 1 fill one unit)
+        const int n = (t0 + 2 * i + hr) & 15, g = (hl >> 1) & 3;
+        char *u = img + (hl >> 3) * 2048 + (g * 16 + (n ^ (g << 1))) * 16 + (hl & 1) * 8;
+        *(uint2 *)u = make_uint2(h0, h1);
+        *(uint2 *)(u + 1024) = make_uint2(l0, l1);
+    }
+    __syncthreads();
+    // block (k-step sl, part) to its place: image (token tile, 4 h + sl),
+    // block (token block within the tile) 2 + part
+    const int K = nv * HD;
+    const size_t base = vx_gemm_pack_unit(tb0, 4 * h * 32, K);   // hi unit 0 of (k-step 4h, token block tb0 / 16)
+#pragma unroll
+    for (int q = 0; q < 2; q++) {
+        const int c = tid + 256 * q, blk = c >> 6, sl = blk >> 1, part = blk & 1;
+        const uint4 v = *(const uint4 *)(img + c * 16);
+        *(uint4 *)(xp + base + (size_t)sl * 32768 + part * 1024 + (c & 63) * 16) = v;
     }
 }
 
@@ -2537,8 +2593,10 @@ static int dn_prefill_check(const vx27_dn_prefill_desc *d) {
 }
 
 // The prefill on caller-provided scratch of vx_dn_prefill_scratch(d) bytes.
-int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *scr) {
+int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *scr, char *out_packed) {
     if (dn_prefill_check(d)) return -1;
+    VX_REQUIRE(!out_packed || (!dn_prefill_is_exact(d) && (d->flags & VX27_DN_OUT_GATE)),
+               "internal: a packed output needs the chunked form with the output gate");
     if (dn_prefill_is_exact(d)) return dn_prefill_exact(ctx, d, scr);
     const bool conv = (d->flags & VX27_DN_CONV) != 0;
     const int NC = (d->T + CH - 1) / CH;
@@ -2617,7 +2675,10 @@ int vx_dn_prefill_into(vx27_hip_ctx *ctx, const vx27_dn_prefill_desc *d, void *s
         VX_LAUNCH(ctx, dnp_prep, dim3((unsigned)NC, (unsigned)d->nv, (unsigned)d->B), dim3(256), pa);
         VX_LAUNCH(ctx, dnp_scan, dim3((unsigned)(d->nv * NSLICE), (unsigned)d->B), dim3(256), sa);
     }
-    if (d->flags & VX27_DN_OUT_GATE) {
+    if (out_packed) {
+        VX_LAUNCH(ctx, dnp_out_gate_packed, dim3((unsigned)((rows + 15) / 16), (unsigned)d->nv), dim3(256), (int)rows,
+                  d->nv, d->out, d->z, d->norm_w, out_packed);
+    } else if (d->flags & VX27_DN_OUT_GATE) {
         const int nrow = (int)(rows * d->nv);
         VX_LAUNCH(ctx, dnp_out_gate, dim3((unsigned)((nrow + 31) / 32)), dim3(256), nrow, d->z, d->norm_w, d->out);
     }

@@ -121,11 +121,11 @@ __device__ __forceinline__ void gemm_store1(const GemmArgs &a, int tm, int tn, i
 // one g) stay one aligned 128-byte block each, and the XOR spreads the
 // units that one token column touches over the LDS's 32 banks.
 // gemm_pack writes this image for every (token tile, k-step) of x (tokens
-// past R as zeros), so that gemm_wx copies it into LDS verbatim by
-// direct-to-LDS loads.  grid (K/32, token tiles), block 256.
+// past R as zeros; vx_gemm_pack_unit gives the layout), so that gemm_wx
+// copies it into LDS verbatim by direct-to-LDS loads.  grid (K/32, token
+// tiles), block 256.
 __global__ __launch_bounds__(256) void gemm_pack(const float *x, size_t x_stride, int R, char *xp) {
-    const int s = blockIdx.x, tm = blockIdx.y;
-    char *img = xp + ((size_t)tm * gridDim.x + s) * G_XIMG;
+    const int s = blockIdx.x, tm = blockIdx.y, K = 32 * gridDim.x;
 #pragma unroll
     for (int q = 0; q < 4; q++) {
         const int u = threadIdx.x + 256 * q, tb = u >> 6, g = (u >> 4) & 3, n = u & 15;
@@ -143,9 +143,9 @@ __global__ __launch_bounds__(256) void gemm_pack(const float *x, size_t x_stride
             h[e] = pack2(v[2 * e], v[2 * e + 1]);   // hi = bf16(x), then lo = bf16(x - hi)
             l[e] = pack2(v[2 * e] - __uint_as_float(h[e] << 16), v[2 * e + 1] - __uint_as_float(h[e] & 0xffff0000u));
         }
-        const int off = (g * 16 + (n ^ (g << 1))) * 16;
-        *(uint4 *)(img + (tb * 2 + 0) * 1024 + off) = make_uint4(h[0], h[1], h[2], h[3]);
-        *(uint4 *)(img + (tb * 2 + 1) * 1024 + off) = make_uint4(l[0], l[1], l[2], l[3]);
+        char *dst = xp + vx_gemm_pack_unit(t, 32 * s + 8 * g, K);
+        *(uint4 *)dst = make_uint4(h[0], h[1], h[2], h[3]);
+        *(uint4 *)(dst + 1024) = make_uint4(l[0], l[1], l[2], l[3]);
     }
 }
 
@@ -269,9 +269,11 @@ __global__ __launch_bounds__(512) void gemm_reduce(GemmArgs a) {
 
 }  // namespace
 
-bool vx_gemm_fits_seg(int N, int K, int R, const float *x, size_t x_stride, const GemmOut &out) {
-    if (!(N > 0 && N % 16 == 0 && K > 0 && K % 64 == 0 && R >= 1 && x_stride % 4 == 0 && ((uintptr_t)x & 15) == 0))
-        return false;
+namespace {
+// the shape and the output segments (N % 16 == 0, K % 64 == 0; segments in
+// increasing row-block order from row block 0, aligned for their stores)
+bool gemm_shape_ok(int N, int K, int R, const GemmOut &out) {
+    if (!(N > 0 && N % 16 == 0 && K > 0 && K % 64 == 0 && R >= 1)) return false;
     if (out.n < 1 || out.n > VX_GEMM_SEGS || out.s[0].rb0 != 0) return false;
     for (int q = 0; q < out.n; q++) {
         const GemmSeg &sg = out.s[q];
@@ -279,6 +281,15 @@ bool vx_gemm_fits_seg(int N, int K, int R, const float *x, size_t x_stride, cons
         if (q > 0 && (sg.rb0 <= out.s[q - 1].rb0 || sg.rb0 >= N / 16)) return false;
     }
     return true;
+}
+}  // namespace
+
+bool vx_gemm_fits_seg(int N, int K, int R, const float *x, size_t x_stride, const GemmOut &out) {
+    return x_stride % 4 == 0 && ((uintptr_t)x & 15) == 0 && gemm_shape_ok(N, K, R, out);
+}
+
+size_t vx_gemm_pack_bytes(int K, int R) {
+    return (size_t)((R + GT - 1) / GT) * (K / 32) * G_XIMG;
 }
 
 bool vx_gemm_fits(int N, int K, int R, const float *x, size_t x_stride, const float *y, size_t y_stride) {
@@ -307,30 +318,25 @@ GemmPlan gemm_plan(int N, int K, int R, int n_cu) {
     }
     return pl;
 }
-size_t gemm_pack_bytes(int K, int R) {
-    return (size_t)((R + GT - 1) / GT) * (K / 32) * G_XIMG;
-}
 }  // namespace
 
 size_t vx_gemm_ws_bytes(int N, int K, int R, int n_cu) {
-    return gemm_plan(N, K, R, n_cu).ws_bytes + gemm_pack_bytes(K, R);
+    return gemm_plan(N, K, R, n_cu).ws_bytes + vx_gemm_pack_bytes(K, R);
 }
 
-int vx_gemm_store_seg(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x, size_t x_stride, int R,
-                      const GemmOut &out, void *ws) {
-    VX_REQUIRE(vx_gemm_fits_seg(N, K, R, x, x_stride, out),
-               "gemm: need N %% 16 == 0, K %% 64 == 0, 16-byte aligned x rows and aligned output segments "
-               "(N=%d K=%d R=%d)", N, K, R);
+int vx_gemm_store_packed(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const char *xp, int R,
+                         const GemmOut &out, void *ws) {
+    VX_REQUIRE(xp && ((uintptr_t)xp & 15) == 0 && gemm_shape_ok(N, K, R, out),
+               "gemm: need N %% 16 == 0, K %% 64 == 0, a 16-byte aligned packed input and aligned output "
+               "segments (N=%d K=%d R=%d)", N, K, R);
     VX_REQUIRE(ws != nullptr, "gemm: needs its workspace (vx_gemm_ws_bytes)");
     GemmArgs a;
     a.W = W; a.N = N; a.K = K; a.R = R; a.kg = vx_gemv_kg(K);
     a.out = out;
+    a.xp = xp;
     a.n_tm = (R + GT - 1) / GT;
     a.n_tn = (N / 16 + GRB - 1) / GRB;
     const GemmPlan pl = gemm_plan(N, K, R, ctx->n_cu);
-    char *xp = (char *)ws + pl.ws_bytes;
-    a.xp = xp;
-    VX_LAUNCH(ctx, gemm_pack, dim3((unsigned)(K / 32), (unsigned)a.n_tm), dim3(256), x, x_stride, R, xp);
     if (pl.n_main > 0) {
         a.tile0 = 0; a.n_t = pl.n_main; a.P = 1; a.ws = nullptr;
         a.per_xcd = (pl.n_main + 7) / 8;
@@ -342,6 +348,18 @@ int vx_gemm_store_seg(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const 
         VX_LAUNCH(ctx, gemm_reduce, dim3((unsigned)pl.rem, 32), dim3(512), a);
     }
     return 0;
+}
+
+int vx_gemm_store_seg(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x, size_t x_stride, int R,
+                      const GemmOut &out, void *ws) {
+    VX_REQUIRE(vx_gemm_fits_seg(N, K, R, x, x_stride, out),
+               "gemm: need N %% 16 == 0, K %% 64 == 0, 16-byte aligned x rows and aligned output segments "
+               "(N=%d K=%d R=%d)", N, K, R);
+    VX_REQUIRE(ws != nullptr, "gemm: needs its workspace (vx_gemm_ws_bytes)");
+    char *xp = (char *)ws + gemm_plan(N, K, R, ctx->n_cu).ws_bytes;
+    VX_LAUNCH(ctx, gemm_pack, dim3((unsigned)(K / 32), (unsigned)((R + GT - 1) / GT)), dim3(256), x, x_stride, R,
+              xp);
+    return vx_gemm_store_packed(ctx, W, N, K, xp, R, out, ws);
 }
 
 int vx_gemm_store(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const float *x, size_t x_stride, int R,

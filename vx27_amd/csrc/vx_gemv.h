@@ -64,6 +64,22 @@ int vx_gemm_store_seg(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const 
                       const GemmOut &out, void *ws);
 bool vx_gemm_fits_seg(int N, int K, int R, const float *x, size_t x_stride, const GemmOut &out);
 constexpr int VX_GEMM_MIN_ROWS = 256;   // layer prefills use the GEMM from this many tokens (one token tile)
+// The GEMM's packed tokens: one 32 KiB image per (256-token tile, 32-wide
+// k-step), [token tiles][K/32][32 KiB].  In an image, part p (0: hi =
+// bf16(x), 1: lo = bf16(x - hi)) of token t's elements 8g .. 8g+7 sit in
+// 1 KiB block ((t % 256) / 16) * 2 + p, 16-byte unit g * 16 + ((t % 16) ^ 2g)
+// (the XOR spreads a token column over the LDS banks).  Byte offset of the
+// hi unit holding element k of token t (its lo unit: + 1024):
+__host__ __device__ __forceinline__ size_t vx_gemm_pack_unit(int t, int k, int K) {
+    const int tb = (t >> 4) & 15, n = t & 15, g = (k >> 3) & 3;
+    return ((size_t)(t >> 8) * (K >> 5) + (k >> 5)) * 32768 + (size_t)tb * 2048 + (size_t)(g * 16 + (n ^ (g << 1))) * 16;
+}
+size_t vx_gemm_pack_bytes(int K, int R);
+// vx_gemm_store_seg on tokens already packed (xp: vx_gemm_pack_bytes, rows
+// past R may hold anything: they feed only outputs that are not stored);
+// ws: vx_gemm_ws_bytes.
+int vx_gemm_store_packed(vx27_hip_ctx *ctx, const uint16_t *W, int N, int K, const char *xp, int R,
+                         const GemmOut &out, void *ws);
 
 // Part p (0 = hi, 1 = mid, 2 = lo) of the exact three-way bf16 split of x:
 // hi = bf16(x), mid = bf16(x - hi), lo = bf16(x - hi - mid); each difference

@@ -395,8 +395,9 @@ extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_
     // (the long-prompt GEMMs' workspace, one region for both)
     const size_t ws_b =
         gemm ? align256(std::max(vx_gemm_ws_bytes(Nin, H, R, ctx->n_cu), vx_gemm_ws_bytes(H, vd, R, ctx->n_cu))) : 0;
+    const size_t opk_b = gemm ? align256(vx_gemm_pack_bytes(vd, R)) : 0;   // the gated output, packed for out_proj
     void *scr;
-    if (vx_ctx_scratch(ctx, pk_x + y_b + x_b + z_b + 2 * g_b + o_b + pk_o + ws_b + inner, &scr)) return -1;
+    if (vx_ctx_scratch(ctx, pk_x + y_b + x_b + z_b + 2 * g_b + o_b + pk_o + ws_b + opk_b + inner, &scr)) return -1;
     char *p = (char *)scr;
     uint16_t *xp = (uint16_t *)p; p += pk_x;
     float *y = (float *)p; p += y_b;
@@ -407,6 +408,7 @@ extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_
     float *o = (float *)p; p += o_b;
     uint16_t *op = (uint16_t *)p; p += pk_o;
     void *gws = p; p += ws_b;
+    char *opk = p; p += opk_b;
     GemmOut seg = {};   // (the GEMM writes qkv, z, a and b straight into their buffers)
     seg.n = 4;
     seg.s[0] = GemmSeg{0, 0, (size_t)C, xq};
@@ -433,9 +435,14 @@ extern "C" int vx27_hip_dn_layer_prefill(vx27_hip_ctx *ctx, const vx27_dn_layer_
                                 hipMemcpyDeviceToDevice, ctx->stream));
     }
     pd.x = xq; pd.z = z; pd.a = ga; pd.b = gb; pd.out = o;
-    if (vx_dn_prefill_into(ctx, &pd, p)) return -1;
-    if (gemm && vx_gemm_fits(H, vd, R, o, (size_t)vd, d->out, (size_t)H))
-        return vx_gemm_store(ctx, d->w_out, H, vd, o, (size_t)vd, R, d->out, (size_t)H, gws);
+    // out_proj in the GEMM takes the gated output straight in its packed
+    // form (the gated norm writes it, in place of fp32 rows to pack)
+    GemmOut oseg = {};
+    oseg.n = 1;
+    oseg.s[0] = GemmSeg{0, 0, (size_t)H, d->out};
+    const bool gemm_out = gemm && vx_gemm_fits_seg(H, vd, R, o, (size_t)vd, oseg);
+    if (vx_dn_prefill_into(ctx, &pd, p, gemm_out ? opk : nullptr)) return -1;
+    if (gemm_out) return vx_gemm_store_packed(ctx, d->w_out, H, vd, opk, R, oseg, gws);
     if (vx_pack(ctx, o, (size_t)vd, R, vd, op)) return -1;
     return vx_gemv_store(ctx, d->w_out, H, vd, op, R, d->out, (size_t)H);
 }
