@@ -499,6 +499,9 @@ extern "C" int vx27_hip_gqa_layer_prefill(vx27_hip_ctx *ctx, const vx27_gqa_laye
     }
     gp.q = qg; gp.gate = qg + hd; gp.k_new = kb; gp.v_new = vb; gp.out = att;
     if (vx_gqa_prefill_into(ctx, &gp, p)) return -1;
+    // (written packed by the attention epilogue, the output measured slower
+    // there than the pack it saves: its scattered stores hold up the next
+    // item's loads)
     if (gemm && vx_gemm_fits(H, Ka, R, att, (size_t)Ka, d->out, (size_t)H))
         return vx_gemm_store(ctx, d->w_o, H, Ka, att, (size_t)Ka, R, d->out, (size_t)H, gws);
     if (vx_pack(ctx, att, (size_t)Ka, R, Ka, ap)) return -1;
