@@ -96,3 +96,17 @@ def test_gemm_matches_exact_gemv(ctx):
     e = float(np.max(np.abs(y - yg) / mag))
     say(f"  gemm vs exact gemv, {N}x{K} R={R}: {e:.2e} of sum|W||x|")
     assert e <= 2.0 ** -15
+
+
+def test_gemm_deterministic(ctx):
+    """The last partial round of tiles is split along k (here 5 tiles of 1040
+    rows x 256 tokens in 20 parts) and its parts are added in part order, so
+    two calls give the same bits."""
+    from vx27_amd import workloads as W
+    r = W.rng(13, "gemm_det")
+    N, K, R = 1040, 5120, 256
+    Wb = W.bf16_bits(W.normal(r, (N, K), 0.02))
+    x = W.normal(r, (R, K))
+    y1 = run_gemm(ctx, Wb, x)
+    y2 = run_gemm(ctx, Wb, x)
+    assert np.array_equal(y1.view(np.uint32), y2.view(np.uint32))
